@@ -1,0 +1,204 @@
+/*
+ * qwen_hip.h — C ABI of the MI355X (gfx950) operator library `libqwen_hip.so`.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, int64 sizes/strides (in elements), a dtype
+ *     code and a hipStream_t passed as `void*` (the caller's current stream);
+ *   - enqueues work on that stream and never allocates device memory; buffers
+ *     beyond inputs and outputs come in as a caller-allocated `ws` workspace
+ *     whose size is given by the matching `*_workspace` query;
+ *   - returns QH_OK (0) or a QH_E_* code; qh_last_error() then holds a
+ *     thread-local message.
+ *
+ * Each declaration cites the reference (luozoupi/Qwen-Triton) interface it
+ * replaces as `path:line`.
+ */
+#ifndef QWEN_HIP_H_
+#define QWEN_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { QH_F32 = 0, QH_F16 = 1, QH_BF16 = 2 };
+enum { QH_OK = 0, QH_E_ARG = 1, QH_E_DTYPE = 2, QH_E_HIP = 3, QH_E_WORKSPACE = 4 };
+
+/* ---- library ------------------------------------------------------------ */
+const char* qh_last_error(void);
+const char* qh_version(void);
+/* Zero `nbytes` of device memory with a kernel (graph-capture safe). */
+int qh_zero(void* ptr, int64_t nbytes, void* stream);
+
+/* ---- elementwise -------------------------------------------------------- */
+/* out = x + r over n contiguous elements.
+ * Replaces qwen_triton/kernels/residual_add.py:50-60 (_residual_add_kernel), :86-101. */
+int qh_add(const void* x, const void* r, void* out, int64_t n, int dtype, void* stream);
+
+/* out = silu(gate) * up, fp32 math, one rounding.
+ * Replaces qwen_triton/kernels/swiglu.py:84-92 (_silu_mul_kernel), :175-190. */
+int qh_silu_mul_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+/* dgate = g*u*s*(1+gate*(1-s)), dup = g*gate*s with s = sigmoid(gate).
+ * Replaces qwen_triton/kernels/swiglu.py:106-132 (_silu_mul_backward_kernel), :39-51. */
+int qh_silu_mul_bwd(const void* gate, const void* up, const void* gout, void* dgate, void* dup,
+                    int64_t n, int dtype, void* stream);
+
+/* out = x * sigmoid(gate).
+ * Replaces qwen_triton/kernels/sigmoid_mul.py:66-83 (_sigmoid_mul_kernel), :180-195. */
+int qh_sigmoid_mul_fwd(const void* x, const void* gate, void* out, int64_t n, int dtype, void* stream);
+/* dx = g*s, dgate = g*x*s*(1-s).
+ * Replaces qwen_triton/kernels/sigmoid_mul.py:97-120 (_sigmoid_mul_backward_kernel), :39-50. */
+int qh_sigmoid_mul_bwd(const void* x, const void* gate, const void* gout, void* dx, void* dgate,
+                       int64_t n, int dtype, void* stream);
+
+/* ---- RMSNorm ------------------------------------------------------------ */
+/* y = x * rsqrt(mean(x^2) + eps) * (w or 1+w), rows x cols contiguous, fp32 math.
+ * `wdtype` is the weight's dtype. Replaces qwen_triton/kernels/rmsnorm.py:101-133, :64-82. */
+int qh_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t cols, float eps,
+                   int one_plus, int dtype, int wdtype, void* stream);
+/* Workspace bytes for qh_rmsnorm_bwd (deterministic two-stage dW). */
+int64_t qh_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype);
+/* gx (dtype) and gw (wdtype, summed over rows in a fixed order, no atomics).
+ * Replaces qwen_triton/kernels/rmsnorm.py:148-196 (_rmsnorm_backward_kernel), :213-240. */
+int qh_rmsnorm_bwd(const void* x, const void* w, const void* gy, void* gx, void* gw, void* ws,
+                   int64_t ws_bytes, int64_t rows, int64_t cols, float eps, int one_plus, int dtype,
+                   int wdtype, void* stream);
+
+/* ---- RoPE --------------------------------------------------------------- */
+/* Rotate-half RoPE of x[B,H,S,D] (any strides) into contiguous out[B,H,S,D]:
+ * for d < rot/2: o[d] = x[d]c - x[d+h]s, o[d+h] = x[d+h]c + x[d]s with c,s =
+ * cos/sin[b', s, d] (only the first rot/2 entries are read); dims >= rot are
+ * copied. cos/sin are [cos_batch, S, >=rot/2] with strides (scb, scs, scd);
+ * cos_batch == 1 broadcasts over B. neg_sin != 0 uses -sin (the exact
+ * transpose, i.e. the backward).
+ * Replaces qwen_triton/kernels/rope.py:78-120 (_rope_tensor_kernel), :131-162, :165-203 and
+ * qwen_triton/csrc/rope_op_kernel.cu:12-39 (rope_tensor_forward_kernel). */
+int qh_rope(const void* x, int64_t sxb, int64_t sxh, int64_t sxs, int64_t sxd, const void* cos,
+            const void* sin, int64_t scb, int64_t scs, int64_t scd, int64_t cos_batch, void* out,
+            int64_t B, int64_t H, int64_t S, int64_t D, int64_t rot, int neg_sin, int dtype,
+            int cdtype, void* stream);
+
+/* ---- KV cache ----------------------------------------------------------- */
+/* cache[b,h,pos[s],:] = values[b,h,s,:] (strided). Positions outside [0,cap)
+ * are skipped. Replaces qwen_triton/kernels/cache.py:72-98 (_write_kv_kernel), :142-181. */
+int qh_kv_write(void* cache, int64_t scb, int64_t sch, int64_t scs, int64_t scd, const void* values,
+                int64_t svb, int64_t svh, int64_t svs, int64_t svd, const int64_t* positions,
+                int64_t B, int64_t H, int64_t S, int64_t D, int64_t cap, int dtype, void* stream);
+/* out[B,H,So+Sn,D] = cat(prefix[B,H,So,D], suffix[B,H,Sn,D]) along S (contiguous).
+ * Replaces qwen_triton/kernels/cache.py:37-69 (_append_kv_kernel), :101-139. */
+int qh_kv_append(const void* prefix, const void* suffix, void* out, int64_t B, int64_t H,
+                 int64_t s_old, int64_t s_new, int64_t D, int dtype, void* stream);
+
+/* ---- embedding ---------------------------------------------------------- */
+/* out[t,:] = w[ids[t],:]; rows of ids outside [0,V) produce zeros.
+ * Replaces qwen_triton/kernels/embedding.py:50-60 (_embedding_kernel), :97-112. */
+int qh_embedding_fwd(const int64_t* ids, const void* w, int64_t stride_w, void* out, int64_t n_tokens,
+                     int64_t V, int64_t Hd, int dtype, void* stream);
+int64_t qh_embedding_bwd_workspace(int64_t n_tokens);
+/* gw[v,:] = sum_{t: ids[t]==v} gout[t,:] (fp32 sum in token order, stored as
+ * wdtype), gw[padding_idx] = 0; rows never referenced are zero. Deterministic
+ * (radix sort by id + segment sums). gw is fully written.
+ * Replaces qwen_triton/kernels/embedding.py:78-94 (_embedding_backward_kernel), :124-145. */
+int qh_embedding_bwd(const int64_t* ids, const void* gout, void* gw, void* ws, int64_t ws_bytes,
+                     int64_t n_tokens, int64_t V, int64_t Hd, int64_t padding_idx, int gdtype,
+                     int wdtype, void* stream);
+
+/* ---- softmax ------------------------------------------------------------ */
+/* Row softmax over the last dim. Replaces qwen_triton/kernels/softmax.py:56-88, :130-135. */
+int qh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int dtype, void* stream);
+/* gx = y * (gy - sum(gy*y)). Replaces qwen_triton/kernels/softmax.py:100-127. */
+int qh_softmax_bwd(const void* y, const void* gy, void* gx, int64_t rows, int64_t cols, int dtype,
+                   void* stream);
+
+/* ---- cross-entropy ------------------------------------------------------ */
+/* Per row: lse = logsumexp(logits[row,:V]) (single-pass online), loss_row =
+ * lse - logits[row, t]; rows with t == ignore_index give 0; rows with t
+ * outside [0,V) give NaN. *loss_out = sum(loss_row) / max(1, n_valid), *nvalid_out
+ * = n_valid (fp32, fixed-order sum). Replaces qwen_triton/kernels/cross_entropy.py:55-95, :142-161. */
+int qh_ce_fwd(const void* logits, int64_t stride, const int64_t* targets, float* lse, float* loss_rows,
+              float* loss_out, float* nvalid_out, int64_t N, int64_t V, int64_t ignore_index, int dtype,
+              void* stream);
+/* glogits = (softmax - onehot(t)) * grad_loss[0] / max(1, nvalid[0]); ignored rows 0.
+ * grad_loss and nvalid are device pointers (no host sync).
+ * Replaces qwen_triton/kernels/cross_entropy.py:108-139, :180-192. */
+int qh_ce_bwd(const void* logits, int64_t stride, const int64_t* targets, const float* lse,
+              const float* grad_loss, const float* nvalid, void* glogits, int64_t gstride, int64_t N,
+              int64_t V, int64_t ignore_index, int dtype, void* stream);
+
+/* ---- MoE routing primitives --------------------------------------------- */
+/* Top-k per row, values sorted descending, ties -> lowest index.
+ * Replaces qwen_triton/kernels/moe_routing.py:45-144 (_topk_k2_kernel, _topk_general_kernel). */
+int qh_topk(const void* x, void* vals, int64_t* idx, int64_t N, int64_t C, int64_t k, int dtype,
+            void* stream);
+/* out[n,c] = (idx[n] == c) as int64. Replaces qwen_triton/kernels/moe_routing.py:175-200. */
+int qh_one_hot(const int64_t* idx, int64_t* out, int64_t N, int64_t C, void* stream);
+int64_t qh_index_add_workspace(int64_t n_src);
+/* target[index[r],:] += src[r,:] (rows with index outside [0,n_target) are
+ * skipped). Each touched row gets target + (fp32 sum of its sources in source
+ * order), rounded once; deterministic.
+ * Replaces qwen_triton/kernels/moe_routing.py:218-255 (_index_add_kernel, _triton_index_add). */
+int qh_index_add(void* target, int64_t stride_t, const void* src, int64_t stride_s, const int64_t* index,
+                 int64_t n_src, int64_t n_target, int64_t D, void* ws, int64_t ws_bytes, int dtype,
+                 void* stream);
+
+/* ---- GEMM (Linear) ------------------------------------------------------ */
+/* C[M,N] = A(M,K) . B(N,K)^T (+ bias[N]) with operand views
+ *   A(m,k) = trans_a ? A[k*lda + m] : A[m*lda + k]
+ *   B(n,k) = trans_b ? B[k*ldb + n] : B[n*ldb + k]
+ * so forward x W^T (0,0), dX = dY W (0,1) and dW = dY^T X (1,1) need no copies.
+ * bf16/f16 run on MFMA 32x32x16 with fp32 accumulation; f32 runs on VALU.
+ * bias has the input dtype; C has out_dtype.
+ * Replaces qwen_triton/kernels/matmul.py:64-97 (_matmul_kernel), :100-111 (_bias_add_kernel),
+ * :130-200 (forward/backward launchers incl. the per-call transposes at :140, :184). */
+int qh_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+            const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
+            void* stream);
+/* out[n] = sum_m X[m*ldx + n] in a fixed order (bias gradient).
+ * Replaces qwen_triton/kernels/matmul.py:114-127 (_row_sum_kernel). */
+int qh_colsum(const void* X, int64_t ldx, int64_t M, int64_t N, void* out, int dtype, int out_dtype,
+              void* stream);
+
+/* ---- flash attention ---------------------------------------------------- */
+/* O = softmax(scale * Q K^T + causal mask) V, LSE = logsumexp per query (fp32,
+ * natural log, [B,Hq,Sq]). q [B,Hq,Sq,D], k/v [B,Hkv,Sk,D] with the given
+ * batch/head/seq strides (unit stride on D); o is contiguous [B,Hq,Sq,D]. GQA
+ * maps q-head h to kv-head h/(Hq/Hkv). Causal: key j visible to query i iff
+ * j <= i + causal_offset (0 = the reference's top-left alignment). bf16/f16,
+ * D % 8 == 0, D <= 128. lse may be NULL.
+ * Replaces qwen_triton/kernels/flash_attention.py:54-152 (_flash_attn_fwd_kernel), :280-314. */
+int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
+                 int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o,
+                 float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                 float scale, int causal, int64_t causal_offset, int dtype, void* stream);
+int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq);
+/* dq [B,Hq,Sq,D], dk/dv [B,Hkv,Sk,D] (contiguous, fully written) from o and
+ * dout (contiguous [B,Hq,Sq,D]) and the forward's lse. Deterministic: a dK/dV
+ * pass over key blocks (looping over the GQA group's q-heads) and a separate
+ * dQ pass over query blocks; no atomics.
+ * Replaces qwen_triton/kernels/flash_attention.py:155-277 (_flash_attn_bwd_preprocess,
+ * _flash_attn_bwd_kernel), :317-367. */
+int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
+                 int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs,
+                 const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv, void* ws,
+                 int64_t ws_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                 float scale, int causal, int64_t causal_offset, int dtype, void* stream);
+int64_t qh_flash_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk, int64_t D);
+/* Single-query attention (Sq == 1, no mask) over a KV cache: split-KV partials
+ * + fixed-order combine. q strides (batch, head); o contiguous [B,Hq,1,D].
+ * seqlens (device int32[B], may be NULL) gives each sequence's valid key count
+ * (clamped to Sk); with it the launch does not depend on the current length, so
+ * a captured decode step can be replayed as the cache grows. Sk then only
+ * bounds the keys read and plans the split count.
+ * Replaces the q_len == 1 use of qwen_triton/kernels/flash_attention.py:54-152 made by
+ * qwen_triton/modules/attention.py:100-109. */
+int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int64_t skb, int64_t skh,
+                    int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o, float* lse,
+                    const int32_t* seqlens, void* ws, int64_t ws_bytes, int64_t B, int64_t Hq, int64_t Hkv,
+                    int64_t Sk, int64_t D, float scale, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN_HIP_H_ */

@@ -1,0 +1,806 @@
+// Flash attention (forward, deterministic backward, split-KV decode) for gfx950.
+//
+// Layouts: q [B,Hq,Sq,D], k/v [B,Hkv,Sk,D] with arbitrary batch/head/seq strides
+// and unit stride on D; outputs are contiguous. GQA maps q-head h to kv-head
+// h / (Hq / Hkv) inside the kernels (no repeated K/V). D is padded to DP in
+// {32, 64, 128} with zeros, so any D <= 128 that is a multiple of 8 works.
+//
+// Causal masking: key j is visible to query i iff j <= i + causal_offset
+// (offset 0 = top-left alignment of the reference kernel; Sk - Sq =
+// bottom-right alignment for chunked prefill).
+//
+// Forward (per workgroup: 4 wavefronts x 32*QT queries of one (b, h)):
+//   S^T = K Q^T on MFMA 32x32x16 with Q kept in registers and K tiles in LDS;
+//   the C layout puts one query per lane, so the online-softmax max/sum are
+//   in-lane reductions plus one cross-half swap. P^T (bf16) is then used
+//   directly as the B operand of O^T += V^T P^T, with V staged transposed in
+//   LDS and the k index permuted to match the C layout (no LDS round trip for
+//   P). Softmax runs in base 2 with the scale folded into one multiply.
+//   LSE (natural log) is saved for the backward.
+//
+// Backward: Delta = rowsum(O * dO); a dK/dV kernel per (b, kv-head, 128 keys)
+// that loops over the group's q-heads and all visible q-tiles (no atomics);
+// and a separate dQ kernel per (b, q-head, 128 queries) that loops over key
+// tiles. Both recompute P from the saved LSE. Results are bitwise
+// reproducible.
+//
+// Decode (Sq == 1): split-KV over the cache with one 16-lane group per key
+// row (fp32 VALU; the pass is HBM-bound on K/V), partial (m, l, o) per split
+// in the workspace, then a fixed-order combine.
+#include "qh_mfma.h"
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::v8 load_frag16(const T* p) {
+  return *reinterpret_cast<const typename Mfma<T>::v8*>(p);
+}
+
+// Two 8-byte LDS reads forming one 8-element fragment (permuted-k operand).
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::v8 load_frag_split(const T* p0, const T* p1) {
+  typedef typename Mfma<T>::v4 v4;
+  typedef typename Mfma<T>::v8 v8;
+  const v4 a = *reinterpret_cast<const v4*>(p0);
+  const v4 b = *reinterpret_cast<const v4*>(p1);
+  v8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
+// Pack accumulator groups g0 and g0+1 (8 values) of a C-layout tile as bf16/f16.
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::v8 pack_pair(const f32x16& c, int g0) {
+  typename Mfma<T>::v8 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = (T)c[g0 * 4 + e];
+    r[4 + e] = (T)c[(g0 + 1) * 4 + e];
+  }
+  return r;
+}
+
+// Stage ROWS rows x DP columns (row-major, rows along seq) into LDS with row
+// stride LD; rows >= nrows or columns >= D are zero.
+template <typename T, int ROWS, int DP, int LD>
+__device__ __forceinline__ void stage_rows(T* __restrict__ S, const T* __restrict__ G, int64_t gstride, int row0,
+                                           int nrows, int D) {
+  constexpr int CPR = DP / 8;  // 16-byte chunks per row
+  const uint4 z = make_uint4(0, 0, 0, 0);
+  for (int c = threadIdx.x; c < ROWS * CPR; c += 256) {
+    const int r = c / CPR, d0 = (c % CPR) * 8;
+    const int gr = row0 + r;
+    uint4 v = z;
+    if (gr < nrows && d0 < D) v = *reinterpret_cast<const uint4*>(G + (int64_t)gr * gstride + d0);
+    *reinterpret_cast<uint4*>(S + r * LD + d0) = v;
+  }
+}
+
+// Stage the transpose: S[d][r] = G[row0 + r][d] for ROWS rows, DP columns;
+// LDS row stride LD (>= ROWS). Zero outside the valid range.
+template <typename T, int ROWS, int DP, int LD>
+__device__ __forceinline__ void stage_rows_t(T* __restrict__ S, const T* __restrict__ G, int64_t gstride, int row0,
+                                             int nrows, int D) {
+  constexpr int RB = ROWS / 8, DB = DP / 8;
+  const uint4 z = make_uint4(0, 0, 0, 0);
+  for (int sb = threadIdx.x; sb < RB * DB; sb += 256) {
+    const int rb = sb % RB, db = sb / RB;
+    const int d0 = db * 8;
+    uint4 in[8], out[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int gr = row0 + rb * 8 + j;
+      in[j] = (gr < nrows && d0 < D) ? *reinterpret_cast<const uint4*>(G + (int64_t)gr * gstride + d0) : z;
+    }
+    transpose8x8(in, out);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) *reinterpret_cast<uint4*>(S + (d0 + c) * LD + rb * 8) = out[c];
+  }
+}
+
+// ===========================================================================
+// Forward
+// ===========================================================================
+template <typename T, int DP, int QT>
+__global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs,
+                                                     const T* __restrict__ K, int64_t skb, int64_t skh, int64_t sks,
+                                                     const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs,
+                                                     T* __restrict__ O, float* __restrict__ LSE, int Hq, int groups,
+                                                     int Sq, int Sk, int D, float scale_log2, int causal, int coff) {
+  constexpr int BN = 64;
+  constexpr int BMQ = 4 * 32 * QT;
+  constexpr int KLD = DP + 8;
+  constexpr int VLD = BN + 8;
+  constexpr int DT = DP / 32, KD = DP / 16;
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ __attribute__((aligned(16))) T Ks[BN * KLD];
+  __shared__ __attribute__((aligned(16))) T Vt[DP * VLD];
+
+  const int nqb = (Sq + BMQ - 1) / BMQ;
+  const int qb = nqb - 1 - (int)blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / Hq, hq = bh % Hq, hk = hq / groups;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int ql = lane & 31, hf = lane >> 5;
+  const T* Qb = Q + b * sqb + hq * sqh;
+  const T* Kb = K + b * skb + hk * skh;
+  const T* Vb = V + b * svb + hk * svh;
+  const int qw0 = qb * BMQ + wid * 32 * QT;
+
+  v8 qf[QT][KD];
+#pragma unroll
+  for (int t = 0; t < QT; ++t)
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      const int qi = qw0 + t * 32 + ql, d0 = kd * 16 + hf * 8;
+      if (qi < Sq && d0 < D) qf[t][kd] = load_frag16<T>(Qb + (int64_t)qi * sqs + d0);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[t][kd][e] = (T)0.f;
+    }
+
+  float m[QT], l[QT];
+  f32x16 acc[QT][DT];
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    m[t] = -INFINITY;
+    l[t] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[t][dt] = zero16();
+  }
+
+  int kv_end = Sk;
+  if (causal) kv_end = min(Sk, qb * BMQ + BMQ + coff);
+
+  for (int kv0 = 0; kv0 < kv_end; kv0 += BN) {
+    __syncthreads();
+    stage_rows<T, BN, DP, KLD>(Ks, Kb, sks, kv0, Sk, D);
+    stage_rows_t<T, BN, DP, VLD>(Vt, Vb, svs, kv0, Sk, D);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const int qi = qw0 + t * 32 + ql;
+      f32x16 s[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        s[kt] = zero16();
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd)
+          s[kt] = Mfma<T>::mma(load_frag16<T>(Ks + (kt * 32 + ql) * KLD + kd * 16 + hf * 8), qf[t][kd], s[kt]);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = kv0 + kt * 32 + g * 8 + hf * 4 + r;
+            float v = s[kt][g * 4 + r] * scale_log2;
+            if (key >= Sk || (causal && key > qi + coff)) v = -INFINITY;
+            s[kt][g * 4 + r] = v;
+            mx = fmaxf(mx, v);
+          }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(m[t], mx);
+      const float mref = (mnew == -INFINITY) ? 0.f : mnew;
+      const float alpha = exp2_(m[t] - mref);
+      float ps = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float p = exp2_(s[kt][e] - mref);
+          s[kt][e] = p;
+          ps += p;
+        }
+      ps += __shfl_xor(ps, 32);
+      l[t] = l[t] * alpha + ps;
+      m[t] = mnew;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[t][dt][e] *= alpha;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const v8 pf = pack_pair<T>(s[ks >> 1], (ks & 1) * 2);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const T* vr = Vt + (dt * 32 + ql) * VLD + ks * 16 + hf * 4;
+          acc[t][dt] = Mfma<T>::mma(load_frag_split<T>(vr, vr + 8), pf, acc[t][dt]);
+        }
+      }
+    }
+  }
+
+  T* Ob = O + (int64_t)bh * Sq * D;
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int qi = qw0 + t * 32 + ql;
+    if (qi >= Sq) continue;
+    const float inv = l[t] > 0.f ? 1.0f / l[t] : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = dt * 32 + g * 8 + hf * 4;
+        if (d < D) {
+          typename Mfma<T>::v4 o4;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o4[r] = (T)(acc[t][dt][g * 4 + r] * inv);
+          *reinterpret_cast<typename Mfma<T>::v4*>(Ob + (int64_t)qi * D + d) = o4;
+        }
+      }
+    if (hf == 0 && LSE) LSE[(int64_t)bh * Sq + qi] = l[t] > 0.f ? (m[t] + __log2f(l[t])) * kLn2 : -INFINITY;
+  }
+}
+
+// ===========================================================================
+// Backward
+// ===========================================================================
+template <typename T>
+__global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const T* __restrict__ O, const T* __restrict__ dO,
+                                                           float* __restrict__ delta, int64_t rows, int D) {
+  // 16 lanes per row, 8 elements per lane per step.
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int li = threadIdx.x & 15;
+  float s = 0.f;
+  if (row < rows) {
+    for (int d = li * 8; d < D; d += 128) {
+      Vec16<T> a = ld16(O + row * D + d), b = ld16(dO + row * D + d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += to_f32(a.v[e]) * to_f32(b.v[e]);
+    }
+  }
+  s = wave_sum(s, 16);
+  if (row < rows && li == 0) delta[row] = s;
+}
+
+// dK, dV for 128 keys (4 wavefronts x 32 keys) of one (b, kv-head).
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
+    const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs, const T* __restrict__ K, int64_t skb, int64_t skh,
+    int64_t sks, const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs, const T* __restrict__ dO,
+    const float* __restrict__ LSE, const float* __restrict__ Delta, T* __restrict__ dK, T* __restrict__ dV, int Hq,
+    int Hkv, int groups, int Sq, int Sk, int D, float scale_log2, float scale, int causal, int coff) {
+  constexpr int BQ = 64;
+  constexpr int KLD = DP + 8, TLD = BQ + 8;
+  constexpr int DT = DP / 32, KD = DP / 16;
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ __attribute__((aligned(16))) T Qs[BQ * KLD];
+  __shared__ __attribute__((aligned(16))) T dOs[BQ * KLD];
+  __shared__ __attribute__((aligned(16))) T Qt[DP * TLD];
+  __shared__ __attribute__((aligned(16))) T dOt[DP * TLD];
+  __shared__ float lse_s[BQ], dl_s[BQ];
+
+  const int bk = blockIdx.y;
+  const int b = bk / Hkv, hk = bk % Hkv;
+  const int k0 = blockIdx.x * 128;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int ql = lane & 31, hf = lane >> 5;
+  const int kj = k0 + wid * 32 + ql;  // this lane's key (C-layout column)
+  const T* Kb = K + b * skb + hk * skh;
+  const T* Vb = V + b * svb + hk * svh;
+
+  v8 kf[KD], vf[KD];
+#pragma unroll
+  for (int kd = 0; kd < KD; ++kd) {
+    const int d0 = kd * 16 + hf * 8;
+    if (kj < Sk && d0 < D) {
+      kf[kd] = load_frag16<T>(Kb + (int64_t)kj * sks + d0);
+      vf[kd] = load_frag16<T>(Vb + (int64_t)kj * svs + d0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kf[kd][e] = vf[kd][e] = (T)0.f;
+    }
+  }
+  f32x16 dk[DT], dv[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dk[dt] = dv[dt] = zero16();
+
+  int q_start = 0;
+  if (causal) {
+    q_start = k0 - coff;
+    if (q_start < 0) q_start = 0;
+    q_start = (q_start / BQ) * BQ;
+  }
+  for (int g = 0; g < groups; ++g) {
+    const int hq = hk * groups + g;
+    const int64_t bh = (int64_t)b * Hq + hq;
+    const T* Qb = Q + b * sqb + hq * sqh;
+    const T* dOb = dO + bh * Sq * D;
+    for (int q0 = q_start; q0 < Sq; q0 += BQ) {
+      __syncthreads();
+      stage_rows<T, BQ, DP, KLD>(Qs, Qb, sqs, q0, Sq, D);
+      stage_rows<T, BQ, DP, KLD>(dOs, dOb, D, q0, Sq, D);
+      stage_rows_t<T, BQ, DP, TLD>(Qt, Qb, sqs, q0, Sq, D);
+      stage_rows_t<T, BQ, DP, TLD>(dOt, dOb, D, q0, Sq, D);
+      if (threadIdx.x < BQ) {
+        const int qi = q0 + threadIdx.x;
+        lse_s[threadIdx.x] = qi < Sq ? LSE[bh * Sq + qi] * kLog2e : 0.f;
+        dl_s[threadIdx.x] = qi < Sq ? Delta[bh * Sq + qi] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) {
+          const int off = (qt * 32 + ql) * KLD + kd * 16 + hf * 8;
+          s = Mfma<T>::mma(load_frag16<T>(Qs + off), kf[kd], s);
+          dp = Mfma<T>::mma(load_frag16<T>(dOs + off), vf[kd], dp);
+        }
+        // C layout: column = key kj, row = query q0 + qt*32 + 8g + 4hf + r
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int il = qt * 32 + gg * 8 + hf * 4 + r;
+            const int qi = q0 + il;
+            const bool ok = qi < Sq && kj < Sk && !(causal && kj > qi + coff);
+            const float p = ok ? exp2_(s[gg * 4 + r] * scale_log2 - lse_s[il]) : 0.f;
+            s[gg * 4 + r] = p;
+            dp[gg * 4 + r] = p * (dp[gg * 4 + r] - dl_s[il]);
+          }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const v8 pf = pack_pair<T>(s, ks * 2);
+          const v8 df = pack_pair<T>(dp, ks * 2);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            const int off = (dt * 32 + ql) * TLD + qt * 32 + ks * 16 + hf * 4;
+            dv[dt] = Mfma<T>::mma(load_frag_split<T>(dOt + off, dOt + off + 8), pf, dv[dt]);
+            dk[dt] = Mfma<T>::mma(load_frag_split<T>(Qt + off, Qt + off + 8), df, dk[dt]);
+          }
+        }
+      }
+    }
+  }
+  if (kj < Sk) {
+    T* dKr = dK + ((int64_t)bk * Sk + kj) * D;
+    T* dVr = dV + ((int64_t)bk * Sk + kj) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) {
+        const int d = dt * 32 + gg * 8 + hf * 4;
+        if (d < D) {
+          typename Mfma<T>::v4 a, c;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            a[r] = (T)(dk[dt][gg * 4 + r] * scale);
+            c[r] = (T)dv[dt][gg * 4 + r];
+          }
+          *reinterpret_cast<typename Mfma<T>::v4*>(dKr + d) = a;
+          *reinterpret_cast<typename Mfma<T>::v4*>(dVr + d) = c;
+        }
+      }
+  }
+}
+
+// dQ for 128 queries (4 wavefronts x 32 queries) of one (b, q-head).
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
+    const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs, const T* __restrict__ K, int64_t skb, int64_t skh,
+    int64_t sks, const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs, const T* __restrict__ dO,
+    const float* __restrict__ LSE, const float* __restrict__ Delta, T* __restrict__ dQ, int Hq, int groups, int Sq,
+    int Sk, int D, float scale_log2, float scale, int causal, int coff) {
+  constexpr int BN = 64;
+  constexpr int KLD = DP + 8, TLD = BN + 8;
+  constexpr int DT = DP / 32, KD = DP / 16;
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ __attribute__((aligned(16))) T Ks[BN * KLD];
+  __shared__ __attribute__((aligned(16))) T Vs[BN * KLD];
+  __shared__ __attribute__((aligned(16))) T Kt[DP * TLD];
+
+  const int nqb = (Sq + 127) / 128;
+  const int qb = nqb - 1 - (int)blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int b = (int)(bh / Hq), hq = (int)(bh % Hq), hk = hq / groups;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int ql = lane & 31, hf = lane >> 5;
+  const int qi = qb * 128 + wid * 32 + ql;
+  const T* Qb = Q + b * sqb + hq * sqh;
+  const T* Kb = K + b * skb + hk * skh;
+  const T* Vb = V + b * svb + hk * svh;
+  const T* dOb = dO + bh * Sq * D;
+
+  v8 qf[KD], of[KD];
+#pragma unroll
+  for (int kd = 0; kd < KD; ++kd) {
+    const int d0 = kd * 16 + hf * 8;
+    if (qi < Sq && d0 < D) {
+      qf[kd] = load_frag16<T>(Qb + (int64_t)qi * sqs + d0);
+      of[kd] = load_frag16<T>(dOb + (int64_t)qi * D + d0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[kd][e] = of[kd][e] = (T)0.f;
+    }
+  }
+  const float lse2 = qi < Sq ? LSE[bh * Sq + qi] * kLog2e : 0.f;
+  const float dl = qi < Sq ? Delta[bh * Sq + qi] : 0.f;
+  f32x16 dq[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dq[dt] = zero16();
+
+  int kv_end = Sk;
+  if (causal) kv_end = min(Sk, qb * 128 + 128 + coff);
+  for (int kv0 = 0; kv0 < kv_end; kv0 += BN) {
+    __syncthreads();
+    stage_rows<T, BN, DP, KLD>(Ks, Kb, sks, kv0, Sk, D);
+    stage_rows<T, BN, DP, KLD>(Vs, Vb, svs, kv0, Sk, D);
+    stage_rows_t<T, BN, DP, TLD>(Kt, Kb, sks, kv0, Sk, D);
+    __syncthreads();
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) {
+        const int off = (kt * 32 + ql) * KLD + kd * 16 + hf * 8;
+        s = Mfma<T>::mma(load_frag16<T>(Ks + off), qf[kd], s);
+        dp = Mfma<T>::mma(load_frag16<T>(Vs + off), of[kd], dp);
+      }
+      // C layout: column = query qi, row = key kv0 + kt*32 + 8g + 4hf + r
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kv0 + kt * 32 + gg * 8 + hf * 4 + r;
+          const bool ok = qi < Sq && key < Sk && !(causal && key > qi + coff);
+          const float p = ok ? exp2_(s[gg * 4 + r] * scale_log2 - lse2) : 0.f;
+          dp[gg * 4 + r] = p * (dp[gg * 4 + r] - dl);
+        }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const v8 df = pack_pair<T>(dp, ks * 2);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int off = (dt * 32 + ql) * TLD + kt * 32 + ks * 16 + hf * 4;
+          dq[dt] = Mfma<T>::mma(load_frag_split<T>(Kt + off, Kt + off + 8), df, dq[dt]);
+        }
+      }
+    }
+  }
+  if (qi < Sq) {
+    T* dQr = dQ + (bh * Sq + qi) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) {
+        const int d = dt * 32 + gg * 8 + hf * 4;
+        if (d < D) {
+          typename Mfma<T>::v4 a;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a[r] = (T)(dq[dt][gg * 4 + r] * scale);
+          *reinterpret_cast<typename Mfma<T>::v4*>(dQr + d) = a;
+        }
+      }
+  }
+}
+
+// ===========================================================================
+// Decode: Sq == 1, split-KV.
+// ===========================================================================
+template <typename T, int DP, int G>
+__global__ __launch_bounds__(256) void fa_decode_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
+                                                        const T* __restrict__ K, int64_t skb, int64_t skh, int64_t sks,
+                                                        const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs,
+                                                        float* __restrict__ ws_o, float* __restrict__ ws_ml,
+                                                        const int* __restrict__ seqlens, int Hkv, int Sk, int D,
+                                                        int kps, float scale_log2) {
+  constexpr int LPK = DP / 8;          // lanes per key row
+  constexpr int GPW = 64 / LPK;        // key groups per wavefront
+  constexpr int NG = 4 * GPW;          // key groups per workgroup
+  constexpr int UNR = 2;               // keys in flight per group
+  __shared__ float red_m[NG][G], red_l[NG][G];
+  __shared__ float red_o[NG][G][DP];
+
+  const int split = blockIdx.x, nsplit = gridDim.x;
+  const int bk = blockIdx.y;
+  const int b = bk / Hkv, hk = bk % Hkv;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int grp = wid * GPW + lane / LPK, li = lane % LPK;
+  const int d0 = li * 8;
+  const bool dok = d0 < D;
+
+  float q[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const T* qp = Q + b * sqb + (int64_t)(hk * G + g) * sqh + d0;
+    if (dok) {
+      Vec16<T> v = ld16(qp);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[g][e] = to_f32(v.v[e]) * scale_log2;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[g][e] = 0.f;
+    }
+  }
+  float m[G], l[G], o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+  }
+  const T* Kb = K + b * skb + hk * skh + d0;
+  const T* Vb = V + b * svb + hk * svh + d0;
+  const int sk_b = seqlens ? min(seqlens[b], Sk) : Sk;
+  const int ks = split * kps;
+  const int ke = min(sk_b, ks + kps);
+  for (int j0 = ks + grp * UNR; j0 < ke; j0 += NG * UNR) {
+    Vec16<T> kv[UNR], vv[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int j = j0 + u;
+      if (j < ke && dok) {
+        kv[u] = ld16(Kb + (int64_t)j * sks);
+        vv[u] = ld16(Vb + (int64_t)j * svs);
+      } else {
+        kv[u].raw = vv[u].raw = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      if (j0 + u >= ke) break;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += q[g][e] * to_f32(kv[u].v[e]);
+        s = wave_sum(s, LPK);
+        const float mn = fmaxf(m[g], s);
+        const float a = exp2_(m[g] - mn);
+        const float p = exp2_(s - mn);
+        l[g] = l[g] * a + p;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] = o[g][e] * a + p * to_f32(vv[u].v[e]);
+        m[g] = mn;
+      }
+    }
+  }
+  // Combine the NG key groups of this workgroup in a fixed order.
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (li == 0) {
+      red_m[grp][g] = m[g];
+      red_l[grp][g] = l[g];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (dok) red_o[grp][g][d0 + e] = o[g][e];
+  }
+  __syncthreads();
+  const int64_t row0 = (int64_t)bk * G;
+  for (int idx = threadIdx.x; idx < G * DP; idx += 256) {
+    const int g = idx / DP, d = idx % DP;
+    float M = -INFINITY;
+    for (int i = 0; i < NG; ++i) M = fmaxf(M, red_m[i][g]);
+    const float Mr = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f, acc = 0.f;
+    for (int i = 0; i < NG; ++i) {
+      const float w = exp2_(red_m[i][g] - Mr);
+      L += red_l[i][g] * w;
+      if (d < D) acc += red_o[i][g][d] * w;
+    }
+    const int64_t slot = (row0 + g) * nsplit + split;
+    if (d < D) ws_o[slot * DP + d] = acc;
+    if (d == 0) {
+      ws_ml[slot * 2] = M;
+      ws_ml[slot * 2 + 1] = L;
+    }
+  }
+}
+
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void fa_decode_combine(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+                                                         T* __restrict__ O, float* __restrict__ LSE, int rows,
+                                                         int nsplit, int D) {
+  const int row = blockIdx.x * (256 / DP) + threadIdx.x / DP;  // one (b, q-head) per DP threads
+  const int d = threadIdx.x % DP;
+  if (row >= rows) return;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ws_ml[((int64_t)row * nsplit + s) * 2]);
+  const float Mr = (M == -INFINITY) ? 0.f : M;
+  float L = 0.f, acc = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const int64_t slot = (int64_t)row * nsplit + s;
+    const float w = exp2_(ws_ml[slot * 2] - Mr);
+    L += ws_ml[slot * 2 + 1] * w;
+    if (d < D) acc += ws_o[slot * DP + d] * w;
+  }
+  if (d < D) O[(int64_t)row * D + d] = from_f32<T>(L > 0.f ? acc / L : 0.f);
+  if (d == 0 && LSE) LSE[row] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+}
+
+static int pick_dp(int64_t D) {
+  if (D <= 32) return 32;
+  if (D <= 64) return 64;
+  if (D <= 128) return 128;
+  return 0;
+}
+
+static int decode_splits(int64_t B, int64_t Hkv, int64_t Sk) {
+  int64_t s = (Sk + 63) / 64;
+  const int64_t want = (2048 + B * Hkv - 1) / (B * Hkv);
+  if (s > want) s = want;
+  if (s < 1) s = 1;
+  return (int)s;
+}
+
+template <typename T, int DP, int G>
+void launch_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int64_t skb, int64_t skh, int64_t sks,
+                   const void* v, int64_t svb, int64_t svh, int64_t svs, float* ws_o, float* ws_ml,
+                   const int* seqlens, int B, int Hkv, int Sk, int D, int nsplit, float scale_log2, hipStream_t st) {
+  const int kps = (Sk + nsplit - 1) / nsplit;
+  dim3 grid(nsplit, B * Hkv);
+  fa_decode_kernel<T, DP, G><<<grid, 256, 0, st>>>((const T*)q, sqb, sqh, (const T*)k, skb, skh, sks, (const T*)v, svb,
+                                                   svh, svs, ws_o, ws_ml, seqlens, Hkv, Sk, D, kps,
+                                                   scale_log2);
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
+                            int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o,
+                            float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                            float scale, int causal, int64_t causal_offset, int dtype, void* stream) {
+  QH_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0, "qh_flash_fwd: bad shape");
+  QH_CHECK_ARG(Hq % Hkv == 0, "qh_flash_fwd: Hq=%lld not a multiple of Hkv=%lld", (long long)Hq, (long long)Hkv);
+  const int dp = pick_dp(D);
+  QH_CHECK_ARG(dp && D % 8 == 0, "qh_flash_fwd: head dim %lld must be a multiple of 8 and <= 128", (long long)D);
+  QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o), "qh_flash_fwd: pointers must be 16-byte aligned");
+  QH_CHECK_ARG(sqs % 8 == 0 && sks % 8 == 0 && svs % 8 == 0 && sqh % 8 == 0 && skh % 8 == 0 && svh % 8 == 0 &&
+                   sqb % 8 == 0 && skb % 8 == 0 && svb % 8 == 0,
+               "qh_flash_fwd: strides must be multiples of 8 elements");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_flash_fwd: bf16/f16 only");
+  QH_CHECK_ARG(B * Hq < 65536 && Sq < (1 << 30) && Sk < (1 << 30), "qh_flash_fwd: too large");
+  if (B * Hq * Sq == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const float sl2 = scale * kLog2e;
+  const int groups = (int)(Hq / Hkv);
+  constexpr int QT = 1;
+  dim3 grid((unsigned)ceil_div(Sq, 128 * QT), (unsigned)(B * Hq));
+#define QH_FWD(T, DPV)                                                                                          \
+  fa_fwd_kernel<T, DPV, QT><<<grid, 256, 0, st>>>((const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks,       \
+                                                 (const T*)v, svb, svh, svs, (T*)o, lse, (int)Hq, groups, (int)Sq, \
+                                                 (int)Sk, (int)D, sl2, causal, (int)causal_offset)
+#define QH_FWD_D(T) \
+  if (dp == 32) QH_FWD(T, 32); else if (dp == 64) QH_FWD(T, 64); else QH_FWD(T, 128);
+  if (dtype == QH_BF16) { QH_FWD_D(bf16_t) } else { QH_FWD_D(f16_t) }
+#undef QH_FWD_D
+#undef QH_FWD
+  QH_CHECK_LAUNCH("qh_flash_fwd");
+  return QH_OK;
+}
+
+extern "C" int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq) { return B * Hq * Sq * 4; }
+
+extern "C" int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
+                            int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs,
+                            const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv, void* ws,
+                            int64_t ws_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                            float scale, int causal, int64_t causal_offset, int dtype, void* stream) {
+  QH_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0, "qh_flash_bwd: bad shape");
+  QH_CHECK_ARG(Hq % Hkv == 0, "qh_flash_bwd: Hq not a multiple of Hkv");
+  const int dp = pick_dp(D);
+  QH_CHECK_ARG(dp && D % 8 == 0, "qh_flash_bwd: head dim must be a multiple of 8 and <= 128");
+  QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && aligned16(dout) && aligned16(dq) &&
+                   aligned16(dk) && aligned16(dv),
+               "qh_flash_bwd: pointers must be 16-byte aligned");
+  QH_CHECK_ARG(sqs % 8 == 0 && sks % 8 == 0 && svs % 8 == 0 && sqh % 8 == 0 && skh % 8 == 0 && svh % 8 == 0 &&
+                   sqb % 8 == 0 && skb % 8 == 0 && svb % 8 == 0,
+               "qh_flash_bwd: strides must be multiples of 8 elements");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_flash_bwd: bf16/f16 only");
+  QH_CHECK_ARG(B * Hq < 65536 && Sq < (1 << 30) && Sk < (1 << 30), "qh_flash_bwd: too large");
+  const int64_t need = qh_flash_bwd_workspace(B, Hq, Sq);
+  if (ws_bytes < need) {
+    qh::set_error("qh_flash_bwd: workspace %lld < %lld", (long long)ws_bytes, (long long)need);
+    return QH_E_WORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const int esz = 2;
+  if (Sq == 0 || B == 0) {
+    int rc = qh_zero(dk, B * Hkv * Sk * D * esz, stream);
+    if (rc) return rc;
+    return qh_zero(dv, B * Hkv * Sk * D * esz, stream);
+  }
+  float* delta = (float*)ws;
+  const int64_t rows = B * Hq * Sq;
+  const float sl2 = scale * kLog2e;
+  const int groups = (int)(Hq / Hkv);
+  dim3 gkv((unsigned)ceil_div(Sk, 128), (unsigned)(B * Hkv));
+  dim3 gq((unsigned)ceil_div(Sq, 128), (unsigned)(B * Hq));
+#define QH_BWD(T, DPV)                                                                                              \
+  do {                                                                                                              \
+    fa_bwd_delta_kernel<T><<<(unsigned)ceil_div(rows, 16), 256, 0, st>>>((const T*)o, (const T*)dout, delta, rows,  \
+                                                                         (int)D);                                   \
+    if (Sk > 0)                                                                                                     \
+      fa_bwd_dkdv_kernel<T, DPV><<<gkv, 256, 0, st>>>((const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks,       \
+                                                      (const T*)v, svb, svh, svs, (const T*)dout, lse, delta, (T*)dk, \
+                                                      (T*)dv, (int)Hq, (int)Hkv, groups, (int)Sq, (int)Sk, (int)D,  \
+                                                      sl2, scale, causal, (int)causal_offset);                      \
+    fa_bwd_dq_kernel<T, DPV><<<gq, 256, 0, st>>>((const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks,            \
+                                                 (const T*)v, svb, svh, svs, (const T*)dout, lse, delta, (T*)dq,    \
+                                                 (int)Hq, groups, (int)Sq, (int)Sk, (int)D, sl2, scale, causal,     \
+                                                 (int)causal_offset);                                               \
+  } while (0)
+#define QH_BWD_D(T) \
+  if (dp == 32) QH_BWD(T, 32); else if (dp == 64) QH_BWD(T, 64); else QH_BWD(T, 128);
+  if (dtype == QH_BF16) { QH_BWD_D(bf16_t) } else { QH_BWD_D(f16_t) }
+#undef QH_BWD_D
+#undef QH_BWD
+  QH_CHECK_LAUNCH("qh_flash_bwd");
+  return QH_OK;
+}
+
+extern "C" int64_t qh_flash_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk, int64_t D) {
+  const int dp = pick_dp(D);
+  if (!dp || Hkv <= 0) return 0;
+  const int ns = decode_splits(B, Hkv, Sk);
+  return B * Hq * ns * (dp + 2) * 4;
+}
+
+extern "C" int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int64_t skb, int64_t skh,
+                               int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o, float* lse,
+                               const int32_t* seqlens, void* ws, int64_t ws_bytes, int64_t B, int64_t Hq, int64_t Hkv,
+                               int64_t Sk, int64_t D, float scale, int dtype, void* stream) {
+  QH_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && Sk >= 0, "qh_flash_decode: bad shape");
+  QH_CHECK_ARG(Hq % Hkv == 0, "qh_flash_decode: Hq not a multiple of Hkv");
+  const int dp = pick_dp(D);
+  QH_CHECK_ARG(dp && D % 8 == 0, "qh_flash_decode: head dim must be a multiple of 8 and <= 128");
+  QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v), "qh_flash_decode: pointers must be 16-byte aligned");
+  QH_CHECK_ARG(sqb % 8 == 0 && sqh % 8 == 0 && skb % 8 == 0 && skh % 8 == 0 && sks % 8 == 0 && svb % 8 == 0 &&
+                   svh % 8 == 0 && svs % 8 == 0,
+               "qh_flash_decode: strides must be multiples of 8 elements");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_flash_decode: bf16/f16 only");
+  const int groups = (int)(Hq / Hkv);
+  QH_CHECK_ARG(groups == 1 || groups == 2 || groups == 4 || groups == 8, "qh_flash_decode: group size %d unsupported",
+               groups);
+  QH_CHECK_ARG(B * Hkv < 65536, "qh_flash_decode: too many sequences");
+  if (B == 0) return QH_OK;
+  const int64_t need = qh_flash_decode_workspace(B, Hq, Hkv, Sk, D);
+  if (ws_bytes < need) {
+    qh::set_error("qh_flash_decode: workspace %lld < %lld", (long long)ws_bytes, (long long)need);
+    return QH_E_WORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const int ns = decode_splits(B, Hkv, Sk);
+  float* ws_o = (float*)ws;
+  float* ws_ml = ws_o + B * Hq * ns * dp;
+  const float sl2 = scale * kLog2e;
+#define QH_DEC(T, DPV, GV)                                                                                   \
+  launch_decode<T, DPV, GV>(q, sqb, sqh, k, skb, skh, sks, v, svb, svh, svs, ws_o, ws_ml, seqlens, (int)B,  \
+                            (int)Hkv, (int)Sk, (int)D, ns, sl2, st)
+#define QH_DEC_G(T, DPV) \
+  if (groups == 1) QH_DEC(T, DPV, 1); else if (groups == 2) QH_DEC(T, DPV, 2); else if (groups == 4) QH_DEC(T, DPV, 4); else QH_DEC(T, DPV, 8);
+#define QH_DEC_D(T) \
+  if (dp == 32) { QH_DEC_G(T, 32) } else if (dp == 64) { QH_DEC_G(T, 64) } else { QH_DEC_G(T, 128) }
+  const int rows = (int)(B * Hq);
+  if (dtype == QH_BF16) {
+    QH_DEC_D(bf16_t)
+    if (dp == 32) fa_decode_combine<bf16_t, 32><<<(unsigned)ceil_div(rows, 8), 256, 0, st>>>(ws_o, ws_ml, (bf16_t*)o, lse, rows, ns, (int)D);
+    else if (dp == 64) fa_decode_combine<bf16_t, 64><<<(unsigned)ceil_div(rows, 4), 256, 0, st>>>(ws_o, ws_ml, (bf16_t*)o, lse, rows, ns, (int)D);
+    else fa_decode_combine<bf16_t, 128><<<(unsigned)ceil_div(rows, 2), 256, 0, st>>>(ws_o, ws_ml, (bf16_t*)o, lse, rows, ns, (int)D);
+  } else {
+    QH_DEC_D(f16_t)
+    if (dp == 32) fa_decode_combine<f16_t, 32><<<(unsigned)ceil_div(rows, 8), 256, 0, st>>>(ws_o, ws_ml, (f16_t*)o, lse, rows, ns, (int)D);
+    else if (dp == 64) fa_decode_combine<f16_t, 64><<<(unsigned)ceil_div(rows, 4), 256, 0, st>>>(ws_o, ws_ml, (f16_t*)o, lse, rows, ns, (int)D);
+    else fa_decode_combine<f16_t, 128><<<(unsigned)ceil_div(rows, 2), 256, 0, st>>>(ws_o, ws_ml, (f16_t*)o, lse, rows, ns, (int)D);
+  }
+#undef QH_DEC_D
+#undef QH_DEC_G
+#undef QH_DEC
+  QH_CHECK_LAUNCH("qh_flash_decode");
+  return QH_OK;
+}

@@ -1,0 +1,145 @@
+// Shared device/host helpers for the gfx950 (MI355X) operator library.
+//
+// Everything here is written for CDNA4 only: 64-lane wavefronts, bf16 converts
+// through the hardware v_cvt_pk_bf16_f32, 16-byte global accesses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <type_traits>
+
+#include "qwen_hip.h"
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+#define QH_WAVE 64
+
+// ---------------------------------------------------------------------------
+// Error reporting: every entry point returns 0 or a QH_E* code and records a
+// thread-local message retrievable through qh_last_error().
+// ---------------------------------------------------------------------------
+namespace qh {
+
+void set_error(const char* fmt, ...);
+
+}  // namespace qh
+
+#define QH_CHECK_ARG(cond, ...)                 \
+  do {                                          \
+    if (!(cond)) {                              \
+      qh::set_error(__VA_ARGS__);               \
+      return QH_E_ARG;                          \
+    }                                           \
+  } while (0)
+
+#define QH_CHECK_LAUNCH(name)                                                  \
+  do {                                                                         \
+    hipError_t _e = hipGetLastError();                                         \
+    if (_e != hipSuccess) {                                                    \
+      qh::set_error("%s: launch failed: %s", name, hipGetErrorString(_e));     \
+      return QH_E_HIP;                                                         \
+    }                                                                          \
+  } while (0)
+
+#define QH_CHECK_HIP(expr, name)                                               \
+  do {                                                                         \
+    hipError_t _e = (expr);                                                    \
+    if (_e != hipSuccess) {                                                    \
+      qh::set_error("%s: %s", name, hipGetErrorString(_e));                    \
+      return QH_E_HIP;                                                         \
+    }                                                                          \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Scalar conversions
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) { return (float)v; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) { return (T)v; }
+
+// ---------------------------------------------------------------------------
+// 16-byte vector of N elements of T (N * sizeof(T) == 16)
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Vec16 {
+  static constexpr int N = 16 / sizeof(T);
+  union {
+    uint4 raw;
+    T v[N];
+  };
+};
+
+template <typename T>
+__device__ __forceinline__ Vec16<T> ld16(const T* p) {
+  Vec16<T> r;
+  r.raw = *reinterpret_cast<const uint4*>(p);
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void st16(T* p, const Vec16<T>& v) {
+  *reinterpret_cast<uint4*>(p) = v.raw;
+}
+
+// ---------------------------------------------------------------------------
+// Wavefront reductions (64 lanes). `width` must be a power of two <= 64 and
+// reduces within aligned groups of `width` lanes.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v, int width = QH_WAVE) {
+  for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, width);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v, int width = QH_WAVE) {
+  for (int o = width >> 1; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, width));
+  return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` must hold
+// blockDim.x / 64 floats. The result is returned to every thread.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];  // fixed order: deterministic
+  return t;
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = -INFINITY;
+  for (int i = 0; i < nw; ++i) t = fmaxf(t, red[i]);
+  return t;
+}
+
+__device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+static inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Dispatch a templated functor over the three storage dtypes.
+#define QH_DISPATCH_DTYPE(dtype, T, name, ...)                         \
+  switch (dtype) {                                                     \
+    case QH_F32: { typedef float T; __VA_ARGS__; break; }              \
+    case QH_F16: { typedef f16_t T; __VA_ARGS__; break; }              \
+    case QH_BF16: { typedef bf16_t T; __VA_ARGS__; break; }            \
+    default: qh::set_error("%s: unsupported dtype %d", name, (int)dtype); return QH_E_DTYPE; \
+  }

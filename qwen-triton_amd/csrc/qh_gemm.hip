@@ -1,0 +1,434 @@
+// GEMM for the Linear layers: C[M,N] = A(M,K) * B(N,K)^T (+ bias[N]).
+//
+// Operand views (element (i, k) of each logical operand):
+//   A(m,k) = A[m*lda + k]  (row-major, "N")   or  A[k*lda + m]  ("T")
+//   B(n,k) = B[n*ldb + k]  (row-major, "N")   or  B[k*ldb + n]  ("T")
+// which covers the three Linear products without copying any operand:
+//   forward  y  = x  W^T : A = x  [M,K] N, B = W  [N,K] N
+//   grad in  dx = dy W   : A = dy [M,N] N, B = W  [N,K] T
+//   grad wt  dW = dy^T x : A = dy [T,N] T, B = x  [T,K] T
+//
+// gfx950 design:
+//  * bf16/fp16 operands on v_mfma_f32_32x32x16_{bf16,f16}; fp32 accumulation.
+//  * 256-thread workgroups (4 wavefronts, 2x2), BK = 64, double-buffered LDS
+//    tiles stored k-contiguous with 16-byte row padding (conflict-free
+//    ds_read_b128 fragment loads); the next k-tile is fetched into registers
+//    while the current one feeds the matrix cores.
+//  * "T" operands are transposed while staging: each thread loads an 8x8 block
+//    with eight 16-byte loads and re-packs it with byte permutes, so every
+//    operand lands in LDS in the same k-contiguous layout.
+//  * Tile order is XCD-aware: the 8 XCDs each take a contiguous run of tiles
+//    (grouped 8 M-tiles at a time) so operand panels are reused out of the
+//    XCD's own L2.
+//  * M <= 8 (decode) uses a VALU GEMV that streams B once at full width.
+#include "qh_mfma.h"
+
+namespace {
+
+constexpr int BK = 64;
+constexpr int LDS_LD = BK + 8;  // padded row length (elements) of an LDS tile
+
+// Stage one operand tile (ROWS x BK) for k-tile starting at k0 into registers.
+// Non-transposed: 16-byte chunk c -> row c/8, k-chunk c%8.
+// Transposed:     8x8 sub-block sb -> row-block sb % (ROWS/8), k-block sb / (ROWS/8).
+template <typename T, int ROWS, bool TR>
+struct TileLoader {
+  static constexpr int SUBS = (ROWS + 255) / 256;          // 8x8 sub-blocks per thread (transposed)
+  static constexpr int NREG = TR ? 8 * SUBS : ROWS / 32;   // uint4 staging registers per thread
+  uint4 r[NREG];
+
+  __device__ __forceinline__ void load(const T* __restrict__ P, int64_t ld, int row0, int rows, int k0, int K) {
+    const int tid = threadIdx.x;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    if constexpr (!TR) {
+#pragma unroll
+      for (int i = 0; i < NREG; ++i) {
+        const int c = tid + i * 256;
+        const int row = c >> 3, kc = c & 7;
+        const int gr = row0 + row, gk = k0 + kc * 8;
+        r[i] = (gr < rows && gk < K) ? *reinterpret_cast<const uint4*>(P + (int64_t)gr * ld + gk) : z;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < SUBS; ++s) {
+        const int sb = tid + s * 256;
+        if (sb < ROWS) {
+          const int rb = sb % (ROWS / 8), kb = sb / (ROWS / 8);
+          const int gr = row0 + rb * 8;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int gk = k0 + kb * 8 + j;
+            r[s * 8 + j] = (gr < rows && gk < K) ? *reinterpret_cast<const uint4*>(P + (int64_t)gk * ld + gr) : z;
+          }
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(T* __restrict__ S) const {
+    const int tid = threadIdx.x;
+    if constexpr (!TR) {
+#pragma unroll
+      for (int i = 0; i < NREG; ++i) {
+        const int c = tid + i * 256;
+        const int row = c >> 3, kc = c & 7;
+        *reinterpret_cast<uint4*>(S + row * LDS_LD + kc * 8) = r[i];
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < SUBS; ++s) {
+        const int sb = tid + s * 256;
+        if (sb < ROWS) {
+          const int rb = sb % (ROWS / 8), kb = sb / (ROWS / 8);
+          uint4 in[8], out[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) in[j] = r[s * 8 + j];
+          transpose8x8(in, out);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) *reinterpret_cast<uint4*>(S + (rb * 8 + c) * LDS_LD + kb * 8) = out[c];
+        }
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+  int pid = blockIdx.x;
+  const int nblk = gridDim.x;
+  // Workgroups are dealt round-robin to the 8 XCDs; renumber so that each XCD
+  // walks a contiguous range of logical tiles.
+  if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
+  constexpr int GROUP = 8;
+  const int group_size = GROUP * tiles_n;
+  const int g = pid / group_size;
+  const int first_m = g * GROUP;
+  const int gm = min(tiles_m - first_m, GROUP);
+  const int in_group = pid - g * group_size;
+  tm = first_m + in_group % gm;
+  tn = in_group / gm;
+}
+
+template <typename T, typename OT, int BM, int BN, int WM, int WN, bool AT, bool BT>
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B,
+                                                        int64_t ldb, OT* __restrict__ C, int64_t ldc,
+                                                        const T* __restrict__ bias, int M, int N, int K,
+                                                        int tiles_m, int tiles_n) {
+  static_assert(WM * WN == 4, "4 wavefronts per workgroup");
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile must cover whole 32x32 MFMA tiles");
+  typedef typename Mfma<T>::v8 v8;
+
+  __shared__ __attribute__((aligned(16))) T smem[2][(BM + BN) * LDS_LD];
+
+  int tm_, tn_;
+  tile_coords(tiles_m, tiles_n, tm_, tn_);
+  const int m0 = tm_ * BM, n0 = tn_ * BN;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid / WN, wn = wid % WN;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  TileLoader<T, BM, AT> la;
+  TileLoader<T, BN, BT> lb;
+  const int nk = (K + BK - 1) / BK;
+
+  la.load(A, lda, m0, M, 0, K);
+  lb.load(B, ldb, n0, N, 0, K);
+  la.store(smem[0]);
+  lb.store(smem[0] + BM * LDS_LD);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      la.load(A, lda, m0, M, (kt + 1) * BK, K);
+      lb.load(B, ldb, n0, N, (kt + 1) * BK, K);
+    }
+    const T* As = smem[buf];
+    const T* Bs = smem[buf] + BM * LDS_LD;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      v8 af[TM], bf[TN];
+      const int koff = kk * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const v8*>(As + (wm * WTM + i * 32 + (lane & 31)) * LDS_LD + koff);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const v8*>(Bs + (wn * WTN + j * 32 + (lane & 31)) * LDS_LD + koff);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af[i], bf[j], acc[i][j]);
+    }
+    if (more) {
+      la.store(smem[buf ^ 1]);
+      lb.store(smem[buf ^ 1] + BM * LDS_LD);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue. MFMA 32x32 output layout: lane holds column (lane % 32) and rows
+  // 8g + 4*(lane / 32) + r for register 4g + r.
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int col = n0 + wn * WTN + j * 32 + (lane & 31);
+    if (col >= N) continue;
+    const float bv = bias ? to_f32(bias[col]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int rbase = m0 + wm * WTM + i * 32 + (lane >> 5) * 4;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = rbase + g * 8 + r;
+          if (row < M) C[(int64_t)row * ldc + col] = from_f32<OT>(acc[i][j][g * 4 + r] + bv);
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV for M <= 8 ("NN" layout: both operands k-contiguous). One wavefront
+// owns NPW output columns; lanes split K in 16-byte vectors.
+// ---------------------------------------------------------------------------
+template <typename T, typename OT, int MR, int NPW>
+__global__ __launch_bounds__(256) void gemv_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B,
+                                                   int64_t ldb, OT* __restrict__ C, int64_t ldc,
+                                                   const T* __restrict__ bias, int M, int N, int K) {
+  constexpr int VN = Vec16<T>::N;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nbase = (blockIdx.x * 4 + wid) * NPW;
+  if (nbase >= N) return;
+  float acc[MR][NPW];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int j = 0; j < NPW; ++j) acc[m][j] = 0.f;
+  for (int k = lane * VN; k < K; k += 64 * VN) {
+    Vec16<T> w[NPW];
+#pragma unroll
+    for (int j = 0; j < NPW; ++j) {
+      const int n = nbase + j;
+      if (n < N) w[j] = ld16(B + (int64_t)n * ldb + k);
+      else w[j].raw = make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m < M) {
+        Vec16<T> x = ld16(A + (int64_t)m * lda + k);
+#pragma unroll
+        for (int j = 0; j < NPW; ++j)
+#pragma unroll
+          for (int e = 0; e < VN; ++e) acc[m][j] += to_f32(x.v[e]) * to_f32(w[j].v[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int j = 0; j < NPW; ++j) acc[m][j] = wave_sum(acc[m][j]);
+  if (lane < NPW) {
+    const int n = nbase + lane;
+    if (n < N) {
+      const float bv = bias ? to_f32(bias[n]) : 0.f;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        float v = 0.f;
+#pragma unroll
+        for (int j = 0; j < NPW; ++j)
+          if (j == lane) v = acc[m][j];
+        if (m < M) C[(int64_t)m * ldc + n] = from_f32<OT>(v + bv);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic VALU GEMM (fp32 and shapes the MFMA path does not take). 64x64 tile,
+// 256 threads each owning a 4x4 block, fp32 accumulation.
+// ---------------------------------------------------------------------------
+template <typename T, typename OT, bool AT, bool BT>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(const T* __restrict__ A, int64_t lda,
+                                                           const T* __restrict__ B, int64_t ldb, OT* __restrict__ C,
+                                                           int64_t ldc, const T* __restrict__ bias, int M, int N,
+                                                           int K) {
+  __shared__ float As[16][64 + 1];
+  __shared__ float Bs[16][64 + 1];
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int e = threadIdx.x; e < 16 * 64; e += 256) {
+      const int kk = e / 64, ii = e % 64;
+      const int gk = k0 + kk;
+      const int gm = m0 + ii, gn = n0 + ii;
+      float a = 0.f, b = 0.f;
+      if (gk < K && gm < M) a = to_f32(AT ? A[(int64_t)gk * lda + gm] : A[(int64_t)gm * lda + gk]);
+      if (gk < K && gn < N) b = to_f32(BT ? B[(int64_t)gk * ldb + gn] : B[(int64_t)gn * ldb + gk]);
+      As[kk][ii] = a;
+      Bs[kk][ii] = b;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + ty * 4 + i;
+    if (row >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + tx * 4 + j;
+      if (col < N) C[(int64_t)row * ldc + col] = from_f32<OT>(acc[i][j] + (bias ? to_f32(bias[col]) : 0.f));
+    }
+  }
+}
+
+template <typename T, typename OT, int BM, int BN, int WM, int WN, bool AT, bool BT>
+void launch_mfma(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_t ldc, const T* bias, int M, int N,
+                 int K, hipStream_t st) {
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  gemm_mfma_kernel<T, OT, BM, BN, WM, WN, AT, BT><<<tm * tn, 256, 0, st>>>(A, lda, B, ldb, C, ldc, bias, M, N, K, tm, tn);
+}
+
+template <typename T, typename OT, bool AT, bool BT>
+void launch_mfma_pick(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_t ldc, const T* bias, int M,
+                      int N, int K, hipStream_t st) {
+  const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+  if (M >= 256 && N >= 256 && big_tiles >= 128)
+    launch_mfma<T, OT, 256, 256, 2, 2, AT, BT>(A, lda, B, ldb, C, ldc, bias, M, N, K, st);
+  else if (M > 64)
+    launch_mfma<T, OT, 128, 128, 2, 2, AT, BT>(A, lda, B, ldb, C, ldc, bias, M, N, K, st);
+  else
+    launch_mfma<T, OT, 64, 128, 1, 4, AT, BT>(A, lda, B, ldb, C, ldc, bias, M, N, K, st);
+}
+
+template <typename T, typename OT>
+int gemm_typed(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
+               int64_t ldc, const void* bias, hipStream_t st) {
+  const T* a = (const T*)A;
+  const T* b = (const T*)B;
+  OT* c = (OT*)C;
+  const T* bi = (const T*)bias;
+  constexpr bool is_mfma_type = !std::is_same<T, float>::value;
+  if constexpr (is_mfma_type) {
+    // GEMV path: M tiny, both operands k-contiguous.
+    if (M <= 8 && !ta && !tb && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B)) {
+      const int grid = (N + 4 * 4 - 1) / (4 * 4);
+#define QH_GEMV(mr) gemv_kernel<T, OT, mr, 4><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K)
+      if (M == 1) QH_GEMV(1);
+      else if (M == 2) QH_GEMV(2);
+      else if (M <= 4) QH_GEMV(4);
+      else QH_GEMV(8);
+#undef QH_GEMV
+      return QH_OK;
+    }
+    // MFMA path: 16-byte aligned operand rows along their contiguous dimension.
+    const bool a_ok = aligned16(A) && lda % 8 == 0 && (ta ? M % 8 == 0 : K % 8 == 0);
+    const bool b_ok = aligned16(B) && ldb % 8 == 0 && (tb ? N % 8 == 0 : K % 8 == 0);
+    if (a_ok && b_ok) {
+      if (!ta && !tb) launch_mfma_pick<T, OT, false, false>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
+      else if (!ta && tb) launch_mfma_pick<T, OT, false, true>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
+      else if (ta && tb) launch_mfma_pick<T, OT, true, true>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
+      else launch_mfma_pick<T, OT, true, false>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
+      return QH_OK;
+    }
+  }
+  dim3 grid((N + 63) / 64, (M + 63) / 64);
+  if (!ta && !tb) gemm_generic_kernel<T, OT, false, false><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K);
+  else if (!ta && tb) gemm_generic_kernel<T, OT, false, true><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K);
+  else if (ta && tb) gemm_generic_kernel<T, OT, true, true><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K);
+  else gemm_generic_kernel<T, OT, true, false><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K);
+  return QH_OK;
+}
+
+// Deterministic column sum (bias gradient): out[n] = sum_m X[m, n].
+template <typename T, typename OT>
+__global__ __launch_bounds__(256) void colsum_kernel(const T* __restrict__ X, int64_t ldx, int M, int N,
+                                                     OT* __restrict__ out) {
+  __shared__ float part[16][17];
+  const int cl = threadIdx.x & 15, sub = threadIdx.x >> 4;
+  const int n = blockIdx.x * 16 + cl;
+  float s = 0.f;
+  if (n < N)
+    for (int m = sub; m < M; m += 16) s += to_f32(X[(int64_t)m * ldx + n]);
+  part[sub][cl] = s;
+  __syncthreads();
+  if (sub == 0 && n < N) {
+    float t = 0.f;
+    for (int i = 0; i < 16; ++i) t += part[i][cl];
+    out[n] = from_f32<OT>(t);
+  }
+}
+
+}  // namespace
+
+extern "C" int qh_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                       const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
+                       void* stream) {
+  QH_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "qh_gemm: negative shape");
+  QH_CHECK_ARG(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31), "qh_gemm: dimension exceeds 2^31");
+  QH_CHECK_ARG(ldc >= N, "qh_gemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
+  QH_CHECK_ARG(trans_a ? lda >= M : lda >= K, "qh_gemm: lda too small");
+  QH_CHECK_ARG(trans_b ? ldb >= N : ldb >= K, "qh_gemm: ldb too small");
+  if (M == 0 || N == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (K == 0) {
+    QH_CHECK_ARG(bias == nullptr && ldc == N, "qh_gemm: K == 0 with bias or strided C is not supported");
+    return qh_zero(C, M * N * (out_dtype == QH_F32 ? 4 : 2), stream);
+  }
+  int rc = QH_OK;
+#define QH_GEMM_OUT(T)                                                                                           \
+  switch (out_dtype) {                                                                                          \
+    case QH_F32: rc = gemm_typed<T, float>(trans_a, trans_b, (int)M, (int)N, (int)K, A, lda, B, ldb, C, ldc, bias, st); break; \
+    case QH_F16: rc = gemm_typed<T, f16_t>(trans_a, trans_b, (int)M, (int)N, (int)K, A, lda, B, ldb, C, ldc, bias, st); break; \
+    case QH_BF16: rc = gemm_typed<T, bf16_t>(trans_a, trans_b, (int)M, (int)N, (int)K, A, lda, B, ldb, C, ldc, bias, st); break; \
+    default: qh::set_error("qh_gemm: bad out dtype %d", out_dtype); return QH_E_DTYPE;                          \
+  }
+  QH_DISPATCH_DTYPE(dtype, T, "qh_gemm", QH_GEMM_OUT(T));
+#undef QH_GEMM_OUT
+  if (rc) return rc;
+  QH_CHECK_LAUNCH("qh_gemm");
+  return QH_OK;
+}
+
+extern "C" int qh_colsum(const void* X, int64_t ldx, int64_t M, int64_t N, void* out, int dtype, int out_dtype,
+                         void* stream) {
+  QH_CHECK_ARG(M >= 0 && N >= 0 && ldx >= N, "qh_colsum: bad shape");
+  QH_CHECK_ARG(M < (1ll << 31) && N < (1ll << 31), "qh_colsum: dimension exceeds 2^31");
+  if (N == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int grid = (int)ceil_div(N, 16);
+#define QH_CS_OUT(T)                                                                                         \
+  switch (out_dtype) {                                                                                      \
+    case QH_F32: colsum_kernel<T, float><<<grid, 256, 0, st>>>((const T*)X, ldx, (int)M, (int)N, (float*)out); break; \
+    case QH_F16: colsum_kernel<T, f16_t><<<grid, 256, 0, st>>>((const T*)X, ldx, (int)M, (int)N, (f16_t*)out); break; \
+    case QH_BF16: colsum_kernel<T, bf16_t><<<grid, 256, 0, st>>>((const T*)X, ldx, (int)M, (int)N, (bf16_t*)out); break; \
+    default: qh::set_error("qh_colsum: bad out dtype"); return QH_E_DTYPE;                                  \
+  }
+  QH_DISPATCH_DTYPE(dtype, T, "qh_colsum", QH_CS_OUT(T));
+#undef QH_CS_OUT
+  QH_CHECK_LAUNCH("qh_colsum");
+  return QH_OK;
+}

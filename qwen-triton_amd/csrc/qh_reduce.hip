@@ -1,0 +1,779 @@
+// Row-reduction operators: RMSNorm (fwd/bwd), softmax (fwd/bwd), cross-entropy
+// (fwd/bwd), top-k and one-hot.
+//
+// Row kernels map a row onto a group of G lanes (G in {8,16,32,64}) that each
+// keep NV 16-byte vectors of the row in registers, so a row is read from HBM
+// exactly once and reductions are register + DPP shuffles only. Rows that do
+// not fit that shape take a one-block-per-row path. Every reduction uses a fixed
+// order, so results are bitwise reproducible run to run (no float atomics).
+#include "qh_common.h"
+
+namespace {
+
+static int grid_cap(int64_t work, int64_t cap = 8192) {
+  if (work < 1) return 1;
+  return (int)(work < cap ? work : cap);
+}
+
+// Pick a (lanes-per-row G, vectors-per-lane NV) shape for a row of `cols`
+// elements of a type with VN elements per 16 bytes. 0 = no fast path.
+static int pick_row_shape(int64_t cols, int VN, int& G, int& NV) {
+  if (cols <= 0 || cols % VN) return 0;
+  const int64_t nv = cols / VN;
+  if (nv <= 8) { G = 8; NV = 1; }
+  else if (nv <= 16) { G = 16; NV = 1; }
+  else if (nv <= 32) { G = 32; NV = 1; }
+  else if (nv <= 64) { G = 64; NV = 1; }
+  else if (nv <= 128) { G = 64; NV = 2; }
+  else if (nv <= 256) { G = 64; NV = 4; }
+  else if (nv <= 512) { G = 64; NV = 8; }
+  else return 0;
+  return 1;
+}
+
+
+__device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
+  if (dtype == QH_F32) return ((const float*)p)[i];
+  if (dtype == QH_F16) return (float)((const f16_t*)p)[i];
+  return (float)((const bf16_t*)p)[i];
+}
+
+__device__ __forceinline__ void store_any(void* p, int dtype, int64_t i, float v) {
+  if (dtype == QH_F32) ((float*)p)[i] = v;
+  else if (dtype == QH_F16) ((f16_t*)p)[i] = (f16_t)v;
+  else ((bf16_t*)p)[i] = (bf16_t)v;
+}
+
+// ===========================================================================
+// RMSNorm
+// ===========================================================================
+template <typename T, int G, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_fast(const T* __restrict__ x, const void* __restrict__ w,
+                                                        int wdtype, T* __restrict__ y, int64_t rows, int cols,
+                                                        float eps, float wadd) {
+  constexpr int VN = Vec16<T>::N;
+  constexpr int RPB = 256 / G;
+  const int grp = threadIdx.x / G, g = threadIdx.x % G;
+  for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
+    const T* xr = x + row * cols;
+    Vec16<T> xv[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        xv[i] = ld16(xr + c);
+#pragma unroll
+        for (int j = 0; j < VN; ++j) {
+          const float f = to_f32(xv[i].v[j]);
+          ss += f * f;
+        }
+      }
+    }
+    ss = wave_sum(ss, G);
+    const float inv = rsqrtf(ss / (float)cols + eps);
+    T* yr = y + row * cols;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        Vec16<T> o;
+#pragma unroll
+        for (int j = 0; j < VN; ++j)
+          o.v[j] = from_f32<T>((to_f32(xv[i].v[j]) * inv) * (load_any(w, wdtype, c + j) + wadd));
+        st16(yr + c, o);
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_generic(const T* __restrict__ x, const void* __restrict__ w,
+                                                           int wdtype, T* __restrict__ y, int64_t rows,
+                                                           int64_t cols, float eps, float wadd) {
+  __shared__ float red[4];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const T* xr = x + row * cols;
+    float ss = 0.f;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      const float f = to_f32(xr[c]);
+      ss += f * f;
+    }
+    ss = block_sum(ss, red);
+    const float inv = rsqrtf(ss / (float)cols + eps);
+    for (int64_t c = threadIdx.x; c < cols; c += 256)
+      y[row * cols + c] = from_f32<T>((to_f32(xr[c]) * inv) * (load_any(w, wdtype, c) + wadd));
+  }
+}
+
+// Backward, fast path. Each row-group accumulates its dW partial in registers
+// over the rows it visits and writes one partial row to ws at the end:
+// ws[(blockIdx.x * RPB + grp) * cols + c].
+template <typename T, int G, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_fast(const T* __restrict__ x, const void* __restrict__ w,
+                                                        int wdtype, const T* __restrict__ gy, T* __restrict__ gx,
+                                                        float* __restrict__ ws, int64_t rows, int cols, float eps,
+                                                        float wadd) {
+  constexpr int VN = Vec16<T>::N;
+  constexpr int RPB = 256 / G;
+  const int grp = threadIdx.x / G, g = threadIdx.x % G;
+  float pw[NV][VN];
+  float sw[NV][VN];
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int j = 0; j < VN; ++j) {
+      pw[i][j] = 0.f;
+      const int c = (i * G + g) * VN + j;
+      sw[i][j] = (c < cols) ? load_any(w, wdtype, c) + wadd : 0.f;
+    }
+  const float inv_cols = 1.0f / (float)cols;
+  for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
+    const T* xr = x + row * cols;
+    const T* gr = gy + row * cols;
+    Vec16<T> xv[NV], gv[NV];
+    float ss = 0.f, dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        xv[i] = ld16(xr + c);
+        gv[i] = ld16(gr + c);
+#pragma unroll
+        for (int j = 0; j < VN; ++j) {
+          const float xf = to_f32(xv[i].v[j]), gf = to_f32(gv[i].v[j]);
+          ss += xf * xf;
+          dot += gf * sw[i][j] * xf;
+        }
+      }
+    }
+    ss = wave_sum(ss, G);
+    dot = wave_sum(dot, G);
+    const float inv = rsqrtf(ss * inv_cols + eps);
+    const float k3 = inv * inv * inv * inv_cols * dot;
+    T* gxr = gx + row * cols;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        Vec16<T> o;
+#pragma unroll
+        for (int j = 0; j < VN; ++j) {
+          const float xf = to_f32(xv[i].v[j]), gf = to_f32(gv[i].v[j]);
+          o.v[j] = from_f32<T>(gf * sw[i][j] * inv - xf * k3);
+          pw[i][j] += gf * (xf * inv);
+        }
+        st16(gxr + c, o);
+      }
+    }
+  }
+  float* wr = ws + ((int64_t)blockIdx.x * RPB + grp) * cols;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * G + g) * VN;
+    if (c < cols) {
+#pragma unroll
+      for (int j = 0; j < VN; ++j) wr[c + j] = pw[i][j];
+    }
+  }
+}
+
+// Backward, generic path: block owns ws row blockIdx.x; thread t owns columns
+// t, t+256, ... of that row, so the partial needs no atomics.
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_generic(const T* __restrict__ x, const void* __restrict__ w,
+                                                           int wdtype, const T* __restrict__ gy,
+                                                           T* __restrict__ gx, float* __restrict__ ws,
+                                                           int64_t rows, int64_t cols, float eps, float wadd) {
+  __shared__ float red[4];
+  float* wr = ws + (int64_t)blockIdx.x * cols;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) wr[c] = 0.f;
+  const float inv_cols = 1.0f / (float)cols;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const T* xr = x + row * cols;
+    const T* gr = gy + row * cols;
+    float ss = 0.f, dot = 0.f;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      const float xf = to_f32(xr[c]), gf = to_f32(gr[c]);
+      ss += xf * xf;
+      dot += gf * (load_any(w, wdtype, c) + wadd) * xf;
+    }
+    ss = block_sum(ss, red);
+    dot = block_sum(dot, red);
+    const float inv = rsqrtf(ss * inv_cols + eps);
+    const float k3 = inv * inv * inv * inv_cols * dot;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      const float xf = to_f32(xr[c]), gf = to_f32(gr[c]);
+      gx[row * cols + c] = from_f32<T>(gf * (load_any(w, wdtype, c) + wadd) * inv - xf * k3);
+      wr[c] += gf * (xf * inv);
+    }
+  }
+}
+
+// Stage 2: gw[c] = sum_r ws[r, c], 16 columns x 16 sub-rows per block; each
+// sub-row sums a fixed stride of partial rows, then the 16 sub-sums are added
+// in order. Deterministic.
+__global__ __launch_bounds__(256) void colsum_partials(const float* __restrict__ ws, int64_t nrows, int64_t cols,
+                                                       void* __restrict__ out, int odtype) {
+  __shared__ float part[16][17];
+  const int cl = threadIdx.x & 15, sub = threadIdx.x >> 4;
+  const int64_t c = blockIdx.x * 16 + cl;
+  float s = 0.f;
+  if (c < cols)
+    for (int64_t r = sub; r < nrows; r += 16) s += ws[r * cols + c];
+  part[sub][cl] = s;
+  __syncthreads();
+  if (sub == 0 && c < cols) {
+    float t = 0.f;
+    for (int i = 0; i < 16; ++i) t += part[i][cl];
+    store_any(out, odtype, c, t);
+  }
+}
+
+static const int kRmsBwdBlocks = 256;
+
+// ===========================================================================
+// Softmax
+// ===========================================================================
+template <typename T, int G, int NV>
+__global__ __launch_bounds__(256) void softmax_fwd_fast(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
+                                                        int cols) {
+  constexpr int VN = Vec16<T>::N;
+  constexpr int RPB = 256 / G;
+  const int grp = threadIdx.x / G, g = threadIdx.x % G;
+  for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
+    const T* xr = x + row * cols;
+    float v[NV][VN];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        Vec16<T> t = ld16(xr + c);
+#pragma unroll
+        for (int j = 0; j < VN; ++j) {
+          v[i][j] = to_f32(t.v[j]);
+          m = fmaxf(m, v[i][j]);
+        }
+      }
+    }
+    m = wave_max(m, G);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+#pragma unroll
+        for (int j = 0; j < VN; ++j) {
+          v[i][j] = fast_exp(v[i][j] - m);
+          s += v[i][j];
+        }
+      }
+    }
+    s = wave_sum(s, G);
+    const float rs = 1.0f / s;
+    T* yr = y + row * cols;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        Vec16<T> o;
+#pragma unroll
+        for (int j = 0; j < VN; ++j) o.v[j] = from_f32<T>(v[i][j] * rs);
+        st16(yr + c, o);
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_fwd_generic(const T* __restrict__ x, T* __restrict__ y,
+                                                           int64_t rows, int64_t cols) {
+  __shared__ float red[4];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const T* xr = x + row * cols;
+    float m = -INFINITY;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) m = fmaxf(m, to_f32(xr[c]));
+    m = block_max(m, red);
+    float s = 0.f;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) s += fast_exp(to_f32(xr[c]) - m);
+    s = block_sum(s, red);
+    const float rs = 1.0f / s;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) y[row * cols + c] = from_f32<T>(fast_exp(to_f32(xr[c]) - m) * rs);
+  }
+}
+
+template <typename T, int G, int NV>
+__global__ __launch_bounds__(256) void softmax_bwd_fast(const T* __restrict__ y, const T* __restrict__ gy,
+                                                        T* __restrict__ gx, int64_t rows, int cols) {
+  constexpr int VN = Vec16<T>::N;
+  constexpr int RPB = 256 / G;
+  const int grp = threadIdx.x / G, g = threadIdx.x % G;
+  for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
+    Vec16<T> yv[NV], gv[NV];
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        yv[i] = ld16(y + row * cols + c);
+        gv[i] = ld16(gy + row * cols + c);
+#pragma unroll
+        for (int j = 0; j < VN; ++j) dot += to_f32(yv[i].v[j]) * to_f32(gv[i].v[j]);
+      }
+    }
+    dot = wave_sum(dot, G);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        Vec16<T> o;
+#pragma unroll
+        for (int j = 0; j < VN; ++j) o.v[j] = from_f32<T>(to_f32(yv[i].v[j]) * (to_f32(gv[i].v[j]) - dot));
+        st16(gx + row * cols + c, o);
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_bwd_generic(const T* __restrict__ y, const T* __restrict__ gy,
+                                                           T* __restrict__ gx, int64_t rows, int64_t cols) {
+  __shared__ float red[4];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    float dot = 0.f;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) dot += to_f32(y[row * cols + c]) * to_f32(gy[row * cols + c]);
+    dot = block_sum(dot, red);
+    for (int64_t c = threadIdx.x; c < cols; c += 256)
+      gx[row * cols + c] = from_f32<T>(to_f32(y[row * cols + c]) * (to_f32(gy[row * cols + c]) - dot));
+  }
+}
+
+// ===========================================================================
+// Cross-entropy: one 256-thread block per row, single pass online logsumexp.
+// ===========================================================================
+__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+  const float M = fmaxf(m, m2);
+  if (M == -INFINITY) return;
+  const float a = (m == -INFINITY) ? 0.f : s * fast_exp(m - M);
+  const float b = (m2 == -INFINITY) ? 0.f : s2 * fast_exp(m2 - M);
+  m = M;
+  s = a + b;
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void ce_fwd_kernel(const T* __restrict__ logits, int64_t stride,
+                                                     const int64_t* __restrict__ tgt, float* __restrict__ lse,
+                                                     float* __restrict__ loss, int64_t V, int64_t ignore) {
+  __shared__ float sm[4], ssum[4];
+  const int64_t row = blockIdx.x;
+  const int64_t t = tgt[row];
+  if (t == ignore) {
+    if (threadIdx.x == 0) {
+      loss[row] = 0.f;
+      lse[row] = 0.f;
+    }
+    return;
+  }
+  const T* xr = logits + row * stride;
+  float m = -INFINITY, s = 0.f;
+  if constexpr (VEC) {
+    constexpr int VN = Vec16<T>::N;
+    for (int64_t c = threadIdx.x * VN; c < V; c += 256 * VN) {
+      Vec16<T> v = ld16(xr + c);
+      float lm = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < VN; ++j) lm = fmaxf(lm, to_f32(v.v[j]));
+      if (lm > m) {
+        s = (m == -INFINITY) ? 0.f : s * fast_exp(m - lm);
+        m = lm;
+      }
+      if (m != -INFINITY) {
+#pragma unroll
+        for (int j = 0; j < VN; ++j) s += fast_exp(to_f32(v.v[j]) - m);
+      }
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < V; c += 256) {
+      const float f = to_f32(xr[c]);
+      if (f > m) {
+        s = (m == -INFINITY) ? 0.f : s * fast_exp(m - f);
+        m = f;
+      }
+      if (m != -INFINITY) s += fast_exp(f - m);
+    }
+  }
+  // wave merge (fixed xor tree), then block merge in wave order
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+    lse_merge(m, s, m2, s2);
+  }
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) {
+    sm[wid] = m;
+    ssum[wid] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = sm[0], S = ssum[0];
+    for (int i = 1; i < 4; ++i) lse_merge(M, S, sm[i], ssum[i]);
+    const float l = M + __logf(S);
+    const float xt = (t >= 0 && t < V) ? to_f32(xr[t]) : __int_as_float(0x7fc00000);
+    lse[row] = l;
+    loss[row] = l - xt;
+  }
+}
+
+// loss_out = sum(loss) / max(1, n_valid); nvalid_out = n_valid.
+__global__ __launch_bounds__(1024) void ce_finalize(const float* __restrict__ loss, const int64_t* __restrict__ tgt,
+                                                    int64_t N, int64_t ignore, float* __restrict__ loss_out,
+                                                    float* __restrict__ nvalid_out) {
+  __shared__ float red[16];
+  float s = 0.f, n = 0.f;
+  for (int64_t i = threadIdx.x; i < N; i += 1024) {
+    s += loss[i];
+    n += (tgt[i] != ignore) ? 1.f : 0.f;
+  }
+  s = block_sum(s, red);
+  n = block_sum(n, red);
+  if (threadIdx.x == 0) {
+    loss_out[0] = s / fmaxf(n, 1.f);
+    nvalid_out[0] = n;
+  }
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void ce_bwd_kernel(const T* __restrict__ logits, int64_t stride,
+                                                     const int64_t* __restrict__ tgt, const float* __restrict__ lse,
+                                                     const float* __restrict__ gloss, const float* __restrict__ nvalid,
+                                                     T* __restrict__ g, int64_t gstride, int64_t V, int64_t ignore) {
+  const int64_t row = blockIdx.x;
+  const int64_t t = tgt[row];
+  T* gr = g + row * gstride;
+  const T* xr = logits + row * stride;
+  const bool ign = (t == ignore);
+  const float scale = gloss[0] / fmaxf(nvalid[0], 1.f);
+  const float l = lse[row];
+  if constexpr (VEC) {
+    constexpr int VN = Vec16<T>::N;
+    for (int64_t c = threadIdx.x * VN; c < V; c += 256 * VN) {
+      Vec16<T> o;
+      if (ign) {
+        o.raw = make_uint4(0, 0, 0, 0);
+      } else {
+        Vec16<T> v = ld16(xr + c);
+#pragma unroll
+        for (int j = 0; j < VN; ++j) {
+          const float p = fast_exp(to_f32(v.v[j]) - l);
+          o.v[j] = from_f32<T>((p - ((c + j) == t ? 1.f : 0.f)) * scale);
+        }
+      }
+      st16(gr + c, o);
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < V; c += 256) {
+      float r = 0.f;
+      if (!ign) r = (fast_exp(to_f32(xr[c]) - l) - (c == t ? 1.f : 0.f)) * scale;
+      gr[c] = from_f32<T>(r);
+    }
+  }
+}
+
+// ===========================================================================
+// Top-k: one wave per row. Selection order: larger value first, equal values
+// by lower index. Round r picks the best element strictly after the (r-1)-th
+// pick in that order, so the input is never modified.
+// ===========================================================================
+__device__ __forceinline__ bool topk_better(float v, int i, float bv, int bi) {
+  return bi < 0 || v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ bool topk_after(float v, int i, float lv, int li) {
+  return v < lv || (v == lv && i > li);
+}
+
+template <typename T, int CPL>
+__global__ __launch_bounds__(256) void topk_kernel(const T* __restrict__ x, T* __restrict__ vals,
+                                                   int64_t* __restrict__ idx, int64_t N, int C, int k) {
+  const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= N) return;
+  const T* xr = x + row * C;
+  float cv[CPL > 0 ? CPL : 1];
+  if constexpr (CPL > 0) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = i * 64 + lane;
+      cv[i] = (c < C) ? to_f32(xr[c]) : -INFINITY;
+    }
+  }
+  float lv = INFINITY;
+  int li = -1;
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int bi = -1;
+    if constexpr (CPL > 0) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = i * 64 + lane;
+        if (c < C && topk_after(cv[i], c, lv, li) && topk_better(cv[i], c, bv, bi)) {
+          bv = cv[i];
+          bi = c;
+        }
+      }
+    } else {
+      for (int c = lane; c < C; c += 64) {
+        const float v = to_f32(xr[c]);
+        if (topk_after(v, c, lv, li) && topk_better(v, c, bv, bi)) {
+          bv = v;
+          bi = c;
+        }
+      }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const float v2 = __shfl_xor(bv, o);
+      const int i2 = __shfl_xor(bi, o);
+      if (i2 >= 0 && topk_better(v2, i2, bv, bi)) {
+        bv = v2;
+        bi = i2;
+      }
+    }
+    if (lane == 0) {
+      vals[row * k + r] = from_f32<T>(bi >= 0 ? bv : __int_as_float(0x7fc00000));
+      idx[row * k + r] = bi;
+    }
+    lv = bv;
+    li = bi;
+    if (bi < 0) lv = -INFINITY, li = 0x7fffffff;
+  }
+}
+
+__global__ __launch_bounds__(256) void one_hot_kernel(const int64_t* __restrict__ idx, int64_t* __restrict__ out,
+                                                      int64_t N, int64_t C, int64_t total) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / C, c = i - n * C;
+    out[i] = (idx[n] == c) ? 1 : 0;
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Host launchers (shape selection happens here, outside the dtype dispatch)
+// ---------------------------------------------------------------------------
+#define QH_SHAPE_SWITCH(KERNEL, ...)                                             \
+  if (G == 8 && NV == 1) KERNEL<T, 8, 1><<<grid, 256, 0, st>>>(__VA_ARGS__);     \
+  else if (G == 16 && NV == 1) KERNEL<T, 16, 1><<<grid, 256, 0, st>>>(__VA_ARGS__); \
+  else if (G == 32 && NV == 1) KERNEL<T, 32, 1><<<grid, 256, 0, st>>>(__VA_ARGS__); \
+  else if (G == 64 && NV == 1) KERNEL<T, 64, 1><<<grid, 256, 0, st>>>(__VA_ARGS__); \
+  else if (G == 64 && NV == 2) KERNEL<T, 64, 2><<<grid, 256, 0, st>>>(__VA_ARGS__); \
+  else if (G == 64 && NV == 4) KERNEL<T, 64, 4><<<grid, 256, 0, st>>>(__VA_ARGS__); \
+  else if (G == 64 && NV == 8) KERNEL<T, 64, 8><<<grid, 256, 0, st>>>(__VA_ARGS__);
+
+template <typename T>
+static void launch_rms_fwd(const void* x, const void* w, int wdtype, void* y, int64_t rows, int64_t cols, float eps,
+                           float wadd, hipStream_t st) {
+  int G = 0, NV = 0;
+  if (pick_row_shape(cols, Vec16<T>::N, G, NV) && aligned16(x) && aligned16(y)) {
+    const int grid = grid_cap(ceil_div(rows, 256 / G));
+    QH_SHAPE_SWITCH(rmsnorm_fwd_fast, (const T*)x, w, wdtype, (T*)y, rows, (int)cols, eps, wadd)
+  } else {
+    rmsnorm_fwd_generic<T><<<grid_cap(rows), 256, 0, st>>>((const T*)x, w, wdtype, (T*)y, rows, cols, eps, wadd);
+  }
+}
+
+template <typename T>
+static void launch_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t st) {
+  int G = 0, NV = 0;
+  if (pick_row_shape(cols, Vec16<T>::N, G, NV) && aligned16(x) && aligned16(y)) {
+    const int grid = grid_cap(ceil_div(rows, 256 / G));
+    QH_SHAPE_SWITCH(softmax_fwd_fast, (const T*)x, (T*)y, rows, (int)cols)
+  } else {
+    softmax_fwd_generic<T><<<grid_cap(rows), 256, 0, st>>>((const T*)x, (T*)y, rows, cols);
+  }
+}
+
+template <typename T>
+static void launch_softmax_bwd(const void* y, const void* gy, void* gx, int64_t rows, int64_t cols, hipStream_t st) {
+  int G = 0, NV = 0;
+  if (pick_row_shape(cols, Vec16<T>::N, G, NV) && aligned16(y) && aligned16(gy) && aligned16(gx)) {
+    const int grid = grid_cap(ceil_div(rows, 256 / G));
+    QH_SHAPE_SWITCH(softmax_bwd_fast, (const T*)y, (const T*)gy, (T*)gx, rows, (int)cols)
+  } else {
+    softmax_bwd_generic<T><<<grid_cap(rows), 256, 0, st>>>((const T*)y, (const T*)gy, (T*)gx, rows, cols);
+  }
+}
+
+template <typename T>
+static void launch_topk(const void* x, void* vals, int64_t* idx, int64_t N, int64_t C, int64_t k, hipStream_t st) {
+  const int grid = (int)ceil_div(N, 4);
+  const int cpl = (int)ceil_div(C, 64);
+  if (cpl <= 1) topk_kernel<T, 1><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
+  else if (cpl <= 2) topk_kernel<T, 2><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
+  else if (cpl <= 4) topk_kernel<T, 4><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
+  else if (cpl <= 8) topk_kernel<T, 8><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
+  else if (cpl <= 16) topk_kernel<T, 16><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
+  else topk_kernel<T, 0><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" int qh_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t cols, float eps,
+                              int one_plus, int dtype, int wdtype, void* stream) {
+  QH_CHECK_ARG(rows >= 0 && cols >= 0, "qh_rmsnorm_fwd: negative shape");
+  QH_CHECK_ARG(wdtype >= QH_F32 && wdtype <= QH_BF16, "qh_rmsnorm_fwd: bad weight dtype");
+  if (rows == 0 || cols == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const float wadd = one_plus ? 1.f : 0.f;
+  QH_DISPATCH_DTYPE(dtype, T, "qh_rmsnorm_fwd", launch_rms_fwd<T>(x, w, wdtype, y, rows, cols, eps, wadd, st));
+  QH_CHECK_LAUNCH("qh_rmsnorm_fwd");
+  return QH_OK;
+}
+
+static int64_t rms_bwd_partial_rows(int64_t rows, int64_t cols, int dtype, int* fast_grid, int* G_out, int* NV_out) {
+  const int VN = dtype == QH_F32 ? 4 : 8;
+  int G = 0, NV = 0;
+  if (pick_row_shape(cols, VN, G, NV)) {
+    const int rpb = 256 / G;
+    int64_t grid = ceil_div(rows, rpb);
+    if (grid > kRmsBwdBlocks) grid = kRmsBwdBlocks;
+    if (grid < 1) grid = 1;
+    if (fast_grid) *fast_grid = (int)grid;
+    if (G_out) *G_out = G;
+    if (NV_out) *NV_out = NV;
+    return grid * rpb;
+  }
+  if (fast_grid) *fast_grid = 0;
+  return 0;
+}
+
+template <typename T>
+static int64_t launch_rms_bwd(const void* x, const void* w, int wdtype, const void* gy, void* gx, void* ws,
+                              int64_t rows, int64_t cols, float eps, float wadd, int dtype, hipStream_t st) {
+  int grid = 0, G = 0, NV = 0;
+  const int64_t fr = rms_bwd_partial_rows(rows, cols, dtype, &grid, &G, &NV);
+  if (fr > 0 && aligned16(x) && aligned16(gy) && aligned16(gx)) {
+    QH_SHAPE_SWITCH(rmsnorm_bwd_fast, (const T*)x, w, wdtype, (const T*)gy, (T*)gx, (float*)ws, rows, (int)cols, eps, wadd)
+    return fr;
+  }
+  const int g = (int)(rows < kRmsBwdBlocks ? rows : kRmsBwdBlocks);
+  rmsnorm_bwd_generic<T><<<g, 256, 0, st>>>((const T*)x, w, wdtype, (const T*)gy, (T*)gx, (float*)ws, rows, cols,
+                                            eps, wadd);
+  return g;
+}
+
+extern "C" int64_t qh_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const int64_t fast_rows = rms_bwd_partial_rows(rows, cols, dtype, nullptr, nullptr, nullptr);
+  const int64_t gen_rows = rows < kRmsBwdBlocks ? rows : kRmsBwdBlocks;
+  const int64_t r = fast_rows > gen_rows ? fast_rows : gen_rows;
+  return r * cols * (int64_t)sizeof(float);
+}
+
+extern "C" int qh_rmsnorm_bwd(const void* x, const void* w, const void* gy, void* gx, void* gw, void* ws,
+                              int64_t ws_bytes, int64_t rows, int64_t cols, float eps, int one_plus, int dtype,
+                              int wdtype, void* stream) {
+  QH_CHECK_ARG(rows >= 0 && cols >= 0, "qh_rmsnorm_bwd: negative shape");
+  QH_CHECK_ARG(wdtype >= QH_F32 && wdtype <= QH_BF16, "qh_rmsnorm_bwd: bad weight dtype");
+  if (cols == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (rows == 0) return qh_zero(gw, cols * (wdtype == QH_F32 ? 4 : 2), stream);
+  const int64_t need = qh_rmsnorm_bwd_workspace(rows, cols, dtype);
+  if (ws_bytes < need) {
+    qh::set_error("qh_rmsnorm_bwd: workspace %lld bytes < required %lld", (long long)ws_bytes, (long long)need);
+    return QH_E_WORKSPACE;
+  }
+  const float wadd = one_plus ? 1.f : 0.f;
+  int64_t prow = 0;
+  QH_DISPATCH_DTYPE(dtype, T, "qh_rmsnorm_bwd",
+                    prow = launch_rms_bwd<T>(x, w, wdtype, gy, gx, ws, rows, cols, eps, wadd, dtype, st));
+  colsum_partials<<<(int)ceil_div(cols, 16), 256, 0, st>>>((const float*)ws, prow, cols, gw, wdtype);
+  QH_CHECK_LAUNCH("qh_rmsnorm_bwd");
+  return QH_OK;
+}
+
+extern "C" int qh_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int dtype, void* stream) {
+  QH_CHECK_ARG(rows >= 0 && cols >= 0, "qh_softmax_fwd: negative shape");
+  if (rows == 0 || cols == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  QH_DISPATCH_DTYPE(dtype, T, "qh_softmax_fwd", launch_softmax_fwd<T>(x, y, rows, cols, st));
+  QH_CHECK_LAUNCH("qh_softmax_fwd");
+  return QH_OK;
+}
+
+extern "C" int qh_softmax_bwd(const void* y, const void* gy, void* gx, int64_t rows, int64_t cols, int dtype,
+                              void* stream) {
+  QH_CHECK_ARG(rows >= 0 && cols >= 0, "qh_softmax_bwd: negative shape");
+  if (rows == 0 || cols == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  QH_DISPATCH_DTYPE(dtype, T, "qh_softmax_bwd", launch_softmax_bwd<T>(y, gy, gx, rows, cols, st));
+  QH_CHECK_LAUNCH("qh_softmax_bwd");
+  return QH_OK;
+}
+
+extern "C" int qh_ce_fwd(const void* logits, int64_t stride, const int64_t* targets, float* lse, float* loss_rows,
+                         float* loss_out, float* nvalid_out, int64_t N, int64_t V, int64_t ignore_index, int dtype, void* stream) {
+  QH_CHECK_ARG(N >= 0 && V > 0 && stride >= V, "qh_ce_fwd: bad shape N=%lld V=%lld stride=%lld", (long long)N,
+               (long long)V, (long long)stride);
+  QH_CHECK_ARG(N < (1ll << 31), "qh_ce_fwd: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  if (N > 0) {
+    QH_DISPATCH_DTYPE(dtype, T, "qh_ce_fwd", {
+      constexpr int VN = Vec16<T>::N;
+      if (aligned16(logits) && V % VN == 0 && stride % VN == 0)
+        ce_fwd_kernel<T, true><<<(int)N, 256, 0, st>>>((const T*)logits, stride, targets, lse, loss_rows, V,
+                                                       ignore_index);
+      else
+        ce_fwd_kernel<T, false><<<(int)N, 256, 0, st>>>((const T*)logits, stride, targets, lse, loss_rows, V,
+                                                        ignore_index);
+    });
+  }
+  ce_finalize<<<1, 1024, 0, st>>>(loss_rows, targets, N, ignore_index, loss_out, nvalid_out);
+  QH_CHECK_LAUNCH("qh_ce_fwd");
+  return QH_OK;
+}
+
+extern "C" int qh_ce_bwd(const void* logits, int64_t stride, const int64_t* targets, const float* lse,
+                         const float* grad_loss, const float* nvalid, void* glogits, int64_t gstride, int64_t N,
+                         int64_t V, int64_t ignore_index, int dtype, void* stream) {
+  QH_CHECK_ARG(N >= 0 && V > 0 && stride >= V && gstride >= V, "qh_ce_bwd: bad shape");
+  QH_CHECK_ARG(N < (1ll << 31), "qh_ce_bwd: too many rows");
+  if (N == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  QH_DISPATCH_DTYPE(dtype, T, "qh_ce_bwd", {
+    constexpr int VN = Vec16<T>::N;
+    if (aligned16(logits) && aligned16(glogits) && V % VN == 0 && stride % VN == 0 && gstride % VN == 0)
+      ce_bwd_kernel<T, true><<<(int)N, 256, 0, st>>>((const T*)logits, stride, targets, lse, grad_loss, nvalid,
+                                                     (T*)glogits, gstride, V, ignore_index);
+    else
+      ce_bwd_kernel<T, false><<<(int)N, 256, 0, st>>>((const T*)logits, stride, targets, lse, grad_loss, nvalid,
+                                                      (T*)glogits, gstride, V, ignore_index);
+  });
+  QH_CHECK_LAUNCH("qh_ce_bwd");
+  return QH_OK;
+}
+
+extern "C" int qh_topk(const void* x, void* vals, int64_t* idx, int64_t N, int64_t C, int64_t k, int dtype,
+                       void* stream) {
+  QH_CHECK_ARG(N >= 0 && C >= 0 && k >= 0, "qh_topk: negative shape");
+  QH_CHECK_ARG(k <= C, "qh_topk: k=%lld > C=%lld", (long long)k, (long long)C);
+  QH_CHECK_ARG(C < (1ll << 30), "qh_topk: C too large");
+  if (N == 0 || k == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  QH_DISPATCH_DTYPE(dtype, T, "qh_topk", launch_topk<T>(x, vals, idx, N, C, k, st));
+  QH_CHECK_LAUNCH("qh_topk");
+  return QH_OK;
+}
+
+extern "C" int qh_one_hot(const int64_t* idx, int64_t* out, int64_t N, int64_t C, void* stream) {
+  QH_CHECK_ARG(N >= 0 && C >= 0, "qh_one_hot: negative shape");
+  const int64_t total = N * C;
+  if (total == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  one_hot_kernel<<<grid_cap(ceil_div(total, 256)), 256, 0, st>>>(idx, out, N, C, total);
+  QH_CHECK_LAUNCH("qh_one_hot");
+  return QH_OK;
+}

@@ -1,0 +1,157 @@
+"""Flash attention (forward, backward, single-query decode) on the HIP library.
+
+Reference: qwen_triton/kernels/flash_attention.py:35-433 (SDPA fallback :35-49,
+forward kernel :54-152, backward kernels :155-277, launchers :280-367, autograd
+:370-406, public op :409-433).
+
+``triton_flash_attention`` keeps the reference contract: q [B,Hq,Sq,D], k/v
+[B,Hkv,Sk,D], GQA through ``num_kv_groups``, causal masking aligned top-left
+(key j visible to query i iff j <= i), LSE saved for the backward. Two
+extensions are used by the model layer only: ``causal_offset`` (bottom-right
+alignment for prefill on top of a cache) and the split-KV decode kernel for a
+single query over a long cache.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _native
+from ._common import OpGuard
+
+_GUARD = OpGuard("FlashAttention")
+
+
+def _torch_flash_attention(q, k, v, scale: float, is_causal: bool = True, num_kv_groups: int = 1) -> torch.Tensor:
+    if num_kv_groups > 1:
+        B, nkv, S, D = k.shape
+        k = k[:, :, None].expand(B, nkv, num_kv_groups, S, D).reshape(B, nkv * num_kv_groups, S, D)
+        v = v[:, :, None].expand(B, nkv, num_kv_groups, S, D).reshape(B, nkv * num_kv_groups, S, D)
+    return torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=None, dropout_p=0.0,
+                                                            is_causal=is_causal, scale=scale)
+
+
+def _unit_last(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _check(q, k, v, num_kv_groups):
+    _native.require_device(q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("flash attention expects 4-D [B, H, S, D] tensors")
+    if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"flash attention shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if q.shape[1] != k.shape[1] * num_kv_groups:
+        raise ValueError(f"q heads {q.shape[1]} != kv heads {k.shape[1]} x groups {num_kv_groups}")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("flash attention kernel needs bf16 or fp16 q/k/v of one dtype")
+
+
+def flash_forward(q, k, v, scale: float, causal: bool, num_kv_groups: int, causal_offset: int = 0,
+                  need_lse: bool = True):
+    """Launch the forward kernel; returns (out [B,Hq,Sq,D] contiguous, lse [B,Hq,Sq] fp32 or None)."""
+    _check(q, k, v, num_kv_groups)
+    q, k, v = _unit_last(q), _unit_last(k), _unit_last(v)
+    B, Hq, Sq, D = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    out = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if need_lse else None
+    _native.call("qh_flash_fwd", q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0),
+                 k.stride(1), k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), out.data_ptr(),
+                 None if lse is None else lse.data_ptr(), B, Hq, Hkv, Sq, Sk, D, float(scale), int(bool(causal)),
+                 int(causal_offset), _native.dtype_code(q.dtype), _native.stream(q.device))
+    return out, lse
+
+
+def flash_backward(q, k, v, out, grad_out, lse, scale: float, causal: bool, num_kv_groups: int,
+                   causal_offset: int = 0):
+    q, k, v = _unit_last(q), _unit_last(k), _unit_last(v)
+    B, Hq, Sq, D = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    o = out.contiguous()
+    do = grad_out.to(q.dtype).contiguous()
+    dq = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
+    dk = torch.empty((B, Hkv, Sk, D), dtype=k.dtype, device=k.device)
+    dv = torch.empty((B, Hkv, Sk, D), dtype=v.dtype, device=v.device)
+    ws = _native.workspace(_native.call("qh_flash_bwd_workspace", B, Hq, Sq), q.device)
+    _native.call("qh_flash_bwd", q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0),
+                 k.stride(1), k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), o.data_ptr(),
+                 do.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(),
+                 B, Hq, Hkv, Sq, Sk, D, float(scale), int(bool(causal)), int(causal_offset),
+                 _native.dtype_code(q.dtype), _native.stream(q.device))
+    return dq, dk, dv
+
+
+def flash_decode(q, k, v, scale: float, num_kv_groups: int, seqlens: torch.Tensor | None = None,
+                 workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Single-query attention over all (or the first ``seqlens[b]``) keys; q [B,Hq,1,D]."""
+    _check(q, k, v, num_kv_groups)
+    if q.shape[2] != 1:
+        raise ValueError("flash_decode expects one query per sequence")
+    k, v = _unit_last(k), _unit_last(v)
+    q = _unit_last(q)
+    B, Hq, _, D = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    out = torch.empty((B, Hq, 1, D), dtype=q.dtype, device=q.device)
+    need = _native.call("qh_flash_decode_workspace", B, Hq, Hkv, Sk, D)
+    if workspace is None or workspace.numel() < need:
+        workspace = _native.workspace(need, q.device)
+    if seqlens is not None and seqlens.dtype != torch.int32:
+        raise ValueError("seqlens must be int32")
+    _native.call("qh_flash_decode", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+                 k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), out.data_ptr(), None,
+                 None if seqlens is None else seqlens.data_ptr(), workspace.data_ptr(), workspace.numel(), B, Hq, Hkv,
+                 Sk, D, float(scale), _native.dtype_code(q.dtype), _native.stream(q.device))
+    return out
+
+
+class _FlashAttentionFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, scale, is_causal, num_kv_groups, causal_offset=0):
+        out, lse = flash_forward(q, k, v, scale, is_causal, num_kv_groups, causal_offset)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.scale = scale
+        ctx.is_causal = is_causal
+        ctx.num_kv_groups = num_kv_groups
+        ctx.causal_offset = causal_offset
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        q, k, v, out, lse = ctx.saved_tensors
+        try:
+            dq, dk, dv = flash_backward(q, k, v, out, grad_output, lse, ctx.scale, ctx.is_causal, ctx.num_kv_groups,
+                                        ctx.causal_offset)
+        except Exception as exc:
+            _GUARD.failed(exc, "backward kernel")
+            with torch.enable_grad():
+                qq, kk, vv = (t.detach().requires_grad_(True) for t in (q, k, v))
+                ref = _torch_flash_attention(qq, kk, vv, ctx.scale, ctx.is_causal, ctx.num_kv_groups)
+                dq, dk, dv = torch.autograd.grad(ref, (qq, kk, vv), grad_output)
+        return dq, dk, dv, None, None, None, None
+
+
+def attention(q, k, v, scale: float, causal: bool, num_kv_groups: int, causal_offset: int = 0) -> torch.Tensor:
+    """Dispatch used by the model layer: decode kernel for one query without grad, else flash fwd(/bwd)."""
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        return _FlashAttentionFunction.apply(q, k, v, scale, causal, num_kv_groups, causal_offset)
+    if q.shape[2] == 1 and (not causal or causal_offset >= k.shape[2] - 1):
+        return flash_decode(q, k, v, scale, num_kv_groups)
+    return flash_forward(q, k, v, scale, causal, num_kv_groups, causal_offset, need_lse=False)[0]
+
+
+def triton_flash_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float,
+    is_causal: bool = True,
+    num_kv_groups: int = 1,
+    use_triton: bool | None = None,
+) -> torch.Tensor:
+    if not _GUARD.use_native(use_triton, q, k, v):
+        return _torch_flash_attention(q, k, v, scale, is_causal, num_kv_groups)
+    try:
+        return attention(q, k, v, scale, is_causal, num_kv_groups, 0)
+    except Exception as exc:
+        _GUARD.failed(exc)
+        return _torch_flash_attention(q, k, v, scale, is_causal, num_kv_groups)

@@ -1,0 +1,122 @@
+"""Linear layer GEMM ``y = x @ W^T (+ b)`` and its backward on the HIP library.
+
+Reference: qwen_triton/kernels/matmul.py:35-255 (torch fallbacks :35-49, tile
+kernel :64-97, bias/row-sum kernels :100-127, forward :130-155, backward
+:158-200, autograd :203-232, public op :235-255).
+
+The three products run on one MFMA kernel with operand-view flags, so neither
+``W.T`` (reference :140) nor ``grad.T`` (:184) is ever materialised:
+forward ``x W^T`` (NT), input grad ``dy W`` (B transposed view) and weight grad
+``dy^T x`` (both operands transposed views).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _native
+from ._common import OpGuard, needs_grad
+
+_GUARD = OpGuard("Matmul")
+
+
+def _torch_matmul(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    return torch.nn.functional.linear(x, weight, bias)
+
+
+def _torch_matmul_backward(x, weight, grad_output, needs_bias_grad: bool):
+    grad_x = grad_output @ weight
+    g2 = grad_output.reshape(-1, grad_output.shape[-1])
+    grad_weight = g2.T @ x.reshape(-1, x.shape[-1])
+    grad_bias = g2.sum(0) if needs_bias_grad else None
+    return grad_x, grad_weight, grad_bias
+
+
+def _rows(t: torch.Tensor, cols: int) -> torch.Tensor:
+    """2-D row-major view [rows, cols] with unit column stride (copies only if needed)."""
+    t2 = t.reshape(-1, cols)
+    if t2.stride(1) != 1 or (t2.shape[0] > 1 and t2.stride(0) < cols):
+        t2 = t2.contiguous()
+    return t2
+
+
+def gemm(trans_a: bool, trans_b: bool, M: int, N: int, K: int, a: torch.Tensor, lda: int, b: torch.Tensor, ldb: int,
+         out: torch.Tensor, ldc: int, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Raw library GEMM: out[M,N] = A(M,K) . B(N,K)^T (+ bias) with operand views."""
+    _native.call("qh_gemm", int(trans_a), int(trans_b), M, N, K, a.data_ptr(), lda, b.data_ptr(), ldb,
+                 out.data_ptr(), ldc, None if bias is None else bias.data_ptr(), _native.dtype_code(a.dtype),
+                 _native.dtype_code(out.dtype), _native.stream(a.device))
+    return out
+
+
+def _native_matmul_forward(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    _native.require_device(x, weight, bias)
+    if x.dtype != weight.dtype or (bias is not None and bias.dtype != weight.dtype):
+        raise ValueError("matmul kernel needs x, weight and bias of one dtype")
+    N, K = weight.shape
+    if x.shape[-1] != K:
+        raise ValueError(f"matmul shape mismatch: x {tuple(x.shape)} weight {tuple(weight.shape)}")
+    x2 = _rows(x, K)
+    w = weight if weight.stride(1) == 1 else weight.contiguous()
+    b = None if bias is None else bias.contiguous()
+    M = x2.shape[0]
+    out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    gemm(False, False, M, N, K, x2, x2.stride(0), w, w.stride(0), out, N, b)
+    return out.view(*x.shape[:-1], N)
+
+
+def _native_matmul_backward(x, weight, grad_output, need_x: bool, need_w: bool, need_b: bool):
+    N, K = weight.shape
+    g2 = _rows(grad_output.to(weight.dtype), N)
+    M = g2.shape[0]
+    grad_x = grad_w = grad_b = None
+    if need_x:
+        w = weight if weight.stride(1) == 1 else weight.contiguous()
+        grad_x = torch.empty((M, K), dtype=x.dtype, device=x.device)
+        gemm(False, True, M, K, N, g2, g2.stride(0), w, w.stride(0), grad_x, K)
+        grad_x = grad_x.view(x.shape)
+    if need_w:
+        x2 = _rows(x, K)
+        grad_w = torch.empty((N, K), dtype=weight.dtype, device=weight.device)
+        gemm(True, True, N, K, M, g2, g2.stride(0), x2, x2.stride(0), grad_w, K)
+    if need_b:
+        grad_b = torch.empty((N,), dtype=weight.dtype, device=weight.device)
+        _native.call("qh_colsum", g2.data_ptr(), g2.stride(0), M, N, grad_b.data_ptr(),
+                     _native.dtype_code(g2.dtype), _native.dtype_code(grad_b.dtype), _native.stream(g2.device))
+    return grad_x, grad_w, grad_b
+
+
+class _MatmulFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        ctx.save_for_backward(x, weight)
+        ctx.has_bias = bias is not None
+        return _native_matmul_forward(x, weight, bias)
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        x, weight = ctx.saved_tensors
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        need_b = ctx.has_bias and ctx.needs_input_grad[2]
+        try:
+            return _native_matmul_backward(x, weight, grad_output, need_x, need_w, need_b)
+        except Exception as exc:
+            _GUARD.failed(exc, "backward kernel")
+            gx, gw, gb = _torch_matmul_backward(x, weight, grad_output, need_b)
+            return gx, gw, gb
+
+
+def triton_matmul(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    use_triton: bool | None = None,
+) -> torch.Tensor:
+    if not _GUARD.use_native(use_triton, x, weight):
+        return _torch_matmul(x, weight, bias)
+    try:
+        if needs_grad(x, weight, bias):
+            return _MatmulFunction.apply(x, weight, bias)
+        return _native_matmul_forward(x, weight, bias)
+    except Exception as exc:
+        _GUARD.failed(exc)
+        return _torch_matmul(x, weight, bias)

@@ -1,0 +1,300 @@
+"""Qwen3 / Qwen3-MoE causal LM on the MI355X operator stack.
+
+Reference: qwen_triton/models/core.py:1-409 (mask builder :47-74, loss shift
+:85-92, decoder layer :95-153, model :156-247, causal LM + greedy decode
+:250-409). Public API, parameter names and output types are the reference's.
+Differences, all in the dispatch rather than the maths:
+
+* without a padding mask the layers get ``attention_mask=None`` and run causal
+  flash attention (the reference always built an additive mask, which sent
+  every prefill to fp32 SDPA);
+* the largest cache position is known on the host when ``cache_position`` is
+  generated here, so the cache write needs no device-to-host sync;
+* ``greedy_generate`` preallocates the KV cache for the whole generation.
+"""
+from __future__ import annotations
+
+from types import SimpleNamespace
+from typing import Any
+
+import torch
+from torch import nn
+from transformers.modeling_outputs import CausalLMOutputWithPast
+
+from qwen_triton.configs import QwenTritonConfig
+from qwen_triton.kernels.cross_entropy import triton_cross_entropy
+from qwen_triton.kernels.residual_add import residual_add
+from qwen_triton.modules import (
+    Qwen3NextLinearAttention,
+    QwenFullAttention,
+    QwenMLP,
+    QwenRMSNorm,
+    QwenRotaryEmbedding,
+    QwenSparseMoeBlock,
+    QwenTritonCache,
+)
+from qwen_triton.modules.embedding import TritonEmbedding
+from qwen_triton.modules.linear import TritonLinear
+
+_DTYPES = {
+    "fp16": torch.float16, "float16": torch.float16, "half": torch.float16,
+    "bf16": torch.bfloat16, "bfloat16": torch.bfloat16,
+    "fp32": torch.float32, "float32": torch.float32,
+}
+
+
+def _parse_dtype(dtype: torch.dtype | str | None) -> torch.dtype | None:
+    if dtype is None or isinstance(dtype, torch.dtype):
+        return dtype
+    try:
+        return _DTYPES[dtype.lower()]
+    except KeyError:
+        raise ValueError(f"Unsupported dtype string: {dtype}") from None
+
+
+def _build_causal_mask(attention_mask, batch_size: int, cache_position, device, past_key_values, window_size=None):
+    """Additive fp32 mask [B, 1, q, kv]: causal (optionally windowed) plus key padding."""
+    q_len = cache_position.shape[0]
+    past = 0 if past_key_values is None else past_key_values.get_seq_length()
+    kv_len = past + q_len
+    keys = torch.arange(kv_len, device=device)
+    allowed = keys[None, :] <= cache_position[:, None]
+    if window_size is not None:
+        allowed = allowed & (keys[None, :] > cache_position[:, None] - window_size)
+    neg = torch.finfo(torch.float32).min
+    mask = torch.full((q_len, kv_len), neg, device=device, dtype=torch.float32).masked_fill(allowed, 0.0)
+    mask = mask[None, None].expand(batch_size, 1, q_len, kv_len)
+    if attention_mask is not None:
+        am = attention_mask.to(device)
+        if am.shape[1] < kv_len:
+            am = torch.cat((torch.ones((am.shape[0], kv_len - am.shape[1]), device=device, dtype=am.dtype), am), dim=-1)
+        mask = mask + (1.0 - am[:, None, None, :kv_len].to(torch.float32)) * neg
+    return mask
+
+
+def _layer_uses_moe(config: QwenTritonConfig, layer_idx: int) -> bool:
+    if not config.is_moe or config.num_experts <= 0 or layer_idx in config.mlp_only_layers:
+        return False
+    return (layer_idx + 1) % config.decoder_sparse_step == 0
+
+
+def _loss_fn(logits: torch.Tensor, labels: torch.Tensor) -> torch.Tensor:
+    shift_logits = logits[:, :-1]
+    shift_labels = labels[:, 1:]
+    return triton_cross_entropy(shift_logits.reshape(-1, shift_logits.shape[-1]), shift_labels.reshape(-1),
+                                ignore_index=-100)
+
+
+class QwenDecoderLayer(nn.Module):
+    def __init__(self, config: QwenTritonConfig, layer_idx: int) -> None:
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.layer_type = config.layer_types[layer_idx]
+        eps, one_plus = config.rms_norm_eps, config.norm_one_plus
+        self.input_layernorm = QwenRMSNorm(config.hidden_size, eps=eps, one_plus_weight=one_plus)
+        self.post_attention_layernorm = QwenRMSNorm(config.hidden_size, eps=eps, one_plus_weight=one_plus)
+        if self.layer_type == "linear_attention":
+            self.linear_attn = Qwen3NextLinearAttention(config, layer_idx)
+        else:
+            self.self_attn = QwenFullAttention(config, layer_idx)
+        self.mlp = QwenSparseMoeBlock(config) if _layer_uses_moe(config, layer_idx) else QwenMLP(
+            config.hidden_size, config.intermediate_size)
+
+    def forward(self, hidden_states, position_embeddings, attention_mask=None, past_key_values=None,
+                cache_position=None, max_position: int | None = None):
+        residual = hidden_states
+        h = self.input_layernorm(hidden_states)
+        if self.layer_type == "linear_attention":
+            h = self.linear_attn(hidden_states=h, cache_params=past_key_values, cache_position=cache_position,
+                                 attention_mask=attention_mask)
+        else:
+            h = self.self_attn(hidden_states=h, position_embeddings=position_embeddings,
+                               attention_mask=attention_mask, past_key_values=past_key_values,
+                               cache_position=cache_position, max_position=max_position)
+        h = residual_add(h, residual)
+        residual = h
+        h = self.mlp(self.post_attention_layernorm(h))
+        router_logits = None
+        if isinstance(h, tuple):
+            h, router_logits = h
+        return residual_add(h, residual), router_logits
+
+
+class QwenTritonModel(nn.Module):
+    def __init__(self, config: QwenTritonConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.embed_tokens = TritonEmbedding(config.vocab_size, config.hidden_size, config.pad_token_id)
+        self.layers = nn.ModuleList([QwenDecoderLayer(config, i) for i in range(config.num_hidden_layers)])
+        self.norm = QwenRMSNorm(config.hidden_size, eps=config.rms_norm_eps, one_plus_weight=config.norm_one_plus)
+        self.rotary_emb = QwenRotaryEmbedding(config)
+
+    @staticmethod
+    def _mask_is_trivial(attention_mask: torch.Tensor | None) -> bool:
+        return attention_mask is None or bool((attention_mask == 1).all())
+
+    def forward(self, input_ids=None, attention_mask=None, position_ids=None, past_key_values=None, inputs_embeds=None,
+                use_cache=None, cache_position=None, output_router_logits: bool = False, **_: Any):
+        if (input_ids is None) == (inputs_embeds is None):
+            raise ValueError("Specify exactly one of input_ids or inputs_embeds")
+        if inputs_embeds is None:
+            inputs_embeds = self.embed_tokens(input_ids)
+        if use_cache and past_key_values is None:
+            past_key_values = QwenTritonCache(self.config.num_hidden_layers, self.config.layer_types,
+                                              max_cache_len=self.config.max_position_embeddings)
+        seq = inputs_embeds.shape[1]
+        max_position = None
+        generated_positions = cache_position is None
+        if cache_position is None:
+            past = 0 if past_key_values is None else past_key_values.get_seq_length()
+            cache_position = torch.arange(past, past + seq, device=inputs_embeds.device)
+            max_position = past + seq - 1
+        if position_ids is None:
+            position_ids = cache_position.unsqueeze(0)
+
+        batch = inputs_embeds.shape[0]
+        plain_causal = generated_positions and self._mask_is_trivial(attention_mask)
+        masks: dict[str, torch.Tensor | None] = {}
+        if plain_causal:
+            masks["full_attention"] = None
+        else:
+            masks["full_attention"] = _build_causal_mask(attention_mask, batch, cache_position, inputs_embeds.device,
+                                                         past_key_values)
+        if "sliding_attention" in self.config.layer_types and self.config.sliding_window is not None:
+            masks["sliding_attention"] = _build_causal_mask(attention_mask, batch, cache_position,
+                                                            inputs_embeds.device, past_key_values,
+                                                            window_size=self.config.sliding_window)
+
+        hidden = inputs_embeds
+        position_embeddings = self.rotary_emb(hidden, position_ids)
+        router_logits: list[torch.Tensor] = []
+        for layer in self.layers:
+            layer_mask = attention_mask if layer.layer_type == "linear_attention" else masks[layer.layer_type]
+            hidden, layer_router = layer(hidden, position_embeddings=position_embeddings, attention_mask=layer_mask,
+                                         past_key_values=past_key_values, cache_position=cache_position,
+                                         max_position=max_position)
+            if output_router_logits and layer_router is not None:
+                router_logits.append(layer_router)
+        hidden = self.norm(hidden)
+        return SimpleNamespace(
+            last_hidden_state=hidden,
+            past_key_values=past_key_values if use_cache else None,
+            router_logits=tuple(router_logits) if output_router_logits else None,
+        )
+
+
+class QwenTritonForCausalLM(nn.Module):
+    def __init__(self, config: QwenTritonConfig, backend: str = "triton", init_weights: bool = True) -> None:
+        super().__init__()
+        if backend != "triton":
+            raise ValueError("Use from_reference_model for backend='ref'")
+        self.config = config
+        self.backend = backend
+        self.ref_model = None
+        self.model = QwenTritonModel(config)
+        self.lm_head = TritonLinear(config.hidden_size, config.vocab_size, bias=False)
+        if init_weights:
+            self._reset_parameters()
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.model.embed_tokens.weight
+
+    def _reset_parameters(self) -> None:
+        std = self.config.initializer_range
+        for module in self.modules():
+            if isinstance(module, (nn.Linear, TritonLinear)):
+                nn.init.normal_(module.weight, mean=0.0, std=std)
+                if module.bias is not None:
+                    nn.init.zeros_(module.bias)
+            elif isinstance(module, (nn.Embedding, TritonEmbedding)):
+                nn.init.normal_(module.weight, mean=0.0, std=std)
+
+    @classmethod
+    def from_reference_model(cls, reference_model: nn.Module, config: QwenTritonConfig) -> "QwenTritonForCausalLM":
+        inst = cls.__new__(cls)
+        nn.Module.__init__(inst)
+        inst.config = config
+        inst.backend = "ref"
+        inst.ref_model = reference_model
+        return inst
+
+    @classmethod
+    def from_config(cls, config, backend: str = "triton", init_weights: bool = True) -> "QwenTritonForCausalLM":
+        cfg = config if isinstance(config, QwenTritonConfig) else QwenTritonConfig.from_hf_config(config)
+        if backend != "triton":
+            raise ValueError("from_config currently supports backend='triton' only")
+        return cls(cfg, backend=backend, init_weights=init_weights)
+
+    @classmethod
+    def from_pretrained_hf(cls, model_id: str, backend: str = "triton", device="cpu", dtype=None):
+        from qwen_triton.loaders import load_config_dict, load_hf_weights_into_model, ensure_local_model_path
+
+        cfg = QwenTritonConfig.from_hf_config(load_config_dict(model_id))
+        parsed = _parse_dtype(dtype) or torch.float32
+        if backend == "ref":
+            from transformers import AutoModelForCausalLM
+
+            ref = AutoModelForCausalLM.from_pretrained(model_id, trust_remote_code=True, torch_dtype=parsed)
+            return cls.from_reference_model(ref.to(device), cfg)
+        path = ensure_local_model_path(model_id, include_weights=True)
+        inst = cls.from_config(cfg, backend="triton", init_weights=False)
+        inst.to(dtype=parsed)
+        load_hf_weights_into_model(inst, path)
+        inst.to(device=device)
+        inst.eval()
+        return inst
+
+    def forward(self, input_ids=None, attention_mask=None, position_ids=None, past_key_values=None, inputs_embeds=None,
+                labels=None, use_cache=None, cache_position=None, logits_to_keep: int | torch.Tensor = 0,
+                output_router_logits: bool = False, **kwargs: Any) -> CausalLMOutputWithPast:
+        if self.backend == "ref":
+            return self.ref_model(input_ids=input_ids, attention_mask=attention_mask, position_ids=position_ids,
+                                  past_key_values=past_key_values, inputs_embeds=inputs_embeds, labels=labels,
+                                  use_cache=use_cache, cache_position=cache_position, **kwargs)
+        outputs = self.model(input_ids=input_ids, attention_mask=attention_mask, position_ids=position_ids,
+                             past_key_values=past_key_values, inputs_embeds=inputs_embeds, use_cache=use_cache,
+                             cache_position=cache_position, output_router_logits=output_router_logits, **kwargs)
+        hidden = outputs.last_hidden_state
+        if isinstance(logits_to_keep, int) and logits_to_keep > 0:
+            hidden = hidden[:, -logits_to_keep:, :]
+        elif not isinstance(logits_to_keep, int):
+            hidden = hidden[:, logits_to_keep, :]
+        logits = self.lm_head(hidden)
+        loss = _loss_fn(logits, labels) if labels is not None else None
+        result = CausalLMOutputWithPast(loss=loss, logits=logits, past_key_values=outputs.past_key_values,
+                                        hidden_states=None, attentions=None)
+        if output_router_logits:
+            result["router_logits"] = outputs.router_logits
+        return result
+
+    def new_cache(self, batch: int, capacity: int, dtype: torch.dtype, device) -> QwenTritonCache:
+        """A cache with every attention layer preallocated to ``capacity`` positions."""
+        cfg = self.config
+        cache = QwenTritonCache(cfg.num_hidden_layers, cfg.layer_types, max_cache_len=cfg.max_position_embeddings)
+        for i, kind in enumerate(cfg.layer_types):
+            if kind != "linear_attention":
+                cache.reserve(i, batch, cfg.num_key_value_heads, capacity, cfg.head_dim, dtype, device)
+        return cache
+
+    @torch.no_grad()
+    def greedy_generate(self, input_ids: torch.LongTensor, attention_mask: torch.Tensor | None = None,
+                        max_new_tokens: int = 16) -> torch.LongTensor:
+        if self.backend == "ref" and hasattr(self.ref_model, "generate"):
+            return self.ref_model.generate(input_ids=input_ids, attention_mask=attention_mask,
+                                           max_new_tokens=max_new_tokens, do_sample=False)
+        generated = input_ids
+        running_mask = attention_mask
+        cache = None
+        if max_new_tokens > 0:
+            dtype = self.lm_head.weight.dtype
+            cache = self.new_cache(input_ids.shape[0], input_ids.shape[1] + max_new_tokens, dtype, input_ids.device)
+        for _ in range(max_new_tokens):
+            step_ids = generated if cache.get_seq_length() == 0 else generated[:, -1:]
+            out = self(input_ids=step_ids, attention_mask=running_mask, past_key_values=cache, use_cache=True,
+                       logits_to_keep=1)
+            cache = out.past_key_values
+            next_token = out.logits[:, -1].argmax(dim=-1, keepdim=True)
+            generated = torch.cat((generated, next_token), dim=-1)
+            if running_mask is not None:
+                running_mask = torch.cat((running_mask, torch.ones_like(next_token, dtype=running_mask.dtype)), dim=-1)
+        return generated

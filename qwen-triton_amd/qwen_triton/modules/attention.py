@@ -1,0 +1,117 @@
+"""Full (softmax) attention block (reference: qwen_triton/modules/attention.py:17-128).
+
+Projections, per-head QK RMSNorm, RoPE, cache update and attention, with the
+reference's parameter names. Dispatch differs from the reference on purpose
+(its K1 defect: the model always passes a mask, so prefill never reached the
+flash kernel):
+
+* no mask: causal flash attention, aligned bottom-right when queries sit on
+  top of cached keys (``causal_offset = kv_len - q_len``); a single query takes
+  the split-KV decode kernel;
+* explicit additive mask (padding): fp32 SDPA over repeated KV heads, as the
+  reference does for masked multi-token attention.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import nn
+
+from qwen_triton.configs import QwenTritonConfig
+from qwen_triton.kernels import sigmoid_mul
+from qwen_triton.kernels import flash_attention as _fa
+from qwen_triton.kernels.flash_attention import triton_flash_attention
+from qwen_triton.modules.cache import QwenTritonCache
+from qwen_triton.modules.linear import TritonLinear
+from qwen_triton.modules.norms import QwenRMSNorm
+from qwen_triton.modules.rotary import apply_rotary_pos_emb
+
+
+def repeat_kv(hidden_states: torch.Tensor, n_rep: int) -> torch.Tensor:
+    b, h, s, d = hidden_states.shape
+    if n_rep == 1:
+        return hidden_states
+    return hidden_states[:, :, None].expand(b, h, n_rep, s, d).reshape(b, h * n_rep, s, d)
+
+
+class QwenFullAttention(nn.Module):
+    def __init__(self, config: QwenTritonConfig, layer_idx: int) -> None:
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.head_dim = config.head_dim
+        self.num_heads = config.num_attention_heads
+        self.num_key_value_heads = config.num_key_value_heads
+        self.num_key_value_groups = config.num_attention_heads // config.num_key_value_heads
+        self.scaling = self.head_dim ** -0.5
+        self.attention_dropout = config.attention_dropout
+        q_out = config.num_attention_heads * self.head_dim * (2 if config.attn_output_gate else 1)
+        kv_out = config.num_key_value_heads * self.head_dim
+        self.q_proj = TritonLinear(config.hidden_size, q_out, bias=config.attention_bias)
+        self.k_proj = TritonLinear(config.hidden_size, kv_out, bias=config.attention_bias)
+        self.v_proj = TritonLinear(config.hidden_size, kv_out, bias=config.attention_bias)
+        self.o_proj = TritonLinear(config.num_attention_heads * self.head_dim, config.hidden_size,
+                                   bias=config.attention_bias)
+        self.q_norm = QwenRMSNorm(self.head_dim, eps=config.rms_norm_eps, one_plus_weight=config.norm_one_plus)
+        self.k_norm = QwenRMSNorm(self.head_dim, eps=config.rms_norm_eps, one_plus_weight=config.norm_one_plus)
+
+    def _attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor | None,
+                out_dtype: torch.dtype) -> torch.Tensor:
+        q_len, kv_len = q.shape[2], k.shape[2]
+        groups = self.num_key_value_groups
+        if mask is None:
+            on_gpu = q.is_cuda and k.is_cuda
+            if on_gpu:
+                if q_len == kv_len:
+                    return triton_flash_attention(q, k, v, scale=self.scaling, is_causal=True, num_kv_groups=groups)
+                return _fa.attention(q, k, v, self.scaling, True, groups, causal_offset=kv_len - q_len)
+            # CPU: reference torch semantics, bottom-right causal.
+            if q_len == kv_len:
+                return _fa._torch_flash_attention(q, k, v, self.scaling, True, groups)
+            if q_len == 1:
+                return _fa._torch_flash_attention(q, k, v, self.scaling, False, groups)
+            pos_q = torch.arange(kv_len - q_len, kv_len, device=q.device)
+            allowed = torch.arange(kv_len, device=q.device)[None, :] <= pos_q[:, None]
+            mask = torch.zeros((q_len, kv_len), device=q.device, dtype=torch.float32).masked_fill(
+                ~allowed, torch.finfo(torch.float32).min)[None, None]
+        ke, ve = repeat_kv(k, groups), repeat_kv(v, groups)
+        m = mask[:, :, :, :kv_len]
+        return torch.nn.functional.scaled_dot_product_attention(
+            q.to(torch.float32), ke.to(torch.float32), ve.to(torch.float32), attn_mask=m, dropout_p=0.0,
+            is_causal=False, scale=self.scaling).to(out_dtype)
+
+    def forward(
+        self,
+        hidden_states: torch.Tensor,
+        position_embeddings: tuple[torch.Tensor, torch.Tensor],
+        attention_mask: Optional[torch.Tensor] = None,
+        past_key_values: Optional[QwenTritonCache] = None,
+        cache_position: Optional[torch.LongTensor] = None,
+        max_position: int | None = None,
+    ) -> torch.Tensor:
+        input_shape = hidden_states.shape[:-1]
+        mixed_q = self.q_proj(hidden_states)
+        gate = None
+        if self.config.attn_output_gate:
+            q, gate = torch.chunk(mixed_q.view(*input_shape, -1, self.head_dim * 2), 2, dim=-1)
+            gate = gate.reshape(*input_shape, -1)
+        else:
+            q = mixed_q.view(*input_shape, -1, self.head_dim)
+        k = self.k_proj(hidden_states).view(*input_shape, -1, self.head_dim)
+        v = self.v_proj(hidden_states).view(*input_shape, -1, self.head_dim)
+
+        q = self.q_norm(q).transpose(1, 2)
+        k = self.k_norm(k).transpose(1, 2)
+        v = v.transpose(1, 2)
+        cos, sin = position_embeddings
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+
+        if past_key_values is not None:
+            k, v = past_key_values.update_attention(self.layer_idx, k, v, cache_position=cache_position,
+                                                    max_position=max_position)
+        out = self._attend(q, k, v, attention_mask, hidden_states.dtype)
+        out = out.transpose(1, 2).reshape(*input_shape, -1)
+        if gate is not None:
+            out = sigmoid_mul(out, gate)
+        return self.o_proj(out)

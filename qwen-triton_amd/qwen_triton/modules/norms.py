@@ -1,0 +1,37 @@
+"""RMSNorm modules (reference: qwen_triton/modules/norms.py:9-36)."""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from qwen_triton.kernels import rmsnorm, silu_mul
+
+
+class QwenRMSNorm(nn.Module):
+    def __init__(self, hidden_size: int, eps: float = 1e-6, one_plus_weight: bool = False) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.full((hidden_size,), 0.0 if one_plus_weight else 1.0))
+        self.eps = eps
+        self.one_plus_weight = one_plus_weight
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return rmsnorm(hidden_states, self.weight, eps=self.eps, one_plus_weight=self.one_plus_weight)
+
+    def extra_repr(self) -> str:
+        return f"{tuple(self.weight.shape)}, eps={self.eps}, one_plus_weight={self.one_plus_weight}"
+
+
+class QwenRMSNormGated(nn.Module):
+    """Gated RMSNorm of the Qwen3-Next linear-attention block (kept for API parity)."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.eps = eps
+
+    def forward(self, hidden_states: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        dtype = hidden_states.dtype
+        x = hidden_states.to(torch.float32)
+        x = x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        x = self.weight.to(torch.float32) * x
+        return silu_mul(gate.to(dtype), x.to(dtype))
