@@ -1,0 +1,438 @@
+"""Throughput benchmark of the Qwen3 operator stack on one MI355X.
+
+Default (``python bench.py``): the Qwen3-0.6B-architecture decode step of
+BASELINE config 3 — 64 sequences, each with a 2048-token bf16 KV cache
+(N(0,1)), one new token at position 2048 through all 28 layers — captured once
+as a HIP graph and replayed ``--steps`` times. ``value`` is decode tokens/s
+(64 tokens per step). The same JSON line also carries:
+
+* config 0 on the GPU: bs1 prefill of 128 tokens and 32 greedy decode steps;
+* ``roofline`` of the dominant kernel (split-KV decode attention, HBM-bound):
+  algorithmic K/V bytes per launch / average launch time from HIP events on the
+  launch stream;
+* ``cpu_baseline``: the CPU oracle (fp32 torch, HF semantics) decoding a
+  bounded sample of the same workload on the host cores.
+
+``--workload fa|dense|moe`` time the other BASELINE configs' kernels (used for
+profiling; they print their own JSON line).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "qwen-triton_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "Qwen3-0.6B prefill/decode tok/s on 1 MI355X + % of MFMA/HBM roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+QWEN3_06B = dict(model_type="qwen3", vocab_size=151936, hidden_size=1024, intermediate_size=3072,
+                 num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8, head_dim=128,
+                 max_position_embeddings=40960, rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_model(dtype, device, layers=None):
+    import torch
+    from qwen_triton import QwenTritonConfig, QwenTritonForCausalLM
+
+    cfg = dict(QWEN3_06B)
+    if layers is not None:
+        cfg["num_hidden_layers"] = layers
+    config = QwenTritonConfig.from_hf_config(cfg)
+    torch.manual_seed(0)
+    model = QwenTritonForCausalLM(config, init_weights=False)
+    gen = torch.Generator().manual_seed(0)
+    with torch.no_grad():  # N(0, 0.02) weights in parameter order, norms = 1
+        for name, p in model.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.copy_(torch.randn(p.shape, generator=gen) * 0.02)
+    return model.to(device=device, dtype=dtype).eval()
+
+
+def sync():
+    import torch
+
+    torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------------------
+# config 3: decode step, batch 64, 2048-token cache
+# ---------------------------------------------------------------------------
+def fill_cache(model, batch, ctx, capacity, seed=0):
+    import torch
+
+    cfg = model.config
+    cache = model.new_cache(batch, capacity, torch.bfloat16, "cuda")
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    for i in range(cfg.num_hidden_layers):
+        cache.key_cache[i][:, :, :ctx].normal_(generator=gen)
+        cache.value_cache[i][:, :, :ctx].normal_(generator=gen)
+        cache.attention_lengths[i] = ctx
+    return cache
+
+
+def decode_step_fn(model, cache, ids, ctx):
+    def step():
+        cache.attention_lengths = [ctx] * len(cache.attention_lengths)
+        logits = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1).logits
+        return logits[:, -1].argmax(dim=-1)
+
+    return step
+
+
+def bench_decode(model, steps, warmup, use_graph=True, batch=64, ctx=2048):
+    import torch
+
+    cache = fill_cache(model, batch, ctx, capacity=ctx + 64)
+    ids = torch.randint(0, model.config.vocab_size, (batch, 1), generator=torch.Generator().manual_seed(0)).cuda()
+    step = decode_step_fn(model, cache, ids, ctx)
+    with torch.no_grad():
+        for _ in range(max(1, warmup)):
+            eager_tok = step()
+        sync()
+        t0 = time.perf_counter()
+        n_eager = max(3, min(steps, 10))
+        for _ in range(n_eager):
+            step()
+        sync()
+        eager_ms = (time.perf_counter() - t0) * 1e3 / n_eager
+        log(f"decode eager: {eager_ms:.3f} ms/step")
+        graph_ms = None
+        if use_graph:
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                step()
+            torch.cuda.current_stream().wait_stream(s)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                graph_tok = step()
+            for _ in range(max(1, warmup)):
+                g.replay()
+            sync()
+            if not torch.equal(graph_tok, eager_tok):
+                raise RuntimeError("graph replay disagrees with the eager decode step")
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                g.replay()
+            sync()
+            graph_ms = (time.perf_counter() - t0) * 1e3 / steps
+            log(f"decode graph: {graph_ms:.3f} ms/step")
+    return cache, eager_ms, graph_ms
+
+
+def attention_roofline(model, cache, reps=50, batch=64, ctx=2048):
+    """Dominant kernel of the decode step: split-KV decode attention over 2049 keys."""
+    import torch
+    from qwen_triton.kernels import flash_attention as FA
+
+    cfg = model.config
+    sk = ctx + 1
+    k = cache.key_cache[0][:, :, :sk]
+    v = cache.value_cache[0][:, :, :sk]
+    q = torch.randn(batch, cfg.num_attention_heads, 1, cfg.head_dim, device="cuda", dtype=torch.bfloat16)
+    groups = cfg.num_attention_heads // cfg.num_key_value_heads
+    scale = cfg.head_dim ** -0.5
+    with torch.no_grad():
+        for _ in range(5):
+            FA.flash_decode(q, k, v, scale, groups)
+        stream = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in ev:
+            a.record(stream)
+            FA.flash_decode(q, k, v, scale, groups)
+            b.record(stream)
+        sync()
+    avg_ms = sum(a.elapsed_time(b) for a, b in ev) / reps
+    kv_bytes = 2 * batch * cfg.num_key_value_heads * sk * cfg.head_dim * 2
+    io_bytes = 2 * batch * cfg.num_attention_heads * cfg.head_dim * 2
+    algo = kv_bytes + io_bytes
+    achieved = algo / (avg_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "fa_decode_kernel+fa_decode_combine", "avg_launch_us": round(avg_ms * 1e3, 2),
+            "algorithmic_bytes_per_launch": algo}
+
+
+# ---------------------------------------------------------------------------
+# config 0 on the GPU: prefill 128, 32 greedy decode steps, batch 1
+# ---------------------------------------------------------------------------
+def bench_cfg0(model, reps=3):
+    import torch
+
+    ids = torch.randint(0, model.config.vocab_size, (1, 128), generator=torch.Generator().manual_seed(0)).cuda()
+    with torch.no_grad():
+        model.greedy_generate(ids, max_new_tokens=2)  # warmup
+        sync()
+        pre = []
+        for _ in range(reps):
+            cache = model.new_cache(1, 160, torch.bfloat16, "cuda")
+            sync()
+            t0 = time.perf_counter()
+            out = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            out.logits[:, -1].argmax(-1)
+            sync()
+            pre.append(time.perf_counter() - t0)
+        sync()
+        t0 = time.perf_counter()
+        model.greedy_generate(ids, max_new_tokens=33)
+        sync()
+        total = time.perf_counter() - t0
+    prefill_s = sorted(pre)[len(pre) // 2]
+    decode_s = max(total - prefill_s, 1e-9) / 32
+    return {"prefill_tok_s": round(128 / prefill_s, 1), "decode_tok_s": round(1 / decode_s, 1),
+            "prefill_ms": round(prefill_s * 1e3, 3), "decode_ms_per_token": round(decode_s * 1e3, 3)}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (fp32 torch) on a bounded sample of config 3
+# ---------------------------------------------------------------------------
+def cpu_baseline(model, sample_batch=4, ctx=2048, reps=3):
+    import torch
+
+    from oracle.model import ModelSpec, OracleQwen
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    params = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    orc = OracleQwen(ModelSpec.from_config(model.config), params, dtype=torch.float32)
+    cfg = model.config
+    gen = torch.Generator().manual_seed(0)
+    shape = (sample_batch, cfg.num_key_value_heads, ctx, cfg.head_dim)
+    kv = [(torch.randn(shape, generator=gen), torch.randn(shape, generator=gen)) for _ in range(cfg.num_hidden_layers)]
+    ids = torch.randint(0, cfg.vocab_size, (sample_batch, 1), generator=gen)
+
+    def run():
+        cache = {"k": [a for a, _ in kv], "v": [b for _, b in kv], "len": ctx}
+        return orc.forward(ids, cache, logits_to_keep=1)
+
+    run()  # warmup
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    return {"value": round(sample_batch / t, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"oracle fp32 decode step, batch {sample_batch} of 64, 2048-token cache, 28 layers "
+                      f"(median of {reps}, {t:.2f} s/step)"}
+
+
+# ---------------------------------------------------------------------------
+# other configs (profiling workloads)
+# ---------------------------------------------------------------------------
+def bench_fa(steps, warmup):
+    import torch
+    from qwen_triton.kernels import flash_attention as FA
+
+    B, Hq, Hkv, S, D = 8, 16, 8, 4096, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(B, Hq, S, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    k = torch.randn(B, Hkv, S, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    v = torch.randn(B, Hkv, S, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    do = torch.randn(B, Hq, S, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    scale = D ** -0.5
+    for _ in range(warmup):
+        o, lse = FA.flash_forward(q, k, v, scale, True, 2)
+        FA.flash_backward(q, k, v, o, do, lse, scale, True, 2)
+    sync()
+    ef, eb = [], []
+    for _ in range(steps):
+        a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        a.record()
+        o, lse = FA.flash_forward(q, k, v, scale, True, 2)
+        b.record()
+        FA.flash_backward(q, k, v, o, do, lse, scale, True, 2)
+        c.record()
+        ef.append((a, b))
+        eb.append((b, c))
+    sync()
+    fwd_ms = sum(x.elapsed_time(y) for x, y in ef) / steps
+    bwd_ms = sum(x.elapsed_time(y) for x, y in eb) / steps
+    fwd_flop = 2 * B * Hq * D * S * (S + 1)
+    bwd_flop = 2.5 * fwd_flop
+    return {"fa_fwd_ms": round(fwd_ms, 3), "fa_bwd_ms": round(bwd_ms, 3),
+            "fa_fwd_tflops": round(fwd_flop / fwd_ms / 1e9, 1), "fa_bwd_tflops": round(bwd_flop / bwd_ms / 1e9, 1),
+            "fa_fwd_frac": round(fwd_flop / fwd_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "fa_bwd_frac": round(bwd_flop / bwd_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
+def bench_dense(steps, warmup):
+    import torch
+    from qwen_triton.kernels import cross_entropy as CE
+    from qwen_triton.kernels import matmul as MM
+    from qwen_triton.kernels import silu_mul
+
+    T, H, I, V = 16384, 1024, 3072, 151936
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(T, H, device="cuda", dtype=torch.bfloat16, generator=g).requires_grad_(True)
+    wg = (torch.randn(I, H, device="cuda", generator=g) * 0.02).bfloat16().requires_grad_(True)
+    wu = (torch.randn(I, H, device="cuda", generator=g) * 0.02).bfloat16().requires_grad_(True)
+    wd = (torch.randn(H, I, device="cuda", generator=g) * 0.02).bfloat16().requires_grad_(True)
+    wl = (torch.randn(V, H, device="cuda", generator=g) * 0.02).bfloat16().requires_grad_(True)
+    labels = torch.randint(0, V, (T,), device="cuda", generator=g)
+
+    def step():
+        h = MM.triton_matmul(silu_mul(MM.triton_matmul(x, wg), MM.triton_matmul(x, wu)), wd)
+        logits = MM.triton_matmul(h, wl)
+        loss = CE.triton_cross_entropy(logits, labels)
+        loss.backward()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    sync()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    flop = 3 * (3 * 2 * T * H * I + 2 * T * H * V)
+    return {"dense_ms_per_step": round(ms, 3), "dense_gemm_tflops": round(flop / ms / 1e9, 1),
+            "dense_gemm_frac_of_step": round(flop / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
+def bench_gemm(steps, warmup):
+    """Per-shape GEMM timing (HIP events): ours vs torch.matmul (hipBLASLt) for context."""
+    import torch
+    from qwen_triton.kernels import matmul as MM
+
+    shapes = [  # (label, layout, M, N, K)
+        ("decode q", "NT", 64, 2048, 1024), ("decode kv", "NT", 64, 1024, 1024), ("decode gate", "NT", 64, 3072, 1024),
+        ("decode down", "NT", 64, 1024, 3072), ("decode lm_head", "NT", 64, 151936, 1024),
+        ("bs1 lm_head", "NT", 1, 151936, 1024), ("bs1 gate", "NT", 1, 3072, 1024),
+        ("prefill128 q", "NT", 128, 2048, 1024), ("prefill128 gate", "NT", 128, 3072, 1024),
+        ("prefill128 down", "NT", 128, 1024, 3072),
+        ("train gate fwd", "NT", 16384, 3072, 1024), ("train down fwd", "NT", 16384, 1024, 3072),
+        ("train lm_head fwd", "NT", 16384, 151936, 1024), ("train down dX", "NN", 16384, 3072, 1024),
+        ("train gate dW", "TN", 3072, 1024, 16384), ("square 8192", "NT", 8192, 8192, 8192),
+    ]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    out = []
+    for label, lay, M, N, K in shapes:
+        if lay == "NT":
+            a = torch.randn(M, K, device="cuda", dtype=torch.bfloat16, generator=g)
+            b = torch.randn(N, K, device="cuda", dtype=torch.bfloat16, generator=g)
+            ours = lambda: MM.gemm(False, False, M, N, K, a, K, b, K, c, N)
+            ref = lambda: torch.matmul(a, b.T)
+        elif lay == "NN":
+            a = torch.randn(M, K, device="cuda", dtype=torch.bfloat16, generator=g)
+            b = torch.randn(K, N, device="cuda", dtype=torch.bfloat16, generator=g)
+            ours = lambda: MM.gemm(False, True, M, N, K, a, K, b, N, c, N)
+            ref = lambda: torch.matmul(a, b)
+        else:
+            a = torch.randn(K, M, device="cuda", dtype=torch.bfloat16, generator=g)
+            b = torch.randn(K, N, device="cuda", dtype=torch.bfloat16, generator=g)
+            ours = lambda: MM.gemm(True, True, M, N, K, a, M, b, N, c, N)
+            ref = lambda: torch.matmul(a.T, b)
+        c = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        res = {}
+        for name, fn in (("ours", ours), ("torch", ref)):
+            for _ in range(warmup):
+                fn()
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+            for e0, e1 in evs:
+                e0.record()
+                fn()
+                e1.record()
+            sync()
+            res[name] = sum(e0.elapsed_time(e1) for e0, e1 in evs) / steps
+        flop = 2 * M * N * K
+        nbytes = 2 * (M * K + N * K + M * N)
+        row = {"shape": label, "layout": lay, "M": M, "N": N, "K": K, "us": round(res["ours"] * 1e3, 2),
+               "tflops": round(flop / res["ours"] / 1e9, 1), "gbs": round(nbytes / res["ours"] / 1e6, 1),
+               "torch_us": round(res["torch"] * 1e3, 2)}
+        log(json.dumps(row))
+        out.append(row)
+    return out
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="decode", choices=["decode", "fa", "dense", "gemm"])
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md for how it "
+              "would shard); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    os.environ.setdefault("QWEN_TRITON_STRICT", "1")
+    import torch
+    from qwen_triton import _native
+
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    if not _native.available():
+        sys.exit(f"libqwen_hip.so not loadable: {_native.load_error()!r}")
+
+    if args.workload == "fa":
+        res = bench_fa(args.steps, args.warmup)
+        print(json.dumps({"metric": "flash attention fwd+bwd (config 1)", **res}), flush=True)
+        return
+    if args.workload == "gemm":
+        res = bench_gemm(args.steps, args.warmup)
+        print(json.dumps({"metric": "GEMM shapes (bf16)", "rows": res}), flush=True)
+        return
+    if args.workload == "dense":
+        res = bench_dense(args.steps, args.warmup)
+        print(json.dumps({"metric": "dense proj + LM head + CE fwd/bwd (config 2)", **res}), flush=True)
+        return
+
+    log("building Qwen3-0.6B (random N(0,0.02) weights, bf16)")
+    model = build_model(torch.bfloat16, "cuda")
+    cache, eager_ms, graph_ms = bench_decode(model, args.steps, args.warmup, use_graph=not args.no_graph)
+    roof = attention_roofline(model, cache)
+    log(f"decode attention: {roof['avg_launch_us']} us/launch, {roof['achieved']} GB/s")
+    del cache
+    torch.cuda.empty_cache()
+    cfg0 = bench_cfg0(model)
+    log(f"config 0: {cfg0}")
+    cpu = None if args.no_cpu_baseline else cpu_baseline(model)
+    if cpu:
+        log(f"cpu baseline: {cpu}")
+    ms = graph_ms if graph_ms is not None else eager_ms
+    line = {
+        "metric": METRIC,
+        "value": round(64 / (ms * 1e-3), 1),
+        "unit": "decode tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random N(0,0.02) weights (seed 0), N(0,1) bf16 KV cache, random token ids",
+        "config": {"workload": "config3: Qwen3-0.6B decode step, batch 64, 2048-token KV cache, position 2048, "
+                               "28 layers, HIP-graph replay",
+                   "global_batch": 64, "seq_len": 2049, "parallelism": "single GPU"},
+        "eager_ms_per_step": round(eager_ms, 4),
+        "prefill_tok_s": cfg0["prefill_tok_s"],
+        "config0_gpu": cfg0,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -96,7 +96,8 @@ __device__ __forceinline__ void stage_rows_t(T* __restrict__ S, const T* __restr
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int gr = row0 + rb * 8 + j;
-      in[j] = (gr < nrows && d0 < D) ? *reinterpret_cast<const uint4*>(G + (int64_t)gr * gstride + d0) : z;
+      if (gr < nrows && d0 < D) in[j] = *reinterpret_cast<const uint4*>(G + (int64_t)gr * gstride + d0);
+      else in[j] = z;
     }
     transpose8x8(in, out);
 #pragma unroll

@@ -272,7 +272,10 @@ __global__ __launch_bounds__(256) void embedding_vec(const int64_t* __restrict__
   T* dst = out + t * Hd;
   Vec16<T> z;
   z.raw = make_uint4(0, 0, 0, 0);
-  for (int64_t c = lane * VN; c < Hd; c += 64 * VN) st16(dst + c, ok ? ld16(src + c) : z);
+  for (int64_t c = lane * VN; c < Hd; c += 64 * VN) {
+    if (ok) st16(dst + c, ld16(src + c));
+    else st16(dst + c, z);
+  }
 }
 
 template <typename T>

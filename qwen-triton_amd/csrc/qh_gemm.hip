@@ -20,7 +20,8 @@
 //  * Tile order is XCD-aware: the 8 XCDs each take a contiguous run of tiles
 //    (grouped 8 M-tiles at a time) so operand panels are reused out of the
 //    XCD's own L2.
-//  * M <= 8 (decode) uses a VALU GEMV that streams B once at full width.
+//  * M <= 8 (decode) uses a VALU GEMV that streams B once at full width;
+//    8 < M <= 64 uses a skinny MFMA kernel with in-workgroup K/N splits.
 #include "qh_mfma.h"
 
 namespace {
@@ -46,7 +47,8 @@ struct TileLoader {
         const int c = tid + i * 256;
         const int row = c >> 3, kc = c & 7;
         const int gr = row0 + row, gk = k0 + kc * 8;
-        r[i] = (gr < rows && gk < K) ? *reinterpret_cast<const uint4*>(P + (int64_t)gr * ld + gk) : z;
+        if (gr < rows && gk < K) r[i] = *reinterpret_cast<const uint4*>(P + (int64_t)gr * ld + gk);
+        else r[i] = z;
       }
     } else {
 #pragma unroll
@@ -58,7 +60,8 @@ struct TileLoader {
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const int gk = k0 + kb * 8 + j;
-            r[s * 8 + j] = (gr < rows && gk < K) ? *reinterpret_cast<const uint4*>(P + (int64_t)gk * ld + gr) : z;
+            if (gr < rows && gk < K) r[s * 8 + j] = *reinterpret_cast<const uint4*>(P + (int64_t)gk * ld + gr);
+            else r[s * 8 + j] = z;
           }
         }
       }
@@ -253,6 +256,105 @@ __global__ __launch_bounds__(256) void gemv_kernel(const T* __restrict__ A, int6
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Skinny GEMM for 8 < M <= 64 (batched decode), "NN" layout (both operands
+// k-contiguous). MFMA 16x16x32 with operand fragments loaded straight from
+// global memory (the activation rows stay L2-resident; each weight byte is
+// read once). A workgroup owns 16*WN output columns; its 4 wavefronts form WN
+// column groups x (4/WN) K-splits whose partial tiles are summed through LDS in
+// a fixed order. 16x16x32 layout for lane l: A row l%16 / B col l%16 with
+// k = 8*(l/16)+e; C col l%16, rows 4*(l/16)+r.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ f32x4 mma16(typename Mfma<T>::v8 a, typename Mfma<T>::v8 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mma16<bf16_t>(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mma16<f16_t>(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+template <typename T, typename OT, int MT, int WN>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B,
+                                                          int64_t ldb, OT* __restrict__ C, int64_t ldc,
+                                                          const T* __restrict__ bias, int M, int N, int K) {
+  constexpr int KS = 4 / WN;  // K-splits per column group
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ float red[4][MT * 16][17];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wn = wid / KS, ks = wid % KS;
+  const int n0 = (blockIdx.x * WN + wn) * 16;
+  const int li = lane & 15, kq = (lane >> 4) * 8;
+  const int n = n0 + li;
+  const bool nok = n < N;
+  const T* brow = B + (int64_t)(nok ? n : 0) * ldb;
+  f32x4 acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  v8 zero;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
+  // Each step consumes 32 k; split s takes steps s, s+KS, ... UNR steps are
+  // loaded before any of them is multiplied to keep enough bytes in flight.
+  constexpr int UNR = 4;
+  for (int k0 = ks * 32; k0 < K; k0 += 32 * KS * UNR) {
+    v8 b[UNR], a[UNR][MT];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int k = k0 + u * 32 * KS + kq;
+      const bool kok = k < K;
+      b[u] = zero;
+      if (nok && kok) b[u] = *reinterpret_cast<const v8*>(brow + k);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = i * 16 + li;
+        a[u][i] = zero;
+        if (m < M && kok) a[u][i] = *reinterpret_cast<const v8*>(A + (int64_t)m * lda + k);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+#pragma unroll
+      for (int i = 0; i < MT; ++i) acc[i] = mma16<T>(a[u][i], b[u], acc[i]);
+  }
+  // C layout: column li, rows 4*(lane/16) + r of each 16-row tile.
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wid][i * 16 + (lane >> 4) * 4 + r][li] = acc[i][r];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < WN * MT * 16 * 16; idx += 256) {
+    const int g = idx / (MT * 256), rem = idx % (MT * 256);
+    const int row = rem / 16, col = rem % 16;
+    float v = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < KS; ++s2) v += red[g * KS + s2][row][col];
+    const int gn = (blockIdx.x * WN + g) * 16 + col;
+    if (row < M && gn < N) C[(int64_t)row * ldc + gn] = from_f32<OT>(v + (bias ? to_f32(bias[gn]) : 0.f));
+  }
+}
+
+template <typename T, typename OT>
+void launch_skinny(const T* a, int64_t lda, const T* b, int64_t ldb, OT* c, int64_t ldc, const T* bi, int M, int N,
+                   int K, hipStream_t st) {
+  // Wide outputs: one 16-column group per wavefront (activation rows read once
+  // per 64 columns). Narrow outputs: 4-way K split for more workgroups.
+  const bool wide = N >= 8192;
+  const int cols = wide ? 64 : 16;
+  const int grid = (N + cols - 1) / cols;
+  const int mt = (M + 15) / 16;
+#define QH_SK(MTV, WNV) gemm_skinny_kernel<T, OT, MTV, WNV><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K)
+#define QH_SK_W(MTV) if (wide) QH_SK(MTV, 4); else QH_SK(MTV, 1);
+  if (mt == 1) { QH_SK_W(1) } else if (mt == 2) { QH_SK_W(2) } else if (mt == 3) { QH_SK_W(3) } else { QH_SK_W(4) }
+#undef QH_SK_W
+#undef QH_SK
+}
+
 // ---------------------------------------------------------------------------
 // Generic VALU GEMM (fp32 and shapes the MFMA path does not take). 64x64 tile,
 // 256 threads each owning a 4x4 block, fp32 accumulation.
@@ -342,6 +444,11 @@ int gemm_typed(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, 
       else if (M <= 4) QH_GEMV(4);
       else QH_GEMV(8);
 #undef QH_GEMV
+      return QH_OK;
+    }
+    // Skinny path for batched decode.
+    if (M <= 64 && !ta && !tb && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B)) {
+      launch_skinny<T, OT>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
       return QH_OK;
     }
     // MFMA path: 16-byte aligned operand rows along their contiguous dimension.

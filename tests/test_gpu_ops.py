@@ -289,7 +289,8 @@ def test_index_add_autograd():
 # GEMM
 # ---------------------------------------------------------------------------
 GEMM_SHAPES = [(1, 64, 128), (5, 300, 256), (8, 1024, 1024), (64, 1024, 1024), (200, 384, 512),
-               (512, 512, 1024), (300, 520, 136), (1024, 3072, 1024), (17, 2048, 72)]
+               (512, 512, 1024), (300, 520, 136), (1024, 3072, 1024), (17, 2048, 72), (33, 9000, 256),
+               (40, 3072, 1024), (64, 100, 64), (16, 8200, 1000), (9, 33, 40)]
 
 
 @pytest.mark.parametrize("M,N,Kd", GEMM_SHAPES)
