@@ -1,0 +1,247 @@
+"""Pins the CPU oracle against independent authorities (CPU only).
+
+Each oracle function is checked against something that does not restate its
+formula: torch built-ins (SDPA, cross_entropy, softmax, topk, index_add_,
+one_hot, embedding, linear), autograd of the forward, HF transformers' Qwen3 /
+Qwen3-MoE code (the reference's ``ref`` backend), complex-number rotation,
+adjoint identities, brute-force loops, and the reference's own known-answer
+test. A plausible slip (dropped term, wrong sign, transposed operand, wrong
+tie rule) fails at least one of them.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import ops as O
+
+D64 = torch.float64
+
+
+def g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rn(*shape, seed=0, dtype=D64):
+    return torch.randn(*shape, generator=g(seed), dtype=dtype)
+
+
+# ---------------------------------------------------------------- attention
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("groups", [1, 2, 4])
+def test_attention_matches_sdpa_and_lse(causal, groups):
+    q = rn(2, 4, 9, 16, seed=1)
+    k = rn(2, 4 // groups, 9, 16, seed=2)
+    v = rn(2, 4 // groups, 9, 16, seed=3)
+    out, lse = O.attention(q, k, v, 0.25, causal, groups)
+    ke, ve = k.repeat_interleave(groups, 1), v.repeat_interleave(groups, 1)
+    ref = F.scaled_dot_product_attention(q, ke, ve, is_causal=causal, scale=0.25)
+    torch.testing.assert_close(out, ref)
+    s = (q @ ke.transpose(-1, -2)) * 0.25
+    if causal:
+        s = s.masked_fill(torch.ones(9, 9, dtype=torch.bool).triu(1), float("-inf"))
+    torch.testing.assert_close(lse, torch.logsumexp(s, -1))
+
+
+def test_attention_bottom_right_offset_equals_explicit_mask():
+    q, k, v = rn(1, 2, 3, 8, seed=4), rn(1, 2, 7, 8, seed=5), rn(1, 2, 7, 8, seed=6)
+    out, _ = O.attention(q, k, v, 0.3, True, 1, causal_offset=4)
+    mask = torch.tensor([[j <= i + 4 for j in range(7)] for i in range(3)])
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=0.3)
+    torch.testing.assert_close(out, ref)
+
+
+@pytest.mark.parametrize("causal,groups,off", [(True, 2, 0), (False, 1, 0), (True, 1, 3)])
+def test_attention_backward_matches_autograd(causal, groups, off):
+    q = rn(1, 4, 6, 8, seed=7).requires_grad_(True)
+    k = rn(1, 4 // groups, 6 + off, 8, seed=8).requires_grad_(True)
+    v = rn(1, 4 // groups, 6 + off, 8, seed=9).requires_grad_(True)
+    go = rn(1, 4, 6, 8, seed=10)
+    ke, ve = k.repeat_interleave(groups, 1), v.repeat_interleave(groups, 1)
+    mask = None
+    if causal:
+        mask = torch.tensor([[j <= i + off for j in range(6 + off)] for i in range(6)])
+    F.scaled_dot_product_attention(q, ke, ve, attn_mask=mask, scale=0.4).backward(go)
+    dq, dk, dv = O.attention_backward(q, k, v, go, 0.4, causal, groups, off)
+    torch.testing.assert_close(dq, q.grad)
+    torch.testing.assert_close(dk, k.grad)
+    torch.testing.assert_close(dv, v.grad)
+
+
+# ---------------------------------------------------------------- RMSNorm
+def test_rmsnorm_matches_hf_qwen3():
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+
+    x = rn(3, 5, 64, seed=11, dtype=torch.float32)
+    norm = Qwen3RMSNorm(64, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(rn(64, seed=12, dtype=torch.float32))
+    torch.testing.assert_close(O.rmsnorm(x, norm.weight, 1e-6).float(), norm(x), atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("one_plus", [False, True])
+def test_rmsnorm_backward_matches_autograd(one_plus):
+    x = rn(4, 7, 32, seed=13).requires_grad_(True)
+    w = rn(32, seed=14).requires_grad_(True)
+    go = rn(4, 7, 32, seed=15)
+    y = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * (w + (1.0 if one_plus else 0.0))
+    y.backward(go)
+    gx, gw = O.rmsnorm_backward(x, w, go, 1e-6, one_plus)
+    torch.testing.assert_close(gx, x.grad)
+    torch.testing.assert_close(gw, w.grad)
+    torch.testing.assert_close(O.rmsnorm(x, w, 1e-6, one_plus), y)
+
+
+# ---------------------------------------------------------------- RoPE
+def test_rope_full_rotary_matches_hf():
+    from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb
+
+    q, k = rn(2, 4, 6, 32, seed=16), rn(2, 2, 6, 32, seed=17)
+    cos, sin = O.rotary_tables(torch.arange(6), 32, 1e6, D64)
+    hq, hk = apply_rotary_pos_emb(q, k, cos, sin)
+    torch.testing.assert_close(O.rope(q, cos, sin), hq)
+    torch.testing.assert_close(O.rope(k, cos, sin), hk)
+
+
+def test_rope_partial_is_complex_rotation():
+    x = rn(2, 3, 5, 16, seed=18)
+    cos, sin = rn(2, 5, 8, seed=19), rn(2, 5, 8, seed=20)  # arbitrary tables, as the reference test uses
+    out = O.rope(x, cos, sin)
+    z = torch.complex(x[..., :4], x[..., 4:8]) * torch.complex(cos[:, None, :, :4], sin[:, None, :, :4])
+    torch.testing.assert_close(out[..., :4], z.real)
+    torch.testing.assert_close(out[..., 4:8], z.imag)
+    torch.testing.assert_close(out[..., 8:], x[..., 8:])
+
+
+def test_rope_backward_is_adjoint():
+    x, gr = rn(2, 3, 5, 16, seed=21), rn(2, 3, 5, 16, seed=22)
+    cos, sin = rn(1, 5, 12, seed=23), rn(1, 5, 12, seed=24)
+    lhs = (O.rope(x, cos, sin) * gr).sum()
+    rhs = (x * O.rope_backward(gr, cos, sin)).sum()
+    torch.testing.assert_close(lhs, rhs)
+
+
+# ---------------------------------------------------------------- gated products
+def test_gated_products_match_torch_and_autograd():
+    a = rn(5, 33, seed=25).requires_grad_(True)
+    b = rn(5, 33, seed=26).requires_grad_(True)
+    go = rn(5, 33, seed=27)
+    y = F.silu(a) * b
+    torch.testing.assert_close(O.silu_mul(a, b), y)
+    y.backward(go)
+    ga, gb = O.silu_mul_backward(a, b, go)
+    torch.testing.assert_close(ga, a.grad)
+    torch.testing.assert_close(gb, b.grad)
+    a.grad = b.grad = None
+    y = a * torch.sigmoid(b)
+    torch.testing.assert_close(O.sigmoid_mul(a, b), y)
+    y.backward(go)
+    ga, gb = O.sigmoid_mul_backward(a, b, go)
+    torch.testing.assert_close(ga, a.grad)
+    torch.testing.assert_close(gb, b.grad)
+
+
+# ---------------------------------------------------------------- CE / softmax
+def test_cross_entropy_matches_torch():
+    x = rn(9, 37, seed=28).requires_grad_(True)
+    t = torch.randint(0, 37, (9,), generator=g(29))
+    t[[2, 5]] = -100
+    ref = F.cross_entropy(x, t, ignore_index=-100)
+    loss, lse, rows = O.cross_entropy(x, t)
+    torch.testing.assert_close(loss, ref)
+    torch.testing.assert_close(lse, torch.logsumexp(x, -1))
+    (ref * 3.0).backward()
+    torch.testing.assert_close(O.cross_entropy_backward(x, t, 3.0), x.grad)
+
+
+def test_cross_entropy_all_ignored_clamps_to_zero():
+    # reference kernel path divides by n_valid.clamp(min=1) (cross_entropy.py:157-160)
+    x, t = rn(3, 5, seed=30), torch.full((3,), -100)
+    assert float(O.cross_entropy(x, t)[0]) == 0.0
+
+
+def test_softmax_matches_torch_and_autograd():
+    x = rn(6, 19, seed=31).requires_grad_(True)
+    y = torch.softmax(x, -1)
+    torch.testing.assert_close(O.softmax(x), y)
+    go = rn(6, 19, seed=32)
+    y.backward(go)
+    torch.testing.assert_close(O.softmax_backward(y, go), x.grad)
+
+
+# ---------------------------------------------------------------- routing
+def test_topk_matches_torch_on_distinct_values():
+    x = rn(50, 128, seed=33, dtype=torch.float32)
+    v, i = O.topk(x, 8)
+    tv, ti = torch.topk(x, 8)
+    assert torch.equal(i, ti) and torch.equal(v, tv)
+
+
+def test_topk_tie_rule_lowest_index_first():
+    x = torch.tensor([[1.0, 3.0, 3.0, 0.5, 3.0, 1.0], [2.0] * 6])
+    assert O.topk(x, 4)[1].tolist() == [[1, 2, 4, 0], [0, 1, 2, 3]]
+
+
+def test_one_hot_and_index_add_match_torch():
+    idx = torch.randint(0, 11, (7, 3), generator=g(34))
+    assert torch.equal(O.one_hot(idx, 11), F.one_hot(idx, 11))
+    tgt, src = rn(10, 4, seed=35), rn(25, 4, seed=36)
+    index = torch.randint(0, 10, (25,), generator=g(37))
+    torch.testing.assert_close(O.index_add(tgt, src, index), tgt.clone().index_add_(0, index, src))
+
+
+# ---------------------------------------------------------------- embedding / linear / cache
+def test_embedding_and_backward_match_autograd():
+    w = rn(20, 6, seed=38).requires_grad_(True)
+    ids = torch.randint(0, 20, (3, 9), generator=g(39))
+    y = F.embedding(ids, w, padding_idx=4)
+    torch.testing.assert_close(O.embedding(ids, w), y)
+    go = rn(3, 9, 6, seed=40)
+    y.backward(go)
+    torch.testing.assert_close(O.embedding_backward(ids, go, 20, padding_idx=4), w.grad)
+
+
+def test_linear_and_backward_match_autograd():
+    x = rn(2, 5, 7, seed=41).requires_grad_(True)
+    w = rn(3, 7, seed=42).requires_grad_(True)
+    b = rn(3, seed=43).requires_grad_(True)
+    y = F.linear(x, w, b)
+    torch.testing.assert_close(O.linear(x, w, b), y)
+    go = rn(2, 5, 3, seed=44)
+    y.backward(go)
+    gx, gw, gb = O.linear_backward(x, w, go, need_bias=True)
+    torch.testing.assert_close(gx, x.grad)
+    torch.testing.assert_close(gw, w.grad)
+    torch.testing.assert_close(gb, b.grad)
+
+
+def test_kv_write_known_answer():
+    # reference tests/test_kernels.py:181-189
+    cache = torch.zeros(2, 3, 16, 8)
+    values = rn(2, 3, 5, 8, seed=45, dtype=torch.float32)
+    out = O.kv_write(cache, values, torch.tensor([0, 1, 4, 7, 8]))
+    for s, p in enumerate([0, 1, 4, 7, 8]):
+        assert torch.equal(out[:, :, p], values[:, :, s])
+    untouched = [p for p in range(16) if p not in (0, 1, 4, 7, 8)]
+    assert torch.count_nonzero(out[:, :, untouched]) == 0
+
+
+# ---------------------------------------------------------------- MoE block vs HF
+def test_moe_block_matches_hf_qwen3_moe():
+    from transformers.models.qwen3_moe.configuration_qwen3_moe import Qwen3MoeConfig
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeSparseMoeBlock
+
+    torch.manual_seed(0)
+    cfg = Qwen3MoeConfig(hidden_size=32, moe_intermediate_size=16, num_experts=6, num_experts_per_tok=2,
+                         norm_topk_prob=True)
+    blk = Qwen3MoeSparseMoeBlock(cfg).double()
+    with torch.no_grad():
+        for p in blk.parameters():
+            p.copy_(torch.randn(p.shape, generator=g(46), dtype=D64) * 0.2)
+    x = rn(2, 7, 32, seed=47)
+    ref = blk(x)
+    gu, dn = blk.experts.gate_up_proj, blk.experts.down_proj
+    out, *_ = O.moe_block(x.view(-1, 32), blk.gate.weight, gu[:, :16], gu[:, 16:], dn, 2, True)
+    torch.testing.assert_close(out.view(2, 7, 32), ref)
