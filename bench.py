@@ -13,8 +13,9 @@ as a HIP graph and replayed ``--steps`` times. ``value`` is decode tokens/s
 * ``cpu_baseline``: the CPU oracle (fp32 torch, HF semantics) decoding a
   bounded sample of the same workload on the host cores.
 
-``--workload fa|dense|moe`` time the other BASELINE configs' kernels (used for
-profiling; they print their own JSON line).
+``--workload fa|dense|gemm`` time the other BASELINE configs' kernels and
+``--workload roofline`` runs only the dominant kernel plus a 1 GiB calibration
+copy (used for the rocprofv3 counter passes); each prints its own JSON line.
 """
 from __future__ import annotations
 
@@ -33,6 +34,12 @@ for _p in (ROOT / "qwen-triton_amd", ROOT):
 METRIC = "Qwen3-0.6B prefill/decode tok/s on 1 MI355X + % of MFMA/HBM roofline"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+# HBM bytes per launch of the decode attention (decode + combine kernels), from the
+# two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`,
+# each scaled by the same counter's reading for a 1 GiB copy (fetch x2.000, write x1.000):
+# (262837.5 + 1070.0) KiB x 2 + (2176.0 + 256.0) KiB = 542,972,928 bytes.
+DECODE_TRAFFIC_BYTES = 542_972_928
 
 QWEN3_06B = dict(model_type="qwen3", vocab_size=151936, hidden_size=1024, intermediate_size=3072,
                  num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8, head_dim=128,
@@ -163,7 +170,7 @@ def attention_roofline(model, cache, reps=50, batch=64, ctx=2048):
     algo = kv_bytes + io_bytes
     achieved = algo / (avg_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC_BYTES,
             "kernel": "fa_decode_kernel+fa_decode_combine", "avg_launch_us": round(avg_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": algo}
 
@@ -361,12 +368,41 @@ def bench_gemm(steps, warmup):
     return out
 
 
+def bench_roofline_kernels(reps=20):
+    """Only the dominant decode kernel (one layer's cache) plus a 1 GiB copy for counter calibration."""
+    import torch
+    from qwen_triton.kernels import flash_attention as FA
+
+    B, Hq, Hkv, D, sk = 64, 16, 8, 128, 2049
+    g = torch.Generator(device="cuda").manual_seed(0)
+    kc = torch.randn(B, Hkv, sk + 63, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    vc = torch.randn(B, Hkv, sk + 63, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    q = torch.randn(B, Hq, 1, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    times = {"decode": [], "copy": []}
+    for i in range(reps):
+        for name, fn in (("decode", lambda: FA.flash_decode(q, kc[:, :, :sk], vc[:, :, :sk], D ** -0.5, Hq // Hkv)),
+                         ("copy", lambda: dst.copy_(src))):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            times[name].append((a, b))
+    sync()
+    res = {k: sum(a.elapsed_time(b) for a, b in v[2:]) / (len(v) - 2) * 1e3 for k, v in times.items()}
+    kv = 2 * B * Hkv * sk * D * 2
+    return {"decode_us": round(res["decode"], 2), "decode_gbs": round(kv / res["decode"] / 1e3, 1),
+            "copy_us": round(res["copy"], 2), "copy_gbs": round(2 * (1 << 30) / res["copy"] / 1e3, 1),
+            "decode_algorithmic_bytes": kv, "copy_bytes_each_way": 1 << 30}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="decode", choices=["decode", "fa", "dense", "gemm"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "fa", "dense", "gemm", "roofline"])
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -386,6 +422,9 @@ def main() -> None:
     if args.workload == "fa":
         res = bench_fa(args.steps, args.warmup)
         print(json.dumps({"metric": "flash attention fwd+bwd (config 1)", **res}), flush=True)
+        return
+    if args.workload == "roofline":
+        print(json.dumps({"metric": "dominant kernel + calibration copy", **bench_roofline_kernels()}), flush=True)
         return
     if args.workload == "gemm":
         res = bench_gemm(args.steps, args.warmup)

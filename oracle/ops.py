@@ -279,12 +279,6 @@ def moe_block(x, gate_w, w_gate, w_up, w_down, top_k, norm_topk_prob=True, route
     return out, logits, weights, experts
 
 
-def swiglu_mlp(x, w_gate, w_up, w_down, dtype=F64):
-    """SwiGLU MLP — qwen_triton/modules/mlp.py:19-22."""
-    xd = _d(x, dtype)
-    return silu_mul(xd @ _d(w_gate, dtype).T, xd @ _d(w_up, dtype).T, dtype) @ _d(w_down, dtype).T
-
-
 def rotary_tables(positions, rotary_dim, theta, dtype=torch.float32):
     """cos/sin [1, S, rot] — qwen_triton/modules/rotary.py:10-26 (fp32 tables)."""
     inv = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2, dtype=torch.float32) / rotary_dim))

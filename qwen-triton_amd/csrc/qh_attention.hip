@@ -498,7 +498,7 @@ __global__ __launch_bounds__(256) void fa_decode_kernel(const T* __restrict__ Q,
   constexpr int LPK = DP / 8;          // lanes per key row
   constexpr int GPW = 64 / LPK;        // key groups per wavefront
   constexpr int NG = 4 * GPW;          // key groups per workgroup
-  constexpr int UNR = 2;               // keys in flight per group
+  constexpr int UNR = 4;               // keys in flight per group
   __shared__ float red_m[NG][G], red_l[NG][G];
   __shared__ float red_o[NG][G][DP];
 

@@ -89,17 +89,39 @@ __device__ __forceinline__ void st16(T* p, const Vec16<T>& v) {
 
 // ---------------------------------------------------------------------------
 // Wavefront reductions (64 lanes). `width` must be a power of two <= 64 and
-// reduces within aligned groups of `width` lanes.
+// reduces within aligned groups of `width` lanes; every lane gets the result.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v, int width = QH_WAVE) {
-  for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, width);
+// DPP lane permutations (gfx9 encodings): quad_perm xor-1 / xor-2, and the
+// half-row / row mirrors that pair lane i with 7-i / 15-i. Applied in sequence
+// they all-reduce 16 lanes with plain VALU ops (no LDS crossbar traffic).
+#define QH_DPP_XOR1 0xB1
+#define QH_DPP_XOR2 0x4E
+#define QH_DPP_HALF_MIRROR 0x141
+#define QH_DPP_MIRROR 0x140
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+template <bool MAX>
+__device__ __forceinline__ float red_op(float a, float b) {
+  return MAX ? fmaxf(a, b) : a + b;
+}
+
+template <bool MAX>
+__device__ __forceinline__ float group_reduce(float v, int width) {
+  if (width >= 2) v = red_op<MAX>(v, dpp_f32<QH_DPP_XOR1>(v));
+  if (width >= 4) v = red_op<MAX>(v, dpp_f32<QH_DPP_XOR2>(v));
+  if (width >= 8) v = red_op<MAX>(v, dpp_f32<QH_DPP_HALF_MIRROR>(v));
+  if (width >= 16) v = red_op<MAX>(v, dpp_f32<QH_DPP_MIRROR>(v));
+  for (int o = 16; o < width; o <<= 1) v = red_op<MAX>(v, __shfl_xor(v, o, width));
   return v;
 }
 
-__device__ __forceinline__ float wave_max(float v, int width = QH_WAVE) {
-  for (int o = width >> 1; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, width));
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v, int width = QH_WAVE) { return group_reduce<false>(v, width); }
+
+__device__ __forceinline__ float wave_max(float v, int width = QH_WAVE) { return group_reduce<true>(v, width); }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` must hold
 // blockDim.x / 64 floats. The result is returned to every thread.

@@ -245,3 +245,12 @@ def test_moe_block_matches_hf_qwen3_moe():
     gu, dn = blk.experts.gate_up_proj, blk.experts.down_proj
     out, *_ = O.moe_block(x.view(-1, 32), blk.gate.weight, gu[:, :16], gu[:, 16:], dn, 2, True)
     torch.testing.assert_close(out.view(2, 7, 32), ref)
+
+
+def test_kv_append_and_residual_add():
+    a, b = rn(2, 3, 4, 5, seed=48), rn(2, 3, 2, 5, seed=49)
+    out = O.kv_append(a, b)
+    assert out.shape == (2, 3, 6, 5)
+    assert torch.equal(out[:, :, :4], a) and torch.equal(out[:, :, 4:], b)
+    x, r = rn(7, seed=50), rn(7, seed=51)
+    assert torch.equal(O.residual_add(x, r), torch.add(x, r))
