@@ -40,6 +40,14 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-file additions. Attention keeps its MFMA accumulators in VGPRs (with no
+# AGPR copies around the online-softmax rescale, the forward fits two waves per
+# SIMD) and assumes NaN-free scores, so max() needs no NaN canonicalisation.
+FILE_FLAGS = {
+    "qh_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
+}
+
+
 def _sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
@@ -50,10 +58,10 @@ def _headers() -> list[Path]:
 
 def _compile(src: Path, force: bool) -> tuple[Path, str]:
     obj = BUILD_DIR / (src.stem + ".o")
-    newest_dep = max([src.stat().st_mtime] + [h.stat().st_mtime for h in _headers()])
+    newest_dep = max([src.stat().st_mtime, Path(__file__).stat().st_mtime] + [h.stat().st_mtime for h in _headers()])
     if not force and obj.exists() and obj.stat().st_mtime >= newest_dep:
         return obj, ""
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")

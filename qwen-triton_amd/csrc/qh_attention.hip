@@ -108,20 +108,191 @@ __device__ __forceinline__ void stage_rows_t(T* __restrict__ S, const T* __restr
 // ===========================================================================
 // Forward
 // ===========================================================================
-template <typename T, int DP, int QT>
+// LDS tiles of K and V are stored in their natural [key][d] layout with DP*2
+// byte rows and no padding; the 16-byte chunks of row r are XOR-swizzled
+// (physical chunk = logical chunk ^ (r % 8)) so that both fragment reads below
+// spread over all 32 banks. Tiles are written straight from global memory by
+// global_load_lds (16 bytes per lane, lane l -> base + 16*l), so staging needs
+// neither registers nor VALU work and overlaps the previous tile's math.
+//
+//  * K is the A operand of S^T = K Q^T: one 16-byte read per fragment.
+//  * V^T is the A operand of O^T += V^T P^T: gfx950's ds_read_b64_tr_b16
+//    returns, in each 16-lane group, element (i % 4) of the 8-byte words
+//    addressed by lanes i/4 + 4e (e = 0..3); lanes that address 4 consecutive
+//    keys x 4 d-quads therefore receive 4 consecutive keys of one d each.
+
+typedef short qh_v4i16 __attribute__((ext_vector_type(4)));
+
+typedef short qh_v8i16 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ int swz(int row, int chunk, int cpr) {
+  return chunk ^ (row & ((cpr < 8 ? cpr : 8) - 1));
+}
+
+// One V^T A-operand fragment: two transpose reads at keys key and key + 8 of
+// column d, joined as whole vectors (element-wise short -> bf16 inserts are
+// lowered incorrectly by the current compiler: they broadcast element 0).
+template <typename T, int DP>
+__device__ __forceinline__ typename Mfma<T>::v8 read_vt_frag(const T* Vt, int key, int d) {
+  constexpr int CPR = DP / 8;
+  const T* s0 = Vt + key * DP + swz(key, d >> 3, CPR) * 8 + (d & 7);
+  const T* s1 = Vt + (key + 8) * DP + swz(key + 8, d >> 3, CPR) * 8 + (d & 7);
+  const qh_v4i16 w0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) qh_v4i16*)(s0));
+  const qh_v4i16 w1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) qh_v4i16*)(s1));
+  const qh_v8i16 w = __builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(typename Mfma<T>::v8, w);
+}
+
+// Direct-to-LDS loads, 16 bytes per lane: lane l's bytes land at LDS byte
+// address lds_base + 16 * l (lds_base is wave-uniform and travels in M0).
+// They are issued as inline asm so the compiler's wait-count pass does not
+// track them: it would otherwise have to assume that every later LDS read may
+// alias the in-flight load and wait for it at once, serialising the prefetch.
+// Callers wait explicitly (s_waitcnt vmcnt(0) + barrier) before reading the
+// destination. M0 has no other user in these kernels.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 64-bit per-lane address.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base)
+               : "memory", "m0");
+}
+// Wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte offset.
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds_base)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Loader of ROWS x DP tiles (rows along seq, DP columns) into the swizzled
+// LDS layout. Each of the 4 waves issues ROWS / RPI / 4 instructions of 1 KiB
+// (RPI rows each). A lane's byte offset inside its rows is the same for every
+// instruction and every tile, so full tiles cost no per-lane address math;
+// a tile that runs past nrows clamps its rows (and d-chunks past D) onto valid
+// memory, whose finite contents are masked or multiplied by zero downstream.
+template <typename T, int ROWS, int DP>
+struct TileLoader {
+  static constexpr int CPR = DP / 8;     // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;   // rows per wave instruction
+  static constexpr int NI = ROWS / RPI;  // instructions per tile
+  static_assert(NI % 4 == 0, "tile must split evenly over 4 waves");
+  int wid, rl, d0;
+  uint32_t voff;
+  __device__ __forceinline__ TileLoader(int64_t gstride, int D) {
+    const int lane = threadIdx.x & 63;
+    wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    rl = lane / CPR;
+    // the row's swizzle depends only on (n * RPI + rl) % 8, which is the same
+    // for every instruction n of this wave (n = 4 i + wid)
+    const int c = swz(wid * RPI + rl, lane % CPR, CPR);
+    d0 = c * 8 < D ? c * 8 : D - 8;
+    voff = (uint32_t)(((int64_t)rl * gstride + d0) * (int64_t)sizeof(T));
+  }
+  __device__ __forceinline__ void load(T* lds_tile, const T* __restrict__ G, int64_t gstride, int row0,
+                                       int nrows) const {
+    const uint32_t base = lds_addr(lds_tile);
+    if (row0 + ROWS <= nrows) {
+#pragma unroll
+      for (int i = 0; i < NI / 4; ++i) {
+        const int n = i * 4 + wid;
+        lds_dma16_s(voff, G + (int64_t)(row0 + n * RPI) * gstride, base + (uint32_t)(n * RPI * DP * sizeof(T)));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI / 4; ++i) {
+        const int n = i * 4 + wid;
+        int gr = row0 + n * RPI + rl;
+        gr = gr < nrows ? gr : nrows - 1;
+        lds_dma16(G + (int64_t)gr * gstride + d0, base + (uint32_t)(n * RPI * DP * sizeof(T)));
+      }
+    }
+  }
+};
+
+template <typename T, int DP, bool MASK>
+__device__ __forceinline__ void fa_fwd_tile(const T* Kt, const T* Vt, const typename Mfma<T>::v8 (&qf)[DP / 16],
+                                            f32x16 (&acc)[DP / 32], float& m, float& l, int kv0, int qi, int lim,
+                                            float scale_log2, int lane) {
+  constexpr int CPR = DP / 8, DT = DP / 32, KD = DP / 16;
+  typedef typename Mfma<T>::v8 v8;
+  const int ql = lane & 31, hf = lane >> 5;
+  f32x16 s[2];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    s[kt] = zero16();
+    const int row = kt * 32 + ql;
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      const int c = swz(row, kd * 2 + hf, CPR);
+      s[kt] = Mfma<T>::mma(load_frag16<T>(Kt + row * DP + c * 8), qf[kd], s[kt]);
+    }
+  }
+  if constexpr (MASK) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kv0 + kt * 32 + g * 8 + hf * 4 + r;
+          s[kt][g * 4 + r] = key > lim ? -INFINITY : s[kt][g * 4 + r];
+        }
+  }
+  float mx = fmaxf(s[0][0], s[1][0]);
+#pragma unroll
+  for (int e = 1; e < 16; ++e) mx = fmaxf(mx, fmaxf(s[0][e], s[1][e]));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  if (__any(mx > m)) {  // rescale only when some lane's running max grew (exact)
+    const float mnew = fmaxf(m, mx);
+    const float alpha = (m == -INFINITY) ? 0.f : exp2_((m - mnew) * scale_log2);
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[dt][e] *= alpha;
+    m = mnew;
+  }
+  const float mb = (m == -INFINITY) ? 0.f : m * scale_log2;
+  float ps = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = exp2_(__builtin_fmaf(s[kt][e], scale_log2, -mb));
+      s[kt][e] = p;
+      ps += p;
+    }
+  l += ps + __shfl_xor(ps, 32);
+  // V^T fragments through the LDS transpose read (see the note above).
+  const int grp = lane >> 4, j = lane & 15;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const v8 pf = pack_pair<T>(s[ks >> 1], (ks & 1) * 2);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d = dt * 32 + 16 * (grp & 1) + 4 * (j & 3);
+      const v8 a = read_vt_frag<T, DP>(Vt, ks * 16 + 4 * (grp >> 1) + (j >> 2), d);
+      acc[dt] = Mfma<T>::mma(a, pf, acc[dt]);
+    }
+  }
+}
+
+template <typename T, int DP>
 __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs,
                                                      const T* __restrict__ K, int64_t skb, int64_t skh, int64_t sks,
                                                      const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs,
                                                      T* __restrict__ O, float* __restrict__ LSE, int Hq, int groups,
                                                      int Sq, int Sk, int D, float scale_log2, int causal, int coff) {
-  constexpr int BN = 64;
-  constexpr int BMQ = 4 * 32 * QT;
-  constexpr int KLD = DP + 8;
-  constexpr int VLD = BN + 8;
+  constexpr int BN = 64, BMQ = 128;
   constexpr int DT = DP / 32, KD = DP / 16;
   typedef typename Mfma<T>::v8 v8;
-  __shared__ __attribute__((aligned(16))) T Ks[BN * KLD];
-  __shared__ __attribute__((aligned(16))) T Vt[DP * VLD];
+  __shared__ __attribute__((aligned(1024))) T Ks[2][BN * DP];
+  __shared__ __attribute__((aligned(1024))) T Vs[2][BN * DP];
 
   const int nqb = (Sq + BMQ - 1) / BMQ;
   const int qb = nqb - 1 - (int)blockIdx.x;
@@ -132,100 +303,54 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
   const T* Qb = Q + b * sqb + hq * sqh;
   const T* Kb = K + b * skb + hk * skh;
   const T* Vb = V + b * svb + hk * svh;
-  const int qw0 = qb * BMQ + wid * 32 * QT;
+  const int qw0 = qb * BMQ + wid * 32;
+  const int qi = qw0 + ql;
 
-  v8 qf[QT][KD];
+  v8 qf[KD];
 #pragma unroll
-  for (int t = 0; t < QT; ++t)
+  for (int kd = 0; kd < KD; ++kd) {
+    const int d0 = kd * 16 + hf * 8;
+    if (qi < Sq && d0 < D) qf[kd] = load_frag16<T>(Qb + (int64_t)qi * sqs + d0);
+    else
 #pragma unroll
-    for (int kd = 0; kd < KD; ++kd) {
-      const int qi = qw0 + t * 32 + ql, d0 = kd * 16 + hf * 8;
-      if (qi < Sq && d0 < D) qf[t][kd] = load_frag16<T>(Qb + (int64_t)qi * sqs + d0);
-      else
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[t][kd][e] = (T)0.f;
-    }
-
-  float m[QT], l[QT];
-  f32x16 acc[QT][DT];
-#pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    m[t] = -INFINITY;
-    l[t] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[t][dt] = zero16();
+      for (int e = 0; e < 8; ++e) qf[kd][e] = (T)0.f;
   }
+  float m = -INFINITY, l = 0.f;
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = zero16();
 
   int kv_end = Sk;
   if (causal) kv_end = min(Sk, qb * BMQ + BMQ + coff);
+  const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
+  // last key visible to this lane's query (causal and/or Sk bound)
+  const int lim = causal ? min(Sk - 1, qi + coff) : Sk - 1;
 
-  for (int kv0 = 0; kv0 < kv_end; kv0 += BN) {
-    __syncthreads();
-    stage_rows<T, BN, DP, KLD>(Ks, Kb, sks, kv0, Sk, D);
-    stage_rows_t<T, BN, DP, VLD>(Vt, Vb, svs, kv0, Sk, D);
-    __syncthreads();
-#pragma unroll
-    for (int t = 0; t < QT; ++t) {
-      const int qi = qw0 + t * 32 + ql;
-      f32x16 s[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        s[kt] = zero16();
-#pragma unroll
-        for (int kd = 0; kd < KD; ++kd)
-          s[kt] = Mfma<T>::mma(load_frag16<T>(Ks + (kt * 32 + ql) * KLD + kd * 16 + hf * 8), qf[t][kd], s[kt]);
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = kv0 + kt * 32 + g * 8 + hf * 4 + r;
-            float v = s[kt][g * 4 + r] * scale_log2;
-            if (key >= Sk || (causal && key > qi + coff)) v = -INFINITY;
-            s[kt][g * 4 + r] = v;
-            mx = fmaxf(mx, v);
-          }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(m[t], mx);
-      const float mref = (mnew == -INFINITY) ? 0.f : mnew;
-      const float alpha = exp2_(m[t] - mref);
-      float ps = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = exp2_(s[kt][e] - mref);
-          s[kt][e] = p;
-          ps += p;
-        }
-      ps += __shfl_xor(ps, 32);
-      l[t] = l[t] * alpha + ps;
-      m[t] = mnew;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[t][dt][e] *= alpha;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const v8 pf = pack_pair<T>(s[ks >> 1], (ks & 1) * 2);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const T* vr = Vt + (dt * 32 + ql) * VLD + ks * 16 + hf * 4;
-          acc[t][dt] = Mfma<T>::mma(load_frag_split<T>(vr, vr + 8), pf, acc[t][dt]);
-        }
-      }
+  const TileLoader<T, BN, DP> kload(sks, D), vload(svs, D);
+  if (ntiles > 0) {
+    kload.load(Ks[0], Kb, sks, 0, Sk);
+    vload.load(Vs[0], Vb, svs, 0, Sk);
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    const int kv0 = it * BN;
+    const int buf = it & 1;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile `it` have landed
+    __syncthreads();                // ... and everyone else's; tile it-1 is fully consumed
+    if (it + 1 < ntiles) {
+      kload.load(Ks[buf ^ 1], Kb, sks, kv0 + BN, Sk);
+      vload.load(Vs[buf ^ 1], Vb, svs, kv0 + BN, Sk);
     }
+    // wave-uniform: does any key of this tile lie past a query's limit?
+    const bool need_mask = (kv0 + BN > Sk) || (causal && kv0 + BN - 1 > qw0 + coff);
+    if (need_mask)
+      fa_fwd_tile<T, DP, true>(Ks[buf], Vs[buf], qf, acc, m, l, kv0, qi, lim, scale_log2, lane);
+    else
+      fa_fwd_tile<T, DP, false>(Ks[buf], Vs[buf], qf, acc, m, l, kv0, qi, lim, scale_log2, lane);
   }
 
-  T* Ob = O + (int64_t)bh * Sq * D;
-#pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    const int qi = qw0 + t * 32 + ql;
-    if (qi >= Sq) continue;
-    const float inv = l[t] > 0.f ? 1.0f / l[t] : 0.f;
+  if (qi < Sq) {
+    T* Ob = O + ((int64_t)bh * Sq + qi) * D;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -234,11 +359,11 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
         if (d < D) {
           typename Mfma<T>::v4 o4;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o4[r] = (T)(acc[t][dt][g * 4 + r] * inv);
-          *reinterpret_cast<typename Mfma<T>::v4*>(Ob + (int64_t)qi * D + d) = o4;
+          for (int r = 0; r < 4; ++r) o4[r] = (T)(acc[dt][g * 4 + r] * inv);
+          *reinterpret_cast<typename Mfma<T>::v4*>(Ob + d) = o4;
         }
       }
-    if (hf == 0 && LSE) LSE[(int64_t)bh * Sq + qi] = l[t] > 0.f ? (m[t] + __log2f(l[t])) * kLn2 : -INFINITY;
+    if (hf == 0 && LSE) LSE[(int64_t)bh * Sq + qi] = l > 0.f ? (m * scale_log2 + __log2f(l)) * kLn2 : -INFINITY;
   }
 }
 
@@ -670,10 +795,9 @@ extern "C" int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
   hipStream_t st = (hipStream_t)stream;
   const float sl2 = scale * kLog2e;
   const int groups = (int)(Hq / Hkv);
-  constexpr int QT = 1;
-  dim3 grid((unsigned)ceil_div(Sq, 128 * QT), (unsigned)(B * Hq));
+  dim3 grid((unsigned)ceil_div(Sq, 128), (unsigned)(B * Hq));
 #define QH_FWD(T, DPV)                                                                                          \
-  fa_fwd_kernel<T, DPV, QT><<<grid, 256, 0, st>>>((const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks,       \
+  fa_fwd_kernel<T, DPV><<<grid, 256, 0, st>>>((const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks,       \
                                                  (const T*)v, svb, svh, svs, (T*)o, lse, (int)Hq, groups, (int)Sq, \
                                                  (int)Sk, (int)D, sl2, causal, (int)causal_offset)
 #define QH_FWD_D(T) \
