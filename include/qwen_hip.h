@@ -147,7 +147,8 @@ int qh_index_add(void* target, int64_t stride_t, const void* src, int64_t stride
  *   A(m,k) = trans_a ? A[k*lda + m] : A[m*lda + k]
  *   B(n,k) = trans_b ? B[k*ldb + n] : B[n*ldb + k]
  * so forward x W^T (0,0), dX = dY W (0,1) and dW = dY^T X (1,1) need no copies.
- * bf16/f16 run on MFMA 32x32x16 with fp32 accumulation; f32 runs on VALU.
+ * bf16/f16 run on MFMA (32x32x16 tiles; 16x16x32 with a 16-way K split in one
+ * workgroup for M <= 64) with fp32 accumulation; f32 runs on VALU.
  * bias has the input dtype; C has out_dtype.
  * Replaces qwen_triton/kernels/matmul.py:64-97 (_matmul_kernel), :100-111 (_bias_add_kernel),
  * :130-200 (forward/backward launchers incl. the per-call transposes at :140, :184). */

@@ -20,8 +20,9 @@
 //  * Tile order is XCD-aware: the 8 XCDs each take a contiguous run of tiles
 //    (grouped 8 M-tiles at a time) so operand panels are reused out of the
 //    XCD's own L2.
-//  * M <= 8 (decode) uses a VALU GEMV that streams B once at full width;
-//    8 < M <= 64 uses a skinny MFMA kernel with in-workgroup K/N splits.
+//  * M <= 64 (decode) uses 1024-thread workgroups of MFMA 16x16x32 whose 16
+//    wavefronts split K, so the weight matrix is requested in one or two
+//    memory round trips; partials are summed through LDS in a fixed order.
 #include "qh_mfma.h"
 
 namespace {
@@ -201,70 +202,11 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
 }
 
 // ---------------------------------------------------------------------------
-// GEMV for M <= 8 ("NN" layout: both operands k-contiguous). One wavefront
-// owns NPW output columns; lanes split K in 16-byte vectors.
-// ---------------------------------------------------------------------------
-template <typename T, typename OT, int MR, int NPW>
-__global__ __launch_bounds__(256) void gemv_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B,
-                                                   int64_t ldb, OT* __restrict__ C, int64_t ldc,
-                                                   const T* __restrict__ bias, int M, int N, int K) {
-  constexpr int VN = Vec16<T>::N;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int nbase = (blockIdx.x * 4 + wid) * NPW;
-  if (nbase >= N) return;
-  float acc[MR][NPW];
-#pragma unroll
-  for (int m = 0; m < MR; ++m)
-#pragma unroll
-    for (int j = 0; j < NPW; ++j) acc[m][j] = 0.f;
-  for (int k = lane * VN; k < K; k += 64 * VN) {
-    Vec16<T> w[NPW];
-#pragma unroll
-    for (int j = 0; j < NPW; ++j) {
-      const int n = nbase + j;
-      if (n < N) w[j] = ld16(B + (int64_t)n * ldb + k);
-      else w[j].raw = make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      if (m < M) {
-        Vec16<T> x = ld16(A + (int64_t)m * lda + k);
-#pragma unroll
-        for (int j = 0; j < NPW; ++j)
-#pragma unroll
-          for (int e = 0; e < VN; ++e) acc[m][j] += to_f32(x.v[e]) * to_f32(w[j].v[e]);
-      }
-    }
-  }
-#pragma unroll
-  for (int m = 0; m < MR; ++m)
-#pragma unroll
-    for (int j = 0; j < NPW; ++j) acc[m][j] = wave_sum(acc[m][j]);
-  if (lane < NPW) {
-    const int n = nbase + lane;
-    if (n < N) {
-      const float bv = bias ? to_f32(bias[n]) : 0.f;
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        float v = 0.f;
-#pragma unroll
-        for (int j = 0; j < NPW; ++j)
-          if (j == lane) v = acc[m][j];
-        if (m < M) C[(int64_t)m * ldc + n] = from_f32<OT>(v + bv);
-      }
-    }
-  }
-}
-
-
-// ---------------------------------------------------------------------------
-// Skinny GEMM for 8 < M <= 64 (batched decode), "NN" layout (both operands
-// k-contiguous). MFMA 16x16x32 with operand fragments loaded straight from
-// global memory (the activation rows stay L2-resident; each weight byte is
-// read once). A workgroup owns 16*WN output columns; its 4 wavefronts form WN
-// column groups x (4/WN) K-splits whose partial tiles are summed through LDS in
-// a fixed order. 16x16x32 layout for lane l: A row l%16 / B col l%16 with
-// k = 8*(l/16)+e; C col l%16, rows 4*(l/16)+r.
+// Skinny GEMM for M <= 64 (decode), "NN" layout (both operands k-contiguous).
+// MFMA 16x16x32 with operand fragments loaded straight from global memory
+// (the activation rows stay cache-resident; each weight byte is read once).
+// 16x16x32 layout for lane l: A row l%16 / B col l%16 with k = 8*(l/16)+e;
+// C col l%16, rows 4*(l/16)+r.
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -279,80 +221,92 @@ __device__ __forceinline__ f32x4 mma16<f16_t>(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-template <typename T, typename OT, int MT, int WN>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B,
-                                                          int64_t ldb, OT* __restrict__ C, int64_t ldc,
-                                                          const T* __restrict__ bias, int M, int N, int K) {
-  constexpr int KS = 4 / WN;  // K-splits per column group
+// Decode GEMM for M <= 64: one 1024-thread workgroup (16 wavefronts) per
+// 16*CG output columns. The 16 waves form CG column groups x KSP K slices;
+// each wave streams its 16 weight columns over its K slice with every load of
+// a chunk (up to CH 32-wide k-steps) in flight before the first multiply, so
+// a whole layer's weight matrix is requested from memory in one or two round
+// trips. The KSP partial tiles are summed through LDS in slice order
+// (deterministic, no workspace, no cross-workgroup traffic).
+//
+// k mapping per 32-wide step: lane group q = lane / 16 takes k0 + 8 q .. +7,
+// so the four groups of a row read 64 contiguous bytes.
+template <typename T, typename OT, int MT, int KSP>
+__global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__ A, int64_t lda,
+                                                           const T* __restrict__ B, int64_t ldb, OT* __restrict__ C,
+                                                           int64_t ldc, const T* __restrict__ bias, int M, int N,
+                                                           int K, int kr) {
+  constexpr int CG = 16 / KSP;
+  constexpr int CH = MT <= 2 ? 8 : 4;  // k-steps whose loads are issued together
   typedef typename Mfma<T>::v8 v8;
-  __shared__ float red[4][MT * 16][17];
+  __shared__ float red[16][MT * 16][16];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int wn = wid / KS, ks = wid % KS;
-  const int n0 = (blockIdx.x * WN + wn) * 16;
-  const int li = lane & 15, kq = (lane >> 4) * 8;
-  const int n = n0 + li;
+  const int cg = wid / KSP, ks = wid % KSP;
+  const int li = lane & 15, q = lane >> 4;
+  const int n = (blockIdx.x * CG + cg) * 16 + li;
   const bool nok = n < N;
   const T* brow = B + (int64_t)(nok ? n : 0) * ldb;
+  const int kb = ks * kr, ke = min(K, kb + kr);
   f32x4 acc[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   v8 zero;
 #pragma unroll
   for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
-  // Each step consumes 32 k; split s takes steps s, s+KS, ... UNR steps are
-  // loaded before any of them is multiplied to keep enough bytes in flight.
-  constexpr int UNR = 4;
-  for (int k0 = ks * 32; k0 < K; k0 += 32 * KS * UNR) {
-    v8 b[UNR], a[UNR][MT];
+  for (int k0 = kb; k0 < ke; k0 += 32 * CH) {
+    v8 b[CH], a[CH][MT];
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int k = k0 + u * 32 * KS + kq;
-      const bool kok = k < K;
-      b[u] = zero;
+    for (int u = 0; u < CH; ++u) {
+      const int k = k0 + u * 32 + q * 8;
+      const bool kok = k < ke;
       if (nok && kok) b[u] = *reinterpret_cast<const v8*>(brow + k);
+      else b[u] = zero;
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int m = i * 16 + li;
-        a[u][i] = zero;
         if (m < M && kok) a[u][i] = *reinterpret_cast<const v8*>(A + (int64_t)m * lda + k);
+        else a[u][i] = zero;
       }
     }
 #pragma unroll
-    for (int u = 0; u < UNR; ++u)
+    for (int u = 0; u < CH; ++u)
 #pragma unroll
       for (int i = 0; i < MT; ++i) acc[i] = mma16<T>(a[u][i], b[u], acc[i]);
   }
-  // C layout: column li, rows 4*(lane/16) + r of each 16-row tile.
+  // C layout: column li, rows 16 i + 4 q + r.
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wid][i * 16 + (lane >> 4) * 4 + r][li] = acc[i][r];
+    for (int r = 0; r < 4; ++r) red[wid][i * 16 + q * 4 + r][li] = acc[i][r];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < WN * MT * 16 * 16; idx += 256) {
+  for (int idx = threadIdx.x; idx < CG * MT * 256; idx += 1024) {
     const int g = idx / (MT * 256), rem = idx % (MT * 256);
     const int row = rem / 16, col = rem % 16;
     float v = 0.f;
 #pragma unroll
-    for (int s2 = 0; s2 < KS; ++s2) v += red[g * KS + s2][row][col];
-    const int gn = (blockIdx.x * WN + g) * 16 + col;
+    for (int s2 = 0; s2 < KSP; ++s2) v += red[g * KSP + s2][row][col];
+    const int gn = (blockIdx.x * CG + g) * 16 + col;
     if (row < M && gn < N) C[(int64_t)row * ldc + gn] = from_f32<OT>(v + (bias ? to_f32(bias[gn]) : 0.f));
   }
 }
 
 template <typename T, typename OT>
-void launch_skinny(const T* a, int64_t lda, const T* b, int64_t ldb, OT* c, int64_t ldc, const T* bi, int M, int N,
-                   int K, hipStream_t st) {
-  // Wide outputs: one 16-column group per wavefront (activation rows read once
-  // per 64 columns). Narrow outputs: 4-way K split for more workgroups.
-  const bool wide = N >= 8192;
-  const int cols = wide ? 64 : 16;
+void launch_decode_gemm(const T* a, int64_t lda, const T* b, int64_t ldb, OT* c, int64_t ldc, const T* bi, int M,
+                        int N, int K, hipStream_t st) {
+  // Narrow outputs: all 16 waves split K (16 columns per workgroup). Wide
+  // outputs already give enough workgroups: 4 column groups x 4 K slices.
+  const bool wide = N > 8192;
+  const int ksp = wide ? 4 : 16;
+  const int cols = 16 * (16 / ksp);
   const int grid = (N + cols - 1) / cols;
+  const int kr = ((K + ksp - 1) / ksp + 31) / 32 * 32;
   const int mt = (M + 15) / 16;
-#define QH_SK(MTV, WNV) gemm_skinny_kernel<T, OT, MTV, WNV><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K)
-#define QH_SK_W(MTV) if (wide) QH_SK(MTV, 4); else QH_SK(MTV, 1);
-  if (mt == 1) { QH_SK_W(1) } else if (mt == 2) { QH_SK_W(2) } else if (mt == 3) { QH_SK_W(3) } else { QH_SK_W(4) }
-#undef QH_SK_W
-#undef QH_SK
+#define QH_DG(MTV, KSPV) \
+  gemm_decode_kernel<T, OT, MTV, KSPV><<<grid, 1024, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K, kr)
+#define QH_DG_W(MTV) if (wide) QH_DG(MTV, 4); else QH_DG(MTV, 16);
+  if (mt == 1) { QH_DG_W(1) } else if (mt == 2) { QH_DG_W(2) } else if (mt == 3) { QH_DG_W(3) } else { QH_DG_W(4) }
+#undef QH_DG_W
+#undef QH_DG
 }
 
 // ---------------------------------------------------------------------------
@@ -435,20 +389,11 @@ int gemm_typed(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, 
   const T* bi = (const T*)bias;
   constexpr bool is_mfma_type = !std::is_same<T, float>::value;
   if constexpr (is_mfma_type) {
-    // GEMV path: M tiny, both operands k-contiguous.
-    if (M <= 8 && !ta && !tb && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B)) {
-      const int grid = (N + 4 * 4 - 1) / (4 * 4);
-#define QH_GEMV(mr) gemv_kernel<T, OT, mr, 4><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K)
-      if (M == 1) QH_GEMV(1);
-      else if (M == 2) QH_GEMV(2);
-      else if (M <= 4) QH_GEMV(4);
-      else QH_GEMV(8);
-#undef QH_GEMV
-      return QH_OK;
-    }
-    // Skinny path for batched decode.
-    if (M <= 64 && !ta && !tb && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(A) && aligned16(B)) {
-      launch_skinny<T, OT>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
+    // Decode path for small M, both operands k-contiguous (wide outputs with
+    // M > 16, i.e. the batched LM head, stream better through the tiled kernel).
+    if (M <= 64 && !(M > 16 && N > 8192) && !ta && !tb && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
+        aligned16(A) && aligned16(B)) {
+      launch_decode_gemm<T, OT>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
       return QH_OK;
     }
     // MFMA path: 16-byte aligned operand rows along their contiguous dimension.

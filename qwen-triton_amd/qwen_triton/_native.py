@@ -152,3 +152,4 @@ def require_device(*tensors: torch.Tensor | None) -> None:
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+

@@ -305,6 +305,18 @@ def test_gemm_forward(M, N, Kd, dtype):
     close(y, O.linear(x, w, b), **BF16_TOL)
 
 
+@pytest.mark.parametrize("M,N,Kd", [(64, 1024, 3072), (64, 2048, 1024), (1, 3072, 1024), (48, 1000, 1000),
+                                    (9, 200, 4104), (64, 151936 // 8, 1024), (3, 20000, 136)])
+def test_gemm_decode_shapes_deterministic(M, N, Kd):
+    # the small-M path splits K across 16 wavefronts and sums the slices in a fixed order
+    x = randn(M, Kd, dtype=torch.bfloat16, seed=190)
+    w = randn(N, Kd, dtype=torch.bfloat16, seed=191, scale=0.05)
+    y0 = K.triton_matmul(x, w)
+    close(y0, O.linear(x, w), **BF16_TOL)
+    for _ in range(2):
+        assert torch.equal(K.triton_matmul(x, w), y0)
+
+
 @pytest.mark.parametrize("M,N,Kd", [(333, 256, 192), (64, 1024, 3072), (1024, 512, 1024), (40, 96, 64)])
 def test_gemm_backward_bf16(M, N, Kd):
     x = randn(2, M, Kd, dtype=torch.bfloat16, seed=93).requires_grad_(True)
