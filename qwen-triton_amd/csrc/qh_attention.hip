@@ -24,9 +24,10 @@
 // tiles. Both recompute P from the saved LSE. Results are bitwise
 // reproducible.
 //
-// Decode (Sq == 1): split-KV over the cache with one 16-lane group per key
-// row (fp32 VALU; the pass is HBM-bound on K/V), partial (m, l, o) per split
-// in the workspace, then a fixed-order combine.
+// Decode (Sq == 1): split-KV over the cache, one wavefront per (split, b,
+// kv-head) streaming K/V tiles through LDS on the matrix cores (the pass is
+// HBM-bound on K/V), partial (m, l, o) per split in the workspace, then a
+// fixed-order combine.
 #include "qh_mfma.h"
 
 namespace {
@@ -154,11 +155,19 @@ __device__ __forceinline__ typename Mfma<T>::v8 read_vt_frag(const T* Vt, int ke
 #pragma clang diagnostic ignored "-Winline-asm"
 // 64-bit per-lane address.
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
+  lds_base = (uint32_t)__builtin_amdgcn_readfirstlane(lds_base);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base)
                : "memory", "m0");
 }
-// Wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte offset.
-__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
+// Wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte offset. The base is
+// uniform by construction; readfirstlane states it for the compiler.
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* base, uint32_t lds_base) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  // readfirstlane returns int: widen through uint32_t (no sign extension)
+  const uint64_t ub = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b) |
+                      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32);
+  const void* sbase = (const void*)(uintptr_t)ub;
+  lds_base = (uint32_t)__builtin_amdgcn_readfirstlane(lds_base);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
                "s"(lds_base)
                : "memory", "m0");
@@ -613,114 +622,186 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
 // ===========================================================================
 // Decode: Sq == 1, split-KV.
 // ===========================================================================
-template <typename T, int DP, int G>
-__global__ __launch_bounds__(256) void fa_decode_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
-                                                        const T* __restrict__ K, int64_t skb, int64_t skh, int64_t sks,
-                                                        const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs,
-                                                        float* __restrict__ ws_o, float* __restrict__ ws_ml,
-                                                        const int* __restrict__ seqlens, int Hkv, int Sk, int D,
-                                                        int kps, float scale_log2) {
-  constexpr int LPK = DP / 8;          // lanes per key row
-  constexpr int GPW = 64 / LPK;        // key groups per wavefront
-  constexpr int NG = 4 * GPW;          // key groups per workgroup
-  constexpr int UNR = 4;               // keys in flight per group
-  __shared__ float red_m[NG][G], red_l[NG][G];
-  __shared__ float red_o[NG][G][DP];
+// s_waitcnt immediates (gfx9 encoding: vmcnt in [3:0] and [15:14], expcnt in
+// [6:4], lgkmcnt in [11:8]) that wait on one counter only.
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int kWaitLgkm0 = 0xF | (0x3 << 14) | (0x7 << 4);
+
+// Split-KV decode on the matrix cores. One wavefront per (split, b, kv-head)
+// streams the split's keys in tiles of 32 through NS LDS stages filled by
+// direct-to-LDS loads (NS - 1 tiles are in flight while one is used; only this
+// wave touches its LDS, so s_waitcnt replaces barriers).
+// Per tile:
+//   S^T = K Q^T  on MFMA 16x16x32 (keys x queries; the G query heads of the
+//                kv-head are the columns, the rest of the 16 are zero),
+//   online softmax on the C layout (a lane holds 8 keys of one query; the
+//                running max is shared by the 4 lanes of a query),
+//   O^T += V^T P^T with V^T read by ds_read_b64_tr_b16 and P^T taken from the
+//                C layout with the key index permuted to match.
+// K/V rows use the same XOR-swizzled layout as the forward kernel.
+template <typename T, int DP, int G, int NS>
+__global__ __launch_bounds__(64) void fa_decode_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
+                                                       const T* __restrict__ K, int64_t skb, int64_t skh, int64_t sks,
+                                                       const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs,
+                                                       float* __restrict__ ws_o, float* __restrict__ ws_ml,
+                                                       const int* __restrict__ seqlens, int Hkv, int Sk, int D,
+                                                       int kps, float scale_log2) {
+  static_assert(G >= 1 && G <= 16, "query heads per kv-head");
+  static_assert(NS >= 2 && NS <= 5, "LDS stages");
+  constexpr int BN = 32;            // keys per tile
+  constexpr int CPR = DP / 8;       // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;     // rows per 1 KiB load instruction
+  constexpr int NI = BN / RPI;      // load instructions per tile and tensor
+  constexpr int KD = DP / 32;       // 32-wide d steps of S
+  constexpr int DT = DP / 16;       // 16-row d tiles of O^T
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ __attribute__((aligned(1024))) T Ks[NS][BN * DP];
+  __shared__ __attribute__((aligned(1024))) T Vs[NS][BN * DP];
 
   const int split = blockIdx.x, nsplit = gridDim.x;
   const int bk = blockIdx.y;
   const int b = bk / Hkv, hk = bk % Hkv;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int grp = wid * GPW + lane / LPK, li = lane % LPK;
-  const int d0 = li * 8;
-  const bool dok = d0 < D;
+  const int lane = threadIdx.x;
+  const int li = lane & 15, lg = lane >> 4;
 
-  float q[G][8];
+  // Q^T fragments (B operand): column = query li, k = d = 32 kd + 8 lg + e.
+  v8 qf[KD];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const T* qp = Q + b * sqb + (int64_t)(hk * G + g) * sqh + d0;
-    if (dok) {
-      Vec16<T> v = ld16(qp);
+  for (int kd = 0; kd < KD; ++kd) {
+    const int d = kd * 32 + lg * 8;
+    if (li < G && d < D) qf[kd] = *reinterpret_cast<const v8*>(Q + b * sqb + (int64_t)(hk * G + li) * sqh + d);
+    else
 #pragma unroll
-      for (int e = 0; e < 8; ++e) q[g][e] = to_f32(v.v[e]) * scale_log2;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) q[g][e] = 0.f;
-    }
+      for (int e = 0; e < 8; ++e) qf[kd][e] = (T)0.f;
   }
-  float m[G], l[G], o[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
-  }
-  const T* Kb = K + b * skb + hk * skh + d0;
-  const T* Vb = V + b * svb + hk * svh + d0;
+
+  const T* Kb = K + b * skb + hk * skh;
+  const T* Vb = V + b * svb + hk * svh;
   const int sk_b = seqlens ? min(seqlens[b], Sk) : Sk;
   const int ks = split * kps;
   const int ke = min(sk_b, ks + kps);
-  for (int j0 = ks + grp * UNR; j0 < ke; j0 += NG * UNR) {
-    Vec16<T> kv[UNR], vv[UNR];
+  const int ntiles = ke > ks ? (ke - ks + BN - 1) / BN : 0;
+
+  // DMA lane geometry: row rl of each RPI-row group, physical chunk p. The
+  // swizzle depends on (n * RPI + rl) % 8, i.e. on the parity of n when RPI = 4.
+  const int rl = lane / CPR, p = lane % CPR;
+  int dsw[2];
+  uint32_t koff[2], voff[2];
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int j = j0 + u;
-      if (j < ke && dok) {
-        kv[u] = ld16(Kb + (int64_t)j * sks);
-        vv[u] = ld16(Vb + (int64_t)j * svs);
-      } else {
-        kv[u].raw = vv[u].raw = make_uint4(0, 0, 0, 0);
+  for (int par = 0; par < 2; ++par) {
+    const int c = swz(par * RPI + rl, p, CPR);
+    dsw[par] = c * 8 < D ? c * 8 : D - 8;
+    koff[par] = (uint32_t)(((int64_t)rl * sks + dsw[par]) * (int64_t)sizeof(T));
+    voff[par] = (uint32_t)(((int64_t)rl * svs + dsw[par]) * (int64_t)sizeof(T));
+  }
+  auto issue = [&](int t) {
+    const int row0 = ks + t * BN;
+    const int st = t % NS;
+    const uint32_t kl = lds_addr(Ks[st]), vl = lds_addr(Vs[st]);
+    if (row0 + BN <= ke) {
+#pragma unroll
+      for (int n = 0; n < NI; ++n) {
+        lds_dma16_s(koff[n & 1], Kb + (int64_t)(row0 + n * RPI) * sks, kl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16_s(voff[n & 1], Vb + (int64_t)(row0 + n * RPI) * svs, vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+      }
+    } else {
+#pragma unroll
+      for (int n = 0; n < NI; ++n) {
+        int gr = row0 + n * RPI + rl;
+        gr = gr < ke ? gr : ke - 1;
+        lds_dma16(Kb + (int64_t)gr * sks + dsw[n & 1], kl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16(Vb + (int64_t)gr * svs + dsw[n & 1], vl + (uint32_t)(n * RPI * DP * sizeof(T)));
       }
     }
+  };
+
+  float m = -INFINITY, l = 0.f;  // running max (log2 units) / this lane's partial sum, query li
+  f32x4 o[DT];
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      if (j0 + u >= ke) break;
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float s = 0.f;
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < ntiles) issue(t);
+  for (int t = 0; t < ntiles; ++t) {
+    // refill the stage of tile t - 1 (its LDS reads completed last iteration),
+    // so NS - 1 tiles stay in flight while tile t is waited for
+    if (t + NS - 1 < ntiles) issue(t + NS - 1);
+    // tile t has landed once only the tiles issued after it (at most NS - 1)
+    // have loads outstanding, 2 NI instructions each
+    const int after = min(ntiles - 1 - t, NS - 1);
+    if (after <= 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    else if (after == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NI));
+    else if (after == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * NI));
+    else if (after == 3) __builtin_amdgcn_s_waitcnt(waitcnt_vm(6 * NI));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 * NI));
+    const T* Kt = Ks[t % NS];
+    const T* Vt = Vs[t % NS];
+    f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += q[g][e] * to_f32(kv[u].v[e]);
-        s = wave_sum(s, LPK);
-        const float mn = fmaxf(m[g], s);
-        const float a = exp2_(m[g] - mn);
-        const float p = exp2_(s - mn);
-        l[g] = l[g] * a + p;
+    for (int kd = 0; kd < KD; ++kd) {
+      const int ch = kd * 4 + lg;
+      const v8 a0 = *reinterpret_cast<const v8*>(Kt + li * DP + swz(li, ch, CPR) * 8);
+      const v8 a1 = *reinterpret_cast<const v8*>(Kt + (16 + li) * DP + swz(16 + li, ch, CPR) * 8);
+      s0 = mma16<T>(a0, qf[kd], s0);
+      s1 = mma16<T>(a1, qf[kd], s1);
+    }
+    // scores of keys 4 lg + r (s0) and 16 + 4 lg + r (s1), in log2 units
+    const int kbase = ks + t * BN + 4 * lg;
+    float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] = o[g][e] * a + p * to_f32(vv[u].v[e]);
-        m[g] = mn;
+    for (int r = 0; r < 4; ++r) {
+      x[r] = kbase + r < ke ? s0[r] * scale_log2 : -INFINITY;
+      x[4 + r] = kbase + 16 + r < ke ? s1[r] * scale_log2 : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (mx > m) {
+      const float a = exp2_(m - mx);  // 0 while m is still -inf
+      l *= a;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= a;
+      m = mx;
+    }
+    const float mr = m == -INFINITY ? 0.f : m;
+    v8 pf;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pe = exp2_(x[e] - mr);
+      l += pe;
+      pf[e] = (T)pe;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      // A = V^T: row d = 16 dt + li; keys 4 lg + e and 16 + 4 lg + e (e < 4)
+      const int key = 4 * lg + (li >> 2);
+      const int d = dt * 16 + 4 * (li & 3);
+      const T* s0p = Vt + key * DP + swz(key, d >> 3, CPR) * 8 + (d & 7);
+      const T* s1p = Vt + (key + 16) * DP + swz(key + 16, d >> 3, CPR) * 8 + (d & 7);
+      const qh_v4i16 w0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) qh_v4i16*)(s0p));
+      const qh_v4i16 w1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) qh_v4i16*)(s1p));
+      const v8 av = __builtin_bit_cast(v8, qh_v8i16(__builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7)));
+      o[dt] = mma16<T>(av, pf, o[dt]);
+    }
+    // the LDS reads of this stage are complete before the stage is refilled
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  }
+  // l: sum the 4 lanes of each query; o: lane holds d = 16 dt + 4 lg + r of query li
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (li < G) {
+    const int64_t slot = ((int64_t)bk * G + li) * nsplit + split;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = dt * 16 + 4 * lg + r;
+        if (d < D) ws_o[slot * DP + d] = o[dt][r];
       }
-    }
-  }
-  // Combine the NG key groups of this workgroup in a fixed order.
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (li == 0) {
-      red_m[grp][g] = m[g];
-      red_l[grp][g] = l[g];
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (dok) red_o[grp][g][d0 + e] = o[g][e];
-  }
-  __syncthreads();
-  const int64_t row0 = (int64_t)bk * G;
-  for (int idx = threadIdx.x; idx < G * DP; idx += 256) {
-    const int g = idx / DP, d = idx % DP;
-    float M = -INFINITY;
-    for (int i = 0; i < NG; ++i) M = fmaxf(M, red_m[i][g]);
-    const float Mr = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f, acc = 0.f;
-    for (int i = 0; i < NG; ++i) {
-      const float w = exp2_(red_m[i][g] - Mr);
-      L += red_l[i][g] * w;
-      if (d < D) acc += red_o[i][g][d] * w;
-    }
-    const int64_t slot = (row0 + g) * nsplit + split;
-    if (d < D) ws_o[slot * DP + d] = acc;
-    if (d == 0) {
-      ws_ml[slot * 2] = M;
-      ws_ml[slot * 2 + 1] = L;
+    if (lg == 0) {
+      ws_ml[slot * 2] = m;
+      ws_ml[slot * 2 + 1] = l;
     }
   }
 }
@@ -753,10 +834,15 @@ static int pick_dp(int64_t D) {
   return 0;
 }
 
+// Splits per (b, kv-head): about 2048 single-wave workgroups in total (a few
+// per SIMD, so one wave's tile math overlaps the others' loads), each with at
+// least 8 tiles of 32 keys. Two LDS stages: more stages cost occupancy and
+// measured slower.
 static int decode_splits(int64_t B, int64_t Hkv, int64_t Sk) {
-  int64_t s = (Sk + 63) / 64;
-  const int64_t want = (2048 + B * Hkv - 1) / (B * Hkv);
-  if (s > want) s = want;
+  const int64_t tiles = (Sk + 31) / 32;
+  int64_t s = (2048 + B * Hkv - 1) / (B * Hkv);
+  const int64_t cap = (tiles + 7) / 8;
+  if (s > cap) s = cap;
   if (s < 1) s = 1;
   return (int)s;
 }
@@ -767,7 +853,7 @@ void launch_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int64
                    const int* seqlens, int B, int Hkv, int Sk, int D, int nsplit, float scale_log2, hipStream_t st) {
   const int kps = (Sk + nsplit - 1) / nsplit;
   dim3 grid(nsplit, B * Hkv);
-  fa_decode_kernel<T, DP, G><<<grid, 256, 0, st>>>((const T*)q, sqb, sqh, (const T*)k, skb, skh, sks, (const T*)v, svb,
+  fa_decode_kernel<T, DP, G, 2><<<grid, 64, 0, st>>>((const T*)q, sqb, sqh, (const T*)k, skb, skh, sks, (const T*)v, svb,
                                                    svh, svs, ws_o, ws_ml, seqlens, Hkv, Sk, D, kps,
                                                    scale_log2);
 }
@@ -893,6 +979,7 @@ extern "C" int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const vo
   QH_CHECK_ARG(groups == 1 || groups == 2 || groups == 4 || groups == 8, "qh_flash_decode: group size %d unsupported",
                groups);
   QH_CHECK_ARG(B * Hkv < 65536, "qh_flash_decode: too many sequences");
+  QH_CHECK_ARG(sks < (1 << 24) && svs < (1 << 24), "qh_flash_decode: key/value row stride too large");
   if (B == 0) return QH_OK;
   const int64_t need = qh_flash_decode_workspace(B, Hq, Hkv, Sk, D);
   if (ws_bytes < need) {

@@ -208,19 +208,6 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
 // 16x16x32 layout for lane l: A row l%16 / B col l%16 with k = 8*(l/16)+e;
 // C col l%16, rows 4*(l/16)+r.
 // ---------------------------------------------------------------------------
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-template <typename T>
-__device__ __forceinline__ f32x4 mma16(typename Mfma<T>::v8 a, typename Mfma<T>::v8 b, f32x4 c);
-template <>
-__device__ __forceinline__ f32x4 mma16<bf16_t>(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-template <>
-__device__ __forceinline__ f32x4 mma16<f16_t>(f16x8 a, f16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
 // Decode GEMM for M <= 64: one 1024-thread workgroup (16 wavefronts) per
 // 16*CG output columns. The 16 waves form CG column groups x KSP K slices;
 // each wave streams its 16 weight columns over its K slice with every load of

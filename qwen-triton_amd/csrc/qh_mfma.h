@@ -36,6 +36,21 @@ struct Mfma<f16_t> {
   }
 };
 
+// 16x16x32 products: lane l holds A row l%16 / B column l%16 with
+// k = 8*(l/16)+e; C column l%16, rows 4*(l/16)+r.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ f32x4 mma16(typename Mfma<T>::v8 a, typename Mfma<T>::v8 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mma16<bf16_t>(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mma16<f16_t>(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
