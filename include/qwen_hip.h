@@ -160,6 +160,26 @@ int qh_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const voi
 int qh_colsum(const void* X, int64_t ldx, int64_t M, int64_t N, void* out, int dtype, int out_dtype,
               void* stream);
 
+/* ---- fused attention input preparation (inference) ---------------------- */
+/* One pass over the projected q/k/v rows of B*S tokens (token-major views
+ * [B*S, H*D] with row strides sq, sk, sv): per-head RMSNorm of q and k with
+ * weights qw, kw (dtype wdtype, +1 when one_plus), rotate-half RoPE of both
+ * with cos/sin [cos_batch, S, rot] (strides scb, scs, unit last; only the first
+ * rot/2 columns are read), q written to q_out [B,Hq,S,D] (contiguous), k and v
+ * written into the caches at positions[s] (same positions for every batch row;
+ * positions outside [0, cap) are skipped). Matches the unfused kernels exactly.
+ * D <= 128, D % 8 == 0, rot = 16 * 2^k <= D.
+ * Replaces, fused, the chain at qwen_triton/modules/attention.py:104-114
+ * (q_norm/k_norm via qwen_triton/kernels/rmsnorm.py:101-196, apply_rope via
+ * qwen_triton/kernels/rope.py:78-120, update_attention via
+ * qwen_triton/kernels/cache.py:72-98). */
+int qh_attn_prepare(const void* q, int64_t sq, const void* k, int64_t sk, const void* v, int64_t sv,
+                    const void* qw, const void* kw, float eps, int one_plus, const void* cos, const void* sin,
+                    int64_t scb, int64_t scs, int64_t cos_batch, int64_t rot, void* q_out, void* k_cache,
+                    int64_t kcb, int64_t kch, int64_t kcs, void* v_cache, int64_t vcb, int64_t vch, int64_t vcs,
+                    const int64_t* positions, int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
+                    int64_t cap, int dtype, int wdtype, int cdtype, void* stream);
+
 /* ---- flash attention ---------------------------------------------------- */
 /* O = softmax(scale * Q K^T + causal mask) V, LSE = logsumexp per query (fp32,
  * natural log, [B,Hq,Sq]). q [B,Hq,Sq,D], k/v [B,Hkv,Sk,D] with the given

@@ -99,6 +99,19 @@ __device__ __forceinline__ void st16(T* p, const Vec16<T>& v) {
 #define QH_DPP_HALF_MIRROR 0x141
 #define QH_DPP_MIRROR 0x140
 
+// Scalar access to a buffer whose dtype (QH_F32/F16/BF16) is only known at run time.
+__device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
+  if (dtype == QH_F32) return ((const float*)p)[i];
+  if (dtype == QH_F16) return (float)((const f16_t*)p)[i];
+  return (float)((const bf16_t*)p)[i];
+}
+
+__device__ __forceinline__ void store_any(void* p, int dtype, int64_t i, float v) {
+  if (dtype == QH_F32) ((float*)p)[i] = v;
+  else if (dtype == QH_F16) ((f16_t*)p)[i] = (f16_t)v;
+  else ((bf16_t*)p)[i] = (bf16_t)v;
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));

@@ -1,0 +1,128 @@
+// Fused passes for the inference path of the attention block and the decoder
+// layer. Each replaces a chain of the single-op kernels with one launch and
+// one pass over the data, with the same per-element arithmetic and rounding
+// points as that chain (so results match it exactly).
+#include "qh_common.h"
+
+namespace {
+
+// Attention input preparation, one 16-lane group per (token, head) row of D
+// (<= 128) elements, 8 per lane:
+//   q, k rows: RMSNorm over D (rounded to T, as the norm kernel), then
+//              rotate-half RoPE with cos/sin[.., :rot/2] (rounded to T);
+//              q goes to q_out [B, Hq, S, D], k into its cache at pos[s];
+//   v rows:    copied into the value cache at pos[s].
+// The lane layout and the DPP reduction are those of the 16-lane RMSNorm
+// kernel and the RoPE expressions are those of the RoPE kernel.
+template <typename T, typename C>
+__global__ __launch_bounds__(256) void attn_prepare_kernel(
+    const T* __restrict__ q, int64_t sq, const T* __restrict__ k, int64_t sk, const T* __restrict__ v, int64_t sv,
+    const void* __restrict__ qw, const void* __restrict__ kw, int wdtype, float eps, float wadd,
+    const C* __restrict__ cs, const C* __restrict__ sn, int64_t scb, int64_t scs, int64_t cos_batch, int half,
+    int rot, T* __restrict__ q_out, T* __restrict__ kc, int64_t kcb, int64_t kch, int64_t kcs, T* __restrict__ vc,
+    int64_t vcb, int64_t vch, int64_t vcs, const int64_t* __restrict__ pos, int S, int Hq, int Hkv, int D,
+    int64_t cap, int64_t rows) {
+  const int grp = threadIdx.x >> 4, g = threadIdx.x & 15;
+  const int HT = Hq + 2 * Hkv;
+  const int d0 = g * 8;
+  const bool act = d0 < D;
+  const int hl = half / 8;  // lane distance between the two rotated halves
+  for (int64_t row = blockIdx.x * 16ll + grp; row < rows; row += (int64_t)gridDim.x * 16) {
+    const int64_t t = row / HT;
+    const int j = (int)(row - t * HT);
+    const int64_t b = t / S;
+    const int s = (int)(t - b * S);
+    const int64_t p = pos[s];
+    Vec16<T> xv;
+    xv.raw = make_uint4(0, 0, 0, 0);
+    if (j >= Hq + Hkv) {  // value row: copy into the cache
+      const int h = j - Hq - Hkv;
+      if (act) xv = ld16(v + t * sv + h * D + d0);
+      if (act && p >= 0 && p < cap) st16(vc + b * vcb + h * vch + p * vcs + d0, xv);
+      continue;
+    }
+    const bool isq = j < Hq;
+    const int h = isq ? j : j - Hq;
+    if (act) xv = ld16(isq ? q + t * sq + h * D + d0 : k + t * sk + h * D + d0);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = to_f32(xv.v[e]);
+      ss += f * f;
+    }
+    ss = wave_sum(ss, 16);
+    const float inv = rsqrtf(ss / (float)D + eps);
+    const void* w = isq ? qw : kw;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      y[e] = act ? to_f32(from_f32<T>((to_f32(xv.v[e]) * inv) * (load_any(w, wdtype, d0 + e) + wadd))) : 0.f;
+    float px[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) px[e] = __shfl_xor(y[e], hl, 16);
+    Vec16<T> o;
+    if (d0 < rot) {
+      const bool lo = d0 < half;
+      const int ci = lo ? d0 : d0 - half;
+      const int64_t co = (cos_batch == 1 ? 0 : b) * scb + s * scs + ci;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float cc = to_f32(cs[co + e]), sv2 = to_f32(sn[co + e]);
+        const float a = lo ? y[e] : px[e], bb = lo ? px[e] : y[e];
+        o.v[e] = lo ? from_f32<T>(a * cc - bb * sv2) : from_f32<T>(bb * cc + a * sv2);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o.v[e] = from_f32<T>(y[e]);
+    }
+    if (!act) continue;
+    if (isq) st16(q_out + ((b * Hq + h) * (int64_t)S + s) * D + d0, o);
+    else if (p >= 0 && p < cap) st16(kc + b * kcb + h * kch + p * kcs + d0, o);
+  }
+}
+
+}  // namespace
+
+extern "C" int qh_attn_prepare(const void* q, int64_t sq, const void* k, int64_t sk, const void* v, int64_t sv,
+                               const void* qw, const void* kw, float eps, int one_plus, const void* cos,
+                               const void* sin, int64_t scb, int64_t scs, int64_t cos_batch, int64_t rot,
+                               void* q_out, void* k_cache, int64_t kcb, int64_t kch, int64_t kcs, void* v_cache,
+                               int64_t vcb, int64_t vch, int64_t vcs, const int64_t* positions, int64_t B,
+                               int64_t S, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int dtype, int wdtype,
+                               int cdtype, void* stream) {
+  QH_CHECK_ARG(B >= 0 && S >= 0 && Hq > 0 && Hkv > 0 && cap >= 0, "qh_attn_prepare: bad shape");
+  QH_CHECK_ARG(D > 0 && D <= 128 && D % 8 == 0, "qh_attn_prepare: head dim %lld must be a multiple of 8 and <= 128",
+               (long long)D);
+  const int64_t half = rot / 2;
+  QH_CHECK_ARG(rot >= 16 && rot <= D && rot % 16 == 0 && ((half / 8) & (half / 8 - 1)) == 0,
+               "qh_attn_prepare: rotary dim %lld must be 16 * 2^k <= D", (long long)rot);
+  QH_CHECK_ARG(cos_batch == 1 || cos_batch == B, "qh_attn_prepare: cos/sin batch must be 1 or B");
+  QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(q_out) && aligned16(k_cache) &&
+                   aligned16(v_cache),
+               "qh_attn_prepare: pointers must be 16-byte aligned");
+  QH_CHECK_ARG(sq % 8 == 0 && sk % 8 == 0 && sv % 8 == 0 && kcb % 8 == 0 && kch % 8 == 0 && kcs % 8 == 0 &&
+                   vcb % 8 == 0 && vch % 8 == 0 && vcs % 8 == 0,
+               "qh_attn_prepare: strides must be multiples of 8 elements");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_attn_prepare: bf16/f16 only");
+  QH_CHECK_ARG(wdtype == QH_F32 || wdtype == dtype, "qh_attn_prepare: norm weights must be fp32 or the input dtype");
+  QH_CHECK_ARG(cdtype == QH_F32 || cdtype == dtype, "qh_attn_prepare: cos/sin must be fp32 or the input dtype");
+  const int64_t rows = B * S * (Hq + 2 * Hkv);
+  if (rows == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const float wadd = one_plus ? 1.f : 0.f;
+  const int64_t nblk = (rows + 15) / 16;
+  const unsigned grid = (unsigned)(nblk < 65536 ? nblk : 65536);
+#define QH_PREP(T, C)                                                                                            \
+  attn_prepare_kernel<T, C><<<grid, 256, 0, st>>>(                                                              \
+      (const T*)q, sq, (const T*)k, sk, (const T*)v, sv, qw, kw, wdtype, eps, wadd, (const C*)cos, (const C*)sin, \
+      scb, scs, cos_batch, (int)half, (int)rot, (T*)q_out, (T*)k_cache, kcb, kch, kcs, (T*)v_cache, vcb, vch, vcs, \
+      positions, (int)S, (int)Hq, (int)Hkv, (int)D, cap, rows)
+  if (dtype == QH_BF16) {
+    if (cdtype == QH_F32) QH_PREP(bf16_t, float); else QH_PREP(bf16_t, bf16_t);
+  } else {
+    if (cdtype == QH_F32) QH_PREP(f16_t, float); else QH_PREP(f16_t, f16_t);
+  }
+#undef QH_PREP
+  QH_CHECK_LAUNCH("qh_attn_prepare");
+  return QH_OK;
+}

@@ -32,17 +32,6 @@ static int pick_row_shape(int64_t cols, int VN, int& G, int& NV) {
 }
 
 
-__device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
-  if (dtype == QH_F32) return ((const float*)p)[i];
-  if (dtype == QH_F16) return (float)((const f16_t*)p)[i];
-  return (float)((const bf16_t*)p)[i];
-}
-
-__device__ __forceinline__ void store_any(void* p, int dtype, int64_t i, float v) {
-  if (dtype == QH_F32) ((float*)p)[i] = v;
-  else if (dtype == QH_F16) ((f16_t*)p)[i] = (f16_t)v;
-  else ((bf16_t*)p)[i] = (bf16_t)v;
-}
 
 // ===========================================================================
 // RMSNorm

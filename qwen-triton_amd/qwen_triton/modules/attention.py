@@ -10,6 +10,10 @@ flash kernel):
   the split-KV decode kernel;
 * explicit additive mask (padding): fp32 SDPA over repeated KV heads, as the
   reference does for masked multi-token attention.
+
+Inference (no autograd, GPU, position-indexed cache): q_norm/k_norm, RoPE and
+the cache writes run as one fused pass (``qh_attn_prepare``) with the same
+arithmetic as the separate kernels.
 """
 from __future__ import annotations
 
@@ -18,6 +22,7 @@ from typing import Optional
 import torch
 from torch import nn
 
+from qwen_triton import _native
 from qwen_triton.configs import QwenTritonConfig
 from qwen_triton.kernels import sigmoid_mul
 from qwen_triton.kernels import flash_attention as _fa
@@ -81,6 +86,48 @@ class QwenFullAttention(nn.Module):
             q.to(torch.float32), ke.to(torch.float32), ve.to(torch.float32), attn_mask=m, dropout_p=0.0,
             is_causal=False, scale=self.scaling).to(out_dtype)
 
+    def _fused_prepare_ok(self, hidden_states: torch.Tensor, cos: torch.Tensor, past_key_values,
+                          cache_position) -> bool:
+        d, rot = self.head_dim, cos.shape[-1]
+        half_lanes = rot // 16
+        return (not torch.is_grad_enabled() and hidden_states.is_cuda and hidden_states.dim() == 3
+                and hidden_states.dtype in (torch.bfloat16, torch.float16) and not self.config.attn_output_gate
+                and past_key_values is not None and cache_position is not None
+                and d % 8 == 0 and d <= 128 and rot % 16 == 0 and 16 <= rot <= d
+                and half_lanes & (half_lanes - 1) == 0
+                and cos.dim() == 3 and cos.shape[0] in (1, hidden_states.shape[0])
+                and cos.shape[1] == hidden_states.shape[1] and cos.dtype in (torch.float32, hidden_states.dtype)
+                and self.q_norm.weight.dtype in (torch.float32, hidden_states.dtype)
+                and self.k_norm.weight.dtype == self.q_norm.weight.dtype
+                and _native.available())
+
+    def _fused_prepare(self, q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor, cos: torch.Tensor,
+                       sin: torch.Tensor, past_key_values: QwenTritonCache, cache_position: torch.Tensor,
+                       max_position: int | None):
+        """q_norm/k_norm + RoPE + cache write in one launch; returns q [B,Hq,S,D] and the cache views."""
+        bsz, seq = q2.shape[0], q2.shape[1]
+        hq, hkv, d = self.num_heads, self.num_key_value_heads, self.head_dim
+        positions = cache_position.to(device=q2.device, dtype=torch.long).reshape(-1)
+        if positions.numel() != seq:
+            raise ValueError("cache_position length must match the sequence dimension of key/value states")
+        kc, vc, n = past_key_values.claim_positions(self.layer_idx, bsz, hkv, d, q2.dtype, q2.device, positions,
+                                                    max_position)
+        q2, k2, v2 = (t.reshape(bsz * seq, -1) for t in (q2, k2, v2))
+        if q2.stride(1) != 1 or k2.stride(1) != 1 or v2.stride(1) != 1:
+            q2, k2, v2 = q2.contiguous(), k2.contiguous(), v2.contiguous()
+        if cos.stride(-1) != 1 or sin.stride() != cos.stride():
+            cos, sin = cos.contiguous(), sin.contiguous()
+        q_out = torch.empty((bsz, hq, seq, d), dtype=q2.dtype, device=q2.device)
+        wq, wk = self.q_norm.weight, self.k_norm.weight
+        _native.call("qh_attn_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0), v2.data_ptr(),
+                     v2.stride(0), wq.data_ptr(), wk.data_ptr(), float(self.q_norm.eps),
+                     int(self.q_norm.one_plus_weight), cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.stride(1),
+                     cos.shape[0], cos.shape[-1], q_out.data_ptr(), kc.data_ptr(), *kc.stride()[:3], vc.data_ptr(),
+                     *vc.stride()[:3], positions.data_ptr(), bsz, seq, hq, hkv, d, kc.shape[2],
+                     _native.dtype_code(q2.dtype), _native.dtype_code(wq.dtype), _native.dtype_code(cos.dtype),
+                     _native.stream(q2.device))
+        return q_out, kc[:, :, :n, :], vc[:, :, :n, :]
+
     def forward(
         self,
         hidden_states: torch.Tensor,
@@ -91,6 +138,13 @@ class QwenFullAttention(nn.Module):
         max_position: int | None = None,
     ) -> torch.Tensor:
         input_shape = hidden_states.shape[:-1]
+        cos, sin = position_embeddings
+        if self._fused_prepare_ok(hidden_states, cos, past_key_values, cache_position):
+            q, k, v = self._fused_prepare(self.q_proj(hidden_states), self.k_proj(hidden_states),
+                                          self.v_proj(hidden_states), cos, sin, past_key_values, cache_position,
+                                          max_position)
+            out = self._attend(q, k, v, attention_mask, hidden_states.dtype)
+            return self.o_proj(out.transpose(1, 2).reshape(*input_shape, -1))
         mixed_q = self.q_proj(hidden_states)
         gate = None
         if self.config.attn_output_gate:
@@ -104,7 +158,6 @@ class QwenFullAttention(nn.Module):
         q = self.q_norm(q).transpose(1, 2)
         k = self.k_norm(k).transpose(1, 2)
         v = v.transpose(1, 2)
-        cos, sin = position_embeddings
         q, k = apply_rotary_pos_emb(q, k, cos, sin)
 
         if past_key_values is not None:

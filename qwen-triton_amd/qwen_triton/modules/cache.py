@@ -107,6 +107,28 @@ class QwenTritonCache:
         n = self.attention_lengths[layer_idx]
         return self.key_cache[layer_idx][:, :, :n, :], self.value_cache[layer_idx][:, :, :n, :]
 
+    def claim_positions(self, layer_idx: int, batch: int, heads: int, head_dim: int, dtype: torch.dtype,
+                        device: torch.device, positions: torch.Tensor,
+                        max_position: int | None = None) -> tuple[torch.Tensor, torch.Tensor, int]:
+        """Make room for writes at ``positions`` (as ``update_attention`` would) without writing.
+
+        Returns the key/value storages and the new valid length; a fused kernel then
+        writes the rows itself.
+        """
+        current = self.attention_lengths[layer_idx]
+        if positions.numel() == 0:
+            required = current
+        elif max_position is not None:
+            required = int(max_position) + 1
+        else:
+            required = int(positions.max().item()) + 1
+        like = torch.empty((batch, heads, 0, head_dim), dtype=dtype, device=device)
+        self.key_cache[layer_idx] = self._ensure_attention_storage(self.key_cache[layer_idx], like, current, required)
+        self.value_cache[layer_idx] = self._ensure_attention_storage(self.value_cache[layer_idx], like, current,
+                                                                     required)
+        self.attention_lengths[layer_idx] = max(current, required)
+        return self.key_cache[layer_idx], self.value_cache[layer_idx], self.attention_lengths[layer_idx]
+
     def get_seq_length(self, layer_idx: int | None = None) -> int:
         if layer_idx is not None and self.key_cache[layer_idx] is not None:
             return self.attention_lengths[layer_idx]

@@ -168,3 +168,41 @@ def test_decode_step_graph_replays_match_eager():
             assert torch.equal(out, eager)
             step()  # eager work between replays
             torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("seq,per_batch_pos", [(1, False), (5, False), (5, True)])
+def test_fused_attention_prepare_matches_unfused_path(seq, per_batch_pos):
+    # inference takes one fused q/k-norm + RoPE + cache-write launch; it must equal the
+    # separate kernels (autograd path) bit for bit, in the output and in both caches
+    from qwen_triton.modules.cache import QwenTritonCache
+
+    cfg = _cfg()
+    m = _model(cfg, seed=6)
+    attn = m.model.layers[1].self_attn
+    B, ctx = 3, 9
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn(B, seq, cfg.hidden_size, device="cuda", dtype=torch.bfloat16, generator=gen)
+    pos = torch.arange(ctx, ctx + seq, device="cuda")
+    pid = (pos[None] + torch.arange(B, device="cuda")[:, None]) if per_batch_pos else pos[None]
+    cos, sin = m.model.rotary_emb(x, pid)
+    caches = []
+    for _ in range(2):
+        c = QwenTritonCache(cfg.num_hidden_layers, cfg.layer_types)
+        c.reserve(1, B, cfg.num_key_value_heads, 32, cfg.head_dim, torch.bfloat16, "cuda")
+        g2 = torch.Generator(device="cuda").manual_seed(8)
+        c.key_cache[1][:, :, :ctx].normal_(generator=g2)
+        c.value_cache[1][:, :, :ctx].normal_(generator=g2)
+        c.attention_lengths[1] = ctx
+        caches.append(c)
+    c0 = _native.CALLS["qh_attn_prepare"]
+    with torch.enable_grad():
+        ref = attn(x, (cos, sin), None, caches[0], pos, max_position=ctx + seq - 1).detach()
+    assert _native.CALLS["qh_attn_prepare"] == c0
+    with torch.no_grad():
+        out = attn(x, (cos, sin), None, caches[1], pos, max_position=ctx + seq - 1)
+    assert _native.CALLS["qh_attn_prepare"] == c0 + 1
+    assert caches[0].attention_lengths[1] == caches[1].attention_lengths[1] == ctx + seq
+    n = ctx + seq  # rows past the valid length are uninitialised storage
+    assert torch.equal(caches[0].key_cache[1][:, :, :n], caches[1].key_cache[1][:, :, :n])
+    assert torch.equal(caches[0].value_cache[1][:, :, :n], caches[1].value_cache[1][:, :, :n])
+    assert torch.equal(ref, out)
