@@ -155,6 +155,20 @@ int qh_index_add(void* target, int64_t stride_t, const void* src, int64_t stride
 int qh_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
             const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
             void* stream);
+/* Several decode-sized products sharing the activations, in one launch:
+ * C_i[M, N_i] = A(M,K) . B_i(N_i,K)^T (+ bias_i) for i < count (<= 4), M <= 64,
+ * all operands k-contiguous, C in the input dtype (bf16/f16). B, ldb, N, C,
+ * ldc and bias are host arrays of count entries (bias may be NULL, or hold NULL
+ * entries). Each product is computed exactly as qh_gemm would. gated = 1 (two
+ * products of equal N, e.g. gate and up) writes C_0 = silu(C_gate) * C_up with
+ * each product rounded to the dtype first, as qh_gemm twice followed by
+ * qh_silu_mul_fwd would (C_1 is not written).
+ * Replaces, fused, the separate TritonLinear calls of
+ * qwen_triton/modules/attention.py:95-103 (q/k/v) and qwen_triton/modules/mlp.py:19-22
+ * (gate/up, silu_mul), each via qwen_triton/kernels/matmul.py:130-155. */
+int qh_gemm_multi(int64_t M, int64_t K, const void* A, int64_t lda, int count, const void* const* B,
+                  const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
+                  const void* const* bias, int gated, int dtype, void* stream);
 /* out[n] = sum_m X[m*ldx + n] in a fixed order (bias gradient).
  * Replaces qwen_triton/kernels/matmul.py:114-127 (_row_sum_kernel). */
 int qh_colsum(const void* X, int64_t ldx, int64_t M, int64_t N, void* out, int dtype, int out_dtype,

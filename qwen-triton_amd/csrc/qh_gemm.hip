@@ -216,38 +216,68 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
 // trips. The KSP partial tiles are summed through LDS in slice order
 // (deterministic, no workspace, no cross-workgroup traffic).
 //
+// One launch can serve several products that share the activations A (the
+// q/k/v or gate/up projections of a layer): workgroups are assigned to the
+// products' column tiles in order, each computing exactly what a launch of
+// its own product would. GATED (two products of equal N): every wave
+// multiplies the same A fragments by both weight matrices and the epilogue
+// writes silu(gate) * up, each product rounded to OT first, as separate GEMMs
+// followed by the SiLU-mul kernel would.
+//
 // k mapping per 32-wide step: lane group q = lane / 16 takes k0 + 8 q .. +7,
 // so the four groups of a row read 64 contiguous bytes.
-template <typename T, typename OT, int MT, int KSP>
+constexpr int kMaxProducts = 4;
+template <typename T, typename OT>
+struct DecodeProducts {
+  const T* B[kMaxProducts];
+  OT* C[kMaxProducts];
+  const T* bias[kMaxProducts];
+  int64_t ldb[kMaxProducts], ldc[kMaxProducts];
+  int N[kMaxProducts];
+  int tile0[kMaxProducts + 1];  // first workgroup of each product
+  int count;
+};
+
+template <typename T, typename OT, int MT, int KSP, bool GATED>
 __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__ A, int64_t lda,
-                                                           const T* __restrict__ B, int64_t ldb, OT* __restrict__ C,
-                                                           int64_t ldc, const T* __restrict__ bias, int M, int N,
-                                                           int K, int kr) {
+                                                           const DecodeProducts<T, OT> P, int M, int K, int kr) {
   constexpr int CG = 16 / KSP;
-  constexpr int CH = MT <= 2 ? 8 : 4;  // k-steps whose loads are issued together
+  constexpr int NB = GATED ? 2 : 1;                       // weight matrices per wave
+  constexpr int CH = (MT <= 2 ? 8 : 4) / NB;              // k-steps whose loads are issued together
   typedef typename Mfma<T>::v8 v8;
   __shared__ float red[16][MT * 16][16];
+  int pi = 0;
+  while (pi + 1 < P.count && (int)blockIdx.x >= P.tile0[pi + 1]) ++pi;
+  const int tile = (int)blockIdx.x - P.tile0[pi];
+  const int N = P.N[pi];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int cg = wid / KSP, ks = wid % KSP;
   const int li = lane & 15, q = lane >> 4;
-  const int n = (blockIdx.x * CG + cg) * 16 + li;
+  const int n = (tile * CG + cg) * 16 + li;
   const bool nok = n < N;
-  const T* brow = B + (int64_t)(nok ? n : 0) * ldb;
-  const int kb = ks * kr, ke = min(K, kb + kr);
-  f32x4 acc[MT];
+  const T* brow[NB];
 #pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < NB; ++j) brow[j] = P.B[pi + j] + (int64_t)(nok ? n : 0) * P.ldb[pi + j];
+  const int kb = ks * kr, ke = min(K, kb + kr);
+  f32x4 acc[NB][MT];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   v8 zero;
 #pragma unroll
   for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
   for (int k0 = kb; k0 < ke; k0 += 32 * CH) {
-    v8 b[CH], a[CH][MT];
+    v8 b[CH][NB], a[CH][MT];
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int k = k0 + u * 32 + q * 8;
       const bool kok = k < ke;
-      if (nok && kok) b[u] = *reinterpret_cast<const v8*>(brow + k);
-      else b[u] = zero;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        if (nok && kok) b[u][j] = *reinterpret_cast<const v8*>(brow[j] + k);
+        else b[u][j] = zero;
+      }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int m = i * 16 + li;
@@ -258,42 +288,84 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
 #pragma unroll
     for (int u = 0; u < CH; ++u)
 #pragma unroll
-      for (int i = 0; i < MT; ++i) acc[i] = mma16<T>(a[u][i], b[u], acc[i]);
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[j][i] = mma16<T>(a[u][i], b[u][j], acc[j][i]);
   }
-  // C layout: column li, rows 16 i + 4 q + r.
+  // Sum the K slices in order, one weight matrix at a time through the same
+  // LDS buffer. C layout: column li, rows 16 i + 4 q + r.
+  float first[(CG * MT * 256 + 1023) / 1024];
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
+  for (int j = 0; j < NB; ++j) {
+    if (j > 0) __syncthreads();  // the previous matrix's sums have been read
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wid][i * 16 + q * 4 + r][li] = acc[i][r];
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < CG * MT * 256; idx += 1024) {
-    const int g = idx / (MT * 256), rem = idx % (MT * 256);
-    const int row = rem / 16, col = rem % 16;
-    float v = 0.f;
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int s2 = 0; s2 < KSP; ++s2) v += red[g * KSP + s2][row][col];
-    const int gn = (blockIdx.x * CG + g) * 16 + col;
-    if (row < M && gn < N) C[(int64_t)row * ldc + gn] = from_f32<OT>(v + (bias ? to_f32(bias[gn]) : 0.f));
+      for (int r = 0; r < 4; ++r) red[wid][i * 16 + q * 4 + r][li] = acc[j][i][r];
+    __syncthreads();
+    int slot = 0;
+    for (int idx = threadIdx.x; idx < CG * MT * 256; idx += 1024, ++slot) {
+      const int g = idx / (MT * 256), rem = idx % (MT * 256);
+      const int row = rem / 16, col = rem % 16;
+      float v = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < KSP; ++s2) v += red[g * KSP + s2][row][col];
+      const int gn = (tile * CG + g) * 16 + col;
+      if (row >= M || gn >= N) continue;
+      const T* bias = P.bias[pi + j];
+      const float val = v + (bias ? to_f32(bias[gn]) : 0.f);
+      if constexpr (GATED) {
+        if (j == 0) {
+          first[slot] = to_f32(from_f32<OT>(val));
+        } else {
+          const float gt = first[slot], up = to_f32(from_f32<OT>(val));
+          P.C[pi][(int64_t)row * P.ldc[pi] + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
+        }
+      } else {
+        P.C[pi][(int64_t)row * P.ldc[pi] + gn] = from_f32<OT>(val);
+      }
+    }
   }
+}
+
+template <typename T, typename OT>
+void launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int M, int K, bool gated,
+                            hipStream_t st) {
+  // Narrow outputs: all 16 waves split K (16 columns per workgroup). Wide
+  // outputs already give enough workgroups: 4 column groups x 4 K slices.
+  int maxN = 0;
+  for (int i = 0; i < P.count; ++i) maxN = P.N[i] > maxN ? P.N[i] : maxN;
+  const bool wide = !gated && maxN > 8192;
+  const int ksp = wide ? 4 : 16;
+  const int cols = 16 * (16 / ksp);
+  const int nprod = gated ? 1 : P.count;  // the gated pair shares its column tiles
+  P.tile0[0] = 0;
+  for (int i = 0; i < nprod; ++i) P.tile0[i + 1] = P.tile0[i] + (P.N[i] + cols - 1) / cols;
+  if (gated) P.count = 1;
+  const int grid = P.tile0[nprod];
+  const int kr = ((K + ksp - 1) / ksp + 31) / 32 * 32;
+  const int mt = (M + 15) / 16;
+#define QH_DG(MTV, KSPV, GV) \
+  gemm_decode_kernel<T, OT, MTV, KSPV, GV><<<grid, 1024, 0, st>>>(a, lda, P, M, K, kr)
+#define QH_DG_W(MTV) \
+  if (gated) QH_DG(MTV, 16, true); else if (wide) QH_DG(MTV, 4, false); else QH_DG(MTV, 16, false);
+  if (mt == 1) { QH_DG_W(1) } else if (mt == 2) { QH_DG_W(2) } else if (mt == 3) { QH_DG_W(3) } else { QH_DG_W(4) }
+#undef QH_DG_W
+#undef QH_DG
 }
 
 template <typename T, typename OT>
 void launch_decode_gemm(const T* a, int64_t lda, const T* b, int64_t ldb, OT* c, int64_t ldc, const T* bi, int M,
                         int N, int K, hipStream_t st) {
-  // Narrow outputs: all 16 waves split K (16 columns per workgroup). Wide
-  // outputs already give enough workgroups: 4 column groups x 4 K slices.
-  const bool wide = N > 8192;
-  const int ksp = wide ? 4 : 16;
-  const int cols = 16 * (16 / ksp);
-  const int grid = (N + cols - 1) / cols;
-  const int kr = ((K + ksp - 1) / ksp + 31) / 32 * 32;
-  const int mt = (M + 15) / 16;
-#define QH_DG(MTV, KSPV) \
-  gemm_decode_kernel<T, OT, MTV, KSPV><<<grid, 1024, 0, st>>>(a, lda, b, ldb, c, ldc, bi, M, N, K, kr)
-#define QH_DG_W(MTV) if (wide) QH_DG(MTV, 4); else QH_DG(MTV, 16);
-  if (mt == 1) { QH_DG_W(1) } else if (mt == 2) { QH_DG_W(2) } else if (mt == 3) { QH_DG_W(3) } else { QH_DG_W(4) }
-#undef QH_DG_W
-#undef QH_DG
+  DecodeProducts<T, OT> P = {};
+  P.B[0] = b;
+  P.C[0] = c;
+  P.bias[0] = bi;
+  P.ldb[0] = ldb;
+  P.ldc[0] = ldc;
+  P.N[0] = N;
+  P.count = 1;
+  launch_decode_products<T, OT>(a, lda, P, M, K, false, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -449,6 +521,42 @@ extern "C" int qh_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
 #undef QH_GEMM_OUT
   if (rc) return rc;
   QH_CHECK_LAUNCH("qh_gemm");
+  return QH_OK;
+}
+
+extern "C" int qh_gemm_multi(int64_t M, int64_t K, const void* A, int64_t lda, int count, const void* const* B,
+                             const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
+                             const void* const* bias, int gated, int dtype, void* stream) {
+  QH_CHECK_ARG(count >= 1 && count <= kMaxProducts, "qh_gemm_multi: 1..%d products", kMaxProducts);
+  QH_CHECK_ARG(M >= 0 && M <= 64 && K > 0 && K < (1ll << 31), "qh_gemm_multi: needs 0 <= M <= 64 and K > 0");
+  QH_CHECK_ARG(!gated || (count == 2 && N[0] == N[1]), "qh_gemm_multi: gated needs two products of equal N");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_gemm_multi: bf16/f16 only");
+  QH_CHECK_ARG(aligned16(A) && lda % 8 == 0 && lda >= K && K % 8 == 0,
+               "qh_gemm_multi: A must be 16-byte aligned with K, lda multiples of 8");
+  for (int i = 0; i < count; ++i) {
+    QH_CHECK_ARG(N[i] > 0 && N[i] < (1ll << 31) && aligned16(B[i]) && ldb[i] % 8 == 0 && ldb[i] >= K,
+                 "qh_gemm_multi: product %d: bad B or N", i);
+    QH_CHECK_ARG((gated && i == 1) || (C[i] != nullptr && ldc[i] >= N[i]), "qh_gemm_multi: product %d: bad C", i);
+  }
+  if (M == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+#define QH_MULTI(T)                                                       \
+  {                                                                       \
+    DecodeProducts<T, T> P = {};                                          \
+    for (int i = 0; i < count; ++i) {                                     \
+      P.B[i] = (const T*)B[i];                                            \
+      P.C[i] = (T*)C[i];                                                  \
+      P.bias[i] = bias ? (const T*)bias[i] : nullptr;                     \
+      P.ldb[i] = ldb[i];                                                  \
+      P.ldc[i] = ldc[i];                                                  \
+      P.N[i] = (int)N[i];                                                 \
+    }                                                                     \
+    P.count = count;                                                      \
+    launch_decode_products<T, T>((const T*)A, lda, P, (int)M, (int)K, gated != 0, st); \
+  }
+  if (dtype == QH_BF16) QH_MULTI(bf16_t) else QH_MULTI(f16_t)
+#undef QH_MULTI
+  QH_CHECK_LAUNCH("qh_gemm_multi");
   return QH_OK;
 }
 

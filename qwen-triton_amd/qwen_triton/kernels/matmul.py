@@ -11,6 +11,8 @@ forward ``x W^T`` (NT), input grad ``dy W`` (B transposed view) and weight grad
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from .. import _native
@@ -46,6 +48,48 @@ def gemm(trans_a: bool, trans_b: bool, M: int, N: int, K: int, a: torch.Tensor, 
                  out.data_ptr(), ldc, None if bias is None else bias.data_ptr(), _native.dtype_code(a.dtype),
                  _native.dtype_code(out.dtype), _native.stream(a.device))
     return out
+
+
+def linear_group_ok(x: torch.Tensor, weights: list[torch.Tensor]) -> bool:
+    """True when ``linear_group`` can serve these operands (decode-sized, k-contiguous, aligned)."""
+    if not (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and _native.available()):
+        return False
+    k = x.shape[-1]
+    if k % 8 or x.numel() // max(k, 1) > 64 or not 1 <= len(weights) <= 4:
+        return False
+    return all(w.dtype == x.dtype and w.is_cuda and w.dim() == 2 and w.shape[1] == k and w.stride(1) == 1
+               and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0 for w in weights)
+
+
+def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torch.Tensor | None] | None = None,
+                 gated: bool = False):
+    """One launch for ``x @ W_i.T (+ b_i)`` over products that share ``x`` (M <= 64, no autograd).
+
+    Returns the list of outputs, or ``silu(x @ W_0.T) * (x @ W_1.T)`` when ``gated``; each
+    product is computed and rounded exactly as ``triton_matmul`` would.
+    """
+    k = x.shape[-1]
+    x2 = _rows(x, k)
+    m = x2.shape[0]
+    n = len(weights)
+    biases = biases or [None] * n
+    outs = [torch.empty((m, w.shape[0]), dtype=x.dtype, device=x.device) for w in (weights[:1] if gated else weights)]
+    arr_p = ctypes.c_void_p * n
+    arr_l = ctypes.c_int64 * n
+    bptr = arr_p(*(w.data_ptr() for w in weights))
+    ldb = arr_l(*(w.stride(0) for w in weights))
+    nn_ = arr_l(*(w.shape[0] for w in weights))
+    cptr = arr_p(*([o.data_ptr() for o in outs] + [None] * (n - len(outs))))
+    ldc = arr_l(*([o.stride(0) for o in outs] + [0] * (n - len(outs))))
+    has_bias = any(b is not None for b in biases)
+    bias_arr = arr_p(*((b.contiguous().data_ptr() if b is not None else None) for b in biases)) if has_bias else None
+    _native.call("qh_gemm_multi", m, k, x2.data_ptr(), x2.stride(0), n, ctypes.addressof(bptr), ctypes.addressof(ldb),
+                 ctypes.addressof(nn_), ctypes.addressof(cptr), ctypes.addressof(ldc),
+                 ctypes.addressof(bias_arr) if has_bias else None, int(gated), _native.dtype_code(x.dtype),
+                 _native.stream(x.device))
+    lead = x.shape[:-1]
+    outs = [o.view(*lead, o.shape[1]) for o in outs]
+    return outs[0] if gated else outs
 
 
 def _native_matmul_forward(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:

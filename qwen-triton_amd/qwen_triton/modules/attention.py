@@ -11,8 +11,9 @@ flash kernel):
 * explicit additive mask (padding): fp32 SDPA over repeated KV heads, as the
   reference does for masked multi-token attention.
 
-Inference (no autograd, GPU, position-indexed cache): q_norm/k_norm, RoPE and
-the cache writes run as one fused pass (``qh_attn_prepare``) with the same
+Inference (no autograd, GPU, position-indexed cache): the q/k/v projections
+of up to 64 tokens run as one grouped launch, and q_norm/k_norm, RoPE and the
+cache writes as one fused pass (``qh_attn_prepare``), both with the same
 arithmetic as the separate kernels.
 """
 from __future__ import annotations
@@ -27,6 +28,7 @@ from qwen_triton.configs import QwenTritonConfig
 from qwen_triton.kernels import sigmoid_mul
 from qwen_triton.kernels import flash_attention as _fa
 from qwen_triton.kernels.flash_attention import triton_flash_attention
+from qwen_triton.kernels.matmul import linear_group, linear_group_ok
 from qwen_triton.modules.cache import QwenTritonCache
 from qwen_triton.modules.linear import TritonLinear
 from qwen_triton.modules.norms import QwenRMSNorm
@@ -140,9 +142,13 @@ class QwenFullAttention(nn.Module):
         input_shape = hidden_states.shape[:-1]
         cos, sin = position_embeddings
         if self._fused_prepare_ok(hidden_states, cos, past_key_values, cache_position):
-            q, k, v = self._fused_prepare(self.q_proj(hidden_states), self.k_proj(hidden_states),
-                                          self.v_proj(hidden_states), cos, sin, past_key_values, cache_position,
-                                          max_position)
+            projs = (self.q_proj, self.k_proj, self.v_proj)
+            weights = [p.weight for p in projs]
+            if linear_group_ok(hidden_states, weights):
+                q2, k2, v2 = linear_group(hidden_states, weights, [p.bias for p in projs])
+            else:
+                q2, k2, v2 = (p(hidden_states) for p in projs)
+            q, k, v = self._fused_prepare(q2, k2, v2, cos, sin, past_key_values, cache_position, max_position)
             out = self._attend(q, k, v, attention_mask, hidden_states.dtype)
             return self.o_proj(out.transpose(1, 2).reshape(*input_shape, -1))
         mixed_q = self.q_proj(hidden_states)

@@ -317,6 +317,51 @@ def test_gemm_decode_shapes_deterministic(M, N, Kd):
         assert torch.equal(K.triton_matmul(x, w), y0)
 
 
+@pytest.mark.parametrize("M", [1, 5, 64])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_linear_group_matches_separate_gemms(M, with_bias):
+    from qwen_triton.kernels.matmul import linear_group, linear_group_ok
+
+    Kd = 1024
+    x = randn(M, Kd, dtype=torch.bfloat16, seed=200)
+    ws = [randn(n, Kd, dtype=torch.bfloat16, seed=201 + i, scale=0.05) for i, n in enumerate((2048, 1024, 1000))]
+    bs = [randn(w.shape[0], dtype=torch.bfloat16, seed=210 + i) if with_bias else None for i, w in enumerate(ws)]
+    assert linear_group_ok(x, ws)
+    c0 = native_calls("qh_gemm_multi")
+    outs = linear_group(x, ws, bs)
+    assert native_calls("qh_gemm_multi") == c0 + 1
+    for w, b, o in zip(ws, bs, outs):
+        assert torch.equal(o, K.triton_matmul(x, w, b))
+
+
+@pytest.mark.parametrize("M", [1, 17, 64])
+def test_linear_group_gated_matches_gemms_then_silu_mul(M):
+    from qwen_triton.kernels.matmul import linear_group
+
+    Kd = 1024
+    x = randn(2, M, Kd, dtype=torch.bfloat16, seed=220)[0]
+    wg = randn(3072, Kd, dtype=torch.bfloat16, seed=221, scale=0.05)
+    wu = randn(3072, Kd, dtype=torch.bfloat16, seed=222, scale=0.05)
+    fused = linear_group(x, [wg, wu], gated=True)
+    assert torch.equal(fused, K.silu_mul(K.triton_matmul(x, wg), K.triton_matmul(x, wu)))
+    close(fused, O.silu_mul(O.linear(x, wg), O.linear(x, wu)), atol=3e-2, rtol=3e-2)
+
+
+def test_mlp_inference_path_matches_autograd_path():
+    from qwen_triton.modules import QwenMLP
+
+    torch.manual_seed(3)
+    mlp = QwenMLP(256, 768).to(DEV, torch.bfloat16)
+    x = randn(4, 3, 256, dtype=torch.bfloat16, seed=230)
+    c0 = native_calls("qh_gemm_multi")
+    with torch.no_grad():
+        fast = mlp(x)
+    assert native_calls("qh_gemm_multi") == c0 + 1
+    with torch.enable_grad():
+        ref = mlp(x).detach()
+    assert torch.equal(fast, ref)
+
+
 @pytest.mark.parametrize("M,N,Kd", [(333, 256, 192), (64, 1024, 3072), (1024, 512, 1024), (40, 96, 64)])
 def test_gemm_backward_bf16(M, N, Kd):
     x = randn(2, M, Kd, dtype=torch.bfloat16, seed=93).requires_grad_(True)
