@@ -240,15 +240,25 @@ struct DecodeProducts {
 
 template <typename T, typename OT, int MT, int KSP, bool GATED>
 __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__ A, int64_t lda,
-                                                           const DecodeProducts<T, OT> P, int M, int K, int kr) {
+                                                           const DecodeProducts<T, OT> P, int M, int K, int kr,
+                                                           int ms, int tiles) {
   constexpr int CG = 16 / KSP;
   constexpr int NB = GATED ? 2 : 1;                       // weight matrices per wave
   constexpr int CH = (MT <= 2 ? 8 : 4) / NB;              // k-steps whose loads are issued together
   typedef typename Mfma<T>::v8 v8;
   __shared__ float red[16][MT * 16][16];
+  // Workgroup -> (column tile, row group). The ms row groups of a tile get
+  // workgroup ids that are equal mod 8, so they run on one XCD and read the
+  // tile's weights through the same L2.
+  const int bid = (int)blockIdx.x;
+  const int rest = bid >> 3;
+  const int mg = rest % ms;
+  const int gtile = (rest / ms) * 8 + (bid & 7);
+  if (gtile >= tiles) return;
+  const int m0 = mg * MT * 16;
   int pi = 0;
-  while (pi + 1 < P.count && (int)blockIdx.x >= P.tile0[pi + 1]) ++pi;
-  const int tile = (int)blockIdx.x - P.tile0[pi];
+  while (pi + 1 < P.count && gtile >= P.tile0[pi + 1]) ++pi;
+  const int tile = gtile - P.tile0[pi];
   const int N = P.N[pi];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int cg = wid / KSP, ks = wid % KSP;
@@ -280,7 +290,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
       }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        const int m = i * 16 + li;
+        const int m = m0 + i * 16 + li;
         if (m < M && kok) a[u][i] = *reinterpret_cast<const v8*>(A + (int64_t)m * lda + k);
         else a[u][i] = zero;
       }
@@ -311,7 +321,8 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
 #pragma unroll
       for (int s2 = 0; s2 < KSP; ++s2) v += red[g * KSP + s2][row][col];
       const int gn = (tile * CG + g) * 16 + col;
-      if (row >= M || gn >= N) continue;
+      const int grow = m0 + row;
+      if (grow >= M || gn >= N) continue;
       const T* bias = P.bias[pi + j];
       const float val = v + (bias ? to_f32(bias[gn]) : 0.f);
       if constexpr (GATED) {
@@ -319,10 +330,10 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
           first[slot] = to_f32(from_f32<OT>(val));
         } else {
           const float gt = first[slot], up = to_f32(from_f32<OT>(val));
-          P.C[pi][(int64_t)row * P.ldc[pi] + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
+          P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
         }
       } else {
-        P.C[pi][(int64_t)row * P.ldc[pi] + gn] = from_f32<OT>(val);
+        P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = from_f32<OT>(val);
       }
     }
   }
@@ -330,7 +341,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
 
 template <typename T, typename OT>
 void launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int M, int K, bool gated,
-                            hipStream_t st) {
+                            hipStream_t st, int ms_force = 0) {
   // Narrow outputs: all 16 waves split K (16 columns per workgroup). Wide
   // outputs already give enough workgroups: 4 column groups x 4 K slices.
   int maxN = 0;
@@ -342,14 +353,23 @@ void launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, i
   P.tile0[0] = 0;
   for (int i = 0; i < nprod; ++i) P.tile0[i + 1] = P.tile0[i] + (P.N[i] + cols - 1) / cols;
   if (gated) P.count = 1;
-  const int grid = P.tile0[nprod];
+  const int tiles = P.tile0[nprod];
   const int kr = ((K + ksp - 1) / ksp + 31) / 32 * 32;
   const int mt = (M + 15) / 16;
+  // Row groups per column tile: with few column tiles, up to one workgroup
+  // per 16 rows, until about one workgroup per CU (measured best: 1024-column
+  // outputs split 4 ways, 2048 two ways, 3072 not at all).
+  int ms = 1;
+  while (ms < mt && tiles * ms * 2 <= 256) ms *= 2;
+  if (ms > mt) ms = mt;
+  if (ms_force > 0 && ms_force <= mt) ms = ms_force;
+  const int mtw = (mt + ms - 1) / ms;
+  const int grid = (tiles + 7) / 8 * 8 * ms;
 #define QH_DG(MTV, KSPV, GV) \
-  gemm_decode_kernel<T, OT, MTV, KSPV, GV><<<grid, 1024, 0, st>>>(a, lda, P, M, K, kr)
+  gemm_decode_kernel<T, OT, MTV, KSPV, GV><<<grid, 1024, 0, st>>>(a, lda, P, M, K, kr, ms, tiles)
 #define QH_DG_W(MTV) \
   if (gated) QH_DG(MTV, 16, true); else if (wide) QH_DG(MTV, 4, false); else QH_DG(MTV, 16, false);
-  if (mt == 1) { QH_DG_W(1) } else if (mt == 2) { QH_DG_W(2) } else if (mt == 3) { QH_DG_W(3) } else { QH_DG_W(4) }
+  if (mtw == 1) { QH_DG_W(1) } else if (mtw == 2) { QH_DG_W(2) } else if (mtw == 3) { QH_DG_W(3) } else { QH_DG_W(4) }
 #undef QH_DG_W
 #undef QH_DG
 }
