@@ -57,6 +57,14 @@ int qh_sigmoid_mul_bwd(const void* x, const void* gate, const void* gout, void* 
  * `wdtype` is the weight's dtype. Replaces qwen_triton/kernels/rmsnorm.py:101-133, :64-82. */
 int qh_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t rows, int64_t cols, float eps,
                    int one_plus, int dtype, int wdtype, void* stream);
+/* sum = x + r (rounded to the dtype) and y = RMSNorm(sum) * (w or 1 + w) in
+ * one pass over rows x cols; both outputs equal qh_add followed by
+ * qh_rmsnorm_fwd. bf16/f16. Replaces, fused, the residual add and the
+ * following norm of qwen_triton/models/core.py:95-153 (QwenDecoderLayer:
+ * residual_add, qwen_triton/kernels/residual_add.py:86-101, then rmsnorm,
+ * qwen_triton/kernels/rmsnorm.py:101-196). */
+int qh_add_rmsnorm(const void* x, const void* r, const void* w, void* sum, void* y, int64_t rows, int64_t cols,
+                   float eps, int one_plus, int dtype, int wdtype, void* stream);
 /* Workspace bytes for qh_rmsnorm_bwd (deterministic two-stage dW). */
 int64_t qh_rmsnorm_bwd_workspace(int64_t rows, int64_t cols, int dtype);
 /* gx (dtype) and gw (wdtype, summed over rows in a fixed order, no atomics).

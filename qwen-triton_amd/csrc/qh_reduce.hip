@@ -76,6 +76,52 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_fast(const T* __restrict__ x,
   }
 }
 
+// Residual add fused with RMSNorm: sum = x + r (rounded to T, as the add
+// kernel), y = RMSNorm(sum) with the row shape and summation order of
+// rmsnorm_fwd_fast, so both outputs equal the two separate kernels'.
+template <typename T, int G, int NV>
+__global__ __launch_bounds__(256) void add_rmsnorm_fast(const T* __restrict__ x, const T* __restrict__ r,
+                                                        const void* __restrict__ w, int wdtype, T* __restrict__ sum,
+                                                        T* __restrict__ y, int64_t rows, int cols, float eps,
+                                                        float wadd) {
+  constexpr int VN = Vec16<T>::N;
+  constexpr int RPB = 256 / G;
+  const int grp = threadIdx.x / G, g = threadIdx.x % G;
+  for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
+    Vec16<T> xv[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        const Vec16<T> a = ld16(x + row * cols + c), b = ld16(r + row * cols + c);
+#pragma unroll
+        for (int j = 0; j < VN; ++j) xv[i].v[j] = from_f32<T>(to_f32(a.v[j]) + to_f32(b.v[j]));
+        st16(sum + row * cols + c, xv[i]);
+#pragma unroll
+        for (int j = 0; j < VN; ++j) {
+          const float f = to_f32(xv[i].v[j]);
+          ss += f * f;
+        }
+      }
+    }
+    ss = wave_sum(ss, G);
+    const float inv = rsqrtf(ss / (float)cols + eps);
+    T* yr = y + row * cols;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * G + g) * VN;
+      if (c < cols) {
+        Vec16<T> o;
+#pragma unroll
+        for (int j = 0; j < VN; ++j)
+          o.v[j] = from_f32<T>((to_f32(xv[i].v[j]) * inv) * (load_any(w, wdtype, c + j) + wadd));
+        st16(yr + c, o);
+      }
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_generic(const T* __restrict__ x, const void* __restrict__ w,
                                                            int wdtype, T* __restrict__ y, int64_t rows,
@@ -619,6 +665,35 @@ extern "C" int qh_rmsnorm_fwd(const void* x, const void* w, void* y, int64_t row
   const float wadd = one_plus ? 1.f : 0.f;
   QH_DISPATCH_DTYPE(dtype, T, "qh_rmsnorm_fwd", launch_rms_fwd<T>(x, w, wdtype, y, rows, cols, eps, wadd, st));
   QH_CHECK_LAUNCH("qh_rmsnorm_fwd");
+  return QH_OK;
+}
+
+extern "C" int qh_add_rmsnorm(const void* x, const void* r, const void* w, void* sum, void* y, int64_t rows,
+                              int64_t cols, float eps, int one_plus, int dtype, int wdtype, void* stream) {
+  QH_CHECK_ARG(rows >= 0 && cols >= 0, "qh_add_rmsnorm: negative shape");
+  QH_CHECK_ARG(wdtype >= QH_F32 && wdtype <= QH_BF16, "qh_add_rmsnorm: bad weight dtype");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_add_rmsnorm: bf16/f16 only");
+  if (rows == 0 || cols == 0) return QH_OK;
+  int G = 0, NV = 0;
+  const bool fast = pick_row_shape(cols, 8, G, NV) && aligned16(x) && aligned16(r) && aligned16(sum) && aligned16(y);
+  if (!fast) {  // the two kernels in sequence
+    int rc = qh_add(x, r, sum, rows * cols, dtype, stream);
+    return rc ? rc : qh_rmsnorm_fwd(sum, w, y, rows, cols, eps, one_plus, dtype, wdtype, stream);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const float wadd = one_plus ? 1.f : 0.f;
+  const int grid = grid_cap(ceil_div(rows, 256 / G));
+#define QH_ADDRMS(T) \
+  QH_SHAPE_SWITCH(add_rmsnorm_fast, (const T*)x, (const T*)r, w, wdtype, (T*)sum, (T*)y, rows, (int)cols, eps, wadd)
+  if (dtype == QH_BF16) {
+    typedef bf16_t T;
+    QH_ADDRMS(T)
+  } else {
+    typedef f16_t T;
+    QH_ADDRMS(T)
+  }
+#undef QH_ADDRMS
+  QH_CHECK_LAUNCH("qh_add_rmsnorm");
   return QH_OK;
 }
 

@@ -101,3 +101,25 @@ def rmsnorm(
     except Exception as exc:
         _GUARD.failed(exc)
         return _torch_rmsnorm(hidden_states, weight, eps, one_plus_weight)
+
+
+def add_rmsnorm_ok(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor) -> bool:
+    """True when the fused residual-add + RMSNorm pass applies (inference on GPU)."""
+    return (not torch.is_grad_enabled() and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
+            and residual.shape == x.shape and residual.dtype == x.dtype and x.is_contiguous()
+            and residual.is_contiguous() and weight.is_contiguous() and weight.dim() == 1
+            and weight.shape[0] == x.shape[-1] and weight.dtype in (torch.float32, torch.float16, torch.bfloat16)
+            and _native.available())
+
+
+def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                one_plus_weight: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """``s = x + residual`` and ``rmsnorm(s)`` in one pass (no autograd); equals
+    ``residual_add`` followed by ``rmsnorm`` exactly. Returns ``(s, rmsnorm(s))``."""
+    cols = x.shape[-1]
+    s = torch.empty_like(x)
+    y = torch.empty_like(x)
+    _native.call("qh_add_rmsnorm", x.data_ptr(), residual.data_ptr(), weight.data_ptr(), s.data_ptr(), y.data_ptr(),
+                 x.numel() // max(cols, 1), cols, float(eps), int(one_plus_weight), _native.dtype_code(x.dtype),
+                 _native.dtype_code(weight.dtype), _native.stream(x.device))
+    return s, y

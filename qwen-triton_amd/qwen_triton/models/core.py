@@ -24,6 +24,7 @@ from transformers.modeling_outputs import CausalLMOutputWithPast
 from qwen_triton.configs import QwenTritonConfig
 from qwen_triton.kernels.cross_entropy import triton_cross_entropy
 from qwen_triton.kernels.residual_add import residual_add
+from qwen_triton.kernels.rmsnorm import add_rmsnorm, add_rmsnorm_ok
 from qwen_triton.modules import (
     Qwen3NextLinearAttention,
     QwenFullAttention,
@@ -101,10 +102,28 @@ class QwenDecoderLayer(nn.Module):
         self.mlp = QwenSparseMoeBlock(config) if _layer_uses_moe(config, layer_idx) else QwenMLP(
             config.hidden_size, config.intermediate_size)
 
+    def _add_norm(self, x: torch.Tensor, residual: torch.Tensor, norm: QwenRMSNorm):
+        """(x + residual, norm(x + residual)), fused into one pass for inference."""
+        if add_rmsnorm_ok(x, residual, norm.weight):
+            return add_rmsnorm(x, residual, norm.weight, norm.eps, norm.one_plus_weight)
+        s = residual_add(x, residual)
+        return s, norm(s)
+
     def forward(self, hidden_states, position_embeddings, attention_mask=None, past_key_values=None,
-                cache_position=None, max_position: int | None = None):
-        residual = hidden_states
-        h = self.input_layernorm(hidden_states)
+                cache_position=None, max_position: int | None = None, residual_in: torch.Tensor | None = None,
+                defer_residual: bool = False):
+        """Reference contract: returns ``(hidden_states, router_logits)``.
+
+        For inference chains the model may pass ``residual_in`` (``hidden_states`` is then the
+        previous layer's un-added output) and ``defer_residual`` (return ``(mlp_out,
+        router_logits, residual)`` without the final add), so that each residual add is fused
+        with the norm that follows it.
+        """
+        if residual_in is not None:
+            residual, h = self._add_norm(hidden_states, residual_in, self.input_layernorm)
+        else:
+            residual = hidden_states
+            h = self.input_layernorm(hidden_states)
         if self.layer_type == "linear_attention":
             h = self.linear_attn(hidden_states=h, cache_params=past_key_values, cache_position=cache_position,
                                  attention_mask=attention_mask)
@@ -112,12 +131,13 @@ class QwenDecoderLayer(nn.Module):
             h = self.self_attn(hidden_states=h, position_embeddings=position_embeddings,
                                attention_mask=attention_mask, past_key_values=past_key_values,
                                cache_position=cache_position, max_position=max_position)
-        h = residual_add(h, residual)
-        residual = h
-        h = self.mlp(self.post_attention_layernorm(h))
+        residual, h = self._add_norm(h, residual, self.post_attention_layernorm)
+        h = self.mlp(h)
         router_logits = None
         if isinstance(h, tuple):
             h, router_logits = h
+        if defer_residual:
+            return h, router_logits, residual
         return residual_add(h, residual), router_logits
 
 
@@ -169,14 +189,27 @@ class QwenTritonModel(nn.Module):
         hidden = inputs_embeds
         position_embeddings = self.rotary_emb(hidden, position_ids)
         router_logits: list[torch.Tensor] = []
+        # Inference on GPU: each layer's closing residual add is fused with the next norm.
+        chain = add_rmsnorm_ok(hidden, hidden, self.norm.weight)
+        residual = None
         for layer in self.layers:
             layer_mask = attention_mask if layer.layer_type == "linear_attention" else masks[layer.layer_type]
-            hidden, layer_router = layer(hidden, position_embeddings=position_embeddings, attention_mask=layer_mask,
-                                         past_key_values=past_key_values, cache_position=cache_position,
-                                         max_position=max_position)
+            out = layer(hidden, position_embeddings=position_embeddings, attention_mask=layer_mask,
+                        past_key_values=past_key_values, cache_position=cache_position, max_position=max_position,
+                        residual_in=residual, defer_residual=chain)
+            if chain:
+                hidden, layer_router, residual = out
+            else:
+                hidden, layer_router = out
             if output_router_logits and layer_router is not None:
                 router_logits.append(layer_router)
-        hidden = self.norm(hidden)
+        if chain and residual is not None:
+            if add_rmsnorm_ok(hidden, residual, self.norm.weight):
+                _, hidden = add_rmsnorm(hidden, residual, self.norm.weight, self.norm.eps, self.norm.one_plus_weight)
+            else:
+                hidden = self.norm(residual_add(hidden, residual))
+        else:
+            hidden = self.norm(hidden)
         return SimpleNamespace(
             last_hidden_state=hidden,
             past_key_values=past_key_values if use_cache else None,

@@ -469,3 +469,18 @@ def test_flash_decode_device_seqlens():
     for b, n in enumerate(lens):
         exp = O.attention(q[b:b + 1], kc[b:b + 1, :, :n], vc[b:b + 1, :, :n], D ** -0.5, False, Hq // Hkv)[0]
         close(out[b:b + 1], exp, **BF16_TOL)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 1024), (3, 2048), (7, 200)])
+def test_add_rmsnorm_matches_add_then_rmsnorm(rows, cols):
+    from qwen_triton.kernels.rmsnorm import add_rmsnorm
+
+    x = randn(rows, cols, dtype=torch.bfloat16, seed=240)
+    r = randn(rows, cols, dtype=torch.bfloat16, seed=241)
+    w = randn(cols, seed=242) * 0.1 + 1.0
+    with torch.no_grad():
+        s, y = add_rmsnorm(x, r, w, 1e-6, False)
+        s_ref = K.residual_add(x, r)
+        y_ref = K.rmsnorm(s_ref, w, eps=1e-6)
+    assert torch.equal(s, s_ref) and torch.equal(y, y_ref)
+    close(y, O.rmsnorm(x.double() + r.double(), w, 1e-6), atol=3e-2, rtol=3e-2)
