@@ -368,6 +368,57 @@ def bench_gemm(steps, warmup):
     return out
 
 
+def bench_moe(steps, warmup, loop_reps=1):
+    """Config 4's expert path: routing + dispatch + grouped expert GEMMs + combine, 16384 tokens."""
+    import torch
+    from qwen_triton import QwenTritonConfig
+    from qwen_triton.modules import QwenSparseMoeBlock
+
+    T, H, E, K, I = 16384, 2048, 128, 8, 768
+    cfg = QwenTritonConfig.from_hf_config(dict(
+        model_type="qwen3_moe", vocab_size=151936, hidden_size=H, intermediate_size=6144, num_hidden_layers=1,
+        num_attention_heads=32, num_key_value_heads=4, head_dim=128, moe_intermediate_size=I, num_experts=E,
+        num_experts_per_tok=K, norm_topk_prob=True, decoder_sparse_step=1, mlp_only_layers=[]))
+    torch.manual_seed(0)
+    blk = QwenSparseMoeBlock(cfg)
+    with torch.no_grad():
+        for n, prm in blk.named_parameters():
+            prm.normal_(0.0, 0.02)
+    blk = blk.to("cuda", torch.bfloat16)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(T, H, device="cuda", dtype=torch.bfloat16, generator=g)
+    logits = torch.randn(T, E, device="cuda", dtype=torch.float32, generator=g)
+
+    def step():
+        w, sel = blk.route(logits, torch.bfloat16)
+        return blk.experts_forward(x, w, sel)
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        sync()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        sync()
+    ms = e0.elapsed_time(e1) / steps
+    flop = 2 * 3 * T * K * H * I  # gate, up, down over the T*K routed rows
+    res = {"moe_fwd_ms": round(ms, 3), "moe_fwd_tflops": round(flop / ms / 1e9, 1),
+           "moe_fwd_frac": round(flop / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4), "tokens": T, "experts": E, "top_k": K}
+    # the reference's per-expert loop (autograd on selects it), for comparison
+    w, sel = blk.route(logits, torch.bfloat16)
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(loop_reps):
+        with torch.enable_grad():
+            blk.experts_forward(x, w, sel)
+    sync()
+    res["loop_fwd_ms"] = round((time.perf_counter() - t0) * 1e3 / loop_reps, 3)
+    return res
+
+
 def bench_roofline_kernels(reps=20):
     """Only the dominant decode kernel (one layer's cache) plus a 1 GiB copy for counter calibration."""
     import torch
@@ -402,7 +453,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="decode", choices=["decode", "fa", "dense", "gemm", "roofline"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "fa", "dense", "gemm", "roofline", "moe"])
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -429,6 +480,10 @@ def main() -> None:
     if args.workload == "gemm":
         res = bench_gemm(args.steps, args.warmup)
         print(json.dumps({"metric": "GEMM shapes (bf16)", "rows": res}), flush=True)
+        return
+    if args.workload == "moe":
+        res = bench_moe(args.steps, args.warmup)
+        print(json.dumps({"metric": "MoE experts fwd (config 4, 30B-A3B layer shape)", **res}), flush=True)
         return
     if args.workload == "dense":
         res = bench_dense(args.steps, args.warmup)

@@ -150,6 +150,38 @@ int qh_index_add(void* target, int64_t stride_t, const void* src, int64_t stride
                  int64_t n_src, int64_t n_target, int64_t D, void* ws, int64_t ws_bytes, int dtype,
                  void* stream);
 
+/* ---- MoE experts: dispatch, grouped GEMM, combine ------------------------ */
+/* Sort/segment dispatch of the n_tokens*top_k routed (token, slot) pairs by
+ * expert (stable radix sort; selected is int64 [n_tokens, top_k], ids outside
+ * [0, n_experts) are dropped). Outputs, for the R = n_tokens*top_k sorted rows:
+ * rows[r] (token), wsorted[r] (routing weight, dtype), inv[token*top_k + slot]
+ * = r; and seg_off[e] (first row of expert e, e = 0..n_experts) and
+ * tile_off[e] (first M-tile of expert e for tiles of tile_m rows, prefix sum).
+ * Replaces the expert_mask / nonzero / where bookkeeping of
+ * qwen_triton/modules/moe.py:45-51 (triton_one_hot, qwen_triton/kernels/moe_routing.py:175-200). */
+int64_t qh_moe_dispatch_workspace(int64_t n_tokens, int64_t top_k, int64_t n_experts);
+int qh_moe_dispatch(const int64_t* selected, const void* weights, int64_t n_tokens, int64_t top_k,
+                    int64_t n_experts, int64_t tile_m, void* ws, int64_t ws_bytes, int32_t* rows, void* wsorted,
+                    int32_t* inv, int32_t* seg_off, int32_t* tile_off, int dtype, void* stream);
+/* Grouped expert GEMM over the dispatch segments (tile_off for tile_m = 128).
+ * B_table is a DEVICE array of weight pointers ([out, in] row-major, row stride
+ * ldb): mode 0 (gated): 2*E entries (gate_e, up_e), A = X gathered through
+ * rows[], C[r] = silu(X[rows[r]] Wg^T) * (X[rows[r]] Wu^T), N = intermediate;
+ * mode 1 (scaled): E entries, A rows contiguous, C[r] = (A[r] Wd^T) * wrow[r].
+ * Each product is rounded to the dtype before the SiLU-mul / scaling, as the
+ * reference's per-expert TritonLinear, silu_mul and multiply do.
+ * Replaces the per-expert QwenMLP calls of qwen_triton/modules/moe.py:47-50
+ * (qwen_triton/modules/mlp.py:19-22, kernels/matmul.py:130-155, kernels/swiglu.py:175-190). */
+int qh_moe_gemm(int mode, const void* A, int64_t lda, const int32_t* rows, const void* const* B_table,
+                int64_t ldb, void* C, int64_t ldc, const void* wrow, const int32_t* seg_off,
+                const int32_t* tile_off, int64_t R, int64_t E, int64_t N, int64_t K, int dtype, void* stream);
+/* out[t] = sum of the token's expert rows Y[inv[t*top_k + j]] in ascending
+ * expert order, rounded to the dtype after every add (the reference's
+ * per-expert index_add into zeros). Deterministic; out fully written.
+ * Replaces qwen_triton/modules/moe.py:50-51 (triton_index_add, kernels/moe_routing.py:322-343). */
+int qh_moe_combine(const void* Y, int64_t ldy, const int32_t* inv, const int64_t* selected, int64_t n_tokens,
+                   int64_t top_k, int64_t n_experts, void* out, int64_t H, int dtype, void* stream);
+
 /* ---- GEMM (Linear) ------------------------------------------------------ */
 /* C[M,N] = A(M,K) . B(N,K)^T (+ bias[N]) with operand views
  *   A(m,k) = trans_a ? A[k*lda + m] : A[m*lda + k]

@@ -389,6 +389,175 @@ void launch_decode_gemm(const T* a, int64_t lda, const T* b, int64_t ldb, OT* c,
 }
 
 // ---------------------------------------------------------------------------
+// Grouped GEMM over expert segments (MoE). The rows of the left operand are
+// grouped by expert: segment e is rows [seg[e], seg[e+1]) and multiplies
+// expert e's weight matrix, found through a device table of pointers (the
+// experts' parameters stay separate tensors). M-tiles never straddle a
+// segment: toff[e] is the first M-tile of expert e (prefix sum of
+// ceil(n_e / 128)) and the grid's x extent is an upper bound (extra
+// workgroups exit). Modes:
+//   MOE_GATED:  A rows gathered from X through rows[] (token of each routed
+//               row); the 128 B-tile rows are 32-row blocks of gate and up
+//               weights in turn, so a wave's two 32-column MFMA tiles hold
+//               the same columns of gate and up and the epilogue writes
+//               silu(gate) * up (each rounded to T first, as the expert MLP's
+//               two GEMMs and SiLU-mul kernel would);
+//   MOE_SCALED: A rows contiguous; the epilogue writes round(acc) * w[row]
+//               rounded, the routing-weight scaling of the expert output.
+// ---------------------------------------------------------------------------
+enum { MOE_GATED = 0, MOE_SCALED = 1 };
+
+// Rows of a ROWS x BK tile read through one row pointer per staging register
+// (nullptr = zero row); k-contiguous LDS layout as TileLoader<.., false>.
+template <typename T, int ROWS>
+struct RowTileLoader {
+  static constexpr int NREG = ROWS / 32;
+  uint4 r[NREG];
+  const T* rowp[NREG];
+  __device__ __forceinline__ void load(int k0, int K) {
+    const int tid = threadIdx.x;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < NREG; ++i) {
+      const int gk = k0 + ((tid + i * 256) & 7) * 8;
+      if (rowp[i] != nullptr && gk < K) r[i] = *reinterpret_cast<const uint4*>(rowp[i] + gk);
+      else r[i] = z;
+    }
+  }
+  __device__ __forceinline__ void store(T* __restrict__ S) const {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NREG; ++i) {
+      const int c = tid + i * 256;
+      *reinterpret_cast<uint4*>(S + (c >> 3) * LDS_LD + (c & 7) * 8) = r[i];
+    }
+  }
+  // tile row of staging register i
+  static __device__ __forceinline__ int row_of(int i) { return (threadIdx.x + i * 256) >> 3; }
+};
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(const T* __restrict__ A, int64_t lda,
+                                                       const int* __restrict__ rows, const T* const* __restrict__ Bt,
+                                                       int64_t ldb, T* __restrict__ C, int64_t ldc,
+                                                       const T* __restrict__ wrow, const int* __restrict__ seg,
+                                                       const int* __restrict__ toff, int E, int N, int K) {
+  constexpr int BM = 128, BN = 128, WM = 2, WN = 2;
+  constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ __attribute__((aligned(16))) T smem[2][(BM + BN) * LDS_LD];
+
+  const int tm = blockIdx.x;
+  if (tm >= toff[E]) return;
+  int lo = 0, hi = E;  // largest e with toff[e] <= tm
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (toff[mid] <= tm) lo = mid;
+    else hi = mid;
+  }
+  const int e = lo;
+  const int r0 = seg[e] + (tm - toff[e]) * BM, r1 = seg[e + 1];
+  // MOE_GATED covers 64 output columns (gate and up), MOE_SCALED 128.
+  const int n0 = blockIdx.y * (MODE == MOE_GATED ? 64 : 128);
+
+  RowTileLoader<T, BM> la;
+  RowTileLoader<T, BN> lb;
+#pragma unroll
+  for (int i = 0; i < RowTileLoader<T, BM>::NREG; ++i) {
+    const int r = r0 + RowTileLoader<T, BM>::row_of(i);
+    const int src = MODE == MOE_GATED ? (r < r1 ? rows[r] : -1) : (r < r1 ? r : -1);
+    la.rowp[i] = src >= 0 ? A + (int64_t)src * lda : nullptr;
+  }
+#pragma unroll
+  for (int i = 0; i < RowTileLoader<T, BN>::NREG; ++i) {
+    const int tr = RowTileLoader<T, BN>::row_of(i);
+    const T* W;
+    int col;
+    if (MODE == MOE_GATED) {
+      const int blk = tr >> 5;
+      W = Bt[2 * e + (blk & 1)];
+      col = n0 + (blk >> 1) * 32 + (tr & 31);
+    } else {
+      W = Bt[e];
+      col = n0 + tr;
+    }
+    lb.rowp[i] = col < N ? W + (int64_t)col * ldb : nullptr;
+  }
+
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wm = wid / WN, wn = wid % WN;
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = zero16();
+
+  const int nk = (K + BK - 1) / BK;
+  la.load(0, K);
+  lb.load(0, K);
+  la.store(smem[0]);
+  lb.store(smem[0] + BM * LDS_LD);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      la.load((kt + 1) * BK, K);
+      lb.load((kt + 1) * BK, K);
+    }
+    const T* As = smem[buf];
+    const T* Bs = smem[buf] + BM * LDS_LD;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      v8 af[TM], bf[TN];
+      const int koff = kk * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const v8*>(As + (wm * WTM + i * 32 + (lane & 31)) * LDS_LD + koff);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const v8*>(Bs + (wn * WTN + j * 32 + (lane & 31)) * LDS_LD + koff);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af[i], bf[j], acc[i][j]);
+    }
+    if (more) {
+      la.store(smem[buf ^ 1]);
+      lb.store(smem[buf ^ 1] + BM * LDS_LD);
+    }
+    __syncthreads();
+  }
+
+  // C layout of a 32x32 tile: column lane % 32, rows 8 g + 4 (lane / 32) + r.
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int rbase = r0 + wm * WTM + i * 32 + (lane >> 5) * 4;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = rbase + g * 8 + r;
+        if (row >= r1) continue;
+        if constexpr (MODE == MOE_GATED) {
+          const int col = n0 + wn * 32 + (lane & 31);
+          if (col < N) {
+            const float gt = to_f32((T)acc[i][0][g * 4 + r]), up = to_f32((T)acc[i][1][g * 4 + r]);
+            C[(int64_t)row * ldc + col] = from_f32<T>(gt * sigmoidf_(gt) * up);
+          }
+        } else {
+          const float w = to_f32(wrow[row]);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * WTN + j * 32 + (lane & 31);
+            if (col < N) C[(int64_t)row * ldc + col] = from_f32<T>(to_f32((T)acc[i][j][g * 4 + r]) * w);
+          }
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic VALU GEMM (fp32 and shapes the MFMA path does not take). 64x64 tile,
 // 256 threads each owning a 4x4 block, fp32 accumulation.
 // ---------------------------------------------------------------------------
@@ -577,6 +746,38 @@ extern "C" int qh_gemm_multi(int64_t M, int64_t K, const void* A, int64_t lda, i
   if (dtype == QH_BF16) QH_MULTI(bf16_t) else QH_MULTI(f16_t)
 #undef QH_MULTI
   QH_CHECK_LAUNCH("qh_gemm_multi");
+  return QH_OK;
+}
+
+extern "C" int qh_moe_gemm(int mode, const void* A, int64_t lda, const int32_t* rows, const void* const* B_table,
+                           int64_t ldb, void* C, int64_t ldc, const void* wrow, const int32_t* seg_off,
+                           const int32_t* tile_off, int64_t R, int64_t E, int64_t N, int64_t K, int dtype,
+                           void* stream) {
+  QH_CHECK_ARG(mode == MOE_GATED || mode == MOE_SCALED, "qh_moe_gemm: bad mode %d", mode);
+  QH_CHECK_ARG(R >= 0 && E > 0 && E < (1 << 20) && N > 0 && K > 0 && N < (1ll << 31) && K < (1ll << 31),
+               "qh_moe_gemm: bad shape");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_gemm: bf16/f16 only");
+  QH_CHECK_ARG(aligned16(A) && lda % 8 == 0 && K % 8 == 0 && lda >= K && ldb % 8 == 0 && ldb >= K && ldc >= N,
+               "qh_moe_gemm: operands must be 16-byte aligned with K, lda, ldb multiples of 8");
+  QH_CHECK_ARG(mode != MOE_GATED || rows != nullptr, "qh_moe_gemm: gated mode gathers through rows");
+  QH_CHECK_ARG(mode != MOE_SCALED || wrow != nullptr, "qh_moe_gemm: scaled mode needs the row weights");
+  if (R == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  // upper bound of the M-tiles: every expert may leave one partial tile
+  const int64_t mt = (R + 127) / 128 + E;
+  const int64_t nt = (N + (mode == MOE_GATED ? 63 : 127)) / (mode == MOE_GATED ? 64 : 128);
+  QH_CHECK_ARG(mt < (1ll << 31) && nt < 65536, "qh_moe_gemm: too many tiles");
+  dim3 grid((unsigned)mt, (unsigned)nt);
+#define QH_MOE(T, MD)                                                                                          \
+  moe_gemm_kernel<T, MD><<<grid, 256, 0, st>>>((const T*)A, lda, rows, (const T* const*)B_table, ldb, (T*)C,  \
+                                                 ldc, (const T*)wrow, seg_off, tile_off, (int)E, (int)N, (int)K)
+  if (dtype == QH_BF16) {
+    if (mode == MOE_GATED) QH_MOE(bf16_t, MOE_GATED); else QH_MOE(bf16_t, MOE_SCALED);
+  } else {
+    if (mode == MOE_GATED) QH_MOE(f16_t, MOE_GATED); else QH_MOE(f16_t, MOE_SCALED);
+  }
+#undef QH_MOE
+  QH_CHECK_LAUNCH("qh_moe_gemm");
   return QH_OK;
 }
 

@@ -1,0 +1,204 @@
+// MoE token dispatch and combine (the data movement around the grouped expert
+// GEMM, qh_moe_gemm).
+//
+// Dispatch: the T*k (token, slot) assignments are sorted by expert with a
+// stable radix sort (rocPRIM), so expert e's rows form one contiguous segment
+// in (token, slot) order. From the sorted keys: segment offsets (binary
+// search, no atomics), the first 128-row M-tile of each expert, and per
+// sorted row its token, its routing weight and (inverse map) its position.
+//
+// Combine: out[t] = sum over t's k expert rows in ascending expert order, with
+// a rounding to the dtype after every add — the order and rounding of the
+// reference's per-expert index_add into a zero tensor.
+#include <cstring>
+#include <rocprim/rocprim.hpp>
+
+#include "qh_common.h"
+
+namespace {
+
+static int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+static size_t sort_temp_bytes(int64_t n, int bits) {
+  size_t sz = 0;
+  rocprim::radix_sort_pairs((void*)nullptr, sz, (const uint32_t*)nullptr, (uint32_t*)nullptr,
+                            (const uint32_t*)nullptr, (uint32_t*)nullptr, (unsigned)n, 0, bits, (hipStream_t)0);
+  return sz;
+}
+
+static int key_bits(int64_t E) {
+  int b = 1;
+  while ((1ll << b) <= E) ++b;  // keys 0..E (E marks an out-of-range expert id)
+  return b;
+}
+
+__global__ __launch_bounds__(256) void moe_keys(const int64_t* __restrict__ sel, int64_t n, int64_t E,
+                                                uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t e = sel[i];
+    keys[i] = (e >= 0 && e < E) ? (uint32_t)e : (uint32_t)E;
+    vals[i] = (uint32_t)i;
+  }
+}
+
+// seg[e] = first sorted position with key >= e, e = 0..E (lower bound).
+__global__ __launch_bounds__(256) void moe_segments(const uint32_t* __restrict__ keys, int64_t n, int E,
+                                                    int32_t* __restrict__ seg) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e > E) return;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (keys[mid] < (uint32_t)e) lo = mid + 1;
+    else hi = mid;
+  }
+  seg[e] = (int32_t)lo;
+}
+
+// toff[e] = sum over e' < e of ceil(n_e' / tile_m) (one workgroup, E <= 65536).
+__global__ __launch_bounds__(1024) void moe_tile_offsets(const int32_t* __restrict__ seg, int E, int tile_m,
+                                                         int32_t* __restrict__ toff) {
+  __shared__ int32_t part[1024];
+  const int per = (E + 1023) / 1024;
+  const int b0 = threadIdx.x * per;
+  int32_t s = 0;
+  for (int e = b0; e < b0 + per && e < E; ++e) s += (seg[e + 1] - seg[e] + tile_m - 1) / tile_m;
+  part[threadIdx.x] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t run = 0;
+    for (int i = 0; i < 1024; ++i) {
+      const int32_t v = part[i];
+      part[i] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  int32_t run = part[threadIdx.x];
+  for (int e = b0; e < b0 + per && e < E; ++e) {
+    toff[e] = run;
+    run += (seg[e + 1] - seg[e] + tile_m - 1) / tile_m;
+  }
+  if (threadIdx.x == 1023) toff[E] = run;  // blocks past E add nothing: this is the total
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void moe_rows(const uint32_t* __restrict__ vals, int64_t n, int k,
+                                                const T* __restrict__ w, int32_t* __restrict__ rows,
+                                                T* __restrict__ wsorted, int32_t* __restrict__ inv) {
+  for (int64_t r = blockIdx.x * 256ll + threadIdx.x; r < n; r += (int64_t)gridDim.x * 256) {
+    const uint32_t a = vals[r];
+    rows[r] = (int32_t)(a / (uint32_t)k);
+    wsorted[r] = w[a];
+    inv[a] = (int32_t)r;
+  }
+}
+
+// One workgroup per token; each thread owns 8 consecutive columns.
+template <typename T, int KMAX>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const T* __restrict__ Y, int64_t ldy,
+                                                          const int32_t* __restrict__ inv,
+                                                          const int64_t* __restrict__ sel, int k, int64_t E,
+                                                          T* __restrict__ out, int64_t H) {
+  const int64_t t = blockIdx.x;
+  int64_t ek[KMAX];
+  int32_t pk[KMAX];
+  int nk = 0;
+  for (int j = 0; j < k; ++j) {  // insertion by expert id (ids of one token are distinct)
+    const int64_t e = sel[t * k + j];
+    if (e < 0 || e >= E) continue;
+    const int32_t p = inv[t * k + j];
+    int q = nk++;
+    while (q > 0 && ek[q - 1] > e) {
+      ek[q] = ek[q - 1];
+      pk[q] = pk[q - 1];
+      --q;
+    }
+    ek[q] = e;
+    pk[q] = p;
+  }
+  for (int64_t c = threadIdx.x * 8; c < H; c += 256 * 8) {
+    Vec16<T> acc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc.v[e] = (T)0.f;
+    for (int j = 0; j < nk; ++j) {
+      const Vec16<T> y = ld16(Y + (int64_t)pk[j] * ldy + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc.v[e] = from_f32<T>(to_f32(acc.v[e]) + to_f32(y.v[e]));
+    }
+    st16(out + t * H + c, acc);
+  }
+}
+
+}  // namespace
+
+extern "C" int64_t qh_moe_dispatch_workspace(int64_t n_tokens, int64_t top_k, int64_t n_experts) {
+  const int64_t n = n_tokens * top_k;
+  if (n <= 0 || n_experts <= 0) return 0;
+  return 4 * align256(n * 4) + align256((int64_t)sort_temp_bytes(n, key_bits(n_experts)));
+}
+
+extern "C" int qh_moe_dispatch(const int64_t* selected, const void* weights, int64_t n_tokens, int64_t top_k,
+                               int64_t n_experts, int64_t tile_m, void* ws, int64_t ws_bytes, int32_t* rows,
+                               void* wsorted, int32_t* inv, int32_t* seg_off, int32_t* tile_off, int dtype,
+                               void* stream) {
+  QH_CHECK_ARG(n_tokens >= 0 && top_k > 0 && n_experts > 0 && n_experts <= 65536 && tile_m > 0,
+               "qh_moe_dispatch: bad shape");
+  const int64_t n = n_tokens * top_k;
+  QH_CHECK_ARG(n < (1ll << 31), "qh_moe_dispatch: too many assignments");
+  QH_CHECK_ARG(dtype >= QH_F32 && dtype <= QH_BF16, "qh_moe_dispatch: bad dtype");
+  const int64_t need = qh_moe_dispatch_workspace(n_tokens, top_k, n_experts);
+  if (ws_bytes < need) {
+    qh::set_error("qh_moe_dispatch: workspace %lld < %lld", (long long)ws_bytes, (long long)need);
+    return QH_E_WORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const int E = (int)n_experts;
+  if (n == 0) {
+    int rc = qh_zero(seg_off, (E + 1) * 4, stream);
+    return rc ? rc : qh_zero(tile_off, (E + 1) * 4, stream);
+  }
+  char* p = (char*)ws;
+  uint32_t* keys_in = (uint32_t*)p; p += align256(n * 4);
+  uint32_t* keys_out = (uint32_t*)p; p += align256(n * 4);
+  uint32_t* vals_in = (uint32_t*)p; p += align256(n * 4);
+  uint32_t* vals_out = (uint32_t*)p; p += align256(n * 4);
+  const int bits = key_bits(n_experts);
+  size_t temp = sort_temp_bytes(n, bits);
+  const unsigned g = (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  moe_keys<<<g, 256, 0, st>>>(selected, n, n_experts, keys_in, vals_in);
+  if (rocprim::radix_sort_pairs((void*)p, temp, keys_in, keys_out, vals_in, vals_out, (unsigned)n, 0, bits, st) !=
+      hipSuccess) {
+    qh::set_error("qh_moe_dispatch: radix sort failed");
+    return QH_E_HIP;
+  }
+  moe_segments<<<(E + 1 + 255) / 256, 256, 0, st>>>(keys_out, n, E, seg_off);
+  moe_tile_offsets<<<1, 1024, 0, st>>>(seg_off, E, (int)tile_m, tile_off);
+#define QH_ROWS(T) moe_rows<T><<<g, 256, 0, st>>>(vals_out, n, (int)top_k, (const T*)weights, rows, (T*)wsorted, inv)
+  if (dtype == QH_BF16) QH_ROWS(bf16_t); else if (dtype == QH_F16) QH_ROWS(f16_t); else QH_ROWS(float);
+#undef QH_ROWS
+  QH_CHECK_LAUNCH("qh_moe_dispatch");
+  return QH_OK;
+}
+
+extern "C" int qh_moe_combine(const void* Y, int64_t ldy, const int32_t* inv, const int64_t* selected,
+                              int64_t n_tokens, int64_t top_k, int64_t n_experts, void* out, int64_t H, int dtype,
+                              void* stream) {
+  QH_CHECK_ARG(n_tokens >= 0 && top_k > 0 && top_k <= 32 && H > 0 && n_experts > 0, "qh_moe_combine: bad shape");
+  QH_CHECK_ARG(H % 8 == 0 && ldy % 8 == 0 && aligned16(Y) && aligned16(out),
+               "qh_moe_combine: rows must be 16-byte aligned with H, ldy multiples of 8");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_combine: bf16/f16 only");
+  QH_CHECK_ARG(n_tokens < (1ll << 31), "qh_moe_combine: too many tokens");
+  if (n_tokens == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+#define QH_COMB(T, KM) \
+  moe_combine_kernel<T, KM><<<(unsigned)n_tokens, 256, 0, st>>>((const T*)Y, ldy, inv, selected, (int)top_k, n_experts, (T*)out, H)
+  if (dtype == QH_BF16) {
+    if (top_k <= 8) QH_COMB(bf16_t, 8); else QH_COMB(bf16_t, 32);
+  } else {
+    if (top_k <= 8) QH_COMB(f16_t, 8); else QH_COMB(f16_t, 32);
+  }
+#undef QH_COMB
+  QH_CHECK_LAUNCH("qh_moe_combine");
+  return QH_OK;
+}

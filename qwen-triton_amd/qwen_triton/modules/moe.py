@@ -6,13 +6,19 @@ reference's routing semantics: fp32 softmax over router logits, top-k with ties
 to the lower expert index, optional renormalisation, routing weights cast to the
 activation dtype, per-expert SwiGLU on the tokens routed to it, scaled by the
 routing weight and scatter-added in ascending expert order.
+
+On the GPU without autograd the experts run as one sort/segment dispatch, two
+grouped expert GEMMs and an ordered combine (``kernels/moe_experts.py``), with
+the same rounding points as the loop.
 """
 from __future__ import annotations
 
 import torch
 from torch import nn
 
+from qwen_triton import _native
 from qwen_triton.configs import QwenTritonConfig
+from qwen_triton.kernels.moe_experts import moe_experts_forward
 from qwen_triton.kernels.moe_routing import triton_index_add, triton_one_hot, triton_topk
 from qwen_triton.kernels.sigmoid_mul import sigmoid_mul
 from qwen_triton.kernels.softmax import triton_softmax
@@ -31,6 +37,8 @@ class QwenSparseMoeBlock(nn.Module):
         self.experts = nn.ModuleList(
             [QwenMLP(config.hidden_size, config.moe_intermediate_size) for _ in range(config.num_experts)]
         )
+        self.moe_intermediate_size = config.moe_intermediate_size
+        self._tables: tuple | None = None  # device pointer tables of the expert weights (not state)
         self.shared_expert = None
         self.shared_expert_gate = None
         if config.shared_expert_intermediate_size > 0:
@@ -56,7 +64,38 @@ class QwenSparseMoeBlock(nn.Module):
             out = out + sigmoid_mul(shared, gate_value.expand_as(shared))
         return out.view(batch, seq, hidden), router_logits
 
+    def _grouped_ok(self, flat: torch.Tensor) -> bool:
+        if torch.is_grad_enabled() or not flat.is_cuda or flat.dtype not in (torch.bfloat16, torch.float16):
+            return False
+        if flat.shape[1] % 8 or self.moe_intermediate_size % 8 or not _native.available():
+            return False
+        ws = [(e.gate_proj.weight, e.up_proj.weight, e.down_proj.weight) for e in self.experts]
+        g0, d0 = ws[0][0], ws[0][2]
+        return all(
+            e.gate_proj.bias is None and e.up_proj.bias is None and e.down_proj.bias is None for e in self.experts
+        ) and all(
+            g.dtype == flat.dtype and u.dtype == flat.dtype and d.dtype == flat.dtype and g.is_cuda
+            and g.stride() == g0.stride() and u.stride() == g0.stride() and d.stride() == d0.stride()
+            and g.stride(1) == 1 and d.stride(1) == 1 and g.stride(0) % 8 == 0 and d.stride(0) % 8 == 0
+            and g.data_ptr() % 16 == 0 and u.data_ptr() % 16 == 0 and d.data_ptr() % 16 == 0
+            for g, u, d in ws)
+
+    def _expert_tables(self, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+        ptrs = [(e.gate_proj.weight.data_ptr(), e.up_proj.weight.data_ptr(), e.down_proj.weight.data_ptr())
+                for e in self.experts]
+        key = (device, tuple(ptrs))
+        if self._tables is None or self._tables[0] != key:
+            gu = torch.tensor([p for g, u, _ in ptrs for p in (g, u)], dtype=torch.int64, device=device)
+            dn = torch.tensor([d for _, _, d in ptrs], dtype=torch.int64, device=device)
+            self._tables = (key, gu, dn)
+        return self._tables[1], self._tables[2]
+
     def experts_forward(self, flat: torch.Tensor, routing_weights: torch.Tensor, selected: torch.Tensor) -> torch.Tensor:
+        if self._grouped_ok(flat):
+            gu, dn = self._expert_tables(flat.device)
+            strides = (self.experts[0].gate_proj.weight.stride(0), self.experts[0].down_proj.weight.stride(0))
+            return moe_experts_forward(flat, routing_weights, selected, gu, dn, self.num_experts,
+                                       self.moe_intermediate_size, strides)
         out = torch.zeros_like(flat)
         expert_mask = triton_one_hot(selected, self.num_experts).permute(2, 1, 0)
         hit = torch.nonzero(expert_mask.sum(dim=(-1, -2)) > 0, as_tuple=False).view(-1)

@@ -484,3 +484,74 @@ def test_add_rmsnorm_matches_add_then_rmsnorm(rows, cols):
         y_ref = K.rmsnorm(s_ref, w, eps=1e-6)
     assert torch.equal(s, s_ref) and torch.equal(y, y_ref)
     close(y, O.rmsnorm(x.double() + r.double(), w, 1e-6), atol=3e-2, rtol=3e-2)
+
+
+# ---------------------------------------------------------------------------
+# MoE experts: dispatch, grouped GEMM, combine
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("T,k,E", [(300, 8, 128), (64, 2, 7), (5, 1, 16)])
+def test_moe_dispatch_segments_are_a_stable_sort(T, k, E):
+    from qwen_triton import _native
+
+    logits = randn(T, E, seed=250)
+    sel = torch.topk(logits, k, dim=-1).indices
+    w = torch.rand(T, k, generator=_gen(251)).to(DEV, torch.bfloat16)
+    R = T * k
+    ws = _native.workspace(_native.call("qh_moe_dispatch_workspace", T, k, E), torch.device(DEV))
+    rows = torch.empty(R, dtype=torch.int32, device=DEV)
+    wsorted = torch.empty(R, dtype=torch.bfloat16, device=DEV)
+    inv = torch.empty(R, dtype=torch.int32, device=DEV)
+    seg = torch.empty(E + 1, dtype=torch.int32, device=DEV)
+    toff = torch.empty(E + 1, dtype=torch.int32, device=DEV)
+    _native.call("qh_moe_dispatch", sel.data_ptr(), w.data_ptr(), T, k, E, 128, ws.data_ptr(), ws.numel(),
+                 rows.data_ptr(), wsorted.data_ptr(), inv.data_ptr(), seg.data_ptr(), toff.data_ptr(), _native.BF16,
+                 _native.stream(torch.device(DEV)))
+    sel_c, w_c = sel.cpu().reshape(-1), w.cpu().reshape(-1)
+    counts = torch.bincount(sel_c, minlength=E)
+    assert torch.equal(seg.cpu().long(), torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]))
+    tiles = (counts + 127) // 128
+    assert torch.equal(toff.cpu().long(), torch.cat([torch.zeros(1, dtype=torch.long), tiles.cumsum(0)]))
+    order = torch.argsort(sel_c, stable=True)  # expert-major, (token, slot) order inside an expert
+    assert torch.equal(rows.cpu().long(), order // k)
+    assert torch.equal(wsorted.cpu(), w_c[order])
+    assert torch.equal(inv.cpu().long()[order], torch.arange(R))
+
+
+def _moe_block(E, k, hidden=256, inter=128, seed=0):
+    from qwen_triton import QwenTritonConfig
+    from qwen_triton.modules import QwenSparseMoeBlock
+
+    cfg = QwenTritonConfig.from_hf_config(dict(
+        model_type="qwen3_moe", vocab_size=64, hidden_size=hidden, intermediate_size=512, num_hidden_layers=1,
+        num_attention_heads=4, num_key_value_heads=2, head_dim=64, moe_intermediate_size=inter, num_experts=E,
+        num_experts_per_tok=k, norm_topk_prob=True, decoder_sparse_step=1, mlp_only_layers=[]))
+    torch.manual_seed(seed)
+    blk = QwenSparseMoeBlock(cfg)
+    with torch.no_grad():
+        for p in blk.parameters():
+            p.normal_(0.0, 0.05)
+    return blk.to(DEV, torch.bfloat16)
+
+
+@pytest.mark.parametrize("E,k,T", [(16, 4, 200), (32, 8, 300), (8, 1, 33)])
+def test_moe_grouped_experts_match_loop(E, k, T):
+    blk = _moe_block(E, k, seed=E)
+    x = randn(T, 256, dtype=torch.bfloat16, seed=260)
+    logits = randn(T, E, seed=261) * 2
+    # route away from the last two experts: segments of zero rows
+    logits[:, -2:] = -30.0
+    w, sel = blk.route(logits, torch.bfloat16)
+    c0 = native_calls("qh_moe_gemm")
+    with torch.no_grad():
+        fused = blk.experts_forward(x, w, sel)
+        again = blk.experts_forward(x, w, sel)
+    assert native_calls("qh_moe_gemm") == c0 + 4
+    assert torch.equal(fused, again)
+    with torch.enable_grad():  # the reference per-expert loop
+        loop = blk.experts_forward(x, w, sel).detach()
+    close(fused, loop, atol=2e-2, rtol=2e-2)
+    wg = torch.stack([ex.gate_proj.weight for ex in blk.experts]).float().cpu()
+    wu = torch.stack([ex.up_proj.weight for ex in blk.experts]).float().cpu()
+    wd = torch.stack([ex.down_proj.weight for ex in blk.experts]).float().cpu()
+    ref, *_ = O.moe_block(x, None, wg, wu, wd, k, True, router_logits=logits)
+    close(fused, ref, atol=3e-2, rtol=3e-2)
