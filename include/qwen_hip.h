@@ -246,6 +246,8 @@ int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const voi
                  int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o,
                  float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
                  float scale, int causal, int64_t causal_offset, int dtype, void* stream);
+/* Workspace bytes of qh_flash_bwd: Delta = rowsum(O dO) and the LSE in log2 units,
+ * per (b, q-head) in rows of Sq rounded up to 64 plus one 64-query tile. */
 int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq);
 /* dq [B,Hq,Sq,D], dk/dv [B,Hkv,Sk,D] (contiguous, fully written) from o and
  * dout (contiguous [B,Hq,Sq,D]) and the forward's lse. Deterministic: a dK/dV

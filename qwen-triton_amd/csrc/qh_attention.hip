@@ -379,14 +379,23 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
 // ===========================================================================
 // Backward
 // ===========================================================================
+// Per query row: Delta = rowsum(O * dO) and the saved LSE in log2 units, in
+// rows of sqp >= Sq + 64 floats per (b, q-head) whose tail is zero, so that
+// the backward kernels read whole 64-query tiles (as float4) without bounds
+// checks. 16 lanes per row, 8 elements per lane per step.
 template <typename T>
-__global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const T* __restrict__ O, const T* __restrict__ dO,
-                                                           float* __restrict__ delta, int64_t rows, int D) {
-  // 16 lanes per row, 8 elements per lane per step.
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+__global__ __launch_bounds__(256) void fa_bwd_prep_kernel(const T* __restrict__ O, const T* __restrict__ dO,
+                                                          const float* __restrict__ LSE, float* __restrict__ delta,
+                                                          float* __restrict__ lse2, int64_t padded_rows, int Sq,
+                                                          int64_t sqp, int D) {
+  const int64_t prow = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int li = threadIdx.x & 15;
+  const int64_t bh = prow / sqp;
+  const int q = (int)(prow - bh * sqp);
+  const bool real = prow < padded_rows && q < Sq;
+  const int64_t row = bh * Sq + q;
   float s = 0.f;
-  if (row < rows) {
+  if (real) {
     for (int d = li * 8; d < D; d += 128) {
       Vec16<T> a = ld16(O + row * D + d), b = ld16(dO + row * D + d);
 #pragma unroll
@@ -394,25 +403,93 @@ __global__ __launch_bounds__(256) void fa_bwd_delta_kernel(const T* __restrict__
     }
   }
   s = wave_sum(s, 16);
-  if (row < rows && li == 0) delta[row] = s;
+  if (prow < padded_rows && li == 0) {
+    delta[prow] = s;
+    lse2[prow] = real ? LSE[row] * kLog2e : 0.f;
+  }
 }
 
-// dK, dV for 128 keys (4 wavefronts x 32 keys) of one (b, kv-head).
+// dK, dV for 128 keys (4 wavefronts x 32 keys) of one (b, kv-head). The
+// wave's K and V fragments stay in registers (B operands); Q and dO tiles of
+// 64 queries stream through double-buffered swizzled LDS (direct-to-LDS
+// loads), over every q-head of the group and every visible q-tile. Per 32
+// queries:
+//   S = Q K^T, dP = dO V^T           (C layout: column = key, rows = queries)
+//   P = exp2(S scale_log2 - lse2), dS = P (dP - Delta)
+//   dV^T += dO^T P, dK^T += Q^T dS   (A operands read transposed from the
+//                                     row-major Q / dO tiles; P and dS are the
+//                                     B operands straight from the C layout)
+template <typename T, int DP, bool MASK>
+__device__ __forceinline__ void fa_bwd_dkdv_tile(const T* Qt, const T* Ot, const typename Mfma<T>::v8 (&kf)[DP / 16],
+                                                 const typename Mfma<T>::v8 (&vf)[DP / 16], f32x16 (&dk)[DP / 32],
+                                                 f32x16 (&dv)[DP / 32], const float* __restrict__ lse_row,
+                                                 const float* __restrict__ dl_row, int q0, int kj, int Sq, int Sk,
+                                                 int causal, int coff, float scale_log2, int lane) {
+  constexpr int CPR = DP / 8, DT = DP / 32, KD = DP / 16;
+  typedef typename Mfma<T>::v8 v8;
+  const int ql = lane & 31, hf = lane >> 5;
+  const int grp = lane >> 4, j = lane & 15;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    // lse (log2 units) and Delta of this lane's 16 queries q0 + qt*32 + 8 g + 4 hf + r
+    float4 ls[4], dl[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int il = qt * 32 + g * 8 + hf * 4;
+      ls[g] = *reinterpret_cast<const float4*>(lse_row + il);
+      dl[g] = *reinterpret_cast<const float4*>(dl_row + il);
+    }
+    f32x16 sc = zero16(), dp = zero16();
+    const int row = qt * 32 + ql;
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      const int c = swz(row, kd * 2 + hf, CPR);
+      sc = Mfma<T>::mma(load_frag16<T>(Qt + row * DP + c * 8), kf[kd], sc);
+      dp = Mfma<T>::mma(load_frag16<T>(Ot + row * DP + c * 8), vf[kd], dp);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float lv[4] = {ls[g].x, ls[g].y, ls[g].z, ls[g].w};
+      const float dv4[4] = {dl[g].x, dl[g].y, dl[g].z, dl[g].w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float p = exp2_(__builtin_fmaf(sc[g * 4 + r], scale_log2, -lv[r]));
+        if constexpr (MASK) {
+          const int qi = q0 + qt * 32 + g * 8 + hf * 4 + r;
+          const bool ok = qi < Sq && kj < Sk && !(causal && kj > qi + coff);
+          p = ok ? p : 0.f;
+        }
+        sc[g * 4 + r] = p;
+        dp[g * 4 + r] = p * (dp[g * 4 + r] - dv4[r]);
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const v8 pf = pack_pair<T>(sc, ks * 2);
+      const v8 df = pack_pair<T>(dp, ks * 2);
+      const int qrow = qt * 32 + ks * 16 + 4 * (grp >> 1) + (j >> 2);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = dt * 32 + 16 * (grp & 1) + 4 * (j & 3);
+        dv[dt] = Mfma<T>::mma(read_vt_frag<T, DP>(Ot, qrow, d), pf, dv[dt]);
+        dk[dt] = Mfma<T>::mma(read_vt_frag<T, DP>(Qt, qrow, d), df, dk[dt]);
+      }
+    }
+  }
+}
+
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
     const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs, const T* __restrict__ K, int64_t skb, int64_t skh,
     int64_t sks, const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs, const T* __restrict__ dO,
-    const float* __restrict__ LSE, const float* __restrict__ Delta, T* __restrict__ dK, T* __restrict__ dV, int Hq,
-    int Hkv, int groups, int Sq, int Sk, int D, float scale_log2, float scale, int causal, int coff) {
+    const float* __restrict__ LSE2, const float* __restrict__ Delta, int64_t sqp, T* __restrict__ dK,
+    T* __restrict__ dV, int Hq, int Hkv, int groups, int Sq, int Sk, int D, float scale_log2, float scale, int causal,
+    int coff) {
   constexpr int BQ = 64;
-  constexpr int KLD = DP + 8, TLD = BQ + 8;
   constexpr int DT = DP / 32, KD = DP / 16;
   typedef typename Mfma<T>::v8 v8;
-  __shared__ __attribute__((aligned(16))) T Qs[BQ * KLD];
-  __shared__ __attribute__((aligned(16))) T dOs[BQ * KLD];
-  __shared__ __attribute__((aligned(16))) T Qt[DP * TLD];
-  __shared__ __attribute__((aligned(16))) T dOt[DP * TLD];
-  __shared__ float lse_s[BQ], dl_s[BQ];
+  __shared__ __attribute__((aligned(1024))) T Qs[2][BQ * DP];
+  __shared__ __attribute__((aligned(1024))) T Os[2][BQ * DP];
 
   const int bk = blockIdx.y;
   const int b = bk / Hkv, hk = bk % Hkv;
@@ -420,6 +497,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int ql = lane & 31, hf = lane >> 5;
   const int kj = k0 + wid * 32 + ql;  // this lane's key (C-layout column)
+  const int kw0 = k0 + wid * 32;      // first key of this wave
   const T* Kb = K + b * skb + hk * skh;
   const T* Vb = V + b * svb + hk * svh;
 
@@ -439,63 +517,40 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dk[dt] = dv[dt] = zero16();
 
+  // visible q-tiles: queries q with q + coff >= k0 (causal), all otherwise
   int q_start = 0;
   if (causal) {
     q_start = k0 - coff;
     if (q_start < 0) q_start = 0;
     q_start = (q_start / BQ) * BQ;
   }
-  for (int g = 0; g < groups; ++g) {
+  const int nqt = q_start < Sq ? (Sq - q_start + BQ - 1) / BQ : 0;
+  const int ntiles = groups * nqt;
+  const TileLoader<T, BQ, DP> qload(sqs, D), oload(D, D);
+  auto issue = [&](int it, int buf) {
+    const int g = it / nqt, q0 = q_start + (it % nqt) * BQ;
     const int hq = hk * groups + g;
-    const int64_t bh = (int64_t)b * Hq + hq;
-    const T* Qb = Q + b * sqb + hq * sqh;
-    const T* dOb = dO + bh * Sq * D;
-    for (int q0 = q_start; q0 < Sq; q0 += BQ) {
-      __syncthreads();
-      stage_rows<T, BQ, DP, KLD>(Qs, Qb, sqs, q0, Sq, D);
-      stage_rows<T, BQ, DP, KLD>(dOs, dOb, D, q0, Sq, D);
-      stage_rows_t<T, BQ, DP, TLD>(Qt, Qb, sqs, q0, Sq, D);
-      stage_rows_t<T, BQ, DP, TLD>(dOt, dOb, D, q0, Sq, D);
-      if (threadIdx.x < BQ) {
-        const int qi = q0 + threadIdx.x;
-        lse_s[threadIdx.x] = qi < Sq ? LSE[bh * Sq + qi] * kLog2e : 0.f;
-        dl_s[threadIdx.x] = qi < Sq ? Delta[bh * Sq + qi] : 0.f;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int kd = 0; kd < KD; ++kd) {
-          const int off = (qt * 32 + ql) * KLD + kd * 16 + hf * 8;
-          s = Mfma<T>::mma(load_frag16<T>(Qs + off), kf[kd], s);
-          dp = Mfma<T>::mma(load_frag16<T>(dOs + off), vf[kd], dp);
-        }
-        // C layout: column = key kj, row = query q0 + qt*32 + 8g + 4hf + r
-#pragma unroll
-        for (int gg = 0; gg < 4; ++gg)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int il = qt * 32 + gg * 8 + hf * 4 + r;
-            const int qi = q0 + il;
-            const bool ok = qi < Sq && kj < Sk && !(causal && kj > qi + coff);
-            const float p = ok ? exp2_(s[gg * 4 + r] * scale_log2 - lse_s[il]) : 0.f;
-            s[gg * 4 + r] = p;
-            dp[gg * 4 + r] = p * (dp[gg * 4 + r] - dl_s[il]);
-          }
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const v8 pf = pack_pair<T>(s, ks * 2);
-          const v8 df = pack_pair<T>(dp, ks * 2);
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const int off = (dt * 32 + ql) * TLD + qt * 32 + ks * 16 + hf * 4;
-            dv[dt] = Mfma<T>::mma(load_frag_split<T>(dOt + off, dOt + off + 8), pf, dv[dt]);
-            dk[dt] = Mfma<T>::mma(load_frag_split<T>(Qt + off, Qt + off + 8), df, dk[dt]);
-          }
-        }
-      }
-    }
+    qload.load(Qs[buf], Q + b * sqb + hq * sqh, sqs, q0, Sq);
+    oload.load(Os[buf], dO + ((int64_t)b * Hq + hq) * Sq * D, D, q0, Sq);
+  };
+  if (ntiles > 0) issue(0, 0);
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile `it` have landed
+    __syncthreads();                // ... and everyone else's; tile it-1 is fully consumed
+    if (it + 1 < ntiles) issue(it + 1, buf ^ 1);
+    const int g = it / nqt, q0 = q_start + (it % nqt) * BQ;
+    const int64_t bh = (int64_t)b * Hq + hk * groups + g;
+    // wave-uniform: does any (query, key) pair of the tile need masking?
+    const bool need_mask = (q0 + BQ > Sq) || (kw0 + 32 > Sk) || (causal && kw0 + 31 > q0 + coff);
+    const float* lse_row = LSE2 + bh * sqp + q0;
+    const float* dl_row = Delta + bh * sqp + q0;
+    if (need_mask)
+      fa_bwd_dkdv_tile<T, DP, true>(Qs[buf], Os[buf], kf, vf, dk, dv, lse_row, dl_row, q0, kj, Sq, Sk, causal, coff,
+                                    scale_log2, lane);
+    else
+      fa_bwd_dkdv_tile<T, DP, false>(Qs[buf], Os[buf], kf, vf, dk, dv, lse_row, dl_row, q0, kj, Sq, Sk, causal,
+                                     coff, scale_log2, lane);
   }
   if (kj < Sk) {
     T* dKr = dK + ((int64_t)bk * Sk + kj) * D;
@@ -519,28 +574,74 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
   }
 }
 
-// dQ for 128 queries (4 wavefronts x 32 queries) of one (b, q-head).
+// dQ for 128 queries (4 wavefronts x 32 queries) of one (b, q-head): the
+// forward kernel's structure with dP computed beside S. K and V tiles of 64
+// keys stream through double-buffered swizzled LDS; per tile
+//   S^T = K Q^T, dP^T = V dO^T      (C layout: column = query, rows = keys)
+//   dS^T = P^T (dP^T - Delta)
+//   dQ^T += K^T dS^T                (K^T read transposed from the K tile)
+template <typename T, int DP, bool MASK>
+__device__ __forceinline__ void fa_bwd_dq_tile(const T* Kt, const T* Vt, const typename Mfma<T>::v8 (&qf)[DP / 16],
+                                               const typename Mfma<T>::v8 (&of)[DP / 16], f32x16 (&dq)[DP / 32],
+                                               float lse2, float dl, int kv0, int lim, float scale_log2, int lane) {
+  constexpr int CPR = DP / 8, DT = DP / 32, KD = DP / 16;
+  typedef typename Mfma<T>::v8 v8;
+  const int ql = lane & 31, hf = lane >> 5;
+  const int grp = lane >> 4, j = lane & 15;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    f32x16 sc = zero16(), dp = zero16();
+    const int row = kt * 32 + ql;
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      const int c = swz(row, kd * 2 + hf, CPR);
+      sc = Mfma<T>::mma(load_frag16<T>(Kt + row * DP + c * 8), qf[kd], sc);
+      dp = Mfma<T>::mma(load_frag16<T>(Vt + row * DP + c * 8), of[kd], dp);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float p = exp2_(__builtin_fmaf(sc[g * 4 + r], scale_log2, -lse2));
+        if constexpr (MASK) {
+          const int key = kv0 + kt * 32 + g * 8 + hf * 4 + r;
+          p = key > lim ? 0.f : p;
+        }
+        dp[g * 4 + r] = p * (dp[g * 4 + r] - dl);
+      }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const v8 df = pack_pair<T>(dp, ks * 2);
+      const int krow = kt * 32 + ks * 16 + 4 * (grp >> 1) + (j >> 2);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = dt * 32 + 16 * (grp & 1) + 4 * (j & 3);
+        dq[dt] = Mfma<T>::mma(read_vt_frag<T, DP>(Kt, krow, d), df, dq[dt]);
+      }
+    }
+  }
+}
+
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
     const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs, const T* __restrict__ K, int64_t skb, int64_t skh,
     int64_t sks, const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs, const T* __restrict__ dO,
-    const float* __restrict__ LSE, const float* __restrict__ Delta, T* __restrict__ dQ, int Hq, int groups, int Sq,
-    int Sk, int D, float scale_log2, float scale, int causal, int coff) {
-  constexpr int BN = 64;
-  constexpr int KLD = DP + 8, TLD = BN + 8;
+    const float* __restrict__ LSE2, const float* __restrict__ Delta, int64_t sqp, T* __restrict__ dQ, int Hq,
+    int groups, int Sq, int Sk, int D, float scale_log2, float scale, int causal, int coff) {
+  constexpr int BN = 64, BMQ = 128;
   constexpr int DT = DP / 32, KD = DP / 16;
   typedef typename Mfma<T>::v8 v8;
-  __shared__ __attribute__((aligned(16))) T Ks[BN * KLD];
-  __shared__ __attribute__((aligned(16))) T Vs[BN * KLD];
-  __shared__ __attribute__((aligned(16))) T Kt[DP * TLD];
+  __shared__ __attribute__((aligned(1024))) T Ks[2][BN * DP];
+  __shared__ __attribute__((aligned(1024))) T Vs[2][BN * DP];
 
-  const int nqb = (Sq + 127) / 128;
+  const int nqb = (Sq + BMQ - 1) / BMQ;
   const int qb = nqb - 1 - (int)blockIdx.x;
   const int64_t bh = blockIdx.y;
   const int b = (int)(bh / Hq), hq = (int)(bh % Hq), hk = hq / groups;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int ql = lane & 31, hf = lane >> 5;
-  const int qi = qb * 128 + wid * 32 + ql;
+  const int qw0 = qb * BMQ + wid * 32;
+  const int qi = qw0 + ql;
   const T* Qb = Q + b * sqb + hq * sqh;
   const T* Kb = K + b * skb + hk * skh;
   const T* Vb = V + b * svb + hk * svh;
@@ -558,49 +659,37 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
       for (int e = 0; e < 8; ++e) qf[kd][e] = of[kd][e] = (T)0.f;
     }
   }
-  const float lse2 = qi < Sq ? LSE[bh * Sq + qi] * kLog2e : 0.f;
-  const float dl = qi < Sq ? Delta[bh * Sq + qi] : 0.f;
+  // queries past Sq read the zero tail of the padded lse / Delta rows
+  const float lse2 = LSE2[bh * sqp + (qi < Sq ? qi : Sq)];
+  const float dl = Delta[bh * sqp + (qi < Sq ? qi : Sq)];
   f32x16 dq[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dq[dt] = zero16();
 
   int kv_end = Sk;
-  if (causal) kv_end = min(Sk, qb * 128 + 128 + coff);
-  for (int kv0 = 0; kv0 < kv_end; kv0 += BN) {
+  if (causal) kv_end = min(Sk, qb * BMQ + BMQ + coff);
+  const int ntiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
+  // last key visible to this lane's query (causal and/or Sk bound); none for padding lanes
+  const int lim = qi < Sq ? (causal ? min(Sk - 1, qi + coff) : Sk - 1) : -1;
+  const TileLoader<T, BN, DP> kload(sks, D), vload(svs, D);
+  if (ntiles > 0) {
+    kload.load(Ks[0], Kb, sks, 0, Sk);
+    vload.load(Vs[0], Vb, svs, 0, Sk);
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    const int kv0 = it * BN;
+    const int buf = it & 1;
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    stage_rows<T, BN, DP, KLD>(Ks, Kb, sks, kv0, Sk, D);
-    stage_rows<T, BN, DP, KLD>(Vs, Vb, svs, kv0, Sk, D);
-    stage_rows_t<T, BN, DP, TLD>(Kt, Kb, sks, kv0, Sk, D);
-    __syncthreads();
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int kd = 0; kd < KD; ++kd) {
-        const int off = (kt * 32 + ql) * KLD + kd * 16 + hf * 8;
-        s = Mfma<T>::mma(load_frag16<T>(Ks + off), qf[kd], s);
-        dp = Mfma<T>::mma(load_frag16<T>(Vs + off), of[kd], dp);
-      }
-      // C layout: column = query qi, row = key kv0 + kt*32 + 8g + 4hf + r
-#pragma unroll
-      for (int gg = 0; gg < 4; ++gg)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kv0 + kt * 32 + gg * 8 + hf * 4 + r;
-          const bool ok = qi < Sq && key < Sk && !(causal && key > qi + coff);
-          const float p = ok ? exp2_(s[gg * 4 + r] * scale_log2 - lse2) : 0.f;
-          dp[gg * 4 + r] = p * (dp[gg * 4 + r] - dl);
-        }
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const v8 df = pack_pair<T>(dp, ks * 2);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const int off = (dt * 32 + ql) * TLD + kt * 32 + ks * 16 + hf * 4;
-          dq[dt] = Mfma<T>::mma(load_frag_split<T>(Kt + off, Kt + off + 8), df, dq[dt]);
-        }
-      }
+    if (it + 1 < ntiles) {
+      kload.load(Ks[buf ^ 1], Kb, sks, kv0 + BN, Sk);
+      vload.load(Vs[buf ^ 1], Vb, svs, kv0 + BN, Sk);
     }
+    const bool need_mask = (kv0 + BN > Sk) || (qw0 + 32 > Sq) || (causal && kv0 + BN - 1 > qw0 + coff);
+    if (need_mask)
+      fa_bwd_dq_tile<T, DP, true>(Ks[buf], Vs[buf], qf, of, dq, lse2, dl, kv0, lim, scale_log2, lane);
+    else
+      fa_bwd_dq_tile<T, DP, false>(Ks[buf], Vs[buf], qf, of, dq, lse2, dl, kv0, lim, scale_log2, lane);
   }
   if (qi < Sq) {
     T* dQr = dQ + (bh * Sq + qi) * D;
@@ -895,7 +984,12 @@ extern "C" int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
   return QH_OK;
 }
 
-extern "C" int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq) { return B * Hq * Sq * 4; }
+// Padded row length of the per-query Delta / LSE2 arrays of the backward.
+static int64_t bwd_row_pad(int64_t Sq) { return (Sq + 63) / 64 * 64 + 64; }
+
+extern "C" int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq) {
+  return 2 * B * Hq * bwd_row_pad(Sq) * 4;
+}
 
 extern "C" int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
                             int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs,
@@ -926,23 +1020,27 @@ extern "C" int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
     if (rc) return rc;
     return qh_zero(dv, B * Hkv * Sk * D * esz, stream);
   }
+  const int64_t sqp = bwd_row_pad(Sq);
+  const int64_t prow = B * Hq * sqp;
   float* delta = (float*)ws;
-  const int64_t rows = B * Hq * Sq;
+  float* lse2 = delta + prow;
   const float sl2 = scale * kLog2e;
   const int groups = (int)(Hq / Hkv);
   dim3 gkv((unsigned)ceil_div(Sk, 128), (unsigned)(B * Hkv));
   dim3 gq((unsigned)ceil_div(Sq, 128), (unsigned)(B * Hq));
 #define QH_BWD(T, DPV)                                                                                              \
   do {                                                                                                              \
-    fa_bwd_delta_kernel<T><<<(unsigned)ceil_div(rows, 16), 256, 0, st>>>((const T*)o, (const T*)dout, delta, rows,  \
-                                                                         (int)D);                                   \
+    fa_bwd_prep_kernel<T><<<(unsigned)ceil_div(prow, 16), 256, 0, st>>>((const T*)o, (const T*)dout, lse, delta,   \
+                                                                        lse2, prow, (int)Sq, sqp, (int)D);          \
     if (Sk > 0)                                                                                                     \
       fa_bwd_dkdv_kernel<T, DPV><<<gkv, 256, 0, st>>>((const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks,       \
-                                                      (const T*)v, svb, svh, svs, (const T*)dout, lse, delta, (T*)dk, \
+                                                      (const T*)v, svb, svh, svs, (const T*)dout, lse2, delta, sqp,   \
+                                                      (T*)dk,                                                         \
                                                       (T*)dv, (int)Hq, (int)Hkv, groups, (int)Sq, (int)Sk, (int)D,  \
                                                       sl2, scale, causal, (int)causal_offset);                      \
     fa_bwd_dq_kernel<T, DPV><<<gq, 256, 0, st>>>((const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks,            \
-                                                 (const T*)v, svb, svh, svs, (const T*)dout, lse, delta, (T*)dq,    \
+                                                 (const T*)v, svb, svh, svs, (const T*)dout, lse2, delta, sqp,      \
+                                                 (T*)dq,                                                            \
                                                  (int)Hq, groups, (int)Sq, (int)Sk, (int)D, sl2, scale, causal,     \
                                                  (int)causal_offset);                                               \
   } while (0)

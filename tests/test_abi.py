@@ -42,7 +42,9 @@ def test_header_signatures_bind():
 def test_workspace_queries_are_host_only():
     assert _native.call("qh_rmsnorm_bwd_workspace", 16384, 1024, _native.BF16) > 0
     assert _native.call("qh_embedding_bwd_workspace", 16384) > 0
-    assert _native.call("qh_flash_bwd_workspace", 8, 16, 4096) == 8 * 16 * 4096 * 4
+    # Delta and log2-scale LSE per query, rows padded to a multiple of 64 plus one 64-query tile
+    assert _native.call("qh_flash_bwd_workspace", 8, 16, 4096) == 2 * 8 * 16 * (4096 + 64) * 4
+    assert _native.call("qh_flash_bwd_workspace", 1, 2, 65) == 2 * 1 * 2 * (128 + 64) * 4
     assert _native.call("qh_flash_decode_workspace", 64, 16, 8, 2049, 128) > 0
 
 
