@@ -111,7 +111,7 @@ __device__ __forceinline__ void stage_rows_t(T* __restrict__ S, const T* __restr
 // ===========================================================================
 // LDS tiles of K and V are stored in their natural [key][d] layout with DP*2
 // byte rows and no padding; the 16-byte chunks of row r are XOR-swizzled
-// (physical chunk = logical chunk ^ (r % 8)) so that both fragment reads below
+// (swz() below) so that both fragment reads below
 // spread over all 32 banks. Tiles are written straight from global memory by
 // global_load_lds (16 bytes per lane, lane l -> base + 16*l), so staging needs
 // neither registers nor VALU work and overlaps the previous tile's math.
@@ -126,8 +126,16 @@ typedef short qh_v4i16 __attribute__((ext_vector_type(4)));
 
 typedef short qh_v8i16 __attribute__((ext_vector_type(8)));
 
+// Physical 16-byte chunk of logical chunk `chunk` in tile row `row` (cpr
+// chunks per row). With 256-byte rows (DP = 128) every row starts on the same
+// LDS banks, so the XOR pattern must (a) give 16 consecutive rows 16 distinct
+// chunk positions for one logical chunk (the 16-byte fragment reads) and
+// (b) place 4 consecutive rows x 4 adjacent chunks in 16 distinct positions
+// (the 8-byte transpose reads): XOR with the row's low 4 bits rotated by two.
+// Narrower rows XOR with (row mod cpr).
 __device__ __forceinline__ int swz(int row, int chunk, int cpr) {
-  return chunk ^ (row & ((cpr < 8 ? cpr : 8) - 1));
+  if (cpr >= 16) return chunk ^ (((row & 3) << 2) | ((row >> 2) & 3));
+  return chunk ^ (row & (cpr - 1));
 }
 
 // One V^T A-operand fragment: two transpose reads at keys key and key + 8 of
@@ -196,8 +204,9 @@ struct TileLoader {
     const int lane = threadIdx.x & 63;
     wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     rl = lane / CPR;
-    // the row's swizzle depends only on (n * RPI + rl) % 8, which is the same
-    // for every instruction n of this wave (n = 4 i + wid)
+    // the row's swizzle depends only on (n * RPI + rl) % min(CPR, 16), which is
+    // the same for every instruction n of this wave (n = 4 i + wid, and 4 RPI
+    // is a multiple of 16)
     const int c = swz(wid * RPI + rl, lane % CPR, CPR);
     d0 = c * 8 < D ? c * 8 : D - 8;
     voff = (uint32_t)(((int64_t)rl * gstride + d0) * (int64_t)sizeof(T));
@@ -771,13 +780,14 @@ __global__ __launch_bounds__(64) void fa_decode_kernel(const T* __restrict__ Q, 
   const int ke = min(sk_b, ks + kps);
   const int ntiles = ke > ks ? (ke - ks + BN - 1) / BN : 0;
 
-  // DMA lane geometry: row rl of each RPI-row group, physical chunk p. The
-  // swizzle depends on (n * RPI + rl) % 8, i.e. on the parity of n when RPI = 4.
+  // DMA lane geometry: row rl of each RPI-row group, physical chunk p.
   const int rl = lane / CPR, p = lane % CPR;
-  int dsw[2];
-  uint32_t koff[2], voff[2];
+  // The swizzle of row n * RPI + rl repeats every NPAT instructions.
+  constexpr int NPAT = (CPR < 16 ? CPR : 16) / RPI > 1 ? (CPR < 16 ? CPR : 16) / RPI : 1;
+  int dsw[NPAT];
+  uint32_t koff[NPAT], voff[NPAT];
 #pragma unroll
-  for (int par = 0; par < 2; ++par) {
+  for (int par = 0; par < NPAT; ++par) {
     const int c = swz(par * RPI + rl, p, CPR);
     dsw[par] = c * 8 < D ? c * 8 : D - 8;
     koff[par] = (uint32_t)(((int64_t)rl * sks + dsw[par]) * (int64_t)sizeof(T));
@@ -790,16 +800,16 @@ __global__ __launch_bounds__(64) void fa_decode_kernel(const T* __restrict__ Q, 
     if (row0 + BN <= ke) {
 #pragma unroll
       for (int n = 0; n < NI; ++n) {
-        lds_dma16_s(koff[n & 1], Kb + (int64_t)(row0 + n * RPI) * sks, kl + (uint32_t)(n * RPI * DP * sizeof(T)));
-        lds_dma16_s(voff[n & 1], Vb + (int64_t)(row0 + n * RPI) * svs, vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16_s(koff[n % NPAT], Kb + (int64_t)(row0 + n * RPI) * sks, kl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16_s(voff[n % NPAT], Vb + (int64_t)(row0 + n * RPI) * svs, vl + (uint32_t)(n * RPI * DP * sizeof(T)));
       }
     } else {
 #pragma unroll
       for (int n = 0; n < NI; ++n) {
         int gr = row0 + n * RPI + rl;
         gr = gr < ke ? gr : ke - 1;
-        lds_dma16(Kb + (int64_t)gr * sks + dsw[n & 1], kl + (uint32_t)(n * RPI * DP * sizeof(T)));
-        lds_dma16(Vb + (int64_t)gr * svs + dsw[n & 1], vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16(Kb + (int64_t)gr * sks + dsw[n % NPAT], kl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16(Vb + (int64_t)gr * svs + dsw[n % NPAT], vl + (uint32_t)(n * RPI * DP * sizeof(T)));
       }
     }
   };
