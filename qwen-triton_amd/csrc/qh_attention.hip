@@ -265,7 +265,11 @@ __device__ __forceinline__ void fa_fwd_tile(const T* Kt, const T* Vt, const type
 #pragma unroll
   for (int e = 1; e < 16; ++e) mx = fmaxf(mx, fmaxf(s[0][e], s[1][e]));
   mx = fmaxf(mx, __shfl_xor(mx, 32));
-  if (__any(mx > m)) {  // rescale only when some lane's running max grew (exact)
+  // Rescale only when some lane's running max grew by more than 2^8 in
+  // probability terms: until then P = exp2((s - m) scale_log2) <= 256 stays
+  // well inside bf16/fp32 range, and O / l and the LSE use the same m, so the
+  // result is unchanged while most tiles skip the 64 multiplies.
+  if (__any((mx - m) * scale_log2 > 8.f)) {
     const float mnew = fmaxf(m, mx);
     const float alpha = (m == -INFINITY) ? 0.f : exp2_((m - mnew) * scale_log2);
     l *= alpha;
