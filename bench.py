@@ -39,7 +39,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`,
 # each scaled by the same counter's reading for a 1 GiB copy (fetch x2.000, write x1.000):
 # (262837.5 + 1070.0) KiB x 2 + (2176.0 + 256.0) KiB = 542,972,928 bytes.
-DECODE_TRAFFIC_BYTES = 542_972_928
+DECODE_TRAFFIC_BYTES = 543_014_400
 
 QWEN3_06B = dict(model_type="qwen3", vocab_size=151936, hidden_size=1024, intermediate_size=3072,
                  num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8, head_dim=128,

@@ -188,7 +188,7 @@ int qh_moe_combine(const void* Y, int64_t ldy, const int32_t* inv, const int64_t
  *   B(n,k) = trans_b ? B[k*ldb + n] : B[n*ldb + k]
  * so forward x W^T (0,0), dX = dY W (0,1) and dW = dY^T X (1,1) need no copies.
  * bf16/f16 run on MFMA (32x32x16 tiles; 16x16x32 with a 16-way K split in one
- * workgroup for M <= 64) with fp32 accumulation; f32 runs on VALU.
+ * workgroup for M <= 128) with fp32 accumulation; f32 runs on VALU.
  * bias has the input dtype; C has out_dtype.
  * Replaces qwen_triton/kernels/matmul.py:64-97 (_matmul_kernel), :100-111 (_bias_add_kernel),
  * :130-200 (forward/backward launchers incl. the per-call transposes at :140, :184). */
@@ -196,7 +196,7 @@ int qh_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const voi
             const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
             void* stream);
 /* Several decode-sized products sharing the activations, in one launch:
- * C_i[M, N_i] = A(M,K) . B_i(N_i,K)^T (+ bias_i) for i < count (<= 4), M <= 64,
+ * C_i[M, N_i] = A(M,K) . B_i(N_i,K)^T (+ bias_i) for i < count (<= 4), M <= 128,
  * all operands k-contiguous, C in the input dtype (bf16/f16). B, ldb, N, C,
  * ldc and bias are host arrays of count entries (bias may be NULL, or hold NULL
  * entries). Each product is computed exactly as qh_gemm would. gated = 1 (two

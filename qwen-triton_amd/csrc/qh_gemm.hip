@@ -20,9 +20,10 @@
 //  * Tile order is XCD-aware: the 8 XCDs each take a contiguous run of tiles
 //    (grouped 8 M-tiles at a time) so operand panels are reused out of the
 //    XCD's own L2.
-//  * M <= 64 (decode) uses 1024-thread workgroups of MFMA 16x16x32 whose 16
-//    wavefronts split K, so the weight matrix is requested in one or two
-//    memory round trips; partials are summed through LDS in a fixed order.
+//  * M <= 128 (decode, short prefill) uses 1024-thread workgroups of MFMA
+//    16x16x32 whose 16 wavefronts split K, so the weight matrix is requested
+//    in one or two memory round trips; partials are summed through LDS in a
+//    fixed order.
 #include "qh_mfma.h"
 
 namespace {
@@ -202,13 +203,13 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
 }
 
 // ---------------------------------------------------------------------------
-// Skinny GEMM for M <= 64 (decode), "NN" layout (both operands k-contiguous).
+// Skinny GEMM for M <= 128 (decode), "NN" layout (both operands k-contiguous).
 // MFMA 16x16x32 with operand fragments loaded straight from global memory
 // (the activation rows stay cache-resident; each weight byte is read once).
 // 16x16x32 layout for lane l: A row l%16 / B col l%16 with k = 8*(l/16)+e;
 // C col l%16, rows 4*(l/16)+r.
 // ---------------------------------------------------------------------------
-// Decode GEMM for M <= 64: one 1024-thread workgroup (16 wavefronts) per
+// Decode GEMM for M <= 128: one 1024-thread workgroup (16 wavefronts) per
 // 16*CG output columns. The 16 waves form CG column groups x KSP K slices;
 // each wave streams its 16 weight columns over its K slice with every load of
 // a chunk (up to CH 32-wide k-steps) in flight before the first multiply, so
@@ -360,6 +361,7 @@ void launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, i
   // per 16 rows, until about one workgroup per CU (measured best: 1024-column
   // outputs split 4 ways, 2048 two ways, 3072 not at all).
   int ms = 1;
+  while (ms * 4 < mt) ms *= 2;  // at most 4 row tiles (64 rows) per workgroup
   while (ms < mt && tiles * ms * 2 <= 256) ms *= 2;
   if (ms > mt) ms = mt;
   if (ms_force > 0 && ms_force <= mt) ms = ms_force;
@@ -637,9 +639,10 @@ int gemm_typed(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, 
   const T* bi = (const T*)bias;
   constexpr bool is_mfma_type = !std::is_same<T, float>::value;
   if constexpr (is_mfma_type) {
-    // Decode path for small M, both operands k-contiguous (wide outputs with
-    // M > 16, i.e. the batched LM head, stream better through the tiled kernel).
-    if (M <= 64 && !(M > 16 && N > 8192) && !ta && !tb && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
+    // Decode path for small M (up to 128 rows: decode batches and short
+    // prefills), both operands k-contiguous; wide outputs with M > 16 (the
+    // batched LM head) stream better through the tiled kernel.
+    if (M <= 128 && !(M > 16 && N > 8192) && !ta && !tb && K % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
         aligned16(A) && aligned16(B)) {
       launch_decode_gemm<T, OT>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
       return QH_OK;
@@ -717,7 +720,7 @@ extern "C" int qh_gemm_multi(int64_t M, int64_t K, const void* A, int64_t lda, i
                              const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
                              const void* const* bias, int gated, int dtype, void* stream) {
   QH_CHECK_ARG(count >= 1 && count <= kMaxProducts, "qh_gemm_multi: 1..%d products", kMaxProducts);
-  QH_CHECK_ARG(M >= 0 && M <= 64 && K > 0 && K < (1ll << 31), "qh_gemm_multi: needs 0 <= M <= 64 and K > 0");
+  QH_CHECK_ARG(M >= 0 && M <= 128 && K > 0 && K < (1ll << 31), "qh_gemm_multi: needs 0 <= M <= 128 and K > 0");
   QH_CHECK_ARG(!gated || (count == 2 && N[0] == N[1]), "qh_gemm_multi: gated needs two products of equal N");
   QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_gemm_multi: bf16/f16 only");
   QH_CHECK_ARG(aligned16(A) && lda % 8 == 0 && lda >= K && K % 8 == 0,

@@ -55,7 +55,7 @@ def linear_group_ok(x: torch.Tensor, weights: list[torch.Tensor]) -> bool:
     if not (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and _native.available()):
         return False
     k = x.shape[-1]
-    if k % 8 or x.numel() // max(k, 1) > 64 or not 1 <= len(weights) <= 4:
+    if k % 8 or x.numel() // max(k, 1) > 128 or not 1 <= len(weights) <= 4:
         return False
     return all(w.dtype == x.dtype and w.is_cuda and w.dim() == 2 and w.shape[1] == k and w.stride(1) == 1
                and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0 for w in weights)
@@ -63,7 +63,7 @@ def linear_group_ok(x: torch.Tensor, weights: list[torch.Tensor]) -> bool:
 
 def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torch.Tensor | None] | None = None,
                  gated: bool = False):
-    """One launch for ``x @ W_i.T (+ b_i)`` over products that share ``x`` (M <= 64, no autograd).
+    """One launch for ``x @ W_i.T (+ b_i)`` over products that share ``x`` (M <= 128, no autograd).
 
     Returns the list of outputs, or ``silu(x @ W_0.T) * (x @ W_1.T)`` when ``gated``; each
     product is computed and rounded exactly as ``triton_matmul`` would.

@@ -12,7 +12,7 @@ flash kernel):
   reference does for masked multi-token attention.
 
 Inference (no autograd, GPU, position-indexed cache): the q/k/v projections
-of up to 64 tokens run as one grouped launch, and q_norm/k_norm, RoPE and the
+of up to 128 tokens run as one grouped launch, and q_norm/k_norm, RoPE and the
 cache writes as one fused pass (``qh_attn_prepare``), both with the same
 arithmetic as the separate kernels.
 """

@@ -1,6 +1,6 @@
 """SwiGLU MLP (reference: qwen_triton/modules/mlp.py:10-22).
 
-Inference with up to 64 tokens computes gate, up and silu(gate) * up in one
+Inference with up to 128 tokens computes gate, up and silu(gate) * up in one
 grouped launch with the arithmetic of the separate kernels.
 """
 from __future__ import annotations

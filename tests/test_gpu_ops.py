@@ -306,7 +306,8 @@ def test_gemm_forward(M, N, Kd, dtype):
 
 
 @pytest.mark.parametrize("M,N,Kd", [(64, 1024, 3072), (64, 2048, 1024), (1, 3072, 1024), (48, 1000, 1000),
-                                    (9, 200, 4104), (64, 151936 // 8, 1024), (3, 20000, 136)])
+                                    (9, 200, 4104), (64, 151936 // 8, 1024), (3, 20000, 136), (128, 1024, 3072),
+                                    (100, 2048, 1024), (65, 6144, 1024)])
 def test_gemm_decode_shapes_deterministic(M, N, Kd):
     # the small-M path splits K across 16 wavefronts and sums the slices in a fixed order
     x = randn(M, Kd, dtype=torch.bfloat16, seed=190)
@@ -317,7 +318,7 @@ def test_gemm_decode_shapes_deterministic(M, N, Kd):
         assert torch.equal(K.triton_matmul(x, w), y0)
 
 
-@pytest.mark.parametrize("M", [1, 5, 64])
+@pytest.mark.parametrize("M", [1, 5, 64, 128])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_linear_group_matches_separate_gemms(M, with_bias):
     from qwen_triton.kernels.matmul import linear_group, linear_group_ok
