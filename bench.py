@@ -419,6 +419,175 @@ def bench_moe(steps, warmup, loop_reps=1):
     return res
 
 
+def bench_ops(reps=20):
+    """Per-operator measurement at config shapes: HIP-event time, achieved GB/s against the HBM
+    roofline, and the oracle (fp32 torch on the host cores) on a bounded row sample beside it."""
+    import torch
+    from oracle import ops as O
+    from qwen_triton import kernels as K
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    cores = torch.get_num_threads()
+    g = torch.Generator(device="cuda").manual_seed(0)
+    bf = torch.bfloat16
+
+    def rnd(*shape, dtype=bf, scale=1.0):
+        return (torch.randn(*shape, device="cuda", generator=g) * scale).to(dtype)
+
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    torch.cuda._sleep(10_000_000)
+    ev1.record()
+    sync()
+    cycles_per_ms = 10_000_000 / ev0.elapsed_time(ev1)
+
+    def gpu_ms(fn, n=reps):
+        """Device time per call: the timed launches are queued behind a spin kernel sized to
+        outlast their host-side enqueue, so they run back to back on the GPU."""
+        fn()
+        sync()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        sync()
+        host_ms = (time.perf_counter() - t0) * 1e3
+        torch.cuda._sleep(int(cycles_per_ms * (1.5 * host_ms + 1.0)))
+        ev0.record()
+        for _ in range(n):
+            fn()
+        ev1.record()
+        sync()
+        return ev0.elapsed_time(ev1) / n
+
+    def cpu_ms(fn, n=3):
+        fn()
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2] * 1e3
+
+    rows = []
+
+    def record(row, op, shape, ms, nbytes, rows_gpu, cpu_fn=None, rows_cpu=None):
+        r = {"row": row, "op": op, "shape": shape, "gpu_us": round(ms * 1e3, 2),
+             "gbs": round(nbytes / ms / 1e6, 1), "hbm_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 3)}
+        if cpu_fn is not None:
+            c = cpu_ms(cpu_fn)
+            r["cpu_sample_rows"] = rows_cpu
+            r["cpu_ms"] = round(c, 2)
+            r["gpu_vs_cpu_per_row"] = round((c / rows_cpu) / (ms / rows_gpu), 1)
+        log(json.dumps(r))
+        rows.append(r)
+
+    f32 = torch.float32
+    # a2 embedding (16384 tokens of the 151936 x 1024 table), fwd and bwd (full dW written)
+    T, H, V = 16384, 1024, 151936
+    w = rnd(V, H, scale=0.02)
+    ids = torch.randint(0, V, (T,), device="cuda", generator=g)
+    ms = gpu_ms(lambda: K.triton_embedding(ids, w))
+    record("a2", "embedding fwd", [T, H], ms, 2 * T * H * 2 + T * 8, T,
+           lambda: O.embedding(ids[:2048].cpu(), w.float().cpu(), dtype=f32), 2048)
+    wg = w.clone().requires_grad_(True)
+    go = rnd(T, H)
+    ms_fb = gpu_ms(lambda: torch.autograd.grad(K.triton_embedding(ids, wg), wg, go), 5)
+    ms_f = gpu_ms(lambda: K.triton_embedding(ids, wg), 5)
+    record("a2", "embedding bwd", [T, H], ms_fb - ms_f, T * H * 2 + V * H * 2 + T * 8, T,
+           lambda: O.embedding_backward(ids[:2048].cpu(), go[:2048].float().cpu(), V, dtype=f32), 2048)
+    # a4 rmsnorm at 16384 x 1024 (config 2) and 16384 x 2048 (config 4), fwd and bwd
+    for C in (1024, 2048):
+        x = rnd(T, C)
+        wn = torch.ones(C, device="cuda", dtype=bf)
+        ms = gpu_ms(lambda: K.rmsnorm(x, wn))
+        record("a4", "rmsnorm fwd", [T, C], ms, 2 * T * C * 2, T,
+               lambda: O.rmsnorm(x[:2048].cpu(), wn.cpu(), dtype=f32), 2048)
+        xg = x.clone().requires_grad_(True)
+        wq = wn.clone().requires_grad_(True)
+        gy = rnd(T, C)
+        ms_fb = gpu_ms(lambda: torch.autograd.grad(K.rmsnorm(xg, wq), (xg, wq), gy), 10)
+        ms_f = gpu_ms(lambda: K.rmsnorm(xg, wq), 10)
+        record("a4", "rmsnorm bwd", [T, C], ms_fb - ms_f, 3 * T * C * 2, T,
+               lambda: O.rmsnorm_backward(x[:2048].cpu(), wn.cpu(), gy[:2048].cpu(), dtype=f32), 2048)
+    # a5 RoPE on config-1 q and k ([8,16,4096,128] / [8,8,4096,128]), cos/sin [1,4096,128]
+    q = rnd(8, 16, 4096, 128)
+    k = rnd(8, 8, 4096, 128)
+    pos = torch.arange(4096, device="cuda")
+    cos, sin = O.rotary_tables(pos, 128, 1e6)
+    cos, sin = cos.to("cuda", bf), sin.to("cuda", bf)
+    ms = gpu_ms(lambda: K.apply_rope(q, k, cos, sin))
+    nq = q.numel() + k.numel()
+    record("a5", "apply_rope (q and k)", [8, 24, 4096, 128], ms, 2 * nq * 2, 8 * 24 * 4096,
+           lambda: O.rope(q[:1, :, :512].cpu(), cos[:, :512].cpu(), sin[:, :512].cpu(), dtype=f32), 16 * 512)
+    # a6 silu_mul and a7 sigmoid_mul at [16384, 3072] / [16384, 2048], fwd and bwd
+    for row, name, fn, ofn, ofb, C in (("a6", "silu_mul", K.silu_mul, O.silu_mul, O.silu_mul_backward, 3072),
+                                       ("a7", "sigmoid_mul", K.sigmoid_mul, O.sigmoid_mul, O.sigmoid_mul_backward,
+                                        2048)):
+        a, b2 = rnd(T, C), rnd(T, C)
+        ms = gpu_ms(lambda: fn(a, b2))
+        record(row, f"{name} fwd", [T, C], ms, 3 * T * C * 2, T, lambda: ofn(a[:2048].cpu(), b2[:2048].cpu(), dtype=f32),
+               2048)
+        ag, bg = a.clone().requires_grad_(True), b2.clone().requires_grad_(True)
+        go2 = rnd(T, C)
+        ms_fb = gpu_ms(lambda: torch.autograd.grad(fn(ag, bg), (ag, bg), go2), 10)
+        ms_f = gpu_ms(lambda: fn(ag, bg), 10)
+        record(row, f"{name} bwd", [T, C], ms_fb - ms_f, 5 * T * C * 2, T,
+               lambda: ofb(a[:2048].cpu(), b2[:2048].cpu(), go2[:2048].cpu(), dtype=f32), 2048)
+    # a15 residual add [16384, 1024]
+    x1, x2 = rnd(T, H), rnd(T, H)
+    ms = gpu_ms(lambda: K.residual_add(x1, x2))
+    record("a15", "residual_add", [T, H], ms, 3 * T * H * 2, T,
+           lambda: O.residual_add(x1[:2048].cpu(), x2[:2048].cpu(), dtype=f32), 2048)
+    # a8 KV cache write: config-3 decode step (64 x 8 x 1 x 128 into cap 4096) and a 4096-token prefill
+    for S in (1, 4096):
+        Bc = 64 if S == 1 else 1
+        cache = rnd(Bc, 8, 4096, 128)
+        vals = rnd(Bc, 8, S, 128)
+        p_ = torch.arange(S, device="cuda") + (2048 if S == 1 else 0)
+        ms = gpu_ms(lambda: K.write_attention_kv(cache, vals, p_))
+        record("a8", f"write_attention_kv S={S}", [Bc, 8, S, 128], ms, 2 * vals.numel() * 2, Bc * 8 * S,
+               lambda: O.kv_write(cache[:1].cpu(), vals[:1].cpu(), p_.cpu()), 8 * S)
+    # a9 cross-entropy over [16384, 151936] bf16 logits, fwd and bwd
+    logits = rnd(T, V)
+    tgt = torch.randint(0, V, (T,), device="cuda", generator=g)
+    ms = gpu_ms(lambda: K.triton_cross_entropy(logits, tgt), 5)
+    record("a9", "cross_entropy fwd", [T, V], ms, T * V * 2, T,
+           lambda: O.cross_entropy(logits[:64].cpu(), tgt[:64].cpu(), dtype=f32), 64)
+    lg = logits.clone().requires_grad_(True)
+    ms_fb = gpu_ms(lambda: torch.autograd.grad(K.triton_cross_entropy(lg, tgt), lg), 3)
+    ms_f = gpu_ms(lambda: K.triton_cross_entropy(lg, tgt), 3)
+    record("a9", "cross_entropy bwd", [T, V], ms_fb - ms_f, 2 * T * V * 2, T,
+           lambda: O.cross_entropy_backward(logits[:64].cpu(), tgt[:64].cpu(), dtype=f32), 64)
+    del logits, lg
+    # MoE routing at config 4: router logits [16384, 128] fp32, top-8
+    E, KK = 128, 8
+    rl = torch.randn(T, E, device="cuda", generator=g)
+    ms = gpu_ms(lambda: K.triton_softmax(rl))
+    record("a10", "softmax fwd", [T, E], ms, 2 * T * E * 4, T, lambda: O.softmax(rl[:2048].cpu(), dtype=f32), 2048)
+    rg = rl.clone().requires_grad_(True)
+    gs = torch.randn(T, E, device="cuda", generator=g)
+    ms_fb = gpu_ms(lambda: torch.autograd.grad(K.triton_softmax(rg), rg, gs), 10)
+    ms_f = gpu_ms(lambda: K.triton_softmax(rg), 10)
+    ys = K.triton_softmax(rl)
+    record("a10", "softmax bwd", [T, E], ms_fb - ms_f, 3 * T * E * 4, T,
+           lambda: O.softmax_backward(ys[:2048].cpu(), gs[:2048].cpu(), dtype=f32), 2048)
+    probs = K.triton_softmax(rl)
+    ms = gpu_ms(lambda: K.triton_topk(probs, KK))
+    record("a11", "topk k=8", [T, E], ms, T * E * 4 + T * KK * 12, T, lambda: O.topk(probs[:2048].cpu(), KK), 2048)
+    sel = K.triton_topk(probs, KK)[1]
+    ms = gpu_ms(lambda: K.triton_one_hot(sel, E))
+    record("a12", "one_hot", [T, KK, E], ms, T * KK * 8 + T * KK * E * 8, T,
+           lambda: O.one_hot(sel[:2048].cpu(), E), 2048)
+    # a13 index_add: one expert's share (1024 routed rows of 2048) into the [16384, 2048] target
+    tgt2 = rnd(T, 2048)
+    src = rnd(1024, 2048)
+    idx = torch.randint(0, T, (1024,), device="cuda", generator=g)
+    ms = gpu_ms(lambda: K.triton_index_add(tgt2, src, idx))
+    record("a13", "index_add (1024 rows into 16384)", [T, 2048], ms, 3 * 1024 * 2048 * 2, 1024,
+           lambda: O.index_add(tgt2[:4096].cpu(), src[:256].cpu(), (idx[:256] % 4096).cpu(), dtype=f32), 256)
+    return {"cpu_cores": cores, "rows": rows}
+
+
 def bench_roofline_kernels(reps=20):
     """Only the dominant decode kernel (one layer's cache) plus a 1 GiB copy for counter calibration."""
     import torch
@@ -453,7 +622,8 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="decode", choices=["decode", "fa", "dense", "gemm", "roofline", "moe"])
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "fa", "dense", "gemm", "roofline", "moe", "ops"])
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -480,6 +650,11 @@ def main() -> None:
     if args.workload == "gemm":
         res = bench_gemm(args.steps, args.warmup)
         print(json.dumps({"metric": "GEMM shapes (bf16)", "rows": res}), flush=True)
+        return
+    if args.workload == "ops":
+        res = bench_ops()
+        print(json.dumps({"metric": "per-operator HBM throughput at config shapes (+ oracle on host cores)",
+                          **res}), flush=True)
         return
     if args.workload == "moe":
         res = bench_moe(args.steps, args.warmup)

@@ -106,6 +106,37 @@ __device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
   return (float)((const bf16_t*)p)[i];
 }
 
+// VN consecutive elements p[i .. i+VN) of a runtime-dtype buffer as fp32, with
+// 16-byte loads when the buffer is 16-byte aligned (al16) and VN elements of the
+// buffer's dtype span whole 16-byte words; i must be a multiple of VN.
+template <int VN>
+__device__ __forceinline__ void load_any_vec(const void* p, int dtype, int64_t i, bool al16, float (&out)[VN]) {
+  if (al16 && dtype == QH_F32 && VN % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < VN; q += 4) {
+      const float4 v = *reinterpret_cast<const float4*>((const float*)p + i + q);
+      out[q] = v.x, out[q + 1] = v.y, out[q + 2] = v.z, out[q + 3] = v.w;
+    }
+  } else if (al16 && dtype == QH_BF16 && VN % 8 == 0) {
+#pragma unroll
+    for (int q = 0; q < VN; q += 8) {
+      const Vec16<bf16_t> v = ld16((const bf16_t*)p + i + q);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) out[q + j] = (float)v.v[j];
+    }
+  } else if (al16 && dtype == QH_F16 && VN % 8 == 0) {
+#pragma unroll
+    for (int q = 0; q < VN; q += 8) {
+      const Vec16<f16_t> v = ld16((const f16_t*)p + i + q);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) out[q + j] = (float)v.v[j];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VN; ++j) out[j] = load_any(p, dtype, i + j);
+  }
+}
+
 __device__ __forceinline__ void store_any(void* p, int dtype, int64_t i, float v) {
   if (dtype == QH_F32) ((float*)p)[i] = v;
   else if (dtype == QH_F16) ((f16_t*)p)[i] = (f16_t)v;

@@ -36,6 +36,26 @@ static int pick_row_shape(int64_t cols, int VN, int& G, int& NV) {
 // ===========================================================================
 // RMSNorm
 // ===========================================================================
+// Per-lane scale (w + wadd) of the columns a lane owns in the (G, NV) row
+// shape, loaded once per workgroup; columns past the row end get 0.
+template <int VN, int NV, int G>
+__device__ __forceinline__ void load_row_scale(const void* w, int wdtype, int cols, int g, float wadd,
+                                               float (&sw)[NV][VN]) {
+  const bool al16 = (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * G + g) * VN;
+    if (c < cols) {
+      load_any_vec<VN>(w, wdtype, c, al16, sw[i]);
+#pragma unroll
+      for (int j = 0; j < VN; ++j) sw[i][j] += wadd;
+    } else {
+#pragma unroll
+      for (int j = 0; j < VN; ++j) sw[i][j] = 0.f;
+    }
+  }
+}
+
 template <typename T, int G, int NV>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_fast(const T* __restrict__ x, const void* __restrict__ w,
                                                         int wdtype, T* __restrict__ y, int64_t rows, int cols,
@@ -43,6 +63,8 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_fast(const T* __restrict__ x,
   constexpr int VN = Vec16<T>::N;
   constexpr int RPB = 256 / G;
   const int grp = threadIdx.x / G, g = threadIdx.x % G;
+  float sw[NV][VN];
+  load_row_scale<VN, NV, G>(w, wdtype, cols, g, wadd, sw);
   for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
     const T* xr = x + row * cols;
     Vec16<T> xv[NV];
@@ -68,8 +90,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_fast(const T* __restrict__ x,
       if (c < cols) {
         Vec16<T> o;
 #pragma unroll
-        for (int j = 0; j < VN; ++j)
-          o.v[j] = from_f32<T>((to_f32(xv[i].v[j]) * inv) * (load_any(w, wdtype, c + j) + wadd));
+        for (int j = 0; j < VN; ++j) o.v[j] = from_f32<T>((to_f32(xv[i].v[j]) * inv) * sw[i][j]);
         st16(yr + c, o);
       }
     }
@@ -87,6 +108,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_fast(const T* __restrict__ x,
   constexpr int VN = Vec16<T>::N;
   constexpr int RPB = 256 / G;
   const int grp = threadIdx.x / G, g = threadIdx.x % G;
+  float sw[NV][VN];
+  load_row_scale<VN, NV, G>(w, wdtype, cols, g, wadd, sw);
   for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
     Vec16<T> xv[NV];
     float ss = 0.f;
@@ -114,8 +137,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_fast(const T* __restrict__ x,
       if (c < cols) {
         Vec16<T> o;
 #pragma unroll
-        for (int j = 0; j < VN; ++j)
-          o.v[j] = from_f32<T>((to_f32(xv[i].v[j]) * inv) * (load_any(w, wdtype, c + j) + wadd));
+        for (int j = 0; j < VN; ++j) o.v[j] = from_f32<T>((to_f32(xv[i].v[j]) * inv) * sw[i][j]);
         st16(yr + c, o);
       }
     }
@@ -154,14 +176,11 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_fast(const T* __restrict__ x,
   const int grp = threadIdx.x / G, g = threadIdx.x % G;
   float pw[NV][VN];
   float sw[NV][VN];
+  load_row_scale<VN, NV, G>(w, wdtype, cols, g, wadd, sw);
 #pragma unroll
   for (int i = 0; i < NV; ++i)
 #pragma unroll
-    for (int j = 0; j < VN; ++j) {
-      pw[i][j] = 0.f;
-      const int c = (i * G + g) * VN + j;
-      sw[i][j] = (c < cols) ? load_any(w, wdtype, c) + wadd : 0.f;
-    }
+    for (int j = 0; j < VN; ++j) pw[i][j] = 0.f;
   const float inv_cols = 1.0f / (float)cols;
   for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
     const T* xr = x + row * cols;
@@ -202,15 +221,24 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_fast(const T* __restrict__ x,
       }
     }
   }
-  float* wr = ws + ((int64_t)blockIdx.x * RPB + grp) * cols;
+  // Combine the RPB row groups' partials in LDS in group order, then write the
+  // workgroup's single partial row ws[blockIdx.x, :].
+  extern __shared__ float acc[];
+  for (int s = 0; s < RPB; ++s) {
+    if (grp == s) {
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = (i * G + g) * VN;
-    if (c < cols) {
+      for (int i = 0; i < NV; ++i) {
+        const int c = (i * G + g) * VN;
+        if (c < cols) {
 #pragma unroll
-      for (int j = 0; j < VN; ++j) wr[c + j] = pw[i][j];
+          for (int j = 0; j < VN; ++j) acc[c + j] = s == 0 ? pw[i][j] : acc[c + j] + pw[i][j];
+        }
+      }
     }
+    __syncthreads();
   }
+  float* wr = ws + (int64_t)blockIdx.x * cols;
+  for (int c = threadIdx.x; c < cols; c += 256) wr[c] = acc[c];
 }
 
 // Backward, generic path: block owns ws row blockIdx.x; thread t owns columns
@@ -245,27 +273,37 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_generic(const T* __restrict__
   }
 }
 
-// Stage 2: gw[c] = sum_r ws[r, c], 16 columns x 16 sub-rows per block; each
-// sub-row sums a fixed stride of partial rows, then the 16 sub-sums are added
-// in order. Deterministic.
-__global__ __launch_bounds__(256) void colsum_partials(const float* __restrict__ ws, int64_t nrows, int64_t cols,
-                                                       void* __restrict__ out, int odtype) {
-  __shared__ float part[16][17];
-  const int cl = threadIdx.x & 15, sub = threadIdx.x >> 4;
-  const int64_t c = blockIdx.x * 16 + cl;
-  float s = 0.f;
-  if (c < cols)
-    for (int64_t r = sub; r < nrows; r += 16) s += ws[r * cols + c];
-  part[sub][cl] = s;
+// Stage 2: gw[c] = sum_r ws[r, c]. A block owns 64 columns; each of its 16
+// waves sums every 16th partial row with four interleaved accumulators (rows
+// w, w+16, w+32, w+48 of each 64-row step), and the 16 wave sums are added in
+// wave order. The order is fixed by the code, so results are deterministic.
+__global__ __launch_bounds__(1024) void colsum_partials(const float* __restrict__ ws, int64_t nrows, int64_t cols,
+                                                        void* __restrict__ out, int odtype) {
+  __shared__ float part[16][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t c = blockIdx.x * 64 + lane;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  if (c < cols) {
+    int64_t r = wv;
+    for (; r + 48 < nrows; r += 64) {
+      a0 += ws[r * cols + c];
+      a1 += ws[(r + 16) * cols + c];
+      a2 += ws[(r + 32) * cols + c];
+      a3 += ws[(r + 48) * cols + c];
+    }
+    for (; r < nrows; r += 16) a0 += ws[r * cols + c];
+  }
+  part[wv][lane] = (a0 + a1) + (a2 + a3);
   __syncthreads();
-  if (sub == 0 && c < cols) {
+  if (wv == 0 && c < cols) {
     float t = 0.f;
-    for (int i = 0; i < 16; ++i) t += part[i][cl];
+    for (int i = 0; i < 16; ++i) t += part[i][lane];
     store_any(out, odtype, c, t);
   }
 }
 
-static const int kRmsBwdBlocks = 256;
+// Workgroups of the backward row kernels (one fp32 partial row each).
+static const int kRmsBwdBlocks = 1024;
 
 // ===========================================================================
 // Softmax
@@ -583,6 +621,84 @@ __global__ __launch_bounds__(256) void topk_kernel(const T* __restrict__ x, T* _
   }
 }
 
+// Top-k for rows of C <= 128 and k <= 16: 16 lanes per row, each holding 8
+// values as 64-bit keys (order-preserving value bits << 32 | ~column), so one
+// unsigned max gives "largest value, then lowest column" -- the order of
+// topk_better/topk_after. NaN gets key 0 and is never selected, as there. Each
+// lane sorts its 8 keys (Batcher's 19-comparator network); each of the k rounds
+// takes the 16-lane max of the list heads with DPP and the winning lane pops
+// its head. Values are re-read from the row so they keep their exact bits.
+__device__ __forceinline__ uint64_t topk_key(float v, int c) {
+  if (v != v) return 0;
+  if (v == 0.f) v = 0.f;
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)c);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, true);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ void cas_desc(uint64_t& a, uint64_t& b) {
+  const uint64_t hi = max_u64(a, b), lo = a > b ? b : a;
+  a = hi;
+  b = lo;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void topk16_kernel(const T* __restrict__ x, T* __restrict__ vals,
+                                                     int64_t* __restrict__ idx, int64_t N, int C, int k) {
+  constexpr int VN = Vec16<T>::N;
+  constexpr int NL = 8 / VN;
+  const int64_t row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int g = threadIdx.x & 15;
+  if (row >= N) return;  // whole 16-lane groups leave together
+  const T* xr = x + row * C;
+  uint64_t key[8];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) {
+    const int c0 = (l * 16 + g) * VN;
+    if (c0 < C) {
+      const Vec16<T> v = ld16(xr + c0);
+#pragma unroll
+      for (int j = 0; j < VN; ++j) key[l * VN + j] = topk_key(to_f32(v.v[j]), c0 + j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VN; ++j) key[l * VN + j] = 0;
+    }
+  }
+  cas_desc(key[0], key[1]); cas_desc(key[2], key[3]); cas_desc(key[4], key[5]); cas_desc(key[6], key[7]);
+  cas_desc(key[0], key[2]); cas_desc(key[1], key[3]); cas_desc(key[4], key[6]); cas_desc(key[5], key[7]);
+  cas_desc(key[1], key[2]); cas_desc(key[5], key[6]);
+  cas_desc(key[0], key[4]); cas_desc(key[1], key[5]); cas_desc(key[2], key[6]); cas_desc(key[3], key[7]);
+  cas_desc(key[2], key[4]); cas_desc(key[3], key[5]);
+  cas_desc(key[1], key[2]); cas_desc(key[3], key[4]); cas_desc(key[5], key[6]);
+  int my_col = -1;
+  for (int r = 0; r < k; ++r) {
+    uint64_t m = key[0];
+    m = max_u64(m, dpp_u64<QH_DPP_XOR1>(m));
+    m = max_u64(m, dpp_u64<QH_DPP_XOR2>(m));
+    m = max_u64(m, dpp_u64<QH_DPP_HALF_MIRROR>(m));
+    m = max_u64(m, dpp_u64<QH_DPP_MIRROR>(m));
+    if (g == r) my_col = m ? (int)(0xFFFFFFFFu - (uint32_t)m) : -1;
+    if (m != 0 && key[0] == m) {
+#pragma unroll
+      for (int j = 0; j < 7; ++j) key[j] = key[j + 1];
+      key[7] = 0;
+    }
+  }
+  if (g < k) {
+    vals[row * k + g] = my_col >= 0 ? xr[my_col] : from_f32<T>(__int_as_float(0x7fc00000));
+    idx[row * k + g] = my_col;
+  }
+}
+
 __global__ __launch_bounds__(256) void one_hot_kernel(const int64_t* __restrict__ idx, int64_t* __restrict__ out,
                                                       int64_t N, int64_t C, int64_t total) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -604,6 +720,15 @@ __global__ __launch_bounds__(256) void one_hot_kernel(const int64_t* __restrict_
   else if (G == 64 && NV == 2) KERNEL<T, 64, 2><<<grid, 256, 0, st>>>(__VA_ARGS__); \
   else if (G == 64 && NV == 4) KERNEL<T, 64, 4><<<grid, 256, 0, st>>>(__VA_ARGS__); \
   else if (G == 64 && NV == 8) KERNEL<T, 64, 8><<<grid, 256, 0, st>>>(__VA_ARGS__);
+
+#define QH_SHAPE_SWITCH_LDS(KERNEL, LDS, ...)                                            \
+  if (G == 8 && NV == 1) KERNEL<T, 8, 1><<<grid, 256, LDS, st>>>(__VA_ARGS__);           \
+  else if (G == 16 && NV == 1) KERNEL<T, 16, 1><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
+  else if (G == 32 && NV == 1) KERNEL<T, 32, 1><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
+  else if (G == 64 && NV == 1) KERNEL<T, 64, 1><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
+  else if (G == 64 && NV == 2) KERNEL<T, 64, 2><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
+  else if (G == 64 && NV == 4) KERNEL<T, 64, 4><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
+  else if (G == 64 && NV == 8) KERNEL<T, 64, 8><<<grid, 256, LDS, st>>>(__VA_ARGS__);
 
 template <typename T>
 static void launch_rms_fwd(const void* x, const void* w, int wdtype, void* y, int64_t rows, int64_t cols, float eps,
@@ -641,6 +766,10 @@ static void launch_softmax_bwd(const void* y, const void* gy, void* gx, int64_t 
 
 template <typename T>
 static void launch_topk(const void* x, void* vals, int64_t* idx, int64_t N, int64_t C, int64_t k, hipStream_t st) {
+  if (C <= 128 && k <= 16 && (C * (int64_t)sizeof(T)) % 16 == 0 && aligned16(x)) {
+    topk16_kernel<T><<<(int)ceil_div(N, 16), 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
+    return;
+  }
   const int grid = (int)ceil_div(N, 4);
   const int cpl = (int)ceil_div(C, 64);
   if (cpl <= 1) topk_kernel<T, 1><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
@@ -708,7 +837,7 @@ static int64_t rms_bwd_partial_rows(int64_t rows, int64_t cols, int dtype, int* 
     if (fast_grid) *fast_grid = (int)grid;
     if (G_out) *G_out = G;
     if (NV_out) *NV_out = NV;
-    return grid * rpb;
+    return grid;
   }
   if (fast_grid) *fast_grid = 0;
   return 0;
@@ -720,7 +849,9 @@ static int64_t launch_rms_bwd(const void* x, const void* w, int wdtype, const vo
   int grid = 0, G = 0, NV = 0;
   const int64_t fr = rms_bwd_partial_rows(rows, cols, dtype, &grid, &G, &NV);
   if (fr > 0 && aligned16(x) && aligned16(gy) && aligned16(gx)) {
-    QH_SHAPE_SWITCH(rmsnorm_bwd_fast, (const T*)x, w, wdtype, (const T*)gy, (T*)gx, (float*)ws, rows, (int)cols, eps, wadd)
+    const size_t lds = (size_t)cols * sizeof(float);
+    QH_SHAPE_SWITCH_LDS(rmsnorm_bwd_fast, lds, (const T*)x, w, wdtype, (const T*)gy, (T*)gx, (float*)ws, rows,
+                        (int)cols, eps, wadd)
     return fr;
   }
   const int g = (int)(rows < kRmsBwdBlocks ? rows : kRmsBwdBlocks);
@@ -754,7 +885,7 @@ extern "C" int qh_rmsnorm_bwd(const void* x, const void* w, const void* gy, void
   int64_t prow = 0;
   QH_DISPATCH_DTYPE(dtype, T, "qh_rmsnorm_bwd",
                     prow = launch_rms_bwd<T>(x, w, wdtype, gy, gx, ws, rows, cols, eps, wadd, dtype, st));
-  colsum_partials<<<(int)ceil_div(cols, 16), 256, 0, st>>>((const float*)ws, prow, cols, gw, wdtype);
+  colsum_partials<<<(int)ceil_div(cols, 64), 1024, 0, st>>>((const float*)ws, prow, cols, gw, wdtype);
   QH_CHECK_LAUNCH("qh_rmsnorm_bwd");
   return QH_OK;
 }

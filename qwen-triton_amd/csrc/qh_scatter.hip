@@ -4,6 +4,7 @@
 // (row-index, source-position) pairs are sorted with a stable LSD radix sort
 // (rocPRIM) and each destination row is produced by exactly one workgroup that
 // sums its sources in source order in fp32 and rounds once.
+#include <algorithm>
 #include <cstring>
 #include <rocprim/rocprim.hpp>
 
@@ -56,13 +57,166 @@ __global__ __launch_bounds__(256) void segment_rows(const uint32_t* __restrict__
   }
 }
 
+// 8 consecutive elements of T as fp32 (16- or 32-byte aligned vector access).
+template <typename T>
+__device__ __forceinline__ void ld8f(const T* p, float (&o)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    o[0] = a.x, o[1] = a.y, o[2] = a.z, o[3] = a.w, o[4] = b.x, o[5] = b.y, o[6] = b.z, o[7] = b.w;
+  } else {
+    const Vec16<T> v = ld16(p);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = to_f32(v.v[j]);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void st8f(T* p, const float (&o)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(o[4], o[5], o[6], o[7]);
+  } else {
+    Vec16<T> v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v.v[j] = from_f32<T>(o[j]);
+    st16(p, v);
+  }
+}
+
+// Sum of the source rows vals[s..e) (in that order, fp32, starting from
+// `init`) for the 8-column chunk at element offset c.
+template <typename S>
+__device__ __forceinline__ void run_sum8(const uint32_t* __restrict__ vals, int64_t s, int64_t e,
+                                         const S* __restrict__ src, int64_t stride_s, int64_t c, float (&acc)[8]) {
+  for (int64_t j = s; j < e; ++j) {
+    float t[8];
+    ld8f(src + (int64_t)vals[j] * stride_s + c, t);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] += t[q];
+  }
+}
+
+// segment_rows with 8-column vector chunks: one wave per sorted position
+// (D, both strides multiple of 8, 16-byte aligned rows). Same summation order.
+template <typename S, typename O, bool ACC>
+__global__ __launch_bounds__(64) void segment_rows_vec(const uint32_t* __restrict__ keys,
+                                                       const uint32_t* __restrict__ vals, int64_t n,
+                                                       const S* __restrict__ src, int64_t stride_s,
+                                                       O* __restrict__ dst, int64_t stride_d, int64_t D,
+                                                       uint32_t n_target, int64_t skip_key) {
+  const int64_t i = blockIdx.x;
+  const uint32_t k = keys[i];
+  if (k >= n_target) return;
+  if (i > 0 && keys[i - 1] == k) return;
+  if ((int64_t)k == skip_key) return;
+  int64_t end = i + 1;
+  while (end < n && keys[end] == k) ++end;
+  O* drow = dst + (int64_t)k * stride_d;
+  for (int64_t c = threadIdx.x * 8; c < D; c += 64 * 8) {
+    float acc[8];
+    if (ACC) ld8f(drow + c, acc);
+    else
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] = 0.f;
+    run_sum8(vals, i, end, src, stride_s, c, acc);
+    st8f(drow + c, acc);
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_i32(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+// runs[k] = [first, end) sorted positions of key k (keys below n_target only).
+__global__ __launch_bounds__(256) void mark_runs(const uint32_t* __restrict__ keys, int64_t n, uint32_t n_target,
+                                                 int2* __restrict__ runs) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t k = keys[i];
+  if (k >= n_target || (i > 0 && keys[i - 1] == k)) return;
+  int64_t e = i + 1;
+  while (e < n && keys[e] == k) ++e;
+  runs[k] = make_int2((int)i, (int)e);
+}
+
+// Embedding weight gradient written row by row, each row exactly once: zeros
+// for rows no token hit (and the padding row), else the ordered fp32 sum of
+// the row's gradient rows, rounded once. A wave takes tiles of 16 consecutive
+// rows (grid-stride, so neighbouring waves write neighbouring tiles). Their
+// run bounds come in through scalar loads, and the rows that need loads are
+// done before the zero rows: stores count in the same vmcnt as loads, so a
+// wait for a load also waits for every store issued before it.
+template <typename S, typename O>
+__global__ __launch_bounds__(256) void embedding_grad_rows(const int2* __restrict__ runs,
+                                                           const uint32_t* __restrict__ vals,
+                                                           const S* __restrict__ src, O* __restrict__ dst, int64_t V,
+                                                           int64_t D, int64_t skip_key) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int64_t v0 = ((int64_t)blockIdx.x * 4 + wave) * 16; v0 < V; v0 += (int64_t)gridDim.x * 64) {
+    const int nr = (int)(V - v0 < 16 ? V - v0 : 16);
+    const int2* wr = runs + v0;
+    uint32_t hits = 0;
+    if (nr == 16) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int2 se = wr[r];
+        if (se.x >= 0 && v0 + r != skip_key) hits |= 1u << r;
+      }
+    } else {
+      for (int r = 0; r < nr; ++r) {
+        const int2 se = wr[r];
+        if (se.x >= 0 && v0 + r != skip_key) hits |= 1u << r;
+      }
+    }
+    for (int r = 0; r < nr; ++r) {
+      if (!(hits >> r & 1)) continue;
+      const int2 se = wr[r];
+      O* drow = dst + (v0 + r) * D;
+      for (int64_t c = lane * 8; c < D; c += 2 * 64 * 8) {
+        const int64_t c2 = c + 64 * 8;
+        float a[8], b[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) a[q] = 0.f, b[q] = 0.f;
+        for (int j = se.x; j < se.y; ++j) {
+          const S* sr = src + (int64_t)vals[j] * D;
+          float t[8], u[8];
+          ld8f(sr + c, t);
+          if (c2 < D) ld8f(sr + c2, u);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) a[q] += t[q];
+          if (c2 < D)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) b[q] += u[q];
+        }
+        st8f(drow + c, a);
+        if (c2 < D) st8f(drow + c2, b);
+      }
+    }
+    float z[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) z[q] = 0.f;
+    for (int r = 0; r < nr; ++r) {
+      if (hits >> r & 1) continue;
+      O* drow = dst + (v0 + r) * D;
+      for (int64_t c = lane * 8; c < D; c += 64 * 8) st8f(drow + c, z);
+    }
+  }
+}
+
 template <bool ACC>
 static int launch_segments(const uint32_t* keys, const uint32_t* vals, int64_t n, const void* src, int sdt,
                            int64_t stride_s, void* dst, int ddt, int64_t stride_d, int64_t D, uint32_t n_target,
                            int64_t skip_key, hipStream_t st) {
-#define QH_SEG(S, O)                                                                                        \
-  segment_rows<S, O, ACC><<<(unsigned)n, 256, 0, st>>>(keys, vals, n, (const S*)src, stride_s, (O*)dst,    \
-                                                       stride_d, D, n_target, skip_key)
+  const bool vec = D % 8 == 0 && stride_s % 8 == 0 && stride_d % 8 == 0 && aligned16(src) && aligned16(dst);
+#define QH_SEG(S, O)                                                                                          \
+  if (vec)                                                                                                    \
+    segment_rows_vec<S, O, ACC><<<(unsigned)n, 64, 0, st>>>(keys, vals, n, (const S*)src, stride_s, (O*)dst, \
+                                                            stride_d, D, n_target, skip_key);                 \
+  else                                                                                                        \
+    segment_rows<S, O, ACC><<<(unsigned)n, 256, 0, st>>>(keys, vals, n, (const S*)src, stride_s, (O*)dst,    \
+                                                         stride_d, D, n_target, skip_key)
 #define QH_SEG_O(S)                                        \
   switch (ddt) {                                           \
     case QH_F32: QH_SEG(S, float); break;                  \
@@ -114,7 +268,11 @@ static int sort_indices(const int64_t* idx, int64_t n, int64_t n_target, void* w
 
 }  // namespace
 
-extern "C" int64_t qh_embedding_bwd_workspace(int64_t n_tokens) { return scatter_ws_bytes(n_tokens); }
+// Sort space for the token ids plus a run table of two int32 per embedding row.
+extern "C" int64_t qh_embedding_bwd_workspace(int64_t n_tokens, int64_t V) {
+  if (n_tokens <= 0 || V <= 0) return 0;
+  return scatter_ws_bytes(n_tokens) + align256(V * 8);
+}
 
 extern "C" int64_t qh_index_add_workspace(int64_t n_src) { return scatter_ws_bytes(n_src); }
 
@@ -125,14 +283,47 @@ extern "C" int qh_embedding_bwd(const int64_t* ids, const void* gout, void* gw, 
   QH_CHECK_ARG(V < (1ll << 31) - 1 && n_tokens < (1ll << 31), "qh_embedding_bwd: sizes exceed 2^31");
   hipStream_t st = (hipStream_t)stream;
   const int wsz = wdtype == QH_F32 ? 4 : 2;
-  int rc = qh_zero(gw, V * Hd * wsz, stream);
-  if (rc) return rc;
-  if (n_tokens == 0 || Hd == 0) return QH_OK;
+  if (n_tokens == 0 || Hd == 0 || V == 0) return qh_zero(gw, V * Hd * wsz, stream);
+  const int64_t need = qh_embedding_bwd_workspace(n_tokens, V);
+  if (ws_bytes < need) {
+    qh::set_error("qh_embedding_bwd: workspace %lld bytes < required %lld", (long long)ws_bytes, (long long)need);
+    return QH_E_WORKSPACE;
+  }
+  const int64_t sort_bytes = scatter_ws_bytes(n_tokens);
   uint32_t *keys = nullptr, *vals = nullptr;
-  rc = sort_indices(ids, n_tokens, V, ws, ws_bytes, &keys, &vals, st, "qh_embedding_bwd");
+  int rc = sort_indices(ids, n_tokens, V, ws, sort_bytes, &keys, &vals, st, "qh_embedding_bwd");
   if (rc) return rc;
-  rc = launch_segments<false>(keys, vals, n_tokens, gout, gdtype, Hd, gw, wdtype, Hd, Hd, (uint32_t)V, padding_idx, st);
-  if (rc) return rc;
+  const bool vec = Hd % 8 == 0 && aligned16(gout) && aligned16(gw);
+  if (!vec) {
+    rc = qh_zero(gw, V * Hd * wsz, stream);
+    if (rc) return rc;
+    rc = launch_segments<false>(keys, vals, n_tokens, gout, gdtype, Hd, gw, wdtype, Hd, Hd, (uint32_t)V, padding_idx,
+                                st);
+    if (rc) return rc;
+    QH_CHECK_LAUNCH("qh_embedding_bwd");
+    return QH_OK;
+  }
+  int2* runs = (int2*)((char*)ws + sort_bytes);
+  fill_i32<<<(int)std::min<int64_t>(ceil_div(2 * V, 256), 2048), 256, 0, st>>>((int32_t*)runs, 2 * V, -1);
+  mark_runs<<<(int)ceil_div(n_tokens, 256), 256, 0, st>>>(keys, n_tokens, (uint32_t)V, runs);
+  const int grid = (int)std::min<int64_t>(ceil_div(V, 64), 2048);
+#define QH_EROWS(S, O) \
+  embedding_grad_rows<S, O><<<grid, 256, 0, st>>>(runs, vals, (const S*)gout, (O*)gw, V, Hd, padding_idx)
+#define QH_EROWS_O(S)                                      \
+  switch (wdtype) {                                        \
+    case QH_F32: QH_EROWS(S, float); break;                \
+    case QH_F16: QH_EROWS(S, f16_t); break;                \
+    case QH_BF16: QH_EROWS(S, bf16_t); break;              \
+    default: qh::set_error("qh_embedding_bwd: bad weight dtype"); return QH_E_DTYPE; \
+  }
+  switch (gdtype) {
+    case QH_F32: QH_EROWS_O(float); break;
+    case QH_F16: QH_EROWS_O(f16_t); break;
+    case QH_BF16: QH_EROWS_O(bf16_t); break;
+    default: qh::set_error("qh_embedding_bwd: bad grad dtype"); return QH_E_DTYPE;
+  }
+#undef QH_EROWS_O
+#undef QH_EROWS
   QH_CHECK_LAUNCH("qh_embedding_bwd");
   return QH_OK;
 }

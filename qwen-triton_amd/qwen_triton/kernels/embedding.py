@@ -3,7 +3,8 @@
 Reference: qwen_triton/kernels/embedding.py:35-186 (torch fallback :35-36,
 kernels :50-94, forward launcher :97-112, autograd :115-163, public op
 :166-186). The backward replaces fp32 atomics into a dense [V, H] buffer with a
-stable radix sort of token ids followed by per-id ordered row sums.
+stable radix sort of token ids, then writes every weight-gradient row once:
+zeros, or the ordered fp32 sum of the rows of the tokens that hit it.
 """
 from __future__ import annotations
 
@@ -40,7 +41,7 @@ def _native_embedding_backward(input_ids, grad_output, num_embeddings, embed_dim
     g = grad_output.contiguous().view(-1, embed_dim)
     n = ids.numel()
     gw = torch.empty((num_embeddings, embed_dim), dtype=weight_dtype, device=device)
-    ws = _native.workspace(_native.call("qh_embedding_bwd_workspace", n), device)
+    ws = _native.workspace(_native.call("qh_embedding_bwd_workspace", n, num_embeddings), device)
     pad = -1 if padding_idx is None else int(padding_idx) % num_embeddings
     _native.call("qh_embedding_bwd", ids.data_ptr(), g.data_ptr(), gw.data_ptr(), ws.data_ptr(), ws.numel(), n,
                  num_embeddings, embed_dim, pad, _native.dtype_code(g.dtype), _native.dtype_code(weight_dtype),

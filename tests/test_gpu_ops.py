@@ -193,6 +193,25 @@ def test_embedding_forward_backward(dtype, padding_idx):
     assert torch.equal(g1, w.grad)
 
 
+@pytest.mark.parametrize("H", [64, 20])  # row-wise vector kernel / scalar segment fallback
+def test_embedding_backward_is_token_order_fp32_sum(H):
+    """Each weight-gradient row is the fp32 sum of its tokens' gradient rows in token order, rounded
+    once; unreferenced rows and the padding row are exactly zero."""
+    V, pad = 5000, 7
+    ids = torch.randint(0, 300, (3, 257), generator=_gen(53))
+    ids[0, :5] = pad
+    ids[2, -1] = V - 1
+    go = torch.randn(3, 257, H, generator=_gen(54)).to(torch.bfloat16)
+    w = torch.zeros(V, H, dtype=torch.bfloat16, device=DEV, requires_grad=True)
+    K.triton_embedding(ids.to(DEV), w, pad).backward(go.to(DEV))
+    exp = torch.zeros(V, H, dtype=torch.float32)
+    flat_ids, flat_go = ids.reshape(-1).tolist(), go.reshape(-1, H).float()
+    for t, v in enumerate(flat_ids):
+        exp[v] += flat_go[t]
+    exp[pad] = 0
+    assert torch.equal(w.grad.cpu().view(torch.int16), exp.to(torch.bfloat16).view(torch.int16))
+
+
 # ---------------------------------------------------------------------------
 # Softmax / cross-entropy
 # ---------------------------------------------------------------------------
@@ -237,6 +256,34 @@ def test_topk_bit_exact(N, C, k):
     ev, ei = O.topk(x, k)
     assert torch.equal(idx.cpu(), ei)
     assert torch.equal(vals.cpu(), ev)
+
+
+@pytest.mark.parametrize("N,C,k,dtype", [(1001, 128, 8, torch.float32), (77, 128, 16, torch.bfloat16),
+                                         (50, 64, 16, torch.float32), (19, 8, 8, torch.float32),
+                                         (40, 16, 3, torch.float16), (16384, 128, 8, torch.float32)])
+def test_topk_narrow_rows_ties_and_specials(N, C, k, dtype):
+    """Rows of <= 128 columns: quantised values (many exact ties), +-0, -inf and NaN entries."""
+    x = torch.round(torch.randn(N, C, generator=_gen(83)) * 2) / 2
+    x[::7, 1] = -0.0
+    x[::5, 2] = float("-inf")
+    x[::11, 3] = float("nan")
+    x[3] = float("-inf")  # a row with fewer finite values than k is still all -inf, selected by column
+    x = x.to(dtype).to(DEV)
+    vals, idx = K.triton_topk(x, k)
+    ev, ei = O.topk(x, k)
+    nan_rows = torch.isnan(x.cpu().float()).any(dim=1)
+    ok = ~nan_rows
+    assert torch.equal(idx.cpu()[ok], ei[ok])
+    assert torch.equal(vals.cpu()[ok].view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       ev[ok].view(torch.int16 if dtype != torch.float32 else torch.int32))
+    # NaN is never selected; rows holding one keep the order of the remaining values
+    xc = x.cpu().float()
+    for r in torch.nonzero(nan_rows).view(-1)[:20].tolist():
+        finite = torch.where(torch.isnan(xc[r]), torch.tensor(float("-inf")), xc[r])
+        order = torch.sort(-finite.double(), stable=True).indices
+        order = order[~torch.isnan(xc[r][order])][:k]
+        got = idx[r].cpu()
+        assert torch.equal(got[:order.numel()], order)
 
 
 def test_topk_ties_go_to_lowest_index():
