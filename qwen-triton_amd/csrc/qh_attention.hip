@@ -28,6 +28,7 @@
 // kv-head) streaming K/V tiles through LDS on the matrix cores (the pass is
 // HBM-bound on K/V), partial (m, l, o) per split in the workspace, then a
 // fixed-order combine.
+#include "qh_lds.h"
 #include "qh_mfma.h"
 
 namespace {
@@ -122,9 +123,6 @@ __device__ __forceinline__ void stage_rows_t(T* __restrict__ S, const T* __restr
 //    addressed by lanes i/4 + 4e (e = 0..3); lanes that address 4 consecutive
 //    keys x 4 d-quads therefore receive 4 consecutive keys of one d each.
 
-typedef short qh_v4i16 __attribute__((ext_vector_type(4)));
-
-typedef short qh_v8i16 __attribute__((ext_vector_type(8)));
 
 // Physical 16-byte chunk of logical chunk `chunk` in tile row `row` (cpr
 // chunks per row). With 256-byte rows (DP = 128) every row starts on the same
@@ -150,40 +148,6 @@ __device__ __forceinline__ typename Mfma<T>::v8 read_vt_frag(const T* Vt, int ke
   const qh_v4i16 w1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) qh_v4i16*)(s1));
   const qh_v8i16 w = __builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(typename Mfma<T>::v8, w);
-}
-
-// Direct-to-LDS loads, 16 bytes per lane: lane l's bytes land at LDS byte
-// address lds_base + 16 * l (lds_base is wave-uniform and travels in M0).
-// They are issued as inline asm so the compiler's wait-count pass does not
-// track them: it would otherwise have to assume that every later LDS read may
-// alias the in-flight load and wait for it at once, serialising the prefetch.
-// Callers wait explicitly (s_waitcnt vmcnt(0) + barrier) before reading the
-// destination. M0 has no other user in these kernels.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-// 64-bit per-lane address.
-__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_base) {
-  lds_base = (uint32_t)__builtin_amdgcn_readfirstlane(lds_base);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_base)
-               : "memory", "m0");
-}
-// Wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte offset. The base is
-// uniform by construction; readfirstlane states it for the compiler.
-__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* base, uint32_t lds_base) {
-  const uint64_t b = (uint64_t)(uintptr_t)base;
-  // readfirstlane returns int: widen through uint32_t (no sign extension)
-  const uint64_t ub = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b) |
-                      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32);
-  const void* sbase = (const void*)(uintptr_t)ub;
-  lds_base = (uint32_t)__builtin_amdgcn_readfirstlane(lds_base);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
-               "s"(lds_base)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
 // Loader of ROWS x DP tiles (rows along seq, DP columns) into the swizzled
@@ -724,10 +688,6 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
 // ===========================================================================
 // Decode: Sq == 1, split-KV.
 // ===========================================================================
-// s_waitcnt immediates (gfx9 encoding: vmcnt in [3:0] and [15:14], expcnt in
-// [6:4], lgkmcnt in [11:8]) that wait on one counter only.
-constexpr int waitcnt_vm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8); }
-constexpr int kWaitLgkm0 = 0xF | (0x3 << 14) | (0x7 << 4);
 
 // Split-KV decode on the matrix cores. One wavefront per (split, b, kv-head)
 // streams the split's keys in tiles of 32 through NS LDS stages filled by

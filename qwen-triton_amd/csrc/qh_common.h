@@ -201,6 +201,16 @@ static inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// QH_* dtype code of a storage type.
+template <typename T>
+constexpr int qh_dtype_of();
+template <>
+constexpr int qh_dtype_of<float>() { return QH_F32; }
+template <>
+constexpr int qh_dtype_of<f16_t>() { return QH_F16; }
+template <>
+constexpr int qh_dtype_of<bf16_t>() { return QH_BF16; }
+
 // Dispatch a templated functor over the three storage dtypes.
 #define QH_DISPATCH_DTYPE(dtype, T, name, ...)                         \
   switch (dtype) {                                                     \

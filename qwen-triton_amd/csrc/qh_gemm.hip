@@ -26,6 +26,11 @@
 //    fixed order.
 #include "qh_mfma.h"
 
+// Large-tile path (qh_gemm_tile.hip).
+int qh_gemm_tile_dispatch(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, const void* B,
+                          int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
+                          hipStream_t st);
+
 namespace {
 
 constexpr int BK = 64;
@@ -97,21 +102,6 @@ struct TileLoader {
   }
 };
 
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
-  int pid = blockIdx.x;
-  const int nblk = gridDim.x;
-  // Workgroups are dealt round-robin to the 8 XCDs; renumber so that each XCD
-  // walks a contiguous range of logical tiles.
-  if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
-  constexpr int GROUP = 8;
-  const int group_size = GROUP * tiles_n;
-  const int g = pid / group_size;
-  const int first_m = g * GROUP;
-  const int gm = min(tiles_m - first_m, GROUP);
-  const int in_group = pid - g * group_size;
-  tm = first_m + in_group % gm;
-  tn = in_group / gm;
-}
 
 template <typename T, typename OT, int BM, int BN, int WM, int WN, bool AT, bool BT>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B,
@@ -127,7 +117,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
   __shared__ __attribute__((aligned(16))) T smem[2][(BM + BN) * LDS_LD];
 
   int tm_, tn_;
-  tile_coords(tiles_m, tiles_n, tm_, tn_);
+  tile_order(tiles_m, tiles_n, tm_, tn_);
   const int m0 = tm_ * BM, n0 = tn_ * BN;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int wm = wid / WN, wn = wid % WN;
@@ -621,10 +611,7 @@ void launch_mfma(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_
 template <typename T, typename OT, bool AT, bool BT>
 void launch_mfma_pick(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_t ldc, const T* bias, int M,
                       int N, int K, hipStream_t st) {
-  const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-  if (M >= 256 && N >= 256 && big_tiles >= 128)
-    launch_mfma<T, OT, 256, 256, 2, 2, AT, BT>(A, lda, B, ldb, C, ldc, bias, M, N, K, st);
-  else if (M > 64)
+  if (M > 64)
     launch_mfma<T, OT, 128, 128, 2, 2, AT, BT>(A, lda, B, ldb, C, ldc, bias, M, N, K, st);
   else
     launch_mfma<T, OT, 64, 128, 1, 4, AT, BT>(A, lda, B, ldb, C, ldc, bias, M, N, K, st);
@@ -651,6 +638,11 @@ int gemm_typed(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, 
     const bool a_ok = aligned16(A) && lda % 8 == 0 && (ta ? M % 8 == 0 : K % 8 == 0);
     const bool b_ok = aligned16(B) && ldb % 8 == 0 && (tb ? N % 8 == 0 : K % 8 == 0);
     if (a_ok && b_ok) {
+      // Large outputs: the 256x256 direct-to-LDS tile kernel.
+      const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+      if (M >= 256 && N >= 256 && big_tiles >= 128)
+        return qh_gemm_tile_dispatch(ta, tb, M, N, K, A, lda, B, ldb, C, ldc, bias, qh_dtype_of<T>(),
+                                     qh_dtype_of<OT>(), st);
       if (!ta && !tb) launch_mfma_pick<T, OT, false, false>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
       else if (!ta && tb) launch_mfma_pick<T, OT, false, true>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);
       else if (ta && tb) launch_mfma_pick<T, OT, true, true>(a, lda, b, ldb, c, ldc, bi, M, N, K, st);

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from oracle import ops as O
+from qwen_triton import _native
 from qwen_triton import kernels as K
 from qwen_triton.kernels import flash_attention as FA
 from qwen_triton.kernels import matmul as MM
@@ -422,6 +423,29 @@ def test_gemm_backward_bf16(M, N, Kd):
     # dW reduces over 2*M rows: scale the absolute band with sqrt(rows)
     close(w.grad, gw, atol=2e-2 * max(1.0, (2 * M) ** 0.5 / 8), rtol=2e-2)
     close(b.grad, gb, atol=2e-2 * max(1.0, (2 * M) ** 0.5 / 8), rtol=2e-2)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 1), (1, 0)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_large_tile_layouts_and_tails(ta, tb, out_dtype):
+    """Shapes of >= 128 output tiles of 256x256 take the direct-to-LDS tile kernel; M, N and K all
+    end in partial tiles (4000 = 15*256 + 160, 2056 = 8*256 + 8, 1000 = 15*64 + 40)."""
+    M, N, Kd = 4000, 2056, 1000
+    a = randn(M, Kd, dtype=torch.bfloat16, seed=300)
+    b = randn(N, Kd, dtype=torch.bfloat16, seed=301, scale=0.05)
+    bias = randn(N, dtype=torch.bfloat16, seed=302)
+    a_op = a.t().contiguous() if ta else a  # "T" operands are stored [K, rows]
+    b_op = b.t().contiguous() if tb else b
+    c = torch.empty(M, N, dtype=out_dtype, device=DEV)
+    _native.call("qh_gemm", ta, tb, M, N, Kd, a_op.data_ptr(), a_op.stride(0), b_op.data_ptr(), b_op.stride(0),
+                 c.data_ptr(), N, bias.data_ptr(), _native.BF16, _native.dtype_code(out_dtype), _native.stream(a.device))
+    ref = a.float() @ b.float().t() + bias.float()
+    tol = dict(atol=2e-3, rtol=2e-3) if out_dtype == torch.float32 else BF16_TOL
+    close(c, ref, **tol)
+    c2 = torch.empty_like(c)
+    _native.call("qh_gemm", ta, tb, M, N, Kd, a_op.data_ptr(), a_op.stride(0), b_op.data_ptr(), b_op.stride(0),
+                 c2.data_ptr(), N, bias.data_ptr(), _native.BF16, _native.dtype_code(out_dtype), _native.stream(a.device))
+    assert torch.equal(c, c2)
 
 
 def test_gemm_fp32_matches_reference_band():
