@@ -369,53 +369,99 @@ def bench_gemm(steps, warmup):
 
 
 def bench_moe(steps, warmup, loop_reps=1):
-    """Config 4's expert path: routing + dispatch + grouped expert GEMMs + combine, 16384 tokens."""
+    """Config 4: one Qwen3-MoE layer at 30B-A3B shape on 16384 bf16 tokens (4 x 4096, causal).
+
+    Times (HIP events, inputs resident): the expert path forward without autograd (routing +
+    dispatch + grouped GEMMs + combine), the expert path forward + backward with autograd
+    (router logits, input and every expert weight get gradients), and the whole decoder layer
+    (RMSNorm, attention, MoE block) forward + backward. The reference's per-expert loop is timed
+    once beside them."""
     import torch
     from qwen_triton import QwenTritonConfig
-    from qwen_triton.modules import QwenSparseMoeBlock
+    from qwen_triton.models.core import QwenDecoderLayer
+    from qwen_triton.modules.rotary import QwenRotaryEmbedding
 
-    T, H, E, K, I = 16384, 2048, 128, 8, 768
+    B, S, H, E, K, I = 4, 4096, 2048, 128, 8, 768
+    T = B * S
     cfg = QwenTritonConfig.from_hf_config(dict(
         model_type="qwen3_moe", vocab_size=151936, hidden_size=H, intermediate_size=6144, num_hidden_layers=1,
         num_attention_heads=32, num_key_value_heads=4, head_dim=128, moe_intermediate_size=I, num_experts=E,
         num_experts_per_tok=K, norm_topk_prob=True, decoder_sparse_step=1, mlp_only_layers=[]))
     torch.manual_seed(0)
-    blk = QwenSparseMoeBlock(cfg)
+    layer = QwenDecoderLayer(cfg, 0)
     with torch.no_grad():
-        for n, prm in blk.named_parameters():
-            prm.normal_(0.0, 0.02)
-    blk = blk.to("cuda", torch.bfloat16)
+        for n, prm in layer.named_parameters():
+            if "norm" in n:
+                prm.fill_(1.0)
+            else:
+                prm.normal_(0.0, 0.02)
+    layer = layer.to("cuda", torch.bfloat16)
+    blk = layer.mlp
     g = torch.Generator(device="cuda").manual_seed(0)
     x = torch.randn(T, H, device="cuda", dtype=torch.bfloat16, generator=g)
     logits = torch.randn(T, E, device="cuda", dtype=torch.float32, generator=g)
+    go = torch.randn(T, H, device="cuda", dtype=torch.bfloat16, generator=g)
 
-    def step():
-        w, sel = blk.route(logits, torch.bfloat16)
-        return blk.experts_forward(x, w, sel)
-
-    with torch.no_grad():
-        for _ in range(warmup):
-            step()
+    def timed(fn, n, w):
+        for _ in range(w):
+            fn()
         sync()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(steps):
-            step()
+        for _ in range(n):
+            fn()
         e1.record()
         sync()
-    ms = e0.elapsed_time(e1) / steps
+        return e0.elapsed_time(e1) / n
+
+    def infer():
+        w, sel = blk.route(logits, torch.bfloat16)
+        return blk.experts_forward(x, w, sel)
+
+    xg = x.clone().requires_grad_(True)
+    lg = logits.clone().requires_grad_(True)
+
+    def train():
+        w, sel = blk.route(lg, torch.bfloat16)
+        out = blk.experts_forward(xg, w, sel)
+        torch.autograd.backward(out, go)
+
+    with torch.no_grad():
+        ms_inf = timed(infer, steps, warmup)
+    ms_train = timed(train, steps, warmup)
     flop = 2 * 3 * T * K * H * I  # gate, up, down over the T*K routed rows
-    res = {"moe_fwd_ms": round(ms, 3), "moe_fwd_tflops": round(flop / ms / 1e9, 1),
-           "moe_fwd_frac": round(flop / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4), "tokens": T, "experts": E, "top_k": K}
-    # the reference's per-expert loop (autograd on selects it), for comparison
-    w, sel = blk.route(logits, torch.bfloat16)
-    sync()
-    t0 = time.perf_counter()
-    for _ in range(loop_reps):
-        with torch.enable_grad():
-            blk.experts_forward(x, w, sel)
-    sync()
-    res["loop_fwd_ms"] = round((time.perf_counter() - t0) * 1e3 / loop_reps, 3)
+    res = {"moe_fwd_ms": round(ms_inf, 3), "moe_fwd_tflops": round(flop / ms_inf / 1e9, 1),
+           "moe_fwd_frac": round(flop / ms_inf / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+           "moe_fwd_bwd_ms": round(ms_train, 3), "moe_fwd_bwd_tflops": round(3 * flop / ms_train / 1e9, 1),
+           "moe_fwd_bwd_frac": round(3 * flop / ms_train / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+           "tokens": T, "experts": E, "top_k": K}
+
+    rot = QwenRotaryEmbedding(cfg).to("cuda")
+    pos = torch.arange(S, device="cuda")[None].expand(B, S)
+    hs = torch.randn(B, S, H, device="cuda", dtype=torch.bfloat16, generator=g).requires_grad_(True)
+    gl = torch.randn(B, S, H, device="cuda", dtype=torch.bfloat16, generator=g)
+    cos, sin = rot(hs, pos)
+
+    def layer_step():
+        out, _ = layer(hs, (cos, sin))
+        torch.autograd.backward(out, gl)
+
+    ms_layer = timed(layer_step, steps, warmup)
+    res["layer_fwd_bwd_ms"] = round(ms_layer, 3)
+    res["layer_tokens_per_s"] = round(T / ms_layer * 1e3, 1)
+
+    # the reference's per-expert loop (forward + backward), once
+    saved = blk._grouped_ok
+    blk._grouped_ok = lambda *a, **kw: False
+    try:
+        sync()
+        t0 = time.perf_counter()
+        for _ in range(loop_reps):
+            train()
+        sync()
+        res["loop_fwd_bwd_ms"] = round((time.perf_counter() - t0) * 1e3 / loop_reps, 3)
+    finally:
+        blk._grouped_ok = saved
     return res
 
 
@@ -658,7 +704,7 @@ def main() -> None:
         return
     if args.workload == "moe":
         res = bench_moe(args.steps, args.warmup)
-        print(json.dumps({"metric": "MoE experts fwd (config 4, 30B-A3B layer shape)", **res}), flush=True)
+        print(json.dumps({"metric": "Qwen3-MoE layer fwd/bwd (config 4, 30B-A3B shape)", **res}), flush=True)
         return
     if args.workload == "dense":
         res = bench_dense(args.steps, args.warmup)

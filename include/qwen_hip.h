@@ -179,10 +179,61 @@ int qh_moe_gemm(int mode, const void* A, int64_t lda, const int32_t* rows, const
                 const int32_t* tile_off, int64_t R, int64_t E, int64_t N, int64_t K, int dtype, void* stream);
 /* out[t] = sum of the token's expert rows Y[inv[t*top_k + j]] in ascending
  * expert order, rounded to the dtype after every add (the reference's
- * per-expert index_add into zeros). Deterministic; out fully written.
- * Replaces qwen_triton/modules/moe.py:50-51 (triton_index_add, kernels/moe_routing.py:322-343). */
-int qh_moe_combine(const void* Y, int64_t ldy, const int32_t* inv, const int64_t* selected, int64_t n_tokens,
-                   int64_t top_k, int64_t n_experts, void* out, int64_t H, int dtype, void* stream);
+ * per-expert index_add into zeros). With weights ([n_tokens, top_k], dtype),
+ * row j contributes round(Y[.] * weights[t, j]) (the routing-weight multiply
+ * of the expert output); weights may be NULL. Deterministic; out fully written.
+ * Replaces qwen_triton/modules/moe.py:49-51 (the routing-weight multiply and
+ * triton_index_add, kernels/moe_routing.py:322-343). */
+int qh_moe_combine(const void* Y, int64_t ldy, const int32_t* inv, const int64_t* selected, const void* weights,
+                   int64_t n_tokens, int64_t top_k, int64_t n_experts, void* out, int64_t H, int dtype, void* stream);
+/* Xs[r] = X[rows[r]] for the R expert-sorted rows (the flat[tok] gather of
+ * qwen_triton/modules/moe.py:48, done once for all experts). */
+int qh_moe_gather(const void* X, int64_t ldx, const int32_t* rows, int64_t R, int64_t H, void* Xs, int64_t lds,
+                  int dtype, void* stream);
+
+/* ---- Grouped expert GEMMs on the 256x256 tile kernel (training path) -----
+ * Rows are the expert-sorted dispatch rows; seg_off from qh_moe_dispatch and
+ * tile_off from it with tile_m = 256. Weight tables are DEVICE arrays of
+ * pointers to the experts' [out, in] row-major weights (row stride ldw);
+ * gu_table holds 2E entries (gate_e, up_e), d_table E entries (down_e).
+ * Together with qh_moe_gather, qh_moe_combine and qh_moe_scale_bwd these
+ * replace the forward and the autograd backward of the per-expert loop of
+ * qwen_triton/modules/moe.py:45-51 (QwenMLP = modules/mlp.py:19-22 over
+ * TritonLinear, kernels/matmul.py:130-155, and silu_mul, kernels/swiglu.py). */
+/* G = Xs Wg_e^T, U = Xs Wu_e^T (each rounded), H = round(silu(G) * U) per
+ * expert segment; G and U (both or neither) may be NULL. I % 128 == 0. */
+int qh_moe_up(const void* X, int64_t ldx, int64_t R, int64_t K, const void* const* gu_table, int64_t ldw, int64_t I,
+              const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* G, void* U, void* H, int64_t ldo,
+              int dtype, void* stream);
+/* C = A Wd_e^T per segment, rounded; with wrow (per-row weights) C =
+ * round(round(A Wd_e^T) * wrow[r]). */
+int qh_moe_down(const void* A, int64_t lda, int64_t R, int64_t K, const void* const* d_table, int64_t ldw, int64_t N,
+                const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* C, int64_t ldc, const void* wrow,
+                int dtype, void* stream);
+/* Gradient through the down projection and SiLU-mul: dH = round(dD Wd_e),
+ * s = sigmoid(G): dG = round(dH U s (1 + G (1 - s))), dU = round(dH G s). */
+int qh_moe_down_dgrad(const void* dD, int64_t ldd, int64_t R, int64_t K, const void* const* d_table, int64_t ldw,
+                      int64_t I, const int32_t* seg_off, const int32_t* tile_off, int64_t E, const void* G,
+                      const void* U, int64_t ldg, void* dG, void* dU, int64_t ldo, int dtype, void* stream);
+/* dXs = dG Wg_e + dU Wu_e per segment (one fp32 accumulation, rounded once).
+ * I % 64 == 0. */
+int qh_moe_up_dgrad(const void* dG, const void* dU, int64_t ldg, int64_t R, int64_t I, const void* const* gu_table,
+                    int64_t ldw, int64_t N, const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* dX,
+                    int64_t ldx, int dtype, void* stream);
+/* Expert weight gradients: out_q + e*out_stride = A_q(rows of e)^T B(rows of e)
+ * ([M, N], row stride ldo, rounded), for parts q < parts (1 or 2) sharing B:
+ * gate/up: A = dG, dU, B = Xs; down: A = dD, B = H. Experts without rows get
+ * zeros. */
+int qh_moe_wgrad(int parts, const void* A0, const void* A1, int64_t lda, int64_t M, const void* B, int64_t ldb,
+                 int64_t N, const int32_t* seg_off, int64_t E, void* out0, void* out1, int64_t ldo,
+                 int64_t out_stride, int dtype, void* stream);
+/* Backward of the routing-weight multiply, per token t and slot j (row p =
+ * inv[t*top_k + j]): dD[p] = round(dout[t] * weights[t, j]) and
+ * dw[t, j] = round(sum_c dout[t, c] * D[p, c]) (fp32, fixed order); slots with
+ * an out-of-range expert get dw = 0. */
+int qh_moe_scale_bwd(const void* dout, int64_t ldo, const void* D, int64_t ldd, const void* weights,
+                     const int32_t* inv, const int64_t* selected, int64_t n_tokens, int64_t top_k, int64_t n_experts,
+                     int64_t H, void* dD, int64_t ldg, void* dw, int dtype, void* stream);
 
 /* ---- GEMM (Linear) ------------------------------------------------------ */
 /* C[M,N] = A(M,K) . B(N,K)^T (+ bias[N]) with operand views

@@ -34,8 +34,11 @@
 // read clamped (valid) memory and their results are not stored.
 //
 // The core is a template over a "problem" type that places the tile (output
-// coordinates, operand bases per k-tile, reduction length) and stores the
-// accumulators, so grouped products reuse the same main loop.
+// coordinates, reduction length), gives the address of any operand element
+// (a_at / b_at; the loaders call it once per 1 KiB instruction, or per lane on
+// partial tiles, so operands may be split over several matrices at 8-row or
+// 8-k boundaries) and stores the accumulators, so grouped products reuse the
+// same main loop.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -76,14 +79,16 @@ struct NTile {
     const int rin = lane / CPR, c = (lane % CPR) ^ sw(RPI * wid + rin);
     return (uint32_t)(((int64_t)rin * ld + 8 * c) * (int64_t)sizeof(T));
   }
-  // g: element (tile row 0, k0). vrows: valid rows from row 0; vk: valid k from k0.
-  static __device__ __forceinline__ void issue(uint32_t lds, const T* g, int64_t ld, int vrows, int vk,
-                                               uint32_t vo, int wid) {
+  // at(i, k): address of element (tile row i, k). Rows RPI n .. RPI n + RPI-1
+  // must share one stride ld. vrows: valid rows; vk: valid k from k0.
+  template <class AT>
+  static __device__ __forceinline__ void issue(uint32_t lds, const AT& at, int k0, int vrows, int vk, uint32_t vo,
+                                               int wid) {
     if (vrows >= ROWS && vk >= BK) {
 #pragma unroll
       for (int i = 0; i < PW; ++i) {
         const int n = wid + NWAVE * i;
-        lds_dma16_s(vo, g + (int64_t)(RPI * n) * ld, lds + (uint32_t)n * 1024u);
+        lds_dma16_s(vo, at(RPI * n, k0), lds + (uint32_t)n * 1024u);
       }
     } else {
       const int lane = threadIdx.x & 63;
@@ -95,7 +100,7 @@ struct NTile {
         const int n = wid + NWAVE * i;
         int r = RPI * n + rin;
         if (r > vrows - 1) r = vrows - 1;
-        lds_dma16(g + (int64_t)r * ld + kc, lds + (uint32_t)n * 1024u);
+        lds_dma16(at(r, k0 + kc), lds + (uint32_t)n * 1024u);
       }
     }
   }
@@ -136,14 +141,16 @@ struct TTile {
     const int c = slot ^ sw(wid * RPI + kin);
     return (uint32_t)(((int64_t)kin * ld + 8 * c) * (int64_t)sizeof(T));
   }
-  // g: element (k0, tile column 0). vcols: valid columns; vk: valid k-rows.
-  static __device__ __forceinline__ void issue(uint32_t lds, const T* g, int64_t ld, int vcols, int vk,
-                                               uint32_t vo, int wid) {
+  // at(i, k): address of element (tile column i, k). k-rows RPI n .. RPI n +
+  // RPI-1 must share one stride ld. vcols: valid columns; vk: valid k-rows.
+  template <class AT>
+  static __device__ __forceinline__ void issue(uint32_t lds, const AT& at, int k0, int vcols, int vk, uint32_t vo,
+                                               int wid) {
     if (vcols >= COLS && vk >= BK) {
 #pragma unroll
       for (int i = 0; i < PW; ++i) {
         const int n = wid + NWAVE * i;
-        lds_dma16_s(vo, g + (int64_t)(n * RPI) * ld, lds + (uint32_t)n * 1024u);
+        lds_dma16_s(vo, at(0, k0 + n * RPI), lds + (uint32_t)n * 1024u);
       }
     } else {
       const int lane = threadIdx.x & 63;
@@ -155,7 +162,7 @@ struct TTile {
         int col = 8 * (slot ^ sw(kr));
         if (col > vcols - 8) col = vcols - 8;  // vcols is a positive multiple of 8
         if (kr > vk - 1) kr = vk - 1;
-        lds_dma16(g + (int64_t)kr * ld + col, lds + (uint32_t)n * 1024u);
+        lds_dma16(at(col, k0 + kr), lds + (uint32_t)n * 1024u);
       }
     }
   }
@@ -193,7 +200,10 @@ struct TileCtx {
   int K;             // reduction length of this tile
   int vm, vn;        // valid output rows / columns from (m0, n0)
   int64_t lda, ldb;  // operand strides
-  int aux;           // problem-defined (e.g. expert index)
+  int aux, aux2;     // problem-defined (expert index, segment start)
+  const T* w0;       // problem-defined operand bases (expert weights)
+  const T* w1;
+  T* out;            // problem-defined output base
 };
 
 // ---------------------------------------------------------------------------
@@ -212,6 +222,22 @@ template <int ND, int SPAN, int... Ms>
 __device__ __forceinline__ void mma_schedule(std::integer_sequence<int, Ms...>) {
   (mma_schedule_slot<ND, SPAN, Ms>(), ...);
 }
+
+// A wavefront's output tile (ROWS x COLS, rounded to T) staged in LDS for a
+// vectorised epilogue. 16-byte chunk c of row r is stored at chunk
+// c ^ 4((r >> 2) & 1): the staging writes (32 columns of rows r and r + 4 per
+// instruction) and the 16-byte row reads are both conflict-free.
+template <typename T, int ROWS, int COLS>
+struct EpiTile {
+  static_assert(COLS == 64, "64-column wavefront tiles");
+  T* base;
+  static __device__ __forceinline__ int at(int r, int col) {
+    return r * COLS + 8 * ((col >> 3) ^ (((r >> 2) & 1) << 2)) + (col & 7);
+  }
+  __device__ __forceinline__ void put(int r, int col, T v) const { base[at(r, col)] = v; }
+  // 8 consecutive columns 8 c8 .. 8 c8 + 7 of row r.
+  __device__ __forceinline__ Vec16<T> row8(int r, int c8) const { return ld16(base + at(r, 8 * c8)); }
+};
 
 template <typename T, int BM, int BN, int BK, int NS, bool AT, bool BT, class P>
 __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
@@ -249,8 +275,9 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
     const int k0 = kt * BK;
     const int vk = c.K - k0;
     const uint32_t base = lds0 + (uint32_t)((kt % NS) * STAGE * (int)sizeof(T));
-    TA::issue(base, p.a_tile(c, k0), c.lda, c.vm, vk, voa, wid);
-    TB::issue(base + (uint32_t)(TA::ELEMS * sizeof(T)), p.b_tile(c, k0), c.ldb, c.vn, vk, vob, wid);
+    TA::issue(base, [&](int i, int k) { return p.a_at(c, i, k); }, k0, c.vm, vk, voa, wid);
+    TB::issue(base + (uint32_t)(TA::ELEMS * sizeof(T)), [&](int i, int k) { return p.b_at(c, i, k); }, k0, c.vn, vk,
+              vob, wid);
   };
   // Make k-tile kt visible to every wave, with `after` later tiles still in flight.
   auto land = [&](int kt, int after) {
@@ -309,6 +336,27 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
     mma((KS - 1) & 1);
     mma_schedule<ND, NM * 3 / 4>(std::make_integer_sequence<int, NM>{});
   }
+  if constexpr (P::kVecEpilogue) {
+    if (p.vec_ok()) {
+      // Stage the wavefront's tile (rounded to T) in LDS, then hand it to the
+      // problem as 16-byte row vectors.
+      __syncthreads();  // every wave is done with the operand stages
+      EpiTile<T, WTM, WTN> et{smem + wid * (WTM * WTN)};
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              et.put(32 * i + 4 * (lane >> 5) + 8 * g + r, 32 * j + (lane & 31), from_f32<T>(acc[i][j][4 * g + r]));
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      __builtin_amdgcn_wave_barrier();
+      p.epilogue_vec(c, et, wm * WTM, wn * WTN, lane);
+      return;
+    }
+  }
   p.template epilogue<TM, TN>(c, acc, wm * WTM, wn * WTN, lane);
 }
 
@@ -324,6 +372,16 @@ struct DenseProblem {
   int64_t lda, ldb, ldc;
   int M, N, K, tiles_m, tiles_n;
 
+  static constexpr bool kVecEpilogue = std::is_same<OT, T>::value;
+  __device__ __forceinline__ bool vec_ok() const { return bias == nullptr; }
+  template <class ET>
+  __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
+    for (int q = lane; q < 128 * 8; q += 64) {
+      const int r = q >> 3, c8 = q & 7;
+      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
+      if (row < M && col < N) st16(reinterpret_cast<T*>(C) + (int64_t)row * ldc + col, et.row8(r, c8));
+    }
+  }
   __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
     int tm, tn;
     tile_order(tiles_m, tiles_n, tm, tn);
@@ -337,11 +395,11 @@ struct DenseProblem {
     c.aux = 0;
     return true;
   }
-  __device__ __forceinline__ const T* a_tile(const TileCtx<T>& c, int k0) const {
-    return AT ? A + (int64_t)k0 * lda + c.m0 : A + (int64_t)c.m0 * lda + k0;
+  __device__ __forceinline__ const T* a_at(const TileCtx<T>& c, int i, int k) const {
+    return AT ? A + (int64_t)k * lda + (c.m0 + i) : A + (int64_t)(c.m0 + i) * lda + k;
   }
-  __device__ __forceinline__ const T* b_tile(const TileCtx<T>& c, int k0) const {
-    return BT ? B + (int64_t)k0 * ldb + c.n0 : B + (int64_t)c.n0 * ldb + k0;
+  __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
+    return BT ? B + (int64_t)k * ldb + (c.n0 + i) : B + (int64_t)(c.n0 + i) * ldb + k;
   }
   // C layout of a 32x32 tile: column lane % 32, rows 8g + 4(lane/32) + r. One
   // base pointer per 32x32 block; rows are constant offsets from it.
@@ -434,6 +492,403 @@ int dense_tile_layout(int ta, int tb, const T* A, int64_t lda, const T* B, int64
   return dense_tile<T, OT, 256, 256, true, false>(A, lda, B, ldb, C, ldc, bias, M, N, K, st);
 }
 
+// ===========================================================================
+// Grouped expert products (MoE) over the segments of an expert-sorted row list
+// ===========================================================================
+// Rows of the activation operands are sorted by expert: expert e owns rows
+// [seg[e], seg[e+1]). Row-tiled products place one 256-row M-tile of one
+// expert per workgroup (toff[e] = first M-tile of expert e, the prefix sum of
+// ceil(n_e / 256); surplus workgroups exit). Weight-gradient products reduce
+// over an expert's rows (K = n_e) and place (expert, part, M-tile, N-tile).
+// Expert weights are separate tensors reached through device pointer tables.
+constexpr int kMoeTileM = 256;
+
+// Workgroup id remapped so each XCD takes a contiguous run of logical tiles
+// (grids are padded to a multiple of 8).
+__device__ __forceinline__ int xcd_logical_tile() {
+  const int pid = blockIdx.x, nblk = gridDim.x;
+  return (nblk & 7) == 0 ? (pid & 7) * (nblk >> 3) + (pid >> 3) : pid;
+}
+
+// M-tile tm of the expert-sorted rows: expert e, first row, valid rows.
+__device__ __forceinline__ bool seg_tile(const int32_t* seg, const int32_t* toff, int E, int tm, int& e, int& row0,
+                                         int& rows) {
+  if (tm >= toff[E]) return false;
+  int lo = 0, hi = E;  // largest e with toff[e] <= tm
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (toff[mid] <= tm) lo = mid;
+    else hi = mid;
+  }
+  e = lo;
+  row0 = seg[e] + (tm - toff[e]) * kMoeTileM;
+  rows = min(kMoeTileM, seg[e + 1] - row0);
+  return true;
+}
+
+// Gate/up: [G | U](rows of e) = Xs(rows) [Wg_e ; Wu_e]^T, H = silu(G) * U.
+// An N-tile holds 128 features: its 256 B-rows alternate 32-row blocks of
+// gate and up rows, so each wavefront's two 32-column MFMA tiles hold the
+// same features of gate and up and the epilogue forms H directly (G and U are
+// rounded to T first, as the expert MLP's two GEMMs would).
+template <typename T>
+struct MoeUpProblem {
+  const T* X;
+  const T* const* Wt;  // 2E pointers: gate_e, up_e
+  T *G, *U, *H;        // G and U may be null
+  const int32_t *seg, *toff;
+  int64_t ldx, ldw, ldo;
+  int E, I, Kdim, tiles_n;
+  __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
+    const int t = xcd_logical_tile();
+    int e, row0, rows;
+    if (!seg_tile(seg, toff, E, t / tiles_n, e, row0, rows)) return false;
+    c.m0 = row0;
+    c.n0 = (t % tiles_n) * 128;
+    c.K = Kdim;
+    c.vm = rows;
+    c.vn = 256;  // I is a multiple of 128
+    c.lda = ldx;
+    c.ldb = ldw;
+    c.aux = e;
+    c.w0 = Wt[2 * e];
+    c.w1 = Wt[2 * e + 1];
+    return true;
+  }
+  __device__ __forceinline__ const T* a_at(const TileCtx<T>& c, int i, int k) const {
+    return X + (int64_t)(c.m0 + i) * ldx + k;
+  }
+  __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
+    const int b = i >> 5;
+    const T* W = (b & 1) ? c.w1 : c.w0;
+    return W + (int64_t)(c.n0 + (b >> 1) * 32 + (i & 31)) * ldw + k;
+  }
+  static constexpr bool kVecEpilogue = true;
+  __device__ __forceinline__ bool vec_ok() const { return true; }
+  // Wavefront tile columns 0..31 hold gate and 32..63 up values of the same 32
+  // features.
+  template <class ET>
+  __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
+    const int row_end = c.m0 + c.vm;
+    for (int q = lane; q < 128 * 4; q += 64) {
+      const int r = q >> 2, c8 = q & 3;
+      const int row = c.m0 + wr + r;
+      if (row >= row_end) continue;
+      const Vec16<T> gv = et.row8(r, c8), uv = et.row8(r, c8 + 4);
+      Vec16<T> hv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float gf = to_f32(gv.v[e]);
+        hv.v[e] = from_f32<T>(gf * sigmoidf_(gf) * to_f32(uv.v[e]));
+      }
+      const int64_t o = (int64_t)row * ldo + c.n0 + (wc >> 1) + 8 * c8;
+      st16(H + o, hv);
+      if (G != nullptr) {
+        st16(G + o, gv);
+        st16(U + o, uv);
+      }
+    }
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ void epilogue(const TileCtx<T>& c, const f32x16 (&acc)[TM][TN], int wr, int wc,
+                                           int lane) const {
+    static_assert(TN == 2, "one gate and one up MFMA tile per wavefront");
+    const int f = c.n0 + (wc >> 1) + (lane & 31);  // wavefront wc/64 holds features 32 (wc/64) ..
+    const int row_end = c.m0 + c.vm;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int rb = c.m0 + wr + 32 * i + 4 * (lane >> 5);
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = rb + 8 * g + r;
+          if (row >= row_end) continue;
+          const T gt = (T)acc[i][0][4 * g + r], up = (T)acc[i][1][4 * g + r];
+          const float gf = to_f32(gt);
+          const int64_t o = (int64_t)row * ldo + f;
+          H[o] = from_f32<T>(gf * sigmoidf_(gf) * to_f32(up));
+          if (G != nullptr) {
+            G[o] = gt;
+            U[o] = up;
+          }
+        }
+    }
+  }
+};
+
+// Row-tiled product with one expert matrix per segment: C(rows of e) =
+// A(rows) op(W_e), W_e either [N, K] ("N", the down projection) or [K, N]
+// ("T", the down projection's input gradient). Epilogues:
+//   0: C = round(acc)
+//   1: C = round(round(acc) * w[row])  (routing-weight scaling)
+//   2: SiLU-mul backward: go = round(acc), with g = G[row, col], u = U[row, col]
+//      and s = sigmoid(g): C = go u s (1 + g (1 - s)), C2 = go g s
+template <typename T, bool BT, int EPI>
+struct MoeRowProblem {
+  const T* A;
+  const T* const* Wt;  // E pointers
+  T* C;
+  T* C2;
+  const T* wrow;
+  const T *G, *U;
+  const int32_t *seg, *toff;
+  int64_t lda, ldw, ldc, ldg;
+  int E, N, Kdim, tiles_n;
+  __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
+    const int t = xcd_logical_tile();
+    int e, row0, rows;
+    if (!seg_tile(seg, toff, E, t / tiles_n, e, row0, rows)) return false;
+    c.m0 = row0;
+    c.n0 = (t % tiles_n) * 256;
+    c.K = Kdim;
+    c.vm = rows;
+    c.vn = N - c.n0;
+    c.lda = lda;
+    c.ldb = ldw;
+    c.aux = e;
+    c.w0 = Wt[e];
+    c.w1 = nullptr;
+    return true;
+  }
+  __device__ __forceinline__ const T* a_at(const TileCtx<T>& c, int i, int k) const {
+    return A + (int64_t)(c.m0 + i) * lda + k;
+  }
+  __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
+    return BT ? c.w0 + (int64_t)k * ldw + (c.n0 + i) : c.w0 + (int64_t)(c.n0 + i) * ldw + k;
+  }
+  static constexpr bool kVecEpilogue = true;
+  __device__ __forceinline__ bool vec_ok() const { return true; }
+  template <class ET>
+  __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
+    const int row_end = c.m0 + c.vm;
+    for (int q = lane; q < 128 * 8; q += 64) {
+      const int r = q >> 3, c8 = q & 7;
+      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
+      if (row >= row_end || col >= N) continue;
+      const Vec16<T> v = et.row8(r, c8);
+      const int64_t o = (int64_t)row * ldc + col;
+      if constexpr (EPI == 0) {
+        st16(C + o, v);
+      } else if constexpr (EPI == 1) {
+        const float w = to_f32(wrow[row]);
+        Vec16<T> out;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out.v[e] = from_f32<T>(to_f32(v.v[e]) * w);
+        st16(C + o, out);
+      } else {
+        const int64_t og = (int64_t)row * ldg + col;
+        const Vec16<T> gv = ld16(G + og), uv = ld16(U + og);
+        Vec16<T> dg, du;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float go = to_f32(v.v[e]), gf = to_f32(gv.v[e]), uf = to_f32(uv.v[e]);
+          const float sg = sigmoidf_(gf);
+          dg.v[e] = from_f32<T>(go * uf * sg * (1.f + gf * (1.f - sg)));
+          du.v[e] = from_f32<T>(go * gf * sg);
+        }
+        st16(C + o, dg);
+        st16(C2 + o, du);
+      }
+    }
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ void epilogue(const TileCtx<T>& c, const f32x16 (&acc)[TM][TN], int wr, int wc,
+                                           int lane) const {
+    const int row_end = c.m0 + c.vm;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = c.n0 + wc + 32 * j + (lane & 31);
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int rb = c.m0 + wr + 32 * i + 4 * (lane >> 5);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = rb + 8 * g + r;
+            if (row >= row_end) continue;
+            const int64_t o = (int64_t)row * ldc + col;
+            const float v = to_f32((T)acc[i][j][4 * g + r]);
+            if constexpr (EPI == 0) {
+              C[o] = from_f32<T>(v);
+            } else if constexpr (EPI == 1) {
+              C[o] = from_f32<T>(v * to_f32(wrow[row]));
+            } else {
+              const int64_t og = (int64_t)row * ldg + col;
+              const float gf = to_f32(G[og]), uf = to_f32(U[og]);
+              const float sg = sigmoidf_(gf);
+              C[o] = from_f32<T>(v * uf * sg * (1.f + gf * (1.f - sg)));
+              C2[o] = from_f32<T>(v * gf * sg);
+            }
+          }
+      }
+    }
+  }
+};
+
+// Input gradient of the gate/up projections: dX(rows of e) = [dG | dU] (rows)
+// [Wg_e ; Wu_e] (K = 2I; I is a multiple of 64 so no k-tile straddles).
+template <typename T>
+struct MoeDxProblem {
+  const T *dG, *dU;
+  const T* const* Wt;  // 2E pointers: gate_e, up_e ([I, H] each)
+  T* C;
+  const int32_t *seg, *toff;
+  int64_t ldg, ldw, ldc;
+  int E, I, N, tiles_n;
+  __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
+    const int t = xcd_logical_tile();
+    int e, row0, rows;
+    if (!seg_tile(seg, toff, E, t / tiles_n, e, row0, rows)) return false;
+    c.m0 = row0;
+    c.n0 = (t % tiles_n) * 256;
+    c.K = 2 * I;
+    c.vm = rows;
+    c.vn = N - c.n0;
+    c.lda = ldg;
+    c.ldb = ldw;
+    c.aux = e;
+    c.w0 = Wt[2 * e];
+    c.w1 = Wt[2 * e + 1];
+    return true;
+  }
+  __device__ __forceinline__ const T* a_at(const TileCtx<T>& c, int i, int k) const {
+    return k < I ? dG + (int64_t)(c.m0 + i) * ldg + k : dU + (int64_t)(c.m0 + i) * ldg + (k - I);
+  }
+  __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
+    return k < I ? c.w0 + (int64_t)k * ldw + (c.n0 + i) : c.w1 + (int64_t)(k - I) * ldw + (c.n0 + i);
+  }
+  static constexpr bool kVecEpilogue = true;
+  __device__ __forceinline__ bool vec_ok() const { return true; }
+  template <class ET>
+  __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
+    const int row_end = c.m0 + c.vm;
+    for (int q = lane; q < 128 * 8; q += 64) {
+      const int r = q >> 3, c8 = q & 7;
+      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
+      if (row < row_end && col < N) st16(C + (int64_t)row * ldc + col, et.row8(r, c8));
+    }
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ void epilogue(const TileCtx<T>& c, const f32x16 (&acc)[TM][TN], int wr, int wc,
+                                           int lane) const {
+    const int row_end = c.m0 + c.vm;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = c.n0 + wc + 32 * j + (lane & 31);
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int rb = c.m0 + wr + 32 * i + 4 * (lane >> 5);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = rb + 8 * g + r;
+            if (row < row_end) C[(int64_t)row * ldc + col] = from_f32<T>(acc[i][j][4 * g + r]);
+          }
+      }
+    }
+  }
+};
+
+// Weight gradients: C_e[m, n] = sum over rows r of expert e of A[r, m] B[r, n]
+// (both operands k-outer, K = n_e). NP parts share the B operand and have
+// their own A and output (gate and up: NP = 2; down: NP = 1). Output e of part
+// q is Out[q] + e * out_stride, row-major with row stride ldo.
+template <typename T, int NP>
+struct MoeWgradProblem {
+  const T* A[NP];
+  const T* B;
+  T* Out[NP];
+  const int32_t* seg;
+  int64_t lda, ldb, ldo, out_stride;
+  int E, M, N, tiles_m, tiles_n;
+  __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
+    const int t = xcd_logical_tile();
+    const int per_part = tiles_m * tiles_n;
+    const int per_e = NP * per_part;
+    const int e = t / per_e;
+    if (e >= E) return false;
+    const int q = (t % per_e) / per_part, rest = t % per_part;
+    c.m0 = (rest / tiles_n) * 256;
+    c.n0 = (rest % tiles_n) * 256;
+    const int s0 = seg[e];
+    c.K = seg[e + 1] - s0;
+    c.vm = M - c.m0;
+    c.vn = N - c.n0;
+    c.lda = lda;
+    c.ldb = ldb;
+    c.aux = e;
+    c.aux2 = s0;
+    c.w0 = A[0];
+    c.out = Out[0];
+    if constexpr (NP > 1) {
+      if (q == 1) {
+        c.w0 = A[1];
+        c.out = Out[1];
+      }
+    }
+    return true;
+  }
+  __device__ __forceinline__ const T* a_at(const TileCtx<T>& c, int i, int k) const {
+    return c.w0 + (int64_t)(c.aux2 + k) * lda + (c.m0 + i);
+  }
+  __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
+    return B + (int64_t)(c.aux2 + k) * ldb + (c.n0 + i);
+  }
+  static constexpr bool kVecEpilogue = true;
+  __device__ __forceinline__ bool vec_ok() const { return true; }
+  template <class ET>
+  __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
+    T* out = c.out + (int64_t)c.aux * out_stride;
+    for (int q = lane; q < 128 * 8; q += 64) {
+      const int r = q >> 3, c8 = q & 7;
+      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
+      if (row < M && col < N) st16(out + (int64_t)row * ldo + col, et.row8(r, c8));
+    }
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ void epilogue(const TileCtx<T>& c, const f32x16 (&acc)[TM][TN], int wr, int wc,
+                                           int lane) const {
+    T* out = c.out + (int64_t)c.aux * out_stride;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = c.n0 + wc + 32 * j + (lane & 31);
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int rb = c.m0 + wr + 32 * i + 4 * (lane >> 5);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = rb + 8 * g + r;
+            if (row < M) out[(int64_t)row * ldo + col] = from_f32<T>(acc[i][j][4 * g + r]);
+          }
+      }
+    }
+  }
+};
+
+// Grid of a row-tiled grouped product: every possible M-tile (an upper bound:
+// ceil(R / 256) + E) times the N-tiles, padded to a multiple of 8.
+inline int moe_row_grid(int64_t R, int64_t E, int tiles_n) {
+  const int64_t g = ((R + kMoeTileM - 1) / kMoeTileM + E) * tiles_n;
+  return (int)((g + 7) / 8 * 8);
+}
+
+template <typename T, bool AT, bool BT, class P>
+int launch_moe(const P& p, int64_t grid, hipStream_t st, const char* name) {
+  if (grid >= (1ll << 31)) {
+    qh::set_error("%s: too many tiles", name);
+    return QH_E_ARG;
+  }
+  return launch_tile<T, 256, 256, kDenseBK, kDenseNS, AT, BT>(p, (int)grid, st, name);
+}
+
 }  // namespace
 
 // Large-tile path of qh_gemm (called by its dispatcher; not part of the C ABI).
@@ -461,4 +916,206 @@ int qh_gemm_tile_dispatch(int ta, int tb, int M, int N, int K, const void* A, in
 #undef QH_TILE_OUT
   qh::set_error("qh_gemm: the tile path takes bf16/f16 operands");
   return QH_E_DTYPE;
+}
+
+// ===========================================================================
+// C ABI: grouped expert products
+// ===========================================================================
+namespace {
+bool moe_ok(const void* p, int64_t ld) { return aligned16(p) && ld % 8 == 0; }
+}  // namespace
+
+extern "C" int qh_moe_up(const void* X, int64_t ldx, int64_t R, int64_t K, const void* const* gu_table, int64_t ldw,
+                         int64_t I, const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* G, void* U,
+                         void* H, int64_t ldo, int dtype, void* stream) {
+  QH_CHECK_ARG(R >= 0 && K > 0 && I > 0 && E > 0 && E <= 65536, "qh_moe_up: bad shape");
+  QH_CHECK_ARG(I % 128 == 0 && K % 8 == 0 && ldo >= I, "qh_moe_up: needs I %% 128 == 0, K %% 8 == 0");
+  QH_CHECK_ARG(moe_ok(X, ldx) && ldw % 8 == 0 && moe_ok(H, ldo) && (G == nullptr) == (U == nullptr),
+               "qh_moe_up: operands must be 16-byte aligned with strides multiples of 8");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_up: bf16/f16 only");
+  if (R == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int tn = (int)(I / 128);
+  int rc = QH_OK;
+#define QH_UP(T)                                                                                        \
+  {                                                                                                     \
+    MoeUpProblem<T> p;                                                                                  \
+    p.X = (const T*)X;                                                                                  \
+    p.Wt = (const T* const*)gu_table;                                                                   \
+    p.G = (T*)G;                                                                                        \
+    p.U = (T*)U;                                                                                        \
+    p.H = (T*)H;                                                                                        \
+    p.seg = seg_off;                                                                                    \
+    p.toff = tile_off;                                                                                  \
+    p.ldx = ldx;                                                                                        \
+    p.ldw = ldw;                                                                                        \
+    p.ldo = ldo;                                                                                        \
+    p.E = (int)E;                                                                                       \
+    p.I = (int)I;                                                                                       \
+    p.Kdim = (int)K;                                                                                    \
+    p.tiles_n = tn;                                                                                     \
+    rc = launch_moe<T, false, false>(p, moe_row_grid(R, E, tn), st, "qh_moe_up");                       \
+  }
+  if (dtype == QH_BF16) QH_UP(bf16_t) else QH_UP(f16_t)
+#undef QH_UP
+  if (rc) return rc;
+  QH_CHECK_LAUNCH("qh_moe_up");
+  return QH_OK;
+}
+
+namespace {
+template <typename T, bool BT, int EPI>
+int moe_row_launch(const void* A, int64_t lda, int64_t R, int64_t K, const void* const* table, int64_t ldw, int64_t N,
+                   const int32_t* seg, const int32_t* toff, int64_t E, void* C, void* C2, int64_t ldc,
+                   const void* wrow, const void* G, const void* U, int64_t ldg, hipStream_t st, const char* name) {
+  MoeRowProblem<T, BT, EPI> p;
+  p.A = (const T*)A;
+  p.Wt = (const T* const*)table;
+  p.C = (T*)C;
+  p.C2 = (T*)C2;
+  p.wrow = (const T*)wrow;
+  p.G = (const T*)G;
+  p.U = (const T*)U;
+  p.seg = seg;
+  p.toff = toff;
+  p.lda = lda;
+  p.ldw = ldw;
+  p.ldc = ldc;
+  p.ldg = ldg;
+  p.E = (int)E;
+  p.N = (int)N;
+  p.Kdim = (int)K;
+  p.tiles_n = (int)((N + 255) / 256);
+  return launch_moe<T, false, BT>(p, moe_row_grid(R, E, p.tiles_n), st, name);
+}
+}  // namespace
+
+extern "C" int qh_moe_down(const void* A, int64_t lda, int64_t R, int64_t K, const void* const* d_table, int64_t ldw,
+                           int64_t N, const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* C,
+                           int64_t ldc, const void* wrow, int dtype, void* stream) {
+  QH_CHECK_ARG(R >= 0 && K > 0 && N > 0 && E > 0 && E <= 65536 && K % 8 == 0 && ldc >= N,
+               "qh_moe_down: bad shape");
+  QH_CHECK_ARG(moe_ok(A, lda) && ldw % 8 == 0, "qh_moe_down: A must be 16-byte aligned with strides multiples of 8");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_down: bf16/f16 only");
+  if (R == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  int rc;
+  if (dtype == QH_BF16)
+    rc = wrow ? moe_row_launch<bf16_t, false, 1>(A, lda, R, K, d_table, ldw, N, seg_off, tile_off, E, C, nullptr, ldc,
+                                                 wrow, nullptr, nullptr, 0, st, "qh_moe_down")
+              : moe_row_launch<bf16_t, false, 0>(A, lda, R, K, d_table, ldw, N, seg_off, tile_off, E, C, nullptr, ldc,
+                                                 nullptr, nullptr, nullptr, 0, st, "qh_moe_down");
+  else
+    rc = wrow ? moe_row_launch<f16_t, false, 1>(A, lda, R, K, d_table, ldw, N, seg_off, tile_off, E, C, nullptr, ldc,
+                                                wrow, nullptr, nullptr, 0, st, "qh_moe_down")
+              : moe_row_launch<f16_t, false, 0>(A, lda, R, K, d_table, ldw, N, seg_off, tile_off, E, C, nullptr, ldc,
+                                                nullptr, nullptr, nullptr, 0, st, "qh_moe_down");
+  if (rc) return rc;
+  QH_CHECK_LAUNCH("qh_moe_down");
+  return QH_OK;
+}
+
+extern "C" int qh_moe_down_dgrad(const void* dD, int64_t ldd, int64_t R, int64_t K, const void* const* d_table,
+                                 int64_t ldw, int64_t I, const int32_t* seg_off, const int32_t* tile_off, int64_t E,
+                                 const void* G, const void* U, int64_t ldg, void* dG, void* dU, int64_t ldo,
+                                 int dtype, void* stream) {
+  QH_CHECK_ARG(R >= 0 && K > 0 && I > 0 && E > 0 && E <= 65536 && K % 8 == 0 && I % 8 == 0,
+               "qh_moe_down_dgrad: bad shape");
+  QH_CHECK_ARG(moe_ok(dD, ldd) && ldw % 8 == 0 && ldo >= I && ldg >= I,
+               "qh_moe_down_dgrad: operands must be 16-byte aligned with strides multiples of 8");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_down_dgrad: bf16/f16 only");
+  if (R == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int rc = dtype == QH_BF16
+                     ? moe_row_launch<bf16_t, true, 2>(dD, ldd, R, K, d_table, ldw, I, seg_off, tile_off, E, dG, dU,
+                                                       ldo, nullptr, G, U, ldg, st, "qh_moe_down_dgrad")
+                     : moe_row_launch<f16_t, true, 2>(dD, ldd, R, K, d_table, ldw, I, seg_off, tile_off, E, dG, dU,
+                                                      ldo, nullptr, G, U, ldg, st, "qh_moe_down_dgrad");
+  if (rc) return rc;
+  QH_CHECK_LAUNCH("qh_moe_down_dgrad");
+  return QH_OK;
+}
+
+extern "C" int qh_moe_up_dgrad(const void* dG, const void* dU, int64_t ldg, int64_t R, int64_t I,
+                               const void* const* gu_table, int64_t ldw, int64_t N, const int32_t* seg_off,
+                               const int32_t* tile_off, int64_t E, void* dX, int64_t ldx, int dtype, void* stream) {
+  QH_CHECK_ARG(R >= 0 && I > 0 && N > 0 && E > 0 && E <= 65536 && I % 64 == 0 && N % 8 == 0 && ldx >= N,
+               "qh_moe_up_dgrad: bad shape (I must be a multiple of 64)");
+  QH_CHECK_ARG(moe_ok(dG, ldg) && moe_ok(dU, ldg) && ldw % 8 == 0,
+               "qh_moe_up_dgrad: operands must be 16-byte aligned with strides multiples of 8");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_up_dgrad: bf16/f16 only");
+  if (R == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int tn = (int)((N + 255) / 256);
+  int rc = QH_OK;
+#define QH_DX(T)                                                              \
+  {                                                                           \
+    MoeDxProblem<T> p;                                                        \
+    p.dG = (const T*)dG;                                                      \
+    p.dU = (const T*)dU;                                                      \
+    p.Wt = (const T* const*)gu_table;                                         \
+    p.C = (T*)dX;                                                             \
+    p.seg = seg_off;                                                          \
+    p.toff = tile_off;                                                        \
+    p.ldg = ldg;                                                              \
+    p.ldw = ldw;                                                              \
+    p.ldc = ldx;                                                              \
+    p.E = (int)E;                                                             \
+    p.I = (int)I;                                                             \
+    p.N = (int)N;                                                             \
+    p.tiles_n = tn;                                                           \
+    rc = launch_moe<T, false, true>(p, moe_row_grid(R, E, tn), st, "qh_moe_up_dgrad"); \
+  }
+  if (dtype == QH_BF16) QH_DX(bf16_t) else QH_DX(f16_t)
+#undef QH_DX
+  if (rc) return rc;
+  QH_CHECK_LAUNCH("qh_moe_up_dgrad");
+  return QH_OK;
+}
+
+extern "C" int qh_moe_wgrad(int parts, const void* A0, const void* A1, int64_t lda, int64_t M, const void* B,
+                            int64_t ldb, int64_t N, const int32_t* seg_off, int64_t E, void* out0, void* out1,
+                            int64_t ldo, int64_t out_stride, int dtype, void* stream) {
+  QH_CHECK_ARG(parts == 1 || parts == 2, "qh_moe_wgrad: 1 or 2 parts");
+  QH_CHECK_ARG(M > 0 && N > 0 && E > 0 && E <= 65536 && M % 8 == 0 && N % 8 == 0 && ldo >= N,
+               "qh_moe_wgrad: bad shape (M, N multiples of 8)");
+  QH_CHECK_ARG(moe_ok(A0, lda) && moe_ok(B, ldb) && (parts == 1 || moe_ok(A1, lda)) && out0 != nullptr &&
+                   (parts == 1 || out1 != nullptr),
+               "qh_moe_wgrad: operands must be 16-byte aligned with strides multiples of 8");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_wgrad: bf16/f16 only");
+  hipStream_t st = (hipStream_t)stream;
+  const int tm = (int)((M + 255) / 256), tn = (int)((N + 255) / 256);
+  const int64_t grid = ((int64_t)E * parts * tm * tn + 7) / 8 * 8;
+  int rc = QH_OK;
+#define QH_WG(T, NP)                                              \
+  {                                                               \
+    MoeWgradProblem<T, NP> p;                                     \
+    p.A[0] = (const T*)A0;                                        \
+    p.Out[0] = (T*)out0;                                          \
+    if constexpr (NP > 1) {                                       \
+      p.A[NP - 1] = (const T*)A1;                                 \
+      p.Out[NP - 1] = (T*)out1;                                   \
+    }                                                             \
+    p.B = (const T*)B;                                            \
+    p.seg = seg_off;                                              \
+    p.lda = lda;                                                  \
+    p.ldb = ldb;                                                  \
+    p.ldo = ldo;                                                  \
+    p.out_stride = out_stride;                                    \
+    p.E = (int)E;                                                 \
+    p.M = (int)M;                                                 \
+    p.N = (int)N;                                                 \
+    p.tiles_m = tm;                                               \
+    p.tiles_n = tn;                                               \
+    rc = launch_moe<T, true, true>(p, grid, st, "qh_moe_wgrad");  \
+  }
+  if (dtype == QH_BF16) {
+    if (parts == 2) QH_WG(bf16_t, 2) else QH_WG(bf16_t, 1)
+  } else {
+    if (parts == 2) QH_WG(f16_t, 2) else QH_WG(f16_t, 1)
+  }
+#undef QH_WG
+  if (rc) return rc;
+  QH_CHECK_LAUNCH("qh_moe_wgrad");
+  return QH_OK;
 }

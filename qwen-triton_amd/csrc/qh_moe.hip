@@ -94,39 +94,108 @@ __global__ __launch_bounds__(256) void moe_rows(const uint32_t* __restrict__ val
   }
 }
 
-// One workgroup per token; each thread owns 8 consecutive columns.
+// One workgroup per token; each thread owns 8 consecutive columns. With
+// weights, row j contributes round(Y[p] * w[t, j]) (the routing-weight scaling
+// of the expert output), else Y[p] itself.
 template <typename T, int KMAX>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const T* __restrict__ Y, int64_t ldy,
                                                           const int32_t* __restrict__ inv,
-                                                          const int64_t* __restrict__ sel, int k, int64_t E,
+                                                          const int64_t* __restrict__ sel,
+                                                          const T* __restrict__ w, int k, int64_t E,
                                                           T* __restrict__ out, int64_t H) {
   const int64_t t = blockIdx.x;
   int64_t ek[KMAX];
   int32_t pk[KMAX];
+  float wk[KMAX];
   int nk = 0;
   for (int j = 0; j < k; ++j) {  // insertion by expert id (ids of one token are distinct)
     const int64_t e = sel[t * k + j];
     if (e < 0 || e >= E) continue;
     const int32_t p = inv[t * k + j];
+    const float wj = w ? to_f32(w[t * k + j]) : 1.f;
     int q = nk++;
     while (q > 0 && ek[q - 1] > e) {
       ek[q] = ek[q - 1];
       pk[q] = pk[q - 1];
+      wk[q] = wk[q - 1];
       --q;
     }
     ek[q] = e;
     pk[q] = p;
+    wk[q] = wj;
   }
   for (int64_t c = threadIdx.x * 8; c < H; c += 256 * 8) {
+    // all rows are requested before the ordered sum consumes them
+    Vec16<T> y[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+      if (j < nk) y[j] = ld16(Y + (int64_t)pk[j] * ldy + c);
     Vec16<T> acc;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc.v[e] = (T)0.f;
-    for (int j = 0; j < nk; ++j) {
-      const Vec16<T> y = ld16(Y + (int64_t)pk[j] * ldy + c);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc.v[e] = from_f32<T>(to_f32(acc.v[e]) + to_f32(y.v[e]));
+    for (int j = 0; j < KMAX; ++j) {
+      if (j >= nk) break;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float yv = w ? to_f32(from_f32<T>(to_f32(y[j].v[e]) * wk[j])) : to_f32(y[j].v[e]);
+        acc.v[e] = from_f32<T>(to_f32(acc.v[e]) + yv);
+      }
     }
     st16(out + t * H + c, acc);
+  }
+}
+
+// Xs[r] = X[rows[r]] (one workgroup per 4 rows, 16-byte vectors).
+template <typename T>
+__global__ __launch_bounds__(256) void moe_gather_kernel(const T* __restrict__ X, int64_t ldx,
+                                                         const int32_t* __restrict__ rows, int64_t R, int64_t H,
+                                                         T* __restrict__ Xs, int64_t lds) {
+  const int64_t r = blockIdx.x * 4ll + (threadIdx.x >> 6);
+  if (r >= R) return;
+  const T* src = X + (int64_t)rows[r] * ldx;
+  T* dst = Xs + r * lds;
+  for (int64_t c = (threadIdx.x & 63) * 8; c < H; c += 64 * 8) st16(dst + c, ld16(src + c));
+}
+
+// Backward of the routing-weight scaling, one workgroup per token t: for each
+// of its expert rows p (slot j), dD[p] = round(dout[t] * w[t, j]) and
+// dw[t, j] = round(sum_c dout[t, c] * D[p, c]) (fp32, fixed-order block sum).
+// Slots with an out-of-range expert id get dw = 0.
+template <typename T>
+__global__ __launch_bounds__(256) void moe_scale_bwd_kernel(const T* __restrict__ dout, int64_t ldo,
+                                                            const T* __restrict__ D, int64_t ldd,
+                                                            const T* __restrict__ w, const int32_t* __restrict__ inv,
+                                                            const int64_t* __restrict__ sel, int k, int64_t E,
+                                                            int64_t H, T* __restrict__ dD, int64_t ldg,
+                                                            T* __restrict__ dw) {
+  __shared__ float red[4];
+  const int64_t t = blockIdx.x;
+  const T* go = dout + t * ldo;
+  for (int j = 0; j < k; ++j) {
+    const int64_t e = sel[t * k + j];
+    if (e < 0 || e >= E) {
+      if (threadIdx.x == 0) dw[t * k + j] = (T)0.f;
+      continue;
+    }
+    const int64_t p = inv[t * k + j];
+    const float wj = to_f32(w[t * k + j]);
+    const T* drow = D + p * ldd;
+    T* grow = dD + p * ldg;
+    float s = 0.f;
+    for (int64_t c = threadIdx.x * 8; c < H; c += 256 * 8) {
+      const Vec16<T> g = ld16(go + c), d = ld16(drow + c);
+      Vec16<T> o;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float gf = to_f32(g.v[q]);
+        o.v[q] = from_f32<T>(gf * wj);
+        s += gf * to_f32(d.v[q]);
+      }
+      st16(grow + c, o);
+    }
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) dw[t * k + j] = from_f32<T>(s);
   }
 }
 
@@ -182,8 +251,8 @@ extern "C" int qh_moe_dispatch(const int64_t* selected, const void* weights, int
 }
 
 extern "C" int qh_moe_combine(const void* Y, int64_t ldy, const int32_t* inv, const int64_t* selected,
-                              int64_t n_tokens, int64_t top_k, int64_t n_experts, void* out, int64_t H, int dtype,
-                              void* stream) {
+                              const void* weights, int64_t n_tokens, int64_t top_k, int64_t n_experts, void* out,
+                              int64_t H, int dtype, void* stream) {
   QH_CHECK_ARG(n_tokens >= 0 && top_k > 0 && top_k <= 32 && H > 0 && n_experts > 0, "qh_moe_combine: bad shape");
   QH_CHECK_ARG(H % 8 == 0 && ldy % 8 == 0 && aligned16(Y) && aligned16(out),
                "qh_moe_combine: rows must be 16-byte aligned with H, ldy multiples of 8");
@@ -192,7 +261,8 @@ extern "C" int qh_moe_combine(const void* Y, int64_t ldy, const int32_t* inv, co
   if (n_tokens == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;
 #define QH_COMB(T, KM) \
-  moe_combine_kernel<T, KM><<<(unsigned)n_tokens, 256, 0, st>>>((const T*)Y, ldy, inv, selected, (int)top_k, n_experts, (T*)out, H)
+  moe_combine_kernel<T, KM><<<(unsigned)n_tokens, 256, 0, st>>>((const T*)Y, ldy, inv, selected, (const T*)weights, \
+                                                                 (int)top_k, n_experts, (T*)out, H)
   if (dtype == QH_BF16) {
     if (top_k <= 8) QH_COMB(bf16_t, 8); else QH_COMB(bf16_t, 32);
   } else {
@@ -200,5 +270,44 @@ extern "C" int qh_moe_combine(const void* Y, int64_t ldy, const int32_t* inv, co
   }
 #undef QH_COMB
   QH_CHECK_LAUNCH("qh_moe_combine");
+  return QH_OK;
+}
+
+extern "C" int qh_moe_gather(const void* X, int64_t ldx, const int32_t* rows, int64_t R, int64_t H, void* Xs,
+                             int64_t lds, int dtype, void* stream) {
+  QH_CHECK_ARG(R >= 0 && H > 0 && R < (1ll << 33), "qh_moe_gather: bad shape");
+  QH_CHECK_ARG(H % 8 == 0 && ldx % 8 == 0 && lds % 8 == 0 && lds >= H && aligned16(X) && aligned16(Xs),
+               "qh_moe_gather: rows must be 16-byte aligned with H and strides multiples of 8");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_gather: bf16/f16 only");
+  if (R == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const unsigned g = (unsigned)((R + 3) / 4);
+  if (dtype == QH_BF16)
+    moe_gather_kernel<bf16_t><<<g, 256, 0, st>>>((const bf16_t*)X, ldx, rows, R, H, (bf16_t*)Xs, lds);
+  else
+    moe_gather_kernel<f16_t><<<g, 256, 0, st>>>((const f16_t*)X, ldx, rows, R, H, (f16_t*)Xs, lds);
+  QH_CHECK_LAUNCH("qh_moe_gather");
+  return QH_OK;
+}
+
+extern "C" int qh_moe_scale_bwd(const void* dout, int64_t ldo, const void* D, int64_t ldd, const void* weights,
+                                const int32_t* inv, const int64_t* selected, int64_t n_tokens, int64_t top_k,
+                                int64_t n_experts, int64_t H, void* dD, int64_t ldg, void* dw, int dtype,
+                                void* stream) {
+  QH_CHECK_ARG(n_tokens >= 0 && top_k > 0 && H > 0 && n_experts > 0 && n_tokens < (1ll << 31),
+               "qh_moe_scale_bwd: bad shape");
+  QH_CHECK_ARG(H % 8 == 0 && ldo % 8 == 0 && ldd % 8 == 0 && ldg % 8 == 0 && aligned16(dout) && aligned16(D) &&
+                   aligned16(dD),
+               "qh_moe_scale_bwd: rows must be 16-byte aligned with H and strides multiples of 8");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_scale_bwd: bf16/f16 only");
+  if (n_tokens == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+#define QH_SB(T)                                                                                              \
+  moe_scale_bwd_kernel<T><<<(unsigned)n_tokens, 256, 0, st>>>((const T*)dout, ldo, (const T*)D, ldd,          \
+                                                              (const T*)weights, inv, selected, (int)top_k,   \
+                                                              n_experts, H, (T*)dD, ldg, (T*)dw)
+  if (dtype == QH_BF16) QH_SB(bf16_t); else QH_SB(f16_t);
+#undef QH_SB
+  QH_CHECK_LAUNCH("qh_moe_scale_bwd");
   return QH_OK;
 }

@@ -11,6 +11,16 @@ all experts (``qh_moe_gemm``: gate/up with the token gather and SiLU-mul fused,
 down with the routing-weight scaling fused), and ``qh_moe_combine`` sums each
 token's expert rows in ascending expert order with the reference's bf16
 rounding after every add. No host synchronisation; deterministic.
+
+Training (autograd on) runs ``GroupedExperts``: the same dispatch (with 256-row
+tiles), a gather of the routed rows, grouped GEMMs on the 256x256 tile kernel
+(gate/up writing G, U and H = silu(G) U; down writing the unscaled expert
+output D) and the combine with the routing-weight multiply fused. Its backward
+mirrors the reference loop's autograd graph: the routing-weight multiply
+(dD, d_weights), the down projection's input gradient with the SiLU-mul
+backward fused (dG, dU), the gate/up input gradient (one K = 2I product),
+the ordered combine of the routed rows' gradients, and the expert weight
+gradients as grouped products that reduce over each expert's rows.
 """
 from __future__ import annotations
 
@@ -54,6 +64,103 @@ def moe_experts_forward(flat: torch.Tensor, routing_weights: torch.Tensor, selec
                  weight_row_stride[1], y.data_ptr(), hidden, wsorted.data_ptr(), seg.data_ptr(), toff.data_ptr(), r,
                  n_experts, hidden, intermediate, code, st)
     out = torch.empty((t, hidden), dtype=dt, device=dev)
-    _native.call("qh_moe_combine", y.data_ptr(), hidden, inv.data_ptr(), sel.data_ptr(), t, k, n_experts,
+    _native.call("qh_moe_combine", y.data_ptr(), hidden, inv.data_ptr(), sel.data_ptr(), None, t, k, n_experts,
                  out.data_ptr(), hidden, code, st)
     return out
+
+
+TRAIN_TILE_M = 256
+
+
+def grouped_training_ok(hidden: int, intermediate: int) -> bool:
+    """Shapes the training kernels take (the feature dimensions tile evenly)."""
+    return intermediate % 128 == 0 and hidden % 8 == 0
+
+
+class GroupedExperts(torch.autograd.Function):
+    """Experts of the sparse MoE block with the reference loop's gradients.
+
+    Inputs: flat [T, H], routing_weights [T, k] (flat's dtype), selected [T, k]
+    int64, the device pointer tables (gate/up interleaved, down), the sizes,
+    then the 3E expert weight tensors (gate_0, up_0, down_0, gate_1, ...) so
+    autograd routes their gradients.
+    """
+
+    @staticmethod
+    def forward(ctx, flat, routing_weights, selected, gu_table, dn_table, n_experts, intermediate, ldw_gu, ldw_dn,
+                *weights):
+        _native.require_device(flat, routing_weights, selected)
+        t, hidden = flat.shape
+        k = selected.shape[1]
+        r = t * k
+        dev, dt = flat.device, flat.dtype
+        code = _native.dtype_code(dt)
+        st = _native.stream(dev)
+        sel = selected.contiguous()
+        w = routing_weights.to(dt).contiguous()
+        ws = _native.workspace(_native.call("qh_moe_dispatch_workspace", t, k, n_experts), dev)
+        rows = torch.empty(r, dtype=torch.int32, device=dev)
+        wsorted = torch.empty(r, dtype=dt, device=dev)
+        inv = torch.empty(r, dtype=torch.int32, device=dev)
+        seg = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+        toff = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+        _native.call("qh_moe_dispatch", sel.data_ptr(), w.data_ptr(), t, k, n_experts, TRAIN_TILE_M, ws.data_ptr(),
+                     ws.numel(), rows.data_ptr(), wsorted.data_ptr(), inv.data_ptr(), seg.data_ptr(), toff.data_ptr(),
+                     code, st)
+        x = flat.contiguous()
+        xs = torch.empty((r, hidden), dtype=dt, device=dev)
+        _native.call("qh_moe_gather", x.data_ptr(), hidden, rows.data_ptr(), r, hidden, xs.data_ptr(), hidden, code, st)
+        g = torch.empty((r, intermediate), dtype=dt, device=dev)
+        u = torch.empty_like(g)
+        h = torch.empty_like(g)
+        _native.call("qh_moe_up", xs.data_ptr(), hidden, r, hidden, gu_table.data_ptr(), ldw_gu, intermediate,
+                     seg.data_ptr(), toff.data_ptr(), n_experts, g.data_ptr(), u.data_ptr(), h.data_ptr(),
+                     intermediate, code, st)
+        d = torch.empty((r, hidden), dtype=dt, device=dev)
+        _native.call("qh_moe_down", h.data_ptr(), intermediate, r, intermediate, dn_table.data_ptr(), ldw_dn, hidden,
+                     seg.data_ptr(), toff.data_ptr(), n_experts, d.data_ptr(), hidden, None, code, st)
+        out = torch.empty((t, hidden), dtype=dt, device=dev)
+        _native.call("qh_moe_combine", d.data_ptr(), hidden, inv.data_ptr(), sel.data_ptr(), w.data_ptr(), t, k,
+                     n_experts, out.data_ptr(), hidden, code, st)
+        ctx.save_for_backward(w, sel, inv, seg, toff, xs, g, u, h, d, gu_table, dn_table)
+        ctx.sizes = (t, k, hidden, intermediate, n_experts, ldw_gu, ldw_dn)
+        ctx.weight_meta = [(wt.shape, wt.dtype) for wt in weights]
+        ctx.rw_dtype = routing_weights.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        w, sel, inv, seg, toff, xs, g, u, h, d, gu_table, dn_table = ctx.saved_tensors
+        t, k, hidden, inter, n_experts, ldw_gu, ldw_dn = ctx.sizes
+        r = t * k
+        dev, dt = xs.device, xs.dtype
+        code = _native.dtype_code(dt)
+        st = _native.stream(dev)
+        go = dout.to(dt).contiguous()
+        dd = torch.empty((r, hidden), dtype=dt, device=dev)
+        dw = torch.empty((t, k), dtype=dt, device=dev)
+        _native.call("qh_moe_scale_bwd", go.data_ptr(), hidden, d.data_ptr(), hidden, w.data_ptr(), inv.data_ptr(),
+                     sel.data_ptr(), t, k, n_experts, hidden, dd.data_ptr(), hidden, dw.data_ptr(), code, st)
+        dg = torch.empty((r, inter), dtype=dt, device=dev)
+        du = torch.empty_like(dg)
+        _native.call("qh_moe_down_dgrad", dd.data_ptr(), hidden, r, hidden, dn_table.data_ptr(), ldw_dn, inter,
+                     seg.data_ptr(), toff.data_ptr(), n_experts, g.data_ptr(), u.data_ptr(), inter, dg.data_ptr(),
+                     du.data_ptr(), inter, code, st)
+        dxs = torch.empty((r, hidden), dtype=dt, device=dev)
+        _native.call("qh_moe_up_dgrad", dg.data_ptr(), du.data_ptr(), inter, r, inter, gu_table.data_ptr(), ldw_gu,
+                     hidden, seg.data_ptr(), toff.data_ptr(), n_experts, dxs.data_ptr(), hidden, code, st)
+        dflat = torch.empty((t, hidden), dtype=dt, device=dev)
+        _native.call("qh_moe_combine", dxs.data_ptr(), hidden, inv.data_ptr(), sel.data_ptr(), None, t, k, n_experts,
+                     dflat.data_ptr(), hidden, code, st)
+        dwg = torch.empty((n_experts, inter, hidden), dtype=dt, device=dev)
+        dwu = torch.empty_like(dwg)
+        dwd = torch.empty((n_experts, hidden, inter), dtype=dt, device=dev)
+        _native.call("qh_moe_wgrad", 2, dg.data_ptr(), du.data_ptr(), inter, inter, xs.data_ptr(), hidden, hidden,
+                     seg.data_ptr(), n_experts, dwg.data_ptr(), dwu.data_ptr(), hidden, inter * hidden, code, st)
+        _native.call("qh_moe_wgrad", 1, dd.data_ptr(), None, hidden, hidden, h.data_ptr(), inter, inter,
+                     seg.data_ptr(), n_experts, dwd.data_ptr(), None, inter, hidden * inter, code, st)
+        wgrads = []
+        for e in range(n_experts):
+            wgrads.extend((dwg[e], dwu[e], dwd[e]))
+        wgrads = [gr.to(dtype_) if gr.dtype != dtype_ else gr for gr, (_, dtype_) in zip(wgrads, ctx.weight_meta)]
+        return (dflat, dw.to(ctx.rw_dtype), None, None, None, None, None, None, None, *wgrads)

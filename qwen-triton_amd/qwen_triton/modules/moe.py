@@ -7,9 +7,11 @@ to the lower expert index, optional renormalisation, routing weights cast to the
 activation dtype, per-expert SwiGLU on the tokens routed to it, scaled by the
 routing weight and scatter-added in ascending expert order.
 
-On the GPU without autograd the experts run as one sort/segment dispatch, two
-grouped expert GEMMs and an ordered combine (``kernels/moe_experts.py``), with
-the same rounding points as the loop.
+On the GPU the experts run as one sort/segment dispatch, grouped expert GEMMs
+and an ordered combine (``kernels/moe_experts.py``) with the loop's rounding
+points: without autograd through the inference kernels, with autograd through
+``GroupedExperts``, whose backward gives the loop's gradients (input, routing
+weights and every expert weight) from grouped products as well.
 """
 from __future__ import annotations
 
@@ -18,7 +20,7 @@ from torch import nn
 
 from qwen_triton import _native
 from qwen_triton.configs import QwenTritonConfig
-from qwen_triton.kernels.moe_experts import moe_experts_forward
+from qwen_triton.kernels.moe_experts import GroupedExperts, grouped_training_ok, moe_experts_forward
 from qwen_triton.kernels.moe_routing import triton_index_add, triton_one_hot, triton_topk
 from qwen_triton.kernels.sigmoid_mul import sigmoid_mul
 from qwen_triton.kernels.softmax import triton_softmax
@@ -64,8 +66,10 @@ class QwenSparseMoeBlock(nn.Module):
             out = out + sigmoid_mul(shared, gate_value.expand_as(shared))
         return out.view(batch, seq, hidden), router_logits
 
-    def _grouped_ok(self, flat: torch.Tensor) -> bool:
-        if torch.is_grad_enabled() or not flat.is_cuda or flat.dtype not in (torch.bfloat16, torch.float16):
+    def _grouped_ok(self, flat: torch.Tensor, training: bool = False) -> bool:
+        if torch.is_grad_enabled() != training or not flat.is_cuda or flat.dtype not in (torch.bfloat16, torch.float16):
+            return False
+        if training and not grouped_training_ok(flat.shape[1], self.moe_intermediate_size):
             return False
         if flat.shape[1] % 8 or self.moe_intermediate_size % 8 or not _native.available():
             return False
@@ -91,11 +95,16 @@ class QwenSparseMoeBlock(nn.Module):
         return self._tables[1], self._tables[2]
 
     def experts_forward(self, flat: torch.Tensor, routing_weights: torch.Tensor, selected: torch.Tensor) -> torch.Tensor:
+        strides = (self.experts[0].gate_proj.weight.stride(0), self.experts[0].down_proj.weight.stride(0))
         if self._grouped_ok(flat):
             gu, dn = self._expert_tables(flat.device)
-            strides = (self.experts[0].gate_proj.weight.stride(0), self.experts[0].down_proj.weight.stride(0))
             return moe_experts_forward(flat, routing_weights, selected, gu, dn, self.num_experts,
                                        self.moe_intermediate_size, strides)
+        if self._grouped_ok(flat, training=True):
+            gu, dn = self._expert_tables(flat.device)
+            weights = [p for e in self.experts for p in (e.gate_proj.weight, e.up_proj.weight, e.down_proj.weight)]
+            return GroupedExperts.apply(flat, routing_weights, selected, gu, dn, self.num_experts,
+                                        self.moe_intermediate_size, strides[0], strides[1], *weights)
         out = torch.zeros_like(flat)
         expert_mask = triton_one_hot(selected, self.num_experts).permute(2, 1, 0)
         hit = torch.nonzero(expert_mask.sum(dim=(-1, -2)) > 0, as_tuple=False).view(-1)

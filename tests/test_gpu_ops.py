@@ -589,6 +589,16 @@ def test_moe_dispatch_segments_are_a_stable_sort(T, k, E):
     assert torch.equal(inv.cpu().long()[order], torch.arange(R))
 
 
+def _loop_experts(blk, x, w, sel):
+    """The reference per-expert loop (grouped paths switched off for this call)."""
+    saved = blk._grouped_ok
+    blk._grouped_ok = lambda *a, **kw: False
+    try:
+        return blk.experts_forward(x, w, sel)
+    finally:
+        blk._grouped_ok = saved
+
+
 def _moe_block(E, k, hidden=256, inter=128, seed=0):
     from qwen_triton import QwenTritonConfig
     from qwen_triton.modules import QwenSparseMoeBlock
@@ -619,11 +629,50 @@ def test_moe_grouped_experts_match_loop(E, k, T):
         again = blk.experts_forward(x, w, sel)
     assert native_calls("qh_moe_gemm") == c0 + 4
     assert torch.equal(fused, again)
-    with torch.enable_grad():  # the reference per-expert loop
-        loop = blk.experts_forward(x, w, sel).detach()
+    loop = _loop_experts(blk, x, w, sel)
     close(fused, loop, atol=2e-2, rtol=2e-2)
     wg = torch.stack([ex.gate_proj.weight for ex in blk.experts]).float().cpu()
     wu = torch.stack([ex.up_proj.weight for ex in blk.experts]).float().cpu()
     wd = torch.stack([ex.down_proj.weight for ex in blk.experts]).float().cpu()
     ref, *_ = O.moe_block(x, None, wg, wu, wd, k, True, router_logits=logits)
     close(fused, ref, atol=3e-2, rtol=3e-2)
+
+
+@pytest.mark.parametrize("E,k,T", [(8, 2, 300), (4, 2, 700), (16, 4, 257)])
+def test_moe_grouped_training_matches_loop_gradients(E, k, T):
+    """Autograd through the grouped training kernels vs the per-expert loop: output and the
+    gradients of the input, the router logits and every expert weight (segments of 0, < 256 and
+    > 256 rows)."""
+    blk = _moe_block(E, k, seed=E + 100)
+    x0 = randn(T, 256, dtype=torch.bfloat16, seed=270)
+    l0 = randn(T, E, seed=271) * 2
+    l0[:, -1] = -30.0  # an expert without rows
+    go = randn(T, 256, dtype=torch.bfloat16, seed=272)
+
+    def run(grouped):
+        x = x0.clone().requires_grad_(True)
+        logits = l0.clone().requires_grad_(True)
+        for p in blk.parameters():
+            p.grad = None
+        w, sel = blk.route(logits, torch.bfloat16)
+        out = blk.experts_forward(x, w, sel) if grouped else _loop_experts(blk, x, w, sel)
+        out.backward(go)
+        wg = [torch.zeros_like(p) if p.grad is None else p.grad.clone()
+              for e in blk.experts for p in (e.gate_proj.weight, e.up_proj.weight, e.down_proj.weight)]
+        return out.detach(), x.grad.clone(), logits.grad.clone(), wg
+
+    c_up, c_wg = native_calls("qh_moe_up"), native_calls("qh_moe_wgrad")
+    out, gx, gl, gw = run(True)
+    assert native_calls("qh_moe_up") == c_up + 1 and native_calls("qh_moe_wgrad") == c_wg + 2
+    out2, gx2, gl2, gw2 = run(True)
+    assert torch.equal(out, out2) and torch.equal(gx, gx2) and torch.equal(gl, gl2)
+    assert all(torch.equal(a, b) for a, b in zip(gw, gw2))
+    rout, rgx, rgl, rgw = run(False)
+    close(out, rout, atol=2e-2, rtol=2e-2)
+    close(gx, rgx, atol=2e-2, rtol=2e-2)
+    close(gl, rgl, atol=2e-2, rtol=2e-2)
+    for a, b in zip(gw, rgw):
+        scale = max(1.0, float(b.abs().max()))
+        close(a, b, atol=2e-2 * scale, rtol=2e-2)
+    # the expert without rows has exactly zero weight gradients
+    assert all(int(torch.count_nonzero(t)) == 0 for t in gw[-3:])
