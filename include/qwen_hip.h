@@ -248,6 +248,15 @@ int qh_moe_scale_bwd(const void* dout, int64_t ldo, const void* D, int64_t ldd, 
 int qh_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
             const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
             void* stream);
+/* Workspace bytes with which qh_gemm_ws splits K for (M, N, K) (0: no split).
+ * Products with few 256x256 output tiles and long K (weight gradients) are
+ * computed as fp32 partials over K ranges, then summed in a fixed order. */
+int64_t qh_gemm_workspace(int64_t M, int64_t N, int64_t K, int dtype);
+/* qh_gemm with a workspace (ws may be NULL: then as qh_gemm). Same results
+ * run to run; the split-K sum order differs from the unsplit product's. */
+int qh_gemm_ws(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+               const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
+               void* ws, int64_t ws_bytes, void* stream);
 /* Several decode-sized products sharing the activations, in one launch:
  * C_i[M, N_i] = A(M,K) . B_i(N_i,K)^T (+ bias_i) for i < count (<= 4), M <= 128,
  * all operands k-contiguous, C in the input dtype (bf16/f16). B, ldb, N, C,

@@ -26,10 +26,14 @@
 //    fixed order.
 #include "qh_mfma.h"
 
-// Large-tile path (qh_gemm_tile.hip).
+// Large-tile and split-K paths (qh_gemm_tile.hip).
 int qh_gemm_tile_dispatch(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, const void* B,
                           int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
                           hipStream_t st);
+int qh_gemm_splitk_count(int64_t M, int64_t N, int64_t K);
+int qh_gemm_splitk_dispatch(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, const void* B,
+                            int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype, int S,
+                            void* ws, hipStream_t st);
 
 namespace {
 
@@ -619,7 +623,7 @@ void launch_mfma_pick(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, i
 
 template <typename T, typename OT>
 int gemm_typed(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
-               int64_t ldc, const void* bias, hipStream_t st) {
+               int64_t ldc, const void* bias, void* ws, int64_t ws_bytes, hipStream_t st) {
   const T* a = (const T*)A;
   const T* b = (const T*)B;
   OT* c = (OT*)C;
@@ -638,6 +642,11 @@ int gemm_typed(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, 
     const bool a_ok = aligned16(A) && lda % 8 == 0 && (ta ? M % 8 == 0 : K % 8 == 0);
     const bool b_ok = aligned16(B) && ldb % 8 == 0 && (tb ? N % 8 == 0 : K % 8 == 0);
     if (a_ok && b_ok) {
+      // Few output tiles and long K: split K when the caller gave a workspace.
+      const int splits = qh_gemm_splitk_count(M, N, K);
+      if (splits > 1 && ws != nullptr && ws_bytes >= (int64_t)splits * M * N * 4)
+        return qh_gemm_splitk_dispatch(ta, tb, M, N, K, A, lda, B, ldb, C, ldc, bias, qh_dtype_of<T>(),
+                                       qh_dtype_of<OT>(), splits, ws, st);
       // Large outputs: the 256x256 direct-to-LDS tile kernel.
       const int64_t big_tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
       if (M >= 256 && N >= 256 && big_tiles >= 128)
@@ -679,9 +688,21 @@ __global__ __launch_bounds__(256) void colsum_kernel(const T* __restrict__ X, in
 
 }  // namespace
 
+extern "C" int64_t qh_gemm_workspace(int64_t M, int64_t N, int64_t K, int dtype) {
+  if (dtype != QH_BF16 && dtype != QH_F16) return 0;
+  const int s = qh_gemm_splitk_count(M, N, K);
+  return s > 1 ? (int64_t)s * M * N * 4 : 0;
+}
+
 extern "C" int qh_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
                        const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
                        void* stream) {
+  return qh_gemm_ws(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, bias, dtype, out_dtype, nullptr, 0, stream);
+}
+
+extern "C" int qh_gemm_ws(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                          const void* B, int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype,
+                          void* ws, int64_t ws_bytes, void* stream) {
   QH_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "qh_gemm: negative shape");
   QH_CHECK_ARG(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31), "qh_gemm: dimension exceeds 2^31");
   QH_CHECK_ARG(ldc >= N, "qh_gemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
@@ -696,15 +717,15 @@ extern "C" int qh_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K
   int rc = QH_OK;
 #define QH_GEMM_OUT(T)                                                                                           \
   switch (out_dtype) {                                                                                          \
-    case QH_F32: rc = gemm_typed<T, float>(trans_a, trans_b, (int)M, (int)N, (int)K, A, lda, B, ldb, C, ldc, bias, st); break; \
-    case QH_F16: rc = gemm_typed<T, f16_t>(trans_a, trans_b, (int)M, (int)N, (int)K, A, lda, B, ldb, C, ldc, bias, st); break; \
-    case QH_BF16: rc = gemm_typed<T, bf16_t>(trans_a, trans_b, (int)M, (int)N, (int)K, A, lda, B, ldb, C, ldc, bias, st); break; \
+    case QH_F32: rc = gemm_typed<T, float>(trans_a, trans_b, (int)M, (int)N, (int)K, A, lda, B, ldb, C, ldc, bias, ws, ws_bytes, st); break; \
+    case QH_F16: rc = gemm_typed<T, f16_t>(trans_a, trans_b, (int)M, (int)N, (int)K, A, lda, B, ldb, C, ldc, bias, ws, ws_bytes, st); break; \
+    case QH_BF16: rc = gemm_typed<T, bf16_t>(trans_a, trans_b, (int)M, (int)N, (int)K, A, lda, B, ldb, C, ldc, bias, ws, ws_bytes, st); break; \
     default: qh::set_error("qh_gemm: bad out dtype %d", out_dtype); return QH_E_DTYPE;                          \
   }
   QH_DISPATCH_DTYPE(dtype, T, "qh_gemm", QH_GEMM_OUT(T));
 #undef QH_GEMM_OUT
   if (rc) return rc;
-  QH_CHECK_LAUNCH("qh_gemm");
+  QH_CHECK_LAUNCH("qh_gemm_ws");
   return QH_OK;
 }
 

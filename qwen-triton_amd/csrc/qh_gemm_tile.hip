@@ -463,6 +463,7 @@ int launch_tile(const P& p, int grid, hipStream_t st, const char* name) {
 
 // Pipeline shape of the dense tile kernel.
 constexpr int kDenseBK = 64, kDenseNS = 2;
+constexpr int TBKS = kDenseBK;  // split-K ranges are whole k-tiles
 
 template <typename T, typename OT, int BM, int BN, bool AT, bool BT>
 int dense_tile(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_t ldc, const T* bias, int M, int N,
@@ -889,6 +890,128 @@ int launch_moe(const P& p, int64_t grid, hipStream_t st, const char* name) {
   return launch_tile<T, 256, 256, kDenseBK, kDenseNS, AT, BT>(p, (int)grid, st, name);
 }
 
+// ---------------------------------------------------------------------------
+// Split-K dense product: few output tiles, long K. Split s of S computes the
+// K range [s Ks, (s+1) Ks) of every tile into an fp32 partial; a reduction
+// then adds the S partials in order (deterministic), adds the bias and
+// converts.
+// ---------------------------------------------------------------------------
+template <typename T, bool AT, bool BT>
+struct SplitKProblem {
+  const T* A;
+  const T* B;
+  float* P;  // S partials of [M, N]
+  int64_t lda, ldb;
+  int M, N, K, Ks, S, tiles_m, tiles_n;
+  static constexpr bool kVecEpilogue = false;
+  __device__ __forceinline__ bool vec_ok() const { return false; }
+  __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
+    const int t = xcd_logical_tile();
+    const int per = tiles_m * tiles_n;
+    const int sp = t / per;
+    if (sp >= S) return false;
+    const int rest = t % per;
+    c.m0 = (rest % tiles_m) * 256;
+    c.n0 = (rest / tiles_m) * 256;
+    c.aux = sp * Ks;
+    c.K = min(Ks, K - c.aux);
+    c.vm = M - c.m0;
+    c.vn = N - c.n0;
+    c.lda = lda;
+    c.ldb = ldb;
+    c.aux2 = sp;
+    return true;
+  }
+  __device__ __forceinline__ const T* a_at(const TileCtx<T>& c, int i, int k) const {
+    const int kk = c.aux + k;
+    return AT ? A + (int64_t)kk * lda + (c.m0 + i) : A + (int64_t)(c.m0 + i) * lda + kk;
+  }
+  __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
+    const int kk = c.aux + k;
+    return BT ? B + (int64_t)kk * ldb + (c.n0 + i) : B + (int64_t)(c.n0 + i) * ldb + kk;
+  }
+  template <class ET>
+  __device__ __forceinline__ void epilogue_vec(const TileCtx<T>&, const ET&, int, int, int) const {}
+  template <int TM, int TN>
+  __device__ __forceinline__ void epilogue(const TileCtx<T>& c, const f32x16 (&acc)[TM][TN], int wr, int wc,
+                                           int lane) const {
+    float* out = P + (int64_t)c.aux2 * M * N;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = c.n0 + wc + 32 * j + (lane & 31);
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int rb = c.m0 + wr + 32 * i + 4 * (lane >> 5);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = rb + 8 * g + r;
+            if (row < M) out[(int64_t)row * N + col] = acc[i][j][4 * g + r];
+          }
+      }
+    }
+  }
+};
+
+template <typename T, typename OT>
+__global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ P, int S, int64_t M, int64_t N,
+                                                     const T* __restrict__ bias, OT* __restrict__ C, int64_t ldc) {
+  const int64_t total = M * N;
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    float s = 0.f;
+    for (int sp = 0; sp < S; ++sp) s += P[sp * total + i];
+    const int64_t row = i / N, col = i - row * N;
+    if (bias) s += to_f32(bias[col]);
+    C[row * ldc + col] = from_f32<OT>(s);
+  }
+}
+
+// Splits for a dense product (1 = no split): few 256x256 tiles and long K.
+inline int splitk_count(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  if (M < 256 || N < 256 || tiles >= 128 || K < 2048) return 1;
+  int64_t s = (384 + tiles - 1) / tiles;
+  if (s > K / 1024) s = K / 1024;
+  if (s > 16) s = 16;
+  return s < 2 ? 1 : (int)s;
+}
+
+template <typename T, typename OT, bool AT, bool BT>
+int splitk_run(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_t ldc, const T* bias, int M, int N,
+               int K, int S, float* ws, hipStream_t st) {
+  SplitKProblem<T, AT, BT> p;
+  p.A = A;
+  p.B = B;
+  p.P = ws;
+  p.lda = lda;
+  p.ldb = ldb;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.Ks = ((K + S - 1) / S + TBKS - 1) / TBKS * TBKS;
+  p.S = (K + p.Ks - 1) / p.Ks;
+  p.tiles_m = (M + 255) / 256;
+  p.tiles_n = (N + 255) / 256;
+  const int64_t grid = ((int64_t)p.S * p.tiles_m * p.tiles_n + 7) / 8 * 8;
+  int rc = launch_tile<T, 256, 256, kDenseBK, kDenseNS, AT, BT>(p, (int)grid, st, "qh_gemm (split-K)");
+  if (rc) return rc;
+  const int64_t total = (int64_t)M * N;
+  const int g = (int)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+  splitk_reduce<T, OT><<<g, 256, 0, st>>>(ws, p.S, M, N, bias, C, ldc);
+  return QH_OK;
+}
+
+template <typename T, typename OT>
+int splitk_layout(int ta, int tb, const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_t ldc,
+                  const T* bias, int M, int N, int K, int S, float* ws, hipStream_t st) {
+  if (!ta && !tb) return splitk_run<T, OT, false, false>(A, lda, B, ldb, C, ldc, bias, M, N, K, S, ws, st);
+  if (!ta && tb) return splitk_run<T, OT, false, true>(A, lda, B, ldb, C, ldc, bias, M, N, K, S, ws, st);
+  if (ta && tb) return splitk_run<T, OT, true, true>(A, lda, B, ldb, C, ldc, bias, M, N, K, S, ws, st);
+  return splitk_run<T, OT, true, false>(A, lda, B, ldb, C, ldc, bias, M, N, K, S, ws, st);
+}
+
 }  // namespace
 
 // Large-tile path of qh_gemm (called by its dispatcher; not part of the C ABI).
@@ -1118,4 +1241,30 @@ extern "C" int qh_moe_wgrad(int parts, const void* A0, const void* A1, int64_t l
   if (rc) return rc;
   QH_CHECK_LAUNCH("qh_moe_wgrad");
   return QH_OK;
+}
+
+// Split-K path of qh_gemm_ws (not part of the C ABI): splits for (M, N, K), or 1.
+int qh_gemm_splitk_count(int64_t M, int64_t N, int64_t K) { return splitk_count(M, N, K); }
+
+int qh_gemm_splitk_dispatch(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, const void* B,
+                            int64_t ldb, void* C, int64_t ldc, const void* bias, int dtype, int out_dtype, int S,
+                            void* ws, hipStream_t st) {
+#define QH_SK_OUT(T)                                                                                             \
+  switch (out_dtype) {                                                                                          \
+    case QH_F32:                                                                                                \
+      return splitk_layout<T, float>(ta, tb, (const T*)A, lda, (const T*)B, ldb, (float*)C, ldc, (const T*)bias, \
+                                     M, N, K, S, (float*)ws, st);                                               \
+    case QH_F16:                                                                                                \
+      return splitk_layout<T, f16_t>(ta, tb, (const T*)A, lda, (const T*)B, ldb, (f16_t*)C, ldc, (const T*)bias, \
+                                     M, N, K, S, (float*)ws, st);                                               \
+    case QH_BF16:                                                                                               \
+      return splitk_layout<T, bf16_t>(ta, tb, (const T*)A, lda, (const T*)B, ldb, (bf16_t*)C, ldc,              \
+                                      (const T*)bias, M, N, K, S, (float*)ws, st);                              \
+    default: qh::set_error("qh_gemm: bad out dtype %d", out_dtype); return QH_E_DTYPE;                          \
+  }
+  if (dtype == QH_BF16) QH_SK_OUT(bf16_t)
+  if (dtype == QH_F16) QH_SK_OUT(f16_t)
+#undef QH_SK_OUT
+  qh::set_error("qh_gemm: the split-K path takes bf16/f16 operands");
+  return QH_E_DTYPE;
 }

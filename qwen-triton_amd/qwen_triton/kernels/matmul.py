@@ -43,10 +43,20 @@ def _rows(t: torch.Tensor, cols: int) -> torch.Tensor:
 
 def gemm(trans_a: bool, trans_b: bool, M: int, N: int, K: int, a: torch.Tensor, lda: int, b: torch.Tensor, ldb: int,
          out: torch.Tensor, ldc: int, bias: torch.Tensor | None = None) -> torch.Tensor:
-    """Raw library GEMM: out[M,N] = A(M,K) . B(N,K)^T (+ bias) with operand views."""
-    _native.call("qh_gemm", int(trans_a), int(trans_b), M, N, K, a.data_ptr(), lda, b.data_ptr(), ldb,
-                 out.data_ptr(), ldc, None if bias is None else bias.data_ptr(), _native.dtype_code(a.dtype),
-                 _native.dtype_code(out.dtype), _native.stream(a.device))
+    """Raw library GEMM: out[M,N] = A(M,K) . B(N,K)^T (+ bias) with operand views.
+
+    Products with few output tiles and a long K (weight gradients) get a workspace so the
+    library can split K."""
+    code = _native.dtype_code(a.dtype)
+    args = (int(trans_a), int(trans_b), M, N, K, a.data_ptr(), lda, b.data_ptr(), ldb, out.data_ptr(), ldc,
+            None if bias is None else bias.data_ptr(), code, _native.dtype_code(out.dtype))
+    if K >= 2048 and M >= 256 and N >= 256 and M * N < 128 * 65536:
+        nbytes = _native.call("qh_gemm_workspace", M, N, K, code)
+        if nbytes:
+            ws = _native.workspace(nbytes, a.device)
+            _native.call("qh_gemm_ws", *args, ws.data_ptr(), ws.numel(), _native.stream(a.device))
+            return out
+    _native.call("qh_gemm", *args, _native.stream(a.device))
     return out
 
 

@@ -448,6 +448,29 @@ def test_gemm_large_tile_layouts_and_tails(ta, tb, out_dtype):
     assert torch.equal(c, c2)
 
 
+@pytest.mark.parametrize("ta,tb", [(1, 1), (0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_gemm_split_k(ta, tb, out_dtype):
+    """Few output tiles and long K (a weight-gradient shape): K is split into fp32 partials that
+    are summed in a fixed order; M and N end in partial tiles."""
+    M, N, Kd = 1000, 776, 8192
+    assert _native.call("qh_gemm_workspace", M, N, Kd, _native.BF16) > 0
+    a = randn(M, Kd, dtype=torch.bfloat16, seed=310)
+    b = randn(N, Kd, dtype=torch.bfloat16, seed=311, scale=0.05)
+    bias = randn(N, dtype=torch.bfloat16, seed=312)
+    a_op = a.t().contiguous() if ta else a
+    b_op = b.t().contiguous() if tb else b
+    c = torch.empty(M, N, dtype=out_dtype, device=DEV)
+    c0 = native_calls("qh_gemm_ws")
+    MM.gemm(bool(ta), bool(tb), M, N, Kd, a_op, a_op.stride(0), b_op, b_op.stride(0), c, N, bias)
+    assert native_calls("qh_gemm_ws") == c0 + 1
+    ref = a.float() @ b.float().t() + bias.float()
+    close(c, ref, **(dict(atol=2e-3, rtol=2e-3) if out_dtype == torch.float32 else BF16_TOL))
+    c2 = torch.empty_like(c)
+    MM.gemm(bool(ta), bool(tb), M, N, Kd, a_op, a_op.stride(0), b_op, b_op.stride(0), c2, N, bias)
+    assert torch.equal(c, c2)
+
+
 def test_gemm_fp32_matches_reference_band():
     x = randn(37, 70, seed=97).requires_grad_(True)
     w = randn(45, 70, seed=98).requires_grad_(True)
