@@ -313,7 +313,7 @@ def bench_dense(steps, warmup):
             "dense_gemm_frac_of_step": round(flop / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
-def bench_gemm(steps, warmup):
+def bench_gemm(steps, warmup, only=None):
     """Per-shape GEMM timing (HIP events): ours vs torch.matmul (hipBLASLt) for context."""
     import torch
     from qwen_triton.kernels import matmul as MM
@@ -328,6 +328,8 @@ def bench_gemm(steps, warmup):
         ("train lm_head fwd", "NT", 16384, 151936, 1024), ("train down dX", "NN", 16384, 3072, 1024),
         ("train gate dW", "TN", 3072, 1024, 16384), ("square 8192", "NT", 8192, 8192, 8192),
     ]
+    if only:
+        shapes = [sh for sh in shapes if sh[0] == only]
     g = torch.Generator(device="cuda").manual_seed(0)
     out = []
     for label, lay, M, N, K in shapes:
@@ -671,6 +673,7 @@ def main() -> None:
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "fa", "dense", "gemm", "roofline", "moe", "ops"])
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--gemm-shape", default=None, help="--workload gemm: time only the shape with this label")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -694,7 +697,7 @@ def main() -> None:
         print(json.dumps({"metric": "dominant kernel + calibration copy", **bench_roofline_kernels()}), flush=True)
         return
     if args.workload == "gemm":
-        res = bench_gemm(args.steps, args.warmup)
+        res = bench_gemm(args.steps, args.warmup, args.gemm_shape)
         print(json.dumps({"metric": "GEMM shapes (bf16)", "rows": res}), flush=True)
         return
     if args.workload == "ops":
