@@ -551,6 +551,211 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
   }
 }
 
+// dK/dV for 128 keys of one (b, kv-head) with 8 wavefronts, two per SIMD:
+// wavefront w owns keys k0 + 32 (w & 3) .. + 31 and, of every 64-query tile,
+// the 32 queries of half w >> 2. K and V of the workgroup's keys are staged in
+// LDS once and their fragments are read per use (holding them in registers
+// would not fit two waves per SIMD); Q and dO tiles stream through two LDS
+// stages, all loaded by wavefronts 0-3. At the end the two
+// query halves' dK/dV partials are added in a fixed order (half 0 + half 1)
+// through LDS. Same per-tile arithmetic as fa_bwd_dkdv_tile.
+template <typename T, int DP>
+__device__ __forceinline__ void fa_bwd_dkdv_half(const T* Qt, const T* Ot, const T* Kk, const T* Vk,
+                                                 f32x16 (&dk)[DP / 32], f32x16 (&dv)[DP / 32],
+                                                 const float* __restrict__ lse_row, const float* __restrict__ dl_row,
+                                                 int q0, int qt, bool need_mask, int q_lo, int q_hi,
+                                                 float scale_log2, int lane) {
+  constexpr int CPR = DP / 8, DT = DP / 32, KD = DP / 16;
+  typedef typename Mfma<T>::v8 v8;
+  const int ql = lane & 31, hf = lane >> 5;
+  const int grp = lane >> 4, j = lane & 15;
+  const int row = qt * 32 + ql;
+  // S and dP: each k16 step's four fragments are read one step ahead; the
+  // scheduling barriers keep the reads from being hoisted further (registers
+  // for two wavefronts per SIMD), the other wavefront covers the latency.
+  f32x16 sc = zero16(), dp = zero16();
+  v8 fq[2], fk[2], fo[2], fv[2];
+  auto rd_s = [&](int kd, int b) {
+    const int c = swz(row, kd * 2 + hf, CPR);
+    const int cv = swz(ql, kd * 2 + hf, CPR);
+    fq[b] = load_frag16<T>(Qt + row * DP + c * 8);
+    fk[b] = load_frag16<T>(Kk + ql * DP + cv * 8);
+    fo[b] = load_frag16<T>(Ot + row * DP + c * 8);
+    fv[b] = load_frag16<T>(Vk + ql * DP + cv * 8);
+  };
+  rd_s(0, 0);
+#pragma unroll
+  for (int kd = 0; kd < KD; ++kd) {
+    if (kd + 1 < KD) rd_s(kd + 1, (kd + 1) & 1);
+    sc = Mfma<T>::mma(fq[kd & 1], fk[kd & 1], sc);
+    dp = Mfma<T>::mma(fo[kd & 1], fv[kd & 1], dp);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int il = qt * 32 + g * 8 + hf * 4;
+    const float4 ls = *reinterpret_cast<const float4*>(lse_row + il);
+    const float4 dl = *reinterpret_cast<const float4*>(dl_row + il);
+    const float lv[4] = {ls.x, ls.y, ls.z, ls.w};
+    const float dv4[4] = {dl.x, dl.y, dl.z, dl.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float p = exp2_(__builtin_fmaf(sc[g * 4 + r], scale_log2, -lv[r]));
+      if (need_mask) {
+        const int qi = q0 + qt * 32 + g * 8 + hf * 4 + r;
+        p = (qi >= q_lo && qi < q_hi) ? p : 0.f;
+      }
+      sc[g * 4 + r] = p;
+      dp[g * 4 + r] = p * (dp[g * 4 + r] - dv4[r]);
+    }
+  }
+  // dV += dO^T P, dK += Q^T dS with the transposed operands read one step ahead.
+  const v8 pf[2] = {pack_pair<T>(sc, 0), pack_pair<T>(sc, 2)};
+  const v8 df[2] = {pack_pair<T>(dp, 0), pack_pair<T>(dp, 2)};
+  v8 ta[2], tb[2];
+  auto rd_t = [&](int st, int b) {
+    const int ks = st / DT, dt = st % DT;
+    const int qrow = qt * 32 + ks * 16 + 4 * (grp >> 1) + (j >> 2);
+    const int d = dt * 32 + 16 * (grp & 1) + 4 * (j & 3);
+    ta[b] = read_vt_frag<T, DP>(Ot, qrow, d);
+    tb[b] = read_vt_frag<T, DP>(Qt, qrow, d);
+  };
+  rd_t(0, 0);
+#pragma unroll
+  for (int st = 0; st < 2 * DT; ++st) {
+    if (st + 1 < 2 * DT) rd_t(st + 1, (st + 1) & 1);
+    const int ks = st / DT, dt = st % DT;
+    dv[dt] = Mfma<T>::mma(ta[st & 1], pf[ks], dv[dt]);
+    dk[dt] = Mfma<T>::mma(tb[st & 1], df[ks], dk[dt]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <typename T, int DP>
+__global__ __launch_bounds__(512) void fa_bwd_dkdv8_kernel(
+    const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs, const T* __restrict__ K, int64_t skb, int64_t skh,
+    int64_t sks, const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs, const T* __restrict__ dO,
+    const float* __restrict__ LSE2, const float* __restrict__ Delta, int64_t sqp, T* __restrict__ dK,
+    T* __restrict__ dV, int Hq, int Hkv, int groups, int Sq, int Sk, int D, float scale_log2, float scale, int causal,
+    int coff) {
+  constexpr int BQ = 64, KB = 128;
+  constexpr int DT = DP / 32, KD = DP / 16;
+  typedef typename Mfma<T>::v8 v8;
+  extern __shared__ __attribute__((aligned(1024))) unsigned char qh_dkdv_smem[];
+  T* Ks = reinterpret_cast<T*>(qh_dkdv_smem);  // [KB][DP]
+  T* Vs = Ks + KB * DP;                         // [KB][DP]
+  T* Qs = Vs + KB * DP;                         // [2][BQ][DP]
+  T* Os = Qs + 2 * BQ * DP;                     // [2][BQ][DP]
+
+  const int bk = blockIdx.y;
+  const int b = bk / Hkv, hk = bk % Hkv;
+  const int k0 = blockIdx.x * KB;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ks = wid & 3, qt = wid >> 2;
+  const int ql = lane & 31, hf = lane >> 5;
+  const int kj = k0 + ks * 32 + ql;  // this lane's key (C-layout column)
+  const int kw0 = k0 + ks * 32;      // first key of this wavefront
+  // queries [q_lo, q_hi) see key kj: below Sq, at or after kj - coff when
+  // causal, none when kj is past Sk
+  const int q_lo = causal ? kj - coff : INT_MIN;
+  const int q_hi = kj < Sk ? Sq : INT_MIN;
+  const T* Kb = K + b * skb + hk * skh;
+  const T* Vb = V + b * svb + hk * svh;
+
+  f32x16 dk[DT], dv[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dk[dt] = dv[dt] = zero16();
+
+  int q_start = 0;
+  if (causal) {
+    q_start = k0 - coff;
+    if (q_start < 0) q_start = 0;
+    q_start = (q_start / BQ) * BQ;
+  }
+  const int nqt = q_start < Sq ? (Sq - q_start + BQ - 1) / BQ : 0;
+  const int ntiles = groups * nqt;
+  const bool loader = wid < 4;  // wavefronts 0-3 issue every LDS fill
+  if (loader) {
+    // K and V of the workgroup's 128 keys (rows past Sk are clamped; their
+    // scores are masked and their dK/dV rows are not stored)
+    const TileLoader<T, KB, DP> kload(sks, D), vload(svs, D);
+    kload.load(Ks, Kb, sks, k0, Sk);
+    vload.load(Vs, Vb, svs, k0, Sk);
+  }
+  auto issue = [&](int it, int buf) {
+    const TileLoader<T, BQ, DP> qload(sqs, D), oload(D, D);
+    const int g = it / nqt, q0 = q_start + (it % nqt) * BQ;
+    const int hq = hk * groups + g;
+    qload.load(Qs + buf * BQ * DP, Q + b * sqb + hq * sqh, sqs, q0, Sq);
+    oload.load(Os + buf * BQ * DP, dO + ((int64_t)b * Hq + hq) * Sq * D, D, q0, Sq);
+  };
+  if (ntiles > 0 && loader) issue(0, 0);
+  // this wavefront's 32 keys; the swizzle depends on the row's low 4 bits only,
+  // so the row within the slice addresses it
+  const T* Kk = Ks + ks * 32 * DP;
+  const T* Vk = Vs + ks * 32 * DP;
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile `it` (and of V) have landed
+    __syncthreads();                // ... and everyone else's; tile it-1 is fully consumed
+    if (it + 1 < ntiles && loader) issue(it + 1, buf ^ 1);
+    const int g = it / nqt, q0 = q_start + (it % nqt) * BQ;
+    const int64_t bh = (int64_t)b * Hq + hk * groups + g;
+    const int qh0 = q0 + qt * 32;
+    const bool need_mask = (qh0 + 32 > Sq) || (kw0 + 32 > Sk) || (causal && kw0 + 31 > qh0 + coff);
+    const float* lse_row = LSE2 + bh * sqp + q0;
+    const float* dl_row = Delta + bh * sqp + q0;
+    const T* Qt = Qs + buf * BQ * DP;
+    const T* Ot = Os + buf * BQ * DP;
+    // one code path for masked and unmasked tiles: two inlined copies would
+    // keep the dK/dV accumulators in different registers on each side
+    fa_bwd_dkdv_half<T, DP>(Qt, Ot, Kk, Vk, dk, dv, lse_row, dl_row, q0, qt, need_mask, q_lo, q_hi, scale_log2,
+                            lane);
+  }
+  // half 1 hands its partials to half 0 through LDS (dV, then dK)
+  float* red = reinterpret_cast<float*>(qh_dkdv_smem);
+  const int slot = ks * DT * 16 * 64 + lane;
+  auto combine = [&](f32x16(&a)[DT]) {
+    __syncthreads();
+    if (qt == 1) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[slot + (dt * 16 + e) * 64] = a[dt][e];
+    }
+    __syncthreads();
+    if (qt == 0) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) a[dt][e] += red[slot + (dt * 16 + e) * 64];
+    }
+  };
+  combine(dv);
+  combine(dk);
+  if (qt == 0 && kj < Sk) {
+    T* dKr = dK + ((int64_t)bk * Sk + kj) * D;
+    T* dVr = dV + ((int64_t)bk * Sk + kj) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg) {
+        const int d = dt * 32 + gg * 8 + hf * 4;
+        if (d < D) {
+          typename Mfma<T>::v4 a, c;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            a[r] = (T)(dk[dt][gg * 4 + r] * scale);
+            c[r] = (T)dv[dt][gg * 4 + r];
+          }
+          *reinterpret_cast<typename Mfma<T>::v4*>(dKr + d) = a;
+          *reinterpret_cast<typename Mfma<T>::v4*>(dVr + d) = c;
+        }
+      }
+  }
+}
+
 // dQ for 128 queries (4 wavefronts x 32 queries) of one (b, q-head): the
 // forward kernel's structure with dP computed beside S. K and V tiles of 64
 // keys stream through double-buffered swizzled LDS; per tile
@@ -965,6 +1170,31 @@ extern "C" int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq) {
   return 2 * B * Hq * bwd_row_pad(Sq) * 4;
 }
 
+namespace {
+// LDS of fa_bwd_dkdv8_kernel: K and V of 128 keys plus two Q and two dO tiles of 64 rows.
+constexpr int kDkdv8Lds = (2 * 128 + 4 * 64) * 128 * 2;
+
+// Raise the dynamic-LDS limit of fa_bwd_dkdv8_kernel once per device.
+template <typename T>
+int dkdv8_lds_ready() {
+  static uint64_t done = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    qh::set_error("qh_flash_bwd: no current device");
+    return QH_E_HIP;
+  }
+  if (done >> dev & 1) return QH_OK;
+  const hipError_t e = hipFuncSetAttribute((const void*)fa_bwd_dkdv8_kernel<T, 128>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kDkdv8Lds);
+  if (e != hipSuccess) {
+    qh::set_error("qh_flash_bwd: cannot raise the LDS limit: %s", hipGetErrorString(e));
+    return QH_E_HIP;
+  }
+  done |= 1ull << dev;
+  return QH_OK;
+}
+}  // namespace
+
 extern "C" int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
                             int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs,
                             const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv, void* ws,
@@ -1006,7 +1236,14 @@ extern "C" int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
   do {                                                                                                              \
     fa_bwd_prep_kernel<T><<<(unsigned)ceil_div(prow, 16), 256, 0, st>>>((const T*)o, (const T*)dout, lse, delta,   \
                                                                         lse2, prow, (int)Sq, sqp, (int)D);          \
-    if (Sk > 0)                                                                                                     \
+    if (Sk > 0 && DPV == 128) {                                                                                     \
+      const int rc8 = dkdv8_lds_ready<T>();                                                                         \
+      if (rc8) return rc8;                                                                                          \
+      fa_bwd_dkdv8_kernel<T, 128><<<gkv, 512, kDkdv8Lds, st>>>(                                                     \
+          (const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks, (const T*)v, svb, svh, svs, (const T*)dout, lse2,  \
+          delta, sqp, (T*)dk, (T*)dv, (int)Hq, (int)Hkv, groups, (int)Sq, (int)Sk, (int)D, sl2, scale, causal,       \
+          (int)causal_offset);                                                                                      \
+    } else if (Sk > 0)                                                                                              \
       fa_bwd_dkdv_kernel<T, DPV><<<gkv, 256, 0, st>>>((const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks,       \
                                                       (const T*)v, svb, svh, svs, (const T*)dout, lse2, delta, sqp,   \
                                                       (T*)dk,                                                         \
