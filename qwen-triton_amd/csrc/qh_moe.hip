@@ -104,26 +104,42 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const T* __restrict__ 
                                                           const T* __restrict__ w, int k, int64_t E,
                                                           T* __restrict__ out, int64_t H) {
   const int64_t t = blockIdx.x;
+  // The token's k slots are loaded together, then ordered by expert id in
+  // registers (ids of one token are distinct; out-of-range ids sort last and
+  // are dropped).
   int64_t ek[KMAX];
   int32_t pk[KMAX];
   float wk[KMAX];
-  int nk = 0;
-  for (int j = 0; j < k; ++j) {  // insertion by expert id (ids of one token are distinct)
-    const int64_t e = sel[t * k + j];
-    if (e < 0 || e >= E) continue;
-    const int32_t p = inv[t * k + j];
-    const float wj = w ? to_f32(w[t * k + j]) : 1.f;
-    int q = nk++;
-    while (q > 0 && ek[q - 1] > e) {
-      ek[q] = ek[q - 1];
-      pk[q] = pk[q - 1];
-      wk[q] = wk[q - 1];
-      --q;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    ek[j] = E;
+    pk[j] = 0;
+    wk[j] = 1.f;
+    if (j < k) {
+      const int64_t e = sel[t * k + j];
+      pk[j] = inv[t * k + j];
+      if (w) wk[j] = to_f32(w[t * k + j]);
+      ek[j] = (e < 0 || e >= E) ? E : e;
     }
-    ek[q] = e;
-    pk[q] = p;
-    wk[q] = wj;
   }
+  int nk = 0;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) nk += ek[j] < E ? 1 : 0;
+#pragma unroll
+  for (int j = 1; j < KMAX; ++j)
+#pragma unroll
+    for (int q = j; q > 0; --q) {
+      const bool sw = ek[q - 1] > ek[q];
+      const int64_t e0 = ek[q - 1], e1 = ek[q];
+      const int32_t p0 = pk[q - 1], p1 = pk[q];
+      const float w0 = wk[q - 1], w1 = wk[q];
+      ek[q - 1] = sw ? e1 : e0;
+      ek[q] = sw ? e0 : e1;
+      pk[q - 1] = sw ? p1 : p0;
+      pk[q] = sw ? p0 : p1;
+      wk[q - 1] = sw ? w1 : w0;
+      wk[q] = sw ? w0 : w1;
+    }
   for (int64_t c = threadIdx.x * 8; c < H; c += 256 * 8) {
     // all rows are requested before the ordered sum consumes them
     Vec16<T> y[KMAX];
@@ -155,7 +171,16 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const T* __restrict__ X
   if (r >= R) return;
   const T* src = X + (int64_t)rows[r] * ldx;
   T* dst = Xs + r * lds;
-  for (int64_t c = (threadIdx.x & 63) * 8; c < H; c += 64 * 8) st16(dst + c, ld16(src + c));
+  // four 16-byte loads in flight before their stores
+  for (int64_t c0 = (threadIdx.x & 63) * 8; c0 < H; c0 += 4 * 64 * 8) {
+    Vec16<T> v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (c0 + u * 512 < H) v[u] = ld16(src + c0 + u * 512);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (c0 + u * 512 < H) st16(dst + c0 + u * 512, v[u]);
+  }
 }
 
 // Backward of the routing-weight scaling, one workgroup per token t: for each

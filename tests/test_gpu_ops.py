@@ -661,6 +661,24 @@ def test_moe_grouped_experts_match_loop(E, k, T):
     close(fused, ref, atol=3e-2, rtol=3e-2)
 
 
+@pytest.mark.parametrize("E,k,T", [(4, 2, 700), (8, 2, 1100)])
+def test_moe_inference_tile_path_matches_training_forward(E, k, T):
+    """With many routed rows per expert the inference forward runs on the 256x256 tile kernels:
+    bitwise the training forward's output, and within the bf16 band of the per-expert loop."""
+    blk = _moe_block(E, k, seed=E + 200)
+    x = randn(T, 256, dtype=torch.bfloat16, seed=280)
+    logits = randn(T, E, seed=281) * 2
+    logits[:, -1] = -30.0  # an expert without rows
+    w, sel = blk.route(logits, torch.bfloat16)
+    c_up, c_gemm = native_calls("qh_moe_up"), native_calls("qh_moe_gemm")
+    with torch.no_grad():
+        inf = blk.experts_forward(x, w, sel)
+    assert native_calls("qh_moe_up") == c_up + 1 and native_calls("qh_moe_gemm") == c_gemm
+    train = blk.experts_forward(x.clone().requires_grad_(True), w, sel).detach()
+    assert torch.equal(inf, train)
+    close(inf, _loop_experts(blk, x, w, sel), atol=2e-2, rtol=2e-2)
+
+
 @pytest.mark.parametrize("E,k,T", [(8, 2, 300), (4, 2, 700), (16, 4, 257)])
 def test_moe_grouped_training_matches_loop_gradients(E, k, T):
     """Autograd through the grouped training kernels vs the per-expert loop: output and the
