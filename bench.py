@@ -179,30 +179,38 @@ def attention_roofline(model, cache, reps=50, batch=64, ctx=2048):
 # config 0 on the GPU: prefill 128, 32 greedy decode steps, batch 1
 # ---------------------------------------------------------------------------
 def bench_cfg0(model, reps=3):
+    """Config 0 on the GPU: bs1 prefill of 128 tokens and greedy decoding. Per-token decode time is
+    (greedy_generate of 33 tokens - of 3 tokens) / 30, which cancels the prefill and, with
+    ``use_graph=True``, the one-time capture of the decode step."""
     import torch
 
     ids = torch.randint(0, model.config.vocab_size, (1, 128), generator=torch.Generator().manual_seed(0)).cuda()
-    with torch.no_grad():
-        model.greedy_generate(ids, max_new_tokens=2)  # warmup
+
+    def timed(fn):
         sync()
+        t0 = time.perf_counter()
+        fn()
+        sync()
+        return time.perf_counter() - t0
+
+    with torch.no_grad():
+        model.greedy_generate(ids, max_new_tokens=3)  # warmup
+        model.greedy_generate(ids, max_new_tokens=3, use_graph=True)
         pre = []
         for _ in range(reps):
             cache = model.new_cache(1, 160, torch.bfloat16, "cuda")
-            sync()
-            t0 = time.perf_counter()
-            out = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
-            out.logits[:, -1].argmax(-1)
-            sync()
-            pre.append(time.perf_counter() - t0)
-        sync()
-        t0 = time.perf_counter()
-        model.greedy_generate(ids, max_new_tokens=33)
-        sync()
-        total = time.perf_counter() - t0
+            pre.append(timed(lambda: model(input_ids=ids, past_key_values=cache, use_cache=True,
+                                           logits_to_keep=1).logits[:, -1].argmax(-1)))
+        per_tok = {}
+        for name, graph in (("eager", False), ("graph", True)):
+            long = min(timed(lambda: model.greedy_generate(ids, max_new_tokens=33, use_graph=graph)) for _ in range(2))
+            short = min(timed(lambda: model.greedy_generate(ids, max_new_tokens=3, use_graph=graph)) for _ in range(2))
+            per_tok[name] = max(long - short, 1e-9) / 30
     prefill_s = sorted(pre)[len(pre) // 2]
-    decode_s = max(total - prefill_s, 1e-9) / 32
-    return {"prefill_tok_s": round(128 / prefill_s, 1), "decode_tok_s": round(1 / decode_s, 1),
-            "prefill_ms": round(prefill_s * 1e3, 3), "decode_ms_per_token": round(decode_s * 1e3, 3)}
+    return {"prefill_tok_s": round(128 / prefill_s, 1), "decode_tok_s": round(1 / per_tok["graph"], 1),
+            "prefill_ms": round(prefill_s * 1e3, 3), "decode_ms_per_token": round(per_tok["graph"] * 1e3, 3),
+            "decode_mode": "greedy_generate(use_graph=True): captured decode step replayed per token",
+            "eager_decode_tok_s": round(1 / per_tok["eager"], 1)}
 
 
 # ---------------------------------------------------------------------------

@@ -621,6 +621,87 @@ __global__ __launch_bounds__(256) void topk_kernel(const T* __restrict__ x, T* _
   }
 }
 
+// Rows wider than 1024 columns (e.g. an argmax over a vocabulary): one
+// 1024-thread workgroup per row. Each round scans the row with 16-byte loads
+// (four in flight per thread), keeps the best element strictly after the
+// previous pick in (value desc, column asc) order, and reduces the 16
+// wavefronts' candidates through LDS. Same selection rule as topk_kernel.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(1024) void topk_wide_kernel(const T* __restrict__ x, T* __restrict__ vals,
+                                                         int64_t* __restrict__ idx, int64_t N, int C, int k) {
+  constexpr int VN = Vec16<T>::N;
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * (int64_t)C;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  float lv = INFINITY;
+  int li = -1;
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int bi = -1;
+    if constexpr (VEC) {
+      const int nv = C / VN;  // C is a multiple of VN
+      for (int v0 = tid; v0 < nv; v0 += 4 * 1024) {
+        Vec16<T> buf[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (v0 + u * 1024 < nv) buf[u] = ld16(xr + (int64_t)(v0 + u * 1024) * VN);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (v0 + u * 1024 < nv) {
+#pragma unroll
+            for (int e = 0; e < VN; ++e) {
+              const int c = (v0 + u * 1024) * VN + e;
+              const float v = to_f32(buf[u].v[e]);
+              if (topk_after(v, c, lv, li) && topk_better(v, c, bv, bi)) {
+                bv = v;
+                bi = c;
+              }
+            }
+          }
+        }
+      }
+    } else {
+      for (int c = tid; c < C; c += 1024) {
+        const float v = to_f32(xr[c]);
+        if (topk_after(v, c, lv, li) && topk_better(v, c, bv, bi)) {
+          bv = v;
+          bi = c;
+        }
+      }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const float v2 = __shfl_xor(bv, o);
+      const int i2 = __shfl_xor(bi, o);
+      if (i2 >= 0 && topk_better(v2, i2, bv, bi)) {
+        bv = v2;
+        bi = i2;
+      }
+    }
+    if (lane == 0) {
+      sv[wid] = bv;
+      si[wid] = bi;
+    }
+    __syncthreads();
+    bv = -INFINITY;
+    bi = -1;
+    for (int w = 0; w < 16; ++w)
+      if (si[w] >= 0 && topk_better(sv[w], si[w], bv, bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    __syncthreads();  // sv / si are rewritten next round
+    if (tid == 0) {
+      vals[row * k + r] = from_f32<T>(bi >= 0 ? bv : __int_as_float(0x7fc00000));
+      idx[row * k + r] = bi;
+    }
+    lv = bv;
+    li = bi;
+    if (bi < 0) lv = -INFINITY, li = 0x7fffffff;
+  }
+}
+
 // Top-k for rows of C <= 128 and k <= 16: 16 lanes per row, each holding 8
 // values as 64-bit keys (order-preserving value bits << 32 | ~column), so one
 // unsigned max gives "largest value, then lowest column" -- the order of
@@ -777,7 +858,10 @@ static void launch_topk(const void* x, void* vals, int64_t* idx, int64_t N, int6
   else if (cpl <= 4) topk_kernel<T, 4><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
   else if (cpl <= 8) topk_kernel<T, 8><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
   else if (cpl <= 16) topk_kernel<T, 16><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
-  else topk_kernel<T, 0><<<grid, 256, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
+  else if (aligned16(x) && (C * (int64_t)sizeof(T)) % 16 == 0)
+    topk_wide_kernel<T, true><<<(unsigned)N, 1024, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
+  else
+    topk_wide_kernel<T, false><<<(unsigned)N, 1024, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
 }
 
 }  // namespace
@@ -955,7 +1039,7 @@ extern "C" int qh_topk(const void* x, void* vals, int64_t* idx, int64_t N, int64
                        void* stream) {
   QH_CHECK_ARG(N >= 0 && C >= 0 && k >= 0, "qh_topk: negative shape");
   QH_CHECK_ARG(k <= C, "qh_topk: k=%lld > C=%lld", (long long)k, (long long)C);
-  QH_CHECK_ARG(C < (1ll << 30), "qh_topk: C too large");
+  QH_CHECK_ARG(C < (1ll << 30) && N < (1ll << 31), "qh_topk: too large");
   if (N == 0 || k == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;
   QH_DISPATCH_DTYPE(dtype, T, "qh_topk", launch_topk<T>(x, vals, idx, N, C, k, st));

@@ -166,7 +166,13 @@ class QwenTritonModel(nn.Module):
         seq = inputs_embeds.shape[1]
         max_position = None
         generated_positions = cache_position is None
-        if cache_position is None:
+        static = getattr(past_key_values, "static", None)
+        if static is not None and cache_position is None:
+            # captured decode step: the position lives in device memory; the attention reads
+            # the whole reserved cache with per-sequence valid lengths
+            cache_position = static.positions
+            max_position = past_key_values.capacity() - 1
+        elif cache_position is None:
             past = 0 if past_key_values is None else past_key_values.get_seq_length()
             cache_position = torch.arange(past, past + seq, device=inputs_embeds.device)
             max_position = past + seq - 1
@@ -311,10 +317,22 @@ class QwenTritonForCausalLM(nn.Module):
 
     @torch.no_grad()
     def greedy_generate(self, input_ids: torch.LongTensor, attention_mask: torch.Tensor | None = None,
-                        max_new_tokens: int = 16) -> torch.LongTensor:
+                        max_new_tokens: int = 16, use_graph: bool = False) -> torch.LongTensor:
+        """Greedy decoding (reference: qwen_triton/models/core.py:378-410).
+
+        ``use_graph=True`` (GPU, bf16/fp16, no padding mask) prefills as usual, then captures one
+        decode step in a HIP graph that reads its cache position and valid lengths from device
+        memory, picks the next token and advances that state itself; the remaining steps are graph
+        replays with no host work in between. With a cache of at most 256 positions the replayed
+        steps run the same kernels as the eager loop and give the same tokens; beyond that the
+        decode attention plans its key splits for the reserved capacity rather than the current
+        length (same tokens within the bf16 band).
+        """
         if self.backend == "ref" and hasattr(self.ref_model, "generate"):
             return self.ref_model.generate(input_ids=input_ids, attention_mask=attention_mask,
                                            max_new_tokens=max_new_tokens, do_sample=False)
+        if use_graph and max_new_tokens > 2 and self._graph_decode_ok(input_ids, attention_mask):
+            return self._greedy_generate_graph(input_ids, max_new_tokens)
         generated = input_ids
         running_mask = attention_mask
         cache = None
@@ -331,3 +349,59 @@ class QwenTritonForCausalLM(nn.Module):
             if running_mask is not None:
                 running_mask = torch.cat((running_mask, torch.ones_like(next_token, dtype=running_mask.dtype)), dim=-1)
         return generated
+
+    def _graph_decode_ok(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None) -> bool:
+        from qwen_triton import _native
+
+        cfg = self.config
+        dtype = self.lm_head.weight.dtype
+        return (input_ids.is_cuda and dtype in (torch.bfloat16, torch.float16) and _native.available()
+                and not cfg.attn_output_gate and all(t == "full_attention" for t in cfg.layer_types)
+                and (attention_mask is None or bool((attention_mask == 1).all())))
+
+    @torch.no_grad()
+    def _greedy_generate_graph(self, input_ids: torch.LongTensor, max_new_tokens: int) -> torch.LongTensor:
+        from qwen_triton.kernels.moe_routing import _native_topk
+        from qwen_triton.modules.cache import StaticDecode
+
+        batch, prompt = input_ids.shape
+        dev = input_ids.device
+        cache = self.new_cache(batch, prompt + max_new_tokens, self.lm_head.weight.dtype, dev)
+
+        def pick(logits: torch.Tensor) -> torch.Tensor:
+            # top-1 on the library kernel (ties: lowest index, as argmax)
+            return _native_topk(logits[:, -1], 1)[1]
+
+        first = pick(self(input_ids=input_ids, past_key_values=cache, use_cache=True, logits_to_keep=1).logits)
+        tokens = torch.empty((batch, max_new_tokens), dtype=torch.long, device=dev)
+        tokens[:, :1] = first
+        ids = first.clone()
+        col = torch.ones((1, 1), dtype=torch.long, device=dev)  # next column of ``tokens``
+        cache.static = StaticDecode(positions=torch.full((1,), prompt, dtype=torch.long, device=dev),
+                                    seqlens=torch.full((batch,), prompt + 1, dtype=torch.int32, device=dev))
+
+        def step() -> None:
+            nxt = pick(self(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1).logits)
+            ids.copy_(nxt)
+            tokens.scatter_(1, col.expand(batch, 1), nxt)
+            col.add_(1)
+            cache.static.positions.add_(1)
+            cache.static.seqlens.add_(1)
+
+        try:
+            # the second token eagerly on a side stream (also the capture's warm-up), then one
+            # captured step replayed for the rest
+            side = torch.cuda.Stream(device=dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(side):
+                step()
+            torch.cuda.current_stream(dev).wait_stream(side)
+            if max_new_tokens > 2:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    step()
+                for _ in range(max_new_tokens - 2):
+                    graph.replay()
+        finally:
+            cache.static = None
+        return torch.cat((input_ids, tokens), dim=-1)

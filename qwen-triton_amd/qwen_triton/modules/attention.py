@@ -149,8 +149,17 @@ class QwenFullAttention(nn.Module):
             else:
                 q2, k2, v2 = (p(hidden_states) for p in projs)
             q, k, v = self._fused_prepare(q2, k2, v2, cos, sin, past_key_values, cache_position, max_position)
-            out = self._attend(q, k, v, attention_mask, hidden_states.dtype)
+            static = getattr(past_key_values, "static", None)
+            if static is not None and q.shape[2] == 1 and attention_mask is None:
+                # captured decode step: k/v span the reserved cache, each sequence's valid length
+                # is read from device memory
+                out = _fa.flash_decode(q, k, v, self.scaling, self.num_key_value_groups, seqlens=static.seqlens)
+            else:
+                out = self._attend(q, k, v, attention_mask, hidden_states.dtype)
             return self.o_proj(out.transpose(1, 2).reshape(*input_shape, -1))
+        if getattr(past_key_values, "static", None) is not None:
+            raise RuntimeError("a captured decode step needs the fused inference path (bf16/fp16 on the GPU, "
+                               "no output gate, no autograd)")
         mixed_q = self.q_proj(hidden_states)
         gate = None
         if self.config.attn_output_gate:

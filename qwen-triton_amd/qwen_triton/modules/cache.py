@@ -17,6 +17,18 @@ from qwen_triton.kernels import append_attention_kv, write_attention_kv
 
 
 @dataclass
+class StaticDecode:
+    """Device-side state of a decode step that is captured once and replayed (HIP graph).
+
+    ``positions`` (int64 [1]) is the cache position the step writes; ``seqlens`` (int32 [B]) is
+    each sequence's valid key count after that write. The captured step reads both from device
+    memory and advances them itself, so every replay decodes the next position without the host.
+    """
+    positions: torch.Tensor
+    seqlens: torch.Tensor
+
+
+@dataclass
 class QwenTritonCache:
     num_layers: int
     layer_types: list[str]
@@ -28,6 +40,8 @@ class QwenTritonCache:
         self.conv_states: list[torch.Tensor | None] = [None] * self.num_layers
         self.recurrent_states: list[torch.Tensor | None] = [None] * self.num_layers
         self.attention_lengths: list[int] = [0] * self.num_layers
+        # set by a graph-captured decode loop (see StaticDecode); None for ordinary use
+        self.static: StaticDecode | None = None
 
     def _resolve_capacity(self, required_len: int) -> int:
         if required_len <= 0:
@@ -128,6 +142,13 @@ class QwenTritonCache:
                                                                      required)
         self.attention_lengths[layer_idx] = max(current, required)
         return self.key_cache[layer_idx], self.value_cache[layer_idx], self.attention_lengths[layer_idx]
+
+    def capacity(self) -> int:
+        """Reserved positions of the attention layers (0 if none is allocated)."""
+        for key in self.key_cache:
+            if key is not None:
+                return key.shape[2]
+        return 0
 
     def get_seq_length(self, layer_idx: int | None = None) -> int:
         if layer_idx is not None and self.key_cache[layer_idx] is not None:

@@ -233,3 +233,29 @@ def test_inference_fusions_match_autograd_path_bitwise():
         outs[mode] = steps
     for a, b in zip(outs["fused"], outs["plain"]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("moe", [False, True])
+def test_greedy_generate_graph_replay_matches_eager(moe):
+    """greedy_generate(use_graph=True): one captured decode step replayed per token, with the
+    position and valid lengths advanced on the device. With a cache of at most 256 positions
+    it runs the eager loop's kernels, so the tokens are identical; the replays (not Python
+    calls) do the work."""
+    extra = dict(model_type="qwen3_moe", moe_intermediate_size=128, num_experts=8, num_experts_per_tok=2,
+                 norm_topk_prob=True, decoder_sparse_step=1, mlp_only_layers=[]) if moe else {}
+    cfg = _cfg(**extra)
+    m = _model(cfg, seed=5)
+    ids = torch.randint(0, cfg.vocab_size, (2, 19), generator=torch.Generator().manual_seed(6)).cuda()
+    new = 24
+    with torch.no_grad():
+        eager = m.greedy_generate(ids, max_new_tokens=new)
+        c0 = _native.CALLS["qh_flash_decode"]
+        graph = m.greedy_generate(ids, max_new_tokens=new, use_graph=True)
+        launched = _native.CALLS["qh_flash_decode"] - c0
+        again = m.greedy_generate(ids, max_new_tokens=new, use_graph=True)
+    assert graph.shape == (2, 19 + new)
+    assert torch.equal(graph, eager)
+    assert torch.equal(again, eager)
+    # decode attention entered from Python twice per layer (the eager second token and the
+    # capture), not once per generated token
+    assert launched == 2 * cfg.num_hidden_layers

@@ -287,6 +287,22 @@ def test_topk_narrow_rows_ties_and_specials(N, C, k, dtype):
         assert torch.equal(got[:order.numel()], order)
 
 
+@pytest.mark.parametrize("N,C,k,dtype", [(2, 151936, 1, torch.bfloat16), (3, 1030, 4, torch.float32),
+                                         (5, 4099, 3, torch.float16)])
+def test_topk_wide_rows(N, C, k, dtype):
+    """Rows wider than 1024 columns (a greedy argmax over a vocabulary; widths with and without
+    16-byte rows): quantised values, so the maximum is tied in several columns."""
+    x = (torch.round(torch.randn(N, C, generator=_gen(84)) * 2) / 2).to(dtype).to(DEV)
+    c0 = native_calls("qh_topk")
+    vals, idx = K.triton_topk(x, k)
+    assert native_calls("qh_topk") == c0 + 1
+    ev, ei = O.topk(x, k)
+    assert torch.equal(idx.cpu(), ei)
+    assert torch.equal(vals.cpu(), ev)
+    if k == 1:
+        assert torch.equal(idx.view(-1).cpu(), torch.argmax(x.float().cpu(), dim=-1))
+
+
 def test_topk_ties_go_to_lowest_index():
     x = torch.tensor([[1.0, 3.0, 3.0, 0.5, 3.0, 1.0], [2.0] * 6], device=DEV)
     vals, idx = K.triton_topk(x, 4)
