@@ -35,11 +35,11 @@ METRIC = "Qwen3-0.6B prefill/decode tok/s on 1 MI355X + % of MFMA/HBM roofline"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
-# HBM bytes per launch of the decode attention (decode + combine kernels), from the
-# two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`,
+# HBM bytes per launch of the decode attention (one fa_decode_wg_kernel dispatch at config 3),
+# from the two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`,
 # each scaled by the same counter's reading for a 1 GiB copy (fetch x 1048576 / 524300.3,
-# write x1.000): (262865.0 + 1068.5) KiB x 1.99995 + (2176.2 + 256.0) KiB = 543,013,669 bytes.
-DECODE_TRAFFIC_BYTES = 543_013_669
+# write x1.000): 262504 KiB x 1.99995 + 256 KiB = 537,857,724 bytes.
+DECODE_TRAFFIC_BYTES = 537_857_724
 
 QWEN3_06B = dict(model_type="qwen3", vocab_size=151936, hidden_size=1024, intermediate_size=3072,
                  num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8, head_dim=128,
@@ -171,7 +171,7 @@ def attention_roofline(model, cache, reps=50, batch=64, ctx=2048):
     achieved = algo / (avg_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC_BYTES,
-            "kernel": "fa_decode_kernel+fa_decode_combine", "avg_launch_us": round(avg_ms * 1e3, 2),
+            "kernel": "fa_decode_wg_kernel", "avg_launch_us": round(avg_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": algo}
 
 

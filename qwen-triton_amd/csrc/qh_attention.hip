@@ -1101,6 +1101,208 @@ __global__ __launch_bounds__(256) void fa_decode_combine(const float* __restrict
   if (d == 0 && LSE) LSE[row] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
 }
 
+// Decode for many sequences: one 256-thread workgroup per (b, kv-head) whose
+// wavefront w takes key tiles w, w + 4, w + 8, ... -- the key partition of
+// fa_decode_kernel with 4 interleaved splits, and the same per-tile arithmetic.
+// K fragments go from global memory straight into registers in the MFMA
+// operand layout (no LDS); V tiles go through two LDS stages per wavefront (the
+// transposed operand reads need LDS), so two workgroups fit on a CU. The four
+// partial (m, l, o) are combined in LDS in wavefront order with
+// fa_decode_combine's arithmetic: no workspace and no second launch, and the
+// same results as the split kernel plus combine at 4 splits.
+template <typename T, int DP, int G>
+__global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
+                                                          const T* __restrict__ K, int64_t skb, int64_t skh,
+                                                          int64_t sks, const T* __restrict__ V, int64_t svb,
+                                                          int64_t svh, int64_t svs, T* __restrict__ O,
+                                                          float* __restrict__ LSE, const int* __restrict__ seqlens,
+                                                          int Hkv, int Sk, int D, float scale_log2) {
+  static_assert(G >= 1 && G <= 8, "query heads per kv-head");
+  constexpr int NW = 4, BN = 32, NS = 2;
+  constexpr int CPR = DP / 8;    // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;  // rows per 1 KiB load instruction
+  constexpr int NI = BN / RPI;   // V load instructions per tile
+  constexpr int KD = DP / 32;    // 32-wide d steps of S
+  constexpr int DT = DP / 16;    // 16-row d tiles of O^T
+  constexpr int NPAT = (CPR < 16 ? CPR : 16) / RPI > 1 ? (CPR < 16 ? CPR : 16) / RPI : 1;
+  constexpr int KLD = 2 * KD;    // K load instructions per tile
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ __attribute__((aligned(1024))) T Vs[NW][NS][BN * DP];
+  __shared__ float cml[NW][G][2];
+  __shared__ float co[NW][G][DP];
+
+  const int bk = blockIdx.x;
+  const int b = bk / Hkv, hk = bk % Hkv;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+
+  v8 qf[KD];
+#pragma unroll
+  for (int kd = 0; kd < KD; ++kd) {
+    const int d = kd * 32 + lg * 8;
+    if (li < G && d < D) qf[kd] = *reinterpret_cast<const v8*>(Q + b * sqb + (int64_t)(hk * G + li) * sqh + d);
+    else
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[kd][e] = (T)0.f;
+  }
+  const T* Kb = K + b * skb + hk * skh;
+  const T* Vb = V + b * svb + hk * svh;
+  const int sk_b = seqlens ? min(seqlens[b], Sk) : Sk;
+  const int ntiles = w * BN < sk_b ? ((sk_b + BN - 1) / BN - w + NW - 1) / NW : 0;
+
+  // K operand lanes: key 16 h + li of the tile, chunk d = 32 kd + 8 lg (clamped
+  // into the row when D < DP; those products meet zero Q entries).
+  int kdo[KD];
+#pragma unroll
+  for (int kd = 0; kd < KD; ++kd) {
+    const int d = kd * 32 + lg * 8;
+    kdo[kd] = d < D ? d : D - 8;
+  }
+  // V DMA lanes: row rl of each RPI-row group, physical chunk p (swizzled).
+  const int rl = lane / CPR, p = lane % CPR;
+  int dsw[NPAT];
+  uint32_t voff[NPAT];
+#pragma unroll
+  for (int par = 0; par < NPAT; ++par) {
+    const int c = swz(par * RPI + rl, p, CPR);
+    dsw[par] = c * 8 < D ? c * 8 : D - 8;
+    voff[par] = (uint32_t)(((int64_t)rl * svs + dsw[par]) * (int64_t)sizeof(T));
+  }
+  auto issue = [&](int t, v8 (&kf)[2][KD]) {
+    const int row0 = (w + t * NW) * BN;
+    const uint32_t vl = lds_addr(Vs[w][t % NS]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int key = row0 + 16 * h + li;
+      key = key < sk_b ? key : sk_b - 1;
+      const T* kr = Kb + (int64_t)key * sks;
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) kf[h][kd] = *reinterpret_cast<const v8*>(kr + kdo[kd]);
+    }
+    if (row0 + BN <= sk_b) {
+#pragma unroll
+      for (int n = 0; n < NI; ++n)
+        lds_dma16_s(voff[n % NPAT], Vb + (int64_t)(row0 + n * RPI) * svs, vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+    } else {
+#pragma unroll
+      for (int n = 0; n < NI; ++n) {
+        int gr = row0 + n * RPI + rl;
+        gr = gr < sk_b ? gr : sk_b - 1;
+        lds_dma16(Vb + (int64_t)gr * svs + dsw[n % NPAT], vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+      }
+    }
+  };
+
+  float m = -INFINITY, l = 0.f;
+  f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int t, const v8 (&kf)[2][KD]) {
+    const T* Vt = Vs[w][t % NS];
+    f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      s0 = mma16<T>(kf[0][kd], qf[kd], s0);
+      s1 = mma16<T>(kf[1][kd], qf[kd], s1);
+    }
+    const int kbase = (w + t * NW) * BN + 4 * lg;
+    float x[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = kbase + r < sk_b ? s0[r] * scale_log2 : -INFINITY;
+      x[4 + r] = kbase + 16 + r < sk_b ? s1[r] * scale_log2 : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (mx > m) {
+      const float a = exp2_(m - mx);
+      l *= a;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= a;
+      m = mx;
+    }
+    const float mr = m == -INFINITY ? 0.f : m;
+    v8 pf;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pe = exp2_(x[e] - mr);
+      l += pe;
+      pf[e] = (T)pe;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int key = 4 * lg + (li >> 2);
+      const int d = dt * 16 + 4 * (li & 3);
+      const T* s0p = Vt + key * DP + swz(key, d >> 3, CPR) * 8 + (d & 7);
+      const T* s1p = Vt + (key + 16) * DP + swz(key + 16, d >> 3, CPR) * 8 + (d & 7);
+      const qh_v4i16 w0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) qh_v4i16*)(s0p));
+      const qh_v4i16 w1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) qh_v4i16*)(s1p));
+      const v8 av = __builtin_bit_cast(v8, qh_v8i16(__builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7)));
+      o[dt] = mma16<T>(av, pf, o[dt]);
+    }
+    // this stage's LDS reads are complete before it is refilled
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  };
+
+  // Two register sets for K (one tile ahead); the loop is unrolled by two so
+  // each set is named statically. Tile t has landed once only tile t + 1's
+  // KLD + NI instructions are outstanding.
+  v8 ka[2][KD], kb[2][KD];
+  if (ntiles > 0) issue(0, ka);
+  for (int t = 0; t < ntiles; t += 2) {
+    if (t + 1 < ntiles) {
+      issue(t + 1, kb);
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(KLD + NI));
+    } else {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    }
+    compute(t, ka);
+    if (t + 1 < ntiles) {
+      if (t + 2 < ntiles) {
+        issue(t + 2, ka);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(KLD + NI));
+      } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      }
+      compute(t + 1, kb);
+    }
+  }
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (li < G) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) co[w][li][dt * 16 + 4 * lg + r] = o[dt][r];
+    if (lg == 0) {
+      cml[w][li][0] = m;
+      cml[w][li][1] = l;
+    }
+  }
+  __syncthreads();
+  // combine the four wavefronts in order (fa_decode_combine's arithmetic)
+  for (int idx = threadIdx.x; idx < G * DP; idx += 256) {
+    const int g = idx / DP, d = idx % DP;
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NW; ++s) M = fmaxf(M, cml[s][g][0]);
+    const float Mr = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f, acc = 0.f;
+#pragma unroll
+    for (int s = 0; s < NW; ++s) {
+      const float wgt = exp2_(cml[s][g][0] - Mr);
+      L += cml[s][g][1] * wgt;
+      acc += co[s][g][d] * wgt;
+    }
+    const int64_t row = (int64_t)bk * G + g;
+    if (d < D) O[row * D + d] = from_f32<T>(L > 0.f ? acc / L : 0.f);
+    if (d == 0 && LSE) LSE[row] = L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+  }
+}
+
 static int pick_dp(int64_t D) {
   if (D <= 32) return 32;
   if (D <= 64) return 64;
@@ -1115,6 +1317,10 @@ static int pick_dp(int64_t D) {
 // s + nsplit, ...): the waves of one sequence then read neighbouring rows at
 // the same time, which measured 3% faster at 4 splits than contiguous ranges
 // (and 10% at 8).
+// From this many (b, kv-head) pairs on (two workgroups per CU), head dim 128
+// decodes with fa_decode_wg_kernel.
+constexpr int64_t kDecodeWgMinSeqs = 512;
+
 static int decode_splits(int64_t B, int64_t Hkv, int64_t Sk) {
   const int64_t tiles = (Sk + 31) / 32;
   int64_t s = (2048 + B * Hkv - 1) / (B * Hkv);
@@ -1305,10 +1511,24 @@ extern "C" int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const vo
     return QH_E_WORKSPACE;
   }
   hipStream_t st = (hipStream_t)stream;
+  const float sl2 = scale * kLog2e;
+  if (dp == 128 && B * Hkv >= kDecodeWgMinSeqs) {
+    // many sequences: one workgroup per (b, kv-head), combined in LDS
+#define QH_WG(T, GV)                                                                                              \
+  fa_decode_wg_kernel<T, 128, GV><<<(unsigned)(B * Hkv), 256, 0, st>>>(                                         \
+      (const T*)q, sqb, sqh, (const T*)k, skb, skh, sks, (const T*)v, svb, svh, svs, (T*)o, lse, seqlens, (int)Hkv, \
+      (int)Sk, (int)D, sl2)
+#define QH_WG_G(T) \
+  if (groups == 1) QH_WG(T, 1); else if (groups == 2) QH_WG(T, 2); else if (groups == 4) QH_WG(T, 4); else QH_WG(T, 8);
+    if (dtype == QH_BF16) { QH_WG_G(bf16_t) } else { QH_WG_G(f16_t) }
+#undef QH_WG_G
+#undef QH_WG
+    QH_CHECK_LAUNCH("qh_flash_decode");
+    return QH_OK;
+  }
   const int ns = decode_splits(B, Hkv, Sk);
   float* ws_o = (float*)ws;
   float* ws_ml = ws_o + B * Hq * ns * dp;
-  const float sl2 = scale * kLog2e;
 #define QH_DEC(T, DPV, GV)                                                                                   \
   launch_decode<T, DPV, GV>(q, sqb, sqh, k, skb, skh, sks, v, svb, svh, svs, ws_o, ws_ml, seqlens, (int)B,  \
                             (int)Hkv, (int)Sk, (int)D, ns, sl2, st)

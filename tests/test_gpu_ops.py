@@ -582,6 +582,36 @@ def test_flash_decode_device_seqlens():
         close(out[b:b + 1], exp, **BF16_TOL)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,dtype", [(64, 16, 8, torch.bfloat16), (128, 32, 4, torch.bfloat16),
+                                             (512, 4, 1, torch.float16), (130, 16, 4, torch.bfloat16)])
+def test_flash_decode_many_sequences(B, Hq, Hkv, dtype):
+    """At least 512 (sequence, kv-head) pairs with head dim 128 take the one-workgroup-per-sequence
+    kernel (partials combined in LDS): per-sequence lengths including 0, 1 and non-multiples of
+    the 32-key tile, GQA groups 2/8/4, checked against fp32 torch row by row; reruns bitwise equal."""
+    D, cap = 128, 700
+    kc = randn(B, Hkv, cap, D, dtype=dtype, seed=126)
+    vc = randn(B, Hkv, cap, D, dtype=dtype, seed=127)
+    q = randn(B, Hq, 1, D, dtype=dtype, seed=128)
+    lens = torch.randint(0, cap + 1, (B,), generator=_gen(129))
+    lens[0], lens[1], lens[2] = 0, 1, cap
+    dl = lens.to(torch.int32).to(DEV)
+    c0 = native_calls("qh_flash_decode")
+    out = FA.flash_decode(q, kc, vc, D ** -0.5, Hq // Hkv, dl)
+    assert native_calls("qh_flash_decode") == c0 + 1
+    assert torch.equal(out, FA.flash_decode(q, kc, vc, D ** -0.5, Hq // Hkv, dl))
+    G = Hq // Hkv
+    qf = q.float().view(B, Hkv, G, D)
+    s = (qf @ kc.float().transpose(-1, -2).contiguous()) * D ** -0.5  # [B, Hkv, G, cap]
+    keep = torch.arange(cap, device=DEV)[None, :] < dl[:, None].long()
+    s = s.masked_fill(~keep[:, None, None, :], float("-inf"))
+    ref = torch.nan_to_num(torch.softmax(s, dim=-1)) @ vc.float()  # empty sequences give 0
+    close(out, ref.view(B, Hq, 1, D), **BF16_TOL)
+    # the full-length sequences without seqlens go through the same kernel
+    full = FA.flash_decode(q, kc, vc, D ** -0.5, G)
+    ref_full = torch.softmax((qf @ kc.float().transpose(-1, -2).contiguous()) * D ** -0.5, dim=-1) @ vc.float()
+    close(full, ref_full.view(B, Hq, 1, D), **BF16_TOL)
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 1024), (3, 2048), (7, 200)])
 def test_add_rmsnorm_matches_add_then_rmsnorm(rows, cols):
     from qwen_triton.kernels.rmsnorm import add_rmsnorm
