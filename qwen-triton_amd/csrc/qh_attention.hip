@@ -38,6 +38,29 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Combine lane l with lane l ^ 32 in registers: v_permlane32_swap exchanges the
+// upper half of its first operand with the lower half of its second, so with x
+// in both the two results hold x[l] and x[l ^ 32] (in low-half, high-half
+// order on every lane, so sums round identically on both halves).
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// A pointer computed from kernel arguments and block indices only, stated
+// wave-uniform so that address arithmetic on it stays in scalar registers.
+template <typename P>
+__device__ __forceinline__ P* uniform_ptr(P* p) {
+  const uint64_t b = (uint64_t)(uintptr_t)p;
+  const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b) |
+                     ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32);
+  return (P*)(uintptr_t)u;
+}
+
 template <typename T>
 __device__ __forceinline__ typename Mfma<T>::v8 load_frag16(const T* p) {
   return *reinterpret_cast<const typename Mfma<T>::v8*>(p);
@@ -214,6 +237,16 @@ __device__ __forceinline__ void fa_fwd_tile(const T* Kt, const T* Vt, const type
       s[kt] = Mfma<T>::mma(load_frag16<T>(Kt + row * DP + c * 8), qf[kd], s[kt]);
     }
   }
+  // Issue order of the 2 KD fragment reads (R) and MFMAs (M): KD reads, then
+  // (M R) x KD, then the last KD MFMAs, so that KD reads are in flight when
+  // the first product needs its operand (LDS latency is several MFMAs long).
+  __builtin_amdgcn_sched_group_barrier(0x100, KD, 0);
+#pragma unroll
+  for (int i = 0; i < KD; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, KD, 0);
   if (need_mask) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -228,7 +261,7 @@ __device__ __forceinline__ void fa_fwd_tile(const T* Kt, const T* Vt, const type
   float mx = fmaxf(s[0][0], s[1][0]);
 #pragma unroll
   for (int e = 1; e < 16; ++e) mx = fmaxf(mx, fmaxf(s[0][e], s[1][e]));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  mx = halves_max(mx);
   // Rescale only when some lane's running max grew by more than 2^8 in
   // probability terms: until then P = exp2((s - m) scale_log2) <= 256 stays
   // well inside bf16/fp32 range, and O / l and the LSE use the same m, so the
@@ -253,7 +286,7 @@ __device__ __forceinline__ void fa_fwd_tile(const T* Kt, const T* Vt, const type
       s[kt][e] = p;
       ps += p;
     }
-  l += ps + __shfl_xor(ps, 32);
+  l += ps;  // this half's keys only: the halves' sums are joined once, after the last tile
   // V^T fragments through the LDS transpose read (see the note above).
   const int grp = lane >> 4, j = lane & 15;
 #pragma unroll
@@ -288,8 +321,8 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: keeps tile branches scalar
   const int ql = lane & 31, hf = lane >> 5;
   const T* Qb = Q + b * sqb + hq * sqh;
-  const T* Kb = K + b * skb + hk * skh;
-  const T* Vb = V + b * svb + hk * svh;
+  const T* Kb = uniform_ptr(K + b * skb + hk * skh);
+  const T* Vb = uniform_ptr(V + b * svb + hk * svh);
   const int qw0 = qb * BMQ + wid * 32;
   const int qi = qw0 + ql;
 
@@ -334,6 +367,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
     fa_fwd_tile<T, DP>(Ks[buf], Vs[buf], qf, acc, m, l, kv0, need_mask, lim, scale_log2, lane);
   }
 
+  l = halves_sum(l);
   if (qi < Sq) {
     T* Ob = O + ((int64_t)bh * Sq + qi) * D;
     const float inv = l > 0.f ? 1.0f / l : 0.f;
@@ -556,7 +590,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
 // the 32 queries of half w >> 2. K and V of the workgroup's keys are staged in
 // LDS once and their fragments are read per use (holding them in registers
 // would not fit two waves per SIMD); Q and dO tiles stream through two LDS
-// stages, all loaded by wavefronts 0-3. At the end the two
+// stages, all loaded by wavefronts 0-3, together with the tile's 64 lse and
+// Delta values (a global load inside the loop would make the compiler's
+// vmcnt wait also cover the next tile's untracked LDS fill). At the end the two
 // query halves' dK/dV partials are added in a fixed order (half 0 + half 1)
 // through LDS. Same per-tile arithmetic as fa_bwd_dkdv_tile.
 template <typename T, int DP>
@@ -591,6 +627,8 @@ __device__ __forceinline__ void fa_bwd_dkdv_half(const T* Qt, const T* Ot, const
     dp = Mfma<T>::mma(fo[kd & 1], fv[kd & 1], dp);
     __builtin_amdgcn_sched_barrier(0);
   }
+  // lse (log2 units) and Delta of this lane's 16 queries, from the tile's LDS
+  // copy (read here: holding them across the products would cost 32 registers)
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int il = qt * 32 + g * 8 + hf * 4;
@@ -646,6 +684,7 @@ __global__ __launch_bounds__(512) void fa_bwd_dkdv8_kernel(
   T* Vs = Ks + KB * DP;                         // [KB][DP]
   T* Qs = Vs + KB * DP;                         // [2][BQ][DP]
   T* Os = Qs + 2 * BQ * DP;                     // [2][BQ][DP]
+  float* Ls = reinterpret_cast<float*>(Os + 2 * BQ * DP);  // [2][lse2 BQ | Delta BQ]
 
   const int bk = blockIdx.y;
   const int b = bk / Hkv, hk = bk % Hkv;
@@ -689,6 +728,13 @@ __global__ __launch_bounds__(512) void fa_bwd_dkdv8_kernel(
     const int hq = hk * groups + g;
     qload.load(Qs + buf * BQ * DP, Q + b * sqb + hq * sqh, sqs, q0, Sq);
     oload.load(Os + buf * BQ * DP, dO + ((int64_t)b * Hq + hq) * Sq * D, D, q0, Sq);
+    // rows are sqp >= q0 + BQ floats long, 16-byte aligned: lanes 0-15 copy
+    // lse2[q0 .. q0 + 63], lanes 16-31 Delta[q0 .. q0 + 63]
+    if (wid == 0 && lane < 32) {
+      const int64_t bhq = (int64_t)b * Hq + hq;
+      const float* src = (lane < 16 ? LSE2 : Delta) + bhq * sqp + q0 + 4 * (lane & 15);
+      lds_dma16(src, lds_addr(Ls + buf * 2 * BQ));
+    }
   };
   if (ntiles > 0 && loader) issue(0, 0);
   // this wavefront's 32 keys; the swizzle depends on the row's low 4 bits only,
@@ -700,12 +746,11 @@ __global__ __launch_bounds__(512) void fa_bwd_dkdv8_kernel(
     __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile `it` (and of V) have landed
     __syncthreads();                // ... and everyone else's; tile it-1 is fully consumed
     if (it + 1 < ntiles && loader) issue(it + 1, buf ^ 1);
-    const int g = it / nqt, q0 = q_start + (it % nqt) * BQ;
-    const int64_t bh = (int64_t)b * Hq + hk * groups + g;
+    const int q0 = q_start + (it % nqt) * BQ;
     const int qh0 = q0 + qt * 32;
     const bool need_mask = (qh0 + 32 > Sq) || (kw0 + 32 > Sk) || (causal && kw0 + 31 > qh0 + coff);
-    const float* lse_row = LSE2 + bh * sqp + q0;
-    const float* dl_row = Delta + bh * sqp + q0;
+    const float* lse_row = Ls + buf * 2 * BQ;
+    const float* dl_row = lse_row + BQ;
     const T* Qt = Qs + buf * BQ * DP;
     const T* Ot = Os + buf * BQ * DP;
     // one code path for masked and unmasked tiles: two inlined copies would
@@ -780,6 +825,17 @@ __device__ __forceinline__ void fa_bwd_dq_tile(const T* Kt, const T* Vt, const t
       sc = Mfma<T>::mma(load_frag16<T>(Kt + row * DP + c * 8), qf[kd], sc);
       dp = Mfma<T>::mma(load_frag16<T>(Vt + row * DP + c * 8), of[kd], dp);
     }
+    // Issue order of the 2 KD fragment reads (R) and MFMAs (M): 4 R, then
+    // (M R) x (2 KD - 4), then 4 M: four reads in flight ahead of their
+    // products instead of one. The fence keeps the later dQ reads out.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * KD - 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int g = 0; g < 4; ++g)
 #pragma unroll
@@ -1386,8 +1442,9 @@ extern "C" int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq) {
 }
 
 namespace {
-// LDS of fa_bwd_dkdv8_kernel: K and V of 128 keys plus two Q and two dO tiles of 64 rows.
-constexpr int kDkdv8Lds = (2 * 128 + 4 * 64) * 128 * 2;
+// LDS of fa_bwd_dkdv8_kernel: K and V of 128 keys plus two Q and two dO tiles of 64 rows,
+// and two (lse2, Delta) pairs of 64 floats.
+constexpr int kDkdv8Lds = (2 * 128 + 4 * 64) * 128 * 2 + 2 * 2 * 64 * 4;
 
 // Raise the dynamic-LDS limit of fa_bwd_dkdv8_kernel once per device.
 template <typename T>
