@@ -51,6 +51,19 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Block order of the (blocks x rows) attention grids: the grid is walked as
+// one sequence in dispatch order (x fastest) and position L runs block rank
+// L / rows of row L % rows. Every row's rank-0 block is dispatched before any
+// row's rank-1 block, so with the heaviest blocks at rank 0 (the most visible
+// keys or queries under a causal mask) the long blocks start first and the
+// short ones fill the tail. A row keeps L mod 8, i.e. one XCD and its L2,
+// when rows is a multiple of 8.
+__device__ __forceinline__ void block_rank_row(int& rank, int& row) {
+  const int L = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+  rank = L / (int)gridDim.y;
+  row = L - rank * (int)gridDim.y;
+}
+
 // A pointer computed from kernel arguments and block indices only, stated
 // wave-uniform so that address arithmetic on it stays in scalar registers.
 template <typename P>
@@ -314,8 +327,9 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
   __shared__ __attribute__((aligned(1024))) T Vs[2][BN * DP];
 
   const int nqb = (Sq + BMQ - 1) / BMQ;
-  const int qb = nqb - 1 - (int)blockIdx.x;
-  const int bh = blockIdx.y;
+  int rank, bh;
+  block_rank_row(rank, bh);
+  const int qb = nqb - 1 - rank;  // last query blocks see the most keys
   const int b = bh / Hq, hq = bh % Hq, hk = hq / groups;
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: keeps tile branches scalar
@@ -502,9 +516,10 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
   __shared__ __attribute__((aligned(1024))) T Qs[2][BQ * DP];
   __shared__ __attribute__((aligned(1024))) T Os[2][BQ * DP];
 
-  const int bk = blockIdx.y;
+  int rank, bk;
+  block_rank_row(rank, bk);  // first key blocks see the most queries
   const int b = bk / Hkv, hk = bk % Hkv;
-  const int k0 = blockIdx.x * 128;
+  const int k0 = rank * 128;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int ql = lane & 31, hf = lane >> 5;
   const int kj = k0 + wid * 32 + ql;  // this lane's key (C-layout column)
@@ -686,9 +701,10 @@ __global__ __launch_bounds__(512) void fa_bwd_dkdv8_kernel(
   T* Os = Qs + 2 * BQ * DP;                     // [2][BQ][DP]
   float* Ls = reinterpret_cast<float*>(Os + 2 * BQ * DP);  // [2][lse2 BQ | Delta BQ]
 
-  const int bk = blockIdx.y;
+  int rank, bk;
+  block_rank_row(rank, bk);  // first key blocks see the most queries
   const int b = bk / Hkv, hk = bk % Hkv;
-  const int k0 = blockIdx.x * KB;
+  const int k0 = rank * KB;
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ks = wid & 3, qt = wid >> 2;
@@ -873,8 +889,10 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
   __shared__ __attribute__((aligned(1024))) T Vs[2][BN * DP];
 
   const int nqb = (Sq + BMQ - 1) / BMQ;
-  const int qb = nqb - 1 - (int)blockIdx.x;
-  const int64_t bh = blockIdx.y;
+  int rank, bhi;
+  block_rank_row(rank, bhi);
+  const int qb = nqb - 1 - rank;  // last query blocks see the most keys
+  const int64_t bh = bhi;
   const int b = (int)(bh / Hq), hq = (int)(bh % Hq), hk = hq / groups;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int ql = lane & 31, hf = lane >> 5;
@@ -1416,6 +1434,7 @@ extern "C" int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
                "qh_flash_fwd: strides must be multiples of 8 elements");
   QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_flash_fwd: bf16/f16 only");
   QH_CHECK_ARG(B * Hq < 65536 && Sq < (1 << 30) && Sk < (1 << 30), "qh_flash_fwd: too large");
+  QH_CHECK_ARG((Sq + 127) / 128 * B * Hq < (1ll << 31), "qh_flash_fwd: too many query blocks");
   if (B * Hq * Sq == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;
   const float sl2 = scale * kLog2e;
@@ -1484,6 +1503,8 @@ extern "C" int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
                "qh_flash_bwd: strides must be multiples of 8 elements");
   QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_flash_bwd: bf16/f16 only");
   QH_CHECK_ARG(B * Hq < 65536 && Sq < (1 << 30) && Sk < (1 << 30), "qh_flash_bwd: too large");
+  QH_CHECK_ARG((Sq + 127) / 128 * B * Hq < (1ll << 31) && (Sk + 127) / 128 * B * Hkv < (1ll << 31),
+               "qh_flash_bwd: too many query or key blocks");
   const int64_t need = qh_flash_bwd_workspace(B, Hq, Sq);
   if (ws_bytes < need) {
     qh::set_error("qh_flash_bwd: workspace %lld < %lld", (long long)ws_bytes, (long long)need);
