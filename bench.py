@@ -93,10 +93,14 @@ def fill_cache(model, batch, ctx, capacity, seed=0):
 
 
 def decode_step_fn(model, cache, ids, ctx):
+    from qwen_triton.kernels.moe_routing import _native_topk
+
     def step():
         cache.attention_lengths = [ctx] * len(cache.attention_lengths)
         logits = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1).logits
-        return logits[:, -1].argmax(dim=-1)
+        # greedy pick on the library's top-1 kernel (ties to the lowest index, as argmax), the
+        # one greedy_generate's captured step uses
+        return _native_topk(logits[:, -1], 1)[1].squeeze(-1)
 
     return step
 

@@ -266,11 +266,36 @@ int qh_gemm_ws(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const 
  * each product rounded to the dtype first, as qh_gemm twice followed by
  * qh_silu_mul_fwd would (C_1 is not written).
  * Replaces, fused, the separate TritonLinear calls of
- * qwen_triton/modules/attention.py:95-103 (q/k/v) and qwen_triton/modules/mlp.py:19-22
+ * qwen_triton/modules/attention.py:55-66 (q/k/v) and qwen_triton/modules/mlp.py:19-22
  * (gate/up, silu_mul), each via qwen_triton/kernels/matmul.py:130-155. */
 int qh_gemm_multi(int64_t M, int64_t K, const void* A, int64_t lda, int count, const void* const* B,
                   const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
                   const void* const* bias, int gated, int dtype, void* stream);
+/* qh_gemm_multi with two fusions of the decoder layer's inference chain:
+ * - norm_w != NULL: A holds RMSNorm inputs h and the products are those of
+ *   RMSNorm(h): operand round(h * (norm_w + one_plus)), each output row scaled
+ *   by rsqrt(mean_k(h^2) + eps) (fp32, fixed order) after the sum over K. The
+ *   single rounding of the normalised operand is taken before the row factor
+ *   instead of after it (qh_rmsnorm_fwd then a product). norm_w [K] has the
+ *   activation dtype (norm_wdtype == dtype), 16-byte aligned. Needs
+ *   qh_gemm_multi_norm_fits(M, K, gated, count, N).
+ * - residual (host array of count entries, or NULL; entries may be NULL):
+ *   C_i = round(round(product_i) + R_i) with R_i [M, N_i] of row stride ldr[i],
+ *   as qh_gemm followed by qh_add; not with gated.
+ * Replaces, fused, the norms of qwen_triton/models/core.py:127 and :146 (via
+ * qwen_triton/kernels/rmsnorm.py:101-196) with the projections that follow
+ * them (qwen_triton/modules/attention.py:55-66, qwen_triton/modules/mlp.py:19-22),
+ * and the residual adds of qwen_triton/models/core.py:144 and :152 (via
+ * qwen_triton/kernels/residual_add.py:86-101) with the o_proj and down_proj
+ * products before them (qwen_triton/modules/attention.py:128, mlp.py:22). */
+int qh_gemm_multi_ex(int64_t M, int64_t K, const void* A, int64_t lda, int count, const void* const* B,
+                     const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
+                     const void* const* bias, const void* const* residual, const int64_t* ldr, int gated,
+                     const void* norm_w, int norm_wdtype, float eps, int one_plus, int dtype, void* stream);
+/* 1 when a qh_gemm_multi_ex launch of these shapes can take the norm prologue
+ * (every workgroup holds all K columns of its rows in one load chunk), else 0.
+ * No counterpart in the reference: a capability query for the fusion above. */
+int64_t qh_gemm_multi_norm_fits(int64_t M, int64_t K, int gated, int count, const int64_t* N);
 /* out[n] = sum_m X[m*ldx + n] in a fixed order (bias gradient).
  * Replaces qwen_triton/kernels/matmul.py:114-127 (_row_sum_kernel). */
 int qh_colsum(const void* X, int64_t ldx, int64_t M, int64_t N, void* out, int dtype, int out_dtype,

@@ -221,27 +221,78 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
 //
 // k mapping per 32-wide step: lane group q = lane / 16 takes k0 + 8 q .. +7,
 // so the four groups of a row read 64 contiguous bytes.
+//
+// NORM: the rows of A are RMSNorm inputs h. The kernel multiplies the
+// operand round(h * (w + wadd)) and scales each output row by
+// rsqrt(mean_k(h^2) + eps) after the sum over K: RMSNorm followed by the
+// product with the per-row factor moved past the (linear) sum, and the one
+// operand rounding taken before it. Every workgroup holds all K columns of its
+// rows (its 16 waves are the K slices, each slice loaded in one chunk), so the
+// row sums of squares are this lane's pairs (v_dot2), the four lane groups
+// of a row, then the 16 slices in order through LDS in the epilogue; the
+// multiplies never wait for them. Residual (per product, optional):
+// C = round(round(product) + R), the residual-add kernel's rounding.
 constexpr int kMaxProducts = 4;
 template <typename T, typename OT>
 struct DecodeProducts {
   const T* B[kMaxProducts];
   OT* C[kMaxProducts];
   const T* bias[kMaxProducts];
-  int64_t ldb[kMaxProducts], ldc[kMaxProducts];
+  const T* res[kMaxProducts];
+  int64_t ldb[kMaxProducts], ldc[kMaxProducts], ldr[kMaxProducts];
   int N[kMaxProducts];
   int tile0[kMaxProducts + 1];  // first workgroup of each product
   int count;
 };
 
-template <typename T, typename OT, int MT, int KSP, bool GATED>
+struct DecodeNorm {
+  const void* w;  // RMSNorm weight [K] in the activation dtype, nullptr = no norm
+  float eps, wadd;
+};
+
+// k-steps whose loads one wave issues together (a NORM launch needs its whole
+// K slice in one chunk).
+__host__ __device__ constexpr int decode_chunk(int mt, bool gated) { return (mt <= 2 ? 8 : 4) / (gated ? 2 : 1); }
+// NORM launches hold the row scaling beside the fragments: at most 8 A
+// fragments per lane (no scratch spills at 128 VGPRs).
+__host__ __device__ constexpr int decode_norm_chunk(int mt, bool gated) {
+  return gated ? (mt == 1 ? 4 : 2) : (mt == 1 ? 8 : 2);
+}
+// Longest row a NORM launch normalises.
+constexpr int kDecodeNormMaxK = 8192;
+
+// acc + sum of the squares of 8 packed 16-bit values, two per v_dot2 (fp32 sums).
+template <typename T>
+__device__ __forceinline__ float sumsq8(const typename Mfma<T>::v8& v, float acc) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    typedef __bf16 p2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const p2 x = {v[e], v[e + 1]};
+      acc = __builtin_amdgcn_fdot2_f32_bf16(x, x, acc, false);
+    }
+  } else {
+    typedef _Float16 p2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const p2 x = {(_Float16)v[e], (_Float16)v[e + 1]};
+      acc = __builtin_amdgcn_fdot2(x, x, acc, false);
+    }
+  }
+  return acc;
+}
+
+template <typename T, typename OT, int MT, int KSP, bool GATED, bool NORM>
 __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__ A, int64_t lda,
-                                                           const DecodeProducts<T, OT> P, int M, int K, int kr,
-                                                           int ms, int tiles) {
+                                                           const DecodeProducts<T, OT> P, const DecodeNorm nrm,
+                                                           int M, int K, int kr, int ms, int tiles) {
   constexpr int CG = 16 / KSP;
   constexpr int NB = GATED ? 2 : 1;                       // weight matrices per wave
-  constexpr int CH = (MT <= 2 ? 8 : 4) / NB;              // k-steps whose loads are issued together
+  constexpr int CH = NORM ? decode_norm_chunk(MT, GATED) : decode_chunk(MT, GATED);  // k-steps loaded together
+  static_assert(!NORM || KSP == 16, "the norm prologue needs all 16 waves on K slices");
   typedef typename Mfma<T>::v8 v8;
   __shared__ float red[16][MT * 16][16];
+  __shared__ float nss[NORM ? 16 : 1][MT * 16];
   // Workgroup -> (column tile, row group). The ms row groups of a tile get
   // workgroup ids that are equal mod 8, so they run on one XCD and read the
   // tile's weights through the same L2.
@@ -272,12 +323,18 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   v8 zero;
 #pragma unroll
   for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
-  for (int k0 = kb; k0 < ke; k0 += 32 * CH) {
+  // With NORM every wave runs exactly one chunk (slices past K load zeros), so
+  // all of them reach the barrier of the norm reduction.
+  for (int k0 = kb; NORM ? k0 == kb : k0 < ke; k0 += 32 * CH) {
     v8 b[CH][NB], a[CH][MT];
+    v8 wr[NORM ? CH : 1];  // norm weights (dtype T) of this lane's 8 columns per step
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int k = k0 + u * 32 + q * 8;
       const bool kok = k < ke;
+      if constexpr (NORM) {
+        if (kok) wr[u] = *reinterpret_cast<const v8*>((const T*)nrm.w + k);
+      }
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
         if (nok && kok) b[u][j] = *reinterpret_cast<const v8*>(brow[j] + k);
@@ -288,6 +345,30 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
         const int m = m0 + i * 16 + li;
         if (m < M && kok) a[u][i] = *reinterpret_cast<const v8*>(A + (int64_t)m * lda + k);
         else a[u][i] = zero;
+      }
+    }
+    if constexpr (NORM) {
+      // Row sums of squares of h (the epilogue adds the slices), then the
+      // operands round(h * (w + wadd)).
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < CH; ++u) ss = sumsq8<T>(a[u][i], ss);
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        if (q == 0) nss[wid][i * 16 + li] = ss;
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        if (k0 + u * 32 + q * 8 >= ke) continue;  // a[u][*] is zero there
+        float wv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wv[e] = to_f32(wr[u][e]) + nrm.wadd;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[u][i][e] = from_f32<T>(to_f32(a[u][i][e]) * wv[e]);
       }
     }
 #pragma unroll
@@ -319,6 +400,12 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
       const int grow = m0 + row;
       if (grow >= M || gn >= N) continue;
       const T* bias = P.bias[pi + j];
+      if constexpr (NORM) {  // the row's RMSNorm factor (slices summed in order)
+        float ss = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) ss += nss[s2][row];
+        v *= rsqrtf(ss / (float)K + nrm.eps);
+      }
       const float val = v + (bias ? to_f32(bias[gn]) : 0.f);
       if constexpr (GATED) {
         if (j == 0) {
@@ -328,20 +415,26 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
           P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
         }
       } else {
-        P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = from_f32<OT>(val);
+        OT o = from_f32<OT>(val);
+        const T* res = P.res[pi];
+        if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)grow * P.ldr[pi] + gn]));
+        P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = o;
       }
     }
   }
 }
 
+// Returns QH_E_ARG (nothing launched) when a norm prologue is asked for a
+// shape whose K slices do not fit one load chunk (decode_norm_fits).
 template <typename T, typename OT>
-void launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int M, int K, bool gated,
-                            hipStream_t st, int ms_force = 0) {
+int launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int M, int K, bool gated,
+                           hipStream_t st, int ms_force = 0, const DecodeNorm* nrm = nullptr) {
   // Narrow outputs: all 16 waves split K (16 columns per workgroup). Wide
   // outputs already give enough workgroups: 4 column groups x 4 K slices.
   int maxN = 0;
   for (int i = 0; i < P.count; ++i) maxN = P.N[i] > maxN ? P.N[i] : maxN;
-  const bool wide = !gated && maxN > 8192;
+  const bool norm = nrm != nullptr && nrm->w != nullptr;
+  const bool wide = !gated && !norm && maxN > 8192;
   const int ksp = wide ? 4 : 16;
   const int cols = 16 * (16 / ksp);
   const int nprod = gated ? 1 : P.count;  // the gated pair shares its column tiles
@@ -361,13 +454,42 @@ void launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, i
   if (ms_force > 0 && ms_force <= mt) ms = ms_force;
   const int mtw = (mt + ms - 1) / ms;
   const int grid = (tiles + 7) / 8 * 8 * ms;
-#define QH_DG(MTV, KSPV, GV) \
-  gemm_decode_kernel<T, OT, MTV, KSPV, GV><<<grid, 1024, 0, st>>>(a, lda, P, M, K, kr, ms, tiles)
-#define QH_DG_W(MTV) \
-  if (gated) QH_DG(MTV, 16, true); else if (wide) QH_DG(MTV, 4, false); else QH_DG(MTV, 16, false);
+  if (norm && (K > kDecodeNormMaxK || kr > 32 * decode_norm_chunk(mtw, gated))) return QH_E_ARG;
+  const DecodeNorm nz = norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f};
+  constexpr bool kNormOk = std::is_same<T, OT>::value;  // the only instantiation a norm launch reaches
+  if (norm && !kNormOk) return QH_E_ARG;
+#define QH_DG(MTV, KSPV, GV, NV) \
+  gemm_decode_kernel<T, OT, MTV, KSPV, GV, NV><<<grid, 1024, 0, st>>>(a, lda, P, nz, M, K, kr, ms, tiles)
+#define QH_DG_W(MTV)                                           \
+  if constexpr (kNormOk) {                                     \
+    if (norm) {                                                \
+      if (gated) QH_DG(MTV, 16, true, true); else QH_DG(MTV, 16, false, true); \
+      return QH_OK;                                            \
+    }                                                          \
+  }                                                            \
+  if (gated) QH_DG(MTV, 16, true, false);                      \
+  else if (wide) QH_DG(MTV, 4, false, false);                  \
+  else QH_DG(MTV, 16, false, false);
   if (mtw == 1) { QH_DG_W(1) } else if (mtw == 2) { QH_DG_W(2) } else if (mtw == 3) { QH_DG_W(3) } else { QH_DG_W(4) }
 #undef QH_DG_W
 #undef QH_DG
+  return QH_OK;
+}
+
+// Whether a norm-prologue launch of M rows, K columns fits (all 16 K slices
+// of every workgroup loaded in one chunk); mirrors launch_decode_products.
+static bool decode_norm_fits(int M, int K, bool gated, int count, const int64_t* N) {
+  const int cols = 16;
+  int tiles = 0;
+  for (int i = 0; i < (gated ? 1 : count); ++i) tiles += (int)((N[i] + cols - 1) / cols);
+  const int kr = ((K + 15) / 16 + 31) / 32 * 32;
+  const int mt = (M + 15) / 16;
+  int ms = 1;
+  while (ms * 4 < mt) ms *= 2;
+  while (ms < mt && tiles * ms * 2 <= 256) ms *= 2;
+  if (ms > mt) ms = mt;
+  const int mtw = (mt + ms - 1) / ms;
+  return K <= kDecodeNormMaxK && kr <= 32 * decode_norm_chunk(mtw, gated);
 }
 
 template <typename T, typename OT>
@@ -729,9 +851,11 @@ extern "C" int qh_gemm_ws(int trans_a, int trans_b, int64_t M, int64_t N, int64_
   return QH_OK;
 }
 
-extern "C" int qh_gemm_multi(int64_t M, int64_t K, const void* A, int64_t lda, int count, const void* const* B,
-                             const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
-                             const void* const* bias, int gated, int dtype, void* stream) {
+extern "C" int qh_gemm_multi_ex(int64_t M, int64_t K, const void* A, int64_t lda, int count, const void* const* B,
+                                const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
+                                const void* const* bias, const void* const* residual, const int64_t* ldr, int gated,
+                                const void* norm_w, int norm_wdtype, float eps, int one_plus, int dtype,
+                                void* stream) {
   QH_CHECK_ARG(count >= 1 && count <= kMaxProducts, "qh_gemm_multi: 1..%d products", kMaxProducts);
   QH_CHECK_ARG(M >= 0 && M <= 128 && K > 0 && K < (1ll << 31), "qh_gemm_multi: needs 0 <= M <= 128 and K > 0");
   QH_CHECK_ARG(!gated || (count == 2 && N[0] == N[1]), "qh_gemm_multi: gated needs two products of equal N");
@@ -742,27 +866,55 @@ extern "C" int qh_gemm_multi(int64_t M, int64_t K, const void* A, int64_t lda, i
     QH_CHECK_ARG(N[i] > 0 && N[i] < (1ll << 31) && aligned16(B[i]) && ldb[i] % 8 == 0 && ldb[i] >= K,
                  "qh_gemm_multi: product %d: bad B or N", i);
     QH_CHECK_ARG((gated && i == 1) || (C[i] != nullptr && ldc[i] >= N[i]), "qh_gemm_multi: product %d: bad C", i);
+    QH_CHECK_ARG(residual == nullptr || residual[i] == nullptr || (!gated && ldr != nullptr && ldr[i] >= N[i]),
+                 "qh_gemm_multi: product %d: residual needs a non-gated product and ldr >= N", i);
   }
+  QH_CHECK_ARG(norm_w == nullptr || (norm_wdtype == dtype && aligned16(norm_w)),
+               "qh_gemm_multi: the norm weight must have the activation dtype and be 16-byte aligned");
+  QH_CHECK_ARG(norm_w == nullptr || M == 0 || decode_norm_fits((int)M, (int)K, gated != 0, count, N),
+               "qh_gemm_multi: the norm prologue does not fit M=%lld K=%lld (see qh_gemm_multi_norm_fits)",
+               (long long)M, (long long)K);
   if (M == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;
-#define QH_MULTI(T)                                                       \
-  {                                                                       \
-    DecodeProducts<T, T> P = {};                                          \
-    for (int i = 0; i < count; ++i) {                                     \
-      P.B[i] = (const T*)B[i];                                            \
-      P.C[i] = (T*)C[i];                                                  \
-      P.bias[i] = bias ? (const T*)bias[i] : nullptr;                     \
-      P.ldb[i] = ldb[i];                                                  \
-      P.ldc[i] = ldc[i];                                                  \
-      P.N[i] = (int)N[i];                                                 \
-    }                                                                     \
-    P.count = count;                                                      \
-    launch_decode_products<T, T>((const T*)A, lda, P, (int)M, (int)K, gated != 0, st); \
+  const DecodeNorm nrm{norm_w, eps, one_plus ? 1.f : 0.f};
+  int rc = QH_OK;
+#define QH_MULTI(T)                                                                                     \
+  {                                                                                                     \
+    DecodeProducts<T, T> P = {};                                                                        \
+    for (int i = 0; i < count; ++i) {                                                                   \
+      P.B[i] = (const T*)B[i];                                                                          \
+      P.C[i] = (T*)C[i];                                                                                \
+      P.bias[i] = bias ? (const T*)bias[i] : nullptr;                                                   \
+      P.res[i] = residual ? (const T*)residual[i] : nullptr;                                            \
+      P.ldb[i] = ldb[i];                                                                                \
+      P.ldc[i] = ldc[i];                                                                                \
+      P.ldr[i] = residual && residual[i] ? ldr[i] : 0;                                                  \
+      P.N[i] = (int)N[i];                                                                               \
+    }                                                                                                   \
+    P.count = count;                                                                                    \
+    rc = launch_decode_products<T, T>((const T*)A, lda, P, (int)M, (int)K, gated != 0, st, 0, &nrm);   \
   }
   if (dtype == QH_BF16) QH_MULTI(bf16_t) else QH_MULTI(f16_t)
 #undef QH_MULTI
+  if (rc) {
+    qh::set_error("qh_gemm_multi: the norm prologue does not fit M=%lld K=%lld", (long long)M, (long long)K);
+    return rc;
+  }
   QH_CHECK_LAUNCH("qh_gemm_multi");
   return QH_OK;
+}
+
+extern "C" int qh_gemm_multi(int64_t M, int64_t K, const void* A, int64_t lda, int count, const void* const* B,
+                             const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
+                             const void* const* bias, int gated, int dtype, void* stream) {
+  return qh_gemm_multi_ex(M, K, A, lda, count, B, ldb, N, C, ldc, bias, nullptr, nullptr, gated, nullptr, QH_F32,
+                          0.f, 0, dtype, stream);
+}
+
+extern "C" int64_t qh_gemm_multi_norm_fits(int64_t M, int64_t K, int gated, int count, const int64_t* N) {
+  if (M < 0 || M > 128 || K <= 0 || K >= (1ll << 31) || count < 1 || count > kMaxProducts) return 0;
+  if (M == 0) return 1;
+  return decode_norm_fits((int)M, (int)K, gated != 0, count, N) ? 1 : 0;
 }
 
 extern "C" int qh_moe_gemm(int mode, const void* A, int64_t lda, const int32_t* rows, const void* const* B_table,

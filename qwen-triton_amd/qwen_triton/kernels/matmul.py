@@ -71,12 +71,38 @@ def linear_group_ok(x: torch.Tensor, weights: list[torch.Tensor]) -> bool:
                and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0 for w in weights)
 
 
+def linear_group_norm_ok(x: torch.Tensor, weights: list[torch.Tensor], norm_weight: torch.Tensor,
+                         gated: bool = False) -> bool:
+    """True when ``linear_group(..., norm=...)`` can normalise the rows of ``x`` inside the launch."""
+    if not linear_group_ok(x, weights):
+        return False
+    k = x.shape[-1]
+    if not (norm_weight.is_cuda and norm_weight.dim() == 1 and norm_weight.shape[0] == k
+            and norm_weight.is_contiguous() and norm_weight.dtype == x.dtype and norm_weight.data_ptr() % 16 == 0):
+        return False
+    if gated and (len(weights) != 2 or weights[0].shape[0] != weights[1].shape[0]):
+        return False
+    n = len(weights)
+    nn_ = (ctypes.c_int64 * n)(*(w.shape[0] for w in weights))
+    m = x.numel() // max(k, 1)
+    return bool(_native.call("qh_gemm_multi_norm_fits", m, k, int(gated), n, ctypes.addressof(nn_)))
+
+
 def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torch.Tensor | None] | None = None,
-                 gated: bool = False):
+                 gated: bool = False, norm: tuple[torch.Tensor, float, bool] | None = None,
+                 residual: list[torch.Tensor | None] | None = None):
     """One launch for ``x @ W_i.T (+ b_i)`` over products that share ``x`` (M <= 128, no autograd).
 
     Returns the list of outputs, or ``silu(x @ W_0.T) * (x @ W_1.T)`` when ``gated``; each
     product is computed and rounded exactly as ``triton_matmul`` would.
+
+    ``norm = (weight, eps, one_plus)``: ``x`` holds RMSNorm inputs and the products use
+    ``rmsnorm(x)``: the operand is ``round(x * (weight + one_plus))`` and each output row is
+    scaled by ``rsqrt(mean(x^2) + eps)`` after the sum over K, so the one rounding of the
+    normalised operand sits before the row factor rather than after it (check
+    ``linear_group_norm_ok`` first; the weight has the activation dtype). ``residual[i]`` (same
+    shape as output i): output i is ``residual_add(x @ W_i.T (+ b_i), residual[i])``, rounded as
+    the two kernels round.
     """
     k = x.shape[-1]
     x2 = _rows(x, k)
@@ -93,10 +119,35 @@ def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torc
     ldc = arr_l(*([o.stride(0) for o in outs] + [0] * (n - len(outs))))
     has_bias = any(b is not None for b in biases)
     bias_arr = arr_p(*((b.contiguous().data_ptr() if b is not None else None) for b in biases)) if has_bias else None
-    _native.call("qh_gemm_multi", m, k, x2.data_ptr(), x2.stride(0), n, ctypes.addressof(bptr), ctypes.addressof(ldb),
-                 ctypes.addressof(nn_), ctypes.addressof(cptr), ctypes.addressof(ldc),
-                 ctypes.addressof(bias_arr) if has_bias else None, int(gated), _native.dtype_code(x.dtype),
-                 _native.stream(x.device))
+    if norm is None and residual is None:
+        _native.call("qh_gemm_multi", m, k, x2.data_ptr(), x2.stride(0), n, ctypes.addressof(bptr),
+                     ctypes.addressof(ldb), ctypes.addressof(nn_), ctypes.addressof(cptr), ctypes.addressof(ldc),
+                     ctypes.addressof(bias_arr) if has_bias else None, int(gated), _native.dtype_code(x.dtype),
+                     _native.stream(x.device))
+    else:
+        res_arr = ldr = None
+        if residual is not None:
+            if gated or len(residual) != n:
+                raise ValueError("linear_group: residual needs one entry per (non-gated) product")
+            rs = []
+            for r, o in zip(residual, outs):
+                if r is None:
+                    rs.append(None)
+                    continue
+                r2 = _rows(r, o.shape[1])
+                if r2.shape != o.shape or r2.dtype != x.dtype or not r2.is_cuda:
+                    raise ValueError(f"linear_group: residual {tuple(r.shape)} does not match output {tuple(o.shape)}")
+                rs.append(r2)
+            res_arr = arr_p(*(None if r is None else r.data_ptr() for r in rs))
+            ldr = arr_l(*(0 if r is None else r.stride(0) for r in rs))
+        nw, eps, one_plus = norm if norm is not None else (None, 0.0, False)
+        _native.call("qh_gemm_multi_ex", m, k, x2.data_ptr(), x2.stride(0), n, ctypes.addressof(bptr),
+                     ctypes.addressof(ldb), ctypes.addressof(nn_), ctypes.addressof(cptr), ctypes.addressof(ldc),
+                     ctypes.addressof(bias_arr) if has_bias else None,
+                     ctypes.addressof(res_arr) if res_arr is not None else None,
+                     ctypes.addressof(ldr) if ldr is not None else None, int(gated),
+                     None if nw is None else nw.data_ptr(), _native.dtype_code(nw.dtype) if nw is not None else 0,
+                     float(eps), int(bool(one_plus)), _native.dtype_code(x.dtype), _native.stream(x.device))
     lead = x.shape[:-1]
     outs = [o.view(*lead, o.shape[1]) for o in outs]
     return outs[0] if gated else outs

@@ -10,7 +10,13 @@ Differences, all in the dispatch rather than the maths:
   every prefill to fp32 SDPA);
 * the largest cache position is known on the host when ``cache_position`` is
   generated here, so the cache write needs no device-to-host sync;
-* ``greedy_generate`` preallocates the KV cache for the whole generation.
+* ``greedy_generate`` preallocates the KV cache for the whole generation;
+* inference with at most 128 tokens runs each dense layer as five launches: the
+  input norm inside the q/k/v product, the attention, o_proj with the residual
+  add, the post-attention norm inside the gate/up product, down_proj with the
+  residual add (``FUSE_NORM_GEMM``; a fused norm rounds the operand
+  ``x * weight`` and applies the row factor after the product, where the RMSNorm
+  kernel rounds ``x * factor * weight``: one rounding step placed differently).
 """
 from __future__ import annotations
 
@@ -23,6 +29,7 @@ from transformers.modeling_outputs import CausalLMOutputWithPast
 
 from qwen_triton.configs import QwenTritonConfig
 from qwen_triton.kernels.cross_entropy import triton_cross_entropy
+from qwen_triton.kernels.matmul import linear_group, linear_group_norm_ok, linear_group_ok
 from qwen_triton.kernels.residual_add import residual_add
 from qwen_triton.kernels.rmsnorm import add_rmsnorm, add_rmsnorm_ok
 from qwen_triton.modules import (
@@ -36,6 +43,11 @@ from qwen_triton.modules import (
 )
 from qwen_triton.modules.embedding import TritonEmbedding
 from qwen_triton.modules.linear import TritonLinear
+
+# Inference on the GPU with at most 128 tokens: fold each dense layer's norms and residual
+# adds into its projections (see QwenDecoderLayer.forward_fused). False keeps the separate
+# (bitwise-reference) kernels.
+FUSE_NORM_GEMM = True
 
 _DTYPES = {
     "fp16": torch.float16, "float16": torch.float16, "half": torch.float16,
@@ -108,6 +120,50 @@ class QwenDecoderLayer(nn.Module):
             return add_rmsnorm(x, residual, norm.weight, norm.eps, norm.one_plus_weight)
         s = residual_add(x, residual)
         return s, norm(s)
+
+    def fused_inference_ok(self, hidden_states: torch.Tensor, position_embeddings, past_key_values,
+                           cache_position) -> bool:
+        """Whether ``forward_fused`` serves this call: a full-attention layer with a dense MLP,
+        inference on the GPU (bf16/fp16, at most 128 tokens, position-indexed cache), shapes the
+        fused launches take."""
+        if not FUSE_NORM_GEMM or torch.is_grad_enabled() or self.layer_type != "full_attention":
+            return False
+        if not isinstance(self.mlp, QwenMLP) or not hidden_states.is_cuda or hidden_states.dim() != 3:
+            return False
+        attn, mlp = self.self_attn, self.mlp
+        if not attn._fused_prepare_ok(hidden_states, position_embeddings[0], past_key_values, cache_position):
+            return False
+        key = (hidden_states.shape[0] * hidden_states.shape[1], hidden_states.dtype, hidden_states.device)
+        cache = self.__dict__.setdefault("_fused_ok_cache", {})
+        if key not in cache:
+            rows = hidden_states.reshape(-1, hidden_states.shape[-1])
+            qkv = [attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight]
+            gu = [mlp.gate_proj.weight, mlp.up_proj.weight]
+            o_in = torch.empty((rows.shape[0], attn.o_proj.weight.shape[1]), dtype=rows.dtype, device=rows.device)
+            d_in = torch.empty((rows.shape[0], mlp.down_proj.weight.shape[1]), dtype=rows.dtype, device=rows.device)
+            cache[key] = (mlp.gate_proj.bias is None and mlp.up_proj.bias is None
+                          and attn.o_proj.weight.shape[0] == rows.shape[1] == mlp.down_proj.weight.shape[0]
+                          and linear_group_norm_ok(rows, qkv, self.input_layernorm.weight)
+                          and linear_group_norm_ok(rows, gu, self.post_attention_layernorm.weight, gated=True)
+                          and linear_group_ok(o_in, [attn.o_proj.weight])
+                          and linear_group_ok(d_in, [mlp.down_proj.weight]))
+        return cache[key]
+
+    def forward_fused(self, hidden_states, position_embeddings, attention_mask=None, past_key_values=None,
+                      cache_position=None, max_position: int | None = None) -> torch.Tensor:
+        """The layer in five launches (``fused_inference_ok``); ``hidden_states`` is the full residual
+        stream and so is the result."""
+        attn, mlp = self.self_attn, self.mlp
+        ln1, ln2 = self.input_layernorm, self.post_attention_layernorm
+        projs = (attn.q_proj, attn.k_proj, attn.v_proj)
+        q2, k2, v2 = linear_group(hidden_states, [p.weight for p in projs], [p.bias for p in projs],
+                                  norm=(ln1.weight, ln1.eps, ln1.one_plus_weight))
+        out = attn.attend_projected(q2, k2, v2, position_embeddings, attention_mask, past_key_values,
+                                    cache_position, max_position)
+        h = linear_group(out, [attn.o_proj.weight], [attn.o_proj.bias], residual=[hidden_states])[0]
+        gu = linear_group(h, [mlp.gate_proj.weight, mlp.up_proj.weight], gated=True,
+                          norm=(ln2.weight, ln2.eps, ln2.one_plus_weight))
+        return linear_group(gu, [mlp.down_proj.weight], [mlp.down_proj.bias], residual=[h])[0]
 
     def forward(self, hidden_states, position_embeddings, attention_mask=None, past_key_values=None,
                 cache_position=None, max_position: int | None = None, residual_in: torch.Tensor | None = None,
@@ -200,6 +256,13 @@ class QwenTritonModel(nn.Module):
         residual = None
         for layer in self.layers:
             layer_mask = attention_mask if layer.layer_type == "linear_attention" else masks[layer.layer_type]
+            if chain and layer.fused_inference_ok(hidden, position_embeddings, past_key_values, cache_position):
+                if residual is not None:  # the previous layer deferred its closing add
+                    hidden, residual = residual_add(hidden, residual), None
+                hidden = layer.forward_fused(hidden, position_embeddings=position_embeddings,
+                                             attention_mask=layer_mask, past_key_values=past_key_values,
+                                             cache_position=cache_position, max_position=max_position)
+                continue
             out = layer(hidden, position_embeddings=position_embeddings, attention_mask=layer_mask,
                         past_key_values=past_key_values, cache_position=cache_position, max_position=max_position,
                         residual_in=residual, defer_residual=chain)

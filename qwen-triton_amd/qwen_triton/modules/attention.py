@@ -130,6 +130,23 @@ class QwenFullAttention(nn.Module):
                      _native.stream(q2.device))
         return q_out, kc[:, :, :n, :], vc[:, :, :n, :]
 
+    def attend_projected(self, q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor,
+                         position_embeddings: tuple[torch.Tensor, torch.Tensor], attention_mask, past_key_values,
+                         cache_position, max_position: int | None) -> torch.Tensor:
+        """Inference after the projections (``_fused_prepare_ok`` holds): q/k norm, RoPE and cache
+        write in one pass, then attention; returns the o_proj input ``[B, S, Hq * D]``."""
+        cos, sin = position_embeddings
+        input_shape = q2.shape[:-1]
+        q, k, v = self._fused_prepare(q2, k2, v2, cos, sin, past_key_values, cache_position, max_position)
+        static = getattr(past_key_values, "static", None)
+        if static is not None and q.shape[2] == 1 and attention_mask is None:
+            # captured decode step: k/v span the reserved cache, each sequence's valid length
+            # is read from device memory
+            out = _fa.flash_decode(q, k, v, self.scaling, self.num_key_value_groups, seqlens=static.seqlens)
+        else:
+            out = self._attend(q, k, v, attention_mask, q2.dtype)
+        return out.transpose(1, 2).reshape(*input_shape, -1)
+
     def forward(
         self,
         hidden_states: torch.Tensor,
@@ -148,15 +165,9 @@ class QwenFullAttention(nn.Module):
                 q2, k2, v2 = linear_group(hidden_states, weights, [p.bias for p in projs])
             else:
                 q2, k2, v2 = (p(hidden_states) for p in projs)
-            q, k, v = self._fused_prepare(q2, k2, v2, cos, sin, past_key_values, cache_position, max_position)
-            static = getattr(past_key_values, "static", None)
-            if static is not None and q.shape[2] == 1 and attention_mask is None:
-                # captured decode step: k/v span the reserved cache, each sequence's valid length
-                # is read from device memory
-                out = _fa.flash_decode(q, k, v, self.scaling, self.num_key_value_groups, seqlens=static.seqlens)
-            else:
-                out = self._attend(q, k, v, attention_mask, hidden_states.dtype)
-            return self.o_proj(out.transpose(1, 2).reshape(*input_shape, -1))
+            out = self.attend_projected(q2, k2, v2, position_embeddings, attention_mask, past_key_values,
+                                        cache_position, max_position)
+            return self.o_proj(out)
         if getattr(past_key_values, "static", None) is not None:
             raise RuntimeError("a captured decode step needs the fused inference path (bf16/fp16 on the GPU, "
                                "no output gate, no autograd)")

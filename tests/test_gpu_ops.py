@@ -412,6 +412,103 @@ def test_linear_group_gated_matches_gemms_then_silu_mul(M):
     close(fused, O.silu_mul(O.linear(x, wg), O.linear(x, wu)), atol=3e-2, rtol=3e-2)
 
 
+@pytest.mark.parametrize("M", [1, 7, 20, 64, 128])
+@pytest.mark.parametrize("gated", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_linear_group_norm_prologue(M, gated, dtype):
+    # rows normalised inside the launch vs rmsnorm followed by the same grouped launch:
+    # the one rounding of the normalised operand is placed differently, so outputs agree
+    # within a few output rounding steps; both within the band of the fp64 oracle
+    from qwen_triton.kernels.matmul import linear_group, linear_group_norm_ok
+
+    Kd = 1024
+    x = randn(M, Kd, dtype=dtype, seed=240, scale=3.0)
+    nw = (1.0 + 0.2 * randn(Kd, dtype=torch.float32, seed=241)).to(dtype)
+    # a norm weight of another dtype keeps the separate norm
+    ws0 = [randn(64, Kd, dtype=dtype, seed=249, scale=0.05)]
+    assert not linear_group_norm_ok(x, ws0, nw.float())
+    ns = (2048, 1024, 1000) if not gated else (3072, 3072)
+    ws = [randn(n, Kd, dtype=dtype, seed=242 + i, scale=0.05) for i, n in enumerate(ns)]
+    assert linear_group_norm_ok(x, ws, nw, gated=gated)
+    c0 = native_calls("qh_gemm_multi_ex")
+    fused = linear_group(x, ws, gated=gated, norm=(nw, 1e-6, False))
+    assert native_calls("qh_gemm_multi_ex") == c0 + 1
+    y = K.rmsnorm(x, nw, 1e-6)
+    plain = linear_group(y, ws, gated=gated)
+    fused, plain = ([fused], [plain]) if gated else (fused, plain)
+    # fp64 oracles with each path's rounding points: the reference rounds the normalised
+    # rows (plain path); the fused path rounds x * w and applies the row factor after the
+    # product. Both round gate and up before the SiLU-mul.
+    bf = lambda t: t.to(dtype).to(torch.float64)  # noqa: E731
+    xd = x.cpu().double()
+    inv = torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6)
+    yo = bf(O.rmsnorm(x, nw, 1e-6))
+    yw = bf(xd * nw.cpu().double())
+
+    def prods(y, scale):
+        outs = [O.linear(y, w) * scale for w in ws]
+        return [O.silu_mul(bf(outs[0]), bf(outs[1]))] if gated else outs
+
+    for f, p_, r_plain, r_fused in zip(fused, plain, prods(yo, 1.0), prods(yw, inv)):
+        # a few rounding steps of the largest output (one bf16 step is 2^-8 to 2^-7 relative):
+        # the reference's bf16 band taken relative to the output scale
+        assert (f.float() - p_.float()).abs().max().item() <= 2e-2 * p_.float().abs().max().item() + 1e-3
+        close(p_, r_plain, atol=3e-2, rtol=3e-2)
+        close(f, r_fused, atol=3e-2, rtol=3e-2)
+    again = linear_group(x, ws, gated=gated, norm=(nw, 1e-6, False))
+    for f, a in zip(fused, [again] if gated else again):
+        assert torch.equal(f, a)
+
+
+def test_linear_group_norm_one_plus_and_zero_rows():
+    from qwen_triton.kernels.matmul import linear_group
+
+    Kd = 512
+    x = randn(5, Kd, dtype=torch.bfloat16, seed=250)
+    x[2].zero_()  # an all-zero row normalises to zero (rsqrt(eps) * 0)
+    nw = 0.1 * randn(Kd, dtype=torch.bfloat16, seed=251)
+    w = randn(256, Kd, dtype=torch.bfloat16, seed=252, scale=0.05)
+    out = linear_group(x, [w], norm=(nw, 1e-6, True))[0]
+    ref = O.linear(O.rmsnorm(x, nw, 1e-6, one_plus=True), w)
+    close(out, ref, atol=3e-2, rtol=3e-2)
+    assert torch.equal(out[2], torch.zeros_like(out[2]))
+
+
+def test_linear_group_norm_fit_limits():
+    # every workgroup must hold all K columns of its rows: K = 1024 fits the gated 64-row
+    # launch with 3072 columns (all 64 rows in one workgroup), K = 2048 does not (then the
+    # caller keeps the separate norm)
+    from qwen_triton.kernels.matmul import linear_group, linear_group_norm_ok
+
+    x = randn(64, 2048, dtype=torch.bfloat16, seed=260)
+    ws = [randn(3072, 2048, dtype=torch.bfloat16, seed=261 + i, scale=0.05) for i in range(2)]
+    nw = torch.ones(2048, dtype=torch.bfloat16, device=DEV)
+    assert not linear_group_norm_ok(x, ws, nw, gated=True)
+    with pytest.raises(_native.NativeError):
+        linear_group(x, ws, gated=True, norm=(nw, 1e-6, False))
+    assert linear_group_norm_ok(x[:, :1024].contiguous(), [w[:, :1024].contiguous() for w in ws],
+                                nw[:1024].contiguous(), gated=True)
+
+
+@pytest.mark.parametrize("M", [1, 64, 128])
+@pytest.mark.parametrize("Kd,N", [(2048, 1024), (3072, 1024), (1024, 9000)])
+def test_linear_group_residual_epilogue_bitwise(M, Kd, N):
+    # o_proj / down_proj with the residual add in the epilogue equal the same launch without
+    # it followed by residual_add, bit for bit (and triton_matmul where it takes the decode
+    # kernel, up to 8192 columns)
+    from qwen_triton.kernels.matmul import linear_group
+
+    x = randn(M, Kd, dtype=torch.bfloat16, seed=270)
+    w = randn(N, Kd, dtype=torch.bfloat16, seed=271, scale=0.05)
+    b = randn(N, dtype=torch.bfloat16, seed=272)
+    r = randn(M, N, dtype=torch.bfloat16, seed=273, scale=4.0)
+    out = linear_group(x, [w], [b], residual=[r])[0]
+    assert torch.equal(out, K.residual_add(linear_group(x, [w], [b])[0], r))
+    if N <= 8192:
+        assert torch.equal(out, K.residual_add(K.triton_matmul(x, w, b), r))
+    close(out, O.residual_add(O.linear(x, w, b).to(torch.bfloat16), r), **BF16_TOL)
+
+
 def test_mlp_inference_path_matches_autograd_path():
     from qwen_triton.modules import QwenMLP
 
