@@ -115,15 +115,20 @@ def version() -> str:
     return lib().qh_version().decode()
 
 
+_FNS: dict[str, tuple] = {}
+
+
 def call(name: str, *args) -> int:
     """Invoke an entry point; raise NativeError on a non-zero status."""
-    handle = lib()
-    fn = getattr(handle, name)
+    entry = _FNS.get(name)
+    if entry is None:
+        handle = lib()
+        entry = _FNS[name] = (getattr(handle, name), _SIGNATURES[name][0] == "i")
+    fn, checked = entry
     rc = fn(*args)
     CALLS[name] += 1
-    restype = _SIGNATURES[name][0]
-    if restype == "i" and rc != 0:
-        msg = handle.qh_last_error().decode(errors="replace")
+    if checked and rc != 0:
+        msg = lib().qh_last_error().decode(errors="replace")
         raise NativeError(f"{name} failed (status {rc}): {msg}")
     return rc
 
@@ -140,7 +145,14 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def stream(device: torch.device | None = None) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """Raw handle of torch's current stream on ``device`` (the stream every kernel is enqueued on)."""
+    if device is None:
+        index = torch.cuda.current_device()
+    else:
+        index = device.index if isinstance(device, torch.device) else int(device)
+        if index is None:
+            index = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def require_device(*tensors: torch.Tensor | None) -> None:

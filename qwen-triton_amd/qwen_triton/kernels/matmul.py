@@ -71,6 +71,36 @@ def linear_group_ok(x: torch.Tensor, weights: list[torch.Tensor]) -> bool:
                and w.stride(0) % 8 == 0 and w.data_ptr() % 16 == 0 for w in weights)
 
 
+_PLANS: dict[tuple, tuple] = {}
+
+
+def _group_plan(weights: list[torch.Tensor], biases: list[torch.Tensor | None] | None) -> tuple:
+    """Host argument arrays of the weight side of a grouped launch (pointer, row stride and rows of
+    each weight, bias pointers), built once per set of weight and bias tensors."""
+    n = len(weights)
+    biases = biases or [None] * n
+    key = tuple((w.data_ptr(), w.shape[0], w.stride(0)) for w in weights) + tuple(
+        None if b is None else (b.data_ptr(), b.stride(0)) for b in biases)
+    plan = _PLANS.get(key)
+    if plan is None:
+        if len(_PLANS) > 4096:
+            _PLANS.clear()
+        arr_p = ctypes.c_void_p * n
+        arr_l = ctypes.c_int64 * n
+        bptr = arr_p(*(w.data_ptr() for w in weights))
+        ldb = arr_l(*(w.stride(0) for w in weights))
+        nn_ = arr_l(*(w.shape[0] for w in weights))
+        if any(b is not None for b in biases):
+            if any(b is not None and b.stride(0) != 1 for b in biases):
+                raise ValueError("linear_group: biases must be contiguous")
+            bias_arr = arr_p(*(None if b is None else b.data_ptr() for b in biases))
+            plan = (bptr, ldb, nn_, ctypes.addressof(bias_arr), bias_arr)
+        else:
+            plan = (bptr, ldb, nn_, None)
+        _PLANS[key] = plan
+    return plan
+
+
 def linear_group_norm_ok(x: torch.Tensor, weights: list[torch.Tensor], norm_weight: torch.Tensor,
                          gated: bool = False) -> bool:
     """True when ``linear_group(..., norm=...)`` can normalise the rows of ``x`` inside the launch."""
@@ -108,22 +138,17 @@ def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torc
     x2 = _rows(x, k)
     m = x2.shape[0]
     n = len(weights)
-    biases = biases or [None] * n
+    plan = _group_plan(weights, biases)
     outs = [torch.empty((m, w.shape[0]), dtype=x.dtype, device=x.device) for w in (weights[:1] if gated else weights)]
     arr_p = ctypes.c_void_p * n
     arr_l = ctypes.c_int64 * n
-    bptr = arr_p(*(w.data_ptr() for w in weights))
-    ldb = arr_l(*(w.stride(0) for w in weights))
-    nn_ = arr_l(*(w.shape[0] for w in weights))
     cptr = arr_p(*([o.data_ptr() for o in outs] + [None] * (n - len(outs))))
     ldc = arr_l(*([o.stride(0) for o in outs] + [0] * (n - len(outs))))
-    has_bias = any(b is not None for b in biases)
-    bias_arr = arr_p(*((b.contiguous().data_ptr() if b is not None else None) for b in biases)) if has_bias else None
+    bptr, ldb, nn_, bias_addr = plan[:4]  # `plan` keeps the bias array alive
     if norm is None and residual is None:
         _native.call("qh_gemm_multi", m, k, x2.data_ptr(), x2.stride(0), n, ctypes.addressof(bptr),
                      ctypes.addressof(ldb), ctypes.addressof(nn_), ctypes.addressof(cptr), ctypes.addressof(ldc),
-                     ctypes.addressof(bias_arr) if has_bias else None, int(gated), _native.dtype_code(x.dtype),
-                     _native.stream(x.device))
+                     bias_addr, int(gated), _native.dtype_code(x.dtype), _native.stream(x.device))
     else:
         res_arr = ldr = None
         if residual is not None:
@@ -143,8 +168,7 @@ def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torc
         nw, eps, one_plus = norm if norm is not None else (None, 0.0, False)
         _native.call("qh_gemm_multi_ex", m, k, x2.data_ptr(), x2.stride(0), n, ctypes.addressof(bptr),
                      ctypes.addressof(ldb), ctypes.addressof(nn_), ctypes.addressof(cptr), ctypes.addressof(ldc),
-                     ctypes.addressof(bias_arr) if has_bias else None,
-                     ctypes.addressof(res_arr) if res_arr is not None else None,
+                     bias_addr, ctypes.addressof(res_arr) if res_arr is not None else None,
                      ctypes.addressof(ldr) if ldr is not None else None, int(gated),
                      None if nw is None else nw.data_ptr(), _native.dtype_code(nw.dtype) if nw is not None else 0,
                      float(eps), int(bool(one_plus)), _native.dtype_code(x.dtype), _native.stream(x.device))
