@@ -360,6 +360,30 @@ int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int6
                     int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o, float* lse,
                     const int32_t* seqlens, void* ws, int64_t ws_bytes, int64_t B, int64_t Hq, int64_t Hkv,
                     int64_t Sk, int64_t D, float scale, int dtype, void* stream);
+/* 1 when qh_flash_decode_prepare serves these shapes (D == 128, Hq / Hkv in
+ * {1, 2, 4, 8}, at least 512 (sequence, kv-head) pairs), else 0. No counterpart
+ * in the reference: a capability query for the fused decode step below. */
+int64_t qh_flash_decode_prepare_ok(int64_t B, int64_t Hq, int64_t Hkv, int64_t D);
+/* One decode step of attention (one new token per sequence) with its input
+ * preparation: q_norm/k_norm, RoPE and the K/V cache writes of qh_attn_prepare
+ * (same arithmetic, bitwise equal) fused into the decode kernel, so the
+ * prepared q never leaves the chip. q, k, v are the step's projected rows
+ * ([B, H*D], row strides sq, sk, sv), cos/sin [cos_batch, 1, rot] (batch stride
+ * scb), positions[0] the step's cache position (rows outside [0, cap) are not
+ * written), k_cache/v_cache [B, Hkv, cap, D] with the given strides. The
+ * attention reads keys [0, min(seqlens[b], Sk)) (seqlens may be NULL: Sk) and
+ * writes o [B, Hq, D] and, if lse is not NULL, the log-sum-exp as qh_flash_decode.
+ * Replaces, fused, qwen_triton/modules/attention.py:68-82 (q/k norm, RoPE, the
+ * cache update) and the q_len == 1 attention of :100-109 (via
+ * qwen_triton/kernels/flash_attention.py:54-152). */
+int qh_flash_decode_prepare(const void* q, int64_t sq, const void* k, int64_t sk, const void* v, int64_t sv,
+                            const void* qw, const void* kw, float eps, int one_plus, const void* cos,
+                            const void* sin, int64_t scb, int64_t cos_batch, int64_t rot, void* k_cache,
+                            int64_t kcb, int64_t kch, int64_t kcs, void* v_cache, int64_t vcb, int64_t vch,
+                            int64_t vcs, int64_t cap, const int64_t* positions, void* o, float* lse,
+                            const int32_t* seqlens, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk,
+                            int64_t D, float scale, int dtype, int wdtype, int cdtype, void* stream);
+
 
 #ifdef __cplusplus
 }

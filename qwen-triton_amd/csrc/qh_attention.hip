@@ -30,6 +30,7 @@
 // fixed-order combine.
 #include "qh_lds.h"
 #include "qh_mfma.h"
+#include "qh_prep.h"
 
 namespace {
 
@@ -1184,13 +1185,43 @@ __global__ __launch_bounds__(256) void fa_decode_combine(const float* __restrict
 // partial (m, l, o) are combined in LDS in wavefront order with
 // fa_decode_combine's arithmetic: no workspace and no second launch, and the
 // same results as the split kernel plus combine at 4 splits.
-template <typename T, int DP, int G>
+//
+// PREP (one new token per sequence): the kernel also prepares its own rows,
+// replacing the separate prepare pass. Each wavefront loads its rows, issues
+// its first two K/V tiles, then normalises and rotates the group's G query
+// rows itself (norm_rope_row, the prepare pass's arithmetic) and regroups them
+// into its MFMA operand through a private LDS slot, so no wavefront waits for
+// another. The wavefront that will read the key tile holding the new position
+// p also writes the new key row (normalised, rotated) and value row into the
+// caches at p. Vector-memory counts retire in issue order, so the loop's wait
+// before tile 2 is requested also covers those stores; only when p lies in the
+// wave's first three tiles does it write first and drain before that tile.
+template <typename T, typename C>
+struct DecodePrepArgs {
+  const T* q;  // projected rows of the step: q [B, Hq * D], k and v [B, Hkv * D] (row strides sq, sk, sv)
+  const T* k;
+  const T* v;
+  int64_t sq, sk, sv;
+  const void* qw;  // q_norm / k_norm weights (wdtype), + wadd
+  const void* kw;
+  int wdtype;
+  float eps, wadd;
+  const C* cs;  // cos / sin of the step, [cos_batch, 1, rot] (batch stride scb)
+  const C* sn;
+  int64_t scb;
+  int cos_batch, half, rot;
+  const int64_t* pos;  // the step's cache position (one for every sequence)
+  int64_t cap;         // rows allocated in the caches (positions outside [0, cap) are not written)
+};
+
+template <typename T, int DP, int G, bool PREP = false, typename C = float>
 __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
                                                           const T* __restrict__ K, int64_t skb, int64_t skh,
                                                           int64_t sks, const T* __restrict__ V, int64_t svb,
                                                           int64_t svh, int64_t svs, T* __restrict__ O,
                                                           float* __restrict__ LSE, const int* __restrict__ seqlens,
-                                                          int Hkv, int Sk, int D, float scale_log2) {
+                                                          int Hkv, int Sk, int D, float scale_log2,
+                                                          const DecodePrepArgs<T, C> pa) {
   static_assert(G >= 1 && G <= 8, "query heads per kv-head");
   constexpr int NW = 4, BN = 32, NS = 2;
   constexpr int CPR = DP / 8;    // 16-byte chunks per row
@@ -1204,6 +1235,7 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
   __shared__ __attribute__((aligned(1024))) T Vs[NW][NS][BN * DP];
   __shared__ float cml[NW][G][2];
   __shared__ float co[NW][G][DP];
+  __shared__ __attribute__((aligned(16))) T qs[PREP ? NW : 1][PREP ? G : 1][DP];
 
   const int bk = blockIdx.x;
   const int b = bk / Hkv, hk = bk % Hkv;
@@ -1211,15 +1243,6 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, lg = lane >> 4;
 
-  v8 qf[KD];
-#pragma unroll
-  for (int kd = 0; kd < KD; ++kd) {
-    const int d = kd * 32 + lg * 8;
-    if (li < G && d < D) qf[kd] = *reinterpret_cast<const v8*>(Q + b * sqb + (int64_t)(hk * G + li) * sqh + d);
-    else
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[kd][e] = (T)0.f;
-  }
   const T* Kb = K + b * skb + hk * skh;
   const T* Vb = V + b * svb + hk * svh;
   const int sk_b = seqlens ? min(seqlens[b], Sk) : Sk;
@@ -1243,9 +1266,11 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
     dsw[par] = c * 8 < D ? c * 8 : D - 8;
     voff[par] = (uint32_t)(((int64_t)rl * svs + dsw[par]) * (int64_t)sizeof(T));
   }
+  int tile_p = -1;  // PREP: the tile whose rows this wave wrote (its loads wait for those stores)
   auto issue = [&](int t, v8 (&kf)[2][KD]) {
     const int row0 = (w + t * NW) * BN;
     const uint32_t vl = lds_addr(Vs[w][t % NS]);
+    if (PREP && w + t * NW == tile_p && t <= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       int key = row0 + 16 * h + li;
@@ -1267,6 +1292,72 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
       }
     }
   };
+
+  // Two register sets for K (one tile ahead); the loop below is unrolled by
+  // two so each set is named statically.
+  v8 ka[2][KD], kb[2][KD];
+  v8 qf[KD];
+  bool pre1 = false;  // tile 1 already requested before the loop
+  if constexpr (PREP) {
+    const int64_t p = pa.pos[0];
+    const bool pin = p >= 0 && p < sk_b;  // the new row is one of the keys read here
+    const int wp = pin ? (int)((p / BN) % NW) : 0;
+    tile_p = w == wp && pin ? (int)(p / BN) : -1;
+    const bool slow = tile_p >= 0 && tile_p < w + 2 * NW;  // p in this wave's first two tiles
+    // 16-lane group gi takes rows gi, gi + 4, ...: the G query rows, then (wave
+    // wp) the key row and the value row; one 16-byte load per lane and pass.
+    constexpr int NPASS = (G + 2 + 3) / 4;
+    const int gi = lane >> 4, g = lane & 15, d0 = 8 * g;
+    const bool act = d0 < D, pok = w == wp && p >= 0 && p < pa.cap;
+    const int dl = act ? d0 : D - 8;
+    Vec16<T> xv[NPASS];
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int r = gi + 4 * ps;
+      const T* src = r < G ? pa.q + b * pa.sq + (int64_t)(hk * G + r) * D
+                           : (r == G ? pa.k + b * pa.sk : pa.v + b * pa.sv) + (int64_t)hk * D;
+      xv[ps] = ld16((r < G + 2 ? src : pa.q + b * pa.sq) + dl);
+    }
+    if (!slow && ntiles > 0) {
+      issue(0, ka);
+      if (ntiles > 1) issue(1, kb), pre1 = true;
+    }
+    const int64_t co_row = (pa.cos_batch == 1 ? 0 : b) * pa.scb;
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int r = gi + 4 * ps;
+      const bool isq = r < G, isk = r == G && pok, isv = r == G + 1 && pok;
+      Vec16<T> x = xv[ps];
+      if (!act) x.raw = make_uint4(0, 0, 0, 0);
+      const Vec16<T> y = norm_rope_row<T, C>(x, act, isq ? pa.qw : pa.kw, pa.wdtype, pa.eps, pa.wadd, D, d0,
+                                             pa.half / 8, pa.half, pa.rot, pa.cs, pa.sn, co_row);
+      if (act) {
+        if (isq) *reinterpret_cast<uint4*>(&qs[w][r][d0]) = y.raw;
+        else if (isk) st16(const_cast<T*>(Kb) + p * sks + d0, y);
+        else if (isv) st16(const_cast<T*>(Vb) + p * svs + d0, x);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this wave's qs rows are written
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      const int d = kd * 32 + lg * 8;
+      if (li < G && d < D) qf[kd] = *reinterpret_cast<const v8*>(&qs[w][li][d]);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[kd][e] = (T)0.f;
+    }
+    if (slow && ntiles > 0) issue(0, ka);  // issue() drains the stores before the tile holding p
+  } else {
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      const int d = kd * 32 + lg * 8;
+      if (li < G && d < D) qf[kd] = *reinterpret_cast<const v8*>(Q + b * sqb + (int64_t)(hk * G + li) * sqh + d);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[kd][e] = (T)0.f;
+    }
+    if (ntiles > 0) issue(0, ka);
+  }
 
   float m = -INFINITY, l = 0.f;
   f32x4 o[DT];
@@ -1321,14 +1412,11 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   };
 
-  // Two register sets for K (one tile ahead); the loop is unrolled by two so
-  // each set is named statically. Tile t has landed once only tile t + 1's
-  // KLD + NI instructions are outstanding.
-  v8 ka[2][KD], kb[2][KD];
-  if (ntiles > 0) issue(0, ka);
+  // Tile t has landed once only tile t + 1's KLD + NI instructions are
+  // outstanding (tile 0 was issued above).
   for (int t = 0; t < ntiles; t += 2) {
     if (t + 1 < ntiles) {
-      issue(t + 1, kb);
+      if (!(pre1 && t == 0)) issue(t + 1, kb);
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(KLD + NI));
     } else {
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -1595,7 +1683,7 @@ extern "C" int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const vo
 #define QH_WG(T, GV)                                                                                              \
   fa_decode_wg_kernel<T, 128, GV><<<(unsigned)(B * Hkv), 256, 0, st>>>(                                         \
       (const T*)q, sqb, sqh, (const T*)k, skb, skh, sks, (const T*)v, svb, svh, svs, (T*)o, lse, seqlens, (int)Hkv, \
-      (int)Sk, (int)D, sl2)
+      (int)Sk, (int)D, sl2, DecodePrepArgs<T, float>{})
 #define QH_WG_G(T) \
   if (groups == 1) QH_WG(T, 1); else if (groups == 2) QH_WG(T, 2); else if (groups == 4) QH_WG(T, 4); else QH_WG(T, 8);
     if (dtype == QH_BF16) { QH_WG_G(bf16_t) } else { QH_WG_G(f16_t) }
@@ -1630,5 +1718,61 @@ extern "C" int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const vo
 #undef QH_DEC_G
 #undef QH_DEC
   QH_CHECK_LAUNCH("qh_flash_decode");
+  return QH_OK;
+}
+
+extern "C" int64_t qh_flash_decode_prepare_ok(int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
+  if (B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D != 128) return 0;
+  const int64_t g = Hq / Hkv;
+  return (g == 1 || g == 2 || g == 4 || g == 8) && B * Hkv >= kDecodeWgMinSeqs && B * Hkv < 65536 ? 1 : 0;
+}
+
+extern "C" int qh_flash_decode_prepare(const void* q, int64_t sq, const void* k, int64_t sk, const void* v, int64_t sv,
+                                       const void* qw, const void* kw, float eps, int one_plus, const void* cos,
+                                       const void* sin, int64_t scb, int64_t cos_batch, int64_t rot, void* k_cache,
+                                       int64_t kcb, int64_t kch, int64_t kcs, void* v_cache, int64_t vcb, int64_t vch,
+                                       int64_t vcs, int64_t cap, const int64_t* positions, void* o, float* lse,
+                                       const int32_t* seqlens, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk,
+                                       int64_t D, float scale, int dtype, int wdtype, int cdtype, void* stream) {
+  QH_CHECK_ARG(qh_flash_decode_prepare_ok(B, Hq, Hkv, D), "qh_flash_decode_prepare: shape not served (B=%lld Hq=%lld "
+               "Hkv=%lld D=%lld; see qh_flash_decode_prepare_ok)", (long long)B, (long long)Hq, (long long)Hkv,
+               (long long)D);
+  QH_CHECK_ARG(Sk >= 0 && Sk <= cap && cap < (1ll << 31), "qh_flash_decode_prepare: need 0 <= Sk <= cap < 2^31");
+  const int64_t half = rot / 2;
+  QH_CHECK_ARG(rot >= 16 && rot <= D && rot % 16 == 0 && ((half / 8) & (half / 8 - 1)) == 0,
+               "qh_flash_decode_prepare: rotary dim %lld must be 16 * 2^k <= D", (long long)rot);
+  QH_CHECK_ARG(cos_batch == 1 || cos_batch == B, "qh_flash_decode_prepare: cos/sin batch must be 1 or B");
+  QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && aligned16(k_cache) &&
+                   aligned16(v_cache),
+               "qh_flash_decode_prepare: pointers must be 16-byte aligned");
+  QH_CHECK_ARG(sq % 8 == 0 && sk % 8 == 0 && sv % 8 == 0 && kcb % 8 == 0 && kch % 8 == 0 && kcs % 8 == 0 &&
+                   vcb % 8 == 0 && vch % 8 == 0 && vcs % 8 == 0,
+               "qh_flash_decode_prepare: strides must be multiples of 8 elements");
+  QH_CHECK_ARG(kcs < (1 << 24) && vcs < (1 << 24), "qh_flash_decode_prepare: key/value row stride too large");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_flash_decode_prepare: bf16/f16 only");
+  QH_CHECK_ARG(wdtype == QH_F32 || wdtype == dtype, "qh_flash_decode_prepare: norm weights must be fp32 or the dtype");
+  QH_CHECK_ARG(cdtype == QH_F32 || cdtype == dtype, "qh_flash_decode_prepare: cos/sin must be fp32 or the dtype");
+  hipStream_t st = (hipStream_t)stream;
+  const float sl2 = scale * kLog2e;
+  const int groups = (int)(Hq / Hkv);
+#define QH_WGP(T, C, GV)                                                                                           \
+  {                                                                                                                \
+    DecodePrepArgs<T, C> pa{(const T*)q, (const T*)k, (const T*)v, sq, sk, sv, qw, kw, wdtype, eps,               \
+                            one_plus ? 1.f : 0.f, (const C*)cos, (const C*)sin, scb, (int)cos_batch, (int)half,    \
+                            (int)rot, positions, cap};                                                            \
+    fa_decode_wg_kernel<T, 128, GV, true, C><<<(unsigned)(B * Hkv), 256, 0, st>>>(                               \
+        (const T*)o, 0, 0, (const T*)k_cache, kcb, kch, kcs, (const T*)v_cache, vcb, vch, vcs, (T*)o, lse, seqlens, \
+        (int)Hkv, (int)Sk, (int)D, sl2, pa);                                                                      \
+  }
+#define QH_WGP_G(T, C) \
+  if (groups == 1) QH_WGP(T, C, 1) else if (groups == 2) QH_WGP(T, C, 2) else if (groups == 4) QH_WGP(T, C, 4) else QH_WGP(T, C, 8)
+  if (dtype == QH_BF16) {
+    if (cdtype == QH_F32) { QH_WGP_G(bf16_t, float) } else { QH_WGP_G(bf16_t, bf16_t) }
+  } else {
+    if (cdtype == QH_F32) { QH_WGP_G(f16_t, float) } else { QH_WGP_G(f16_t, f16_t) }
+  }
+#undef QH_WGP_G
+#undef QH_WGP
+  QH_CHECK_LAUNCH("qh_flash_decode_prepare");
   return QH_OK;
 }

@@ -2,7 +2,7 @@
 // layer. Each replaces a chain of the single-op kernels with one launch and
 // one pass over the data, with the same per-element arithmetic and rounding
 // points as that chain (so results match it exactly).
-#include "qh_common.h"
+#include "qh_prep.h"
 
 namespace {
 
@@ -44,37 +44,8 @@ __global__ __launch_bounds__(256) void attn_prepare_kernel(
     const bool isq = j < Hq;
     const int h = isq ? j : j - Hq;
     if (act) xv = ld16(isq ? q + t * sq + h * D + d0 : k + t * sk + h * D + d0);
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float f = to_f32(xv.v[e]);
-      ss += f * f;
-    }
-    ss = wave_sum(ss, 16);
-    const float inv = rsqrtf(ss / (float)D + eps);
-    const void* w = isq ? qw : kw;
-    float y[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      y[e] = act ? to_f32(from_f32<T>((to_f32(xv.v[e]) * inv) * (load_any(w, wdtype, d0 + e) + wadd))) : 0.f;
-    float px[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) px[e] = __shfl_xor(y[e], hl, 16);
-    Vec16<T> o;
-    if (d0 < rot) {
-      const bool lo = d0 < half;
-      const int ci = lo ? d0 : d0 - half;
-      const int64_t co = (cos_batch == 1 ? 0 : b) * scb + s * scs + ci;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float cc = to_f32(cs[co + e]), sv2 = to_f32(sn[co + e]);
-        const float a = lo ? y[e] : px[e], bb = lo ? px[e] : y[e];
-        o.v[e] = lo ? from_f32<T>(a * cc - bb * sv2) : from_f32<T>(bb * cc + a * sv2);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o.v[e] = from_f32<T>(y[e]);
-    }
+    const Vec16<T> o = norm_rope_row<T, C>(xv, act, isq ? qw : kw, wdtype, eps, wadd, D, d0, hl, half, rot, cs, sn,
+                                           (cos_batch == 1 ? 0 : b) * scb + s * scs);
     if (!act) continue;
     if (isq) st16(q_out + ((b * Hq + h) * (int64_t)S + s) * D + d0, o);
     else if (p >= 0 && p < cap) st16(kc + b * kcb + h * kch + p * kcs + d0, o);

@@ -1,0 +1,49 @@
+// Attention input preparation of one (token, head) row, shared by the fused
+// prepare pass (qh_fused.hip) and the decode attention that prepares its own
+// rows (qh_attention.hip), so both round exactly alike.
+#pragma once
+#include "qh_common.h"
+
+// A row of D <= 128 elements on a 16-lane group, 8 per lane (lane g holds
+// d0 = 8 g .. d0 + 7; act = d0 < D): RMSNorm over D (fp32 sums, the 16-lane
+// DPP reduction of the norm kernel, rounded to T), then rotate-half RoPE of the
+// first rot elements with cos/sin[co_row + (d mod half)] (rounded to T); the
+// rest passes through. hl = half / 8 is the lane distance between the halves.
+// All 16 lanes of the group must call it together.
+template <typename T, typename C>
+__device__ __forceinline__ Vec16<T> norm_rope_row(const Vec16<T>& xv, bool act, const void* w, int wdtype, float eps,
+                                                  float wadd, int D, int d0, int hl, int half, int rot,
+                                                  const C* __restrict__ cs, const C* __restrict__ sn,
+                                                  int64_t co_row) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float f = to_f32(xv.v[e]);
+    ss += f * f;
+  }
+  ss = wave_sum(ss, 16);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    y[e] = act ? to_f32(from_f32<T>((to_f32(xv.v[e]) * inv) * (load_any(w, wdtype, d0 + e) + wadd))) : 0.f;
+  float px[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) px[e] = __shfl_xor(y[e], hl, 16);
+  Vec16<T> o;
+  if (d0 < rot) {
+    const bool lo = d0 < half;
+    const int ci = lo ? d0 : d0 - half;
+    const int64_t co = co_row + ci;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float cc = to_f32(cs[co + e]), sv2 = to_f32(sn[co + e]);
+      const float a = lo ? y[e] : px[e], bb = lo ? px[e] : y[e];
+      o.v[e] = lo ? from_f32<T>(a * cc - bb * sv2) : from_f32<T>(bb * cc + a * sv2);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o.v[e] = from_f32<T>(y[e]);
+  }
+  return o;
+}

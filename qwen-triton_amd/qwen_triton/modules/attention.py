@@ -35,6 +35,12 @@ from qwen_triton.modules.norms import QwenRMSNorm
 from qwen_triton.modules.rotary import apply_rotary_pos_emb
 
 
+# Decode steps (one new token per sequence) of many sequences run the q/k norm, RoPE and cache
+# writes inside the decode-attention kernel (``qh_flash_decode_prepare``); False keeps the
+# separate prepare pass. Both give identical results.
+FUSE_DECODE_PREPARE = True
+
+
 def repeat_kv(hidden_states: torch.Tensor, n_rep: int) -> torch.Tensor:
     b, h, s, d = hidden_states.shape
     if n_rep == 1:
@@ -130,6 +136,49 @@ class QwenFullAttention(nn.Module):
                      _native.stream(q2.device))
         return q_out, kc[:, :, :n, :], vc[:, :, :n, :]
 
+    def _decode_prepare_ok(self, q2: torch.Tensor, attention_mask, cos: torch.Tensor, sin: torch.Tensor) -> bool:
+        if not (FUSE_DECODE_PREPARE and attention_mask is None and q2.shape[1] == 1
+                and cos.shape[1] == 1 and sin.shape == cos.shape):
+            return False
+        cache = self.__dict__.setdefault("_decode_prepare_cache", {})
+        bsz = q2.shape[0]
+        if bsz not in cache:
+            cache[bsz] = bool(_native.call("qh_flash_decode_prepare_ok", bsz, self.num_heads,
+                                           self.num_key_value_heads, self.head_dim))
+        return cache[bsz]
+
+    def _fused_decode(self, q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor, cos: torch.Tensor,
+                      sin: torch.Tensor, past_key_values: QwenTritonCache, cache_position: torch.Tensor,
+                      max_position: int | None) -> torch.Tensor:
+        """One decode step (a token per sequence): q/k norm, RoPE, the cache writes and the attention
+        in one launch; returns ``[B, Hq, D]``."""
+        bsz = q2.shape[0]
+        hq, hkv, d = self.num_heads, self.num_key_value_heads, self.head_dim
+        positions = cache_position.to(device=q2.device, dtype=torch.long).reshape(-1)
+        if positions.numel() != 1:
+            raise ValueError("cache_position length must match the sequence dimension of key/value states")
+        kc, vc, n = past_key_values.claim_positions(self.layer_idx, bsz, hkv, d, q2.dtype, q2.device, positions,
+                                                    max_position)
+        static = getattr(past_key_values, "static", None)
+        # captured decode step: keys span the reserved cache, each sequence's valid length is read
+        # from device memory
+        seqlens, sk = (static.seqlens, kc.shape[2]) if static is not None else (None, n)
+        q2, k2, v2 = (t.reshape(bsz, -1) for t in (q2, k2, v2))
+        if q2.stride(1) != 1 or k2.stride(1) != 1 or v2.stride(1) != 1:
+            q2, k2, v2 = q2.contiguous(), k2.contiguous(), v2.contiguous()
+        if cos.stride(-1) != 1 or sin.stride() != cos.stride():
+            cos, sin = cos.contiguous(), sin.contiguous()
+        out = torch.empty((bsz, hq, d), dtype=q2.dtype, device=q2.device)
+        wq, wk = self.q_norm.weight, self.k_norm.weight
+        _native.call("qh_flash_decode_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0),
+                     v2.data_ptr(), v2.stride(0), wq.data_ptr(), wk.data_ptr(), float(self.q_norm.eps),
+                     int(self.q_norm.one_plus_weight), cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0],
+                     cos.shape[-1], kc.data_ptr(), *kc.stride()[:3], vc.data_ptr(), *vc.stride()[:3], kc.shape[2],
+                     positions.data_ptr(), out.data_ptr(), None, None if seqlens is None else seqlens.data_ptr(),
+                     bsz, hq, hkv, sk, d, float(self.scaling), _native.dtype_code(q2.dtype),
+                     _native.dtype_code(wq.dtype), _native.dtype_code(cos.dtype), _native.stream(q2.device))
+        return out
+
     def attend_projected(self, q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor,
                          position_embeddings: tuple[torch.Tensor, torch.Tensor], attention_mask, past_key_values,
                          cache_position, max_position: int | None) -> torch.Tensor:
@@ -137,6 +186,9 @@ class QwenFullAttention(nn.Module):
         write in one pass, then attention; returns the o_proj input ``[B, S, Hq * D]``."""
         cos, sin = position_embeddings
         input_shape = q2.shape[:-1]
+        if self._decode_prepare_ok(q2, attention_mask, cos, sin):
+            out = self._fused_decode(q2, k2, v2, cos, sin, past_key_values, cache_position, max_position)
+            return out.view(*input_shape, -1)
         q, k, v = self._fused_prepare(q2, k2, v2, cos, sin, past_key_values, cache_position, max_position)
         static = getattr(past_key_values, "static", None)
         if static is not None and q.shape[2] == 1 and attention_mask is None:

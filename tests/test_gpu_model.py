@@ -307,3 +307,35 @@ def test_greedy_generate_graph_replay_matches_eager(moe):
     # decode attention entered from Python twice per layer (the eager second token and the
     # capture), not once per generated token
     assert launched == 2 * cfg.num_hidden_layers
+
+
+def test_fused_decode_prepare_in_model_bitwise(monkeypatch):
+    # 64 sequences x 8 kv-heads: decode steps take qh_flash_decode_prepare (norm, RoPE and cache
+    # writes inside the decode-attention kernel); the separate prepare pass must give identical
+    # logits and caches, eager and in a captured greedy decode
+    from qwen_triton.modules import attention as attn_mod
+
+    cfg = _cfg(hidden_size=256, num_attention_heads=16, num_key_value_heads=8, head_dim=128, num_hidden_layers=2,
+               vocab_size=512)
+    m = _model(cfg, seed=41)
+    ids = torch.randint(0, cfg.vocab_size, (64, 6), generator=torch.Generator().manual_seed(42)).cuda()
+    outs = {}
+    for fused in (True, False):
+        monkeypatch.setattr(attn_mod, "FUSE_DECODE_PREPARE", fused)
+        c0 = _native.CALLS["qh_flash_decode_prepare"]
+        with torch.no_grad():
+            p = m(input_ids=ids[:, :3], use_cache=True)
+            steps = [p.logits[:, -1]]
+            cache = p.past_key_values
+            for t in range(3, 6):
+                steps.append(m(input_ids=ids[:, t:t + 1], past_key_values=cache, use_cache=True).logits[:, -1])
+        assert _native.CALLS["qh_flash_decode_prepare"] - c0 == (3 * cfg.num_hidden_layers if fused else 0)
+        outs[fused] = (torch.stack(steps, 1), [c[:, :, :6].clone() for c in cache.key_cache])
+    assert torch.equal(outs[True][0], outs[False][0])
+    for a, b in zip(outs[True][1], outs[False][1]):
+        assert torch.equal(a, b)
+    monkeypatch.setattr(attn_mod, "FUSE_DECODE_PREPARE", True)
+    with torch.no_grad():
+        eager = m.greedy_generate(ids[:, :3], max_new_tokens=8)
+        graph = m.greedy_generate(ids[:, :3], max_new_tokens=8, use_graph=True)
+    assert torch.equal(graph, eager)

@@ -860,3 +860,86 @@ def test_moe_grouped_training_matches_loop_gradients(E, k, T):
         close(a, b, atol=2e-2 * scale, rtol=2e-2)
     # the expert without rows has exactly zero weight gradients
     assert all(int(torch.count_nonzero(t)) == 0 for t in gw[-3:])
+
+
+def _decode_step_inputs(B, Hq, Hkv, D, cap, seed):
+    q2 = randn(B, Hq * D, dtype=torch.bfloat16, seed=seed)
+    k2 = randn(B, Hkv * D, dtype=torch.bfloat16, seed=seed + 1, scale=2.0)
+    v2 = randn(B, Hkv * D, dtype=torch.bfloat16, seed=seed + 2)
+    kc = randn(B, Hkv, cap, D, dtype=torch.bfloat16, seed=seed + 3)
+    vc = randn(B, Hkv, cap, D, dtype=torch.bfloat16, seed=seed + 4)
+    qw = (1.0 + 0.2 * randn(D, seed=seed + 5)).to(torch.bfloat16)
+    kw = (1.0 + 0.2 * randn(D, seed=seed + 6)).to(torch.bfloat16)
+    return q2, k2, v2, kc, vc, qw, kw
+
+
+@pytest.mark.parametrize("Hq,Hkv,B", [(16, 8, 64), (32, 8, 64), (8, 8, 70)])
+@pytest.mark.parametrize("p", [0, 31, 32, 200, 383, 500, 639])
+@pytest.mark.parametrize("cdtype", [torch.float32, torch.bfloat16])
+def test_flash_decode_prepare_matches_prepare_then_decode(Hq, Hkv, B, p, cdtype):
+    # the decode step that prepares its own rows equals the prepare pass followed by the decode
+    # kernel bit for bit: output and the whole caches (new rows at p, nothing else touched).
+    # p < 384 puts the new row in its wave's first three key tiles (written, then drained, before
+    # that tile is read); larger p relies on the loop's own wait before the third tile
+    D, cap = 128, 640
+    assert _native.call("qh_flash_decode_prepare_ok", B, Hq, Hkv, D) == 1
+    q2, k2, v2, kc, vc, qw, kw = _decode_step_inputs(B, Hq, Hkv, D, cap, seed=300 + p)
+    theta = (p * torch.pow(1e6, -torch.arange(0, D, 2, dtype=torch.float64) / D)).float()
+    cos = torch.cat([theta.cos(), theta.cos()]).view(1, 1, D).to(cdtype).to(DEV)
+    sin = torch.cat([theta.sin(), theta.sin()]).view(1, 1, D).to(cdtype).to(DEV)
+    pos = torch.tensor([p], dtype=torch.long, device=DEV)
+    sk = p + 1
+    code = _native.dtype_code
+    st = _native.stream(torch.device(DEV))
+    # reference: prepare pass, then the decode kernel over keys [0, sk)
+    kc_r, vc_r = kc.clone(), vc.clone()
+    q_r = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device=DEV)
+    _native.call("qh_attn_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0), v2.data_ptr(),
+                 v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 0, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                 cos.stride(1), 1, D, q_r.data_ptr(), kc_r.data_ptr(), *kc_r.stride()[:3], vc_r.data_ptr(),
+                 *vc_r.stride()[:3], pos.data_ptr(), B, 1, Hq, Hkv, D, cap, code(torch.bfloat16), code(qw.dtype),
+                 code(cdtype), st)
+    o_r = FA.flash_decode(q_r, kc_r[:, :, :sk], vc_r[:, :, :sk], D ** -0.5, Hq // Hkv)
+    # fused
+    o = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=DEV)
+    c0 = native_calls("qh_flash_decode_prepare")
+    _native.call("qh_flash_decode_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0), v2.data_ptr(),
+                 v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 0, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                 1, D, kc.data_ptr(), *kc.stride()[:3], vc.data_ptr(), *vc.stride()[:3], cap, pos.data_ptr(),
+                 o.data_ptr(), None, None, B, Hq, Hkv, sk, D, D ** -0.5, code(torch.bfloat16), code(qw.dtype),
+                 code(cdtype), st)
+    assert native_calls("qh_flash_decode_prepare") == c0 + 1
+    assert torch.equal(kc, kc_r) and torch.equal(vc, vc_r)
+    assert torch.equal(o, o_r.view(B, Hq, D))
+    # and against the oracle: attention over the prepared rows
+    qo = q_r.view(B, Hq, 1, D)
+    close(o.view(B, Hq, 1, D), O.attention(qo, kc_r[:, :, :sk], vc_r[:, :, :sk], D ** -0.5, False, Hq // Hkv)[0],
+          **BF16_TOL)
+
+
+def test_flash_decode_prepare_static_cache_seqlens():
+    # captured-step form: keys span the whole cache, each sequence's valid length from seqlens
+    B, Hq, Hkv, D, cap, p = 64, 16, 8, 128, 160, 100
+    q2, k2, v2, kc, vc, qw, kw = _decode_step_inputs(B, Hq, Hkv, D, cap, seed=330)
+    cos = torch.rand(1, 1, D, device=DEV)
+    sin = torch.rand(1, 1, D, device=DEV)
+    pos = torch.tensor([p], dtype=torch.long, device=DEV)
+    seqlens = torch.randint(p + 1, cap + 1, (B,), generator=_gen(331), dtype=torch.int32).to(DEV)
+    code = _native.dtype_code
+    st = _native.stream(torch.device(DEV))
+    kc_r, vc_r = kc.clone(), vc.clone()
+    q_r = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device=DEV)
+    _native.call("qh_attn_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0), v2.data_ptr(),
+                 v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 1, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                 cos.stride(1), 1, D, q_r.data_ptr(), kc_r.data_ptr(), *kc_r.stride()[:3], vc_r.data_ptr(),
+                 *vc_r.stride()[:3], pos.data_ptr(), B, 1, Hq, Hkv, D, cap, code(torch.bfloat16), code(qw.dtype),
+                 code(torch.float32), st)
+    o_r = FA.flash_decode(q_r, kc_r, vc_r, D ** -0.5, Hq // Hkv, seqlens=seqlens)
+    o = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=DEV)
+    _native.call("qh_flash_decode_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0), v2.data_ptr(),
+                 v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 1, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                 1, D, kc.data_ptr(), *kc.stride()[:3], vc.data_ptr(), *vc.stride()[:3], cap, pos.data_ptr(),
+                 o.data_ptr(), None, seqlens.data_ptr(), B, Hq, Hkv, cap, D, D ** -0.5, code(torch.bfloat16),
+                 code(qw.dtype), code(torch.float32), st)
+    assert torch.equal(kc, kc_r) and torch.equal(vc, vc_r)
+    assert torch.equal(o, o_r.view(B, Hq, D))
