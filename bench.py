@@ -7,9 +7,10 @@ as a HIP graph and replayed ``--steps`` times. ``value`` is decode tokens/s
 (64 tokens per step). The same JSON line also carries:
 
 * config 0 on the GPU: bs1 prefill of 128 tokens and 32 greedy decode steps;
-* ``roofline`` of the dominant kernel (split-KV decode attention, HBM-bound):
-  algorithmic K/V bytes per launch / average launch time from HIP events on the
-  launch stream;
+* ``roofline`` of the dominant kernel (decode attention with its row preparation,
+  HBM-bound): algorithmic bytes per launch (K/V cache read, the step's q/k/v rows
+  read, the output and new cache rows written) / average launch time from HIP
+  events on the launch stream;
 * ``cpu_baseline``: the CPU oracle (fp32 torch, HF semantics) decoding a
   bounded sample of the same workload on the host cores.
 
@@ -35,11 +36,12 @@ METRIC = "Qwen3-0.6B prefill/decode tok/s on 1 MI355X + % of MFMA/HBM roofline"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
-# HBM bytes per launch of the decode attention (one fa_decode_wg_kernel dispatch at config 3),
-# from the two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`,
-# each scaled by the same counter's reading for a 1 GiB copy (fetch x 1048576 / 524300.3,
-# write x1.000): 262504 KiB x 1.99995 + 256 KiB = 537,857,724 bytes.
-DECODE_TRAFFIC_BYTES = 537_857_724
+# HBM bytes per launch of the decode attention as the config-3 step runs it (one
+# fa_decode_wg_kernel<bf16,128,2,PREP> dispatch), from the two rocprofv3 --pmc passes
+# (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`, each scaled by the same counter's
+# reading for a 1 GiB copy (fetch x 1048576 / 524310.06, write x 1.000):
+# 262679.5 KiB x 1.99991 + 512 KiB = 538,467,731 bytes.
+DECODE_TRAFFIC_BYTES = 538_467_731
 
 QWEN3_06B = dict(model_type="qwen3", vocab_size=151936, hidden_size=1024, intermediate_size=3072,
                  num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8, head_dim=128,
@@ -146,36 +148,78 @@ def bench_decode(model, steps, warmup, use_graph=True, batch=64, ctx=2048):
     return cache, eager_ms, graph_ms
 
 
-def attention_roofline(model, cache, reps=50, batch=64, ctx=2048):
-    """Dominant kernel of the decode step: split-KV decode attention over 2049 keys."""
+def decode_layer_launch(batch=64, hq=16, hkv=8, d=128, ctx=2048, seed=0):
+    """One layer's decode attention as the config-3 step runs it (qh_flash_decode_prepare: the q/k
+    norm, RoPE and cache writes of the step inside the decode kernel) on synthetic inputs of that
+    shape: a 2048-token bf16 cache (capacity 2112), the new token at position 2048. Returns
+    (launch, algorithmic bytes per launch)."""
     import torch
-    from qwen_triton.kernels import flash_attention as FA
+    from qwen_triton import _native
 
-    cfg = model.config
-    sk = ctx + 1
-    k = cache.key_cache[0][:, :, :sk]
-    v = cache.value_cache[0][:, :, :sk]
-    q = torch.randn(batch, cfg.num_attention_heads, 1, cfg.head_dim, device="cuda", dtype=torch.bfloat16)
-    groups = cfg.num_attention_heads // cfg.num_key_value_heads
-    scale = cfg.head_dim ** -0.5
-    with torch.no_grad():
-        for _ in range(5):
-            FA.flash_decode(q, k, v, scale, groups)
-        stream = torch.cuda.current_stream()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for a, b in ev:
-            a.record(stream)
-            FA.flash_decode(q, k, v, scale, groups)
-            b.record(stream)
-        sync()
-    avg_ms = sum(a.elapsed_time(b) for a, b in ev) / reps
-    kv_bytes = 2 * batch * cfg.num_key_value_heads * sk * cfg.head_dim * 2
-    io_bytes = 2 * batch * cfg.num_attention_heads * cfg.head_dim * 2
-    algo = kv_bytes + io_bytes
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    bf = torch.bfloat16
+    cap, sk = ctx + 64, ctx + 1
+    kc = torch.randn(batch, hkv, cap, d, device="cuda", dtype=bf, generator=g)
+    vc = torch.randn(batch, hkv, cap, d, device="cuda", dtype=bf, generator=g)
+    q2 = torch.randn(batch, hq * d, device="cuda", dtype=bf, generator=g)
+    k2 = torch.randn(batch, hkv * d, device="cuda", dtype=bf, generator=g)
+    v2 = torch.randn(batch, hkv * d, device="cuda", dtype=bf, generator=g)
+    qw = torch.ones(d, device="cuda", dtype=bf)
+    kw = torch.ones(d, device="cuda", dtype=bf)
+    inv = 1e6 ** (-torch.arange(0, d, 2, dtype=torch.float64, device="cuda") / d)
+    ang = torch.cat([ctx * inv, ctx * inv]).float().view(1, 1, d)
+    cos, sin = ang.cos().to(bf), ang.sin().to(bf)  # the model passes cos/sin in the activation dtype
+    pos = torch.tensor([ctx], dtype=torch.long, device="cuda")
+    out = torch.empty(batch, hq, d, device="cuda", dtype=bf)
+    code = _native.dtype_code
+    if not _native.call("qh_flash_decode_prepare_ok", batch, hq, hkv, d):
+        raise RuntimeError("the config-3 decode shape is not served by qh_flash_decode_prepare")
+
+    def launch():
+        _native.call("qh_flash_decode_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0),
+                     v2.data_ptr(), v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 0, cos.data_ptr(),
+                     sin.data_ptr(), cos.stride(0), 1, d, kc.data_ptr(), *kc.stride()[:3], vc.data_ptr(),
+                     *vc.stride()[:3], cap, pos.data_ptr(), out.data_ptr(), None, None, batch, hq, hkv, sk, d,
+                     d ** -0.5, code(bf), code(bf), code(bf), _native.stream(torch.device("cuda")))
+
+    kv_bytes = 2 * batch * hkv * sk * d * 2
+    rows_bytes = (batch * hq * d + 2 * batch * hkv * d) * 2  # projected q, k, v rows read
+    write_bytes = (batch * hq * d + 2 * batch * hkv * d) * 2  # o, new cache rows written
+    return launch, kv_bytes + rows_bytes + write_bytes
+
+
+def attention_roofline(per_graph=20, replays=5):
+    """Dominant kernel of the decode step: decode attention with its row preparation over 2049 keys.
+    Its launches are captured back to back in a HIP graph (as the step replays them) and timed with
+    HIP events around the replays on the stream they run on: average launch = elapsed / launches."""
+    import torch
+
+    launch, algo = decode_layer_launch()
+    for _ in range(5):
+        launch()
+    sync()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(per_graph):
+                launch()
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()
+    sync()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    b.record(stream)
+    sync()
+    avg_ms = a.elapsed_time(b) / (per_graph * replays)
     achieved = algo / (avg_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC_BYTES,
-            "kernel": "fa_decode_wg_kernel", "avg_launch_us": round(avg_ms * 1e3, 2),
+            "kernel": "fa_decode_wg_kernel<bf16,128,2,PREP>", "avg_launch_us": round(avg_ms * 1e3, 2),
             "algorithmic_bytes_per_launch": algo}
 
 
@@ -654,21 +698,15 @@ def bench_ops(reps=20):
 
 
 def bench_roofline_kernels(reps=20):
-    """Only the dominant decode kernel (one layer's cache) plus a 1 GiB copy for counter calibration."""
+    """Only the dominant decode kernel (one layer of the step) plus a 1 GiB copy for counter calibration."""
     import torch
-    from qwen_triton.kernels import flash_attention as FA
 
-    B, Hq, Hkv, D, sk = 64, 16, 8, 128, 2049
-    g = torch.Generator(device="cuda").manual_seed(0)
-    kc = torch.randn(B, Hkv, sk + 63, D, device="cuda", dtype=torch.bfloat16, generator=g)
-    vc = torch.randn(B, Hkv, sk + 63, D, device="cuda", dtype=torch.bfloat16, generator=g)
-    q = torch.randn(B, Hq, 1, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    launch, algo = decode_layer_launch()
     src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     times = {"decode": [], "copy": []}
     for i in range(reps):
-        for name, fn in (("decode", lambda: FA.flash_decode(q, kc[:, :, :sk], vc[:, :, :sk], D ** -0.5, Hq // Hkv)),
-                         ("copy", lambda: dst.copy_(src))):
+        for name, fn in (("decode", launch), ("copy", lambda: dst.copy_(src))):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             fn()
@@ -676,10 +714,9 @@ def bench_roofline_kernels(reps=20):
             times[name].append((a, b))
     sync()
     res = {k: sum(a.elapsed_time(b) for a, b in v[2:]) / (len(v) - 2) * 1e3 for k, v in times.items()}
-    kv = 2 * B * Hkv * sk * D * 2
-    return {"decode_us": round(res["decode"], 2), "decode_gbs": round(kv / res["decode"] / 1e3, 1),
+    return {"decode_us": round(res["decode"], 2), "decode_gbs": round(algo / res["decode"] / 1e3, 1),
             "copy_us": round(res["copy"], 2), "copy_gbs": round(2 * (1 << 30) / res["copy"] / 1e3, 1),
-            "decode_algorithmic_bytes": kv, "copy_bytes_each_way": 1 << 30}
+            "decode_algorithmic_bytes": algo, "copy_bytes_each_way": 1 << 30}
 
 
 def main() -> None:
@@ -734,10 +771,10 @@ def main() -> None:
     log("building Qwen3-0.6B (random N(0,0.02) weights, bf16)")
     model = build_model(torch.bfloat16, "cuda")
     cache, eager_ms, graph_ms = bench_decode(model, args.steps, args.warmup, use_graph=not args.no_graph)
-    roof = attention_roofline(model, cache)
-    log(f"decode attention: {roof['avg_launch_us']} us/launch, {roof['achieved']} GB/s")
     del cache
     torch.cuda.empty_cache()
+    roof = attention_roofline()
+    log(f"decode attention: {roof['avg_launch_us']} us/launch, {roof['achieved']} GB/s")
     cfg0 = bench_cfg0(model)
     log(f"config 0: {cfg0}")
     cpu = None if args.no_cpu_baseline else cpu_baseline(model)

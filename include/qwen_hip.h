@@ -369,7 +369,9 @@ int64_t qh_flash_decode_prepare_ok(int64_t B, int64_t Hq, int64_t Hkv, int64_t D
  * (same arithmetic, bitwise equal) fused into the decode kernel, so the
  * prepared q never leaves the chip. q, k, v are the step's projected rows
  * ([B, H*D], row strides sq, sk, sv), cos/sin [cos_batch, 1, rot] (batch stride
- * scb), positions[0] the step's cache position (rows outside [0, cap) are not
+ * scb; the activation dtype, so every product is exact in fp32 and the result
+ * is independent of multiply-add contraction), positions[0] the step's cache
+ * position (rows outside [0, cap) are not
  * written), k_cache/v_cache [B, Hkv, cap, D] with the given strides. The
  * attention reads keys [0, min(seqlens[b], Sk)) (seqlens may be NULL: Sk) and
  * writes o [B, Hq, D] and, if lse is not NULL, the log-sum-exp as qh_flash_decode.

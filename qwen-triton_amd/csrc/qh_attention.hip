@@ -1186,6 +1186,9 @@ __global__ __launch_bounds__(256) void fa_decode_combine(const float* __restrict
 // fa_decode_combine's arithmetic: no workspace and no second launch, and the
 // same results as the split kernel plus combine at 4 splits.
 //
+// K and V are not __restrict__: with PREP the kernel writes the new cache rows
+// and later reads them through the same pointers.
+//
 // PREP (one new token per sequence): the kernel also prepares its own rows,
 // replacing the separate prepare pass. Each wavefront loads its rows, issues
 // its first two K/V tiles, then normalises and rotates the group's G query
@@ -1216,8 +1219,8 @@ struct DecodePrepArgs {
 
 template <typename T, int DP, int G, bool PREP = false, typename C = float>
 __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
-                                                          const T* __restrict__ K, int64_t skb, int64_t skh,
-                                                          int64_t sks, const T* __restrict__ V, int64_t svb,
+                                                          const T* K, int64_t skb, int64_t skh,
+                                                          int64_t sks, const T* V, int64_t svb,
                                                           int64_t svh, int64_t svs, T* __restrict__ O,
                                                           float* __restrict__ LSE, const int* __restrict__ seqlens,
                                                           int Hkv, int Sk, int D, float scale_log2,
@@ -1270,7 +1273,7 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
   auto issue = [&](int t, v8 (&kf)[2][KD]) {
     const int row0 = (w + t * NW) * BN;
     const uint32_t vl = lds_addr(Vs[w][t % NS]);
-    if (PREP && w + t * NW == tile_p && t <= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    if (PREP && w + t * NW == tile_p && t <= 2) __threadfence_block();  // the new rows are stored
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       int key = row0 + 16 * h + li;
@@ -1310,27 +1313,31 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
     const int gi = lane >> 4, g = lane & 15, d0 = 8 * g;
     const bool act = d0 < D, pok = w == wp && p >= 0 && p < pa.cap;
     const int dl = act ? d0 : D - 8;
+    // Rows and their parameters (norm scales, cos/sin) are requested before the
+    // tiles, so waiting for them never waits for a tile.
+    const int64_t co_row = (pa.cos_batch == 1 ? 0 : b) * pa.scb;
     Vec16<T> xv[NPASS];
+    RowParams rp[NPASS];
 #pragma unroll
     for (int ps = 0; ps < NPASS; ++ps) {
       const int r = gi + 4 * ps;
       const T* src = r < G ? pa.q + b * pa.sq + (int64_t)(hk * G + r) * D
                            : (r == G ? pa.k + b * pa.sk : pa.v + b * pa.sv) + (int64_t)hk * D;
       xv[ps] = ld16((r < G + 2 ? src : pa.q + b * pa.sq) + dl);
+      rp[ps] = load_row_params<C>(r < G ? pa.qw : pa.kw, pa.wdtype, pa.wadd, d0, act, pa.half, pa.rot, pa.cs, pa.sn,
+                                  co_row);
     }
     if (!slow && ntiles > 0) {
       issue(0, ka);
       if (ntiles > 1) issue(1, kb), pre1 = true;
     }
-    const int64_t co_row = (pa.cos_batch == 1 ? 0 : b) * pa.scb;
 #pragma unroll
     for (int ps = 0; ps < NPASS; ++ps) {
       const int r = gi + 4 * ps;
       const bool isq = r < G, isk = r == G && pok, isv = r == G + 1 && pok;
       Vec16<T> x = xv[ps];
       if (!act) x.raw = make_uint4(0, 0, 0, 0);
-      const Vec16<T> y = norm_rope_row<T, C>(x, act, isq ? pa.qw : pa.kw, pa.wdtype, pa.eps, pa.wadd, D, d0,
-                                             pa.half / 8, pa.half, pa.rot, pa.cs, pa.sn, co_row);
+      const Vec16<T> y = norm_rope_apply<T>(x, act, rp[ps], pa.eps, D, d0, pa.half / 8, pa.half, pa.rot);
       if (act) {
         if (isq) *reinterpret_cast<uint4*>(&qs[w][r][d0]) = y.raw;
         else if (isk) st16(const_cast<T*>(Kb) + p * sks + d0, y);
@@ -1751,7 +1758,10 @@ extern "C" int qh_flash_decode_prepare(const void* q, int64_t sq, const void* k,
   QH_CHECK_ARG(kcs < (1 << 24) && vcs < (1 << 24), "qh_flash_decode_prepare: key/value row stride too large");
   QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_flash_decode_prepare: bf16/f16 only");
   QH_CHECK_ARG(wdtype == QH_F32 || wdtype == dtype, "qh_flash_decode_prepare: norm weights must be fp32 or the dtype");
-  QH_CHECK_ARG(cdtype == QH_F32 || cdtype == dtype, "qh_flash_decode_prepare: cos/sin must be fp32 or the dtype");
+  // cos/sin in the activation dtype: every product of the norm and the rotation is then a product of
+  // two 16-bit values, exact in fp32, so the result cannot depend on how the compiler contracts
+  // multiply-adds and equals qh_attn_prepare's bit for bit.
+  QH_CHECK_ARG(cdtype == dtype, "qh_flash_decode_prepare: cos/sin must have the activation dtype");
   hipStream_t st = (hipStream_t)stream;
   const float sl2 = scale * kLog2e;
   const int groups = (int)(Hq / Hkv);
@@ -1767,9 +1777,9 @@ extern "C" int qh_flash_decode_prepare(const void* q, int64_t sq, const void* k,
 #define QH_WGP_G(T, C) \
   if (groups == 1) QH_WGP(T, C, 1) else if (groups == 2) QH_WGP(T, C, 2) else if (groups == 4) QH_WGP(T, C, 4) else QH_WGP(T, C, 8)
   if (dtype == QH_BF16) {
-    if (cdtype == QH_F32) { QH_WGP_G(bf16_t, float) } else { QH_WGP_G(bf16_t, bf16_t) }
+    QH_WGP_G(bf16_t, bf16_t)
   } else {
-    if (cdtype == QH_F32) { QH_WGP_G(f16_t, float) } else { QH_WGP_G(f16_t, f16_t) }
+    QH_WGP_G(f16_t, f16_t)
   }
 #undef QH_WGP_G
 #undef QH_WGP

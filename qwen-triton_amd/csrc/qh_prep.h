@@ -4,17 +4,39 @@
 #pragma once
 #include "qh_common.h"
 
+// Per-lane parameters of a row: norm scale (w + wadd) and cos/sin of the lane's
+// 8 columns (d0 .. d0 + 7; cos/sin only below rot, at (d mod half)).
+struct RowParams {
+  float w[8], c[8], s[8];
+};
+
+template <typename C>
+__device__ __forceinline__ RowParams load_row_params(const void* w, int wdtype, float wadd, int d0, bool act,
+                                                     int half, int rot, const C* __restrict__ cs,
+                                                     const C* __restrict__ sn, int64_t co_row) {
+  RowParams rp;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) rp.w[e] = act ? load_any(w, wdtype, d0 + e) + wadd : 0.f;
+  if (d0 < rot) {
+    const int64_t co = co_row + (d0 < half ? d0 : d0 - half);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rp.c[e] = to_f32(cs[co + e]), rp.s[e] = to_f32(sn[co + e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rp.c[e] = 0.f, rp.s[e] = 0.f;
+  }
+  return rp;
+}
+
 // A row of D <= 128 elements on a 16-lane group, 8 per lane (lane g holds
 // d0 = 8 g .. d0 + 7; act = d0 < D): RMSNorm over D (fp32 sums, the 16-lane
 // DPP reduction of the norm kernel, rounded to T), then rotate-half RoPE of the
-// first rot elements with cos/sin[co_row + (d mod half)] (rounded to T); the
-// rest passes through. hl = half / 8 is the lane distance between the halves.
-// All 16 lanes of the group must call it together.
-template <typename T, typename C>
-__device__ __forceinline__ Vec16<T> norm_rope_row(const Vec16<T>& xv, bool act, const void* w, int wdtype, float eps,
-                                                  float wadd, int D, int d0, int hl, int half, int rot,
-                                                  const C* __restrict__ cs, const C* __restrict__ sn,
-                                                  int64_t co_row) {
+// first rot elements with the lane's cos/sin (rounded to T); the rest passes
+// through. hl = half / 8 is the lane distance between the halves. All 16 lanes
+// of the group must call it together.
+template <typename T>
+__device__ __forceinline__ Vec16<T> norm_rope_apply(const Vec16<T>& xv, bool act, const RowParams& rp, float eps,
+                                                    int D, int d0, int hl, int half, int rot) {
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -25,19 +47,16 @@ __device__ __forceinline__ Vec16<T> norm_rope_row(const Vec16<T>& xv, bool act, 
   const float inv = rsqrtf(ss / (float)D + eps);
   float y[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
-    y[e] = act ? to_f32(from_f32<T>((to_f32(xv.v[e]) * inv) * (load_any(w, wdtype, d0 + e) + wadd))) : 0.f;
+  for (int e = 0; e < 8; ++e) y[e] = act ? to_f32(from_f32<T>((to_f32(xv.v[e]) * inv) * rp.w[e])) : 0.f;
   float px[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) px[e] = __shfl_xor(y[e], hl, 16);
   Vec16<T> o;
   if (d0 < rot) {
     const bool lo = d0 < half;
-    const int ci = lo ? d0 : d0 - half;
-    const int64_t co = co_row + ci;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float cc = to_f32(cs[co + e]), sv2 = to_f32(sn[co + e]);
+      const float cc = rp.c[e], sv2 = rp.s[e];
       const float a = lo ? y[e] : px[e], bb = lo ? px[e] : y[e];
       o.v[e] = lo ? from_f32<T>(a * cc - bb * sv2) : from_f32<T>(bb * cc + a * sv2);
     }
@@ -46,4 +65,14 @@ __device__ __forceinline__ Vec16<T> norm_rope_row(const Vec16<T>& xv, bool act, 
     for (int e = 0; e < 8; ++e) o.v[e] = from_f32<T>(y[e]);
   }
   return o;
+}
+
+// load_row_params + norm_rope_apply.
+template <typename T, typename C>
+__device__ __forceinline__ Vec16<T> norm_rope_row(const Vec16<T>& xv, bool act, const void* w, int wdtype, float eps,
+                                                  float wadd, int D, int d0, int hl, int half, int rot,
+                                                  const C* __restrict__ cs, const C* __restrict__ sn,
+                                                  int64_t co_row) {
+  const RowParams rp = load_row_params<C>(w, wdtype, wadd, d0, act, half, rot, cs, sn, co_row);
+  return norm_rope_apply<T>(xv, act, rp, eps, D, d0, hl, half, rot);
 }

@@ -137,8 +137,10 @@ class QwenFullAttention(nn.Module):
         return q_out, kc[:, :, :n, :], vc[:, :, :n, :]
 
     def _decode_prepare_ok(self, q2: torch.Tensor, attention_mask, cos: torch.Tensor, sin: torch.Tensor) -> bool:
-        if not (FUSE_DECODE_PREPARE and attention_mask is None and q2.shape[1] == 1
-                and cos.shape[1] == 1 and sin.shape == cos.shape):
+        # cos/sin in the activation dtype: the fused kernel's products are then all exact in fp32
+        # and its rows equal the prepare pass's bit for bit
+        if not (FUSE_DECODE_PREPARE and attention_mask is None and q2.shape[1] == 1 and cos.shape[1] == 1
+                and sin.shape == cos.shape and cos.dtype == q2.dtype and sin.dtype == q2.dtype):
             return False
         cache = self.__dict__.setdefault("_decode_prepare_cache", {})
         bsz = q2.shape[0]

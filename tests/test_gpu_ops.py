@@ -874,8 +874,8 @@ def _decode_step_inputs(B, Hq, Hkv, D, cap, seed):
 
 
 @pytest.mark.parametrize("Hq,Hkv,B", [(16, 8, 64), (32, 8, 64), (8, 8, 70)])
-@pytest.mark.parametrize("p", [0, 31, 32, 200, 383, 500, 639])
-@pytest.mark.parametrize("cdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("p", [0, 1, 15, 16, 31, 32, 200, 383, 500, 639])
+@pytest.mark.parametrize("cdtype", [torch.bfloat16])
 def test_flash_decode_prepare_matches_prepare_then_decode(Hq, Hkv, B, p, cdtype):
     # the decode step that prepares its own rows equals the prepare pass followed by the decode
     # kernel bit for bit: output and the whole caches (new rows at p, nothing else touched).
@@ -917,12 +917,29 @@ def test_flash_decode_prepare_matches_prepare_then_decode(Hq, Hkv, B, p, cdtype)
           **BF16_TOL)
 
 
+def test_flash_decode_prepare_rejects_fp32_cos():
+    # fp32 cos/sin would make the rotation's products inexact, and the fused rows could then differ
+    # from the prepare pass's by the compiler's multiply-add contraction: the entry point refuses
+    B, Hq, Hkv, D, cap = 64, 16, 8, 128, 64
+    q2, k2, v2, kc, vc, qw, kw = _decode_step_inputs(B, Hq, Hkv, D, cap, seed=340)
+    cos = torch.rand(1, 1, D, device=DEV)
+    pos = torch.tensor([3], dtype=torch.long, device=DEV)
+    o = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=DEV)
+    code = _native.dtype_code
+    with pytest.raises(_native.NativeError, match="activation dtype"):
+        _native.call("qh_flash_decode_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0),
+                     v2.data_ptr(), v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 0, cos.data_ptr(),
+                     cos.data_ptr(), cos.stride(0), 1, D, kc.data_ptr(), *kc.stride()[:3], vc.data_ptr(),
+                     *vc.stride()[:3], cap, pos.data_ptr(), o.data_ptr(), None, None, B, Hq, Hkv, 4, D, D ** -0.5,
+                     code(torch.bfloat16), code(qw.dtype), code(torch.float32), _native.stream(torch.device(DEV)))
+
+
 def test_flash_decode_prepare_static_cache_seqlens():
     # captured-step form: keys span the whole cache, each sequence's valid length from seqlens
     B, Hq, Hkv, D, cap, p = 64, 16, 8, 128, 160, 100
     q2, k2, v2, kc, vc, qw, kw = _decode_step_inputs(B, Hq, Hkv, D, cap, seed=330)
-    cos = torch.rand(1, 1, D, device=DEV)
-    sin = torch.rand(1, 1, D, device=DEV)
+    cos = torch.rand(1, 1, D, device=DEV).to(torch.bfloat16)
+    sin = torch.rand(1, 1, D, device=DEV).to(torch.bfloat16)
     pos = torch.tensor([p], dtype=torch.long, device=DEV)
     seqlens = torch.randint(p + 1, cap + 1, (B,), generator=_gen(331), dtype=torch.int32).to(DEV)
     code = _native.dtype_code
@@ -933,13 +950,13 @@ def test_flash_decode_prepare_static_cache_seqlens():
                  v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 1, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
                  cos.stride(1), 1, D, q_r.data_ptr(), kc_r.data_ptr(), *kc_r.stride()[:3], vc_r.data_ptr(),
                  *vc_r.stride()[:3], pos.data_ptr(), B, 1, Hq, Hkv, D, cap, code(torch.bfloat16), code(qw.dtype),
-                 code(torch.float32), st)
+                 code(torch.bfloat16), st)
     o_r = FA.flash_decode(q_r, kc_r, vc_r, D ** -0.5, Hq // Hkv, seqlens=seqlens)
     o = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=DEV)
     _native.call("qh_flash_decode_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0), v2.data_ptr(),
                  v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 1, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
                  1, D, kc.data_ptr(), *kc.stride()[:3], vc.data_ptr(), *vc.stride()[:3], cap, pos.data_ptr(),
                  o.data_ptr(), None, seqlens.data_ptr(), B, Hq, Hkv, cap, D, D ** -0.5, code(torch.bfloat16),
-                 code(qw.dtype), code(torch.float32), st)
+                 code(qw.dtype), code(torch.bfloat16), st)
     assert torch.equal(kc, kc_r) and torch.equal(vc, vc_r)
     assert torch.equal(o, o_r.view(B, Hq, D))
