@@ -768,13 +768,16 @@ def main() -> None:
         print(json.dumps({"metric": "dense proj + LM head + CE fwd/bwd (config 2)", **res}), flush=True)
         return
 
+    # the dominant kernel first, on fresh allocations (after the 15 GB decode cache has been
+    # allocated and freed the same launches time 3-4 us slower)
+    roof = attention_roofline()
+    log(f"decode attention: {roof['avg_launch_us']} us/launch, {roof['achieved']} GB/s")
+    torch.cuda.empty_cache()
     log("building Qwen3-0.6B (random N(0,0.02) weights, bf16)")
     model = build_model(torch.bfloat16, "cuda")
     cache, eager_ms, graph_ms = bench_decode(model, args.steps, args.warmup, use_graph=not args.no_graph)
     del cache
     torch.cuda.empty_cache()
-    roof = attention_roofline()
-    log(f"decode attention: {roof['avg_launch_us']} us/launch, {roof['achieved']} GB/s")
     cfg0 = bench_cfg0(model)
     log(f"config 0: {cfg0}")
     cpu = None if args.no_cpu_baseline else cpu_baseline(model)

@@ -1186,8 +1186,8 @@ __global__ __launch_bounds__(256) void fa_decode_combine(const float* __restrict
 // fa_decode_combine's arithmetic: no workspace and no second launch, and the
 // same results as the split kernel plus combine at 4 splits.
 //
-// K and V are not __restrict__: with PREP the kernel writes the new cache rows
-// and later reads them through the same pointers.
+// K and V are __restrict__ except with PREP, where the kernel writes the new
+// cache rows and later reads them through the same pointers.
 //
 // PREP (one new token per sequence): the kernel also prepares its own rows,
 // replacing the separate prepare pass. Each wavefront loads its rows, issues
@@ -1199,6 +1199,9 @@ __global__ __launch_bounds__(256) void fa_decode_combine(const float* __restrict
 // caches at p. Vector-memory counts retire in issue order, so the loop's wait
 // before tile 2 is requested also covers those stores; only when p lies in the
 // wave's first three tiles does it write first and drain before that tile.
+template <typename T, bool PREP>
+using kv_ptr = typename std::conditional<PREP, const T*, const T* __restrict__>::type;
+
 template <typename T, typename C>
 struct DecodePrepArgs {
   const T* q;  // projected rows of the step: q [B, Hq * D], k and v [B, Hkv * D] (row strides sq, sk, sv)
@@ -1219,8 +1222,8 @@ struct DecodePrepArgs {
 
 template <typename T, int DP, int G, bool PREP = false, typename C = float>
 __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
-                                                          const T* K, int64_t skb, int64_t skh,
-                                                          int64_t sks, const T* V, int64_t svb,
+                                                          kv_ptr<T, PREP> K, int64_t skb, int64_t skh,
+                                                          int64_t sks, kv_ptr<T, PREP> V, int64_t svb,
                                                           int64_t svh, int64_t svs, T* __restrict__ O,
                                                           float* __restrict__ LSE, const int* __restrict__ seqlens,
                                                           int Hkv, int Sk, int D, float scale_log2,
@@ -1324,8 +1327,8 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
       const T* src = r < G ? pa.q + b * pa.sq + (int64_t)(hk * G + r) * D
                            : (r == G ? pa.k + b * pa.sk : pa.v + b * pa.sv) + (int64_t)hk * D;
       xv[ps] = ld16((r < G + 2 ? src : pa.q + b * pa.sq) + dl);
-      rp[ps] = load_row_params<C>(r < G ? pa.qw : pa.kw, pa.wdtype, pa.wadd, d0, act, pa.half, pa.rot, pa.cs, pa.sn,
-                                  co_row);
+      rp[ps] = load_row_params<C, true>(r < G ? pa.qw : pa.kw, pa.wdtype, pa.wadd, d0, act, pa.half, pa.rot, pa.cs,
+                                        pa.sn, co_row);
     }
     if (!slow && ntiles > 0) {
       issue(0, ka);
@@ -1762,6 +1765,8 @@ extern "C" int qh_flash_decode_prepare(const void* q, int64_t sq, const void* k,
   // two 16-bit values, exact in fp32, so the result cannot depend on how the compiler contracts
   // multiply-adds and equals qh_attn_prepare's bit for bit.
   QH_CHECK_ARG(cdtype == dtype, "qh_flash_decode_prepare: cos/sin must have the activation dtype");
+  QH_CHECK_ARG(aligned16(qw) && aligned16(kw) && aligned16(cos) && aligned16(sin) && scb % 8 == 0,
+               "qh_flash_decode_prepare: norm weights and cos/sin must be 16-byte aligned (batch stride multiple of 8)");
   hipStream_t st = (hipStream_t)stream;
   const float sl2 = scale * kLog2e;
   const int groups = (int)(Hq / Hkv);

@@ -10,17 +10,41 @@ struct RowParams {
   float w[8], c[8], s[8];
 };
 
-template <typename C>
+// VEC: 16-byte loads (w, cs and sn 16-byte aligned; C a 16-bit type; wdtype
+// fp32 or C's dtype); the values are the same as the element loads'.
+template <typename C, bool VEC = false>
 __device__ __forceinline__ RowParams load_row_params(const void* w, int wdtype, float wadd, int d0, bool act,
                                                      int half, int rot, const C* __restrict__ cs,
                                                      const C* __restrict__ sn, int64_t co_row) {
   RowParams rp;
+  if constexpr (VEC) {
+    static_assert(sizeof(C) == 2, "vector row parameters need a 16-bit cos/sin type");
+    const int dw = act ? d0 : 0;
+    if (wdtype == QH_F32) {
+      const float4 a = *reinterpret_cast<const float4*>((const float*)w + dw);
+      const float4 b = *reinterpret_cast<const float4*>((const float*)w + dw + 4);
+      const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) rp.w[e] = act ? load_any(w, wdtype, d0 + e) + wadd : 0.f;
+      for (int e = 0; e < 8; ++e) rp.w[e] = act ? f[e] + wadd : 0.f;
+    } else {
+      const Vec16<C> v = ld16((const C*)w + dw);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rp.w[e] = act ? to_f32(v.v[e]) + wadd : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rp.w[e] = act ? load_any(w, wdtype, d0 + e) + wadd : 0.f;
+  }
   if (d0 < rot) {
     const int64_t co = co_row + (d0 < half ? d0 : d0 - half);
+    if constexpr (VEC) {
+      const Vec16<C> c = ld16(cs + co), sv = ld16(sn + co);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) rp.c[e] = to_f32(cs[co + e]), rp.s[e] = to_f32(sn[co + e]);
+      for (int e = 0; e < 8; ++e) rp.c[e] = to_f32(c.v[e]), rp.s[e] = to_f32(sv.v[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rp.c[e] = to_f32(cs[co + e]), rp.s[e] = to_f32(sn[co + e]);
+    }
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) rp.c[e] = 0.f, rp.s[e] = 0.f;

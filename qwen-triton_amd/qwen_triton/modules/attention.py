@@ -140,7 +140,12 @@ class QwenFullAttention(nn.Module):
         # cos/sin in the activation dtype: the fused kernel's products are then all exact in fp32
         # and its rows equal the prepare pass's bit for bit
         if not (FUSE_DECODE_PREPARE and attention_mask is None and q2.shape[1] == 1 and cos.shape[1] == 1
-                and sin.shape == cos.shape and cos.dtype == q2.dtype and sin.dtype == q2.dtype):
+                and sin.shape == cos.shape and cos.dtype == q2.dtype and sin.dtype == q2.dtype
+                and cos.data_ptr() % 16 == 0 and sin.data_ptr() % 16 == 0 and cos.stride(0) % 8 == 0
+                and cos.stride(-1) == 1 and sin.stride() == cos.stride()
+                and self.q_norm.weight.data_ptr() % 16 == 0 and self.k_norm.weight.data_ptr() % 16 == 0
+                and self.k_norm.weight.dtype == self.q_norm.weight.dtype
+                and self.q_norm.weight.dtype in (torch.float32, q2.dtype)):
             return False
         cache = self.__dict__.setdefault("_decode_prepare_cache", {})
         bsz = q2.shape[0]
