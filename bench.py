@@ -172,7 +172,7 @@ def decode_layer_launch(batch=64, hq=16, hkv=8, d=128, ctx=2048, seed=0):
     pos = torch.tensor([ctx], dtype=torch.long, device="cuda")
     out = torch.empty(batch, hq, d, device="cuda", dtype=bf)
     code = _native.dtype_code
-    if not _native.call("qh_flash_decode_prepare_ok", batch, hq, hkv, d):
+    if not _native.call("qh_flash_decode_prepare_ok", batch, hq, hkv, ctx + 1, d):
         raise RuntimeError("the config-3 decode shape is not served by qh_flash_decode_prepare")
 
     def launch():

@@ -361,9 +361,10 @@ int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int6
                     const int32_t* seqlens, void* ws, int64_t ws_bytes, int64_t B, int64_t Hq, int64_t Hkv,
                     int64_t Sk, int64_t D, float scale, int dtype, void* stream);
 /* 1 when qh_flash_decode_prepare serves these shapes (D == 128, Hq / Hkv in
- * {1, 2, 4, 8}, at least 512 (sequence, kv-head) pairs), else 0. No counterpart
- * in the reference: a capability query for the fused decode step below. */
-int64_t qh_flash_decode_prepare_ok(int64_t B, int64_t Hq, int64_t Hkv, int64_t D);
+ * {1, 2, 4, 8}, and at least 512 (sequence, kv-head) pairs or at most 512 keys
+ * Sk), else 0. No counterpart in the reference: a capability query for the
+ * fused decode step below. */
+int64_t qh_flash_decode_prepare_ok(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk, int64_t D);
 /* One decode step of attention (one new token per sequence) with its input
  * preparation: q_norm/k_norm, RoPE and the K/V cache writes of qh_attn_prepare
  * (same arithmetic, bitwise equal) fused into the decode kernel, so the

@@ -1731,10 +1731,17 @@ extern "C" int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const vo
   return QH_OK;
 }
 
-extern "C" int64_t qh_flash_decode_prepare_ok(int64_t B, int64_t Hq, int64_t Hkv, int64_t D) {
-  if (B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D != 128) return 0;
+// Keys a few workgroups stream fast enough on their own: short caches take the
+// one-workgroup-per-(sequence, kv-head) kernel whatever the batch.
+constexpr int64_t kDecodeWgShortKeys = 512;
+
+extern "C" int64_t qh_flash_decode_prepare_ok(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk, int64_t D) {
+  if (B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D != 128 || Sk < 0) return 0;
   const int64_t g = Hq / Hkv;
-  return (g == 1 || g == 2 || g == 4 || g == 8) && B * Hkv >= kDecodeWgMinSeqs && B * Hkv < 65536 ? 1 : 0;
+  return (g == 1 || g == 2 || g == 4 || g == 8) && (B * Hkv >= kDecodeWgMinSeqs || Sk <= kDecodeWgShortKeys) &&
+                 B * Hkv < 65536
+             ? 1
+             : 0;
 }
 
 extern "C" int qh_flash_decode_prepare(const void* q, int64_t sq, const void* k, int64_t sk, const void* v, int64_t sv,
@@ -1744,9 +1751,9 @@ extern "C" int qh_flash_decode_prepare(const void* q, int64_t sq, const void* k,
                                        int64_t vcs, int64_t cap, const int64_t* positions, void* o, float* lse,
                                        const int32_t* seqlens, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk,
                                        int64_t D, float scale, int dtype, int wdtype, int cdtype, void* stream) {
-  QH_CHECK_ARG(qh_flash_decode_prepare_ok(B, Hq, Hkv, D), "qh_flash_decode_prepare: shape not served (B=%lld Hq=%lld "
-               "Hkv=%lld D=%lld; see qh_flash_decode_prepare_ok)", (long long)B, (long long)Hq, (long long)Hkv,
-               (long long)D);
+  QH_CHECK_ARG(qh_flash_decode_prepare_ok(B, Hq, Hkv, Sk, D), "qh_flash_decode_prepare: shape not served (B=%lld "
+               "Hq=%lld Hkv=%lld Sk=%lld D=%lld; see qh_flash_decode_prepare_ok)", (long long)B, (long long)Hq,
+               (long long)Hkv, (long long)Sk, (long long)D);
   QH_CHECK_ARG(Sk >= 0 && Sk <= cap && cap < (1ll << 31), "qh_flash_decode_prepare: need 0 <= Sk <= cap < 2^31");
   const int64_t half = rot / 2;
   QH_CHECK_ARG(rot >= 16 && rot <= D && rot % 16 == 0 && ((half / 8) & (half / 8 - 1)) == 0,

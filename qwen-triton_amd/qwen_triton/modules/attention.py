@@ -147,18 +147,14 @@ class QwenFullAttention(nn.Module):
                 and self.k_norm.weight.dtype == self.q_norm.weight.dtype
                 and self.q_norm.weight.dtype in (torch.float32, q2.dtype)):
             return False
-        cache = self.__dict__.setdefault("_decode_prepare_cache", {})
-        bsz = q2.shape[0]
-        if bsz not in cache:
-            cache[bsz] = bool(_native.call("qh_flash_decode_prepare_ok", bsz, self.num_heads,
-                                           self.num_key_value_heads, self.head_dim))
-        return cache[bsz]
+        return True
 
     def _fused_decode(self, q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor, cos: torch.Tensor,
                       sin: torch.Tensor, past_key_values: QwenTritonCache, cache_position: torch.Tensor,
                       max_position: int | None) -> torch.Tensor:
         """One decode step (a token per sequence): q/k norm, RoPE, the cache writes and the attention
-        in one launch; returns ``[B, Hq, D]``."""
+        in one launch; returns ``[B, Hq, D]``, or None (nothing launched) for shapes the kernel does
+        not serve."""
         bsz = q2.shape[0]
         hq, hkv, d = self.num_heads, self.num_key_value_heads, self.head_dim
         positions = cache_position.to(device=q2.device, dtype=torch.long).reshape(-1)
@@ -170,6 +166,10 @@ class QwenFullAttention(nn.Module):
         # captured decode step: keys span the reserved cache, each sequence's valid length is read
         # from device memory
         seqlens, sk = (static.seqlens, kc.shape[2]) if static is not None else (None, n)
+        # many sequences, or few keys (the kernel's own rule); otherwise the caller takes the
+        # prepare pass and the split decode kernel
+        if not _native.call("qh_flash_decode_prepare_ok", bsz, hq, hkv, sk, d):
+            return None
         q2, k2, v2 = (t.reshape(bsz, -1) for t in (q2, k2, v2))
         if q2.stride(1) != 1 or k2.stride(1) != 1 or v2.stride(1) != 1:
             q2, k2, v2 = q2.contiguous(), k2.contiguous(), v2.contiguous()
@@ -195,7 +195,8 @@ class QwenFullAttention(nn.Module):
         input_shape = q2.shape[:-1]
         if self._decode_prepare_ok(q2, attention_mask, cos, sin):
             out = self._fused_decode(q2, k2, v2, cos, sin, past_key_values, cache_position, max_position)
-            return out.view(*input_shape, -1)
+            if out is not None:
+                return out.view(*input_shape, -1)
         q, k, v = self._fused_prepare(q2, k2, v2, cos, sin, past_key_values, cache_position, max_position)
         static = getattr(past_key_values, "static", None)
         if static is not None and q.shape[2] == 1 and attention_mask is None:

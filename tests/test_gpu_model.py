@@ -339,3 +339,25 @@ def test_fused_decode_prepare_in_model_bitwise(monkeypatch):
         eager = m.greedy_generate(ids[:, :3], max_new_tokens=8)
         graph = m.greedy_generate(ids[:, :3], max_new_tokens=8, use_graph=True)
     assert torch.equal(graph, eager)
+
+
+def test_config0_like_decode_takes_fused_prepare():
+    # batch 1, head_dim 128, short cache: decode steps take qh_flash_decode_prepare; greedy tokens
+    # equal with and without the captured graph, logits within the band of the fp32 oracle
+    cfg = _cfg(hidden_size=256, num_attention_heads=16, num_key_value_heads=8, head_dim=128, num_hidden_layers=2,
+               vocab_size=512)
+    m = _model(cfg, seed=51)
+    ids = torch.randint(0, cfg.vocab_size, (1, 20), generator=torch.Generator().manual_seed(52)).cuda()
+    c0 = _native.CALLS["qh_flash_decode_prepare"]
+    with torch.no_grad():
+        eager = m.greedy_generate(ids, max_new_tokens=12)
+        graph = m.greedy_generate(ids, max_new_tokens=12, use_graph=True)
+    assert _native.CALLS["qh_flash_decode_prepare"] > c0
+    assert torch.equal(graph, eager)
+    with torch.no_grad():
+        p = m(input_ids=eager[:, :20], use_cache=True)
+        steps = [p.logits[:, -1]]
+        for t in range(20, eager.shape[1] - 1):
+            steps.append(m(input_ids=eager[:, t:t + 1], past_key_values=p.past_key_values, use_cache=True).logits[:, -1])
+    ref = OracleQwen(ModelSpec.from_config(cfg), m.state_dict(), dtype=torch.float32).forward(eager[:, :-1].cpu())
+    _band(torch.stack(steps, 1).float().cpu(), ref[:, 19:])

@@ -882,7 +882,7 @@ def test_flash_decode_prepare_matches_prepare_then_decode(Hq, Hkv, B, p, cdtype)
     # p < 384 puts the new row in its wave's first three key tiles (written, then drained, before
     # that tile is read); larger p relies on the loop's own wait before the third tile
     D, cap = 128, 640
-    assert _native.call("qh_flash_decode_prepare_ok", B, Hq, Hkv, D) == 1
+    assert _native.call("qh_flash_decode_prepare_ok", B, Hq, Hkv, p + 1, D) == 1
     q2, k2, v2, kc, vc, qw, kw = _decode_step_inputs(B, Hq, Hkv, D, cap, seed=300 + p)
     theta = (p * torch.pow(1e6, -torch.arange(0, D, 2, dtype=torch.float64) / D)).float()
     cos = torch.cat([theta.cos(), theta.cos()]).view(1, 1, D).to(cdtype).to(DEV)
@@ -960,3 +960,43 @@ def test_flash_decode_prepare_static_cache_seqlens():
                  code(qw.dtype), code(torch.bfloat16), st)
     assert torch.equal(kc, kc_r) and torch.equal(vc, vc_r)
     assert torch.equal(o, o_r.view(B, Hq, D))
+
+
+@pytest.mark.parametrize("B", [1, 3])
+@pytest.mark.parametrize("p", [0, 37, 200, 511])
+def test_flash_decode_prepare_short_context_small_batch(B, p):
+    # few sequences with at most 512 keys also take the workgroup kernel that prepares its own rows
+    # (the split kernel otherwise serves them, summing in another order): cache rows bitwise equal
+    # to the prepare pass, output within the bf16 band of the fp64 oracle over the prepared rows
+    Hq, Hkv, D, cap = 16, 8, 128, 640
+    sk = p + 1
+    assert _native.call("qh_flash_decode_prepare_ok", B, Hq, Hkv, sk, D) == 1
+    assert _native.call("qh_flash_decode_prepare_ok", B, Hq, Hkv, 513, D) == 0
+    q2, k2, v2, kc, vc, qw, kw = _decode_step_inputs(B, Hq, Hkv, D, cap, seed=360 + p)
+    theta = (p * torch.pow(1e6, -torch.arange(0, D, 2, dtype=torch.float64) / D)).float()
+    cos = torch.cat([theta.cos(), theta.cos()]).view(1, 1, D).to(torch.bfloat16).to(DEV)
+    sin = torch.cat([theta.sin(), theta.sin()]).view(1, 1, D).to(torch.bfloat16).to(DEV)
+    pos = torch.tensor([p], dtype=torch.long, device=DEV)
+    code = _native.dtype_code
+    st = _native.stream(torch.device(DEV))
+    kc_r, vc_r = kc.clone(), vc.clone()
+    q_r = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device=DEV)
+    _native.call("qh_attn_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0), v2.data_ptr(),
+                 v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 0, cos.data_ptr(), sin.data_ptr(), cos.stride(0),
+                 cos.stride(1), 1, D, q_r.data_ptr(), kc_r.data_ptr(), *kc_r.stride()[:3], vc_r.data_ptr(),
+                 *vc_r.stride()[:3], pos.data_ptr(), B, 1, Hq, Hkv, D, cap, code(torch.bfloat16), code(qw.dtype),
+                 code(torch.bfloat16), st)
+    o = torch.empty((B, Hq, D), dtype=torch.bfloat16, device=DEV)
+    for _ in range(2):  # reruns are bitwise equal
+        _native.call("qh_flash_decode_prepare", q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0),
+                     v2.data_ptr(), v2.stride(0), qw.data_ptr(), kw.data_ptr(), 1e-6, 0, cos.data_ptr(),
+                     sin.data_ptr(), cos.stride(0), 1, D, kc.data_ptr(), *kc.stride()[:3], vc.data_ptr(),
+                     *vc.stride()[:3], cap, pos.data_ptr(), o.data_ptr(), None, None, B, Hq, Hkv, sk, D, D ** -0.5,
+                     code(torch.bfloat16), code(qw.dtype), code(torch.bfloat16), st)
+        o0 = o.clone() if _ == 0 else o0
+    assert torch.equal(o, o0)
+    assert torch.equal(kc, kc_r) and torch.equal(vc, vc_r)
+    ref = O.attention(q_r, kc_r[:, :, :sk], vc_r[:, :, :sk], D ** -0.5, False, Hq // Hkv)[0]
+    close(o.view(B, Hq, 1, D), ref, **BF16_TOL)
+    o_split = FA.flash_decode(q_r, kc_r[:, :, :sk], vc_r[:, :, :sk], D ** -0.5, Hq // Hkv)
+    close(o.view(B, Hq, 1, D), o_split, atol=1e-2, rtol=1e-2)
