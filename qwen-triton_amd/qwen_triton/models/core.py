@@ -133,7 +133,12 @@ class QwenDecoderLayer(nn.Module):
         attn, mlp = self.self_attn, self.mlp
         if not attn._fused_prepare_ok(hidden_states, position_embeddings[0], past_key_values, cache_position):
             return False
-        key = (hidden_states.shape[0] * hidden_states.shape[1], hidden_states.dtype, hidden_states.device)
+        # the answer depends on the activation shape and on the weights (a cast or a reassignment
+        # of the parameters changes their dtype or storage)
+        key = (hidden_states.shape[0] * hidden_states.shape[1], hidden_states.dtype, hidden_states.device) + tuple(
+            (w.data_ptr(), w.dtype) for w in (attn.q_proj.weight, attn.o_proj.weight, mlp.gate_proj.weight,
+                                              mlp.down_proj.weight, self.input_layernorm.weight,
+                                              self.post_attention_layernorm.weight))
         cache = self.__dict__.setdefault("_fused_ok_cache", {})
         if key not in cache:
             rows = hidden_states.reshape(-1, hidden_states.shape[-1])
