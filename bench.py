@@ -37,11 +37,11 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 # HBM bytes per launch of the decode attention as the config-3 step runs it (one
-# fa_decode_wg_kernel<bf16,128,2,PREP> dispatch), from the two rocprofv3 --pmc passes
-# (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`, each scaled by the same counter's
-# reading for a 1 GiB copy (fetch x 1048576 / 524310.06, write x 1.000):
-# 262679.5 KiB x 1.99991 + 512 KiB = 538,467,731 bytes.
-DECODE_TRAFFIC_BYTES = 538_467_731
+# fa_decode_wg_kernel<bf16,128,2,PREP> dispatch on the interleaved K/V cache), from the two
+# rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`, each scaled by
+# the same counter's reading for a 1 GiB copy (fetch x 1048576 / 524310.0, write x 1.000):
+# 262670.3 KiB x 1.99992 + 512 KiB = 538,450,490 bytes.
+DECODE_TRAFFIC_BYTES = 538_450_490
 
 QWEN3_06B = dict(model_type="qwen3", vocab_size=151936, hidden_size=1024, intermediate_size=3072,
                  num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8, head_dim=128,
@@ -151,7 +151,8 @@ def bench_decode(model, steps, warmup, use_graph=True, batch=64, ctx=2048):
 def decode_layer_launch(batch=64, hq=16, hkv=8, d=128, ctx=2048, seed=0):
     """One layer's decode attention as the config-3 step runs it (qh_flash_decode_prepare: the q/k
     norm, RoPE and cache writes of the step inside the decode kernel) on synthetic inputs of that
-    shape: a 2048-token bf16 cache (capacity 2112), the new token at position 2048. Returns
+    shape: a 2048-token bf16 cache (capacity 2112, key and value rows interleaved as the model's cache
+    lays them out), the new token at position 2048. Returns
     (launch, algorithmic bytes per launch)."""
     import torch
     from qwen_triton import _native
@@ -159,8 +160,9 @@ def decode_layer_launch(batch=64, hq=16, hkv=8, d=128, ctx=2048, seed=0):
     g = torch.Generator(device="cuda").manual_seed(seed)
     bf = torch.bfloat16
     cap, sk = ctx + 64, ctx + 1
-    kc = torch.randn(batch, hkv, cap, d, device="cuda", dtype=bf, generator=g)
-    vc = torch.randn(batch, hkv, cap, d, device="cuda", dtype=bf, generator=g)
+    # the model cache's layout: key and value rows interleaved in one buffer
+    kv = torch.randn(batch, hkv, cap, 2, d, device="cuda", dtype=bf, generator=g)
+    kc, vc = kv[:, :, :, 0, :], kv[:, :, :, 1, :]
     q2 = torch.randn(batch, hq * d, device="cuda", dtype=bf, generator=g)
     k2 = torch.randn(batch, hkv * d, device="cuda", dtype=bf, generator=g)
     v2 = torch.randn(batch, hkv * d, device="cuda", dtype=bf, generator=g)

@@ -5,7 +5,9 @@ Same fields and growth policy as the reference (power-of-two capacity, at least
 Additions: ``update_attention`` accepts ``max_position`` so callers that know the
 largest written position on the host skip the ``positions.max().item()``
 synchronisation, and ``reserve`` preallocates a layer's storage up front (no
-regrowth copies during decoding).
+regrowth copies during decoding). A layer's key and value storages are two views
+of one buffer with their rows interleaved (``[B, H, cap, 2, D]``): a decode step
+then streams one contiguous region per (sequence, kv-head) instead of two.
 """
 from __future__ import annotations
 
@@ -64,6 +66,35 @@ class QwenTritonCache:
             and storage.shape[3] == like.shape[3]
         )
 
+    @staticmethod
+    def _new_kv_pair(shape: tuple[int, int, int, int], dtype: torch.dtype,
+                     device: torch.device | str) -> tuple[torch.Tensor, torch.Tensor]:
+        """Key and value storage ``shape`` = (B, H, cap, D) as views of one [B, H, cap, 2, D] buffer."""
+        b, h, cap, d = shape
+        buf = torch.empty((b, h, cap, 2, d), dtype=dtype, device=device)
+        return buf[:, :, :, 0, :], buf[:, :, :, 1, :]
+
+    def _ensure_kv_storage(self, layer_idx: int, like_k: torch.Tensor, like_v: torch.Tensor, current_length: int,
+                           required_len: int) -> None:
+        """Grow a layer's key/value storages together (the reference grows each as
+        ``_ensure_attention_storage`` does: power-of-two capacity, valid rows copied)."""
+        k, v = self.key_cache[layer_idx], self.value_cache[layer_idx]
+        if (self._compatible(k, like_k) and self._compatible(v, like_v) and k.shape[2] >= required_len
+                and v.shape[2] >= required_len):
+            return
+        if like_k.shape[3] != like_v.shape[3] or like_k.dtype != like_v.dtype or like_k.shape[:2] != like_v.shape[:2]:
+            self.key_cache[layer_idx] = self._ensure_attention_storage(k, like_k, current_length, required_len)
+            self.value_cache[layer_idx] = self._ensure_attention_storage(v, like_v, current_length, required_len)
+            return
+        capacity = self._resolve_capacity(required_len)
+        nk, nv = self._new_kv_pair((like_k.shape[0], like_k.shape[1], capacity, like_k.shape[3]), like_k.dtype,
+                                   like_k.device)
+        for old, new, like in ((k, nk, like_k), (v, nv, like_v)):
+            if self._compatible(old, like) and current_length > 0:
+                n = min(current_length, old.shape[2], capacity)
+                new[:, :, :n].copy_(old[:, :, :n])
+        self.key_cache[layer_idx], self.value_cache[layer_idx] = nk, nv
+
     def _ensure_attention_storage(self, storage, like, current_length: int, required_len: int) -> torch.Tensor:
         if self._compatible(storage, like) and storage.shape[2] >= required_len:
             return storage
@@ -78,14 +109,16 @@ class QwenTritonCache:
                 device: torch.device | str) -> None:
         """Preallocate key/value storage of ``capacity`` positions for one layer."""
         shape = (batch, heads, capacity, head_dim)
-        for store in (self.key_cache, self.value_cache):
-            cur = store[layer_idx]
-            if cur is None or cur.shape[2] < capacity or tuple(cur.shape[:2]) != shape[:2]:
-                new = torch.empty(shape, dtype=dtype, device=device)
-                n = self.attention_lengths[layer_idx]
-                if cur is not None and n > 0 and tuple(cur.shape[:2]) == shape[:2]:
-                    new[:, :, :n].copy_(cur[:, :, :n])
-                store[layer_idx] = new
+        cur_k, cur_v = self.key_cache[layer_idx], self.value_cache[layer_idx]
+        if all(cur is not None and cur.shape[2] >= capacity and tuple(cur.shape[:2]) == shape[:2]
+               and cur.shape[3] == head_dim for cur in (cur_k, cur_v)):
+            return
+        new_k, new_v = self._new_kv_pair(shape, dtype, device)
+        n = self.attention_lengths[layer_idx]
+        for cur, new in ((cur_k, new_k), (cur_v, new_v)):
+            if cur is not None and n > 0 and tuple(cur.shape[:2]) == shape[:2] and cur.shape[3] == head_dim:
+                new[:, :, :n].copy_(cur[:, :, :n])
+        self.key_cache[layer_idx], self.value_cache[layer_idx] = new_k, new_v
 
     def update_attention(
         self,
@@ -111,10 +144,7 @@ class QwenTritonCache:
             required = int(max_position) + 1
         else:
             required = int(positions.max().item()) + 1
-        self.key_cache[layer_idx] = self._ensure_attention_storage(self.key_cache[layer_idx], key_states, current, required)
-        self.value_cache[layer_idx] = self._ensure_attention_storage(
-            self.value_cache[layer_idx], value_states, current, required
-        )
+        self._ensure_kv_storage(layer_idx, key_states, value_states, current, required)
         write_attention_kv(self.key_cache[layer_idx], key_states, positions)
         write_attention_kv(self.value_cache[layer_idx], value_states, positions)
         self.attention_lengths[layer_idx] = max(current, required)
@@ -137,9 +167,7 @@ class QwenTritonCache:
         else:
             required = int(positions.max().item()) + 1
         like = torch.empty((batch, heads, 0, head_dim), dtype=dtype, device=device)
-        self.key_cache[layer_idx] = self._ensure_attention_storage(self.key_cache[layer_idx], like, current, required)
-        self.value_cache[layer_idx] = self._ensure_attention_storage(self.value_cache[layer_idx], like, current,
-                                                                     required)
+        self._ensure_kv_storage(layer_idx, like, like, current, required)
         self.attention_lengths[layer_idx] = max(current, required)
         return self.key_cache[layer_idx], self.value_cache[layer_idx], self.attention_lengths[layer_idx]
 
