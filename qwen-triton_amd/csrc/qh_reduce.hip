@@ -640,7 +640,31 @@ __global__ __launch_bounds__(1024) void topk_wide_kernel(const T* __restrict__ x
   for (int r = 0; r < k; ++r) {
     float bv = -INFINITY;
     int bi = -1;
-    if constexpr (VEC) {
+    if (VEC && k == 1) {
+      // Top-1: each thread visits its columns in increasing order, so a strict > keeps the
+      // lowest index of equal maxima; NaN is never taken (topk_after is false for it) and the
+      // first non-NaN value is taken whatever it is (bi < 0 in topk_better).
+      const int nv = C / VN;
+      for (int v0 = tid; v0 < nv; v0 += 8 * 1024) {
+        Vec16<T> buf[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (v0 + u * 1024 < nv) buf[u] = ld16(xr + (int64_t)(v0 + u * 1024) * VN);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (v0 + u * 1024 < nv) {
+#pragma unroll
+            for (int e = 0; e < VN; ++e) {
+              const float v = to_f32(buf[u].v[e]);
+              if (v > bv || (bi < 0 && v == v)) {
+                bv = v;
+                bi = (v0 + u * 1024) * VN + e;
+              }
+            }
+          }
+        }
+      }
+    } else if constexpr (VEC) {
       const int nv = C / VN;  // C is a multiple of VN
       for (int v0 = tid; v0 < nv; v0 += 4 * 1024) {
         Vec16<T> buf[4];

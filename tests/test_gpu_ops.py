@@ -303,6 +303,30 @@ def test_topk_wide_rows(N, C, k, dtype):
         assert torch.equal(idx.view(-1).cpu(), torch.argmax(x.float().cpu(), dim=-1))
 
 
+@pytest.mark.parametrize("N", [1, 64])
+def test_topk1_wide_rows_ties_and_specials(N):
+    """The greedy pick over a vocabulary row (k = 1, 151936 columns; configs 0 and 3): quantised
+    values with tied maxima, +-0, -inf and NaN entries, and an all -inf row."""
+    C = 151936
+    x = torch.round(torch.randn(N, C, generator=_gen(85)) * 2) / 2
+    x[:, ::997] = -0.0
+    x[:, 5::1009] = float("-inf")
+    x[::2, 11::4001] = float("nan")
+    x[:, 70000] = 7.5  # a tied maximum: the lower column wins
+    x[:, 150000] = 7.5
+    if N > 3:
+        x[3] = float("-inf")
+    x = x.to(torch.bfloat16).to(DEV)
+    vals, idx = K.triton_topk(x, 1)
+    xc = x.cpu().float()
+    ref = torch.where(torch.isnan(xc), torch.tensor(float("-inf")), xc)
+    order = torch.sort(-ref.double(), dim=-1, stable=True).indices[:, 0]
+    assert torch.equal(idx.view(-1).cpu(), order)
+    assert torch.equal(vals.view(-1).cpu().float(), xc.gather(1, order[:, None]).view(-1))
+    if N > 3:
+        assert idx.view(-1)[3].item() == 0
+
+
 def test_topk_ties_go_to_lowest_index():
     x = torch.tensor([[1.0, 3.0, 3.0, 0.5, 3.0, 1.0], [2.0] * 6], device=DEV)
     vals, idx = K.triton_topk(x, 4)
