@@ -1050,16 +1050,16 @@ __global__ __launch_bounds__(64) void fa_decode_kernel(const T* __restrict__ Q, 
     if (row0 + BN <= ke) {
 #pragma unroll
       for (int n = 0; n < NI; ++n) {
-        lds_dma16_s(koff[n % NPAT], Kb + (int64_t)(row0 + n * RPI) * sks, kl + (uint32_t)(n * RPI * DP * sizeof(T)));
-        lds_dma16_s(voff[n % NPAT], Vb + (int64_t)(row0 + n * RPI) * svs, vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16_s_nt(koff[n % NPAT], Kb + (int64_t)(row0 + n * RPI) * sks, kl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16_s_nt(voff[n % NPAT], Vb + (int64_t)(row0 + n * RPI) * svs, vl + (uint32_t)(n * RPI * DP * sizeof(T)));
       }
     } else {
 #pragma unroll
       for (int n = 0; n < NI; ++n) {
         int gr = row0 + n * RPI + rl;
         gr = gr < ke ? gr : ke - 1;
-        lds_dma16(Kb + (int64_t)gr * sks + dsw[n % NPAT], kl + (uint32_t)(n * RPI * DP * sizeof(T)));
-        lds_dma16(Vb + (int64_t)gr * svs + dsw[n % NPAT], vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16_nt(Kb + (int64_t)gr * sks + dsw[n % NPAT], kl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16_nt(Vb + (int64_t)gr * svs + dsw[n % NPAT], vl + (uint32_t)(n * RPI * DP * sizeof(T)));
       }
     }
   };
@@ -1283,18 +1283,19 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
       key = key < sk_b ? key : sk_b - 1;
       const T* kr = Kb + (int64_t)key * sks;
 #pragma unroll
-      for (int kd = 0; kd < KD; ++kd) kf[h][kd] = *reinterpret_cast<const v8*>(kr + kdo[kd]);
+      for (int kd = 0; kd < KD; ++kd)
+        kf[h][kd] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(kr + kdo[kd]));
     }
     if (row0 + BN <= sk_b) {
 #pragma unroll
       for (int n = 0; n < NI; ++n)
-        lds_dma16_s(voff[n % NPAT], Vb + (int64_t)(row0 + n * RPI) * svs, vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16_s_nt(voff[n % NPAT], Vb + (int64_t)(row0 + n * RPI) * svs, vl + (uint32_t)(n * RPI * DP * sizeof(T)));
     } else {
 #pragma unroll
       for (int n = 0; n < NI; ++n) {
         int gr = row0 + n * RPI + rl;
         gr = gr < sk_b ? gr : sk_b - 1;
-        lds_dma16(Vb + (int64_t)gr * svs + dsw[n % NPAT], vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        lds_dma16_nt(Vb + (int64_t)gr * svs + dsw[n % NPAT], vl + (uint32_t)(n * RPI * DP * sizeof(T)));
       }
     }
   };

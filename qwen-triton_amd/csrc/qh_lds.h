@@ -37,6 +37,24 @@ __device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* base, uin
                "s"(lds_base)
                : "memory", "m0");
 }
+// Non-temporal forms (the `nt` cache-policy hint): for data read once and
+// streamed past the caches, such as a decode step's KV cache, whose 0.5 GB per
+// layer exceeds the last-level cache so keeping it there only evicts other data.
+__device__ __forceinline__ void lds_dma16_nt(const void* src, uint32_t lds_base) {
+  lds_base = (uint32_t)__builtin_amdgcn_readfirstlane(lds_base);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(lds_base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma16_s_nt(uint32_t voff, const void* base, uint32_t lds_base) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint64_t ub = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b) |
+                      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32);
+  const void* sbase = (const void*)(uintptr_t)ub;
+  lds_base = (uint32_t)__builtin_amdgcn_readfirstlane(lds_base);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase),
+               "s"(lds_base)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
