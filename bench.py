@@ -37,11 +37,11 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 # HBM bytes per launch of the decode attention as the config-3 step runs it (one
-# fa_decode_wg_kernel<bf16,128,2,PREP> dispatch on the interleaved K/V cache), from the two
-# rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`, each scaled by
-# the same counter's reading for a 1 GiB copy (fetch x 1048576 / 524310.0, write x 1.000):
-# 262670.3 KiB x 1.99992 + 512 KiB = 538,450,490 bytes.
-DECODE_TRAFFIC_BYTES = 538_450_490
+# fa_decode_wg_kernel<bf16,128,2,PREP> dispatch on the interleaved K/V cache, non-temporal loads),
+# from the two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`,
+# each scaled by the same counter's reading for a 1 GiB copy (fetch x 1048576 / 524310.0, write
+# x 1.000): 263125.5 KiB x 1.99992 + 512 KiB = 539,382,701 bytes.
+DECODE_TRAFFIC_BYTES = 539_382_701
 
 QWEN3_06B = dict(model_type="qwen3", vocab_size=151936, hidden_size=1024, intermediate_size=3072,
                  num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8, head_dim=128,
