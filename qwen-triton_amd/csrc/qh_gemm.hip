@@ -43,7 +43,9 @@ constexpr int LDS_LD = BK + 8;  // padded row length (elements) of an LDS tile
 // Stage one operand tile (ROWS x BK) for k-tile starting at k0 into registers.
 // Non-transposed: 16-byte chunk c -> row c/8, k-chunk c%8.
 // Transposed:     8x8 sub-block sb -> row-block sb % (ROWS/8), k-block sb / (ROWS/8).
-template <typename T, int ROWS, bool TR>
+// NT: non-temporal loads (operands read exactly once, e.g. the weights of a
+// product with a single row of output tiles).
+template <typename T, int ROWS, bool TR, bool NT = false>
 struct TileLoader {
   static constexpr int SUBS = (ROWS + 255) / 256;          // 8x8 sub-blocks per thread (transposed)
   static constexpr int NREG = TR ? 8 * SUBS : ROWS / 32;   // uint4 staging registers per thread
@@ -58,8 +60,18 @@ struct TileLoader {
         const int c = tid + i * 256;
         const int row = c >> 3, kc = c & 7;
         const int gr = row0 + row, gk = k0 + kc * 8;
-        if (gr < rows && gk < K) r[i] = *reinterpret_cast<const uint4*>(P + (int64_t)gr * ld + gk);
-        else r[i] = z;
+        if (gr < rows && gk < K) {
+          const T* src = P + (int64_t)gr * ld + gk;
+          if constexpr (NT) {
+            typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+            const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+            r[i] = make_uint4(v.x, v.y, v.z, v.w);
+          } else {
+            r[i] = *reinterpret_cast<const uint4*>(src);
+          }
+        } else {
+          r[i] = z;
+        }
       }
     } else {
 #pragma unroll
@@ -107,7 +119,7 @@ struct TileLoader {
 };
 
 
-template <typename T, typename OT, int BM, int BN, int WM, int WN, bool AT, bool BT>
+template <typename T, typename OT, int BM, int BN, int WM, int WN, bool AT, bool BT, bool BNT = false>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A, int64_t lda, const T* __restrict__ B,
                                                         int64_t ldb, OT* __restrict__ C, int64_t ldc,
                                                         const T* __restrict__ bias, int M, int N, int K,
@@ -135,7 +147,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   TileLoader<T, BM, AT> la;
-  TileLoader<T, BN, BT> lb;
+  TileLoader<T, BN, BT, BNT> lb;
   const int nk = (K + BK - 1) / BK;
 
   la.load(A, lda, m0, M, 0, K);
@@ -337,7 +349,8 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
       }
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        if (nok && kok) b[u][j] = *reinterpret_cast<const v8*>(brow[j] + k);
+        // weights are read once per decode step: non-temporal, so they do not evict cached data
+        if (nok && kok) b[u][j] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(brow[j] + k));
         else b[u][j] = zero;
       }
 #pragma unroll
@@ -731,7 +744,12 @@ template <typename T, typename OT, int BM, int BN, int WM, int WN, bool AT, bool
 void launch_mfma(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_t ldc, const T* bias, int M, int N,
                  int K, hipStream_t st) {
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-  gemm_mfma_kernel<T, OT, BM, BN, WM, WN, AT, BT><<<tm * tn, 256, 0, st>>>(A, lda, B, ldb, C, ldc, bias, M, N, K, tm, tn);
+  if (tm == 1 && !BT)  // one row of tiles: every weight element is read once (the batched LM head)
+    gemm_mfma_kernel<T, OT, BM, BN, WM, WN, AT, BT, true><<<tn, 256, 0, st>>>(A, lda, B, ldb, C, ldc, bias, M, N, K,
+                                                                              tm, tn);
+  else
+    gemm_mfma_kernel<T, OT, BM, BN, WM, WN, AT, BT><<<tm * tn, 256, 0, st>>>(A, lda, B, ldb, C, ldc, bias, M, N, K,
+                                                                             tm, tn);
 }
 
 template <typename T, typename OT, bool AT, bool BT>
