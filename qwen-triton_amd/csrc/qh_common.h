@@ -87,6 +87,25 @@ __device__ __forceinline__ void st16(T* p, const Vec16<T>& v) {
   *reinterpret_cast<uint4*>(p) = v.raw;
 }
 
+// Non-temporal forms, for tensors streamed once that exceed the last-level
+// cache (e.g. logits over a 151936-word vocabulary): they do not displace
+// cached data.
+typedef unsigned int qh_u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ Vec16<T> ld16_nt(const T* p) {
+  const qh_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const qh_u32x4*>(p));
+  Vec16<T> r;
+  r.raw = make_uint4(v.x, v.y, v.z, v.w);
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void st16_nt(T* p, const Vec16<T>& v) {
+  const qh_u32x4 w = {v.raw.x, v.raw.y, v.raw.z, v.raw.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<qh_u32x4*>(p));
+}
+
 // ---------------------------------------------------------------------------
 // Wavefront reductions (64 lanes). `width` must be a power of two <= 64 and
 // reduces within aligned groups of `width` lanes; every lane gets the result.

@@ -453,7 +453,7 @@ __global__ __launch_bounds__(256) void ce_fwd_kernel(const T* __restrict__ logit
   if constexpr (VEC) {
     constexpr int VN = Vec16<T>::N;
     for (int64_t c = threadIdx.x * VN; c < V; c += 256 * VN) {
-      Vec16<T> v = ld16(xr + c);
+      Vec16<T> v = ld16_nt(xr + c);
       float lm = -INFINITY;
 #pragma unroll
       for (int j = 0; j < VN; ++j) lm = fmaxf(lm, to_f32(v.v[j]));
@@ -534,14 +534,14 @@ __global__ __launch_bounds__(256) void ce_bwd_kernel(const T* __restrict__ logit
       if (ign) {
         o.raw = make_uint4(0, 0, 0, 0);
       } else {
-        Vec16<T> v = ld16(xr + c);
+        Vec16<T> v = ld16_nt(xr + c);
 #pragma unroll
         for (int j = 0; j < VN; ++j) {
           const float p = fast_exp(to_f32(v.v[j]) - l);
           o.v[j] = from_f32<T>((p - ((c + j) == t ? 1.f : 0.f)) * scale);
         }
       }
-      st16(gr + c, o);
+      st16_nt(gr + c, o);
     }
   } else {
     for (int64_t c = threadIdx.x; c < V; c += 256) {
