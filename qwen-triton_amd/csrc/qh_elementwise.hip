@@ -20,16 +20,31 @@ __device__ __forceinline__ float ew_apply(float a, float b) {
   return a * sigmoidf_(b);                                           // x * sigmoid(gate)
 }
 
-template <EwOp OP, typename T>
+// Launches whose traffic reaches the last-level cache's size (256 MB) stream
+// with non-temporal accesses (NT): caching them would only evict other data.
+constexpr int64_t kStreamBytes = 256ll << 20;
+
+template <bool NT, typename T>
+__device__ __forceinline__ Vec16<T> ld16s(const T* p) {
+  if constexpr (NT) return ld16_nt(p);
+  else return ld16(p);
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void st16s(T* p, const Vec16<T>& v) {
+  if constexpr (NT) st16_nt(p, v);
+  else st16(p, v);
+}
+
+template <EwOp OP, typename T, bool NT>
 __global__ __launch_bounds__(256) void ew_binary_vec(const T* __restrict__ a, const T* __restrict__ b,
                                                      T* __restrict__ o, int64_t nvec) {
   constexpr int VN = Vec16<T>::N;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
        i += (int64_t)gridDim.x * blockDim.x) {
-    Vec16<T> va = ld16(a + i * VN), vb = ld16(b + i * VN), vo;
+    Vec16<T> va = ld16s<NT>(a + i * VN), vb = ld16s<NT>(b + i * VN), vo;
 #pragma unroll
     for (int j = 0; j < VN; ++j) vo.v[j] = from_f32<T>(ew_apply<OP>(to_f32(va.v[j]), to_f32(vb.v[j])));
-    st16(o + i * VN, vo);
+    st16s<NT>(o + i * VN, vo);
   }
 }
 
@@ -53,8 +68,12 @@ int launch_binary(const void* a, const void* b, void* o, int64_t n, hipStream_t 
   constexpr int VN = Vec16<T>::N;
   int64_t nvec = 0;
   if (aligned16(a) && aligned16(b) && aligned16(o)) nvec = n / VN;
-  if (nvec > 0)
-    ew_binary_vec<OP, T><<<grid_for(nvec), 256, 0, st>>>((const T*)a, (const T*)b, (T*)o, nvec);
+  if (nvec > 0) {
+    if (3 * nvec * 16 >= kStreamBytes)
+      ew_binary_vec<OP, T, true><<<grid_for(nvec), 256, 0, st>>>((const T*)a, (const T*)b, (T*)o, nvec);
+    else
+      ew_binary_vec<OP, T, false><<<grid_for(nvec), 256, 0, st>>>((const T*)a, (const T*)b, (T*)o, nvec);
+  }
   int64_t done = nvec * VN;
   if (done < n)
     ew_binary_scalar<OP, T><<<grid_for(n - done), 256, 0, st>>>((const T*)a, (const T*)b, (T*)o, done, n);
@@ -75,14 +94,14 @@ __device__ __forceinline__ void ew_grad(float a, float b, float g, float& ga, fl
   }
 }
 
-template <EwOp OP, typename T>
+template <EwOp OP, typename T, bool NT>
 __global__ __launch_bounds__(256) void ew_grad_vec(const T* __restrict__ a, const T* __restrict__ b,
                                                    const T* __restrict__ g, T* __restrict__ ga,
                                                    T* __restrict__ gb, int64_t nvec) {
   constexpr int VN = Vec16<T>::N;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
        i += (int64_t)gridDim.x * blockDim.x) {
-    Vec16<T> va = ld16(a + i * VN), vb = ld16(b + i * VN), vg = ld16(g + i * VN), oa, ob;
+    Vec16<T> va = ld16s<NT>(a + i * VN), vb = ld16s<NT>(b + i * VN), vg = ld16s<NT>(g + i * VN), oa, ob;
 #pragma unroll
     for (int j = 0; j < VN; ++j) {
       float x, y;
@@ -90,8 +109,8 @@ __global__ __launch_bounds__(256) void ew_grad_vec(const T* __restrict__ a, cons
       oa.v[j] = from_f32<T>(x);
       ob.v[j] = from_f32<T>(y);
     }
-    st16(ga + i * VN, oa);
-    st16(gb + i * VN, ob);
+    st16s<NT>(ga + i * VN, oa);
+    st16s<NT>(gb + i * VN, ob);
   }
 }
 
@@ -113,9 +132,14 @@ int launch_grad(const void* a, const void* b, const void* g, void* ga, void* gb,
   constexpr int VN = Vec16<T>::N;
   int64_t nvec = 0;
   if (aligned16(a) && aligned16(b) && aligned16(g) && aligned16(ga) && aligned16(gb)) nvec = n / VN;
-  if (nvec > 0)
-    ew_grad_vec<OP, T><<<grid_for(nvec), 256, 0, st>>>((const T*)a, (const T*)b, (const T*)g, (T*)ga,
-                                                       (T*)gb, nvec);
+  if (nvec > 0) {
+    if (5 * nvec * 16 >= kStreamBytes)
+      ew_grad_vec<OP, T, true><<<grid_for(nvec), 256, 0, st>>>((const T*)a, (const T*)b, (const T*)g, (T*)ga,
+                                                               (T*)gb, nvec);
+    else
+      ew_grad_vec<OP, T, false><<<grid_for(nvec), 256, 0, st>>>((const T*)a, (const T*)b, (const T*)g, (T*)ga,
+                                                                (T*)gb, nvec);
+  }
   int64_t done = nvec * VN;
   if (done < n)
     ew_grad_scalar<OP, T><<<grid_for(n - done), 256, 0, st>>>((const T*)a, (const T*)b, (const T*)g,
@@ -158,7 +182,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, int6
 
 // Vectorised RoPE for the common case: contiguous last dim, rot == D, half a
 // multiple of the vector width. Each thread rotates VN pairs.
-template <typename T>
+template <typename T, bool NT>
 __global__ __launch_bounds__(256) void rope_vec_kernel(const T* __restrict__ x, int64_t sxb, int64_t sxh,
                                                        int64_t sxs, const T* __restrict__ cs,
                                                        const T* __restrict__ sn, int64_t scb, int64_t scs,
@@ -176,7 +200,7 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(const T* __restrict__ x, 
     const T* xr = x + b * sxb + h * sxh + s * sxs;
     const int64_t cb = (cos_batch == 1) ? 0 : b;
     const int64_t co = cb * scb + s * scs + w;
-    Vec16<T> x1 = ld16(xr + w), x2 = ld16(xr + w + half), c = ld16(cs + co), sv = ld16(sn + co), o1, o2;
+    Vec16<T> x1 = ld16s<NT>(xr + w), x2 = ld16s<NT>(xr + w + half), c = ld16(cs + co), sv = ld16(sn + co), o1, o2;
 #pragma unroll
     for (int j = 0; j < VN; ++j) {
       const float a = to_f32(x1.v[j]), bb = to_f32(x2.v[j]), cc = to_f32(c.v[j]), ss = sgn * to_f32(sv.v[j]);
@@ -184,8 +208,8 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(const T* __restrict__ x, 
       o2.v[j] = from_f32<T>(bb * cc + a * ss);
     }
     T* orow = out + row * D;
-    st16(orow + w, o1);
-    st16(orow + w + half, o2);
+    st16s<NT>(orow + w, o1);
+    st16s<NT>(orow + w + half, o2);
   }
 }
 
@@ -357,8 +381,14 @@ static int launch_rope(const void* x, int64_t sxb, int64_t sxh, int64_t sxs, int
                    sxh % VN == 0 && sxs % VN == 0 && scb % VN == 0 && scs % VN == 0;
   if (vec) {
     const int64_t total = rows * (half / VN);
-    rope_vec_kernel<T><<<grid_for(total), 256, 0, st>>>((const T*)x, sxb, sxh, sxs, (const T*)cs, (const T*)sn,
-                                                        scb, scs, cos_batch, (T*)out, H, S, D, half, total, sgn);
+    if (2 * rows * D * (int64_t)sizeof(T) >= kStreamBytes)
+      rope_vec_kernel<T, true><<<grid_for(total), 256, 0, st>>>((const T*)x, sxb, sxh, sxs, (const T*)cs,
+                                                                (const T*)sn, scb, scs, cos_batch, (T*)out, H, S, D,
+                                                                half, total, sgn);
+    else
+      rope_vec_kernel<T, false><<<grid_for(total), 256, 0, st>>>((const T*)x, sxb, sxh, sxs, (const T*)cs,
+                                                                 (const T*)sn, scb, scs, cos_batch, (T*)out, H, S, D,
+                                                                 half, total, sgn);
   } else {
     const int64_t items = half + (D - rot);
     const int64_t total = rows * items;
