@@ -1198,7 +1198,8 @@ __global__ __launch_bounds__(256) void fa_decode_combine(const float* __restrict
 // p also writes the new key row (normalised, rotated) and value row into the
 // caches at p. Vector-memory counts retire in issue order, so the loop's wait
 // before tile 2 is requested also covers those stores; only when p lies in the
-// wave's first three tiles does it write first and drain before that tile.
+// wave's first three tiles does it write first and wait for vmcnt(0) (the
+// stores' completion) before it requests that tile.
 template <typename T, bool PREP>
 using kv_ptr = typename std::conditional<PREP, const T*, const T* __restrict__>::type;
 
@@ -1276,7 +1277,9 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
   auto issue = [&](int t, v8 (&kf)[2][KD]) {
     const int row0 = (w + t * NW) * BN;
     const uint32_t vl = lds_addr(Vs[w][t % NS]);
-    if (PREP && w + t * NW == tile_p && t <= 2) __threadfence_block();  // the new rows are stored
+    // the new rows are stored before the loads of their tile are issued: vmcnt counts this wave's
+    // vector stores as well as its loads (gfx9 family), so vmcnt(0) waits for the row stores
+    if (PREP && w + t * NW == tile_p && t <= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       int key = row0 + 16 * h + li;
@@ -1357,7 +1360,7 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
 #pragma unroll
         for (int e = 0; e < 8; ++e) qf[kd][e] = (T)0.f;
     }
-    if (slow && ntiles > 0) issue(0, ka);  // issue() drains the stores before the tile holding p
+    if (slow && ntiles > 0) issue(0, ka);  // issue() waits for vmcnt(0) before the tile holding p
   } else {
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd) {
