@@ -360,6 +360,19 @@ int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int6
                     int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o, float* lse,
                     const int32_t* seqlens, void* ws, int64_t ws_bytes, int64_t B, int64_t Hq, int64_t Hkv,
                     int64_t Sk, int64_t D, float scale, int dtype, void* stream);
+/* qh_flash_decode without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc). The split partials live in a static 16 MiB device array
+ * per GPU (held from the first call on that GPU until the process ends);
+ * shapes whose partials need more (qh_flash_decode_workspace, or 0 where head
+ * dim 128 meets at least 512 (sequence, kv-head) pairs) return QH_E_WORKSPACE.
+ * Results equal qh_flash_decode's bit for bit. Calls that overlap on one GPU
+ * share the array and race; serialise them (one stream). */
+int qh_flash_decode_noalloc(const void* q, int64_t sqb, int64_t sqh, const void* k, int64_t skb, int64_t skh,
+                            int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o, float* lse,
+                            const int32_t* seqlens, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk, int64_t D,
+                            float scale, int dtype, void* stream);
 /* 1 when qh_flash_decode_prepare serves these shapes (D == 128, Hq / Hkv in
  * {1, 2, 4, 8}, and at least 512 (sequence, kv-head) pairs or at most 512 keys
  * Sk), else 0. No counterpart in the reference: a capability query for the

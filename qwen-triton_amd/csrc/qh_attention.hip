@@ -28,6 +28,8 @@
 // kv-head) streaming K/V tiles through LDS on the matrix cores (the pass is
 // HBM-bound on K/V), partial (m, l, o) per split in the workspace, then a
 // fixed-order combine.
+#include <mutex>
+
 #include "qh_lds.h"
 #include "qh_mfma.h"
 #include "qh_prep.h"
@@ -1733,6 +1735,75 @@ extern "C" int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const vo
 #undef QH_DEC
   QH_CHECK_LAUNCH("qh_flash_decode");
   return QH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: qh_flash_decode with its split partials in a
+// file-scope device array instead of a caller workspace, for callers that
+// cannot allocate (code under HIP graph capture, serving loops that forbid
+// hipMalloc). Each GPU holds its own copy of the array from the first call on
+// it until the process ends. The array keeps the last call's contents; nothing
+// needs clearing, because every split of a call writes all of its partials
+// (m, l and o, also for a split with no keys) before the combine reads them.
+// Calls that overlap on one GPU (two streams, or two host threads) share the
+// array and race.
+constexpr int64_t kDecodeScratchBytes = 16ll << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+namespace {
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchMaxDevices] = {};
+
+// Device address of `scratch` on the device of `st` (hipGetSymbolAddress once
+// per device, with that device current). Host code uses only this address:
+// the array's name on the host side is a stand-in, not a device pointer.
+int decode_scratch(hipStream_t st, void** out) {
+  int cur = 0;
+  QH_CHECK_HIP(hipGetDevice(&cur), "qh_flash_decode_noalloc: hipGetDevice");
+  int dev = cur;
+  if (st != nullptr) QH_CHECK_HIP(hipStreamGetDevice(st, &dev), "qh_flash_decode_noalloc: hipStreamGetDevice");
+  QH_CHECK_ARG(dev >= 0 && dev < kScratchMaxDevices, "qh_flash_decode_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur) QH_CHECK_HIP(hipSetDevice(dev), "qh_flash_decode_noalloc: hipSetDevice");
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) QH_CHECK_HIP(hipSetDevice(cur), "qh_flash_decode_noalloc: hipSetDevice");
+    if (e != hipSuccess || p == nullptr) {
+      qh::set_error("qh_flash_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                    hipGetErrorString(e));
+      return QH_E_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return QH_OK;
+}
+}  // namespace
+
+extern "C" int qh_flash_decode_noalloc(const void* q, int64_t sqb, int64_t sqh, const void* k, int64_t skb,
+                                       int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh,
+                                       int64_t svs, void* o, float* lse, const int32_t* seqlens, int64_t B,
+                                       int64_t Hq, int64_t Hkv, int64_t Sk, int64_t D, float scale, int dtype,
+                                       void* stream) {
+  QH_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && Sk >= 0, "qh_flash_decode_noalloc: bad shape");
+  // the workgroup kernel (head dim 128, many sequences) keeps its partials on chip
+  const bool on_chip = pick_dp(D) == 128 && B * Hkv >= kDecodeWgMinSeqs;
+  const int64_t need = on_chip ? 0 : qh_flash_decode_workspace(B, Hq, Hkv, Sk, D);
+  if (need > kDecodeScratchBytes) {
+    qh::set_error("qh_flash_decode_noalloc: this shape needs %lld bytes of split partials, more than the %lld-byte "
+                  "static scratch; use qh_flash_decode with a workspace",
+                  (long long)need, (long long)kDecodeScratchBytes);
+    return QH_E_WORKSPACE;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = decode_scratch((hipStream_t)stream, &ws);
+    if (rc != QH_OK) return rc;
+  }
+  return qh_flash_decode(q, sqb, sqh, k, skb, skh, sks, v, svb, svh, svs, o, lse, seqlens, ws, need, B, Hq, Hkv, Sk,
+                         D, scale, dtype, stream);
 }
 
 // Keys a few workgroups stream fast enough on their own: short caches take the
