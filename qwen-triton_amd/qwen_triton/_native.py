@@ -3,8 +3,8 @@
 The library exposes a plain C ABI (``include/qwen_hip.h``): device pointers,
 int64 sizes/strides, a dtype code and the caller's HIP stream. This module
 loads it once, declares every entry point's signature, maps non-zero return
-codes to :class:`NativeError` carrying ``qh_last_error()``, and counts calls per
-entry point so tests can prove that the HIP path (not a fallback) executed.
+codes to :class:`NativeError` carrying ``qh_last_error()``, and counts successful
+calls per entry point so tests can prove that the HIP path (not a fallback) executed.
 """
 from __future__ import annotations
 
@@ -67,6 +67,19 @@ class NativeError(RuntimeError):
     """A libqwen_hip entry point returned a non-zero status."""
 
 
+class Unsupported(ValueError):
+    """Inputs that are valid for the operator but outside what the HIP kernels take (a dtype, a head
+    dimension, an alignment or layout). Raised before anything is launched; the operator wrappers run
+    such a call on torch and keep using the kernels for later calls."""
+
+
+class NativeUnsupported(NativeError, Unsupported):
+    """The library rejected its arguments (QH_E_ARG / QH_E_DTYPE) before launching anything."""
+
+
+_REJECTED = (1, 2)  # QH_E_ARG, QH_E_DTYPE: argument checks that run before any launch
+
+
 def _bind(lib: ctypes.CDLL, name: str) -> None:
     restype, argtypes = _SIGNATURES[name]
     fn = getattr(lib, name)
@@ -126,10 +139,11 @@ def call(name: str, *args) -> int:
         entry = _FNS[name] = (getattr(handle, name), _SIGNATURES[name][0] == "i")
     fn, checked = entry
     rc = fn(*args)
-    CALLS[name] += 1
     if checked and rc != 0:
         msg = lib().qh_last_error().decode(errors="replace")
-        raise NativeError(f"{name} failed (status {rc}): {msg}")
+        cls = NativeUnsupported if rc in _REJECTED else NativeError
+        raise cls(f"{name} failed (status {rc}): {msg}")
+    CALLS[name] += 1  # counts calls that returned success
     return rc
 
 
@@ -137,7 +151,7 @@ def dtype_code(dtype: torch.dtype) -> int:
     try:
         return _DTYPE_CODE[dtype]
     except KeyError:
-        raise TypeError(f"libqwen_hip supports float32/float16/bfloat16, got {dtype}") from None
+        raise Unsupported(f"libqwen_hip supports float32/float16/bfloat16, got {dtype}") from None
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
@@ -159,7 +173,7 @@ def require_device(*tensors: torch.Tensor | None) -> None:
     """Native kernels only take device tensors; anything else is a caller error."""
     for t in tensors:
         if t is not None and not t.is_cuda:
-            raise ValueError("libqwen_hip kernels require GPU tensors")
+            raise Unsupported("libqwen_hip kernels require GPU tensors")
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:

@@ -9,6 +9,12 @@ qwen_triton/kernels/matmul.py:19-32, :235-255):
   ``RuntimeError`` (``QWEN_TRITON_STRICT=1``) or warns once with a
   ``[Qwen-Triton fallback]`` ``RuntimeWarning`` and uses torch from then on.
 
+Inputs outside what the HIP kernels take (``Unsupported``: a dtype, head
+dimension or layout the kernels do not serve, rejected before any launch) are
+not kernel failures: that one call runs on torch (after a warning, or a
+``RuntimeError`` in strict mode) and the flag stays set, so later calls with
+supported inputs still reach the kernels.
+
 One deliberate difference: if the native library itself cannot be loaded while
 the inputs live on the GPU, the call raises instead of silently running torch,
 so a GPU run can never pass on a fallback without anyone noticing.
@@ -21,6 +27,7 @@ import warnings
 import torch
 
 from .. import _native
+from .._native import Unsupported  # noqa: F401  (re-exported for the wrappers)
 
 
 def strict_mode() -> bool:
@@ -34,6 +41,7 @@ class OpGuard:
         self.label = label
         self.runtime_ok = True
         self.warned = False
+        self.unsupported_seen: set[str] = set()
 
     def use_native(self, use_triton: bool | None, *tensors: torch.Tensor | None) -> bool:
         if use_triton is None:
@@ -50,7 +58,19 @@ class OpGuard:
         return True
 
     def failed(self, exc: BaseException, what: str = "kernel") -> None:
-        """Record a failure; raises in strict mode, otherwise warns once."""
+        """Record a failure; raises in strict mode, otherwise warns once.
+
+        ``Unsupported`` inputs only route the current call to torch: the flag is left alone."""
+        if isinstance(exc, Unsupported):
+            if strict_mode():
+                raise RuntimeError(f"{self.label}: inputs not served by the HIP {what} ({exc}) and strict "
+                                   "mode is enabled.") from exc
+            reason = str(exc)
+            if reason not in self.unsupported_seen:
+                self.unsupported_seen.add(reason)
+                warnings.warn(f"[Qwen-Triton fallback] {self.label}: {reason}. This call uses torch.",
+                              RuntimeWarning, stacklevel=3)
+            return
         self.runtime_ok = False
         if strict_mode():
             raise RuntimeError(f"{self.label} HIP {what} failed and strict mode is enabled.") from exc
@@ -66,6 +86,7 @@ class OpGuard:
     def reset(self) -> None:
         self.runtime_ok = True
         self.warned = False
+        self.unsupported_seen.clear()
 
 
 def needs_grad(*tensors: torch.Tensor | None) -> bool:

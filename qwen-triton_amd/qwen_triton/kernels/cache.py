@@ -9,7 +9,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from ._common import OpGuard
+from ._common import OpGuard, Unsupported
 
 _GUARD = OpGuard("KV cache")
 
@@ -25,7 +25,7 @@ def append_attention_kv(prefix: torch.Tensor | None, suffix: torch.Tensor) -> to
         B, H, so, D = prefix.shape
         sn = suffix.shape[-2]
         if suffix.shape[:2] != prefix.shape[:2] or suffix.shape[-1] != D or suffix.dtype != prefix.dtype:
-            raise ValueError("append_attention_kv shape/dtype mismatch")
+            raise Unsupported("append_attention_kv shape/dtype mismatch")
         pre, suf = prefix.contiguous(), suffix.contiguous()
         out = torch.empty((B, H, so + sn, D), dtype=prefix.dtype, device=prefix.device)
         _native.call("qh_kv_append", pre.data_ptr(), suf.data_ptr(), out.data_ptr(), B, H, so, sn, D,
@@ -50,7 +50,7 @@ def write_attention_kv(cache: torch.Tensor, values: torch.Tensor, positions: tor
     try:
         B, H, S, D = values.shape
         if cache.shape[0] != B or cache.shape[1] != H or cache.shape[3] != D or positions.numel() != S:
-            raise ValueError(f"write_attention_kv shape mismatch: cache {tuple(cache.shape)} values {tuple(values.shape)}")
+            raise Unsupported(f"write_attention_kv shape mismatch: cache {tuple(cache.shape)} values {tuple(values.shape)}")
         if values.dtype != cache.dtype:
             values = values.to(cache.dtype)
         _native.call("qh_kv_write", cache.data_ptr(), *cache.stride(), values.data_ptr(), *values.stride(),

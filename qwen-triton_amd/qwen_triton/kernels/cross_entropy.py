@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from ._common import OpGuard
+from ._common import OpGuard, Unsupported
 
 _GUARD = OpGuard("CrossEntropy")
 
@@ -24,7 +24,7 @@ def _torch_cross_entropy(logits: torch.Tensor, targets: torch.Tensor, ignore_ind
 def _native_ce_forward(logits: torch.Tensor, targets: torch.Tensor, ignore_index: int):
     _native.require_device(logits, targets)
     if logits.dim() != 2:
-        raise ValueError("cross-entropy kernel expects 2-D logits [N, V]")
+        raise Unsupported("cross-entropy kernel expects 2-D logits [N, V]")
     if logits.stride(1) != 1:
         logits = logits.contiguous()
     tg = targets.contiguous().view(-1)
@@ -32,7 +32,7 @@ def _native_ce_forward(logits: torch.Tensor, targets: torch.Tensor, ignore_index
         tg = tg.long()
     N, V = logits.shape
     if tg.numel() != N:
-        raise ValueError("targets must have one entry per logits row")
+        raise Unsupported("targets must have one entry per logits row")
     dev = logits.device
     lse = torch.empty(N, dtype=torch.float32, device=dev)
     rows = torch.empty(N, dtype=torch.float32, device=dev)

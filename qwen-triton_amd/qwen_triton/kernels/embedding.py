@@ -11,7 +11,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from ._common import OpGuard, needs_grad
+from ._common import OpGuard, needs_grad, Unsupported
 
 _GUARD = OpGuard("Embedding")
 
@@ -23,7 +23,7 @@ def _torch_embedding(input_ids: torch.Tensor, weight: torch.Tensor, padding_idx:
 def _native_embedding(input_ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     _native.require_device(input_ids, weight)
     if weight.dim() != 2 or weight.stride(1) != 1:
-        raise ValueError("embedding weight must be a row-major [V, H] matrix")
+        raise Unsupported("embedding weight must be a row-major [V, H] matrix")
     ids = input_ids.contiguous().view(-1)
     if ids.dtype != torch.long:
         ids = ids.long()

@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from ._common import OpGuard
+from ._common import OpGuard, Unsupported
 
 _GUARD = OpGuard("FlashAttention")
 
@@ -30,6 +30,20 @@ def _torch_flash_attention(q, k, v, scale: float, is_causal: bool = True, num_kv
                                                             is_causal=is_causal, scale=scale)
 
 
+def _torch_attention_offset(q, k, v, scale: float, causal: bool, num_kv_groups: int, causal_offset: int):
+    """Torch attention with the kernels' mask rule: key j visible to query i iff j <= i + causal_offset
+    (offset 0 is SDPA's top-left ``is_causal``)."""
+    if not causal or causal_offset == 0:
+        return _torch_flash_attention(q, k, v, scale, causal, num_kv_groups)
+    if num_kv_groups > 1:
+        k = k.repeat_interleave(num_kv_groups, dim=1)
+        v = v.repeat_interleave(num_kv_groups, dim=1)
+    sq, sk = q.shape[2], k.shape[2]
+    keep = (torch.arange(sk, device=q.device)[None, :]
+            <= torch.arange(sq, device=q.device)[:, None] + causal_offset)
+    return torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=keep, dropout_p=0.0, scale=scale)
+
+
 def _unit_last(t: torch.Tensor) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
@@ -37,13 +51,13 @@ def _unit_last(t: torch.Tensor) -> torch.Tensor:
 def _check(q, k, v, num_kv_groups):
     _native.require_device(q, k, v)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
-        raise ValueError("flash attention expects 4-D [B, H, S, D] tensors")
+        raise Unsupported("flash attention expects 4-D [B, H, S, D] tensors")
     if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[3] != k.shape[3]:
-        raise ValueError(f"flash attention shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+        raise Unsupported(f"flash attention shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
     if q.shape[1] != k.shape[1] * num_kv_groups:
-        raise ValueError(f"q heads {q.shape[1]} != kv heads {k.shape[1]} x groups {num_kv_groups}")
+        raise Unsupported(f"q heads {q.shape[1]} != kv heads {k.shape[1]} x groups {num_kv_groups}")
     if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.bfloat16, torch.float16):
-        raise ValueError("flash attention kernel needs bf16 or fp16 q/k/v of one dtype")
+        raise Unsupported("flash attention kernel needs bf16 or fp16 q/k/v of one dtype")
 
 
 def flash_forward(q, k, v, scale: float, causal: bool, num_kv_groups: int, causal_offset: int = 0,
@@ -86,7 +100,7 @@ def flash_decode(q, k, v, scale: float, num_kv_groups: int, seqlens: torch.Tenso
     """Single-query attention over all (or the first ``seqlens[b]``) keys; q [B,Hq,1,D]."""
     _check(q, k, v, num_kv_groups)
     if q.shape[2] != 1:
-        raise ValueError("flash_decode expects one query per sequence")
+        raise Unsupported("flash_decode expects one query per sequence")
     k, v = _unit_last(k), _unit_last(v)
     q = _unit_last(q)
     B, Hq, _, D = q.shape
@@ -96,7 +110,7 @@ def flash_decode(q, k, v, scale: float, num_kv_groups: int, seqlens: torch.Tenso
     if workspace is None or workspace.numel() < need:
         workspace = _native.workspace(need, q.device)
     if seqlens is not None and seqlens.dtype != torch.int32:
-        raise ValueError("seqlens must be int32")
+        raise Unsupported("seqlens must be int32")
     _native.call("qh_flash_decode", q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
                  k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), out.data_ptr(), None,
                  None if seqlens is None else seqlens.data_ptr(), workspace.data_ptr(), workspace.numel(), B, Hq, Hkv,
@@ -125,7 +139,8 @@ class _FlashAttentionFunction(torch.autograd.Function):
             _GUARD.failed(exc, "backward kernel")
             with torch.enable_grad():
                 qq, kk, vv = (t.detach().requires_grad_(True) for t in (q, k, v))
-                ref = _torch_flash_attention(qq, kk, vv, ctx.scale, ctx.is_causal, ctx.num_kv_groups)
+                ref = _torch_attention_offset(qq, kk, vv, ctx.scale, ctx.is_causal, ctx.num_kv_groups,
+                                              ctx.causal_offset)
                 dq, dk, dv = torch.autograd.grad(ref, (qq, kk, vv), grad_output)
         return dq, dk, dv, None, None, None, None
 

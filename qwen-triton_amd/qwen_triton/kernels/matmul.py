@@ -16,7 +16,7 @@ import ctypes
 import torch
 
 from .. import _native
-from ._common import OpGuard, needs_grad
+from ._common import OpGuard, needs_grad, Unsupported
 
 _GUARD = OpGuard("Matmul")
 
@@ -180,10 +180,10 @@ def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torc
 def _native_matmul_forward(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
     _native.require_device(x, weight, bias)
     if x.dtype != weight.dtype or (bias is not None and bias.dtype != weight.dtype):
-        raise ValueError("matmul kernel needs x, weight and bias of one dtype")
+        raise Unsupported("matmul kernel needs x, weight and bias of one dtype")
     N, K = weight.shape
     if x.shape[-1] != K:
-        raise ValueError(f"matmul shape mismatch: x {tuple(x.shape)} weight {tuple(weight.shape)}")
+        raise Unsupported(f"matmul shape mismatch: x {tuple(x.shape)} weight {tuple(weight.shape)}")
     x2 = _rows(x, K)
     w = weight if weight.stride(1) == 1 else weight.contiguous()
     b = None if bias is None else bias.contiguous()

@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from ._common import OpGuard, needs_grad
+from ._common import OpGuard, needs_grad, Unsupported
 
 _GUARD = OpGuard("MoE routing")
 
@@ -37,7 +37,7 @@ def _torch_index_add(target: torch.Tensor, source: torch.Tensor, index: torch.Te
 def _native_topk(x: torch.Tensor, k: int):
     _native.require_device(x)
     if x.dim() != 2:
-        raise ValueError("top-k kernel expects a 2-D [N, C] input")
+        raise Unsupported("top-k kernel expects a 2-D [N, C] input")
     xc = x.contiguous()
     N, C = xc.shape
     vals = torch.empty((N, k), dtype=x.dtype, device=x.device)
@@ -101,9 +101,9 @@ def _native_index_add(target: torch.Tensor, source: torch.Tensor, index: torch.T
     """In place on ``target``; rows of ``index`` outside [0, len(target)) are skipped."""
     _native.require_device(target, source, index)
     if target.dim() != 2 or source.dim() != 2 or target.shape[1] != source.shape[1]:
-        raise ValueError("index_add kernel expects 2-D target/source with equal row width")
+        raise Unsupported("index_add kernel expects 2-D target/source with equal row width")
     if target.stride(1) != 1:
-        raise ValueError("index_add kernel needs a row-major target")
+        raise Unsupported("index_add kernel needs a row-major target")
     src = source if source.stride(1) == 1 else source.contiguous()
     if src.dtype != target.dtype:
         src = src.to(target.dtype)
@@ -112,7 +112,7 @@ def _native_index_add(target: torch.Tensor, source: torch.Tensor, index: torch.T
         idx = idx.long()
     n_src = src.shape[0]
     if idx.numel() != n_src:
-        raise ValueError("index must have one entry per source row")
+        raise Unsupported("index must have one entry per source row")
     ws = _native.workspace(_native.call("qh_index_add_workspace", n_src), target.device)
     _native.call("qh_index_add", target.data_ptr(), target.stride(0), src.data_ptr(), src.stride(0), idx.data_ptr(),
                  n_src, target.shape[0], target.shape[1], ws.data_ptr(), ws.numel(),

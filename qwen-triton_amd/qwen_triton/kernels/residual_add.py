@@ -8,7 +8,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from ._common import OpGuard, needs_grad
+from ._common import OpGuard, needs_grad, Unsupported
 
 _GUARD = OpGuard("ResidualAdd")
 
@@ -20,7 +20,7 @@ def _torch_residual_add(x: torch.Tensor, residual: torch.Tensor) -> torch.Tensor
 def _native_residual_add(x: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
     _native.require_device(x, residual)
     if x.shape != residual.shape or x.dtype != residual.dtype:
-        raise ValueError("residual_add kernel needs equal shapes and dtypes")
+        raise Unsupported("residual_add kernel needs equal shapes and dtypes")
     xc, rc = x.contiguous(), residual.contiguous()
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     _native.call("qh_add", xc.data_ptr(), rc.data_ptr(), out.data_ptr(), out.numel(),

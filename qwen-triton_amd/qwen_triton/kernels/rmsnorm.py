@@ -10,7 +10,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from ._common import OpGuard, needs_grad
+from ._common import OpGuard, needs_grad, Unsupported
 
 _GUARD = OpGuard("RMSNorm")
 
@@ -38,7 +38,7 @@ def _native_rmsnorm(hidden_states: torch.Tensor, weight: torch.Tensor, eps: floa
     _native.require_device(hidden_states, weight)
     cols = hidden_states.shape[-1]
     if weight.numel() != cols:
-        raise ValueError(f"rmsnorm weight has {weight.numel()} elements, expected {cols}")
+        raise Unsupported(f"rmsnorm weight has {weight.numel()} elements, expected {cols}")
     x = hidden_states.contiguous()
     w = weight.contiguous()
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)

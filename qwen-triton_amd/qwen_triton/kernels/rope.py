@@ -14,37 +14,15 @@ from __future__ import annotations
 
 import os
 import warnings
+from typing import Callable
 
 import torch
 
 from .. import _native
 from ..ops import apply_rope_cuda_op, get_rope_cuda_op_error, load_rope_cuda_op
-from ._common import OpGuard
+from ._common import OpGuard, Unsupported
 
 _GUARD = OpGuard("RoPE")
-_CUDA_OP_FALLBACK_WARNED = False
-_TORCH_FALLBACK_WARNED = False
-
-
-def _warn_cuda_op_fallback_once(exc: BaseException) -> None:
-    global _CUDA_OP_FALLBACK_WARNED
-    if _CUDA_OP_FALLBACK_WARNED:
-        return
-    _CUDA_OP_FALLBACK_WARNED = True
-    warnings.warn(
-        f"[Qwen-Triton fallback] RoPE custom op unavailable ({exc.__class__.__name__}: {exc}). "
-        "Using the direct HIP kernel.",
-        RuntimeWarning,
-        stacklevel=3,
-    )
-
-
-def _warn_torch_fallback_once(reason: str) -> None:
-    global _TORCH_FALLBACK_WARNED
-    if _TORCH_FALLBACK_WARNED:
-        return
-    _TORCH_FALLBACK_WARNED = True
-    warnings.warn(f"[Qwen-Triton fallback] {reason}. Using torch fallback.", RuntimeWarning, stacklevel=3)
 
 
 def _torch_apply_rope_tensor(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
@@ -65,13 +43,13 @@ def rope_tensor(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, neg_sin: 
     """One HIP launch of rotate-half RoPE; returns a contiguous [B, H, S, D] tensor."""
     _native.require_device(x, cos, sin)
     if x.dim() != 4 or cos.dim() != 3 or sin.shape != cos.shape:
-        raise ValueError("rope expects x [B,H,S,D] and cos/sin [B or 1, S, rotary_dim]")
+        raise Unsupported("rope expects x [B,H,S,D] and cos/sin [B or 1, S, rotary_dim]")
     B, H, S, D = x.shape
     rot = cos.shape[-1]
     if cos.shape[1] != S or rot > D or rot % 2:
-        raise ValueError(f"rope shape mismatch: x {tuple(x.shape)} cos {tuple(cos.shape)}")
+        raise Unsupported(f"rope shape mismatch: x {tuple(x.shape)} cos {tuple(cos.shape)}")
     if cos.shape[0] not in (1, B):
-        raise ValueError(f"rope cos/sin batch {cos.shape[0]} must be 1 or {B}")
+        raise Unsupported(f"rope cos/sin batch {cos.shape[0]} must be 1 or {B}")
     if sin.stride() != cos.stride():
         sin = sin.contiguous()
         cos = cos.contiguous()
@@ -82,103 +60,146 @@ def rope_tensor(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, neg_sin: 
     return out
 
 
+# ---------------------------------------------------------------------------
+# Backend routing.
+#
+# A requested backend names the accelerated routes to try, in order; torch
+# always ends the list. Routes:
+#   "custom_op"  torch.ops.qwen_triton.rope_tensor_forward, registered by
+#                qwen_triton.ops (it calls the same HIP kernel);
+#   "hip"        rope_tensor, the library kernel called directly.
+# A route flagged `required` may not be skipped under QWEN_TRITON_STRICT=1: if
+# it cannot run, or fails, the call raises RuntimeError. Otherwise the call
+# moves on to the next route, with at most one RuntimeWarning per kind of
+# hand-over in the process. The backward retraces the route the forward took.
+# ---------------------------------------------------------------------------
+_FORWARD_ROUTES: dict[str, tuple[tuple[str, bool], ...]] = {
+    "torch": (),
+    "triton": (("hip", True),),
+    "cuda_op": (("custom_op", True), ("hip", True)),
+    "auto": (("custom_op", False), ("hip", True)),
+}
+# what each route reports as the backend it ran (the reference's names)
+_BACKEND_OF = {"custom_op": "cuda_op", "hip": "triton", "torch": "torch"}
+_BACKWARD_ROUTES = {"cuda_op": _FORWARD_ROUTES["cuda_op"], "triton": _FORWARD_ROUTES["triton"], "torch": ()}
+
+_HANDOVER_WARNED: set[str] = set()
+
+
+def _warn_handover(kind: str, detail: str) -> None:
+    if kind in _HANDOVER_WARNED:
+        return
+    _HANDOVER_WARNED.add(kind)
+    nxt = "the direct HIP kernel" if kind == "custom_op" else "torch"
+    warnings.warn(f"[Qwen-Triton fallback] RoPE {detail}. Using {nxt}.", RuntimeWarning, stacklevel=4)
+
+
 def _resolve_backend(use_triton: bool | None, backend: str | None) -> str:
-    if backend is None:
-        if use_triton is False:
-            return "torch"
-        return os.environ.get("QWEN_TRITON_ROPE_BACKEND", "triton").lower()
-    return backend.lower()
+    """Requested backend: the explicit argument, else torch for use_triton=False, else
+    QWEN_TRITON_ROPE_BACKEND (default "triton")."""
+    if backend is not None:
+        return backend.lower()
+    if use_triton is False:
+        return "torch"
+    return os.environ.get("QWEN_TRITON_ROPE_BACKEND", "triton").lower()
+
+
+def _on_gpu(*tensors: torch.Tensor) -> bool:
+    return all(t.is_cuda for t in tensors)
+
+
+def _custom_op_single(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    return torch.ops.qwen_triton.rope_tensor_forward(x, cos, sin)
+
+
+def _route_unready(route: str, on_gpu: bool) -> str | None:
+    """Why `route` cannot run now (None when it can)."""
+    if not on_gpu:
+        return "inputs are not on the GPU"
+    if route == "custom_op":
+        if load_rope_cuda_op(verbose=os.environ.get("QWEN_TRITON_BUILD_VERBOSE") == "1"):
+            return None
+        return f"custom op unavailable ({get_rope_cuda_op_error()!r})"
+    if not _GUARD.runtime_ok:
+        return "HIP kernel disabled after an earlier failure"
+    if not _native.available():  # GPU inputs never fall back silently for a missing library
+        raise RuntimeError(f"RoPE: the HIP operator library could not be loaded: {_native.load_error()!r}")
+    return None
+
+
+def _run_routes(routes, on_gpu: bool, strict: bool, attempt: Callable[[str], object], what: str):
+    """Try `routes` in order; returns (result, route), or (None, "torch") when torch must compute it."""
+    for route, required in routes:
+        why = _route_unready(route, on_gpu)
+        if why is not None:
+            if strict and required:
+                raise RuntimeError(f"RoPE {what}: {route} route unavailable ({why}) and strict mode is enabled.")
+            if on_gpu and required and route == "custom_op":
+                _warn_handover("custom_op", why)
+            continue
+        try:
+            return attempt(route), route
+        except Exception as exc:
+            if route == "hip":
+                _GUARD.failed(exc, what)  # sticky unless Unsupported; raises in strict mode
+            elif strict and required:
+                raise RuntimeError(f"RoPE {what}: custom op failed and strict mode is enabled.") from exc
+            else:
+                _warn_handover("custom_op", f"custom op failed ({exc.__class__.__name__}: {exc})")
+    if on_gpu and routes:
+        _warn_handover("torch", f"{what}: no accelerated route ran")
+    return None, "torch"
+
+
+def _apply_rope_backend_pair(q, k, cos, sin, requested: str, strict: bool):
+    """Forward over the requested backend's routes; returns ((q_out, k_out), backend that ran)."""
+    routes = _FORWARD_ROUTES.get(requested)
+    if routes is None:
+        raise ValueError(f"Unsupported RoPE backend: {requested}")
+
+    def attempt(route: str):
+        if route == "custom_op":
+            return apply_rope_cuda_op(q, k, cos, sin)
+        return rope_tensor(q, cos, sin), rope_tensor(k, cos, sin)
+
+    out, route = _run_routes(routes, _on_gpu(q, k), strict, attempt, "kernel")
+    if out is None:
+        out = _torch_apply_rope(q, k, cos, sin)
+    return out, _BACKEND_OF[route]
 
 
 def _apply_rope_grad_tensor(grad, cos, sin, backend: str, strict: bool) -> torch.Tensor:
-    if backend == "cuda_op" and grad.is_cuda:
-        if load_rope_cuda_op(verbose=os.environ.get("QWEN_TRITON_BUILD_VERBOSE") == "1"):
-            try:
-                return torch.ops.qwen_triton.rope_tensor_forward(grad.contiguous(), cos, torch.neg(sin))
-            except Exception as exc:
-                if strict:
-                    raise RuntimeError("RoPE custom op backward failed and strict mode is enabled.") from exc
-                _warn_cuda_op_fallback_once(exc)
-        elif strict:
-            raise RuntimeError("RoPE custom op failed to load and strict mode is enabled.") from get_rope_cuda_op_error()
+    """Backward of one tensor (RoPE with -sin, its exact transpose) over the forward's routes."""
 
-    if backend in {"triton", "cuda_op"} and grad.is_cuda and _GUARD.runtime_ok and _native.available():
-        try:
-            return rope_tensor(grad, cos, sin, neg_sin=True)
-        except Exception as exc:
-            _GUARD.runtime_ok = False
-            if strict:
-                raise RuntimeError("RoPE HIP backward failed and strict mode is enabled.") from exc
-            _GUARD.failed(exc, "backward kernel")
+    def attempt(route: str):
+        if route == "custom_op":
+            return _custom_op_single(grad.contiguous(), cos, torch.neg(sin))
+        return rope_tensor(grad, cos, sin, neg_sin=True)
 
-    if strict and backend in {"triton", "cuda_op"} and grad.is_cuda:
-        raise RuntimeError("RoPE backward fast path is unavailable and strict mode is enabled.")
-    if grad.is_cuda and backend != "torch":
-        _warn_torch_fallback_once("RoPE backward fast path is unavailable")
-    return _torch_apply_rope_tensor(grad, cos, torch.neg(sin))
-
-
-def _apply_rope_backend_pair(q, k, cos, sin, resolved_backend: str, strict: bool):
-    if resolved_backend == "torch":
-        return _torch_apply_rope(q, k, cos, sin), "torch"
-    if resolved_backend not in {"auto", "cuda_op", "triton"}:
-        raise ValueError(f"Unsupported RoPE backend: {resolved_backend}")
-
-    if resolved_backend in {"auto", "cuda_op"} and q.is_cuda and k.is_cuda:
-        if load_rope_cuda_op(verbose=os.environ.get("QWEN_TRITON_BUILD_VERBOSE") == "1"):
-            try:
-                return apply_rope_cuda_op(q, k, cos, sin), "cuda_op"
-            except Exception as exc:
-                if strict and resolved_backend == "cuda_op":
-                    raise RuntimeError("RoPE custom op failed and strict mode is enabled.") from exc
-                _warn_cuda_op_fallback_once(exc)
-        elif resolved_backend == "cuda_op":
-            error = get_rope_cuda_op_error()
-            if strict:
-                raise RuntimeError("RoPE custom op failed to load and strict mode is enabled.") from error
-            _warn_cuda_op_fallback_once(error or RuntimeError("unknown custom op load failure"))
-
-    on_gpu = q.is_cuda and k.is_cuda
-    if on_gpu and _GUARD.runtime_ok and not _native.available():
-        raise RuntimeError(f"RoPE: the HIP operator library could not be loaded: {_native.load_error()!r}")
-    if not (on_gpu and _GUARD.runtime_ok):
-        if strict and resolved_backend in {"triton", "auto", "cuda_op"}:
-            raise RuntimeError("RoPE HIP kernel is unavailable and strict mode is enabled.")
-        if on_gpu:
-            _warn_torch_fallback_once("RoPE HIP kernel is unavailable")
-        return _torch_apply_rope(q, k, cos, sin), "torch"
-
-    try:
-        return (rope_tensor(q, cos, sin), rope_tensor(k, cos, sin)), "triton"
-    except Exception as exc:
-        _GUARD.runtime_ok = False
-        if strict:
-            raise RuntimeError("RoPE HIP kernel failed and strict mode is enabled.") from exc
-        _GUARD.failed(exc)
-        return _torch_apply_rope(q, k, cos, sin), "torch"
+    out, _ = _run_routes(_BACKWARD_ROUTES[backend], _on_gpu(grad), strict, attempt, "backward kernel")
+    return out if out is not None else _torch_apply_rope_tensor(grad, cos, torch.neg(sin))
 
 
 class _RoPEPairFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, cos, sin, resolved_backend: str, strict: bool):
+        (qo, ko), ran = _apply_rope_backend_pair(q, k, cos, sin, resolved_backend, strict)
         ctx.save_for_backward(cos, sin)
-        outputs, actual_backend = _apply_rope_backend_pair(q, k, cos, sin, resolved_backend, strict)
-        ctx.actual_backend = actual_backend
-        ctx.strict = strict
-        return outputs
+        ctx.ran, ctx.strict = ran, strict
+        return qo, ko
 
     @staticmethod
     def backward(ctx, grad_q, grad_k):
         cos, sin = ctx.saved_tensors
-        gq = _apply_rope_grad_tensor(grad_q, cos, sin, ctx.actual_backend, ctx.strict) if ctx.needs_input_grad[0] else None
-        gk = _apply_rope_grad_tensor(grad_k, cos, sin, ctx.actual_backend, ctx.strict) if ctx.needs_input_grad[1] else None
+        need_q, need_k = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        gq = _apply_rope_grad_tensor(grad_q, cos, sin, ctx.ran, ctx.strict) if need_q else None
+        gk = _apply_rope_grad_tensor(grad_k, cos, sin, ctx.ran, ctx.strict) if need_k else None
         return gq, gk, None, None, None, None
 
 
 def apply_rope(q, k, cos, sin, use_triton: bool | None = None, backend: str | None = None):
-    resolved_backend = _resolve_backend(use_triton, backend)
+    requested = _resolve_backend(use_triton, backend)
     strict = os.environ.get("QWEN_TRITON_STRICT") == "1"
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad):
-        return _RoPEPairFunction.apply(q, k, cos, sin, resolved_backend, strict)
-    outputs, _ = _apply_rope_backend_pair(q, k, cos, sin, resolved_backend, strict)
-    return outputs
+        return _RoPEPairFunction.apply(q, k, cos, sin, requested, strict)
+    return _apply_rope_backend_pair(q, k, cos, sin, requested, strict)[0]

@@ -8,7 +8,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from ._common import OpGuard, needs_grad
+from ._common import OpGuard, needs_grad, Unsupported
 
 _GUARD = OpGuard("Sigmoid-mul")
 
@@ -28,7 +28,7 @@ def _torch_sigmoid_mul_backward(x: torch.Tensor, gate: torch.Tensor, grad_output
 def _native_sigmoid_mul(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
     _native.require_device(x, gate)
     if x.shape != gate.shape or x.dtype != gate.dtype:
-        raise ValueError("sigmoid_mul kernel needs equal shapes and dtypes")
+        raise Unsupported("sigmoid_mul kernel needs equal shapes and dtypes")
     xc, gc = x.contiguous(), gate.contiguous()
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     _native.call("qh_sigmoid_mul_fwd", xc.data_ptr(), gc.data_ptr(), out.data_ptr(), out.numel(),

@@ -8,7 +8,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native
-from ._common import OpGuard, needs_grad
+from ._common import OpGuard, needs_grad, Unsupported
 
 _GUARD = OpGuard("SiLU-mul")
 
@@ -30,7 +30,7 @@ def _torch_silu_mul_backward(gate: torch.Tensor, up: torch.Tensor, grad_output: 
 def _check(gate: torch.Tensor, up: torch.Tensor) -> None:
     _native.require_device(gate, up)
     if gate.shape != up.shape or gate.dtype != up.dtype:
-        raise ValueError("silu_mul kernel needs equal shapes and dtypes")
+        raise Unsupported("silu_mul kernel needs equal shapes and dtypes")
 
 
 def _native_silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:

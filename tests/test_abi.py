@@ -78,7 +78,9 @@ def test_forced_native_on_cpu_falls_back_with_one_warning(monkeypatch):
         torch.testing.assert_close(out2, out)
         msgs = [str(r.message) for r in rec if "[Qwen-Triton fallback]" in str(r.message)]
         assert len(msgs) == 1
-        assert swiglu._GUARD.runtime_ok is False  # sticky, as in the reference
+        # CPU tensors are inputs the kernels do not take, not a kernel failure: the operator stays on
+        # the kernels for later GPU calls (the reference's flag would stick here)
+        assert swiglu._GUARD.runtime_ok is True
     finally:
         swiglu._GUARD.reset()
 
@@ -104,16 +106,3 @@ def test_missing_library_is_loud_for_gpu_tensors(monkeypatch):
     monkeypatch.setattr(_native, "available", lambda: False)
     with pytest.raises(RuntimeError, match="could not be loaded"):
         guard.use_native(None, FakeCuda())
-
-
-def test_rope_backend_resolution(monkeypatch):
-    from qwen_triton.kernels.rope import _resolve_backend
-
-    monkeypatch.delenv("QWEN_TRITON_ROPE_BACKEND", raising=False)
-    assert _resolve_backend(None, None) == "triton"
-    assert _resolve_backend(False, None) == "torch"
-    monkeypatch.setenv("QWEN_TRITON_ROPE_BACKEND", "CUDA_OP")
-    assert _resolve_backend(None, None) == "cuda_op"
-    with pytest.raises(ValueError):
-        K.apply_rope(torch.randn(1, 1, 2, 4), torch.randn(1, 1, 2, 4), torch.randn(1, 2, 4), torch.randn(1, 2, 4),
-                     backend="bogus")

@@ -691,6 +691,28 @@ def test_flash_decode_over_cache_slice(B, Hq, Hkv, Sk, D):
     close(out, O.attention(q, k, v, D ** -0.5, False, Hq // Hkv)[0], **BF16_TOL)
 
 
+def test_flash_attention_unsupported_call_keeps_later_calls_on_the_kernel(monkeypatch):
+    """A call the kernels do not serve (head dim 132 > 128) runs on torch for that call only; the next
+    bf16 call still launches qh_flash_fwd (the flag is sticky only on a real kernel failure)."""
+    import warnings
+
+    monkeypatch.delenv("QWEN_TRITON_STRICT", raising=False)
+    FA._GUARD.reset()
+    q, k, v = (randn(1, 4, 64, 132, dtype=torch.bfloat16, seed=s) for s in (140, 141, 142))
+    c0 = native_calls("qh_flash_fwd")
+    with warnings.catch_warnings(record=True) as rec:
+        warnings.simplefilter("always")
+        out = K.triton_flash_attention(q, k, v, scale=132 ** -0.5, is_causal=True, num_kv_groups=1)
+    assert native_calls("qh_flash_fwd") == c0
+    assert any("This call uses torch" in str(w.message) for w in rec)
+    close(out, O.attention(q, k, v, 132 ** -0.5, True, 1)[0], **BF16_TOL)
+    assert FA._GUARD.runtime_ok
+    q, k, v = (randn(1, 4, 64, 128, dtype=torch.bfloat16, seed=s) for s in (143, 144, 145))
+    out = K.triton_flash_attention(q, k, v, scale=128 ** -0.5, is_causal=True, num_kv_groups=2 // 2)
+    assert native_calls("qh_flash_fwd") == c0 + 1
+    close(out, O.attention(q, k, v, 128 ** -0.5, True, 1)[0], **BF16_TOL)
+
+
 def test_flash_decode_device_seqlens():
     B, Hq, Hkv, cap, D = 3, 8, 4, 300, 128
     kc = randn(B, Hkv, cap, D, dtype=torch.bfloat16, seed=123)
