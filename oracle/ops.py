@@ -279,6 +279,35 @@ def moe_block(x, gate_w, w_gate, w_up, w_down, top_k, norm_topk_prob=True, route
     return out, logits, weights, experts
 
 
+def moe_block_grads(x, gate_w, w_gate, w_up, w_down, top_k, grad_out, norm_topk_prob=True, dtype=F64,
+                    experts=None):
+    """Gradients of sum(moe_block(x, gate_w, ...) * grad_out) by autograd, through both the experts
+    and the router (softmax, the selected probabilities, their renormalisation, the gate projection).
+    The expert choice is the forward's top-k selection and carries no gradient itself, as in the
+    reference, whose top-k backward scatters only into the selected entries
+    (qwen_triton/kernels/moe_routing.py:147-162). ``experts`` [T, top_k] may fix that choice (a
+    caller comparing against another evaluation whose near-ties could resolve differently).
+    Returns (out, dx, dgate_w, dw_gate, dw_up, dw_down)."""
+    leaves = [_d(t, dtype).requires_grad_(True) for t in (x, gate_w, w_gate, w_up, w_down)]
+    xd, gw, wg, wu, wdn = leaves
+    with torch.enable_grad():
+        probs = torch.softmax(xd @ gw.T, dim=-1)
+        experts = topk(probs, top_k)[1] if experts is None else experts.cpu().long()
+        weights = probs.gather(1, experts)
+        if norm_topk_prob:
+            weights = weights / weights.sum(-1, keepdim=True)
+        out = torch.zeros_like(xd)
+        for e in range(wg.shape[0]):
+            tok, slot = torch.where(experts == e)
+            if tok.numel() == 0:
+                continue
+            xe = xd[tok]
+            h = (torch.nn.functional.silu(xe @ wg[e].T) * (xe @ wu[e].T)) @ wdn[e].T
+            out = out.index_add(0, tok, h * weights[tok, slot, None])
+        (out * _d(grad_out, dtype)).sum().backward()
+    return (out.detach(),) + tuple(t.grad for t in leaves)
+
+
 def rotary_tables(positions, rotary_dim, theta, dtype=torch.float32):
     """cos/sin [1, S, rot] — qwen_triton/modules/rotary.py:10-26 (fp32 tables)."""
     inv = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2, dtype=torch.float32) / rotary_dim))

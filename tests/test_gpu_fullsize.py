@@ -257,3 +257,205 @@ def test_model_decode_step_config3_full_size():
     err = float((got - ref).abs().max())
     band = max(1.5 * noise, 3e-2 * float(ref.abs().max())) + 1e-2
     assert err <= band, f"max|gpu - oracle| = {err:.4f}, bf16 oracle vs fp32 oracle = {noise:.4f}, band {band:.4f}"
+
+
+# ---------------------------------------------------------------------------
+# config 0: Qwen3-0.6B, batch 1, prefill 128 tokens then 32 greedy steps
+# ---------------------------------------------------------------------------
+QWEN3_06B = dict(model_type="qwen3", vocab_size=151936, hidden_size=1024, intermediate_size=3072,
+                 num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8, head_dim=128,
+                 max_position_embeddings=40960, rope_theta=1e6, rms_norm_eps=1e-6, tie_word_embeddings=True)
+
+
+def _qwen06b(seed: int):
+    """The 28-layer Qwen3-0.6B architecture in bf16 on the GPU, weights N(0, 0.02) drawn on the GPU
+    from `seed`, norms 1."""
+    from qwen_triton import QwenTritonConfig, QwenTritonForCausalLM
+
+    cfg = QwenTritonConfig.from_hf_config(dict(QWEN3_06B))
+    model = QwenTritonForCausalLM(cfg, init_weights=False).to(DEV, torch.bfloat16).eval()
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, 0.02, generator=gen)
+    return model, cfg
+
+
+def test_model_config0_full_size_prefill_and_greedy_decode():
+    """Config 0 end to end: prefill 128 seed-0 ids, 32 greedy steps replayed from one captured HIP
+    graph (tokens equal the eager loop's), and the logits of all 160 positions -- 128 from the
+    prefill, 32 from cached decode steps -- against the fp32 CPU oracle, teacher-forced on the
+    generated sequence, in the band the oracle's own bf16 run calibrates."""
+    from oracle.model import ModelSpec, OracleQwen
+
+    model, cfg = _qwen06b(0)
+    V = cfg.vocab_size
+    ids = torch.randint(0, V, (1, 128), generator=torch.Generator().manual_seed(0)).to(DEV)
+    with torch.no_grad():
+        gen_graph = model.greedy_generate(ids, max_new_tokens=32, use_graph=True)
+        gen_eager = model.greedy_generate(ids, max_new_tokens=32)
+    assert gen_graph.shape == (1, 160)
+    assert torch.equal(gen_graph, gen_eager), "graph-replayed greedy tokens differ from the eager loop's"
+    seq = gen_graph
+    cd = native_calls("qh_flash_decode_prepare")
+    with torch.no_grad():
+        cache = model.new_cache(1, 160, torch.bfloat16, DEV)
+        parts = [model(input_ids=seq[:, :128], past_key_values=cache, use_cache=True).logits.float().cpu()]
+        for t in range(128, 160):
+            step = model(input_ids=seq[:, t:t + 1], past_key_values=cache, use_cache=True, logits_to_keep=1)
+            parts.append(step.logits.float().cpu())
+    assert native_calls("qh_flash_decode_prepare") >= cd + 32 * cfg.num_hidden_layers
+    got = torch.cat(parts, dim=1)[0]  # [160, V]
+    params = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    spec = ModelSpec.from_config(cfg)
+    ref = OracleQwen(spec, params, dtype=torch.float32).forward(seq.cpu())[0]
+    ref16 = OracleQwen(spec, params, dtype=torch.bfloat16).forward(seq.cpu())[0].float()
+    noise = float((ref16 - ref).abs().max())
+    err = float((got - ref).abs().max())
+    band = max(1.5 * noise, 3e-2 * float(ref.abs().max())) + 1e-2
+    assert err <= band, f"max|gpu - oracle| = {err:.4f}, bf16 oracle vs fp32 oracle = {noise:.4f}, band {band:.4f}"
+    # each greedy pick is the oracle's best token up to the band (near-ties may resolve either way)
+    for t in range(128, 160):
+        row = ref[t - 1]
+        assert float(row[seq[0, t]]) >= float(row.max()) - band, f"step {t - 128}: token far from the oracle's argmax"
+    print(f"config0: max|d| {err:.4f} (bf16 oracle noise {noise:.4f}, band {band:.4f})")
+
+
+# ---------------------------------------------------------------------------
+# config 4: attention at 30B-A3B shape (32 q-heads / 4 kv-heads, GQA group 8), B4 x S4096, causal
+# ---------------------------------------------------------------------------
+def test_flash_attention_config4_full_size():
+    B, Hq, Hkv, S, D = 4, 32, 4, 4096, 128
+    G = Hq // Hkv
+    scale = D ** -0.5
+    q, k, v, do = _randn((B, Hq, S, D), 51), _randn((B, Hkv, S, D), 52), _randn((B, Hkv, S, D), 53), \
+        _randn((B, Hq, S, D), 54)
+    cf, cb = native_calls("qh_flash_fwd"), native_calls("qh_flash_bwd")
+    o, lse = FA.flash_forward(q, k, v, scale, True, G)
+    dq, dk, dv = FA.flash_backward(q, k, v, o, do, lse, scale, True, G)
+    assert native_calls("qh_flash_fwd") == cf + 1 and native_calls("qh_flash_bwd") == cb + 1
+    visible = torch.ones(S, S, dtype=torch.bool, device=DEV).tril()
+    worst = {"o": 0.0, "lse": 0.0, "dq": 0.0, "dk": 0.0, "dv": 0.0}
+    for b in range(B):
+        for hk in range(Hkv):
+            dk_ref = torch.zeros(S, D, device=DEV)
+            dv_ref = torch.zeros(S, D, device=DEV)
+            kf, vf = k[b, hk].float(), v[b, hk].float()
+            for h in range(hk * G, (hk + 1) * G):
+                qf, dof = q[b, h].float(), do[b, h].float()
+                s = (qf @ kf.t().contiguous()) * scale
+                s.masked_fill_(~visible, float("-inf"))
+                lse_ref = torch.logsumexp(s, dim=-1)
+                p = torch.exp(s - lse_ref[:, None])
+                o_ref = p @ vf
+                ds = p * ((dof @ vf.t().contiguous()) - (dof * o_ref).sum(-1, keepdim=True))
+                worst["o"] = max(worst["o"], _rel_err(o[b, h], o_ref))
+                worst["lse"] = max(worst["lse"], float((lse[b, h] - lse_ref).abs().max()))
+                worst["dq"] = max(worst["dq"], _rel_err(dq[b, h], (ds @ kf) * scale))
+                dk_ref += (ds.t().contiguous() @ qf) * scale
+                dv_ref += p.t().contiguous() @ dof
+            worst["dk"] = max(worst["dk"], _rel_err(dk[b, hk], dk_ref))
+            worst["dv"] = max(worst["dv"], _rel_err(dv[b, hk], dv_ref))
+    print("config4 attention:", worst)
+    assert worst["o"] <= 2e-2 and worst["dq"] <= 2e-2 and worst["dk"] <= 2e-2 and worst["dv"] <= 2e-2, worst
+    assert worst["lse"] <= 1e-3, worst
+
+
+def test_moe_decoder_layer_config4_full_size():
+    """One Qwen3-MoE decoder layer at 30B-A3B shape (hidden 2048, 32/4 heads, 128 experts, top-8,
+    expert intermediate 768) on 4 x 4096 tokens, forward + backward, against an fp32 torch
+    composition of the same layer (RMSNorm, q/k/v, q/k norm, RoPE, causal GQA attention, o_proj,
+    residual, RMSNorm, router softmax + top-8 + renormalisation, per-expert SwiGLU, weighted
+    combine, residual) under autograd. The fp32 composition takes the layer's expert choice, so that
+    near-tied routings cannot flip between the two evaluations."""
+    from qwen_triton import QwenTritonConfig
+    from qwen_triton.models.core import QwenDecoderLayer
+    from qwen_triton.modules.rotary import QwenRotaryEmbedding
+
+    B, S, H, E, K, I, Hq, Hkv, D = 4, 4096, 2048, 128, 8, 768, 32, 4, 128
+    T = B * S
+    cfg = QwenTritonConfig.from_hf_config(dict(
+        model_type="qwen3_moe", vocab_size=151936, hidden_size=H, intermediate_size=6144, num_hidden_layers=1,
+        num_attention_heads=Hq, num_key_value_heads=Hkv, head_dim=D, moe_intermediate_size=I, num_experts=E,
+        num_experts_per_tok=K, norm_topk_prob=True, decoder_sparse_step=1, mlp_only_layers=[]))
+    layer = QwenDecoderLayer(cfg, 0).to(DEV, torch.bfloat16)
+    gen = torch.Generator(device=DEV).manual_seed(61)
+    with torch.no_grad():
+        for n, p in layer.named_parameters():
+            if "norm" in n:
+                p.uniform_(0.8, 1.2, generator=gen)
+            else:
+                p.normal_(0.0, 0.02, generator=gen)
+    blk = layer.mlp
+    chosen = {}
+    route = blk.route
+
+    def recording_route(logits, dtype):
+        w, sel = route(logits, dtype)
+        chosen["sel"] = sel
+        return w, sel
+
+    blk.route = recording_route
+    rot = QwenRotaryEmbedding(cfg).to(DEV)
+    pos = torch.arange(S, device=DEV)[None].expand(B, S)
+    x = _randn((B, S, H), 62).requires_grad_(True)
+    gy = _randn((B, S, H), 63)
+    cos, sin = rot(x, pos)
+    cf, cu = native_calls("qh_flash_bwd"), native_calls("qh_moe_up")
+    y, _ = layer(x, (cos, sin))
+    y.backward(gy)
+    assert native_calls("qh_flash_bwd") == cf + 1 and native_calls("qh_moe_up") == cu + 1
+
+    # fp32 composition with autograd
+    P = {n: p.detach().float().requires_grad_(True) for n, p in layer.named_parameters()}
+    xf = x.detach().float().requires_grad_(True)
+    cf32, sf32 = cos.float(), sin.float()
+    eps = cfg.rms_norm_eps
+
+    def rms(t, w):
+        return t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + eps) * w
+
+    def rope(t):
+        half = D // 2
+        return t * cf32[:, None] + torch.cat((-t[..., half:], t[..., :half]), dim=-1) * sf32[:, None]
+
+    a = "self_attn."
+    h = rms(xf, P["input_layernorm.weight"])
+    q = rms((h @ P[a + "q_proj.weight"].T).view(B, S, Hq, D), P[a + "q_norm.weight"]).transpose(1, 2)
+    k = rms((h @ P[a + "k_proj.weight"].T).view(B, S, Hkv, D), P[a + "k_norm.weight"]).transpose(1, 2)
+    v = (h @ P[a + "v_proj.weight"].T).view(B, S, Hkv, D).transpose(1, 2)
+    q, k = rope(q), rope(k)
+    att = torch.nn.functional.scaled_dot_product_attention(
+        q, k.repeat_interleave(Hq // Hkv, 1), v.repeat_interleave(Hq // Hkv, 1), is_causal=True, scale=D ** -0.5)
+    x1 = xf + att.transpose(1, 2).reshape(B, S, Hq * D) @ P[a + "o_proj.weight"].T
+    h2 = rms(x1, P["post_attention_layernorm.weight"]).view(T, H)
+    probs = torch.softmax(h2 @ P["mlp.gate.weight"].T, dim=-1)
+    sel = chosen["sel"]
+    w = probs.gather(1, sel)
+    w = w / w.sum(-1, keepdim=True)
+    moe = torch.zeros_like(h2)
+    for e in range(E):
+        tok, slot = torch.where(sel == e)
+        if tok.numel() == 0:
+            continue
+        pre = f"mlp.experts.{e}."
+        xe = h2[tok]
+        he = (torch.nn.functional.silu(xe @ P[pre + "gate_proj.weight"].T) * (xe @ P[pre + "up_proj.weight"].T))
+        moe = moe.index_add(0, tok, (he @ P[pre + "down_proj.weight"].T) * w[tok, slot, None])
+    yf = x1 + moe.view(B, S, H)
+    yf.backward(gy.float())
+
+    report = {"y": _rel_err(y, yf), "dx": _rel_err(x.grad, xf.grad)}
+    grads = dict(layer.named_parameters())
+    groups = {"attention weights": [n for n in P if n.startswith(a) and "norm" not in n],
+              "norm weights": [n for n in P if "norm" in n], "router": ["mlp.gate.weight"],
+              "experts": [n for n in P if "experts" in n]}
+    for gname, names in groups.items():
+        report[gname] = max(_rel_err(grads[n].grad, P[n].grad) for n in names)
+    print("config4 layer:", {k2: f"{v2:.3e}" for k2, v2 in report.items()})
+    assert report["y"] <= 2e-2 and report["dx"] <= 3e-2, report
+    assert report["attention weights"] <= 4e-2 and report["router"] <= 4e-2 and report["experts"] <= 4e-2, report
+    assert report["norm weights"] <= 5e-2, report

@@ -247,6 +247,37 @@ def test_moe_block_matches_hf_qwen3_moe():
     torch.testing.assert_close(out.view(2, 7, 32), ref)
 
 
+def test_moe_block_grads_match_hf_qwen3_moe_autograd():
+    """The oracle's MoE gradients (input, router, every expert weight) against autograd through HF's
+    Qwen3MoeSparseMoeBlock (transformers 5.15, fused expert layout) on shared fp64 weights."""
+    from transformers.models.qwen3_moe.configuration_qwen3_moe import Qwen3MoeConfig
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeSparseMoeBlock
+
+    torch.manual_seed(0)
+    I = 16
+    cfg = Qwen3MoeConfig(hidden_size=32, moe_intermediate_size=I, num_experts=6, num_experts_per_tok=2,
+                         norm_topk_prob=True)
+    blk = Qwen3MoeSparseMoeBlock(cfg).double()
+    with torch.no_grad():
+        for p in blk.parameters():
+            p.copy_(torch.randn(p.shape, generator=g(52), dtype=D64) * 0.3)
+    x = rn(2, 9, 32, seed=53).requires_grad_(True)
+    gout = rn(2, 9, 32, seed=54)
+    ref = blk(x)
+    (ref * gout).sum().backward()
+    gu, dn = blk.experts.gate_up_proj, blk.experts.down_proj
+    out, dx, dgw, dwg, dwu, dwd = O.moe_block_grads(x.view(-1, 32), blk.gate.weight, gu[:, :I], gu[:, I:], dn, 2,
+                                                    gout.view(-1, 32), True)
+    tol = dict(atol=1e-6, rtol=1e-5)  # HF takes the router softmax in fp32 even for fp64 weights
+    torch.testing.assert_close(out.view(2, 9, 32), ref.detach(), **tol)
+    torch.testing.assert_close(dx.view(2, 9, 32), x.grad, **tol)
+    torch.testing.assert_close(dgw, blk.gate.weight.grad, **tol)
+    torch.testing.assert_close(dwg, blk.experts.gate_up_proj.grad[:, :I], **tol)
+    torch.testing.assert_close(dwu, blk.experts.gate_up_proj.grad[:, I:], **tol)
+    torch.testing.assert_close(dwd, blk.experts.down_proj.grad, **tol)
+    assert dgw.abs().max() > 1e-3  # the router path carries gradient
+
+
 def test_kv_append_and_residual_add():
     a, b = rn(2, 3, 4, 5, seed=48), rn(2, 3, 2, 5, seed=49)
     out = O.kv_append(a, b)
