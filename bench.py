@@ -228,10 +228,24 @@ def attention_roofline(per_graph=20, replays=5):
 # ---------------------------------------------------------------------------
 # config 0 on the GPU: prefill 128, 32 greedy decode steps, batch 1
 # ---------------------------------------------------------------------------
-def bench_cfg0(model, reps=3):
-    """Config 0 on the GPU: bs1 prefill of 128 tokens and greedy decoding. Per-token decode time is
-    (greedy_generate of 33 tokens - of 3 tokens) / 30, which cancels the prefill and, with
-    ``use_graph=True``, the one-time capture of the decode step."""
+# algorithmic work of config 0 (Qwen3-0.6B, bs1): every weight matrix read once per forward
+# (28 layers x 31.46 MB + the 311.2 MB tied LM head), the KV cache written once (prefill) or read
+# once (decode); prefill flops from the linear layers, attention and the LM head on the last token
+CFG0_WEIGHT_BYTES = 28 * 2 * 1024 * (2048 + 1024 + 1024 + 2048 + 3 * 3072) + 2 * 151936 * 1024
+CFG0_KV_BYTES_PER_POS = 28 * 2 * 8 * 128 * 2
+CFG0_PREFILL_FLOP = 114.95e9
+
+
+def bench_cfg0(model, reps=5):
+    """Config 0 on the GPU: bs1 prefill of 128 tokens and greedy decoding.
+
+    * prefill: a replay of the captured prefill graph (``greedy_graphs``), host-timed around the
+      replay with synchronisations; the eager forward beside it;
+    * decode: per-token time = (generation of 33 tokens - of 3 tokens) / 30 with
+      ``greedy_generate(use_graph=True)``, which cancels the prefill (both graphs are captured
+      beforehand, so no capture is timed);
+    * roofline of each: algorithmic bytes (weights read once, KV written or read once) over the
+      measured time against 8 TB/s, and the prefill's flops against the bf16 MFMA peak."""
     import torch
 
     ids = torch.randint(0, model.config.vocab_size, (1, 128), generator=torch.Generator().manual_seed(0)).cuda()
@@ -245,22 +259,66 @@ def bench_cfg0(model, reps=3):
 
     with torch.no_grad():
         model.greedy_generate(ids, max_new_tokens=3)  # warmup
-        model.greedy_generate(ids, max_new_tokens=3, use_graph=True)
-        pre = []
+        for n in (3, 33):
+            model.greedy_generate(ids, max_new_tokens=n, use_graph=True)  # captures both shapes
+        runner = model.greedy_graphs(1, 128, 33)
+        pre_graph = sorted(timed(lambda: runner.prefill(ids)) for _ in range(reps))[reps // 2]
+        pre_eager = []
         for _ in range(reps):
             cache = model.new_cache(1, 160, torch.bfloat16, "cuda")
-            pre.append(timed(lambda: model(input_ids=ids, past_key_values=cache, use_cache=True,
-                                           logits_to_keep=1).logits[:, -1].argmax(-1)))
+            pre_eager.append(timed(lambda: model(input_ids=ids, past_key_values=cache, use_cache=True,
+                                                 logits_to_keep=1).logits[:, -1].argmax(-1)))
+        pre_eager = sorted(pre_eager)[reps // 2]
         per_tok = {}
         for name, graph in (("eager", False), ("graph", True)):
-            long = min(timed(lambda: model.greedy_generate(ids, max_new_tokens=33, use_graph=graph)) for _ in range(2))
-            short = min(timed(lambda: model.greedy_generate(ids, max_new_tokens=3, use_graph=graph)) for _ in range(2))
+            long = min(timed(lambda: model.greedy_generate(ids, max_new_tokens=33, use_graph=graph)) for _ in range(3))
+            short = min(timed(lambda: model.greedy_generate(ids, max_new_tokens=3, use_graph=graph)) for _ in range(3))
             per_tok[name] = max(long - short, 1e-9) / 30
-    prefill_s = sorted(pre)[len(pre) // 2]
-    return {"prefill_tok_s": round(128 / prefill_s, 1), "decode_tok_s": round(1 / per_tok["graph"], 1),
-            "prefill_ms": round(prefill_s * 1e3, 3), "decode_ms_per_token": round(per_tok["graph"] * 1e3, 3),
+    tok = per_tok["graph"]
+    pre_bytes = CFG0_WEIGHT_BYTES + 128 * CFG0_KV_BYTES_PER_POS
+    dec_bytes = CFG0_WEIGHT_BYTES + 145 * CFG0_KV_BYTES_PER_POS  # mean context of the 30 timed steps
+    pre_gbs = pre_bytes / pre_graph / 1e9
+    dec_gbs = dec_bytes / tok / 1e9
+    return {"prefill_tok_s": round(128 / pre_graph, 1), "prefill_ms": round(pre_graph * 1e3, 3),
+            "prefill_mode": "captured prefill graph replayed (greedy_graphs)",
+            "prefill_eager_ms": round(pre_eager * 1e3, 3),
+            "decode_tok_s": round(1 / tok, 1), "decode_ms_per_token": round(tok * 1e3, 3),
             "decode_mode": "greedy_generate(use_graph=True): captured decode step replayed per token",
-            "eager_decode_tok_s": round(1 / per_tok["eager"], 1)}
+            "eager_decode_tok_s": round(1 / per_tok["eager"], 1),
+            "roofline": {
+                "prefill": {"bound": "hbm", "achieved": round(pre_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(pre_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": pre_bytes,
+                            "mfma_frac": round(CFG0_PREFILL_FLOP / pre_graph / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+                "decode_token": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
+                                 "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+                                 "algorithmic_bytes": dec_bytes}}}
+
+
+def cpu_baseline_cfg0(model, new_tokens=32):
+    """Config 0 on the host cores: the oracle (fp32, HF semantics) prefilling the same 128 ids and
+    greedily decoding ``new_tokens`` steps with its KV cache."""
+    import torch
+
+    from oracle.model import ModelSpec, OracleQwen
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    params = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    orc = OracleQwen(ModelSpec.from_config(model.config), params, dtype=torch.float32)
+    ids = torch.randint(0, model.config.vocab_size, (1, 128), generator=torch.Generator().manual_seed(0))
+    orc.forward(ids[:, :16], orc.new_cache(), logits_to_keep=1)  # warmup
+    cache = orc.new_cache()
+    t0 = time.perf_counter()
+    nxt = orc.forward(ids, cache, logits_to_keep=1)[:, -1].argmax(-1, keepdim=True)
+    t1 = time.perf_counter()
+    for _ in range(new_tokens):
+        nxt = orc.forward(nxt, cache, logits_to_keep=1)[:, -1].argmax(-1, keepdim=True)
+    t2 = time.perf_counter()
+    del params, orc
+    return {"prefill_tok_s": round(128 / (t1 - t0), 1), "decode_tok_s": round(new_tokens / (t2 - t1), 2),
+            "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"oracle fp32 prefill of the 128 ids ({(t1 - t0) * 1e3:.0f} ms) then {new_tokens} greedy steps "
+                      f"({(t2 - t1) * 1e3:.0f} ms), the whole workload"}
 
 
 # ---------------------------------------------------------------------------
@@ -515,6 +573,8 @@ def bench_moe(steps, warmup, loop_reps=1):
     res["layer_fwd_bwd_ms"] = round(ms_layer, 3)
     res["layer_tokens_per_s"] = round(T / ms_layer * 1e3, 1)
 
+    if loop_reps <= 0:
+        return res
     # the reference's per-expert loop (forward + backward), once
     saved = blk._grouped_ok
     blk._grouped_ok = lambda *a, **kw: False
@@ -731,6 +791,7 @@ def main() -> None:
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--gemm-shape", default=None, help="--workload gemm: time only the shape with this label")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true", help="default run: skip the config 1/2/4 keys")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md for how it "
@@ -785,6 +846,22 @@ def main() -> None:
     cpu = None if args.no_cpu_baseline else cpu_baseline(model)
     if cpu:
         log(f"cpu baseline: {cpu}")
+        cfg0["cpu_baseline"] = cpu_baseline_cfg0(model)
+        log(f"config 0 cpu baseline: {cfg0['cpu_baseline']}")
+    del model
+    torch.cuda.empty_cache()
+    others = {}
+    if not args.no_other_configs:
+        # the other BASELINE configs' kernels, timed compactly (HIP events / host clock around synchronised steps)
+        others["config1_fa"] = bench_fa(5, 2)
+        log(f"config 1: {others['config1_fa']}")
+        torch.cuda.empty_cache()
+        others["config2_dense"] = bench_dense(3, 1)
+        log(f"config 2: {others['config2_dense']}")
+        torch.cuda.empty_cache()
+        others["config4_moe"] = bench_moe(3, 1, loop_reps=0)
+        log(f"config 4: {others['config4_moe']}")
+        torch.cuda.empty_cache()
     ms = graph_ms if graph_ms is not None else eager_ms
     line = {
         "metric": METRIC,
@@ -805,6 +882,7 @@ def main() -> None:
         "eager_ms_per_step": round(eager_ms, 4),
         "prefill_tok_s": cfg0["prefill_tok_s"],
         "config0_gpu": cfg0,
+        **others,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

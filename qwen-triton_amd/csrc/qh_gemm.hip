@@ -437,6 +437,172 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   }
 }
 
+// Decode products of at most kGemvMaxRows activation rows (batch-1 and small-
+// batch decode): one wavefront per output column of every product, each wave
+// streaming its weight row over the whole K range with all of a chunk's
+// 16-byte loads in flight (non-temporal: the weights are read once per step),
+// fp32 sums per lane, then a fixed-order xor-tree sum across the wave. The
+// MFMA decode kernel would use 1..4 of its 16 MFMA rows here, and gives each
+// workgroup 16 columns, so o_proj/down (1024 columns) ran on 64 workgroups;
+// this kernel gives every 4 columns a workgroup (256+ for 1024 columns) and
+// measured 2.9-4.1 us for the 4-12 MB config-0 products against 4.8-7.3 us.
+// Same fusions and rounding points as gemm_decode_kernel: NORM (operand
+// round(h * (w + wadd)), row factor rsqrt(mean(h^2) + eps) after the sum),
+// bias, residual round(round(product) + R), GATED silu(round(g)) * round(u).
+constexpr int kGemvMaxRows = 4;
+
+// 16-byte loads per lane and operand row in one chunk (512 K values each).
+__host__ __device__ constexpr int gemv_chunk(int mr, bool gated, int rc) {
+  return rc > 1 ? 2 : (mr == 1 ? (gated ? 4 : 8) : (mr == 2 ? 4 : 2));
+}
+// Columns a wave takes in a single wide product (the LM head): a wave of one
+// column there lives for one memory round trip, and the 152K waves of a
+// vocabulary-wide output then queue for wave slots.
+constexpr int kGemvWideCols = 4;
+constexpr int kGemvWideMin = 32768;
+
+// NB weight rows per column (2: gate and up); RC columns per wave (a single
+// non-gated product; the wave's NB = RC rows are consecutive columns).
+template <typename T, typename OT, int MR, bool GATED, bool NORM, int RC = 1>
+__global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ A, int64_t lda,
+                                                          const DecodeProducts<T, OT> P, const DecodeNorm nrm, int M,
+                                                          int K, int ncols) {
+  static_assert(RC == 1 || !GATED, "a wave takes several columns of one non-gated product only");
+  constexpr int NB = GATED ? 2 : RC;
+  constexpr int CH = gemv_chunk(MR, GATED, RC);
+  typedef typename Mfma<T>::v8 v8;
+  const int lane = threadIdx.x & 63;
+  const int col = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * RC;
+  if (col >= ncols) return;
+  int pi = 0;  // P.tile0 holds the first column of each product here
+  while (pi + 1 < P.count && col >= P.tile0[pi + 1]) ++pi;
+  const int n = col - P.tile0[pi];
+  const T* brow[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int nj = RC > 1 ? min(n + j, P.N[pi] - 1) : n;  // columns past N re-read the last row
+    brow[j] = P.B[pi + (RC > 1 ? 0 : j)] + (int64_t)nj * P.ldb[pi + (RC > 1 ? 0 : j)];
+  }
+  float acc[NB][MR], ss[MR];
+#pragma unroll
+  for (int i = 0; i < MR; ++i) {
+    ss[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j][i] = 0.f;
+  }
+  v8 zero;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
+  for (int k0 = 0; k0 < K; k0 += 512 * CH) {
+    v8 b[CH][NB], a[CH][MR];
+    v8 wr[NORM ? CH : 1];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int k = k0 + u * 512 + lane * 8;
+      const bool kok = k < K;
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        b[u][j] = kok ? __builtin_nontemporal_load(reinterpret_cast<const v8*>(brow[j] + k)) : zero;
+#pragma unroll
+      for (int i = 0; i < MR; ++i)
+        a[u][i] = (kok && i < M) ? *reinterpret_cast<const v8*>(A + (int64_t)i * lda + k) : zero;
+      if constexpr (NORM) wr[u] = kok ? *reinterpret_cast<const v8*>((const T*)nrm.w + k) : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+#pragma unroll
+      for (int i = 0; i < MR; ++i) {
+        if constexpr (NORM) {
+          ss[i] = sumsq8<T>(a[u][i], ss[i]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[u][i][e] = from_f32<T>(to_f32(a[u][i][e]) * (to_f32(wr[u][e]) + nrm.wadd));
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[j][i] += to_f32(b[u][j][e]) * to_f32(a[u][i][e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      if constexpr (NORM) ss[i] += __shfl_xor(ss[i], o);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) acc[j][i] += __shfl_xor(acc[j][i], o);
+    }
+  }
+  // lane i writes row i
+#pragma unroll
+  for (int i = 0; i < MR; ++i) {
+    if (lane != i || i >= M) continue;
+    float v[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      v[j] = acc[j][i];
+      if constexpr (NORM) v[j] *= rsqrtf(ss[i] / (float)K + nrm.eps);
+      const T* bias = P.bias[pi + (RC > 1 ? 0 : j)];
+      v[j] += bias ? to_f32(bias[RC > 1 ? min(n + j, P.N[pi] - 1) : n]) : 0.f;
+    }
+    if constexpr (RC > 1) {
+      const T* res = P.res[pi];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        if (n + j >= P.N[pi]) continue;
+        OT o = from_f32<OT>(v[j]);
+        if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)i * P.ldr[pi] + n + j]));
+        P.C[pi][(int64_t)i * P.ldc[pi] + n + j] = o;
+      }
+    } else if constexpr (GATED) {
+      const float gt = to_f32(from_f32<OT>(v[0])), up = to_f32(from_f32<OT>(v[1]));
+      P.C[pi][(int64_t)i * P.ldc[pi] + n] = from_f32<OT>(gt * sigmoidf_(gt) * up);
+    } else {
+      OT o = from_f32<OT>(v[0]);
+      const T* res = P.res[pi];
+      if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)i * P.ldr[pi] + n]));
+      P.C[pi][(int64_t)i * P.ldc[pi] + n] = o;
+    }
+  }
+}
+
+template <typename T, typename OT>
+void launch_gemv_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int M, int K, bool gated,
+                          const DecodeNorm& nz, hipStream_t st) {
+  const int nprod = gated ? 1 : P.count;  // the gated pair shares its columns
+  P.tile0[0] = 0;
+  for (int i = 0; i < nprod; ++i) P.tile0[i + 1] = P.tile0[i] + P.N[i];
+  if (gated) P.count = 1;
+  const int ncols = P.tile0[nprod];
+  const bool norm = nz.w != nullptr;
+  if (!gated && nprod == 1 && ncols >= kGemvWideMin) {  // a wide single product: several columns per wave
+    const unsigned grid = (unsigned)((ncols + 4 * kGemvWideCols - 1) / (4 * kGemvWideCols));
+#define QH_GW(MRV, NV) gemv_decode_kernel<T, OT, MRV, false, NV, kGemvWideCols><<<grid, 256, 0, st>>>(a, lda, P, nz, M, K, ncols)
+    if constexpr (std::is_same<T, OT>::value) {
+      if (norm) {
+        if (M == 1) QH_GW(1, true); else if (M == 2) QH_GW(2, true); else QH_GW(4, true);
+        return;
+      }
+    }
+    if (M == 1) QH_GW(1, false); else if (M == 2) QH_GW(2, false); else QH_GW(4, false);
+#undef QH_GW
+    return;
+  }
+  const unsigned grid = (unsigned)((ncols + 3) / 4);
+#define QH_GV(MRV, GV, NV) gemv_decode_kernel<T, OT, MRV, GV, NV><<<grid, 256, 0, st>>>(a, lda, P, nz, M, K, ncols)
+#define QH_GV_M(MRV)                                                      \
+  if constexpr (std::is_same<T, OT>::value) {                             \
+    if (norm) {                                                           \
+      if (gated) QH_GV(MRV, true, true); else QH_GV(MRV, false, true);    \
+      return;                                                             \
+    }                                                                     \
+  }                                                                       \
+  if (gated) QH_GV(MRV, true, false); else QH_GV(MRV, false, false);
+  if (M == 1) { QH_GV_M(1) } else if (M == 2) { QH_GV_M(2) } else { QH_GV_M(4) }
+#undef QH_GV_M
+#undef QH_GV
+}
+
 // Returns QH_E_ARG (nothing launched) when a norm prologue is asked for a
 // shape whose K slices do not fit one load chunk (decode_norm_fits).
 template <typename T, typename OT>
@@ -444,9 +610,14 @@ int launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, in
                            hipStream_t st, int ms_force = 0, const DecodeNorm* nrm = nullptr) {
   // Narrow outputs: all 16 waves split K (16 columns per workgroup). Wide
   // outputs already give enough workgroups: 4 column groups x 4 K slices.
+  const bool norm = nrm != nullptr && nrm->w != nullptr;
+  if (M <= kGemvMaxRows && ms_force == 0) {
+    if (norm && !std::is_same<T, OT>::value) return QH_E_ARG;
+    launch_gemv_products<T, OT>(a, lda, P, M, K, gated, norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f}, st);
+    return QH_OK;
+  }
   int maxN = 0;
   for (int i = 0; i < P.count; ++i) maxN = P.N[i] > maxN ? P.N[i] : maxN;
-  const bool norm = nrm != nullptr && nrm->w != nullptr;
   const bool wide = !gated && !norm && maxN > 8192;
   const int ksp = wide ? 4 : 16;
   const int cols = 16 * (16 / ksp);
@@ -492,6 +663,7 @@ int launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, in
 // Whether a norm-prologue launch of M rows, K columns fits (all 16 K slices
 // of every workgroup loaded in one chunk); mirrors launch_decode_products.
 static bool decode_norm_fits(int M, int K, bool gated, int count, const int64_t* N) {
+  if (M <= kGemvMaxRows) return true;  // the one-wave-per-column kernel normalises any K
   const int cols = 16;
   int tiles = 0;
   for (int i = 0; i < (gated ? 1 : count); ++i) tiles += (int)((N[i] + cols - 1) / cols);

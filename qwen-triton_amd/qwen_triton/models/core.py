@@ -237,8 +237,10 @@ class QwenTritonModel(nn.Module):
             past = 0 if past_key_values is None else past_key_values.get_seq_length()
             cache_position = torch.arange(past, past + seq, device=inputs_embeds.device)
             max_position = past + seq - 1
+        rope_bound = None
         if position_ids is None:
             position_ids = cache_position.unsqueeze(0)
+            rope_bound = max_position  # every position id is at most max_position
 
         batch = inputs_embeds.shape[0]
         plain_causal = generated_positions and self._mask_is_trivial(attention_mask)
@@ -254,7 +256,7 @@ class QwenTritonModel(nn.Module):
                                                             window_size=self.config.sliding_window)
 
         hidden = inputs_embeds
-        position_embeddings = self.rotary_emb(hidden, position_ids)
+        position_embeddings = self.rotary_emb(hidden, position_ids, rope_bound)
         router_logits: list[torch.Tensor] = []
         # Inference on GPU: each layer's closing residual add is fused with the next norm.
         chain = add_rmsnorm_ok(hidden, hidden, self.norm.weight)
@@ -388,10 +390,10 @@ class QwenTritonForCausalLM(nn.Module):
                         max_new_tokens: int = 16, use_graph: bool = False) -> torch.LongTensor:
         """Greedy decoding (reference: qwen_triton/models/core.py:378-410).
 
-        ``use_graph=True`` (GPU, bf16/fp16, no padding mask) prefills as usual, then captures one
-        decode step in a HIP graph that reads its cache position and valid lengths from device
-        memory, picks the next token and advances that state itself; the remaining steps are graph
-        replays with no host work in between. With a cache of at most 256 positions the replayed
+        ``use_graph=True`` (GPU, bf16/fp16, no padding mask) runs the prefill and every decode step
+        as replays of two HIP graphs captured once per generation shape (``greedy_graphs``): the
+        step reads its cache position and valid lengths from device memory, picks the next token
+        and advances that state itself, so there is no host work between tokens. With a cache of at most 256 positions the replayed
         steps run the same kernels as the eager loop and give the same tokens; beyond that the
         decode attention plans its key splits for the reserved capacity rather than the current
         length (same tokens within the bf16 band).
@@ -427,49 +429,29 @@ class QwenTritonForCausalLM(nn.Module):
                 and not cfg.attn_output_gate and all(t == "full_attention" for t in cfg.layer_types)
                 and (attention_mask is None or bool((attention_mask == 1).all())))
 
+    def greedy_graphs(self, batch: int, prompt: int, max_new_tokens: int):
+        """The captured-graph runner (``models.graphs.GreedyGraphs``) for this generation shape,
+        created on first use and kept (the four most recent shapes; ``release_graphs`` frees them).
+        Runners are keyed on the parameters' storage too, so replaced parameters get new graphs."""
+        from collections import OrderedDict
+
+        from qwen_triton.models.graphs import GreedyGraphs
+
+        w = self.lm_head.weight
+        key = (batch, prompt, max_new_tokens, w.dtype, w.device, tuple(p.data_ptr() for p in self.parameters()))
+        runners = self.__dict__.setdefault("_graph_runners", OrderedDict())
+        runner = runners.get(key)
+        if runner is None:
+            while len(runners) >= 4:
+                runners.popitem(last=False)
+            runner = runners[key] = GreedyGraphs(self, batch, prompt, max_new_tokens, w.dtype, w.device)
+        runners.move_to_end(key)
+        return runner
+
+    def release_graphs(self) -> None:
+        """Drop the captured generation graphs and their caches."""
+        self.__dict__.pop("_graph_runners", None)
+
     @torch.no_grad()
     def _greedy_generate_graph(self, input_ids: torch.LongTensor, max_new_tokens: int) -> torch.LongTensor:
-        from qwen_triton.kernels.moe_routing import _native_topk
-        from qwen_triton.modules.cache import StaticDecode
-
-        batch, prompt = input_ids.shape
-        dev = input_ids.device
-        cache = self.new_cache(batch, prompt + max_new_tokens, self.lm_head.weight.dtype, dev)
-
-        def pick(logits: torch.Tensor) -> torch.Tensor:
-            # top-1 on the library kernel (ties: lowest index, as argmax)
-            return _native_topk(logits[:, -1], 1)[1]
-
-        first = pick(self(input_ids=input_ids, past_key_values=cache, use_cache=True, logits_to_keep=1).logits)
-        tokens = torch.empty((batch, max_new_tokens), dtype=torch.long, device=dev)
-        tokens[:, :1] = first
-        ids = first.clone()
-        col = torch.ones((1, 1), dtype=torch.long, device=dev)  # next column of ``tokens``
-        cache.static = StaticDecode(positions=torch.full((1,), prompt, dtype=torch.long, device=dev),
-                                    seqlens=torch.full((batch,), prompt + 1, dtype=torch.int32, device=dev))
-
-        def step() -> None:
-            nxt = pick(self(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1).logits)
-            ids.copy_(nxt)
-            tokens.scatter_(1, col.expand(batch, 1), nxt)
-            col.add_(1)
-            cache.static.positions.add_(1)
-            cache.static.seqlens.add_(1)
-
-        try:
-            # the second token eagerly on a side stream (also the capture's warm-up), then one
-            # captured step replayed for the rest
-            side = torch.cuda.Stream(device=dev)
-            side.wait_stream(torch.cuda.current_stream(dev))
-            with torch.cuda.stream(side):
-                step()
-            torch.cuda.current_stream(dev).wait_stream(side)
-            if max_new_tokens > 2:
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph):
-                    step()
-                for _ in range(max_new_tokens - 2):
-                    graph.replay()
-        finally:
-            cache.static = None
-        return torch.cat((input_ids, tokens), dim=-1)
+        return self.greedy_graphs(input_ids.shape[0], input_ids.shape[1], max_new_tokens).generate(input_ids)

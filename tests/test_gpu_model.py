@@ -209,6 +209,25 @@ def test_loader_checkpoint_on_gpu_matches_golden_logits(tmp_path):
         _band(ours, logits)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rotary_table_rows_equal_the_per_call_computation(dtype):
+    """The cached cos/sin table (one gather per forward) gives the same bits as computing cos/sin of
+    the positions directly, at positions up to 40959 and for a batch of position rows."""
+    from qwen_triton.modules.rotary import QwenRotaryEmbedding
+
+    rot = QwenRotaryEmbedding(_cfg(max_position_embeddings=40960)).to("cuda")
+    x = torch.zeros(1, 1, 8, device="cuda", dtype=dtype)
+    pos = torch.cat((torch.arange(0, 300), torch.tensor([2047, 2048, 4095, 40959]))).cuda()[None]
+    c0, s0 = rot(x, pos)
+    c1, s1 = rot(x, pos, max_position=40959)
+    assert torch.equal(c0, c1) and torch.equal(s0, s1)
+    pos2 = torch.randint(0, 5000, (3, 17), generator=torch.Generator().manual_seed(11)).cuda()
+    c0, s0 = rot(x, pos2)
+    c1, s1 = rot(x, pos2, max_position=4999)
+    assert torch.equal(c0, c1) and torch.equal(s0, s1)
+    assert c1.stride() == s1.stride() and c1.stride(-1) == 1
+
+
 def test_moe_block_routing_exact_and_output_close():
     cfg = QwenTritonConfig.from_hf_config(dict(
         model_type="qwen3_moe", vocab_size=64, hidden_size=256, intermediate_size=512, num_hidden_layers=1,
