@@ -409,24 +409,37 @@ def bench_dense(steps, warmup):
     wl = (torch.randn(V, H, device="cuda", generator=g) * 0.02).bfloat16().requires_grad_(True)
     labels = torch.randint(0, V, (T,), device="cuda", generator=g)
 
-    def step():
+    from qwen_triton.kernels import fused_linear_cross_entropy
+
+    def step(fused=False):
         h = MM.triton_matmul(silu_mul(MM.triton_matmul(x, wg), MM.triton_matmul(x, wu)), wd)
-        logits = MM.triton_matmul(h, wl)
-        loss = CE.triton_cross_entropy(logits, labels)
+        if fused:  # LM head + CE without the [16384, 151936] logits (recomputed per vocabulary chunk)
+            loss = fused_linear_cross_entropy(h, wl, labels)
+        else:
+            loss = CE.triton_cross_entropy(MM.triton_matmul(h, wl), labels)
         loss.backward()
         return loss
 
-    for _ in range(warmup):
-        step()
-    sync()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    sync()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
+    res = {}
     flop = 3 * (3 * 2 * T * H * I + 2 * T * H * V)
-    return {"dense_ms_per_step": round(ms, 3), "dense_gemm_tflops": round(flop / ms / 1e9, 1),
-            "dense_gemm_frac_of_step": round(flop / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    for fused in (False, True):
+        for _ in range(warmup):
+            step(fused)
+        sync()
+        torch.cuda.reset_peak_memory_stats()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(fused)
+        sync()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        key = "dense_fused_ce" if fused else "dense"
+        res[f"{key}_ms_per_step"] = round(ms, 3)
+        res[f"{key}_gemm_tflops"] = round(flop / ms / 1e9, 1)
+        res[f"{key}_gemm_frac_of_step"] = round(flop / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)
+        res[f"{key}_peak_mem_gb"] = round(torch.cuda.max_memory_allocated() / 1e9, 2)
+    # the fused backward recomputes the LM-head logits (one more 16384 x 151936 x 1024 product), so its
+    # GEMM flop count is higher than `flop`; the rates above use the unfused count for both
+    return res
 
 
 def bench_gemm(steps, warmup, only=None):

@@ -301,6 +301,42 @@ int64_t qh_gemm_multi_norm_fits(int64_t M, int64_t K, int gated, int count, cons
 int qh_colsum(const void* X, int64_t ldx, int64_t M, int64_t N, void* out, int dtype, int out_dtype,
               void* stream);
 
+/* ---- fused LM head + cross-entropy ---------------------------------------- */
+/* The reference computes logits = TritonLinear(hidden) ([N, V], written to
+ * memory) and then triton_cross_entropy(logits, targets) (README.md:370 of the
+ * reference lists the fused form as its next step). These entry points produce
+ * the same loss and gradients without any [N, V] tensor: the logits exist only
+ * as GEMM tiles, rounded to the activation dtype as the unfused LM head rounds
+ * them.
+ * Replaces, fused, qwen_triton/kernels/matmul.py:130-200 (the LM head product of
+ * qwen_triton/models/core.py:333, tied weights) with
+ * qwen_triton/kernels/cross_entropy.py:55-202 (forward and backward). */
+/* Workspace bytes of qh_lmce_fwd: per-row partials of every 256-column tile,
+ * target logits and per-row losses. */
+int64_t qh_lmce_workspace(int64_t N, int64_t V);
+/* X [N, H] (row stride ldx), W [V, H] (row stride ldw), targets [N] int64.
+ * lse[row] = logsumexp of the row's logits, loss_rows[row] (may be NULL) =
+ * lse - logit[target] (0 for ignore_index rows, NaN for targets outside
+ * [0, V)); *loss_out = sum / max(1, n_valid), *nvalid_out = n_valid (fp32,
+ * fixed-order sums, as qh_ce_fwd). bf16/f16. */
+int qh_lmce_fwd(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets, int64_t N,
+                int64_t V, int64_t H, int64_t ignore_index, float* lse, float* loss_rows, float* loss_out,
+                float* nvalid_out, void* ws, int64_t ws_bytes, int dtype, void* stream);
+/* Logit gradient of the vocabulary columns [v0, v0 + Vc): G[row, j] =
+ * (exp(logit[row, v0 + j] - lse[row]) - [v0 + j == target]) * grad_loss[0] /
+ * max(1, nvalid[0]) in the activation dtype (ignored rows 0), recomputing the
+ * logits of those columns; G [N, Vc] with row stride ldg (Vc % 8 == 0). The
+ * caller forms dW[v0:v0+Vc] = G^T X and dX += G W[v0:v0+Vc] (qh_gemm_acc). */
+int qh_lmce_grad(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets, const float* lse,
+                 const float* grad_loss, const float* nvalid, int64_t N, int64_t v0, int64_t Vc, int64_t H,
+                 int64_t ignore_index, void* G, int64_t ldg, int dtype, void* stream);
+/* C[M,N] += A(M,K) . B(N,K)^T with fp32 C and bf16/f16 operands in the operand
+ * views of qh_gemm (256x256 tile kernel). No counterpart in the reference: the
+ * fixed-order accumulation of the fused cross-entropy's input gradient over
+ * vocabulary chunks. */
+int qh_gemm_acc(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* B,
+                int64_t ldb, float* C, int64_t ldc, int dtype, void* stream);
+
 /* ---- fused attention input preparation (inference) ---------------------- */
 /* One pass over the projected q/k/v rows of B*S tokens (token-major views
  * [B*S, H*D] with row strides sq, sk, sv): per-head RMSNorm of q and k with

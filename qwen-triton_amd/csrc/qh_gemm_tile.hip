@@ -363,8 +363,10 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
 // ---------------------------------------------------------------------------
 // Dense problem: C = A B^T (+ bias), OT output.
 // ---------------------------------------------------------------------------
-template <typename T, typename OT, int BM, int BN, bool AT, bool BT>
+// ACC (fp32 C only): C += A B^T instead of C = A B^T (+ bias).
+template <typename T, typename OT, int BM, int BN, bool AT, bool BT, bool ACC = false>
 struct DenseProblem {
+  static_assert(!ACC || std::is_same<OT, float>::value, "accumulation into fp32 outputs only");
   const T* A;
   const T* B;
   OT* C;
@@ -372,7 +374,7 @@ struct DenseProblem {
   int64_t lda, ldb, ldc;
   int M, N, K, tiles_m, tiles_n;
 
-  static constexpr bool kVecEpilogue = std::is_same<OT, T>::value;
+  static constexpr bool kVecEpilogue = std::is_same<OT, T>::value && !ACC;
   __device__ __forceinline__ bool vec_ok() const { return bias == nullptr; }
   template <class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
@@ -420,13 +422,19 @@ struct DenseProblem {
 #pragma unroll
           for (int g = 0; g < 4; ++g)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) base[(8 * g + r) * ldc] = from_f32<OT>(acc[i][j][4 * g + r] + bv);
+            for (int r = 0; r < 4; ++r) {
+              if constexpr (ACC) base[(8 * g + r) * ldc] += acc[i][j][4 * g + r];
+              else base[(8 * g + r) * ldc] = from_f32<OT>(acc[i][j][4 * g + r] + bv);
+            }
         } else {
 #pragma unroll
           for (int g = 0; g < 4; ++g)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-              if (rb + 8 * g + r < M) base[(8 * g + r) * ldc] = from_f32<OT>(acc[i][j][4 * g + r] + bv);
+              if (rb + 8 * g + r < M) {
+                if constexpr (ACC) base[(8 * g + r) * ldc] += acc[i][j][4 * g + r];
+                else base[(8 * g + r) * ldc] = from_f32<OT>(acc[i][j][4 * g + r] + bv);
+              }
         }
       }
     }
@@ -1012,6 +1020,235 @@ int splitk_layout(int ta, int tb, const T* A, int64_t lda, const T* B, int64_t l
   return splitk_run<T, OT, true, false>(A, lda, B, ldb, C, ldc, bias, M, N, K, S, ws, st);
 }
 
+// ===========================================================================
+// Fused LM head + cross-entropy over vocabulary tiles
+// ===========================================================================
+// Logits S = X W^T (X [N, H] token rows, W [V, H] vocabulary rows, both
+// k-contiguous) are produced tile by tile by the main loop and consumed by
+// the epilogue, rounded to T first (the dtype the unfused LM head writes its
+// logits in), so no [N, V] logits tensor exists.
+//
+// Forward: each 256-column tile of a row becomes one partial (max, sum of
+// exp(s - max)) in a fixed layout part[row][tile]; the tile holding a row's
+// target also stores that logit. Each wavefront stages its 128 x 64 tile; lane
+// l folds rows l and l + 64 (max pass, then sum pass over the 64 values in
+// LDS); the four column waves of a row half then fold their partials through
+// LDS in column order, so a row's partial does not depend on timing.
+__device__ __forceinline__ void lmce_merge(float& m, float& s, float m2, float s2) {
+  const float M = fmaxf(m, m2);
+  if (M == -INFINITY) return;
+  s = (m == -INFINITY ? 0.f : s * __expf(m - M)) + (m2 == -INFINITY ? 0.f : s2 * __expf(m2 - M));
+  m = M;
+}
+
+template <typename T>
+struct LmceFwdProblem {
+  const T* X;
+  const T* W;
+  const int64_t* tgt;
+  float* part;    // [M][tiles_n][2]
+  float* tlogit;  // [M]
+  int64_t ldx, ldw;
+  int M, N, K, tiles_m, tiles_n;
+
+  static constexpr bool kVecEpilogue = true;
+  __device__ __forceinline__ bool vec_ok() const { return true; }
+  __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
+    int tm, tn;
+    tile_order(tiles_m, tiles_n, tm, tn);
+    c.m0 = tm * 256;
+    c.n0 = tn * 256;
+    c.K = K;
+    c.vm = M - c.m0;
+    c.vn = N - c.n0;
+    c.lda = ldx;
+    c.ldb = ldw;
+    c.aux = tn;
+    return true;
+  }
+  __device__ __forceinline__ const T* a_at(const TileCtx<T>& c, int i, int k) const {
+    return X + (int64_t)(c.m0 + i) * ldx + k;
+  }
+  __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
+    return W + (int64_t)(c.n0 + i) * ldw + k;
+  }
+  template <class ET>
+  __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
+    const int ncol = max(0, min(64, c.vn - wc));  // valid columns of this wave's tile
+    float pm[2], ps[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = lane + 64 * h;
+      const int row = c.m0 + wr + r;
+      float m = -INFINITY, sum = 0.f;
+      if (row < M && ncol > 0) {
+#pragma unroll
+        for (int c8 = 0; c8 < 8; ++c8) {
+          const Vec16<T> v = et.row8(r, c8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (8 * c8 + e < ncol) m = fmaxf(m, to_f32(v.v[e]));
+        }
+#pragma unroll
+        for (int c8 = 0; c8 < 8; ++c8) {
+          const Vec16<T> v = et.row8(r, c8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (8 * c8 + e < ncol) sum += __expf(to_f32(v.v[e]) - m);
+        }
+        const int64_t t = tgt[row];
+        const int64_t tc = t - (int64_t)(c.n0 + wc);
+        if (tc >= 0 && tc < ncol) tlogit[row] = to_f32(et.row8(r, (int)(tc >> 3)).v[tc & 7]);
+      }
+      pm[h] = m;
+      ps[h] = sum;
+    }
+    // fold the four column waves of this row half in column order
+    const int wm = wr / 128, wn = wc / 64;
+    float* mine = reinterpret_cast<float*>(et.base);  // this wave's staging area, reads above are done
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      mine[2 * (lane + 64 * h)] = pm[h];
+      mine[2 * (lane + 64 * h) + 1] = ps[h];
+    }
+    __syncthreads();
+    if (wn != 0) return;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = lane + 64 * h;
+      const int row = c.m0 + wr + r;
+      float m = -INFINITY, sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float* other = reinterpret_cast<const float*>(et.base + w * 128 * 64);  // wave (wm, w)
+        lmce_merge(m, sum, other[2 * r], other[2 * r + 1]);
+      }
+      if (row < M) {
+        float* o = part + ((int64_t)row * tiles_n + c.aux) * 2;
+        o[0] = m;
+        o[1] = sum;
+      }
+    }
+    (void)wm;
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ void epilogue(const TileCtx<T>&, const f32x16 (&)[TM][TN], int, int, int) const {}
+};
+
+// Backward of one vocabulary chunk [v0, v0 + N): recomputes its logits and
+// writes G[row][col] = (exp(s - lse[row]) - [v0 + col == target]) * g / n_valid
+// in T (ignored rows 0), the unfused cross-entropy backward's values for
+// these columns.
+template <typename T>
+struct LmceGradProblem {
+  const T* X;
+  const T* W;  // first row = vocabulary entry v0
+  const int64_t* tgt;
+  const float* lse;
+  const float* gloss;
+  const float* nvalid;
+  T* G;
+  int64_t ldx, ldw, ldg, v0, ignore;
+  int M, N, K, tiles_m, tiles_n;
+
+  static constexpr bool kVecEpilogue = true;
+  __device__ __forceinline__ bool vec_ok() const { return true; }
+  __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
+    int tm, tn;
+    tile_order(tiles_m, tiles_n, tm, tn);
+    c.m0 = tm * 256;
+    c.n0 = tn * 256;
+    c.K = K;
+    c.vm = M - c.m0;
+    c.vn = N - c.n0;
+    c.lda = ldx;
+    c.ldb = ldw;
+    c.aux = 0;
+    return true;
+  }
+  __device__ __forceinline__ const T* a_at(const TileCtx<T>& c, int i, int k) const {
+    return X + (int64_t)(c.m0 + i) * ldx + k;
+  }
+  __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
+    return W + (int64_t)(c.n0 + i) * ldw + k;
+  }
+  template <class ET>
+  __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
+    const float scale = gloss[0] / fmaxf(nvalid[0], 1.f);
+    for (int q = lane; q < 128 * 8; q += 64) {
+      const int r = q >> 3, c8 = q & 7;
+      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
+      if (row >= M || col >= N) continue;
+      const int64_t t = tgt[row];
+      Vec16<T> o;
+      if (t == ignore) {
+        o.raw = make_uint4(0, 0, 0, 0);
+      } else {
+        const Vec16<T> v = et.row8(r, c8);
+        const float l = lse[row];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pr = __expf(to_f32(v.v[e]) - l);
+          o.v[e] = from_f32<T>((pr - (v0 + col + e == t ? 1.f : 0.f)) * scale);
+        }
+      }
+      st16(G + (int64_t)row * ldg + col, o);
+    }
+  }
+  template <int TM, int TN>
+  __device__ __forceinline__ void epilogue(const TileCtx<T>&, const f32x16 (&)[TM][TN], int, int, int) const {}
+};
+
+// lse[row] from the row's tile partials (tile order), loss_rows[row] =
+// lse - target logit (0 for ignored rows, NaN for targets outside [0, V)).
+__global__ __launch_bounds__(256) void lmce_combine_kernel(const float* __restrict__ part,
+                                                           const float* __restrict__ tlogit,
+                                                           const int64_t* __restrict__ tgt, int64_t N, int tiles,
+                                                           int64_t V, int64_t ignore, float* __restrict__ lse,
+                                                           float* __restrict__ loss_rows) {
+  const int64_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= N) return;
+  // lanes fold interleaved tiles, then a fixed xor tree
+  float m = -INFINITY, s = 0.f;
+  for (int t = lane; t < tiles; t += 64) lmce_merge(m, s, part[(row * tiles + t) * 2], part[(row * tiles + t) * 2 + 1]);
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+    lmce_merge(m, s, m2, s2);
+  }
+  if (lane == 0) {
+    const int64_t t = tgt[row];
+    const float l = m + __logf(s);
+    if (t == ignore) {
+      lse[row] = 0.f;
+      loss_rows[row] = 0.f;
+    } else {
+      lse[row] = l;
+      loss_rows[row] = (t >= 0 && t < V) ? l - tlogit[row] : __int_as_float(0x7fc00000);
+    }
+  }
+}
+
+// loss_out = sum(loss_rows) / max(1, n_valid) (fixed order), nvalid_out = n_valid.
+__global__ __launch_bounds__(1024) void lmce_finalize_kernel(const float* __restrict__ loss_rows,
+                                                             const int64_t* __restrict__ tgt, int64_t N,
+                                                             int64_t ignore, float* __restrict__ loss_out,
+                                                             float* __restrict__ nvalid_out) {
+  __shared__ float red[16];
+  float s = 0.f, n = 0.f;
+  for (int64_t i = threadIdx.x; i < N; i += 1024) {
+    s += loss_rows[i];
+    n += (tgt[i] != ignore) ? 1.f : 0.f;
+  }
+  s = block_sum(s, red);
+  n = block_sum(n, red);
+  if (threadIdx.x == 0) {
+    loss_out[0] = s / fmaxf(n, 1.f);
+    nvalid_out[0] = n;
+  }
+}
+
 }  // namespace
 
 // Large-tile path of qh_gemm (called by its dispatcher; not part of the C ABI).
@@ -1267,4 +1504,146 @@ int qh_gemm_splitk_dispatch(int ta, int tb, int M, int N, int K, const void* A, 
 #undef QH_SK_OUT
   qh::set_error("qh_gemm: the split-K path takes bf16/f16 operands");
   return QH_E_DTYPE;
+}
+
+// ===========================================================================
+// C ABI: fused LM head + cross-entropy, fp32 accumulating GEMM
+// ===========================================================================
+namespace {
+constexpr int kLmceTile = 256;
+int64_t lmce_tiles(int64_t V) { return (V + kLmceTile - 1) / kLmceTile; }
+}  // namespace
+
+extern "C" int64_t qh_lmce_workspace(int64_t N, int64_t V) {
+  if (N <= 0 || V <= 0) return 0;
+  return N * lmce_tiles(V) * 2 * 4 + 2 * N * 4;  // tile partials, target logits, per-row losses
+}
+
+extern "C" int qh_lmce_fwd(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets, int64_t N,
+                           int64_t V, int64_t H, int64_t ignore_index, float* lse, float* loss_rows, float* loss_out,
+                           float* nvalid_out, void* ws, int64_t ws_bytes, int dtype, void* stream) {
+  QH_CHECK_ARG(N >= 0 && V > 0 && H > 0 && N < (1ll << 31) && V < (1ll << 31) && H < (1ll << 31),
+               "qh_lmce_fwd: bad shape N=%lld V=%lld H=%lld", (long long)N, (long long)V, (long long)H);
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_lmce_fwd: bf16/f16 only");
+  QH_CHECK_ARG(aligned16(X) && aligned16(W) && ldx % 8 == 0 && ldw % 8 == 0 && H % 8 == 0 && ldx >= H && ldw >= H,
+               "qh_lmce_fwd: X and W must be 16-byte aligned k-contiguous rows with H, ldx, ldw multiples of 8");
+  QH_CHECK_ARG(ws_bytes >= qh_lmce_workspace(N, V), "qh_lmce_fwd: workspace %lld < %lld", (long long)ws_bytes,
+               (long long)qh_lmce_workspace(N, V));
+  if (N == 0) return qh_zero(loss_out, 4, stream) || qh_zero(nvalid_out, 4, stream);
+  hipStream_t st = (hipStream_t)stream;
+  const int tiles_n = (int)lmce_tiles(V);
+  float* part = (float*)ws;
+  float* tlog = part + N * tiles_n * 2;
+  float* rows = loss_rows ? loss_rows : tlog + N;
+  int rc = QH_OK;
+#define QH_LMCE(TT)                                                                              \
+  {                                                                                              \
+    LmceFwdProblem<TT> p;                                                                        \
+    p.X = (const TT*)X;                                                                          \
+    p.W = (const TT*)W;                                                                          \
+    p.tgt = targets;                                                                             \
+    p.part = part;                                                                               \
+    p.tlogit = tlog;                                                                             \
+    p.ldx = ldx;                                                                                 \
+    p.ldw = ldw;                                                                                 \
+    p.M = (int)N;                                                                                \
+    p.N = (int)V;                                                                                \
+    p.K = (int)H;                                                                                \
+    p.tiles_m = (int)((N + 255) / 256);                                                          \
+    p.tiles_n = tiles_n;                                                                         \
+    rc = launch_tile<TT, 256, 256, kDenseBK, kDenseNS, false, false>(p, p.tiles_m * p.tiles_n, st, "qh_lmce_fwd"); \
+  }
+  if (dtype == QH_BF16) QH_LMCE(bf16_t) else QH_LMCE(f16_t)
+#undef QH_LMCE
+  if (rc) return rc;
+  lmce_combine_kernel<<<(unsigned)((N + 3) / 4), 256, 0, st>>>(part, tlog, targets, N, tiles_n, V, ignore_index, lse,
+                                                               rows);
+  lmce_finalize_kernel<<<1, 1024, 0, st>>>(rows, targets, N, ignore_index, loss_out, nvalid_out);
+  QH_CHECK_LAUNCH("qh_lmce_fwd");
+  return QH_OK;
+}
+
+extern "C" int qh_lmce_grad(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets,
+                            const float* lse, const float* grad_loss, const float* nvalid, int64_t N, int64_t v0,
+                            int64_t Vc, int64_t H, int64_t ignore_index, void* G, int64_t ldg, int dtype,
+                            void* stream) {
+  QH_CHECK_ARG(N >= 0 && Vc > 0 && H > 0 && v0 >= 0 && N < (1ll << 31) && Vc < (1ll << 31) && H < (1ll << 31),
+               "qh_lmce_grad: bad shape");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_lmce_grad: bf16/f16 only");
+  QH_CHECK_ARG(aligned16(X) && aligned16(W) && aligned16(G) && ldx % 8 == 0 && ldw % 8 == 0 && ldg % 8 == 0 &&
+                   H % 8 == 0 && Vc % 8 == 0 && ldx >= H && ldw >= H && ldg >= Vc,
+               "qh_lmce_grad: 16-byte aligned operands with H, Vc, ldx, ldw, ldg multiples of 8 required");
+  if (N == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  int rc = QH_OK;
+#define QH_LMCEG(TT)                                                                             \
+  {                                                                                              \
+    LmceGradProblem<TT> p;                                                                       \
+    p.X = (const TT*)X;                                                                          \
+    p.W = (const TT*)W + v0 * ldw;                                                               \
+    p.tgt = targets;                                                                             \
+    p.lse = lse;                                                                                 \
+    p.gloss = grad_loss;                                                                         \
+    p.nvalid = nvalid;                                                                           \
+    p.G = (TT*)G;                                                                                \
+    p.ldx = ldx;                                                                                 \
+    p.ldw = ldw;                                                                                 \
+    p.ldg = ldg;                                                                                 \
+    p.v0 = v0;                                                                                   \
+    p.ignore = ignore_index;                                                                     \
+    p.M = (int)N;                                                                                \
+    p.N = (int)Vc;                                                                               \
+    p.K = (int)H;                                                                                \
+    p.tiles_m = (int)((N + 255) / 256);                                                          \
+    p.tiles_n = (int)((Vc + 255) / 256);                                                         \
+    rc = launch_tile<TT, 256, 256, kDenseBK, kDenseNS, false, false>(p, p.tiles_m * p.tiles_n, st, "qh_lmce_grad"); \
+  }
+  if (dtype == QH_BF16) QH_LMCEG(bf16_t) else QH_LMCEG(f16_t)
+#undef QH_LMCEG
+  if (rc) return rc;
+  QH_CHECK_LAUNCH("qh_lmce_grad");
+  return QH_OK;
+}
+
+extern "C" int qh_gemm_acc(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                           const void* B, int64_t ldb, float* C, int64_t ldc, int dtype, void* stream) {
+  QH_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31),
+               "qh_gemm_acc: bad shape");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_gemm_acc: bf16/f16 operands only");
+  QH_CHECK_ARG(ldc >= N && (trans_a ? lda >= M : lda >= K) && (trans_b ? ldb >= N : ldb >= K),
+               "qh_gemm_acc: leading dimensions too small");
+  QH_CHECK_ARG(aligned16(A) && aligned16(B) && lda % 8 == 0 && ldb % 8 == 0 && (trans_a ? M % 8 == 0 : K % 8 == 0) &&
+                   (trans_b ? N % 8 == 0 : K % 8 == 0),
+               "qh_gemm_acc: 16-byte aligned operands with contiguous extents and strides multiples of 8 required");
+  if (M == 0 || N == 0 || K == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  int rc = QH_OK;
+#define QH_ACC_L(TT, ATV, BTV)                                                                        \
+  {                                                                                                   \
+    DenseProblem<TT, float, 256, 256, ATV, BTV, true> p;                                              \
+    p.A = (const TT*)A;                                                                               \
+    p.B = (const TT*)B;                                                                               \
+    p.C = C;                                                                                          \
+    p.bias = nullptr;                                                                                 \
+    p.lda = lda;                                                                                      \
+    p.ldb = ldb;                                                                                      \
+    p.ldc = ldc;                                                                                      \
+    p.M = (int)M;                                                                                     \
+    p.N = (int)N;                                                                                     \
+    p.K = (int)K;                                                                                     \
+    p.tiles_m = (int)((M + 255) / 256);                                                               \
+    p.tiles_n = (int)((N + 255) / 256);                                                               \
+    rc = launch_tile<TT, 256, 256, kDenseBK, kDenseNS, ATV, BTV>(p, p.tiles_m * p.tiles_n, st, "qh_gemm_acc"); \
+  }
+#define QH_ACC(TT)                                               \
+  if (!trans_a && !trans_b) QH_ACC_L(TT, false, false)           \
+  else if (!trans_a && trans_b) QH_ACC_L(TT, false, true)        \
+  else if (trans_a && trans_b) QH_ACC_L(TT, true, true)          \
+  else QH_ACC_L(TT, true, false)
+  if (dtype == QH_BF16) { QH_ACC(bf16_t) } else { QH_ACC(f16_t) }
+#undef QH_ACC
+#undef QH_ACC_L
+  if (rc) return rc;
+  QH_CHECK_LAUNCH("qh_gemm_acc");
+  return QH_OK;
 }

@@ -6,6 +6,7 @@ from .cross_entropy import triton_cross_entropy
 from .embedding import triton_embedding
 from .flash_attention import triton_flash_attention
 from .linear_attention import gated_delta_rule_sequence
+from .linear_cross_entropy import fused_linear_cross_entropy
 from .matmul import triton_matmul
 from .moe_routing import triton_index_add, triton_one_hot, triton_topk
 from .residual_add import residual_add
@@ -22,6 +23,7 @@ __all__ = [
     "triton_embedding",
     "triton_flash_attention",
     "gated_delta_rule_sequence",
+    "fused_linear_cross_entropy",
     "triton_matmul",
     "triton_index_add",
     "triton_one_hot",

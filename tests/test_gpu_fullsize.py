@@ -459,3 +459,35 @@ def test_moe_decoder_layer_config4_full_size():
     assert report["y"] <= 2e-2 and report["dx"] <= 3e-2, report
     assert report["attention weights"] <= 4e-2 and report["router"] <= 4e-2 and report["experts"] <= 4e-2, report
     assert report["norm weights"] <= 5e-2, report
+
+
+# ---------------------------------------------------------------------------
+# config 2: the fused LM head + cross-entropy at 16384 tokens x 151936 classes
+# ---------------------------------------------------------------------------
+def test_fused_lm_head_cross_entropy_config2_full_size():
+    """Loss, dX and dW of fused_linear_cross_entropy at config 2's LM-head shape against fp32 torch
+    (logits in fp32 from the same bf16 inputs) and against the unfused HIP path; each dW row block of a
+    vocabulary chunk is written once, dX accumulates over the 19 chunks in order."""
+    T, H, V = 16384, 1024, 151936
+    x0 = _randn((T, H), 71)
+    w0 = _randn((V, H), 72, scale=0.02)
+    t = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(73)).to(DEV)
+    x, w = x0.clone().requires_grad_(True), w0.clone().requires_grad_(True)
+    loss = K.fused_linear_cross_entropy(x, w, t)
+    loss.backward()
+    # fp32 reference
+    xf, wf = x0.float().requires_grad_(True), w0.float().requires_grad_(True)
+    lf = torch.nn.functional.cross_entropy(xf @ wf.t().contiguous(), t)
+    lf.backward()
+    assert abs(float(loss) - float(lf)) <= 2e-3 * abs(float(lf)), (float(loss), float(lf))
+    _check(x.grad, xf.grad, 3e-2, "dX vs fp32")
+    _check(w.grad, wf.grad, 3e-2, "dW vs fp32")
+    del xf, wf, lf
+    torch.cuda.empty_cache()
+    # unfused HIP path (logits materialised)
+    xu, wu = x0.clone().requires_grad_(True), w0.clone().requires_grad_(True)
+    lu = K.triton_cross_entropy(K.triton_matmul(xu, wu), t)
+    lu.backward()
+    assert abs(float(loss) - float(lu)) <= 1e-5 * abs(float(lu))
+    _check(x.grad, xu.grad, 1e-2, "dX vs unfused")
+    _check(w.grad, wu.grad, 1e-2, "dW vs unfused")
