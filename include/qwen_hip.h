@@ -301,6 +301,24 @@ int64_t qh_gemm_multi_norm_fits(int64_t M, int64_t K, int gated, int count, cons
 int qh_colsum(const void* X, int64_t ldx, int64_t M, int64_t N, void* out, int dtype, int out_dtype,
               void* stream);
 
+/* ---- gated delta rule (Qwen3-Next / Qwen3.5 linear attention) ------------ */
+/* Whole-sequence recurrence per (b, head): with the fp32 state S [K, Vd]
+ * (state_in, or zeros when NULL), for t = 0..S-1: S *= exp(g[b,t,h]);
+ * d = (v_t - S^T k_t) * beta[b,t,h]; S += k_t d^T; out[b,t,h,:] = S^T q'_t
+ * with q'_t = q_t * scale rounded to the dtype (output rounded to the dtype). q/k [B,S,H,K] share strides (sqb, sqs, sqh),
+ * v [B,S,H,Vd] (svb, svs, svh), out (sob, sos, soh), all with unit last
+ * stride; g and beta fp32 [B,S,H] with strides (sgb, sgs, sgh); state_out
+ * (may be NULL) receives the final fp32 state [B,H,K,Vd] (contiguous, as
+ * state_in). K <= 128. One launch for the whole sequence.
+ * Replaces qwen_triton/kernels/linear_attention.py:54-101
+ * (_gated_delta_rule_step_kernel, one launch per token) and the token loop of
+ * :130-189 (gated_delta_rule_sequence). */
+int qh_gated_delta_rule(const void* q, const void* k, int64_t sqb, int64_t sqs, int64_t sqh, const void* v,
+                        int64_t svb, int64_t svs, int64_t svh, const float* g, const float* beta, int64_t sgb,
+                        int64_t sgs, int64_t sgh, const float* state_in, float* state_out, void* out, int64_t sob,
+                        int64_t sos, int64_t soh, int64_t B, int64_t S, int64_t H, int64_t K, int64_t Vd,
+                        float scale, int dtype, void* stream);
+
 /* ---- fused LM head + cross-entropy ---------------------------------------- */
 /* The reference computes logits = TritonLinear(hidden) ([N, V], written to
  * memory) and then triton_cross_entropy(logits, targets) (README.md:370 of the

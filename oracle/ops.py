@@ -308,6 +308,28 @@ def moe_block_grads(x, gate_w, w_gate, w_up, w_down, top_k, grad_out, norm_topk_
     return (out.detach(),) + tuple(t.grad for t in leaves)
 
 
+# ---------------------------------------------------------------------------
+# Gated delta rule — qwen_triton/kernels/linear_attention.py:35-51 (step) and :130-189 (sequence)
+# ---------------------------------------------------------------------------
+def gated_delta_rule(q, k, v, g, beta, initial_state=None, dtype=F64):
+    """q/k [B,S,H,K], v [B,S,H,V], g/beta [B,S,H] -> (out [B,S,H,V], final state [B,H,K,V]).
+
+    The query is scaled by K^-0.5 in its own dtype first (as the reference does), then, per token,
+    S = S exp(g); d = (v - S^T k) beta; S += k d^T; o = S^T q."""
+    B, S, H, K = q.shape
+    q = (q * (K ** -0.5)).detach().to("cpu", dtype)
+    k, v, g, beta = (_d(t, dtype) for t in (k, v, g, beta))
+    st = torch.zeros(B, H, K, v.shape[-1], dtype=dtype) if initial_state is None else _d(initial_state, dtype)
+    out = torch.zeros(B, S, H, v.shape[-1], dtype=dtype)
+    for t in range(S):
+        st = st * g[:, t].exp()[:, :, None, None]
+        kv = (st * k[:, t, :, :, None]).sum(dim=-2)
+        d = (v[:, t] - kv) * beta[:, t, :, None]
+        st = st + k[:, t, :, :, None] * d[:, :, None, :]
+        out[:, t] = (st * q[:, t, :, :, None]).sum(dim=-2)
+    return out, st
+
+
 def rotary_tables(positions, rotary_dim, theta, dtype=torch.float32):
     """cos/sin [1, S, rot] — qwen_triton/modules/rotary.py:10-26 (fp32 tables)."""
     inv = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2, dtype=torch.float32) / rotary_dim))

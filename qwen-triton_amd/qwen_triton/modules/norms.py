@@ -22,7 +22,9 @@ class QwenRMSNorm(nn.Module):
 
 
 class QwenRMSNormGated(nn.Module):
-    """Gated RMSNorm of the Qwen3-Next linear-attention block (kept for API parity)."""
+    """RMSNorm of the linear-attention output gated by SiLU(gate) (Qwen3-Next / Qwen3.5):
+    silu(gate) * rmsnorm(x) * weight, the norm in fp32 with one rounding (the RMSNorm kernel), then
+    the SiLU-mul kernel (reference: qwen_triton/modules/norms.py:24-36)."""
 
     def __init__(self, hidden_size: int, eps: float = 1e-6) -> None:
         super().__init__()
@@ -30,8 +32,5 @@ class QwenRMSNormGated(nn.Module):
         self.eps = eps
 
     def forward(self, hidden_states: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
-        dtype = hidden_states.dtype
-        x = hidden_states.to(torch.float32)
-        x = x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + self.eps)
-        x = self.weight.to(torch.float32) * x
-        return silu_mul(gate.to(dtype), x.to(dtype))
+        normed = rmsnorm(hidden_states, self.weight, eps=self.eps)
+        return silu_mul(gate.to(normed.dtype), normed)

@@ -479,3 +479,26 @@ def test_config0_like_decode_takes_fused_prepare():
             steps.append(m(input_ids=eager[:, t:t + 1], past_key_values=p.past_key_values, use_cache=True).logits[:, -1])
     ref = OracleQwen(ModelSpec.from_config(cfg), m.state_dict(), dtype=torch.float32).forward(eager[:, :-1].cpu())
     _band(torch.stack(steps, 1).float().cpu(), ref[:, 19:])
+
+
+def test_qwen3_next_model_on_gpu_matches_golden_logits():
+    """The golden Qwen3-Next model in bf16 on the GPU (linear-attention layers on the gated-delta
+    kernel, gated full attention on flash attention): logits within the bf16 band of HF's, and
+    token-by-token decoding through the caches within the band of the full forward."""
+    from test_model_cpu import _next_model
+
+    model, ids, logits = _next_model()
+    model = model.to("cuda", torch.bfloat16)
+    ids = ids.cuda()
+    c0 = _native.CALLS["qh_gated_delta_rule"]
+    with torch.no_grad():
+        ours = model(input_ids=ids, use_cache=False).logits
+        assert _native.CALLS["qh_gated_delta_rule"] == c0 + 2  # two linear-attention layers
+        _band(ours, logits)
+        out = model(input_ids=ids[:, :5], use_cache=True)
+        cache, steps = out.past_key_values, [out.logits]
+        for t in range(5, ids.shape[1]):
+            o = model(input_ids=ids[:, t:t + 1], past_key_values=cache, use_cache=True)
+            cache = o.past_key_values
+            steps.append(o.logits)
+    _band(torch.cat(steps, dim=1), logits)

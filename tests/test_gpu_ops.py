@@ -1101,3 +1101,39 @@ def test_fused_linear_cross_entropy_all_rows_ignored():
     loss.backward()
     assert float(loss) == 0.0
     assert float(x.grad.abs().max()) == 0.0 and float(w.grad.abs().max()) == 0.0
+
+
+# ---------------------------------------------------------------------------
+# gated delta rule (Qwen3-Next linear attention)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,S,H,K,V,dtype,init", [
+    (2, 37, 3, 16, 8, torch.float32, False), (2, 37, 3, 16, 8, torch.float32, True),
+    (1, 300, 4, 128, 128, torch.bfloat16, True), (3, 65, 2, 64, 100, torch.bfloat16, False),
+    (1, 1, 8, 128, 128, torch.float16, True), (2, 0, 2, 32, 32, torch.bfloat16, True)])
+def test_gated_delta_rule_matches_oracle(B, S, H, K, V, dtype, init):
+    """One launch over the whole sequence against the fp64 recurrence: outputs, final state, an initial
+    state, value widths that are not multiples of the 64-column block, a single token and an empty
+    sequence (the state passes through)."""
+    from qwen_triton.kernels import gated_delta_rule_sequence
+
+    q = randn(B, S, H, K, seed=160)
+    k = randn(B, S, H, K, seed=161)
+    q, k = (q / q.norm(dim=-1, keepdim=True)).to(dtype), (k / k.norm(dim=-1, keepdim=True)).to(dtype)
+    v = randn(B, S, H, V, dtype=dtype, seed=162)
+    g = -randn(B, S, H, seed=163).abs() * 0.2
+    beta = torch.sigmoid(randn(B, S, H, seed=164))
+    s0 = randn(B, H, K, V, seed=165, scale=0.5) if init else None
+    c0 = native_calls("qh_gated_delta_rule")
+    out, st = gated_delta_rule_sequence(q, k, v, g, beta, initial_state=s0)
+    assert native_calls("qh_gated_delta_rule") == c0 + 1
+    assert out.dtype == dtype and st.dtype == torch.float32 and st.shape == (B, H, K, V)
+    eo, es = O.gated_delta_rule(q, k, v, g, beta, s0)
+    tol = F32_TOL if dtype == torch.float32 else BF16_TOL
+    close(out, eo, **tol)
+    close(st, es, atol=1e-3 if dtype == torch.float32 else 3e-2, rtol=1e-3 if dtype == torch.float32 else 3e-2)
+    # chunked in two launches through the state = one launch
+    if S >= 2:
+        h = S // 2
+        o1, s1 = gated_delta_rule_sequence(q[:, :h], k[:, :h], v[:, :h], g[:, :h], beta[:, :h], initial_state=s0)
+        o2, s2 = gated_delta_rule_sequence(q[:, h:], k[:, h:], v[:, h:], g[:, h:], beta[:, h:], initial_state=s1)
+        assert torch.equal(torch.cat((o1, o2), dim=1), out) and torch.equal(s2, st)

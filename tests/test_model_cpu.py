@@ -163,3 +163,37 @@ def test_qwen3_dense_normalization():
 def test_hf5_config_rope_parameters_are_read():
     c = QwenTritonConfig.from_hf_config(_tiny_dense())
     assert c.rope_theta == 10000.0 and c.head_dim == 16 and c.num_key_value_heads == 2
+
+
+def _next_model():
+    params, ids, logits, cfg = _load_golden("qwen3_next_tiny.npz")
+    raw = {k: (int(v) if float(v).is_integer() and k not in ("rope_theta", "rms_norm_eps", "partial_rotary_factor")
+               else v) for k, v in cfg.items()}
+    raw["model_type"] = "qwen3_next"
+    raw["tie_word_embeddings"] = bool(raw["tie_word_embeddings"])
+    raw["norm_topk_prob"] = bool(raw["norm_topk_prob"])
+    raw["mlp_only_layers"] = []
+    config = QwenTritonConfig.from_hf_config(raw)
+    assert config.layer_types == ["linear_attention", "full_attention"] * 2
+    model = QwenTritonForCausalLM.from_config(config).eval()
+    missing, unexpected = model.load_state_dict(_converted(params), strict=False)
+    assert not missing and not unexpected, (missing, unexpected)
+    return model, ids, logits
+
+
+def test_golden_qwen3_next_logits_and_cached_decode():
+    """Qwen3-Next (gated-delta linear attention + gated full attention, partial rotary, (1+w) norms,
+    MoE with a shared expert) against HF Qwen3NextForCausalLM's logits (transformers 5.15, whose
+    prefill uses the chunked delta-rule form), then token-by-token decoding through the conv and
+    recurrent cache states against the full forward."""
+    model, ids, logits = _next_model()
+    with torch.no_grad():
+        ours = model(input_ids=ids, attention_mask=torch.ones_like(ids), use_cache=False).logits
+        torch.testing.assert_close(ours, logits, atol=2e-4, rtol=2e-4)
+        out = model(input_ids=ids[:, :5], use_cache=True)
+        cache, steps = out.past_key_values, [out.logits]
+        for t in range(5, ids.shape[1]):
+            o = model(input_ids=ids[:, t:t + 1], past_key_values=cache, use_cache=True)
+            cache = o.past_key_values
+            steps.append(o.logits)
+    torch.testing.assert_close(torch.cat(steps, dim=1), logits, atol=2e-4, rtol=2e-4)

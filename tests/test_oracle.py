@@ -285,3 +285,39 @@ def test_kv_append_and_residual_add():
     assert torch.equal(out[:, :, :4], a) and torch.equal(out[:, :, 4:], b)
     x, r = rn(7, seed=50), rn(7, seed=51)
     assert torch.equal(O.residual_add(x, r), torch.add(x, r))
+
+
+def test_gated_delta_rule_matches_hf_recurrent_and_chunked_forms():
+    """The oracle's recurrence against transformers 5.15's torch_recurrent_gated_delta_rule and
+    torch_chunk_gated_delta_rule (Qwen3-Next) in fp64, with and without an initial state."""
+    from transformers.models.qwen3_next import modeling_qwen3_next as M
+
+    B, S, H, K, V = 2, 37, 3, 16, 8
+    # L2-normalised q and k, as the model feeds them (the update I - beta k k^T is then a contraction;
+    # HF evaluates in fp32 whatever the input dtype, hence the fp32 band)
+    q, k, v = rn(B, S, H, K, seed=60), rn(B, S, H, K, seed=61), rn(B, S, H, V, seed=62)
+    q, k = q / q.norm(dim=-1, keepdim=True), k / k.norm(dim=-1, keepdim=True)
+    g = -rn(B, S, H, seed=63).abs() * 0.3
+    beta = torch.sigmoid(rn(B, S, H, seed=64))
+    s0 = rn(B, H, K, V, seed=65)
+    for init in (None, s0):
+        out, st = O.gated_delta_rule(q, k, v, g, beta, init)
+        ho, hs = M.torch_recurrent_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=init,
+                                                    output_final_state=True)
+        f32 = dict(atol=2e-5, rtol=2e-5)
+        torch.testing.assert_close(out, ho.double(), **f32)
+        torch.testing.assert_close(st, hs.double(), **f32)
+        co, cs = M.torch_chunk_gated_delta_rule(q, k, v, g=g, beta=beta, initial_state=init,
+                                                output_final_state=True)
+        torch.testing.assert_close(out, co.double(), **f32)
+        torch.testing.assert_close(st, cs.double(), **f32)
+
+
+def test_gated_delta_rule_closed_form_single_token():
+    """One token from a zero state: S = beta k v^T, so o = beta (q.k) v / sqrt(K) for every head."""
+    q, k, v = rn(1, 1, 2, 4, seed=66), rn(1, 1, 2, 4, seed=67), rn(1, 1, 2, 3, seed=68)
+    g, beta = rn(1, 1, 2, seed=69), torch.sigmoid(rn(1, 1, 2, seed=70))
+    out, st = O.gated_delta_rule(q, k, v, g, beta)
+    expect = beta[..., None] * (q * k).sum(-1, keepdim=True) * v / 2.0
+    torch.testing.assert_close(out, expect)
+    torch.testing.assert_close(st[0, 0], beta[0, 0, 0] * torch.outer(k[0, 0, 0], v[0, 0, 0]))
