@@ -294,7 +294,9 @@ __device__ __forceinline__ float sumsq8(const typename Mfma<T>::v8& v, float acc
   return acc;
 }
 
-template <typename T, typename OT, int MT, int KSP, bool GATED, bool NORM>
+// NTB: weights loaded non-temporally (each weight tile read by one workgroup, ms == 1); with
+// several row groups per column tile the repeat reads should find the tile in the caches.
+template <typename T, typename OT, int MT, int KSP, bool GATED, bool NORM, bool NTB = true>
 __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__ A, int64_t lda,
                                                            const DecodeProducts<T, OT> P, const DecodeNorm nrm,
                                                            int M, int K, int kr, int ms, int tiles) {
@@ -349,9 +351,13 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
       }
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        // weights are read once per decode step: non-temporal, so they do not evict cached data
-        if (nok && kok) b[u][j] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(brow[j] + k));
-        else b[u][j] = zero;
+        // weights read by one workgroup per decode step: non-temporal, so they do not evict cached data
+        if (nok && kok) {
+          if constexpr (NTB) b[u][j] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(brow[j] + k));
+          else b[u][j] = *reinterpret_cast<const v8*>(brow[j] + k);
+        } else {
+          b[u][j] = zero;
+        }
       }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
@@ -642,8 +648,11 @@ int launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, in
   const DecodeNorm nz = norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f};
   constexpr bool kNormOk = std::is_same<T, OT>::value;  // the only instantiation a norm launch reaches
   if (norm && !kNormOk) return QH_E_ARG;
-#define QH_DG(MTV, KSPV, GV, NV) \
-  gemm_decode_kernel<T, OT, MTV, KSPV, GV, NV><<<grid, 1024, 0, st>>>(a, lda, P, nz, M, K, kr, ms, tiles)
+#define QH_DG(MTV, KSPV, GV, NV)                                                                        \
+  do {                                                                                                 \
+    if (ms == 1) gemm_decode_kernel<T, OT, MTV, KSPV, GV, NV, true><<<grid, 1024, 0, st>>>(a, lda, P, nz, M, K, kr, ms, tiles); \
+    else gemm_decode_kernel<T, OT, MTV, KSPV, GV, NV, false><<<grid, 1024, 0, st>>>(a, lda, P, nz, M, K, kr, ms, tiles); \
+  } while (0)
 #define QH_DG_W(MTV)                                           \
   if constexpr (kNormOk) {                                     \
     if (norm) {                                                \
