@@ -25,6 +25,7 @@
 //    in one or two memory round trips; partials are summed through LDS in a
 //    fixed order.
 #include "qh_mfma.h"
+#include "qh_lds.h"
 
 // Large-tile and split-K paths (qh_gemm_tile.hip).
 int qh_gemm_tile_dispatch(int ta, int tb, int M, int N, int K, const void* A, int64_t lda, const void* B,
@@ -263,13 +264,15 @@ struct DecodeNorm {
 };
 
 // k-steps whose loads one wave issues together (a NORM launch needs its whole
-// K slice in one chunk).
-__host__ __device__ constexpr int decode_chunk(int mt, bool gated) { return (mt <= 2 ? 8 : 4) / (gated ? 2 : 1); }
-// NORM launches hold the row scaling beside the fragments: at most 8 A
-// fragments per lane (no scratch spills at 128 VGPRs).
-__host__ __device__ constexpr int decode_norm_chunk(int mt, bool gated) {
-  return gated ? (mt == 1 ? 4 : 2) : (mt == 1 ? 8 : 2);
+// K slice in one chunk). A chunk's activation block (16 MT rows x 32 CH k) is
+// staged through the wave's 8 KB LDS slot, so MT x CH <= 8 with rows of at
+// least 128 bytes (CH >= 2).
+constexpr int kDecodeSlot = 8192;
+__host__ __device__ constexpr int decode_chunk(int mt, bool gated) {
+  return mt == 1 ? (gated ? 4 : 8) : (mt == 2 ? 4 : 2);
 }
+// NORM launches hold the row scaling beside the fragments; the same chunks.
+__host__ __device__ constexpr int decode_norm_chunk(int mt, bool gated) { return decode_chunk(mt, gated); }
 // Longest row a NORM launch normalises.
 constexpr int kDecodeNormMaxK = 8192;
 
@@ -305,7 +308,17 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   constexpr int CH = NORM ? decode_norm_chunk(MT, GATED) : decode_chunk(MT, GATED);  // k-steps loaded together
   static_assert(!NORM || KSP == 16, "the norm prologue needs all 16 waves on K slices");
   typedef typename Mfma<T>::v8 v8;
-  __shared__ float red[16][MT * 16][16];
+  // Activation rows of a chunk: each wave DMAs its 16 MT x (64 CH bytes) block
+  // into its own slot as whole 128-byte lines (a row-per-lane fragment load
+  // would touch 16 half-used lines per instruction, measured 3-4x slower from
+  // L2), 16-byte slots XOR-swizzled per row so the fragment reads are
+  // conflict-free. The K-slice sums reuse the slots after a barrier.
+  constexpr int RB = CH * 64;   // bytes of one activation row in a chunk
+  constexpr int S16 = RB / 16;  // 16-byte slots per row
+  static_assert(MT * 16 * RB <= kDecodeSlot && CH >= 2, "activation block exceeds the wave's LDS slot");
+  static_assert(16 * MT * 16 * 16 * 4 <= 16 * kDecodeSlot, "K-slice sums exceed the slots");
+  __shared__ __align__(16) unsigned char aslot[16][kDecodeSlot];
+  float(*red)[MT * 16][16] = reinterpret_cast<float(*)[MT * 16][16]>(&aslot[0][0]);
   __shared__ float nss[NORM ? 16 : 1][MT * 16];
   // Workgroup -> (column tile, row group). The ms row groups of a tile get
   // workgroup ids that are equal mod 8, so they run on one XCD and read the
@@ -342,6 +355,17 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   for (int k0 = kb; NORM ? k0 == kb : k0 < ke; k0 += 32 * CH) {
     v8 b[CH][NB], a[CH][MT];
     v8 wr[NORM ? CH : 1];  // norm weights (dtype T) of this lane's 8 columns per step
+    // slot s of row r holds the row's 16-byte chunk s ^ swz(r)
+    auto swz = [](int r) { return S16 >= 16 ? (r & 15) : ((r >> 1) & 7); };
+    if (k0 != kb) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // previous chunk's fragments read
+    const uint32_t abase = lds_addr(&aslot[wid][0]);
+#pragma unroll
+    for (int j = 0; j < MT * CH; ++j) {
+      const int c = j * 64 + lane, r = c / S16;
+      const int m = m0 + r, k = k0 + ((c % S16) ^ swz(r)) * 8;
+      // rows past M and chunks past the slice stage A[0..7] (in bounds; zeroed below)
+      lds_dma16(m < M && k < ke ? A + (int64_t)m * lda + k : A, abase + j * 1024);
+    }
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int k = k0 + u * 32 + q * 8;
@@ -359,11 +383,18 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
           b[u][j] = zero;
         }
       }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged rows (untracked DMA) and the weights
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const bool kok = k0 + u * 32 + q * 8 < ke;
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        const int m = m0 + i * 16 + li;
-        if (m < M && kok) a[u][i] = *reinterpret_cast<const v8*>(A + (int64_t)m * lda + k);
-        else a[u][i] = zero;
+        const int r = i * 16 + li;
+        if (m0 + r < M && kok)
+          a[u][i] = *reinterpret_cast<const v8*>(&aslot[wid][r * RB + (((u * 4 + q) ^ swz(r)) << 4)]);
+        else
+          a[u][i] = zero;
       }
     }
     if constexpr (NORM) {
@@ -402,7 +433,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   float first[(CG * MT * 256 + 1023) / 1024];
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
-    if (j > 0) __syncthreads();  // the previous matrix's sums have been read
+    __syncthreads();  // every wave's fragments (j = 0) or the previous matrix's sums have been read
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
