@@ -136,6 +136,19 @@ int qh_ce_bwd(const void* logits, int64_t stride, const int64_t* targets, const 
               const float* grad_loss, const float* nvalid, void* glogits, int64_t gstride, int64_t N,
               int64_t V, int64_t ignore_index, int dtype, void* stream);
 
+/* ---- Greedy decoding --------------------------------------------------- */
+/* One greedy step on device state: per row b of logits [B, V] (row stride ld) the
+ * argmax (torch.argmax: NaN is the largest value, ties -> lowest column), then
+ * ids[b] = tokens[b * ldt + col] = argmax (the token is stored only when
+ * 0 <= col < ncols), seqlens[b] += 1, col += 1, positions += 1. Every output
+ * pointer may be NULL. B <= 64; ws of at least qh_greedy_step_workspace(B, V)
+ * bytes. Two launches, no host synchronisation (graph-capturable).
+ * Replaces the argmax and bookkeeping of qwen_triton/models/core.py:405-408. */
+int64_t qh_greedy_step_workspace(int64_t B, int64_t V);
+int qh_greedy_step(const void* logits, int64_t ld, int64_t B, int64_t V, int64_t* ids, int64_t* tokens,
+                   int64_t ldt, int64_t ncols, int64_t* col, int64_t* positions, int32_t* seqlens, void* ws,
+                   int64_t ws_bytes, int dtype, void* stream);
+
 /* ---- MoE routing primitives --------------------------------------------- */
 /* Top-k per row, values sorted descending, ties -> lowest index.
  * Replaces qwen_triton/kernels/moe_routing.py:45-144 (_topk_k2_kernel, _topk_general_kernel). */
@@ -378,15 +391,18 @@ int qh_attn_prepare(const void* q, int64_t sq, const void* k, int64_t sk, const 
 /* ---- flash attention ---------------------------------------------------- */
 /* O = softmax(scale * Q K^T + causal mask) V, LSE = logsumexp per query (fp32,
  * natural log, [B,Hq,Sq]). q [B,Hq,Sq,D], k/v [B,Hkv,Sk,D] with the given
- * batch/head/seq strides (unit stride on D); o is contiguous [B,Hq,Sq,D]. GQA
+ * batch/head/seq strides (unit stride on D); o [B,Hq,Sq,D] with its own batch/head/
+ * seq strides (sob, soh, sos; contiguous: Hq*Sq*D, Sq*D, D; [B,Sq,Hq*D] rows for the
+ * output projection: Sq*Hq*D, D, Hq*D). GQA
  * maps q-head h to kv-head h/(Hq/Hkv). Causal: key j visible to query i iff
  * j <= i + causal_offset (0 = the reference's top-left alignment). bf16/f16,
  * D % 8 == 0, D <= 128. lse may be NULL.
  * Replaces qwen_triton/kernels/flash_attention.py:54-152 (_flash_attn_fwd_kernel), :280-314. */
 int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
                  int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o,
-                 float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
-                 float scale, int causal, int64_t causal_offset, int dtype, void* stream);
+                 int64_t sob, int64_t soh, int64_t sos, float* lse, int64_t B, int64_t Hq, int64_t Hkv,
+                 int64_t Sq, int64_t Sk, int64_t D, float scale, int causal, int64_t causal_offset, int dtype,
+                 void* stream);
 /* Workspace bytes of qh_flash_bwd: Delta = rowsum(O dO) and the LSE in log2 units,
  * per (b, q-head) in rows of Sq rounded up to 64 plus one 64-query tile. */
 int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq);

@@ -321,8 +321,9 @@ template <typename T, int DP>
 __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs,
                                                      const T* __restrict__ K, int64_t skb, int64_t skh, int64_t sks,
                                                      const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs,
-                                                     T* __restrict__ O, float* __restrict__ LSE, int Hq, int groups,
-                                                     int Sq, int Sk, int D, float scale_log2, int causal, int coff) {
+                                                     T* __restrict__ O, int64_t sob, int64_t soh, int64_t sos,
+                                                     float* __restrict__ LSE, int Hq, int groups, int Sq, int Sk, int D,
+                                                     float scale_log2, int causal, int coff) {
   constexpr int BN = 64, BMQ = 128;
   constexpr int DT = DP / 32, KD = DP / 16;
   typedef typename Mfma<T>::v8 v8;
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
 
   l = halves_sum(l);
   if (qi < Sq) {
-    T* Ob = O + ((int64_t)bh * Sq + qi) * D;
+    T* Ob = O + b * sob + hq * soh + (int64_t)qi * sos;
     const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -1526,15 +1527,16 @@ void launch_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int64
 // ===========================================================================
 extern "C" int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
                             int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o,
-                            float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
-                            float scale, int causal, int64_t causal_offset, int dtype, void* stream) {
+                            int64_t sob, int64_t soh, int64_t sos, float* lse, int64_t B, int64_t Hq, int64_t Hkv,
+                            int64_t Sq, int64_t Sk, int64_t D, float scale, int causal, int64_t causal_offset, int dtype,
+                            void* stream) {
   QH_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0, "qh_flash_fwd: bad shape");
   QH_CHECK_ARG(Hq % Hkv == 0, "qh_flash_fwd: Hq=%lld not a multiple of Hkv=%lld", (long long)Hq, (long long)Hkv);
   const int dp = pick_dp(D);
   QH_CHECK_ARG(dp && D % 8 == 0, "qh_flash_fwd: head dim %lld must be a multiple of 8 and <= 128", (long long)D);
   QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o), "qh_flash_fwd: pointers must be 16-byte aligned");
   QH_CHECK_ARG(sqs % 8 == 0 && sks % 8 == 0 && svs % 8 == 0 && sqh % 8 == 0 && skh % 8 == 0 && svh % 8 == 0 &&
-                   sqb % 8 == 0 && skb % 8 == 0 && svb % 8 == 0,
+                   sqb % 8 == 0 && skb % 8 == 0 && svb % 8 == 0 && sob % 8 == 0 && soh % 8 == 0 && sos % 8 == 0,
                "qh_flash_fwd: strides must be multiples of 8 elements");
   QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_flash_fwd: bf16/f16 only");
   QH_CHECK_ARG(B * Hq < 65536 && Sq < (1 << 30) && Sk < (1 << 30), "qh_flash_fwd: too large");
@@ -1546,8 +1548,8 @@ extern "C" int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
   dim3 grid((unsigned)ceil_div(Sq, 128), (unsigned)(B * Hq));
 #define QH_FWD(T, DPV)                                                                                          \
   fa_fwd_kernel<T, DPV><<<grid, 256, 0, st>>>((const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks,       \
-                                                 (const T*)v, svb, svh, svs, (T*)o, lse, (int)Hq, groups, (int)Sq, \
-                                                 (int)Sk, (int)D, sl2, causal, (int)causal_offset)
+                                                 (const T*)v, svb, svh, svs, (T*)o, sob, soh, sos, lse, (int)Hq,   \
+                                                 groups, (int)Sq, (int)Sk, (int)D, sl2, causal, (int)causal_offset)
 #define QH_FWD_D(T) \
   if (dp == 32) QH_FWD(T, 32); else if (dp == 64) QH_FWD(T, 64); else QH_FWD(T, 128);
   if (dtype == QH_BF16) { QH_FWD_D(bf16_t) } else { QH_FWD_D(f16_t) }

@@ -888,6 +888,105 @@ static void launch_topk(const void* x, void* vals, int64_t* idx, int64_t N, int6
     topk_wide_kernel<T, false><<<(unsigned)N, 1024, 0, st>>>((const T*)x, (T*)vals, idx, N, (int)C, (int)k);
 }
 
+
+// ---------------------------------------------------------------------------
+// Greedy decode step: the argmax of each row of the last logits (torch.argmax
+// semantics: NaN counts as the largest value, ties go to the lowest column)
+// and the step's bookkeeping in device memory. An element's key is
+// (order-preserving value bits, NaN above +inf) << 32 | ~column, so the
+// largest key is the answer whatever the reduction order.
+constexpr int kGreedyMaxRows = 64;  // rows one launch serves
+
+__device__ __forceinline__ uint64_t greedy_key(float v, int c) {
+  uint32_t b = __float_as_uint(v);
+  b = (v != v) ? 0xFFFFFFFFu : (b ^ ((b >> 31) ? 0xFFFFFFFFu : 0x80000000u));
+  return ((uint64_t)b << 32) | (uint32_t)~(uint32_t)c;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t k2 = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), o) << 32) |
+                        (uint32_t)__shfl_xor((int)(uint32_t)k, o);
+    k = k2 > k ? k2 : k;
+  }
+  return k;
+}
+
+// Columns one first-stage workgroup keys: one 16-byte load per thread.
+template <typename T>
+__host__ __device__ constexpr int greedy_cols() { return 256 * (16 / (int)sizeof(T)); }
+
+// Stage 1: workgroup (p, row) reduces its greedy_cols<T>() columns to one key.
+template <typename T>
+__global__ __launch_bounds__(256) void greedy_partial_kernel(const T* __restrict__ x, int64_t ld, int V,
+                                                             uint64_t* __restrict__ part, int P) {
+  constexpr int VN = Vec16<T>::N;
+  __shared__ uint64_t sk[4];
+  const int row = blockIdx.y, p = blockIdx.x;
+  const T* xr = x + (int64_t)row * ld;
+  const int c0 = p * greedy_cols<T>() + threadIdx.x * VN;
+  uint64_t best = 0;  // below every element's key
+  if (c0 + VN <= V) {
+    const Vec16<T> v = ld16(xr + c0);
+#pragma unroll
+    for (int e = 0; e < VN; ++e) {
+      const uint64_t k = greedy_key(to_f32(v.v[e]), c0 + e);
+      best = k > best ? k : best;
+    }
+  } else {
+    for (int c = c0; c < V && c < c0 + VN; ++c) {
+      const uint64_t k = greedy_key(to_f32(xr[c]), c);
+      best = k > best ? k : best;
+    }
+  }
+  best = wave_max_u64(best);
+  if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t b = sk[0];
+    for (int w = 1; w < 4; ++w) b = sk[w] > b ? sk[w] : b;
+    part[(int64_t)row * P + p] = b;
+  }
+}
+
+// Stage 2 (one workgroup): each row's answer from its P partial keys, then the step's
+// bookkeeping: ids[b] = tokens[b, col] = answer, seqlens[b] += 1, col += 1, positions += 1
+// (each pointer optional). One thread reads the counters before writing them.
+__global__ __launch_bounds__(256) void greedy_finish_kernel(const uint64_t* __restrict__ part, int P, int B,
+                                                            int64_t* __restrict__ ids, int64_t* __restrict__ tokens,
+                                                            int64_t ldt, int64_t ncols, int64_t* __restrict__ col,
+                                                            int64_t* __restrict__ positions,
+                                                            int32_t* __restrict__ seqlens) {
+  __shared__ uint64_t sk[4];
+  __shared__ int64_t ans[kGreedyMaxRows];
+  for (int b = 0; b < B; ++b) {
+    uint64_t best = 0;
+    for (int p = threadIdx.x; p < P; p += 256) {
+      const uint64_t k = part[(int64_t)b * P + p];
+      best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint64_t m = sk[0];
+      for (int w = 1; w < 4; ++w) m = sk[w] > m ? sk[w] : m;
+      ans[b] = (int64_t)(uint32_t)~(uint32_t)m;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const int64_t c = col ? col[0] : -1;
+    for (int b = 0; b < B; ++b) {
+      if (ids) ids[b] = ans[b];
+      if (tokens && c >= 0 && c < ncols) tokens[(int64_t)b * ldt + c] = ans[b];
+      if (seqlens) seqlens[b] += 1;
+    }
+    if (col) col[0] = c + 1;
+    if (positions) positions[0] += 1;
+  }
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -1068,6 +1167,32 @@ extern "C" int qh_topk(const void* x, void* vals, int64_t* idx, int64_t N, int64
   hipStream_t st = (hipStream_t)stream;
   QH_DISPATCH_DTYPE(dtype, T, "qh_topk", launch_topk<T>(x, vals, idx, N, C, k, st));
   QH_CHECK_LAUNCH("qh_topk");
+  return QH_OK;
+}
+
+extern "C" int64_t qh_greedy_step_workspace(int64_t B, int64_t V) {
+  return B * ((V + greedy_cols<float>() - 1) / greedy_cols<float>()) * (int64_t)sizeof(uint64_t);
+}
+
+extern "C" int qh_greedy_step(const void* logits, int64_t ld, int64_t B, int64_t V, int64_t* ids, int64_t* tokens,
+                              int64_t ldt, int64_t ncols, int64_t* col, int64_t* positions, int32_t* seqlens,
+                              void* ws, int64_t ws_bytes, int dtype, void* stream) {
+  QH_CHECK_ARG(B >= 1 && B <= kGreedyMaxRows && V >= 1 && V < (1ll << 31) && ld >= V,
+               "qh_greedy_step: bad shape B=%lld V=%lld ld=%lld", (long long)B, (long long)V, (long long)ld);
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16 || dtype == QH_F32, "qh_greedy_step: bf16/f16/f32 logits");
+  QH_CHECK_ARG(aligned16(logits) && (ld * (dtype == QH_F32 ? 4 : 2)) % 16 == 0,
+               "qh_greedy_step: logits rows must be 16-byte aligned");
+  QH_CHECK_ARG(ws != nullptr && ws_bytes >= qh_greedy_step_workspace(B, V), "qh_greedy_step: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  uint64_t* part = (uint64_t*)ws;
+  int P = 0;
+#define QH_GREEDY(TT)                                                                                \
+  P = (int)((V + greedy_cols<TT>() - 1) / greedy_cols<TT>());                                         \
+  greedy_partial_kernel<TT><<<dim3((unsigned)P, (unsigned)B), 256, 0, st>>>((const TT*)logits, ld, (int)V, part, P)
+  if (dtype == QH_BF16) { QH_GREEDY(bf16_t); } else if (dtype == QH_F16) { QH_GREEDY(f16_t); } else { QH_GREEDY(float); }
+#undef QH_GREEDY
+  greedy_finish_kernel<<<1, 256, 0, st>>>(part, P, (int)B, ids, tokens, ldt, ncols, col, positions, seqlens);
+  QH_CHECK_LAUNCH("qh_greedy_step");
   return QH_OK;
 }
 

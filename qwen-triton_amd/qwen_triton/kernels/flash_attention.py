@@ -61,19 +61,39 @@ def _check(q, k, v, num_kv_groups):
 
 
 def flash_forward(q, k, v, scale: float, causal: bool, num_kv_groups: int, causal_offset: int = 0,
-                  need_lse: bool = True):
-    """Launch the forward kernel; returns (out [B,Hq,Sq,D] contiguous, lse [B,Hq,Sq] fp32 or None)."""
+                  need_lse: bool = True, seq_major: bool = False):
+    """Launch the forward kernel; returns (out [B,Hq,Sq,D], lse [B,Hq,Sq] fp32 or None). ``out`` is
+    contiguous, or with ``seq_major`` the [B,Hq,Sq,D] view of a [B,Sq,Hq,D] buffer (the rows the
+    output projection reads, written in place by the kernel)."""
     _check(q, k, v, num_kv_groups)
     q, k, v = _unit_last(q), _unit_last(k), _unit_last(v)
     B, Hq, Sq, D = q.shape
     Hkv, Sk = k.shape[1], k.shape[2]
-    out = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
+    if seq_major:
+        out = torch.empty((B, Sq, Hq, D), dtype=q.dtype, device=q.device).permute(0, 2, 1, 3)
+    else:
+        out = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if need_lse else None
     _native.call("qh_flash_fwd", q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0),
                  k.stride(1), k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), out.data_ptr(),
-                 None if lse is None else lse.data_ptr(), B, Hq, Hkv, Sq, Sk, D, float(scale), int(bool(causal)),
-                 int(causal_offset), _native.dtype_code(q.dtype), _native.stream(q.device))
+                 out.stride(0), out.stride(1), out.stride(2), None if lse is None else lse.data_ptr(), B, Hq, Hkv,
+                 Sq, Sk, D, float(scale), int(bool(causal)), int(causal_offset), _native.dtype_code(q.dtype),
+                 _native.stream(q.device))
     return out, lse
+
+
+def attention_rows(q, k, v, scale: float, num_kv_groups: int, causal_offset: int = 0) -> torch.Tensor | None:
+    """Causal inference attention (no autograd) returned as the output projection's input rows
+    [B, Sq, Hq * D], which the kernel writes in place (no transpose copy); None when the call is not
+    served by the library (the caller then takes its usual path)."""
+    if not _GUARD.use_native(None, q, k, v):
+        return None
+    try:
+        out = flash_forward(q, k, v, scale, True, num_kv_groups, causal_offset, need_lse=False, seq_major=True)[0]
+    except Exception as exc:
+        _GUARD.failed(exc)
+        return None
+    return out.transpose(1, 2).reshape(q.shape[0], q.shape[2], -1)
 
 
 def flash_backward(q, k, v, out, grad_out, lse, scale: float, causal: bool, num_kv_groups: int,

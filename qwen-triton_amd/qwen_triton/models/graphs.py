@@ -5,9 +5,13 @@ re-runs the Python of every layer for each token. A serving loop that generates 
 one shape many times replays these graphs instead:
 
 * the prefill graph runs the forward over the prompt buffer into a preallocated cache, picks
-  the first token (top-1 on the library kernel, ties to the lowest index as argmax) and resets
-  the device-side decode state (cache position, valid lengths, next output column);
+  the first token and resets the device-side decode state (cache position, valid lengths, next
+  output column);
 * the step graph decodes one token from that device state and advances it.
+
+The pick is torch.argmax's (NaN largest, ties to the lowest index); it and the state updates
+are two library launches (``qh_greedy_step``), or for more than 64 rows a top-1 kernel and
+torch ops on the same buffers.
 
 Both are captured on first use. Each replay overwrites the same buffers (cache, tokens), so a
 runner serves one call at a time; the graphs hold the parameters' storage addresses, so a model
@@ -18,6 +22,7 @@ from __future__ import annotations
 
 import torch
 
+from qwen_triton import _native
 from qwen_triton.modules.cache import StaticDecode
 
 
@@ -25,6 +30,15 @@ def _pick(logits: torch.Tensor) -> torch.Tensor:
     from qwen_triton.kernels.moe_routing import _native_topk
 
     return _native_topk(logits[:, -1], 1)[1]
+
+
+_GREEDY_MAX_ROWS = 64  # rows qh_greedy_step serves
+_GREEDY_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def _greedy_step_ok(batch: int, vocab: int, dtype: torch.dtype) -> bool:
+    return batch <= _GREEDY_MAX_ROWS and dtype in _GREEDY_DTYPES \
+        and (vocab * torch.tensor([], dtype=dtype).element_size()) % 16 == 0
 
 
 class GreedyGraphs:
@@ -42,18 +56,43 @@ class GreedyGraphs:
                                    seqlens=torch.full((batch,), prompt + 1, dtype=torch.int32, device=device))
         self.prefill_graph: torch.cuda.CUDAGraph | None = None
         self.step_graph: torch.cuda.CUDAGraph | None = None
+        # the pick and the step's bookkeeping in two library launches (qh_greedy_step) when the
+        # shape allows; otherwise top-1 and torch ops on the same buffers
+        vocab = model.config.vocab_size
+        self.greedy_ws = None
+        if _greedy_step_ok(batch, vocab, dtype):
+            self.greedy_ws = _native.workspace(_native.call("qh_greedy_step_workspace", batch, vocab), device)
+
+    def _greedy(self, logits: torch.Tensor) -> None:
+        last = logits[:, -1]
+        if last.stride(-1) != 1 or last.data_ptr() % 16 or (last.stride(0) * last.element_size()) % 16:
+            last = last.contiguous()
+        _native.call("qh_greedy_step", last.data_ptr(), last.stride(0), self.batch, last.shape[-1],
+                     self.ids.data_ptr(), self.tokens.data_ptr(), self.tokens.stride(0), self.tokens.shape[1],
+                     self.col.data_ptr(), self.static.positions.data_ptr(), self.static.seqlens.data_ptr(),
+                     self.greedy_ws.data_ptr(), self.greedy_ws.numel(), _native.dtype_code(last.dtype),
+                     _native.stream(last.device))
 
     def _prefill_body(self) -> None:
         cache = self.cache
         cache.static = None
         cache.attention_lengths = [0] * cache.num_layers  # prefill from position 0
         logits = self.model(input_ids=self.prompt_ids, past_key_values=cache, use_cache=True, logits_to_keep=1).logits
+        if self.greedy_ws is not None and logits.dtype in _GREEDY_DTYPES:
+            # the step kernel stores the first token at column 0 and leaves col = 1,
+            # position = prompt, lengths = prompt + 1
+            self.col.fill_(0)
+            self.static.positions.fill_(self.prompt - 1)
+            self.static.seqlens.fill_(self.prompt)
+            self._greedy(logits)
+            return
         first = _pick(logits)
         self.tokens[:, :1].copy_(first)
         self.ids.copy_(first)
         self.col.fill_(1)
         self.static.positions.fill_(self.prompt)
         self.static.seqlens.fill_(self.prompt + 1)
+
 
     def _step_body(self) -> None:
         self.cache.static = self.static
@@ -62,6 +101,9 @@ class GreedyGraphs:
                                 logits_to_keep=1).logits
         finally:
             self.cache.static = None
+        if self.greedy_ws is not None and logits.dtype in _GREEDY_DTYPES:
+            self._greedy(logits)
+            return
         nxt = _pick(logits)
         self.ids.copy_(nxt)
         self.tokens.scatter_(1, self.col.expand(self.batch, 1), nxt)

@@ -204,6 +204,11 @@ class QwenFullAttention(nn.Module):
             # is read from device memory
             out = _fa.flash_decode(q, k, v, self.scaling, self.num_key_value_groups, seqlens=static.seqlens)
         else:
+            if attention_mask is None and q.shape[2] > 1:
+                rows = _fa.attention_rows(q, k, v, self.scaling, self.num_key_value_groups,
+                                          causal_offset=k.shape[2] - q.shape[2])
+                if rows is not None:
+                    return rows.view(*input_shape, -1)
             out = self._attend(q, k, v, attention_mask, q2.dtype)
         return out.transpose(1, 2).reshape(*input_shape, -1)
 

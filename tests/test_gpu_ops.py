@@ -1137,3 +1137,48 @@ def test_gated_delta_rule_matches_oracle(B, S, H, K, V, dtype, init):
         o1, s1 = gated_delta_rule_sequence(q[:, :h], k[:, :h], v[:, :h], g[:, :h], beta[:, :h], initial_state=s0)
         o2, s2 = gated_delta_rule_sequence(q[:, h:], k[:, h:], v[:, h:], g[:, h:], beta[:, h:], initial_state=s1)
         assert torch.equal(torch.cat((o1, o2), dim=1), out) and torch.equal(s2, st)
+
+
+# ---------------------------------------------------------------------------
+# greedy decode step
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,V", [(1, 151936), (3, 1000), (64, 4104), (2, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_greedy_step_is_argmax_and_advances_the_state(B, V, dtype):
+    """qh_greedy_step against torch.argmax of the same values (ties to the lowest column, NaN the
+    largest), the token written at the device column, the counters advanced; a column past the
+    buffer stores nothing."""
+    x = randn(B, V, dtype=dtype, seed=300)
+    if V >= 8:
+        top = x.float().max(dim=-1).values
+        x[0, V // 2] = top[0].to(dtype)          # tie with the row's maximum at a later column
+        x[0, 1] = top[0].to(dtype)               # and an earlier one: the earliest wins
+    if B >= 3:
+        x[2, V - 1] = float("nan")               # NaN is the largest value
+        x[2, V - 3] = float("nan")
+    expect = x.float().cpu().argmax(dim=-1)
+    ids = torch.full((B, 1), -5, dtype=torch.long, device=DEV)
+    tokens = torch.full((B, 6), -7, dtype=torch.long, device=DEV)
+    col = torch.full((1, 1), 2, dtype=torch.long, device=DEV)
+    pos = torch.full((1,), 40, dtype=torch.long, device=DEV)
+    lens = torch.arange(B, dtype=torch.int32, device=DEV) + 10
+    ws = _native.workspace(_native.call("qh_greedy_step_workspace", B, V), x.device)
+    c0 = native_calls("qh_greedy_step")
+
+    def step():
+        _native.call("qh_greedy_step", x.data_ptr(), x.stride(0), B, V, ids.data_ptr(), tokens.data_ptr(),
+                     tokens.stride(0), tokens.shape[1], col.data_ptr(), pos.data_ptr(), lens.data_ptr(),
+                     ws.data_ptr(), ws.numel(), _native.dtype_code(dtype), _native.stream(x.device))
+
+    step()
+    assert native_calls("qh_greedy_step") == c0 + 1
+    assert torch.equal(ids[:, 0].cpu(), expect)
+    assert torch.equal(tokens[:, 2].cpu(), expect)
+    assert (tokens[:, [0, 1, 3, 4, 5]] == -7).all()
+    assert int(col) == 3 and int(pos) == 41
+    assert torch.equal(lens.cpu(), torch.arange(B, dtype=torch.int32) + 11)
+    col.fill_(6)  # past the token buffer: ids still written, no token stored
+    ids.fill_(-5)
+    step()
+    assert torch.equal(ids[:, 0].cpu(), expect) and (tokens[:, [0, 1, 3, 4, 5]] == -7).all()
+    assert int(col) == 7 and int(pos) == 42
