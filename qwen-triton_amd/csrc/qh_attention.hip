@@ -1199,10 +1199,11 @@ __global__ __launch_bounds__(256) void fa_decode_combine(const float* __restrict
 // into its MFMA operand through a private LDS slot, so no wavefront waits for
 // another. The wavefront that will read the key tile holding the new position
 // p also writes the new key row (normalised, rotated) and value row into the
-// caches at p. Vector-memory counts retire in issue order, so the loop's wait
-// before tile 2 is requested also covers those stores; only when p lies in the
-// wave's first three tiles does it write first and wait for vmcnt(0) (the
-// stores' completion) before it requests that tile.
+// caches at p, and keeps both in LDS: when that tile has landed, the lanes
+// holding key p take the key row from LDS and the value rows from p to the
+// tile's end (key p, and the rows past the last key that the tile load clamps
+// to it) are rewritten in the V stage. So no load waits for the stores, whose
+// bytes are those the patch supplies.
 template <typename T, bool PREP>
 using kv_ptr = typename std::conditional<PREP, const T*, const T* __restrict__>::type;
 
@@ -1224,7 +1225,9 @@ struct DecodePrepArgs {
   int64_t cap;         // rows allocated in the caches (positions outside [0, cap) are not written)
 };
 
-template <typename T, int DP, int G, bool PREP = false, typename C = float>
+// NTKV: K/V tiles read non-temporally (a large cache streamed once per step past the
+// last-level cache); short caches, read again at the next step, keep the default policy.
+template <typename T, int DP, int G, bool PREP = false, typename C = float, bool NTKV = true>
 __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
                                                           kv_ptr<T, PREP> K, int64_t skb, int64_t skh,
                                                           int64_t sks, kv_ptr<T, PREP> V, int64_t svb,
@@ -1246,6 +1249,7 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
   __shared__ float cml[NW][G][2];
   __shared__ float co[NW][G][DP];
   __shared__ __attribute__((aligned(16))) T qs[PREP ? NW : 1][PREP ? G : 1][DP];
+  __shared__ __attribute__((aligned(16))) T kvp[PREP ? NW : 1][2][PREP ? DP : 8];  // PREP: new key / value row
 
   const int bk = blockIdx.x;
   const int b = bk / Hkv, hk = bk % Hkv;
@@ -1276,13 +1280,12 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
     dsw[par] = c * 8 < D ? c * 8 : D - 8;
     voff[par] = (uint32_t)(((int64_t)rl * svs + dsw[par]) * (int64_t)sizeof(T));
   }
-  int tile_p = -1;  // PREP: the tile whose rows this wave wrote (its loads wait for those stores)
+  // PREP: this wave's tile holding the new position p, p's row in it, and the end of the V
+  // rows to rewrite (past p only when p is the last key: the tile load clamps later rows to it)
+  int tp = -1, kp = 0, kpe = 0;
   auto issue = [&](int t, v8 (&kf)[2][KD]) {
     const int row0 = (w + t * NW) * BN;
     const uint32_t vl = lds_addr(Vs[w][t % NS]);
-    // the new rows are stored before the loads of their tile are issued: vmcnt counts this wave's
-    // vector stores as well as its loads (gfx9 family), so vmcnt(0) waits for the row stores
-    if (PREP && w + t * NW == tile_p && t <= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       int key = row0 + 16 * h + li;
@@ -1290,18 +1293,26 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
       const T* kr = Kb + (int64_t)key * sks;
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd)
-        kf[h][kd] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(kr + kdo[kd]));
+        kf[h][kd] = NTKV ? __builtin_nontemporal_load(reinterpret_cast<const v8*>(kr + kdo[kd]))
+                         : *reinterpret_cast<const v8*>(kr + kdo[kd]);
     }
     if (row0 + BN <= sk_b) {
 #pragma unroll
-      for (int n = 0; n < NI; ++n)
-        lds_dma16_s_nt(voff[n % NPAT], Vb + (int64_t)(row0 + n * RPI) * svs, vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+      for (int n = 0; n < NI; ++n) {
+        const T* vb = Vb + (int64_t)(row0 + n * RPI) * svs;
+        const uint32_t dst = vl + (uint32_t)(n * RPI * DP * sizeof(T));
+        if constexpr (NTKV) lds_dma16_s_nt(voff[n % NPAT], vb, dst);
+        else lds_dma16_s(voff[n % NPAT], vb, dst);
+      }
     } else {
 #pragma unroll
       for (int n = 0; n < NI; ++n) {
         int gr = row0 + n * RPI + rl;
         gr = gr < sk_b ? gr : sk_b - 1;
-        lds_dma16_nt(Vb + (int64_t)gr * svs + dsw[n % NPAT], vl + (uint32_t)(n * RPI * DP * sizeof(T)));
+        const T* src = Vb + (int64_t)gr * svs + dsw[n % NPAT];
+        const uint32_t dst = vl + (uint32_t)(n * RPI * DP * sizeof(T));
+        if constexpr (NTKV) lds_dma16_nt(src, dst);
+        else lds_dma16(src, dst);
       }
     }
   };
@@ -1313,10 +1324,13 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
   bool pre1 = false;  // tile 1 already requested before the loop
   if constexpr (PREP) {
     const int64_t p = pa.pos[0];
-    const bool pin = p >= 0 && p < sk_b;  // the new row is one of the keys read here
+    const bool pin = p >= 0 && p < sk_b && p < pa.cap;  // the new row is one of the keys read here
     const int wp = pin ? (int)((p / BN) % NW) : 0;
-    tile_p = w == wp && pin ? (int)(p / BN) : -1;
-    const bool slow = tile_p >= 0 && tile_p < w + 2 * NW;  // p in this wave's first two tiles
+    if (pin && w == wp) {
+      tp = (int)(p / BN - w) / NW;
+      kp = (int)(p % BN);
+      kpe = p == sk_b - 1 ? BN : kp + 1;
+    }
     // 16-lane group gi takes rows gi, gi + 4, ...: the G query rows, then (wave
     // wp) the key row and the value row; one 16-byte load per lane and pass.
     constexpr int NPASS = (G + 2 + 3) / 4;
@@ -1337,7 +1351,7 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
       rp[ps] = load_row_params<C, true>(r < G ? pa.qw : pa.kw, pa.wdtype, pa.wadd, d0, act, pa.half, pa.rot, pa.cs,
                                         pa.sn, co_row);
     }
-    if (!slow && ntiles > 0) {
+    if (ntiles > 0) {
       issue(0, ka);
       if (ntiles > 1) issue(1, kb), pre1 = true;
     }
@@ -1349,12 +1363,18 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
       if (!act) x.raw = make_uint4(0, 0, 0, 0);
       const Vec16<T> y = norm_rope_apply<T>(x, act, rp[ps], pa.eps, D, d0, pa.half / 8, pa.half, pa.rot);
       if (act) {
-        if (isq) *reinterpret_cast<uint4*>(&qs[w][r][d0]) = y.raw;
-        else if (isk) st16(const_cast<T*>(Kb) + p * sks + d0, y);
-        else if (isv) st16(const_cast<T*>(Vb) + p * svs + d0, x);
+        if (isq) {
+          *reinterpret_cast<uint4*>(&qs[w][r][d0]) = y.raw;
+        } else if (isk) {
+          st16(const_cast<T*>(Kb) + p * sks + d0, y);
+          *reinterpret_cast<uint4*>(&kvp[w][0][d0]) = y.raw;
+        } else if (isv) {
+          st16(const_cast<T*>(Vb) + p * svs + d0, x);
+          *reinterpret_cast<uint4*>(&kvp[w][1][d0]) = x.raw;
+        }
       }
     }
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this wave's qs rows are written
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this wave's qs (and kvp) rows are written
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd) {
       const int d = kd * 32 + lg * 8;
@@ -1363,7 +1383,6 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
 #pragma unroll
         for (int e = 0; e < 8; ++e) qf[kd][e] = (T)0.f;
     }
-    if (slow && ntiles > 0) issue(0, ka);  // issue() waits for vmcnt(0) before the tile holding p
   } else {
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd) {
@@ -1429,6 +1448,27 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   };
 
+  // PREP, tile tp (landed): key p's fragments from the kept row; V rows kp..kpe-1
+  // (key p, and when p is the last key the clamped rows past it) rewritten with the new value row.
+  auto patch = [&](int t, v8 (&kf)[2][KD]) {
+    if (!PREP || t != tp) return;
+    if (li == (kp & 15)) {
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) {
+        const v8 kv = *reinterpret_cast<const v8*>(&kvp[w][0][kdo[kd]]);
+        if (kp < 16) kf[0][kd] = kv;
+        else kf[1][kd] = kv;
+      }
+    }
+    T* Vt = Vs[w][t % NS];
+    for (int i = lane; i < (kpe - kp) * CPR; i += 64) {
+      const int r = kp + i / CPR, c = i % CPR;
+      const int dsrc = c * 8 < D ? c * 8 : D - 8;
+      *reinterpret_cast<uint4*>(Vt + r * DP + swz(r, c, CPR) * 8) = *reinterpret_cast<const uint4*>(&kvp[w][1][dsrc]);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  };
+
   // Tile t has landed once only tile t + 1's KLD + NI instructions are
   // outstanding (tile 0 was issued above).
   for (int t = 0; t < ntiles; t += 2) {
@@ -1438,6 +1478,7 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
     } else {
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     }
+    patch(t, ka);
     compute(t, ka);
     if (t + 1 < ntiles) {
       if (t + 2 < ntiles) {
@@ -1446,6 +1487,7 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
       } else {
         __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
       }
+      patch(t + 1, kb);
       compute(t + 1, kb);
     }
   }
@@ -1859,9 +1901,14 @@ extern "C" int qh_flash_decode_prepare(const void* q, int64_t sq, const void* k,
     DecodePrepArgs<T, C> pa{(const T*)q, (const T*)k, (const T*)v, sq, sk, sv, qw, kw, wdtype, eps,               \
                             one_plus ? 1.f : 0.f, (const C*)cos, (const C*)sin, scb, (int)cos_batch, (int)half,    \
                             (int)rot, positions, cap};                                                            \
-    fa_decode_wg_kernel<T, 128, GV, true, C><<<(unsigned)(B * Hkv), 256, 0, st>>>(                               \
-        (const T*)o, 0, 0, (const T*)k_cache, kcb, kch, kcs, (const T*)v_cache, vcb, vch, vcs, (T*)o, lse, seqlens, \
-        (int)Hkv, (int)Sk, (int)D, sl2, pa);                                                                      \
+    if (B * Hkv >= kDecodeWgMinSeqs)                                                                              \
+      fa_decode_wg_kernel<T, 128, GV, true, C><<<(unsigned)(B * Hkv), 256, 0, st>>>(                             \
+          (const T*)o, 0, 0, (const T*)k_cache, kcb, kch, kcs, (const T*)v_cache, vcb, vch, vcs, (T*)o, lse,      \
+          seqlens, (int)Hkv, (int)Sk, (int)D, sl2, pa);                                                           \
+    else                                                                                                           \
+      fa_decode_wg_kernel<T, 128, GV, true, C, false><<<(unsigned)(B * Hkv), 256, 0, st>>>(                      \
+          (const T*)o, 0, 0, (const T*)k_cache, kcb, kch, kcs, (const T*)v_cache, vcb, vch, vcs, (T*)o, lse,      \
+          seqlens, (int)Hkv, (int)Sk, (int)D, sl2, pa);                                                           \
   }
 #define QH_WGP_G(T, C) \
   if (groups == 1) QH_WGP(T, C, 1) else if (groups == 2) QH_WGP(T, C, 2) else if (groups == 4) QH_WGP(T, C, 4) else QH_WGP(T, C, 8)

@@ -497,14 +497,16 @@ __host__ __device__ constexpr int gemv_chunk(int mr, bool gated, int rc) {
 // vocabulary-wide output then queue for wave slots.
 constexpr int kGemvWideCols = 4;
 constexpr int kGemvWideMin = 32768;
+constexpr int kGemvTwoColMin = 4096;
 
-// NB weight rows per column (2: gate and up); RC columns per wave (a single
-// non-gated product; the wave's NB = RC rows are consecutive columns).
+// NB weight rows per column (2: gate and up); RC columns per wave (non-gated
+// products whose widths are multiples of RC; the wave's NB = RC rows are
+// consecutive columns of one product).
 template <typename T, typename OT, int MR, bool GATED, bool NORM, int RC = 1>
 __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ A, int64_t lda,
                                                           const DecodeProducts<T, OT> P, const DecodeNorm nrm, int M,
                                                           int K, int ncols) {
-  static_assert(RC == 1 || !GATED, "a wave takes several columns of one non-gated product only");
+  static_assert(RC == 1 || !GATED, "a wave takes several columns of non-gated products only");
   constexpr int NB = GATED ? 2 : RC;
   constexpr int CH = gemv_chunk(MR, GATED, RC);
   typedef typename Mfma<T>::v8 v8;
@@ -612,17 +614,31 @@ void launch_gemv_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int
   if (gated) P.count = 1;
   const int ncols = P.tile0[nprod];
   const bool norm = nz.w != nullptr;
-  if (!gated && nprod == 1 && ncols >= kGemvWideMin) {  // a wide single product: several columns per wave
-    const unsigned grid = (unsigned)((ncols + 4 * kGemvWideCols - 1) / (4 * kGemvWideCols));
-#define QH_GW(MRV, NV) gemv_decode_kernel<T, OT, MRV, false, NV, kGemvWideCols><<<grid, 256, 0, st>>>(a, lda, P, nz, M, K, ncols)
+  // Columns per wave: 4 for a vocabulary-wide product; 2 when that still gives 2048+ waves and
+  // no wave straddles two products (each wave re-reads the activation row and the norm weights,
+  // so fewer waves read less: the config-0 q/k/v launch, 4096 columns, 4.7 us against 7.5 us at
+  // one column); else 1 (o_proj/down, 1024 columns, are fastest at 1).
+  int rc = 1;
+  if (!gated && nprod == 1 && ncols >= kGemvWideMin) {
+    rc = kGemvWideCols;
+  } else if (!gated && ncols >= kGemvTwoColMin) {
+    rc = 2;
+    for (int i = 0; i < nprod; ++i) rc = P.N[i] % 2 ? 1 : rc;
+  }
+  if (rc > 1) {
+    const unsigned grid = (unsigned)((ncols + 4 * rc - 1) / (4 * rc));
+#define QH_GR(MRV, NV, RCV) gemv_decode_kernel<T, OT, MRV, false, NV, RCV><<<grid, 256, 0, st>>>(a, lda, P, nz, M, K, ncols)
+#define QH_GW(MRV, NV) \
+  if (rc == 2) QH_GR(MRV, NV, 2); else QH_GR(MRV, NV, kGemvWideCols);
     if constexpr (std::is_same<T, OT>::value) {
       if (norm) {
-        if (M == 1) QH_GW(1, true); else if (M == 2) QH_GW(2, true); else QH_GW(4, true);
+        if (M == 1) { QH_GW(1, true) } else if (M == 2) { QH_GW(2, true) } else { QH_GW(4, true) }
         return;
       }
     }
-    if (M == 1) QH_GW(1, false); else if (M == 2) QH_GW(2, false); else QH_GW(4, false);
+    if (M == 1) { QH_GW(1, false) } else if (M == 2) { QH_GW(2, false) } else { QH_GW(4, false) }
 #undef QH_GW
+#undef QH_GR
     return;
   }
   const unsigned grid = (unsigned)((ncols + 3) / 4);

@@ -406,14 +406,17 @@ def test_gemm_decode_shapes_deterministic(M, N, Kd):
         assert torch.equal(K.triton_matmul(x, w), y0)
 
 
-@pytest.mark.parametrize("M", [1, 5, 64, 128])
+@pytest.mark.parametrize("M", [1, 2, 5, 64, 128])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_linear_group_matches_separate_gemms(M, with_bias):
+@pytest.mark.parametrize("ns", [(2048, 1024, 1000), (2048, 1024, 1024)])
+def test_linear_group_matches_separate_gemms(M, with_bias, ns):
+    # (2048, 1024, 1024) at M <= 4: two columns per wave in the grouped launch, one per wave in
+    # the separate ones; each column is summed in the same order, so the outputs are equal
     from qwen_triton.kernels.matmul import linear_group, linear_group_ok
 
     Kd = 1024
     x = randn(M, Kd, dtype=torch.bfloat16, seed=200)
-    ws = [randn(n, Kd, dtype=torch.bfloat16, seed=201 + i, scale=0.05) for i, n in enumerate((2048, 1024, 1000))]
+    ws = [randn(n, Kd, dtype=torch.bfloat16, seed=201 + i, scale=0.05) for i, n in enumerate(ns)]
     bs = [randn(w.shape[0], dtype=torch.bfloat16, seed=210 + i) if with_bias else None for i, w in enumerate(ws)]
     assert linear_group_ok(x, ws)
     c0 = native_calls("qh_gemm_multi")
