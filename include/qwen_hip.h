@@ -395,8 +395,9 @@ int qh_attn_prepare(const void* q, int64_t sq, const void* k, int64_t sk, const 
  * seq strides (sob, soh, sos; contiguous: Hq*Sq*D, Sq*D, D; [B,Sq,Hq*D] rows for the
  * output projection: Sq*Hq*D, D, Hq*D). GQA
  * maps q-head h to kv-head h/(Hq/Hkv). Causal: key j visible to query i iff
- * j <= i + causal_offset (0 = the reference's top-left alignment). bf16/f16,
- * D % 8 == 0, D <= 128. lse may be NULL.
+ * j <= i + causal_offset (0 = the reference's top-left alignment). bf16/f16
+ * (D % 8 == 0, strides multiples of 8) or fp32 (fp32 matrix cores; D % 4 == 0,
+ * strides multiples of 4), D <= 128. lse may be NULL.
  * Replaces qwen_triton/kernels/flash_attention.py:54-152 (_flash_attn_fwd_kernel), :280-314. */
 int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
                  int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o,

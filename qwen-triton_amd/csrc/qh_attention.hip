@@ -34,6 +34,17 @@
 #include "qh_mfma.h"
 #include "qh_prep.h"
 
+// fp32 inputs (qh_attention_f32.hip): same arguments, after the shape checks.
+int qh_flash_fwd_f32(const float* q, int64_t sqb, int64_t sqh, int64_t sqs, const float* k, int64_t skb, int64_t skh,
+                     int64_t sks, const float* v, int64_t svb, int64_t svh, int64_t svs, float* o, int64_t sob,
+                     int64_t soh, int64_t sos, float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
+                     int64_t D, float scale, int causal, int64_t coff, hipStream_t st);
+int qh_flash_bwd_f32(const float* q, int64_t sqb, int64_t sqh, int64_t sqs, const float* k, int64_t skb, int64_t skh,
+                     int64_t sks, const float* v, int64_t svb, int64_t svh, int64_t svs, const float* o,
+                     const float* dout, const float* lse, float* dq, float* dk, float* dv, float* delta, float* lse2,
+                     int64_t sqp, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, float scale,
+                     int causal, int64_t coff, hipStream_t st);
+
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -1574,6 +1585,21 @@ extern "C" int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
                             void* stream) {
   QH_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0, "qh_flash_fwd: bad shape");
   QH_CHECK_ARG(Hq % Hkv == 0, "qh_flash_fwd: Hq=%lld not a multiple of Hkv=%lld", (long long)Hq, (long long)Hkv);
+  if (dtype == QH_F32) {
+    QH_CHECK_ARG(pick_dp(D) && D % 4 == 0, "qh_flash_fwd: fp32 head dim %lld must be a multiple of 4 and <= 128",
+                 (long long)D);
+    QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o), "qh_flash_fwd: pointers must be 16-byte aligned");
+    QH_CHECK_ARG(sqs % 4 == 0 && sks % 4 == 0 && svs % 4 == 0 && sqh % 4 == 0 && skh % 4 == 0 && svh % 4 == 0 &&
+                     sqb % 4 == 0 && skb % 4 == 0 && svb % 4 == 0 && sob % 4 == 0 && soh % 4 == 0 && sos % 4 == 0,
+                 "qh_flash_fwd: fp32 strides must be multiples of 4 elements");
+    QH_CHECK_ARG(B * Hq < 65536 && Sq < (1 << 30) && Sk < (1 << 30), "qh_flash_fwd: too large");
+    if (B * Hq * Sq == 0) return QH_OK;
+    qh_flash_fwd_f32((const float*)q, sqb, sqh, sqs, (const float*)k, skb, skh, sks, (const float*)v, svb, svh, svs,
+                     (float*)o, sob, soh, sos, lse, B, Hq, Hkv, Sq, Sk, D, scale, causal, causal_offset,
+                     (hipStream_t)stream);
+    QH_CHECK_LAUNCH("qh_flash_fwd");
+    return QH_OK;
+  }
   const int dp = pick_dp(D);
   QH_CHECK_ARG(dp && D % 8 == 0, "qh_flash_fwd: head dim %lld must be a multiple of 8 and <= 128", (long long)D);
   QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o), "qh_flash_fwd: pointers must be 16-byte aligned");
@@ -1641,6 +1667,34 @@ extern "C" int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
                             float scale, int causal, int64_t causal_offset, int dtype, void* stream) {
   QH_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0, "qh_flash_bwd: bad shape");
   QH_CHECK_ARG(Hq % Hkv == 0, "qh_flash_bwd: Hq not a multiple of Hkv");
+  if (dtype == QH_F32) {
+    QH_CHECK_ARG(pick_dp(D) && D % 4 == 0, "qh_flash_bwd: fp32 head dim must be a multiple of 4 and <= 128");
+    QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && aligned16(dout) && aligned16(dq) &&
+                     aligned16(dk) && aligned16(dv),
+                 "qh_flash_bwd: pointers must be 16-byte aligned");
+    QH_CHECK_ARG(sqs % 4 == 0 && sks % 4 == 0 && svs % 4 == 0 && sqh % 4 == 0 && skh % 4 == 0 && svh % 4 == 0 &&
+                     sqb % 4 == 0 && skb % 4 == 0 && svb % 4 == 0,
+                 "qh_flash_bwd: fp32 strides must be multiples of 4 elements");
+    QH_CHECK_ARG(B * Hq < 65536 && Sq < (1 << 30) && Sk < (1 << 30), "qh_flash_bwd: too large");
+    const int64_t need32 = qh_flash_bwd_workspace(B, Hq, Sq);
+    if (ws_bytes < need32) {
+      qh::set_error("qh_flash_bwd: workspace %lld < %lld", (long long)ws_bytes, (long long)need32);
+      return QH_E_WORKSPACE;
+    }
+    if (Sq == 0 || B == 0) {
+      int rc = qh_zero(dk, B * Hkv * Sk * D * 4, stream);
+      if (rc) return rc;
+      return qh_zero(dv, B * Hkv * Sk * D * 4, stream);
+    }
+    const int64_t sqp32 = bwd_row_pad(Sq);
+    float* delta32 = (float*)ws;
+    qh_flash_bwd_f32((const float*)q, sqb, sqh, sqs, (const float*)k, skb, skh, sks, (const float*)v, svb, svh, svs,
+                     (const float*)o, (const float*)dout, lse, (float*)dq, (float*)dk, (float*)dv, delta32,
+                     delta32 + B * Hq * sqp32, sqp32, B, Hq, Hkv, Sq, Sk, D, scale, causal, causal_offset,
+                     (hipStream_t)stream);
+    QH_CHECK_LAUNCH("qh_flash_bwd");
+    return QH_OK;
+  }
   const int dp = pick_dp(D);
   QH_CHECK_ARG(dp && D % 8 == 0, "qh_flash_bwd: head dim must be a multiple of 8 and <= 128");
   QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && aligned16(dout) && aligned16(dq) &&

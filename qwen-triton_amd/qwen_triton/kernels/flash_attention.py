@@ -56,8 +56,8 @@ def _check(q, k, v, num_kv_groups):
         raise Unsupported(f"flash attention shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
     if q.shape[1] != k.shape[1] * num_kv_groups:
         raise Unsupported(f"q heads {q.shape[1]} != kv heads {k.shape[1]} x groups {num_kv_groups}")
-    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.bfloat16, torch.float16):
-        raise Unsupported("flash attention kernel needs bf16 or fp16 q/k/v of one dtype")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise Unsupported("flash attention kernels need bf16, fp16 or fp32 q/k/v of one dtype")
 
 
 def flash_forward(q, k, v, scale: float, causal: bool, num_kv_groups: int, causal_offset: int = 0,
@@ -169,8 +169,8 @@ def attention(q, k, v, scale: float, causal: bool, num_kv_groups: int, causal_of
     """Dispatch used by the model layer: decode kernel for one query without grad, else flash fwd(/bwd)."""
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
         return _FlashAttentionFunction.apply(q, k, v, scale, causal, num_kv_groups, causal_offset)
-    if q.shape[2] == 1 and (not causal or causal_offset >= k.shape[2] - 1):
-        return flash_decode(q, k, v, scale, num_kv_groups)
+    if q.shape[2] == 1 and (not causal or causal_offset >= k.shape[2] - 1) and q.dtype != torch.float32:
+        return flash_decode(q, k, v, scale, num_kv_groups)  # (fp32 single queries take the forward kernel)
     return flash_forward(q, k, v, scale, causal, num_kv_groups, causal_offset, need_lse=False)[0]
 
 

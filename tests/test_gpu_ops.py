@@ -649,6 +649,50 @@ def test_flash_forward(B, Hq, Hkv, Sq, Sk, D, causal, off):
     close(lse, el, atol=2e-2, rtol=1e-3)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D,causal,off", FA_CASES + [(2, 8, 1, 100, 100, 128, True, 0),
+                                                         (1, 2, 2, 70, 70, 20, True, 0)])
+def test_flash_forward_fp32(B, Hq, Hkv, Sq, Sk, D, causal, off):
+    """fp32 q/k/v on the fp32 matrix-core kernels (as the reference runs fp32 through its kernel):
+    output and LSE against the fp64 oracle at fp32 accuracy, incl. GQA 8, a bottom-right causal
+    offset, a single query and a head dim that is not a multiple of 8."""
+    q = randn(B, Hq, Sq, D, seed=130)
+    k = randn(B, Hkv, Sk, D, seed=131)
+    v = randn(B, Hkv, Sk, D, seed=132)
+    scale = D ** -0.5
+    c0 = native_calls("qh_flash_fwd")
+    out, lse = FA.flash_forward(q, k, v, scale, causal, Hq // Hkv, off)
+    assert native_calls("qh_flash_fwd") == c0 + 1
+    eo, el = O.attention(q, k, v, scale, causal, Hq // Hkv, off)
+    close(out, eo, atol=2e-5, rtol=2e-5)
+    close(lse, el, atol=2e-5, rtol=2e-5)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [(1, 4, 2, 200, 128, True), (2, 2, 1, 96, 64, False),
+                                                 (1, 2, 2, 130, 32, True), (1, 8, 1, 150, 128, True),
+                                                 (1, 2, 1, 65, 20, False)])
+def test_flash_backward_fp32(B, Hq, Hkv, S, D, causal):
+    """fp32 backward (dK/dV over key blocks looping over the GQA group, dQ over query blocks) against
+    the fp64 oracle's gradients; two runs bitwise equal; the public API keeps fp32 on the kernels."""
+    q = randn(B, Hq, S, D, seed=140).requires_grad_(True)
+    k = randn(B, Hkv, S, D, seed=141).requires_grad_(True)
+    v = randn(B, Hkv, S, D, seed=142).requires_grad_(True)
+    go = randn(B, Hq, S, D, seed=143)
+    scale = D ** -0.5
+    cf, cb = native_calls("qh_flash_fwd"), native_calls("qh_flash_bwd")
+    out = K.triton_flash_attention(q, k, v, scale=scale, is_causal=causal, num_kv_groups=Hq // Hkv)
+    out.backward(go)
+    assert native_calls("qh_flash_fwd") == cf + 1 and native_calls("qh_flash_bwd") == cb + 1
+    dq, dk, dv = O.attention_backward(q, k, v, go, scale, causal, Hq // Hkv)
+    tol = dict(atol=1e-4, rtol=1e-4)
+    close(q.grad, dq, **tol)
+    close(k.grad, dk, **tol)
+    close(v.grad, dv, **tol)
+    g = (q.grad.clone(), k.grad.clone(), v.grad.clone())
+    q.grad = k.grad = v.grad = None
+    K.triton_flash_attention(q, k, v, scale=scale, is_causal=causal, num_kv_groups=Hq // Hkv).backward(go)
+    assert torch.equal(g[0], q.grad) and torch.equal(g[1], k.grad) and torch.equal(g[2], v.grad)
+
+
 def test_flash_public_api_matches_reference_fallback_semantics():
     q = randn(1, 4, 96, 64, dtype=torch.bfloat16, seed=103)
     k = randn(1, 2, 96, 64, dtype=torch.bfloat16, seed=104)
