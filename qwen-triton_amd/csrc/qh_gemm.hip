@@ -235,15 +235,17 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
 // k mapping per 32-wide step: lane group q = lane / 16 takes k0 + 8 q .. +7,
 // so the four groups of a row read 64 contiguous bytes.
 //
-// NORM: the rows of A are RMSNorm inputs h. The kernel multiplies the
-// operand round(h * (w + wadd)) and scales each output row by
+// NORM: the rows of A are RMSNorm inputs h. The kernel multiplies h by the
+// weight operand round((w + wadd) * B) (the norm weight applied to the weight
+// fragments: 8 NB values per lane and step instead of 8 MT activation values,
+// which every column tile would scale again) and scales each output row by
 // rsqrt(mean_k(h^2) + eps) after the sum over K: RMSNorm followed by the
-// product with the per-row factor moved past the (linear) sum, and the one
-// operand rounding taken before it. Every workgroup holds all K columns of its
-// rows (its 16 waves are the K slices, each slice loaded in one chunk), so the
-// row sums of squares are this lane's pairs (v_dot2), the four lane groups
-// of a row, then the 16 slices in order through LDS in the epilogue; the
-// multiplies never wait for them. Residual (per product, optional):
+// product with the per-row factor moved past the (linear) sum, and one
+// rounding per product term, as the separate norm's normalised operand has.
+// Every workgroup holds all K columns of its rows (its waves' K slices each
+// loaded in one chunk), so the row sums of squares are this lane's pairs
+// (v_dot2), the four lane groups of a row, then the slices in order through
+// LDS in the epilogue; the multiplies never wait for them. Residual (per product, optional):
 // C = round(round(product) + R), the residual-add kernel's rounding.
 constexpr int kMaxProducts = 4;
 template <typename T, typename OT>
@@ -263,16 +265,20 @@ struct DecodeNorm {
   float eps, wadd;
 };
 
-// k-steps whose loads one wave issues together (a NORM launch needs its whole
-// K slice in one chunk). A chunk's activation block (16 MT rows x 32 CH k) is
-// staged through the wave's 8 KB LDS slot, so MT x CH <= 8 with rows of at
-// least 128 bytes (CH >= 2).
-constexpr int kDecodeSlot = 8192;
-__host__ __device__ constexpr int decode_chunk(int mt, bool gated) {
-  return mt == 1 ? (gated ? 4 : 8) : (mt == 2 ? 4 : 2);
+// k-steps of 32 whose loads one wave issues together (a NORM launch needs its
+// whole K slice in one chunk). A chunk's activation block (16 MT rows x 32 CH k)
+// is staged in the LDS slot of the wave's K slice: 128 KB / KSP, shared by the
+// slice's 16 / KSP column groups, so MT x CH <= 128 / KSP, with rows of at least
+// 128 bytes (CH >= 2). Weight fragments of a chunk stay in registers (CH x NB).
+constexpr int kDecodeLds = 128 * 1024;
+__host__ __device__ constexpr int decode_chunk(int mt, bool gated, int ksp = 16) {
+  return ksp >= 16 ? (mt == 1 ? (gated ? 4 : 8) : (mt == 2 ? 4 : 2))
+                   : (mt <= 2 ? (gated ? 4 : 8) : (gated ? 4 : (ksp <= 4 ? 8 : 4)));
 }
-// NORM launches hold the row scaling beside the fragments; the same chunks.
-__host__ __device__ constexpr int decode_norm_chunk(int mt, bool gated) { return decode_chunk(mt, gated); }
+// NORM launches: the same chunks.
+__host__ __device__ constexpr int decode_norm_chunk(int mt, bool gated, int ksp = 16) {
+  return decode_chunk(mt, gated, ksp);
+}
 // Longest row a NORM launch normalises.
 constexpr int kDecodeNormMaxK = 8192;
 
@@ -304,21 +310,22 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
                                                            const DecodeProducts<T, OT> P, const DecodeNorm nrm,
                                                            int M, int K, int kr, int ms, int tiles) {
   constexpr int CG = 16 / KSP;
-  constexpr int NB = GATED ? 2 : 1;                       // weight matrices per wave
-  constexpr int CH = NORM ? decode_norm_chunk(MT, GATED) : decode_chunk(MT, GATED);  // k-steps loaded together
-  static_assert(!NORM || KSP == 16, "the norm prologue needs all 16 waves on K slices");
+  constexpr int NB = GATED ? 2 : 1;                   // weight matrices per wave
+  constexpr int CH = decode_chunk(MT, GATED, KSP);    // k-steps loaded together
   typedef typename Mfma<T>::v8 v8;
-  // Activation rows of a chunk: each wave DMAs its 16 MT x (64 CH bytes) block
-  // into its own slot as whole 128-byte lines (a row-per-lane fragment load
-  // would touch 16 half-used lines per instruction, measured 3-4x slower from
-  // L2), 16-byte slots XOR-swizzled per row so the fragment reads are
-  // conflict-free. The K-slice sums reuse the slots after a barrier.
-  constexpr int RB = CH * 64;   // bytes of one activation row in a chunk
-  constexpr int S16 = RB / 16;  // 16-byte slots per row
-  static_assert(MT * 16 * RB <= kDecodeSlot && CH >= 2, "activation block exceeds the wave's LDS slot");
-  static_assert(16 * MT * 16 * 16 * 4 <= 16 * kDecodeSlot, "K-slice sums exceed the slots");
-  __shared__ __align__(16) unsigned char aslot[16][kDecodeSlot];
-  float(*red)[MT * 16][16] = reinterpret_cast<float(*)[MT * 16][16]>(&aslot[0][0]);
+  // Activation rows of a chunk: the waves of a K slice DMA its 16 MT x (64 CH
+  // bytes) block into the slice's LDS slot as whole 128-byte lines (a row-per-
+  // lane fragment load would touch 16 half-used lines per instruction, measured
+  // 3-4x slower from L2), 16-byte slots XOR-swizzled per row so the fragment
+  // reads are conflict-free; the slice's CG column groups share the block. The
+  // K-slice sums reuse the slots after a barrier.
+  constexpr int SLOT = kDecodeLds / KSP;  // LDS bytes per K slice
+  constexpr int RB = CH * 64;             // bytes of one activation row in a chunk
+  constexpr int S16 = RB / 16;            // 16-byte slots per row
+  static_assert(MT * 16 * RB <= SLOT && CH >= 2, "activation block exceeds the slice's LDS slot");
+  static_assert(16 * MT * 16 * 16 * 4 <= kDecodeLds, "K-slice sums exceed the slots");
+  __shared__ __align__(16) unsigned char abuf[kDecodeLds];
+  float(*red)[MT * 16][16] = reinterpret_cast<float(*)[MT * 16][16]>(abuf);
   __shared__ float nss[NORM ? 16 : 1][MT * 16];
   // Workgroup -> (column tile, row group). The ms row groups of a tile get
   // workgroup ids that are equal mod 8, so they run on one XCD and read the
@@ -350,17 +357,25 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   v8 zero;
 #pragma unroll
   for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
-  // With NORM every wave runs exactly one chunk (slices past K load zeros), so
-  // all of them reach the barrier of the norm reduction.
-  for (int k0 = kb; NORM ? k0 == kb : k0 < ke; k0 += 32 * CH) {
-    v8 b[CH][NB], a[CH][MT];
-    v8 wr[NORM ? CH : 1];  // norm weights (dtype T) of this lane's 8 columns per step
-    // slot s of row r holds the row's 16-byte chunk s ^ swz(r)
-    auto swz = [](int r) { return S16 >= 16 ? (r & 15) : ((r >> 1) & 7); };
-    if (k0 != kb) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // previous chunk's fragments read
-    const uint32_t abase = lds_addr(&aslot[wid][0]);
+  // Every wave runs the same number of chunks (with NORM exactly one; slices
+  // past K load zeros), so all of them reach the barriers.
+  auto swz = [](int r) { return S16 >= 16 ? (r & 15) : ((r >> 1) & 7); };  // slot s of row r: chunk s ^ swz(r)
+  unsigned char* slot = abuf + ks * SLOT;
+  const uint32_t abase = lds_addr(slot);
+  const int nch = NORM ? 1 : (kr + 32 * CH - 1) / (32 * CH);
+  float sq[MT];  // NORM: this lane's row sums of squares
 #pragma unroll
-    for (int j = 0; j < MT * CH; ++j) {
+  for (int i = 0; i < MT; ++i) sq[i] = 0.f;
+  for (int ci = 0; ci < nch; ++ci) {
+    const int k0 = kb + ci * 32 * CH;
+    v8 b[CH][NB];
+    v8 wr[NORM ? CH : 1];  // norm weights (dtype T) of this lane's 8 columns per step
+    if (ci > 0) {  // the previous chunk's fragments have been read from the slot
+      if constexpr (CG > 1) __syncthreads();
+      else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+#pragma unroll
+    for (int j = cg; j < MT * CH; j += CG) {
       const int c = j * 64 + lane, r = c / S16;
       const int m = m0 + r, k = k0 + ((c % S16) ^ swz(r)) * 8;
       // rows past M and chunks past the slice stage A[0..7] (in bounds; zeroed below)
@@ -370,9 +385,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
     for (int u = 0; u < CH; ++u) {
       const int k = k0 + u * 32 + q * 8;
       const bool kok = k < ke;
-      if constexpr (NORM) {
-        if (kok) wr[u] = *reinterpret_cast<const v8*>((const T*)nrm.w + k);
-      }
+      if constexpr (NORM) wr[u] = kok ? *reinterpret_cast<const v8*>((const T*)nrm.w + k) : zero;
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
         // weights read by one workgroup per decode step: non-temporal, so they do not evict cached data
@@ -385,48 +398,38 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged rows (untracked DMA) and the weights
+    if constexpr (CG > 1) __syncthreads();             // and the slice's other column groups' rows
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const bool kok = k0 + u * 32 + q * 8 < ke;
+      if constexpr (NORM) {  // the weight operand round((w + wadd) * B): 8 NB values per lane, not 8 MT
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float wv = to_f32(wr[u][e]) + nrm.wadd;
+#pragma unroll
+          for (int j = 0; j < NB; ++j) b[u][j][e] = from_f32<T>(to_f32(b[u][j][e]) * wv);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const int r = i * 16 + li;
-        if (m0 + r < M && kok)
-          a[u][i] = *reinterpret_cast<const v8*>(&aslot[wid][r * RB + (((u * 4 + q) ^ swz(r)) << 4)]);
-        else
-          a[u][i] = zero;
+        v8 a;
+        if (m0 + r < M && kok) a = *reinterpret_cast<const v8*>(slot + r * RB + (((u * 4 + q) ^ swz(r)) << 4));
+        else a = zero;
+        if constexpr (NORM) sq[i] = sumsq8<T>(a, sq[i]);  // row sums of squares (the epilogue adds the slices)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[j][i] = mma16<T>(a, b[u][j], acc[j][i]);
       }
     }
-    if constexpr (NORM) {
-      // Row sums of squares of h (the epilogue adds the slices), then the
-      // operands round(h * (w + wadd)).
+  }
+  if constexpr (NORM) {
 #pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        float ss = 0.f;
-#pragma unroll
-        for (int u = 0; u < CH; ++u) ss = sumsq8<T>(a[u][i], ss);
-        ss += __shfl_xor(ss, 16);
-        ss += __shfl_xor(ss, 32);
-        if (q == 0) nss[wid][i * 16 + li] = ss;
-      }
-#pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        if (k0 + u * 32 + q * 8 >= ke) continue;  // a[u][*] is zero there
-        float wv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) wv[e] = to_f32(wr[u][e]) + nrm.wadd;
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a[u][i][e] = from_f32<T>(to_f32(a[u][i][e]) * wv[e]);
-      }
+    for (int i = 0; i < MT; ++i) {
+      float v = sq[i];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (q == 0) nss[wid][i * 16 + li] = v;
     }
-#pragma unroll
-    for (int u = 0; u < CH; ++u)
-#pragma unroll
-      for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int i = 0; i < MT; ++i) acc[j][i] = mma16<T>(a[u][i], b[u][j], acc[j][i]);
   }
   // Sum the K slices in order, one weight matrix at a time through the same
   // LDS buffer. C layout: column li, rows 16 i + 4 q + r.
@@ -453,7 +456,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
       if constexpr (NORM) {  // the row's RMSNorm factor (slices summed in order)
         float ss = 0.f;
 #pragma unroll
-        for (int s2 = 0; s2 < 16; ++s2) ss += nss[s2][row];
+        for (int s2 = 0; s2 < KSP; ++s2) ss += nss[s2][row];  // column group 0's slices
         v *= rsqrtf(ss / (float)K + nrm.eps);
       }
       const float val = v + (bias ? to_f32(bias[gn]) : 0.f);
@@ -483,9 +486,11 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
 // workgroup 16 columns, so o_proj/down (1024 columns) ran on 64 workgroups;
 // this kernel gives every 4 columns a workgroup (256+ for 1024 columns) and
 // measured 2.9-4.1 us for the 4-12 MB config-0 products against 4.8-7.3 us.
-// Same fusions and rounding points as gemm_decode_kernel: NORM (operand
-// round(h * (w + wadd)), row factor rsqrt(mean(h^2) + eps) after the sum),
-// bias, residual round(round(product) + R), GATED silu(round(g)) * round(u).
+// Same fusions as gemm_decode_kernel: NORM (row factor rsqrt(mean(h^2) + eps)
+// after the sum; here the activation operand round(h * (w + wadd)) is the one
+// rounded, 8 MR values per lane and step, where the MFMA kernel rounds the
+// weight operand), bias, residual round(round(product) + R), GATED
+// silu(round(g)) * round(u).
 constexpr int kGemvMaxRows = 4;
 
 // 16-byte loads per lane and operand row in one chunk (512 K values each).
@@ -658,40 +663,69 @@ void launch_gemv_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int
 
 // Returns QH_E_ARG (nothing launched) when a norm prologue is asked for a
 // shape whose K slices do not fit one load chunk (decode_norm_fits).
+// Launch shape of a decode-kernel launch. K slices per column group (ksp): 4
+// for wide outputs (4 column groups x 4 slices); 8 from 65 rows when 16-column
+// tiles would need more than one workgroup per CU (2 column groups share each
+// slice's activation block: a 128-row q/k/v launch 11.9 us instead of 14.0, gate/
+// up 16.3 instead of 18.0; slower at 1024 columns and at 64 rows); else 16. Row
+// groups per column tile (ms): with few column tiles, up to one workgroup per
+// 16 rows, until about one workgroup per CU.
+struct DecodePlan {
+  int ksp, cols, tiles, kr, ms, mtw;
+  bool norm_fits;
+};
+
+static DecodePlan decode_plan(int M, int K, bool gated, bool norm, int count, const int* N, int ksp_force,
+                              int ms_force) {
+  DecodePlan d{};
+  int maxN = 0;
+  for (int i = 0; i < count; ++i) maxN = N[i] > maxN ? N[i] : maxN;
+  const bool wide = !gated && !norm && maxN > 8192;
+  const int mt = (M + 15) / 16;
+  d.ksp = wide ? 4 : 16;
+  if (!wide && mt > 4) {  // 8 slices when 16-column tiles would need more than one workgroup per CU
+    int t16 = 0;
+    for (int i = 0; i < (gated ? 1 : count); ++i) t16 += (N[i] + 15) / 16;
+    int ms16 = 1;
+    while (ms16 * 4 < mt) ms16 *= 2;
+    if (t16 * ms16 > 256) d.ksp = 8;
+  }
+  if (!wide && (ksp_force == 8 || ksp_force == 16)) d.ksp = ksp_force;
+  d.cols = 16 * (16 / d.ksp);
+  const int nprod = gated ? 1 : count;  // the gated pair shares its column tiles
+  d.tiles = 0;
+  for (int i = 0; i < nprod; ++i) d.tiles += (N[i] + d.cols - 1) / d.cols;
+  d.kr = ((K + d.ksp - 1) / d.ksp + 31) / 32 * 32;
+  int ms = 1;
+  while (ms * 4 < mt) ms *= 2;  // at most 4 row tiles (64 rows) per workgroup
+  while (ms < mt && d.tiles * ms * 2 <= 256) ms *= 2;
+  if (ms > mt) ms = mt;
+  if (ms_force > 0 && ms_force <= mt) ms = ms_force;
+  d.ms = ms;
+  d.mtw = (mt + ms - 1) / ms;
+  d.norm_fits = K <= kDecodeNormMaxK && d.kr <= 32 * decode_norm_chunk(d.mtw, gated, d.ksp);
+  return d;
+}
+
+// Returns QH_E_ARG (nothing launched) when a norm prologue is asked for a
+// shape whose K slices do not fit one load chunk (decode_norm_fits).
 template <typename T, typename OT>
 int launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int M, int K, bool gated,
-                           hipStream_t st, int ms_force = 0, const DecodeNorm* nrm = nullptr) {
-  // Narrow outputs: all 16 waves split K (16 columns per workgroup). Wide
-  // outputs already give enough workgroups: 4 column groups x 4 K slices.
+                           hipStream_t st, int ms_force = 0, const DecodeNorm* nrm = nullptr, int ksp_force = 0) {
   const bool norm = nrm != nullptr && nrm->w != nullptr;
-  if (M <= kGemvMaxRows && ms_force == 0) {
+  if (M <= kGemvMaxRows && ms_force == 0 && ksp_force == 0) {
     if (norm && !std::is_same<T, OT>::value) return QH_E_ARG;
     launch_gemv_products<T, OT>(a, lda, P, M, K, gated, norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f}, st);
     return QH_OK;
   }
-  int maxN = 0;
-  for (int i = 0; i < P.count; ++i) maxN = P.N[i] > maxN ? P.N[i] : maxN;
-  const bool wide = !gated && !norm && maxN > 8192;
-  const int ksp = wide ? 4 : 16;
-  const int cols = 16 * (16 / ksp);
-  const int nprod = gated ? 1 : P.count;  // the gated pair shares its column tiles
+  const DecodePlan d = decode_plan(M, K, gated, norm, P.count, P.N, ksp_force, ms_force);
+  const int nprod = gated ? 1 : P.count;
   P.tile0[0] = 0;
-  for (int i = 0; i < nprod; ++i) P.tile0[i + 1] = P.tile0[i] + (P.N[i] + cols - 1) / cols;
+  for (int i = 0; i < nprod; ++i) P.tile0[i + 1] = P.tile0[i] + (P.N[i] + d.cols - 1) / d.cols;
   if (gated) P.count = 1;
-  const int tiles = P.tile0[nprod];
-  const int kr = ((K + ksp - 1) / ksp + 31) / 32 * 32;
-  const int mt = (M + 15) / 16;
-  // Row groups per column tile: with few column tiles, up to one workgroup
-  // per 16 rows, until about one workgroup per CU (measured best: 1024-column
-  // outputs split 4 ways, 2048 two ways, 3072 not at all).
-  int ms = 1;
-  while (ms * 4 < mt) ms *= 2;  // at most 4 row tiles (64 rows) per workgroup
-  while (ms < mt && tiles * ms * 2 <= 256) ms *= 2;
-  if (ms > mt) ms = mt;
-  if (ms_force > 0 && ms_force <= mt) ms = ms_force;
-  const int mtw = (mt + ms - 1) / ms;
+  const int tiles = d.tiles, kr = d.kr, ms = d.ms, mtw = d.mtw, ksp = d.ksp;
   const int grid = (tiles + 7) / 8 * 8 * ms;
-  if (norm && (K > kDecodeNormMaxK || kr > 32 * decode_norm_chunk(mtw, gated))) return QH_E_ARG;
+  if (norm && !d.norm_fits) return QH_E_ARG;
   const DecodeNorm nz = norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f};
   constexpr bool kNormOk = std::is_same<T, OT>::value;  // the only instantiation a norm launch reaches
   if (norm && !kNormOk) return QH_E_ARG;
@@ -700,37 +734,32 @@ int launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, in
     if (ms == 1) gemm_decode_kernel<T, OT, MTV, KSPV, GV, NV, true><<<grid, 1024, 0, st>>>(a, lda, P, nz, M, K, kr, ms, tiles); \
     else gemm_decode_kernel<T, OT, MTV, KSPV, GV, NV, false><<<grid, 1024, 0, st>>>(a, lda, P, nz, M, K, kr, ms, tiles); \
   } while (0)
+#define QH_DG_K(MTV, GV, NV) \
+  if (ksp == 8) QH_DG(MTV, 8, GV, NV); else QH_DG(MTV, 16, GV, NV);
 #define QH_DG_W(MTV)                                           \
   if constexpr (kNormOk) {                                     \
     if (norm) {                                                \
-      if (gated) QH_DG(MTV, 16, true, true); else QH_DG(MTV, 16, false, true); \
+      if (gated) { QH_DG_K(MTV, true, true) } else { QH_DG_K(MTV, false, true) } \
       return QH_OK;                                            \
     }                                                          \
   }                                                            \
-  if (gated) QH_DG(MTV, 16, true, false);                      \
-  else if (wide) QH_DG(MTV, 4, false, false);                  \
-  else QH_DG(MTV, 16, false, false);
+  if (gated) { QH_DG_K(MTV, true, false) }                     \
+  else if (ksp == 4) QH_DG(MTV, 4, false, false);              \
+  else { QH_DG_K(MTV, false, false) }
   if (mtw == 1) { QH_DG_W(1) } else if (mtw == 2) { QH_DG_W(2) } else if (mtw == 3) { QH_DG_W(3) } else { QH_DG_W(4) }
 #undef QH_DG_W
+#undef QH_DG_K
 #undef QH_DG
   return QH_OK;
 }
 
-// Whether a norm-prologue launch of M rows, K columns fits (all 16 K slices
-// of every workgroup loaded in one chunk); mirrors launch_decode_products.
+// Whether a norm-prologue launch of M rows, K columns fits (all K slices of
+// every workgroup loaded in one chunk); mirrors launch_decode_products.
 static bool decode_norm_fits(int M, int K, bool gated, int count, const int64_t* N) {
   if (M <= kGemvMaxRows) return true;  // the one-wave-per-column kernel normalises any K
-  const int cols = 16;
-  int tiles = 0;
-  for (int i = 0; i < (gated ? 1 : count); ++i) tiles += (int)((N[i] + cols - 1) / cols);
-  const int kr = ((K + 15) / 16 + 31) / 32 * 32;
-  const int mt = (M + 15) / 16;
-  int ms = 1;
-  while (ms * 4 < mt) ms *= 2;
-  while (ms < mt && tiles * ms * 2 <= 256) ms *= 2;
-  if (ms > mt) ms = mt;
-  const int mtw = (mt + ms - 1) / ms;
-  return K <= kDecodeNormMaxK && kr <= 32 * decode_norm_chunk(mtw, gated);
+  int n32[kMaxProducts];
+  for (int i = 0; i < count && i < kMaxProducts; ++i) n32[i] = (int)N[i];
+  return decode_plan(M, K, gated, true, count, n32, 0, 0).norm_fits;
 }
 
 template <typename T, typename OT>

@@ -411,7 +411,10 @@ def test_gemm_decode_shapes_deterministic(M, N, Kd):
 @pytest.mark.parametrize("ns", [(2048, 1024, 1000), (2048, 1024, 1024)])
 def test_linear_group_matches_separate_gemms(M, with_bias, ns):
     # (2048, 1024, 1024) at M <= 4: two columns per wave in the grouped launch, one per wave in
-    # the separate ones; each column is summed in the same order, so the outputs are equal
+    # the separate ones; each column is summed in the same order, so the outputs are equal. At 128
+    # rows the grouped launch (4096 columns) splits K into 8 slices per column group, as its
+    # 16-column tiles would need two workgroups per CU, and a single product into 16: equal within
+    # the fp32 summation order there.
     from qwen_triton.kernels.matmul import linear_group, linear_group_ok
 
     Kd = 1024
@@ -423,7 +426,11 @@ def test_linear_group_matches_separate_gemms(M, with_bias, ns):
     outs = linear_group(x, ws, bs)
     assert native_calls("qh_gemm_multi") == c0 + 1
     for w, b, o in zip(ws, bs, outs):
-        assert torch.equal(o, K.triton_matmul(x, w, b))
+        if M <= 64:
+            assert torch.equal(o, K.triton_matmul(x, w, b))
+        else:
+            sep = K.triton_matmul(x, w, b).float()
+            assert (o.float() - sep).abs().max().item() <= 1e-2 * sep.abs().max().item()
 
 
 @pytest.mark.parametrize("M", [1, 17, 64])
@@ -464,19 +471,24 @@ def test_linear_group_norm_prologue(M, gated, dtype):
     plain = linear_group(y, ws, gated=gated)
     fused, plain = ([fused], [plain]) if gated else (fused, plain)
     # fp64 oracles with each path's rounding points: the reference rounds the normalised
-    # rows (plain path); the fused path rounds x * w and applies the row factor after the
-    # product. Both round gate and up before the SiLU-mul.
+    # rows (plain path); the fused path applies the row factor after the product, with the one
+    # rounding on x * w (at most 4 rows, one wave per column) or on w * W (the MFMA kernel, more
+    # rows: it scales the weight fragments). Both round gate and up before the SiLU-mul.
     bf = lambda t: t.to(dtype).to(torch.float64)  # noqa: E731
     xd = x.cpu().double()
+    nwd = nw.cpu().double()
     inv = torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6)
     yo = bf(O.rmsnorm(x, nw, 1e-6))
-    yw = bf(xd * nw.cpu().double())
 
-    def prods(y, scale):
-        outs = [O.linear(y, w) * scale for w in ws]
+    def prods(y, scale, weights):
+        outs = [O.linear(y, w) * scale for w in weights]
         return [O.silu_mul(bf(outs[0]), bf(outs[1]))] if gated else outs
 
-    for f, p_, r_plain, r_fused in zip(fused, plain, prods(yo, 1.0), prods(yw, inv)):
+    if M <= 4:
+        r_fused_all = prods(bf(xd * nwd), inv, ws)
+    else:
+        r_fused_all = prods(xd, inv, [bf(w.cpu().double() * nwd[None, :]) for w in ws])
+    for f, p_, r_plain, r_fused in zip(fused, plain, prods(yo, 1.0, ws), r_fused_all):
         # a few rounding steps of the largest output (one bf16 step is 2^-8 to 2^-7 relative):
         # the reference's bf16 band taken relative to the output scale
         assert (f.float() - p_.float()).abs().max().item() <= 2e-2 * p_.float().abs().max().item() + 1e-3
