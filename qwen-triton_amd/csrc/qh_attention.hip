@@ -615,6 +615,91 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
   }
 }
 
+// LDS layout of the 8-wave dK/dV kernel (bytes): K and V of the block, two
+// stages of Q and of dO, two stages of the tile's lse2 | Delta rows. A stage
+// is selected by one address bit (each region is aligned to twice its stage
+// size), so the per-lane fragment offsets switch stage with one XOR per tile.
+template <int DP>
+struct DkdvLds {
+  static constexpr int BQ = 64, KB = 128;
+  static constexpr uint32_t K = 0, V = KB * DP * 2, Q = 2 * V, QSTAGE = BQ * DP * 2, O = Q + 2 * QSTAGE,
+                            L = O + 2 * QSTAGE, LSTAGE = 2 * BQ * 4, DELTA = BQ * 4, BYTES = L + 2 * LSTAGE;
+  static_assert((QSTAGE & (QSTAGE - 1)) == 0 && Q % (2 * QSTAGE) == 0 && O % (2 * QSTAGE) == 0,
+                "Q/dO stages must differ in one address bit");
+  static_assert((LSTAGE & (LSTAGE - 1)) == 0 && L % (2 * LSTAGE) == 0, "lse stages must differ in one address bit");
+  static_assert(O - Q < 65536 && V - K < 65536, "partner operands must be an immediate offset apart");
+};
+
+// Per-lane LDS addresses of one wavefront's fragment reads (loop-invariant
+// apart from the stage bit; the dynamic LDS block's own address included, so
+// that every read is a register plus an immediate): K fragments of each k16 step (V = +V-K), Q rows of
+// each k16 step in the current stage (dO = +O-Q), the transposed Q/dO reads of
+// each 32-column block at query rows r and r + 8 (the second 16-query step is
+// +16 rows), and the lane's first lse value.
+template <int DP>
+struct DkdvOffsets {
+  static constexpr int KD = DP / 16, DT = DP / 32;
+  uint32_t kv[KD], qo[KD], tr[DT][2], ls;
+};
+
+template <int DP>
+__device__ __forceinline__ DkdvOffsets<DP> dkdv_offsets(const unsigned char* lds, int ks, int qt, int lane) {
+  typedef DkdvLds<DP> L;
+  constexpr int CPR = DP / 8;
+  const uint32_t base = lds_addr(lds);
+  const int ql = lane & 31, hf = lane >> 5, grp = lane >> 4, j = lane & 15;
+  const int row = qt * 32 + ql, key = ks * 32 + ql;
+  DkdvOffsets<DP> o;
+#pragma unroll
+  for (int kd = 0; kd < DkdvOffsets<DP>::KD; ++kd) {
+    o.kv[kd] = base + L::K + (key * CPR + swz(key, kd * 2 + hf, CPR)) * 16;
+    o.qo[kd] = base + L::Q + (row * CPR + swz(row, kd * 2 + hf, CPR)) * 16;
+  }
+  const int qrow = qt * 32 + 4 * (grp >> 1) + (j >> 2);
+#pragma unroll
+  for (int dt = 0; dt < DkdvOffsets<DP>::DT; ++dt) {
+    const int d = dt * 32 + 16 * (grp & 1) + 4 * (j & 3);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = qrow + 8 * h;
+      o.tr[dt][h] = base + L::Q + (r * CPR + swz(r, d >> 3, CPR)) * 16 + (d & 7) * 2;
+    }
+  }
+  o.ls = base + L::L + (qt * 32 + hf * 4) * 4;
+  return o;
+}
+
+template <int DP>
+__device__ __forceinline__ void dkdv_next_stage(DkdvOffsets<DP>& o) {
+  typedef DkdvLds<DP> L;
+#pragma unroll
+  for (int kd = 0; kd < DkdvOffsets<DP>::KD; ++kd) o.qo[kd] ^= L::QSTAGE;
+#pragma unroll
+  for (int dt = 0; dt < DkdvOffsets<DP>::DT; ++dt) o.tr[dt][0] ^= L::QSTAGE, o.tr[dt][1] ^= L::QSTAGE;
+  o.ls ^= L::LSTAGE;
+}
+
+typedef const __attribute__((address_space(3))) unsigned char lds_u8;
+typedef float lds_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ lds_u8* lds_at(uint32_t a) { return (lds_u8*)(uintptr_t)a; }
+
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::v8 lds_frag16(uint32_t a, uint32_t imm = 0) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) typename Mfma<T>::v8*>(lds_at(a) + imm);
+}
+
+// One transposed A-operand fragment from two 8-byte transpose reads (rows r and
+// r + 8 of a 4-row x 4-column block per 16 lanes), joined as whole vectors.
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::v8 lds_tr_frag(uint32_t a0, uint32_t a1, uint32_t imm) {
+  typedef __attribute__((address_space(3))) qh_v4i16 lv4;
+  const qh_v4i16 w0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lv4*)(lds_at(a0) + imm));
+  const qh_v4i16 w1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lv4*)(lds_at(a1) + imm));
+  const qh_v8i16 w = __builtin_shufflevector(w0, w1, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(typename Mfma<T>::v8, w);
+}
+
 // dK/dV for 128 keys of one (b, kv-head) with 8 wavefronts, two per SIMD:
 // wavefront w owns keys k0 + 32 (w & 3) .. + 31 and, of every 64-query tile,
 // the 32 queries of half w >> 2. K and V of the workgroup's keys are staged in
@@ -624,30 +709,26 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
 // Delta values (a global load inside the loop would make the compiler's
 // vmcnt wait also cover the next tile's untracked LDS fill). At the end the two
 // query halves' dK/dV partials are added in a fixed order (half 0 + half 1)
-// through LDS. Same per-tile arithmetic as fa_bwd_dkdv_tile.
+// through LDS. Same per-tile arithmetic as fa_bwd_dkdv_tile. Every fragment
+// read is a per-lane offset (DkdvOffsets) plus an immediate.
 template <typename T, int DP>
-__device__ __forceinline__ void fa_bwd_dkdv_half(const T* Qt, const T* Ot, const T* Kk, const T* Vk,
-                                                 f32x16 (&dk)[DP / 32], f32x16 (&dv)[DP / 32],
-                                                 const float* __restrict__ lse_row, const float* __restrict__ dl_row,
-                                                 int q0, int qt, bool need_mask, int q_lo, int q_hi,
-                                                 float scale_log2, int lane) {
-  constexpr int CPR = DP / 8, DT = DP / 32, KD = DP / 16;
+__device__ __forceinline__ void fa_bwd_dkdv_half(const DkdvOffsets<DP>& o,
+                                                 f32x16 (&dk)[DP / 32], f32x16 (&dv)[DP / 32], int q0, int qt,
+                                                 bool need_mask, int q_lo, int q_hi, float scale_log2, int lane) {
+  typedef DkdvLds<DP> L;
+  constexpr int DT = DP / 32, KD = DP / 16;
   typedef typename Mfma<T>::v8 v8;
-  const int ql = lane & 31, hf = lane >> 5;
-  const int grp = lane >> 4, j = lane & 15;
-  const int row = qt * 32 + ql;
+  const int hf = lane >> 5;
   // S and dP: each k16 step's four fragments are read one step ahead; the
   // scheduling barriers keep the reads from being hoisted further (registers
   // for two wavefronts per SIMD), the other wavefront covers the latency.
   f32x16 sc = zero16(), dp = zero16();
   v8 fq[2], fk[2], fo[2], fv[2];
   auto rd_s = [&](int kd, int b) {
-    const int c = swz(row, kd * 2 + hf, CPR);
-    const int cv = swz(ql, kd * 2 + hf, CPR);
-    fq[b] = load_frag16<T>(Qt + row * DP + c * 8);
-    fk[b] = load_frag16<T>(Kk + ql * DP + cv * 8);
-    fo[b] = load_frag16<T>(Ot + row * DP + c * 8);
-    fv[b] = load_frag16<T>(Vk + ql * DP + cv * 8);
+    fq[b] = lds_frag16<T>(o.qo[kd]);
+    fk[b] = lds_frag16<T>(o.kv[kd]);
+    fo[b] = lds_frag16<T>(o.qo[kd], L::O - L::Q);
+    fv[b] = lds_frag16<T>(o.kv[kd], L::V - L::K);
   };
   rd_s(0, 0);
 #pragma unroll
@@ -661,21 +742,25 @@ __device__ __forceinline__ void fa_bwd_dkdv_half(const T* Qt, const T* Ot, const
   // copy (read here: holding them across the products would cost 32 registers)
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    const int il = qt * 32 + g * 8 + hf * 4;
-    const float4 ls = *reinterpret_cast<const float4*>(lse_row + il);
-    const float4 dl = *reinterpret_cast<const float4*>(dl_row + il);
-    const float lv[4] = {ls.x, ls.y, ls.z, ls.w};
-    const float dv4[4] = {dl.x, dl.y, dl.z, dl.w};
+    const lds_f32x4 lv = *reinterpret_cast<const __attribute__((address_space(3))) lds_f32x4*>(lds_at(o.ls) + g * 32);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float p = exp2_(__builtin_fmaf(sc[g * 4 + r], scale_log2, -lv[r]));
-      if (need_mask) {
-        const int qi = q0 + qt * 32 + g * 8 + hf * 4 + r;
-        p = (qi >= q_lo && qi < q_hi) ? p : 0.f;
-      }
-      sc[g * 4 + r] = p;
-      dp[g * 4 + r] = p * (dp[g * 4 + r] - dv4[r]);
+    for (int r = 0; r < 4; ++r) sc[g * 4 + r] = exp2_(__builtin_fmaf(sc[g * 4 + r], scale_log2, -lv[r]));
+  }
+  // masked scores (diagonal and tail tiles only: the flag is wave-uniform, so
+  // the other tiles branch past the compares and selects)
+  if (__builtin_amdgcn_readfirstlane((int)need_mask)) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int qi = q0 + qt * 32 + (e >> 2) * 8 + hf * 4 + (e & 3);
+      sc[e] = (qi >= q_lo && qi < q_hi) ? sc[e] : 0.f;
     }
+  }
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const lds_f32x4 dv4 =
+        *reinterpret_cast<const __attribute__((address_space(3))) lds_f32x4*>(lds_at(o.ls) + L::DELTA + g * 32);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dp[g * 4 + r] = sc[g * 4 + r] * (dp[g * 4 + r] - dv4[r]);
   }
   // dV += dO^T P, dK += Q^T dS with the transposed operands read one step ahead.
   const v8 pf[2] = {pack_pair<T>(sc, 0), pack_pair<T>(sc, 2)};
@@ -683,10 +768,9 @@ __device__ __forceinline__ void fa_bwd_dkdv_half(const T* Qt, const T* Ot, const
   v8 ta[2], tb[2];
   auto rd_t = [&](int st, int b) {
     const int ks = st / DT, dt = st % DT;
-    const int qrow = qt * 32 + ks * 16 + 4 * (grp >> 1) + (j >> 2);
-    const int d = dt * 32 + 16 * (grp & 1) + 4 * (j & 3);
-    ta[b] = read_vt_frag<T, DP>(Ot, qrow, d);
-    tb[b] = read_vt_frag<T, DP>(Qt, qrow, d);
+    const uint32_t rs = ks * 16 * DP * 2;  // second 16-query step: 16 rows on
+    ta[b] = lds_tr_frag<T>(o.tr[dt][0], o.tr[dt][1], rs + (L::O - L::Q));
+    tb[b] = lds_tr_frag<T>(o.tr[dt][0], o.tr[dt][1], rs);
   };
   rd_t(0, 0);
 #pragma unroll
@@ -706,15 +790,15 @@ __global__ __launch_bounds__(512) void fa_bwd_dkdv8_kernel(
     const float* __restrict__ LSE2, const float* __restrict__ Delta, int64_t sqp, T* __restrict__ dK,
     T* __restrict__ dV, int Hq, int Hkv, int groups, int Sq, int Sk, int D, float scale_log2, float scale, int causal,
     int coff) {
-  constexpr int BQ = 64, KB = 128;
-  constexpr int DT = DP / 32, KD = DP / 16;
-  typedef typename Mfma<T>::v8 v8;
+  typedef DkdvLds<DP> L;
+  constexpr int BQ = L::BQ, KB = L::KB;
+  constexpr int DT = DP / 32;
   extern __shared__ __attribute__((aligned(1024))) unsigned char qh_dkdv_smem[];
-  T* Ks = reinterpret_cast<T*>(qh_dkdv_smem);  // [KB][DP]
-  T* Vs = Ks + KB * DP;                         // [KB][DP]
-  T* Qs = Vs + KB * DP;                         // [2][BQ][DP]
-  T* Os = Qs + 2 * BQ * DP;                     // [2][BQ][DP]
-  float* Ls = reinterpret_cast<float*>(Os + 2 * BQ * DP);  // [2][lse2 BQ | Delta BQ]
+  T* Ks = reinterpret_cast<T*>(qh_dkdv_smem + L::K);      // [KB][DP]
+  T* Vs = reinterpret_cast<T*>(qh_dkdv_smem + L::V);      // [KB][DP]
+  T* Qs = reinterpret_cast<T*>(qh_dkdv_smem + L::Q);      // [2][BQ][DP]
+  T* Os = reinterpret_cast<T*>(qh_dkdv_smem + L::O);      // [2][BQ][DP]
+  float* Ls = reinterpret_cast<float*>(qh_dkdv_smem + L::L);  // [2][lse2 BQ | Delta BQ]
 
   int rank, bk;
   block_rank_row(rank, bk);  // first key blocks see the most queries
@@ -768,10 +852,7 @@ __global__ __launch_bounds__(512) void fa_bwd_dkdv8_kernel(
     }
   };
   if (ntiles > 0 && loader) issue(0, 0);
-  // this wavefront's 32 keys; the swizzle depends on the row's low 4 bits only,
-  // so the row within the slice addresses it
-  const T* Kk = Ks + ks * 32 * DP;
-  const T* Vk = Vs + ks * 32 * DP;
+  DkdvOffsets<DP> off = dkdv_offsets<DP>(qh_dkdv_smem, ks, qt, lane);
   for (int it = 0; it < ntiles; ++it) {
     const int buf = it & 1;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile `it` (and of V) have landed
@@ -780,14 +861,11 @@ __global__ __launch_bounds__(512) void fa_bwd_dkdv8_kernel(
     const int q0 = q_start + (it % nqt) * BQ;
     const int qh0 = q0 + qt * 32;
     const bool need_mask = (qh0 + 32 > Sq) || (kw0 + 32 > Sk) || (causal && kw0 + 31 > qh0 + coff);
-    const float* lse_row = Ls + buf * 2 * BQ;
-    const float* dl_row = lse_row + BQ;
-    const T* Qt = Qs + buf * BQ * DP;
-    const T* Ot = Os + buf * BQ * DP;
-    // one code path for masked and unmasked tiles: two inlined copies would
-    // keep the dK/dV accumulators in different registers on each side
-    fa_bwd_dkdv_half<T, DP>(Qt, Ot, Kk, Vk, dk, dv, lse_row, dl_row, q0, qt, need_mask, q_lo, q_hi, scale_log2,
-                            lane);
+    // one code path for masked and unmasked tiles (the mask is a wave-uniform
+    // branch inside): two inlined copies would keep the dK/dV accumulators in
+    // different registers on each side
+    fa_bwd_dkdv_half<T, DP>(off, dk, dv, q0, qt, need_mask, q_lo, q_hi, scale_log2, lane);
+    dkdv_next_stage<DP>(off);
   }
   // half 1 hands its partials to half 0 through LDS (dV, then dK)
   float* red = reinterpret_cast<float*>(qh_dkdv_smem);
@@ -1637,7 +1715,7 @@ extern "C" int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq) {
 namespace {
 // LDS of fa_bwd_dkdv8_kernel: K and V of 128 keys plus two Q and two dO tiles of 64 rows,
 // and two (lse2, Delta) pairs of 64 floats.
-constexpr int kDkdv8Lds = (2 * 128 + 4 * 64) * 128 * 2 + 2 * 2 * 64 * 4;
+constexpr int kDkdv8Lds = DkdvLds<128>::BYTES;
 
 // Raise the dynamic-LDS limit of fa_bwd_dkdv8_kernel once per device.
 template <typename T>
