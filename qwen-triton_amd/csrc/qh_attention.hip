@@ -916,23 +916,67 @@ __global__ __launch_bounds__(512) void fa_bwd_dkdv8_kernel(
 //   S^T = K Q^T, dP^T = V dO^T      (C layout: column = query, rows = keys)
 //   dS^T = P^T (dP^T - Delta)
 //   dQ^T += K^T dS^T                (K^T read transposed from the K tile)
-template <typename T, int DP, bool MASK>
-__device__ __forceinline__ void fa_bwd_dq_tile(const T* Kt, const T* Vt, const typename Mfma<T>::v8 (&qf)[DP / 16],
+// Per-lane LDS addresses of the dQ kernel's fragment reads in the current K/V
+// stage: K rows of each k16 step (V = +KV_OFF, the second 32-key half = +32
+// rows) and the transposed K reads of each 32-column block at key rows r and
+// r + 8 (the other 16-key steps: +16 rows). The row swizzle depends on a row's
+// low 4 bits only, so those steps are immediates.
+template <int DP>
+struct DqOffsets {
+  static constexpr int KD = DP / 16, DT = DP / 32;
+  uint32_t kf[KD], tr[DT][2];
+};
+
+template <int DP>
+__device__ __forceinline__ DqOffsets<DP> dq_offsets(uint32_t kbase, int lane) {
+  constexpr int CPR = DP / 8;
+  const int ql = lane & 31, hf = lane >> 5, grp = lane >> 4, j = lane & 15;
+  DqOffsets<DP> o;
+#pragma unroll
+  for (int kd = 0; kd < DqOffsets<DP>::KD; ++kd) o.kf[kd] = kbase + (ql * CPR + swz(ql, kd * 2 + hf, CPR)) * 16;
+  const int krow = 4 * (grp >> 1) + (j >> 2);
+#pragma unroll
+  for (int dt = 0; dt < DqOffsets<DP>::DT; ++dt) {
+    const int d = dt * 32 + 16 * (grp & 1) + 4 * (j & 3);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = krow + 8 * h;
+      o.tr[dt][h] = kbase + (r * CPR + swz(r, d >> 3, CPR)) * 16 + (d & 7) * 2;
+    }
+  }
+  return o;
+}
+
+template <int DP>
+__device__ __forceinline__ void dq_shift(DqOffsets<DP>& o, int delta) {
+#pragma unroll
+  for (int kd = 0; kd < DqOffsets<DP>::KD; ++kd) o.kf[kd] += delta;
+#pragma unroll
+  for (int dt = 0; dt < DqOffsets<DP>::DT; ++dt) o.tr[dt][0] += delta, o.tr[dt][1] += delta;
+}
+
+// dQ for 128 queries (4 wavefronts x 32 queries) of one (b, q-head): the
+// forward kernel's structure with dP computed beside S. K and V tiles of 64
+// keys stream through double-buffered swizzled LDS; per tile
+//   S^T = K Q^T, dP^T = V dO^T      (C layout: column = query, rows = keys)
+//   dS^T = P^T (dP^T - Delta)
+//   dQ^T += K^T dS^T                (K^T read transposed from the K tile)
+// KV_OFF: bytes from a K tile to the V tile of the same stage.
+template <typename T, int DP, bool MASK, uint32_t KV_OFF>
+__device__ __forceinline__ void fa_bwd_dq_tile(const DqOffsets<DP>& o, const typename Mfma<T>::v8 (&qf)[DP / 16],
                                                const typename Mfma<T>::v8 (&of)[DP / 16], f32x16 (&dq)[DP / 32],
                                                float lse2, float dl, int kv0, int lim, float scale_log2, int lane) {
-  constexpr int CPR = DP / 8, DT = DP / 32, KD = DP / 16;
+  constexpr int DT = DP / 32, KD = DP / 16;
   typedef typename Mfma<T>::v8 v8;
-  const int ql = lane & 31, hf = lane >> 5;
-  const int grp = lane >> 4, j = lane & 15;
+  const int hf = lane >> 5;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
     f32x16 sc = zero16(), dp = zero16();
-    const int row = kt * 32 + ql;
+    constexpr uint32_t kt_rows = 32 * DP * 2;
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd) {
-      const int c = swz(row, kd * 2 + hf, CPR);
-      sc = Mfma<T>::mma(load_frag16<T>(Kt + row * DP + c * 8), qf[kd], sc);
-      dp = Mfma<T>::mma(load_frag16<T>(Vt + row * DP + c * 8), of[kd], dp);
+      sc = Mfma<T>::mma(lds_frag16<T>(o.kf[kd], kt * kt_rows), qf[kd], sc);
+      dp = Mfma<T>::mma(lds_frag16<T>(o.kf[kd], KV_OFF + kt * kt_rows), of[kd], dp);
     }
     // Issue order of the 2 KD fragment reads (R) and MFMAs (M): 4 R, then
     // (M R) x (2 KD - 4), then 4 M: four reads in flight ahead of their
@@ -959,12 +1003,9 @@ __device__ __forceinline__ void fa_bwd_dq_tile(const T* Kt, const T* Vt, const t
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const v8 df = pack_pair<T>(dp, ks * 2);
-      const int krow = kt * 32 + ks * 16 + 4 * (grp >> 1) + (j >> 2);
+      const uint32_t rows = (kt * 32 + ks * 16) * DP * 2;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int d = dt * 32 + 16 * (grp & 1) + 4 * (j & 3);
-        dq[dt] = Mfma<T>::mma(read_vt_frag<T, DP>(Kt, krow, d), df, dq[dt]);
-      }
+      for (int dt = 0; dt < DT; ++dt) dq[dt] = Mfma<T>::mma(lds_tr_frag<T>(o.tr[dt][0], o.tr[dt][1], rows), df, dq[dt]);
     }
   }
 }
@@ -978,8 +1019,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
   constexpr int BN = 64, BMQ = 128;
   constexpr int DT = DP / 32, KD = DP / 16;
   typedef typename Mfma<T>::v8 v8;
-  __shared__ __attribute__((aligned(1024))) T Ks[2][BN * DP];
-  __shared__ __attribute__((aligned(1024))) T Vs[2][BN * DP];
+  // K stage 0, K stage 1, V stage 0, V stage 1
+  __shared__ __attribute__((aligned(1024))) T KVs[4][BN * DP];
+  constexpr uint32_t kStage = BN * DP * 2, kKv = 2 * kStage;
 
   const int nqb = (Sq + BMQ - 1) / BMQ;
   int rank, bhi;
@@ -1022,23 +1064,27 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
   const int lim = qi < Sq ? (causal ? min(Sk - 1, qi + coff) : Sk - 1) : -1;
   const TileLoader<T, BN, DP> kload(sks, D), vload(svs, D);
   if (ntiles > 0) {
-    kload.load(Ks[0], Kb, sks, 0, Sk);
-    vload.load(Vs[0], Vb, svs, 0, Sk);
+    kload.load(KVs[0], Kb, sks, 0, Sk);
+    vload.load(KVs[2], Vb, svs, 0, Sk);
   }
+  DqOffsets<DP> off = dq_offsets<DP>(lds_addr(KVs[0]), lane);
+  int shift = (int)kStage;  // to the other stage: +kStage after even tiles, -kStage after odd ones
   for (int it = 0; it < ntiles; ++it) {
     const int kv0 = it * BN;
     const int buf = it & 1;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (it + 1 < ntiles) {
-      kload.load(Ks[buf ^ 1], Kb, sks, kv0 + BN, Sk);
-      vload.load(Vs[buf ^ 1], Vb, svs, kv0 + BN, Sk);
+      kload.load(KVs[buf ^ 1], Kb, sks, kv0 + BN, Sk);
+      vload.load(KVs[2 + (buf ^ 1)], Vb, svs, kv0 + BN, Sk);
     }
     const bool need_mask = (kv0 + BN > Sk) || (qw0 + 32 > Sq) || (causal && kv0 + BN - 1 > qw0 + coff);
     if (need_mask)
-      fa_bwd_dq_tile<T, DP, true>(Ks[buf], Vs[buf], qf, of, dq, lse2, dl, kv0, lim, scale_log2, lane);
+      fa_bwd_dq_tile<T, DP, true, kKv>(off, qf, of, dq, lse2, dl, kv0, lim, scale_log2, lane);
     else
-      fa_bwd_dq_tile<T, DP, false>(Ks[buf], Vs[buf], qf, of, dq, lse2, dl, kv0, lim, scale_log2, lane);
+      fa_bwd_dq_tile<T, DP, false, kKv>(off, qf, of, dq, lse2, dl, kv0, lim, scale_log2, lane);
+    dq_shift<DP>(off, shift);
+    shift = -shift;
   }
   if (qi < Sq) {
     T* dQr = dQ + (bh * Sq + qi) * D;
