@@ -41,6 +41,7 @@ from qwen_triton.modules import (
     QwenSparseMoeBlock,
     QwenTritonCache,
 )
+from qwen_triton.modules.cache import StaticDecode
 from qwen_triton.modules.embedding import TritonEmbedding
 from qwen_triton.modules.linear import TritonLinear
 
@@ -92,10 +93,16 @@ def _layer_uses_moe(config: QwenTritonConfig, layer_idx: int) -> bool:
 
 
 def _loss_fn(logits: torch.Tensor, labels: torch.Tensor) -> torch.Tensor:
-    shift_logits = logits[:, :-1]
-    shift_labels = labels[:, 1:]
-    return triton_cross_entropy(shift_logits.reshape(-1, shift_logits.shape[-1]), shift_labels.reshape(-1),
-                                ignore_index=-100)
+    """Mean next-token cross-entropy (reference: qwen_triton/models/core.py, logits[:, :-1] against
+    labels[:, 1:]). The labels are shifted instead of the logits: position s is scored against
+    labels[:, s + 1] and each sequence's last position is ignored, so the logits enter as a
+    [B * S, V] view (slicing them would copy the whole tensor for B > 1, and its gradient again)
+    and the mean over the valid positions is the same."""
+    if labels.shape != logits.shape[:-1]:
+        raise ValueError(f"labels {tuple(labels.shape)} do not match logits {tuple(logits.shape)}")
+    shift_labels = torch.full_like(labels, -100)
+    shift_labels[:, :-1] = labels[:, 1:]
+    return triton_cross_entropy(logits.reshape(-1, logits.shape[-1]), shift_labels.reshape(-1), ignore_index=-100)
 
 
 class QwenDecoderLayer(nn.Module):
@@ -393,41 +400,58 @@ class QwenTritonForCausalLM(nn.Module):
         ``use_graph=True`` (GPU, bf16/fp16, no padding mask) runs the prefill and every decode step
         as replays of two HIP graphs captured once per generation shape (``greedy_graphs``): the
         step reads its cache position and valid lengths from device memory, picks the next token
-        and advances that state itself, so there is no host work between tokens. With a cache of at most 256 positions the replayed
-        steps run the same kernels as the eager loop and give the same tokens; beyond that the
-        decode attention plans its key splits for the reserved capacity rather than the current
-        length (same tokens within the bf16 band).
+        and advances that state itself, so there is no host work between tokens. The eager loop
+        of a model that qualifies for the graphs decodes through the same device state (a
+        ``StaticDecode`` on its cache, advanced by two small device ops per token) without
+        capturing it, so both run the same kernels with the same arguments and give the same
+        tokens at every cache length.
         """
         if self.backend == "ref" and hasattr(self.ref_model, "generate"):
             return self.ref_model.generate(input_ids=input_ids, attention_mask=attention_mask,
                                            max_new_tokens=max_new_tokens, do_sample=False)
-        if use_graph and max_new_tokens > 2 and self._graph_decode_ok(input_ids, attention_mask):
+        # one device sync for the whole generation: an all-ones mask (and the ones appended to
+        # it) means plain causal attention, so the steps run without it and without a check each
+        trivial_mask = QwenTritonModel._mask_is_trivial(attention_mask)
+        if use_graph and max_new_tokens > 2 and self._graph_decode_ok(input_ids, trivial_mask):
             return self._greedy_generate_graph(input_ids, max_new_tokens)
         generated = input_ids
-        running_mask = attention_mask
+        running_mask = None if trivial_mask else attention_mask
         cache = None
         if max_new_tokens > 0:
             dtype = self.lm_head.weight.dtype
             cache = self.new_cache(input_ids.shape[0], input_ids.shape[1] + max_new_tokens, dtype, input_ids.device)
-        for _ in range(max_new_tokens):
-            step_ids = generated if cache.get_seq_length() == 0 else generated[:, -1:]
-            out = self(input_ids=step_ids, attention_mask=running_mask, past_key_values=cache, use_cache=True,
-                       logits_to_keep=1)
-            cache = out.past_key_values
+        # decode steps through device-side state, as the captured step does (see the docstring)
+        static = None
+        if max_new_tokens > 1 and self._graph_decode_ok(input_ids, trivial_mask):
+            batch, prompt = input_ids.shape
+            static = StaticDecode(positions=torch.full((1,), prompt, dtype=torch.long, device=input_ids.device),
+                                  seqlens=torch.full((batch,), prompt + 1, dtype=torch.int32, device=input_ids.device))
+        for i in range(max_new_tokens):
+            step_ids = generated if i == 0 else generated[:, -1:]
+            if i > 0 and static is not None:
+                cache.static = static
+            try:
+                out = self(input_ids=step_ids, attention_mask=running_mask, past_key_values=cache, use_cache=True,
+                           logits_to_keep=1)
+            finally:
+                cache.static = None
+            if i > 0 and static is not None:
+                static.positions.add_(1)
+                static.seqlens.add_(1)
             next_token = out.logits[:, -1].argmax(dim=-1, keepdim=True)
             generated = torch.cat((generated, next_token), dim=-1)
             if running_mask is not None:
                 running_mask = torch.cat((running_mask, torch.ones_like(next_token, dtype=running_mask.dtype)), dim=-1)
         return generated
 
-    def _graph_decode_ok(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None) -> bool:
+    def _graph_decode_ok(self, input_ids: torch.Tensor, trivial_mask: bool) -> bool:
         from qwen_triton import _native
 
         cfg = self.config
         dtype = self.lm_head.weight.dtype
         return (input_ids.is_cuda and dtype in (torch.bfloat16, torch.float16) and _native.available()
                 and not cfg.attn_output_gate and all(t == "full_attention" for t in cfg.layer_types)
-                and (attention_mask is None or bool((attention_mask == 1).all())))
+                and trivial_mask)
 
     def greedy_graphs(self, batch: int, prompt: int, max_new_tokens: int):
         """The captured-graph runner (``models.graphs.GreedyGraphs``) for this generation shape,

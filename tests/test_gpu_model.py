@@ -401,17 +401,18 @@ def test_fused_layer_path_matches_separate_kernels(monkeypatch, batch):
     assert torch.equal(torch.stack(again, 1).float().cpu(), a)
 
 
-@pytest.mark.parametrize("moe", [False, True])
-def test_greedy_generate_graph_replay_matches_eager(moe):
+@pytest.mark.parametrize("moe,prompt", [(False, 19), (True, 19), (False, 300), (False, 600)])
+def test_greedy_generate_graph_replay_matches_eager(moe, prompt):
     """greedy_generate(use_graph=True): one captured decode step replayed per token, with the
-    position and valid lengths advanced on the device. With a cache of at most 256 positions
-    it runs the eager loop's kernels, so the tokens are identical; the replays (not Python
-    calls) do the work."""
+    position and valid lengths advanced on the device. The eager loop decodes through the same
+    device state, so the tokens are identical at every cache length (caches of 43, 324 and 624
+    positions, planned as one to several key splits of the decode attention); the replays (not
+    Python calls) do the work."""
     extra = dict(model_type="qwen3_moe", moe_intermediate_size=128, num_experts=8, num_experts_per_tok=2,
                  norm_topk_prob=True, decoder_sparse_step=1, mlp_only_layers=[]) if moe else {}
-    cfg = _cfg(**extra)
+    cfg = _cfg(max_position_embeddings=1024, **extra)
     m = _model(cfg, seed=5)
-    ids = torch.randint(0, cfg.vocab_size, (2, 19), generator=torch.Generator().manual_seed(6)).cuda()
+    ids = torch.randint(0, cfg.vocab_size, (2, prompt), generator=torch.Generator().manual_seed(6)).cuda()
     new = 24
     with torch.no_grad():
         eager = m.greedy_generate(ids, max_new_tokens=new)
@@ -419,7 +420,7 @@ def test_greedy_generate_graph_replay_matches_eager(moe):
         graph = m.greedy_generate(ids, max_new_tokens=new, use_graph=True)
         launched = _native.CALLS["qh_flash_decode"] - c0
         again = m.greedy_generate(ids, max_new_tokens=new, use_graph=True)
-    assert graph.shape == (2, 19 + new)
+    assert graph.shape == (2, prompt + new)
     assert torch.equal(graph, eager)
     assert torch.equal(again, eager)
     # decode attention entered from Python twice per layer (the eager second token and the

@@ -81,6 +81,28 @@ def test_rmsnorm_matches_hf_qwen3():
     torch.testing.assert_close(O.rmsnorm(x, norm.weight, 1e-6).float(), norm(x), atol=1e-6, rtol=1e-5)
 
 
+def test_rmsnorm_one_plus_matches_hf_qwen3_next():
+    """The one_plus branch (weight stored as w, applied as 1 + w) against HF's Qwen3-Next RMSNorm,
+    an independent implementation of that form: forward, and the input and weight gradients
+    of the oracle's closed-form backward against autograd through the HF module."""
+    from transformers.models.qwen3_next.modeling_qwen3_next import Qwen3NextRMSNorm
+
+    x = rn(3, 5, 64, seed=16, dtype=torch.float32).requires_grad_(True)
+    go = rn(3, 5, 64, seed=18, dtype=torch.float32)
+    norm = Qwen3NextRMSNorm(64, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(0.3 * rn(64, seed=17, dtype=torch.float32))
+    y = norm(x)
+    y.backward(go)
+    torch.testing.assert_close(O.rmsnorm(x.detach(), norm.weight.detach(), 1e-6, one_plus=True).float(), y.detach(),
+                               atol=1e-6, rtol=1e-5)
+    gx, gw = O.rmsnorm_backward(x.detach(), norm.weight.detach(), go, 1e-6, one_plus=True)
+    torch.testing.assert_close(gx.float(), x.grad, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(gw.float(), norm.weight.grad, atol=1e-5, rtol=1e-5)
+    # without the offset the same weights give a different result (the branch is live)
+    assert (O.rmsnorm(x.detach(), norm.weight.detach(), 1e-6).float() - y.detach()).abs().max() > 0.1
+
+
 @pytest.mark.parametrize("one_plus", [False, True])
 def test_rmsnorm_backward_matches_autograd(one_plus):
     x = rn(4, 7, 32, seed=13).requires_grad_(True)
