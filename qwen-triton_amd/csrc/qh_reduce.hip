@@ -163,16 +163,17 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_generic(const T* __restrict__
   }
 }
 
-// Backward, fast path. Each row-group accumulates its dW partial in registers
-// over the rows it visits and writes one partial row to ws at the end:
-// ws[(blockIdx.x * RPB + grp) * cols + c].
-template <typename T, int G, int NV>
-__global__ __launch_bounds__(256) void rmsnorm_bwd_fast(const T* __restrict__ x, const void* __restrict__ w,
-                                                        int wdtype, const T* __restrict__ gy, T* __restrict__ gx,
-                                                        float* __restrict__ ws, int64_t rows, int cols, float eps,
-                                                        float wadd) {
+// Backward, fast path. BT threads per workgroup, RPB = BT / G row groups. Each
+// row group accumulates its dW partial in registers over the rows it visits;
+// at the end the groups' partials are summed in LDS in group order and the
+// workgroup writes one partial row ws[blockIdx.x, :].
+template <typename T, int G, int NV, int BT>
+__global__ __launch_bounds__(BT) void rmsnorm_bwd_fast(const T* __restrict__ x, const void* __restrict__ w,
+                                                       int wdtype, const T* __restrict__ gy, T* __restrict__ gx,
+                                                       float* __restrict__ ws, int64_t rows, int cols, float eps,
+                                                       float wadd) {
   constexpr int VN = Vec16<T>::N;
-  constexpr int RPB = 256 / G;
+  constexpr int RPB = BT / G;
   const int grp = threadIdx.x / G, g = threadIdx.x % G;
   float pw[NV][VN];
   float sw[NV][VN];
@@ -221,24 +222,24 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_fast(const T* __restrict__ x,
       }
     }
   }
-  // Combine the RPB row groups' partials in LDS in group order, then write the
-  // workgroup's single partial row ws[blockIdx.x, :].
+  // The RPB groups' partials side by side in LDS (acc[grp][cols]), then each
+  // column summed over the groups in group order: the workgroup's partial row.
   extern __shared__ float acc[];
-  for (int s = 0; s < RPB; ++s) {
-    if (grp == s) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int c = (i * G + g) * VN;
-        if (c < cols) {
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * G + g) * VN;
+    if (c < cols) {
 #pragma unroll
-          for (int j = 0; j < VN; ++j) acc[c + j] = s == 0 ? pw[i][j] : acc[c + j] + pw[i][j];
-        }
-      }
+      for (int j = 0; j < VN; ++j) acc[grp * cols + c + j] = pw[i][j];
     }
-    __syncthreads();
   }
+  __syncthreads();
   float* wr = ws + (int64_t)blockIdx.x * cols;
-  for (int c = threadIdx.x; c < cols; c += 256) wr[c] = acc[c];
+  for (int c = threadIdx.x; c < cols; c += BT) {
+    float t = acc[c];
+    for (int s2 = 1; s2 < RPB; ++s2) t += acc[s2 * cols + c];
+    wr[c] = t;
+  }
 }
 
 // Backward, generic path: block owns ws row blockIdx.x; thread t owns columns
@@ -302,8 +303,14 @@ __global__ __launch_bounds__(1024) void colsum_partials(const float* __restrict_
   }
 }
 
-// Workgroups of the backward row kernels (one fp32 partial row each).
+// Workgroups of the backward row kernels (one fp32 partial row each): 1024 of
+// 256 threads for the generic kernel; the fast kernel keeps the same 4096 waves
+// in larger workgroups where its registers allow (fewer partial rows to sum).
 static const int kRmsBwdBlocks = 1024;
+
+// Threads per workgroup of rmsnorm_bwd_fast for NV vectors per lane: 1024 (four
+// waves per SIMD, 128 registers) while the row's values fit, then 512, 256.
+static int rms_bwd_threads(int NV) { return NV <= 2 ? 1024 : NV == 4 ? 512 : 256; }
 
 // ===========================================================================
 // Softmax
@@ -826,15 +833,6 @@ __global__ __launch_bounds__(256) void one_hot_kernel(const int64_t* __restrict_
   else if (G == 64 && NV == 4) KERNEL<T, 64, 4><<<grid, 256, 0, st>>>(__VA_ARGS__); \
   else if (G == 64 && NV == 8) KERNEL<T, 64, 8><<<grid, 256, 0, st>>>(__VA_ARGS__);
 
-#define QH_SHAPE_SWITCH_LDS(KERNEL, LDS, ...)                                            \
-  if (G == 8 && NV == 1) KERNEL<T, 8, 1><<<grid, 256, LDS, st>>>(__VA_ARGS__);           \
-  else if (G == 16 && NV == 1) KERNEL<T, 16, 1><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
-  else if (G == 32 && NV == 1) KERNEL<T, 32, 1><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
-  else if (G == 64 && NV == 1) KERNEL<T, 64, 1><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
-  else if (G == 64 && NV == 2) KERNEL<T, 64, 2><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
-  else if (G == 64 && NV == 4) KERNEL<T, 64, 4><<<grid, 256, LDS, st>>>(__VA_ARGS__);    \
-  else if (G == 64 && NV == 8) KERNEL<T, 64, 8><<<grid, 256, LDS, st>>>(__VA_ARGS__);
-
 template <typename T>
 static void launch_rms_fwd(const void* x, const void* w, int wdtype, void* y, int64_t rows, int64_t cols, float eps,
                            float wadd, hipStream_t st) {
@@ -1037,9 +1035,11 @@ static int64_t rms_bwd_partial_rows(int64_t rows, int64_t cols, int dtype, int* 
   const int VN = dtype == QH_F32 ? 4 : 8;
   int G = 0, NV = 0;
   if (pick_row_shape(cols, VN, G, NV)) {
-    const int rpb = 256 / G;
+    const int bt = rms_bwd_threads(NV);
+    const int rpb = bt / G;
     int64_t grid = ceil_div(rows, rpb);
-    if (grid > kRmsBwdBlocks) grid = kRmsBwdBlocks;
+    const int64_t cap = (int64_t)kRmsBwdBlocks * 256 / bt;
+    if (grid > cap) grid = cap;
     if (grid < 1) grid = 1;
     if (fast_grid) *fast_grid = (int)grid;
     if (G_out) *G_out = G;
@@ -1056,9 +1056,19 @@ static int64_t launch_rms_bwd(const void* x, const void* w, int wdtype, const vo
   int grid = 0, G = 0, NV = 0;
   const int64_t fr = rms_bwd_partial_rows(rows, cols, dtype, &grid, &G, &NV);
   if (fr > 0 && aligned16(x) && aligned16(gy) && aligned16(gx)) {
-    const size_t lds = (size_t)cols * sizeof(float);
-    QH_SHAPE_SWITCH_LDS(rmsnorm_bwd_fast, lds, (const T*)x, w, wdtype, (const T*)gy, (T*)gx, (float*)ws, rows,
-                        (int)cols, eps, wadd)
+    const int bt = rms_bwd_threads(NV);
+    const size_t lds = (size_t)(bt / G) * cols * sizeof(float);  // at most 64 KB for the shapes served
+#define QH_RBW(GG, NN, BB)                                                                                        \
+  rmsnorm_bwd_fast<T, GG, NN, BB><<<grid, BB, lds, st>>>((const T*)x, w, wdtype, (const T*)gy, (T*)gx, (float*)ws, \
+                                                        rows, (int)cols, eps, wadd)
+    if (G == 8) QH_RBW(8, 1, 1024);
+    else if (G == 16) QH_RBW(16, 1, 1024);
+    else if (G == 32) QH_RBW(32, 1, 1024);
+    else if (NV == 1) QH_RBW(64, 1, 1024);
+    else if (NV == 2) QH_RBW(64, 2, 1024);
+    else if (NV == 4) QH_RBW(64, 4, 512);
+    else QH_RBW(64, 8, 256);
+#undef QH_RBW
     return fr;
   }
   const int g = (int)(rows < kRmsBwdBlocks ? rows : kRmsBwdBlocks);
