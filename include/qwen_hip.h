@@ -309,6 +309,20 @@ int qh_gemm_multi_ex(int64_t M, int64_t K, const void* A, int64_t lda, int count
  * (every workgroup holds all K columns of its rows in one load chunk), else 0.
  * No counterpart in the reference: a capability query for the fusion above. */
 int64_t qh_gemm_multi_norm_fits(int64_t M, int64_t K, int gated, int count, const int64_t* N);
+/* qh_gemm_multi_ex's norm fusion for weights that already carry the norm weight:
+ * B_i[n][k] = round(W_i[n][k] * (norm_w[k] + one_plus)) (fp32 product, one
+ * rounding to the dtype; prepared once per weight). A holds the RMSNorm inputs
+ * h; each output row is scaled by rsqrt(mean_k(h^2) + eps) (fp32, fixed order)
+ * after the sum over K, then bias. For M > 4 the results equal qh_gemm_multi_ex
+ * with norm_w bit for bit; for M <= 4 the normalised operand is rounded on the
+ * weight side too (qh_gemm_multi_ex rounds round(h * w) there). Any shape
+ * qh_gemm_multi takes (no qh_gemm_multi_norm_fits condition).
+ * Replaces, fused, the same reference calls as qh_gemm_multi_ex's norm fusion
+ * (qwen_triton/models/core.py:127 and :146 with the projections after them);
+ * the folded-weight form has no counterpart in the reference. */
+int qh_gemm_multi_rms(int64_t M, int64_t K, const void* A, int64_t lda, int count, const void* const* B,
+                      const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
+                      const void* const* bias, int gated, float eps, int dtype, void* stream);
 /* out[n] = sum_m X[m*ldx + n] in a fixed order (bias gradient).
  * Replaces qwen_triton/kernels/matmul.py:114-127 (_row_sum_kernel). */
 int qh_colsum(const void* X, int64_t ldx, int64_t M, int64_t N, void* out, int dtype, int out_dtype,

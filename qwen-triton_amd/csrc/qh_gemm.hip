@@ -245,8 +245,14 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
 // Every workgroup holds all K columns of its rows (its waves' K slices each
 // loaded in one chunk), so the row sums of squares are this lane's pairs
 // (v_dot2), the four lane groups of a row, then the slices in order through
-// LDS in the epilogue; the multiplies never wait for them. Residual (per product, optional):
-// C = round(round(product) + R), the residual-add kernel's rounding.
+// LDS in the epilogue; the multiplies never wait for them. NORM modes 2 and 3
+// are the same with the norm weight already folded into B (B = round((w + wadd)
+// * W), made once per weight): the weight fragments are used as loaded and the
+// results equal mode 1's bit for bit. Mode 2 keeps mode 1's one load chunk per K
+// slice (a loop of a run-time chunk count holds more registers and spilled);
+// mode 3 serves the shapes whose slices need several chunks.
+// Residual (per product, optional): C = round(round(product) + R), the
+// residual-add kernel's rounding.
 constexpr int kMaxProducts = 4;
 template <typename T, typename OT>
 struct DecodeProducts {
@@ -261,9 +267,16 @@ struct DecodeProducts {
 };
 
 struct DecodeNorm {
-  const void* w;  // RMSNorm weight [K] in the activation dtype, nullptr = no norm
+  const void* w;  // RMSNorm weight [K] in the activation dtype, nullptr = no norm (unless folded)
   float eps, wadd;
+  int folded;  // 1: the weight is folded into B (row factor only)
 };
+
+// NORM template mode: 0 none, 1 weight applied in the kernel, 2 folded into B
+// (3: folded, K slices in several chunks; chosen at launch).
+__host__ __device__ constexpr int decode_norm_mode(const DecodeNorm* n) {
+  return n == nullptr ? 0 : (n->folded ? 2 : (n->w != nullptr ? 1 : 0));
+}
 
 // k-steps of 32 whose loads one wave issues together (a NORM launch needs its
 // whole K slice in one chunk). A chunk's activation block (16 MT rows x 32 CH k)
@@ -305,11 +318,13 @@ __device__ __forceinline__ float sumsq8(const typename Mfma<T>::v8& v, float acc
 
 // NTB: weights loaded non-temporally (each weight tile read by one workgroup, ms == 1); with
 // several row groups per column tile the repeat reads should find the tile in the caches.
-template <typename T, typename OT, int MT, int KSP, bool GATED, bool NORM, bool NTB = true>
+template <typename T, typename OT, int MT, int KSP, bool GATED, int NORM, bool NTB = true>
 __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__ A, int64_t lda,
                                                            const DecodeProducts<T, OT> P, const DecodeNorm nrm,
                                                            int M, int K, int kr, int ms, int tiles) {
   constexpr int CG = 16 / KSP;
+  constexpr bool SCALE = NORM == 1, ROWS = NORM != 0;  // weight scaled here; row factor applied
+  constexpr bool ONE = NORM == 1 || NORM == 2;         // each K slice in one load chunk
   constexpr int NB = GATED ? 2 : 1;                   // weight matrices per wave
   constexpr int CH = decode_chunk(MT, GATED, KSP);    // k-steps loaded together
   typedef typename Mfma<T>::v8 v8;
@@ -326,7 +341,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   static_assert(16 * MT * 16 * 16 * 4 <= kDecodeLds, "K-slice sums exceed the slots");
   __shared__ __align__(16) unsigned char abuf[kDecodeLds];
   float(*red)[MT * 16][16] = reinterpret_cast<float(*)[MT * 16][16]>(abuf);
-  __shared__ float nss[NORM ? 16 : 1][MT * 16];
+  __shared__ float nss[ROWS ? 16 : 1][MT * 16];
   // Workgroup -> (column tile, row group). The ms row groups of a tile get
   // workgroup ids that are equal mod 8, so they run on one XCD and read the
   // tile's weights through the same L2.
@@ -357,19 +372,19 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   v8 zero;
 #pragma unroll
   for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
-  // Every wave runs the same number of chunks (with NORM exactly one; slices
-  // past K load zeros), so all of them reach the barriers.
+  // Every wave runs the same number of chunks (with NORM modes 1 and 2 exactly
+  // one; slices past K load zeros), so all of them reach the barriers.
   auto swz = [](int r) { return S16 >= 16 ? (r & 15) : ((r >> 1) & 7); };  // slot s of row r: chunk s ^ swz(r)
   unsigned char* slot = abuf + ks * SLOT;
   const uint32_t abase = lds_addr(slot);
-  const int nch = NORM ? 1 : (kr + 32 * CH - 1) / (32 * CH);
-  float sq[MT];  // NORM: this lane's row sums of squares
+  const int nch = ONE ? 1 : (kr + 32 * CH - 1) / (32 * CH);
+  float sq[MT];  // NORM: this lane's row sums of squares (over all its chunks)
 #pragma unroll
   for (int i = 0; i < MT; ++i) sq[i] = 0.f;
   for (int ci = 0; ci < nch; ++ci) {
     const int k0 = kb + ci * 32 * CH;
     v8 b[CH][NB];
-    v8 wr[NORM ? CH : 1];  // norm weights (dtype T) of this lane's 8 columns per step
+    v8 wr[SCALE ? CH : 1];  // norm weights (dtype T) of this lane's 8 columns per step
     if (ci > 0) {  // the previous chunk's fragments have been read from the slot
       if constexpr (CG > 1) __syncthreads();
       else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -385,7 +400,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
     for (int u = 0; u < CH; ++u) {
       const int k = k0 + u * 32 + q * 8;
       const bool kok = k < ke;
-      if constexpr (NORM) wr[u] = kok ? *reinterpret_cast<const v8*>((const T*)nrm.w + k) : zero;
+      if constexpr (SCALE) wr[u] = kok ? *reinterpret_cast<const v8*>((const T*)nrm.w + k) : zero;
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
         // weights read by one workgroup per decode step: non-temporal, so they do not evict cached data
@@ -402,7 +417,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const bool kok = k0 + u * 32 + q * 8 < ke;
-      if constexpr (NORM) {  // the weight operand round((w + wadd) * B): 8 NB values per lane, not 8 MT
+      if constexpr (SCALE) {  // the weight operand round((w + wadd) * B): 8 NB values per lane, not 8 MT
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float wv = to_f32(wr[u][e]) + nrm.wadd;
@@ -416,13 +431,13 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
         v8 a;
         if (m0 + r < M && kok) a = *reinterpret_cast<const v8*>(slot + r * RB + (((u * 4 + q) ^ swz(r)) << 4));
         else a = zero;
-        if constexpr (NORM) sq[i] = sumsq8<T>(a, sq[i]);  // row sums of squares (the epilogue adds the slices)
+        if constexpr (ROWS) sq[i] = sumsq8<T>(a, sq[i]);  // row sums of squares (the epilogue adds the slices)
 #pragma unroll
         for (int j = 0; j < NB; ++j) acc[j][i] = mma16<T>(a, b[u][j], acc[j][i]);
       }
     }
   }
-  if constexpr (NORM) {
+  if constexpr (ROWS) {
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
       float v = sq[i];
@@ -453,7 +468,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
       const int grow = m0 + row;
       if (grow >= M || gn >= N) continue;
       const T* bias = P.bias[pi + j];
-      if constexpr (NORM) {  // the row's RMSNorm factor (slices summed in order)
+      if constexpr (ROWS) {  // the row's RMSNorm factor (slices summed in order)
         float ss = 0.f;
 #pragma unroll
         for (int s2 = 0; s2 < KSP; ++s2) ss += nss[s2][row];  // column group 0's slices
@@ -507,11 +522,12 @@ constexpr int kGemvTwoColMin = 4096;
 // NB weight rows per column (2: gate and up); RC columns per wave (non-gated
 // products whose widths are multiples of RC; the wave's NB = RC rows are
 // consecutive columns of one product).
-template <typename T, typename OT, int MR, bool GATED, bool NORM, int RC = 1>
+template <typename T, typename OT, int MR, bool GATED, int NORM, int RC = 1>
 __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ A, int64_t lda,
                                                           const DecodeProducts<T, OT> P, const DecodeNorm nrm, int M,
                                                           int K, int ncols) {
   static_assert(RC == 1 || !GATED, "a wave takes several columns of non-gated products only");
+  constexpr bool SCALE = NORM == 1, ROWS = NORM != 0;  // activation scaled here; row factor applied
   constexpr int NB = GATED ? 2 : RC;
   constexpr int CH = gemv_chunk(MR, GATED, RC);
   typedef typename Mfma<T>::v8 v8;
@@ -539,7 +555,7 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
   for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
   for (int k0 = 0; k0 < K; k0 += 512 * CH) {
     v8 b[CH][NB], a[CH][MR];
-    v8 wr[NORM ? CH : 1];
+    v8 wr[SCALE ? CH : 1];
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int k = k0 + u * 512 + lane * 8;
@@ -550,14 +566,14 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
 #pragma unroll
       for (int i = 0; i < MR; ++i)
         a[u][i] = (kok && i < M) ? *reinterpret_cast<const v8*>(A + (int64_t)i * lda + k) : zero;
-      if constexpr (NORM) wr[u] = kok ? *reinterpret_cast<const v8*>((const T*)nrm.w + k) : zero;
+      if constexpr (SCALE) wr[u] = kok ? *reinterpret_cast<const v8*>((const T*)nrm.w + k) : zero;
     }
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
 #pragma unroll
       for (int i = 0; i < MR; ++i) {
-        if constexpr (NORM) {
-          ss[i] = sumsq8<T>(a[u][i], ss[i]);
+        if constexpr (ROWS) ss[i] = sumsq8<T>(a[u][i], ss[i]);
+        if constexpr (SCALE) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) a[u][i][e] = from_f32<T>(to_f32(a[u][i][e]) * (to_f32(wr[u][e]) + nrm.wadd));
         }
@@ -572,7 +588,7 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
   for (int o = 32; o > 0; o >>= 1) {
 #pragma unroll
     for (int i = 0; i < MR; ++i) {
-      if constexpr (NORM) ss[i] += __shfl_xor(ss[i], o);
+      if constexpr (ROWS) ss[i] += __shfl_xor(ss[i], o);
 #pragma unroll
       for (int j = 0; j < NB; ++j) acc[j][i] += __shfl_xor(acc[j][i], o);
     }
@@ -585,7 +601,7 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       v[j] = acc[j][i];
-      if constexpr (NORM) v[j] *= rsqrtf(ss[i] / (float)K + nrm.eps);
+      if constexpr (ROWS) v[j] *= rsqrtf(ss[i] / (float)K + nrm.eps);
       const T* bias = P.bias[pi + (RC > 1 ? 0 : j)];
       v[j] += bias ? to_f32(bias[RC > 1 ? min(n + j, P.N[pi] - 1) : n]) : 0.f;
     }
@@ -618,7 +634,7 @@ void launch_gemv_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int
   for (int i = 0; i < nprod; ++i) P.tile0[i + 1] = P.tile0[i] + P.N[i];
   if (gated) P.count = 1;
   const int ncols = P.tile0[nprod];
-  const bool norm = nz.w != nullptr;
+  const int nmode = decode_norm_mode(&nz);
   // Columns per wave: 4 for a vocabulary-wide product; 2 when that still gives 2048+ waves and
   // no wave straddles two products (each wave re-reads the activation row and the norm weights,
   // so fewer waves read less: the config-0 q/k/v launch, 4096 columns, 4.7 us against 7.5 us at
@@ -636,12 +652,16 @@ void launch_gemv_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int
 #define QH_GW(MRV, NV) \
   if (rc == 2) QH_GR(MRV, NV, 2); else QH_GR(MRV, NV, kGemvWideCols);
     if constexpr (std::is_same<T, OT>::value) {
-      if (norm) {
-        if (M == 1) { QH_GW(1, true) } else if (M == 2) { QH_GW(2, true) } else { QH_GW(4, true) }
+      if (nmode == 1) {
+        if (M == 1) { QH_GW(1, 1) } else if (M == 2) { QH_GW(2, 1) } else { QH_GW(4, 1) }
+        return;
+      }
+      if (nmode == 2) {
+        if (M == 1) { QH_GW(1, 2) } else if (M == 2) { QH_GW(2, 2) } else { QH_GW(4, 2) }
         return;
       }
     }
-    if (M == 1) { QH_GW(1, false) } else if (M == 2) { QH_GW(2, false) } else { QH_GW(4, false) }
+    if (M == 1) { QH_GW(1, 0) } else if (M == 2) { QH_GW(2, 0) } else { QH_GW(4, 0) }
 #undef QH_GW
 #undef QH_GR
     return;
@@ -650,12 +670,16 @@ void launch_gemv_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int
 #define QH_GV(MRV, GV, NV) gemv_decode_kernel<T, OT, MRV, GV, NV><<<grid, 256, 0, st>>>(a, lda, P, nz, M, K, ncols)
 #define QH_GV_M(MRV)                                                      \
   if constexpr (std::is_same<T, OT>::value) {                             \
-    if (norm) {                                                           \
-      if (gated) QH_GV(MRV, true, true); else QH_GV(MRV, false, true);    \
+    if (nmode == 1) {                                                     \
+      if (gated) QH_GV(MRV, true, 1); else QH_GV(MRV, false, 1);          \
+      return;                                                             \
+    }                                                                     \
+    if (nmode == 2) {                                                     \
+      if (gated) QH_GV(MRV, true, 2); else QH_GV(MRV, false, 2);          \
       return;                                                             \
     }                                                                     \
   }                                                                       \
-  if (gated) QH_GV(MRV, true, false); else QH_GV(MRV, false, false);
+  if (gated) QH_GV(MRV, true, 0); else QH_GV(MRV, false, 0);
   if (M == 1) { QH_GV_M(1) } else if (M == 2) { QH_GV_M(2) } else { QH_GV_M(4) }
 #undef QH_GV_M
 #undef QH_GV
@@ -712,21 +736,29 @@ static DecodePlan decode_plan(int M, int K, bool gated, bool norm, int count, co
 template <typename T, typename OT>
 int launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int M, int K, bool gated,
                            hipStream_t st, int ms_force = 0, const DecodeNorm* nrm = nullptr, int ksp_force = 0) {
-  const bool norm = nrm != nullptr && nrm->w != nullptr;
+  const int nmode = decode_norm_mode(nrm);
+  const bool norm = nmode != 0;
   if (M <= kGemvMaxRows && ms_force == 0 && ksp_force == 0) {
     if (norm && !std::is_same<T, OT>::value) return QH_E_ARG;
-    launch_gemv_products<T, OT>(a, lda, P, M, K, gated, norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f}, st);
+    launch_gemv_products<T, OT>(a, lda, P, M, K, gated, norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f, 0}, st);
     return QH_OK;
   }
-  const DecodePlan d = decode_plan(M, K, gated, norm, P.count, P.N, ksp_force, ms_force);
+  // modes 1 and 2 load each K slice in one chunk; folded weights whose slices do not fit
+  // one chunk take the plain plan (mode 3)
+  DecodePlan d = decode_plan(M, K, gated, nmode != 0, P.count, P.N, ksp_force, ms_force);
+  int kmode = nmode;
+  if (nmode == 2 && !d.norm_fits) {
+    d = decode_plan(M, K, gated, false, P.count, P.N, ksp_force, ms_force);
+    kmode = 3;
+  }
   const int nprod = gated ? 1 : P.count;
   P.tile0[0] = 0;
   for (int i = 0; i < nprod; ++i) P.tile0[i + 1] = P.tile0[i] + (P.N[i] + d.cols - 1) / d.cols;
   if (gated) P.count = 1;
   const int tiles = d.tiles, kr = d.kr, ms = d.ms, mtw = d.mtw, ksp = d.ksp;
   const int grid = (tiles + 7) / 8 * 8 * ms;
-  if (norm && !d.norm_fits) return QH_E_ARG;
-  const DecodeNorm nz = norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f};
+  if (nmode == 1 && !d.norm_fits) return QH_E_ARG;
+  const DecodeNorm nz = norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f, 0};
   constexpr bool kNormOk = std::is_same<T, OT>::value;  // the only instantiation a norm launch reaches
   if (norm && !kNormOk) return QH_E_ARG;
 #define QH_DG(MTV, KSPV, GV, NV)                                                                        \
@@ -738,14 +770,22 @@ int launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, in
   if (ksp == 8) QH_DG(MTV, 8, GV, NV); else QH_DG(MTV, 16, GV, NV);
 #define QH_DG_W(MTV)                                           \
   if constexpr (kNormOk) {                                     \
-    if (norm) {                                                \
-      if (gated) { QH_DG_K(MTV, true, true) } else { QH_DG_K(MTV, false, true) } \
+    if (nmode == 1) {                                          \
+      if (gated) { QH_DG_K(MTV, true, 1) } else { QH_DG_K(MTV, false, 1) } \
+      return QH_OK;                                            \
+    }                                                          \
+    if (kmode == 2) {                                          \
+      if (gated) { QH_DG_K(MTV, true, 2) } else { QH_DG_K(MTV, false, 2) } \
+      return QH_OK;                                            \
+    }                                                          \
+    if (kmode == 3) {                                          \
+      if (gated) { QH_DG_K(MTV, true, 3) } else { QH_DG_K(MTV, false, 3) } \
       return QH_OK;                                            \
     }                                                          \
   }                                                            \
-  if (gated) { QH_DG_K(MTV, true, false) }                     \
-  else if (ksp == 4) QH_DG(MTV, 4, false, false);              \
-  else { QH_DG_K(MTV, false, false) }
+  if (gated) { QH_DG_K(MTV, true, 0) }                         \
+  else if (ksp == 4) QH_DG(MTV, 4, false, 0);                  \
+  else { QH_DG_K(MTV, false, 0) }
   if (mtw == 1) { QH_DG_W(1) } else if (mtw == 2) { QH_DG_W(2) } else if (mtw == 3) { QH_DG_W(3) } else { QH_DG_W(4) }
 #undef QH_DG_W
 #undef QH_DG_K
@@ -1151,7 +1191,7 @@ extern "C" int qh_gemm_multi_ex(int64_t M, int64_t K, const void* A, int64_t lda
                (long long)M, (long long)K);
   if (M == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;
-  const DecodeNorm nrm{norm_w, eps, one_plus ? 1.f : 0.f};
+  const DecodeNorm nrm{norm_w, eps, one_plus ? 1.f : 0.f, 0};
   int rc = QH_OK;
 #define QH_MULTI(T)                                                                                     \
   {                                                                                                     \
@@ -1176,6 +1216,49 @@ extern "C" int qh_gemm_multi_ex(int64_t M, int64_t K, const void* A, int64_t lda
     return rc;
   }
   QH_CHECK_LAUNCH("qh_gemm_multi");
+  return QH_OK;
+}
+
+extern "C" int qh_gemm_multi_rms(int64_t M, int64_t K, const void* A, int64_t lda, int count, const void* const* B,
+                                 const int64_t* ldb, const int64_t* N, void* const* C, const int64_t* ldc,
+                                 const void* const* bias, int gated, float eps, int dtype, void* stream) {
+  QH_CHECK_ARG(count >= 1 && count <= kMaxProducts, "qh_gemm_multi_rms: 1..%d products", kMaxProducts);
+  QH_CHECK_ARG(M >= 0 && M <= 128 && K > 0 && K < (1ll << 31), "qh_gemm_multi_rms: needs 0 <= M <= 128 and K > 0");
+  QH_CHECK_ARG(!gated || (count == 2 && N[0] == N[1]), "qh_gemm_multi_rms: gated needs two products of equal N");
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_gemm_multi_rms: bf16/f16 only");
+  QH_CHECK_ARG(aligned16(A) && lda % 8 == 0 && lda >= K && K % 8 == 0,
+               "qh_gemm_multi_rms: A must be 16-byte aligned with K, lda multiples of 8");
+  for (int i = 0; i < count; ++i) {
+    QH_CHECK_ARG(N[i] > 0 && N[i] < (1ll << 31) && aligned16(B[i]) && ldb[i] % 8 == 0 && ldb[i] >= K,
+                 "qh_gemm_multi_rms: product %d: bad B or N", i);
+    QH_CHECK_ARG((gated && i == 1) || (C[i] != nullptr && ldc[i] >= N[i]), "qh_gemm_multi_rms: product %d: bad C",
+                 i);
+  }
+  if (M == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const DecodeNorm nrm{nullptr, eps, 0.f, 1};
+  int rc = QH_OK;
+#define QH_MULTI(T)                                                                                     \
+  {                                                                                                     \
+    DecodeProducts<T, T> P = {};                                                                        \
+    for (int i = 0; i < count; ++i) {                                                                   \
+      P.B[i] = (const T*)B[i];                                                                          \
+      P.C[i] = (T*)C[i];                                                                                \
+      P.bias[i] = bias ? (const T*)bias[i] : nullptr;                                                   \
+      P.ldb[i] = ldb[i];                                                                                \
+      P.ldc[i] = ldc[i];                                                                                \
+      P.N[i] = (int)N[i];                                                                               \
+    }                                                                                                   \
+    P.count = count;                                                                                    \
+    rc = launch_decode_products<T, T>((const T*)A, lda, P, (int)M, (int)K, gated != 0, st, 0, &nrm);   \
+  }
+  if (dtype == QH_BF16) QH_MULTI(bf16_t) else QH_MULTI(f16_t)
+#undef QH_MULTI
+  if (rc) {
+    qh::set_error("qh_gemm_multi_rms: launch failed (M=%lld K=%lld)", (long long)M, (long long)K);
+    return rc;
+  }
+  QH_CHECK_LAUNCH("qh_gemm_multi_rms");
   return QH_OK;
 }
 

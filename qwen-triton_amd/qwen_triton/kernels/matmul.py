@@ -108,14 +108,42 @@ def linear_group_norm_ok(x: torch.Tensor, weights: list[torch.Tensor], norm_weig
         return False
     k = x.shape[-1]
     if not (norm_weight.is_cuda and norm_weight.dim() == 1 and norm_weight.shape[0] == k
-            and norm_weight.is_contiguous() and norm_weight.dtype == x.dtype and norm_weight.data_ptr() % 16 == 0):
+            and norm_weight.is_contiguous() and norm_weight.dtype == x.dtype):
         return False
-    if gated and (len(weights) != 2 or weights[0].shape[0] != weights[1].shape[0]):
-        return False
-    n = len(weights)
-    nn_ = (ctypes.c_int64 * n)(*(w.shape[0] for w in weights))
-    m = x.numel() // max(k, 1)
-    return bool(_native.call("qh_gemm_multi_norm_fits", m, k, int(gated), n, ctypes.addressof(nn_)))
+    return not gated or (len(weights) == 2 and weights[0].shape[0] == weights[1].shape[0])
+
+
+def _folded_group(weights: list[torch.Tensor], biases: list[torch.Tensor | None] | None, norm_weight: torch.Tensor,
+                  one_plus: bool, concat: bool) -> tuple[list[torch.Tensor], list[torch.Tensor | None] | None]:
+    """The weights with the RMSNorm weight folded in, ``round(W * (w + one_plus))`` per column as the
+    in-kernel norm rounds its weight operand (fp32 product, one rounding to the dtype), made once and
+    kept on the norm weight; rebuilt when any of the tensors is modified (version counters). With
+    ``concat`` the products are stacked into one weight (and bias) so that one product serves them."""
+    sig = (tuple((w.data_ptr(), tuple(w.shape), w.stride(0)) for w in weights), bool(one_plus), bool(concat),
+           None if biases is None else tuple(None if b is None else b.data_ptr() for b in biases))
+    versions = (tuple(w._version for w in weights), norm_weight._version, norm_weight.data_ptr(),
+                None if biases is None else tuple(None if b is None else b._version for b in biases))
+    store = getattr(norm_weight, "_qh_folded", None)
+    if store is None:
+        store = {}
+        norm_weight._qh_folded = store
+    hit = store.get(sig)
+    if hit is not None and hit[0] == versions:
+        return hit[1], hit[2]
+    with torch.no_grad():
+        scale = norm_weight.float() + (1.0 if one_plus else 0.0)
+        folded = [(w.float() * scale).to(w.dtype) for w in weights]
+        fb = biases
+        if concat:
+            folded = [torch.cat(folded)]
+            if biases is not None and all(b is not None for b in biases):
+                fb = [torch.cat([b.reshape(-1) for b in biases])]
+            else:
+                fb = None
+    if len(store) > 8:
+        store.clear()
+    store[sig] = (versions, folded, fb)
+    return folded, fb
 
 
 def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torch.Tensor | None] | None = None,
@@ -127,16 +155,22 @@ def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torc
     product is computed and rounded exactly as ``triton_matmul`` would.
 
     ``norm = (weight, eps, one_plus)``: ``x`` holds RMSNorm inputs and the products use
-    ``rmsnorm(x)``: the operand is ``round(x * (weight + one_plus))`` and each output row is
-    scaled by ``rsqrt(mean(x^2) + eps)`` after the sum over K, so the one rounding of the
-    normalised operand sits before the row factor rather than after it (check
-    ``linear_group_norm_ok`` first; the weight has the activation dtype). ``residual[i]`` (same
-    shape as output i): output i is ``residual_add(x @ W_i.T (+ b_i), residual[i])``, rounded as
-    the two kernels round.
+    ``rmsnorm(x)``: the norm weight is folded into the weights once (``round(W * (weight +
+    one_plus))``, kept with the norm weight, see ``_folded_group``) and each output row is scaled
+    by ``rsqrt(mean(x^2) + eps)`` after the sum over K, so the one rounding of the normalised
+    operand sits in the weight operand, before the row factor (check ``linear_group_norm_ok``
+    first; the weight has the activation dtype). Non-gated groups run as one product over the
+    stacked weights and return column views of its output. ``residual[i]`` (same shape as output
+    i): output i is ``residual_add(x @ W_i.T (+ b_i), residual[i])``, rounded as the two kernels
+    round.
     """
     k = x.shape[-1]
     x2 = _rows(x, k)
     m = x2.shape[0]
+    if norm is not None:
+        if residual is not None:
+            raise ValueError("linear_group: norm and residual do not combine")
+        return _linear_group_rms(x, x2, weights, biases, gated, norm)
     n = len(weights)
     plan = _group_plan(weights, biases)
     outs = [torch.empty((m, w.shape[0]), dtype=x.dtype, device=x.device) for w in (weights[:1] if gated else weights)]
@@ -165,16 +199,43 @@ def linear_group(x: torch.Tensor, weights: list[torch.Tensor], biases: list[torc
                 rs.append(r2)
             res_arr = arr_p(*(None if r is None else r.data_ptr() for r in rs))
             ldr = arr_l(*(0 if r is None else r.stride(0) for r in rs))
-        nw, eps, one_plus = norm if norm is not None else (None, 0.0, False)
         _native.call("qh_gemm_multi_ex", m, k, x2.data_ptr(), x2.stride(0), n, ctypes.addressof(bptr),
                      ctypes.addressof(ldb), ctypes.addressof(nn_), ctypes.addressof(cptr), ctypes.addressof(ldc),
                      bias_addr, ctypes.addressof(res_arr) if res_arr is not None else None,
-                     ctypes.addressof(ldr) if ldr is not None else None, int(gated),
-                     None if nw is None else nw.data_ptr(), _native.dtype_code(nw.dtype) if nw is not None else 0,
-                     float(eps), int(bool(one_plus)), _native.dtype_code(x.dtype), _native.stream(x.device))
+                     ctypes.addressof(ldr) if ldr is not None else None, int(gated), None, 0, 0.0, 0,
+                     _native.dtype_code(x.dtype), _native.stream(x.device))
     lead = x.shape[:-1]
     outs = [o.view(*lead, o.shape[1]) for o in outs]
     return outs[0] if gated else outs
+
+
+def _linear_group_rms(x, x2, weights, biases, gated, norm):
+    """``linear_group(..., norm=...)``: folded weights, the row factor applied in the launch
+    (``qh_gemm_multi_rms``)."""
+    nw, eps, one_plus = norm
+    k, m = x2.shape[1], x2.shape[0]
+    concat = not gated and len(weights) > 1
+    fw, fb = _folded_group(weights, biases, nw, one_plus, concat)
+    n = len(fw)
+    bptr, ldb, nn_, bias_addr = _group_plan(fw, fb)[:4]
+    outs = [torch.empty((m, w.shape[0]), dtype=x.dtype, device=x.device) for w in (fw[:1] if gated else fw)]
+    arr_p = ctypes.c_void_p * n
+    arr_l = ctypes.c_int64 * n
+    cptr = arr_p(*([o.data_ptr() for o in outs] + [None] * (n - len(outs))))
+    ldc = arr_l(*([o.stride(0) for o in outs] + [0] * (n - len(outs))))
+    _native.call("qh_gemm_multi_rms", m, k, x2.data_ptr(), x2.stride(0), n, ctypes.addressof(bptr),
+                 ctypes.addressof(ldb), ctypes.addressof(nn_), ctypes.addressof(cptr), ctypes.addressof(ldc),
+                 bias_addr, int(gated), float(eps), _native.dtype_code(x.dtype), _native.stream(x.device))
+    lead = x.shape[:-1]
+    if gated:
+        return outs[0].view(*lead, outs[0].shape[1])
+    if concat:
+        cols, c0 = [], 0
+        for w in weights:
+            cols.append(outs[0][:, c0:c0 + w.shape[0]].view(*lead, w.shape[0]))
+            c0 += w.shape[0]
+        return cols
+    return [outs[0].view(*lead, outs[0].shape[1])]
 
 
 def _native_matmul_forward(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:

@@ -371,15 +371,15 @@ def test_fused_layer_path_matches_separate_kernels(monkeypatch, batch):
     outs = {}
     for fused in (True, False):
         monkeypatch.setattr(core, "FUSE_NORM_GEMM", fused)
-        c0 = _native.CALLS["qh_gemm_multi_ex"]
+        c0 = _native.CALLS["qh_gemm_multi_ex"] + _native.CALLS["qh_gemm_multi_rms"]
         with torch.no_grad():
             p = m(input_ids=ids[:, :33], use_cache=True)
             steps = [p.logits[:, -1]]
             cache = p.past_key_values
             for t in range(33, 40):
                 steps.append(m(input_ids=ids[:, t:t + 1], past_key_values=cache, use_cache=True).logits[:, -1])
-        launched = _native.CALLS["qh_gemm_multi_ex"] - c0
-        # 3 fused launches per layer and token (q/k/v, o_proj, gate/up, down: 4; the prefill of
+        launched = _native.CALLS["qh_gemm_multi_ex"] + _native.CALLS["qh_gemm_multi_rms"] - c0
+        # fused launches per layer and token (q/k/v, o_proj, gate/up, down: 4; the prefill of
         # 33 * batch rows takes the fused path too when it has at most 128 rows)
         per_pass = 4 * cfg.num_hidden_layers
         expect = per_pass * (7 + (1 if 33 * batch <= 128 else 0)) if fused else 0

@@ -450,9 +450,10 @@ def test_linear_group_gated_matches_gemms_then_silu_mul(M):
 @pytest.mark.parametrize("gated", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_linear_group_norm_prologue(M, gated, dtype):
-    # rows normalised inside the launch vs rmsnorm followed by the same grouped launch:
-    # the one rounding of the normalised operand is placed differently, so outputs agree
-    # within a few output rounding steps; both within the band of the fp64 oracle
+    # rows normalised inside the launch (norm weight folded into the weights) vs rmsnorm followed
+    # by the same grouped launch: the one rounding of the normalised operand is placed
+    # differently, so outputs agree within a few output rounding steps; both within the band of
+    # the fp64 oracle
     from qwen_triton.kernels.matmul import linear_group, linear_group_norm_ok
 
     Kd = 1024
@@ -464,16 +465,15 @@ def test_linear_group_norm_prologue(M, gated, dtype):
     ns = (2048, 1024, 1000) if not gated else (3072, 3072)
     ws = [randn(n, Kd, dtype=dtype, seed=242 + i, scale=0.05) for i, n in enumerate(ns)]
     assert linear_group_norm_ok(x, ws, nw, gated=gated)
-    c0 = native_calls("qh_gemm_multi_ex")
+    c0 = native_calls("qh_gemm_multi_rms")
     fused = linear_group(x, ws, gated=gated, norm=(nw, 1e-6, False))
-    assert native_calls("qh_gemm_multi_ex") == c0 + 1
+    assert native_calls("qh_gemm_multi_rms") == c0 + 1
     y = K.rmsnorm(x, nw, 1e-6)
     plain = linear_group(y, ws, gated=gated)
     fused, plain = ([fused], [plain]) if gated else (fused, plain)
     # fp64 oracles with each path's rounding points: the reference rounds the normalised
     # rows (plain path); the fused path applies the row factor after the product, with the one
-    # rounding on x * w (at most 4 rows, one wave per column) or on w * W (the MFMA kernel, more
-    # rows: it scales the weight fragments). Both round gate and up before the SiLU-mul.
+    # rounding on w * W (the folded weights). Both round gate and up before the SiLU-mul.
     bf = lambda t: t.to(dtype).to(torch.float64)  # noqa: E731
     xd = x.cpu().double()
     nwd = nw.cpu().double()
@@ -484,10 +484,7 @@ def test_linear_group_norm_prologue(M, gated, dtype):
         outs = [O.linear(y, w) * scale for w in weights]
         return [O.silu_mul(bf(outs[0]), bf(outs[1]))] if gated else outs
 
-    if M <= 4:
-        r_fused_all = prods(bf(xd * nwd), inv, ws)
-    else:
-        r_fused_all = prods(xd, inv, [bf(w.cpu().double() * nwd[None, :]) for w in ws])
+    r_fused_all = prods(xd, inv, [bf(w.cpu().double() * nwd[None, :]) for w in ws])
     for f, p_, r_plain, r_fused in zip(fused, plain, prods(yo, 1.0, ws), r_fused_all):
         # a few rounding steps of the largest output (one bf16 step is 2^-8 to 2^-7 relative):
         # the reference's bf16 band taken relative to the output scale
@@ -497,6 +494,74 @@ def test_linear_group_norm_prologue(M, gated, dtype):
     again = linear_group(x, ws, gated=gated, norm=(nw, 1e-6, False))
     for f, a in zip(fused, [again] if gated else again):
         assert torch.equal(f, a)
+
+
+@pytest.mark.parametrize("M", [2, 7, 64, 128])
+@pytest.mark.parametrize("gated", [False, True])
+def test_gemm_multi_rms_equals_the_in_kernel_norm(M, gated):
+    """qh_gemm_multi_rms on folded weights round(W * (w + 1)) vs qh_gemm_multi_ex scaling the weight
+    fragments itself: bit for bit above 4 rows (the same operand rounding); at 2 rows (where
+    qh_gemm_multi_ex rounds x * w instead) both within the fp64 oracle's band."""
+    import ctypes
+
+    from qwen_triton import _native
+
+    Kd, dt = 1024, torch.bfloat16
+    x = randn(M, Kd, dtype=dt, seed=290, scale=2.0)
+    nw = (0.2 * randn(Kd, dtype=torch.float32, seed=291)).to(dt)
+    ns = (1024, 1024) if gated else (2048, 1024, 512)
+    ws = [randn(n, Kd, dtype=dt, seed=292 + i, scale=0.05) for i, n in enumerate(ns)]
+    folded = [(w.float() * (nw.float() + 1.0)).to(dt) for w in ws]
+    cnt = len(ws)
+    outs = {}
+    for name, bs in (("ex", ws), ("rms", folded)):
+        o = [torch.empty(M, n, dtype=dt, device="cuda") for n in (ns[:1] if gated else ns)]
+        P = ctypes.c_void_p * cnt
+        L = ctypes.c_int64 * cnt
+        bp, ld, nn = P(*(b.data_ptr() for b in bs)), L(*(Kd,) * cnt), L(*ns)
+        cp = P(*([t.data_ptr() for t in o] + [None] * (cnt - len(o))))
+        lc = L(*([t.stride(0) for t in o] + [0] * (cnt - len(o))))
+        if name == "ex":
+            _native.call("qh_gemm_multi_ex", M, Kd, x.data_ptr(), Kd, cnt, ctypes.addressof(bp), ctypes.addressof(ld),
+                         ctypes.addressof(nn), ctypes.addressof(cp), ctypes.addressof(lc), None, None, None,
+                         int(gated), nw.data_ptr(), _native.dtype_code(dt), 1e-6, 1, _native.dtype_code(dt),
+                         _native.stream(x.device))
+        else:
+            _native.call("qh_gemm_multi_rms", M, Kd, x.data_ptr(), Kd, cnt, ctypes.addressof(bp), ctypes.addressof(ld),
+                         ctypes.addressof(nn), ctypes.addressof(cp), ctypes.addressof(lc), None, int(gated), 1e-6,
+                         _native.dtype_code(dt), _native.stream(x.device))
+        outs[name] = o
+    bf = lambda t: t.to(dt).to(torch.float64)  # noqa: E731
+    xd = x.cpu().double()
+    inv = torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6)
+    ref = [O.linear(xd, f) * inv for f in folded]
+    if gated:
+        ref = [O.silu_mul(bf(ref[0]), bf(ref[1]))]
+    for a, b, r in zip(outs["ex"], outs["rms"], ref):
+        if M > 4:
+            assert torch.equal(a, b)
+        close(b, r, atol=3e-2, rtol=3e-2)
+
+
+def test_linear_group_norm_refolds_after_an_in_place_update():
+    """The folded weights are kept with the norm weight and rebuilt when a weight or the norm
+    weight changes in place (version counters): results equal a fresh group on new tensors."""
+    from qwen_triton.kernels.matmul import linear_group
+
+    Kd, dt = 512, torch.bfloat16
+    x = randn(16, Kd, dtype=dt, seed=300)
+    nw = (1.0 + 0.1 * randn(Kd, dtype=torch.float32, seed=301)).to(dt)
+    ws = [randn(256, Kd, dtype=dt, seed=302 + i, scale=0.05) for i in range(3)]
+    first = linear_group(x, ws, norm=(nw, 1e-6, False))
+    assert torch.equal(linear_group(x, ws, norm=(nw, 1e-6, False))[1], first[1])
+    with torch.no_grad():
+        ws[1].mul_(1.5)
+        nw.add_(0.25)
+    after = linear_group(x, ws, norm=(nw, 1e-6, False))
+    fresh = linear_group(x, [w.clone() for w in ws], norm=(nw.clone(), 1e-6, False))
+    for a, f, o in zip(after, fresh, first):
+        assert torch.equal(a, f)
+        assert not torch.equal(a, o)
 
 
 def test_linear_group_norm_one_plus_and_zero_rows():
@@ -514,19 +579,26 @@ def test_linear_group_norm_one_plus_and_zero_rows():
 
 
 def test_linear_group_norm_fit_limits():
-    # every workgroup must hold all K columns of its rows: K = 1024 fits the gated 64-row
-    # launch with 3072 columns (all 64 rows in one workgroup), K = 2048 does not (then the
-    # caller keeps the separate norm)
+    # qh_gemm_multi_ex's in-kernel norm needs every workgroup to hold all K columns of its rows:
+    # K = 1024 fits the gated 64-row launch with 3072 columns, K = 2048 does not. linear_group
+    # folds the norm weight into the weights (qh_gemm_multi_rms), which has no such limit.
+    import ctypes
+
     from qwen_triton.kernels.matmul import linear_group, linear_group_norm_ok
 
     x = randn(64, 2048, dtype=torch.bfloat16, seed=260)
     ws = [randn(3072, 2048, dtype=torch.bfloat16, seed=261 + i, scale=0.05) for i in range(2)]
-    nw = torch.ones(2048, dtype=torch.bfloat16, device=DEV)
-    assert not linear_group_norm_ok(x, ws, nw, gated=True)
-    with pytest.raises(_native.NativeError):
-        linear_group(x, ws, gated=True, norm=(nw, 1e-6, False))
-    assert linear_group_norm_ok(x[:, :1024].contiguous(), [w[:, :1024].contiguous() for w in ws],
-                                nw[:1024].contiguous(), gated=True)
+    nw = (1.0 + 0.1 * randn(2048, dtype=torch.float32, seed=264)).to(torch.bfloat16)
+    nn = (ctypes.c_int64 * 2)(3072, 3072)
+    assert not _native.call("qh_gemm_multi_norm_fits", 64, 2048, 1, 2, ctypes.addressof(nn))
+    assert _native.call("qh_gemm_multi_norm_fits", 64, 1024, 1, 2, ctypes.addressof(nn))
+    assert linear_group_norm_ok(x, ws, nw, gated=True)
+    out = linear_group(x, ws, gated=True, norm=(nw, 1e-6, False))
+    bf = lambda t: t.to(torch.bfloat16).to(torch.float64)  # noqa: E731
+    xd = x.cpu().double()
+    inv = torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6)
+    g, u = (O.linear(xd, bf(w.cpu().double() * nw.cpu().double()[None, :])) * inv for w in ws)
+    close(out, O.silu_mul(bf(g), bf(u)), atol=3e-2, rtol=3e-2)
 
 
 @pytest.mark.parametrize("M", [1, 64, 128])
