@@ -1476,15 +1476,14 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
     // tiles, so waiting for them never waits for a tile.
     const int64_t co_row = (pa.cos_batch == 1 ? 0 : b) * pa.scb;
     Vec16<T> xv[NPASS];
-    RowParams rp[NPASS];
+    RowRaw rr[NPASS];
 #pragma unroll
     for (int ps = 0; ps < NPASS; ++ps) {
       const int r = gi + 4 * ps;
       const T* src = r < G ? pa.q + b * pa.sq + (int64_t)(hk * G + r) * D
                            : (r == G ? pa.k + b * pa.sk : pa.v + b * pa.sv) + (int64_t)hk * D;
       xv[ps] = ld16((r < G + 2 ? src : pa.q + b * pa.sq) + dl);
-      rp[ps] = load_row_params<C, true>(r < G ? pa.qw : pa.kw, pa.wdtype, pa.wadd, d0, act, pa.half, pa.rot, pa.cs,
-                                        pa.sn, co_row);
+      rr[ps] = load_row_raw<C>(r < G ? pa.qw : pa.kw, pa.wdtype, d0, act, pa.half, pa.rot, pa.cs, pa.sn, co_row);
     }
     if (ntiles > 0) {
       issue(0, ka);
@@ -1496,7 +1495,8 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
       const bool isq = r < G, isk = r == G && pok, isv = r == G + 1 && pok;
       Vec16<T> x = xv[ps];
       if (!act) x.raw = make_uint4(0, 0, 0, 0);
-      const Vec16<T> y = norm_rope_apply<T>(x, act, rp[ps], pa.eps, D, d0, pa.half / 8, pa.half, pa.rot);
+      const RowParams rp = row_params_from<C>(rr[ps], pa.wdtype, pa.wadd, d0, act, pa.rot);
+      const Vec16<T> y = norm_rope_apply<T>(x, act, rp, pa.eps, D, d0, pa.half / 8, pa.half, pa.rot);
       if (act) {
         if (isq) {
           *reinterpret_cast<uint4*>(&qs[w][r][d0]) = y.raw;

@@ -10,44 +10,75 @@ struct RowParams {
   float w[8], c[8], s[8];
 };
 
-// VEC: 16-byte loads (w, cs and sn 16-byte aligned; C a 16-bit type; wdtype
-// fp32 or C's dtype); the values are the same as the element loads'.
-template <typename C, bool VEC = false>
+// Per-element loads (any alignment; wdtype fp32 or a 16-bit type).
+template <typename C>
 __device__ __forceinline__ RowParams load_row_params(const void* w, int wdtype, float wadd, int d0, bool act,
                                                      int half, int rot, const C* __restrict__ cs,
                                                      const C* __restrict__ sn, int64_t co_row) {
   RowParams rp;
-  if constexpr (VEC) {
-    static_assert(sizeof(C) == 2, "vector row parameters need a 16-bit cos/sin type");
-    const int dw = act ? d0 : 0;
-    if (wdtype == QH_F32) {
-      const float4 a = *reinterpret_cast<const float4*>((const float*)w + dw);
-      const float4 b = *reinterpret_cast<const float4*>((const float*)w + dw + 4);
-      const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) rp.w[e] = act ? f[e] + wadd : 0.f;
-    } else {
-      const Vec16<C> v = ld16((const C*)w + dw);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) rp.w[e] = act ? to_f32(v.v[e]) + wadd : 0.f;
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) rp.w[e] = act ? load_any(w, wdtype, d0 + e) + wadd : 0.f;
-  }
+  for (int e = 0; e < 8; ++e) rp.w[e] = act ? load_any(w, wdtype, d0 + e) + wadd : 0.f;
   if (d0 < rot) {
     const int64_t co = co_row + (d0 < half ? d0 : d0 - half);
-    if constexpr (VEC) {
-      const Vec16<C> c = ld16(cs + co), sv = ld16(sn + co);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) rp.c[e] = to_f32(c.v[e]), rp.s[e] = to_f32(sv.v[e]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) rp.c[e] = to_f32(cs[co + e]), rp.s[e] = to_f32(sn[co + e]);
-    }
+    for (int e = 0; e < 8; ++e) rp.c[e] = to_f32(cs[co + e]), rp.s[e] = to_f32(sn[co + e]);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) rp.c[e] = 0.f, rp.s[e] = 0.f;
+  }
+  return rp;
+}
+
+// The same values from 16-byte words (w, cs and sn 16-byte aligned; C a 16-bit
+// type; wdtype fp32 or C's dtype), in two steps: the raw 16-byte words, loaded with no
+// branch (so that a caller can have them in flight together with its other
+// loads before the first use: a branch ends the block the loads can be
+// scheduled in), then their conversion. w1 is the second word of fp32 weights
+// (bf16/f16 weights load the first word twice); lanes at or past rot load the
+// row's first cos/sin word (in bounds) and get zeros.
+struct RowRaw {
+  uint4 w0, w1, c, s;
+};
+
+template <typename C>
+__device__ __forceinline__ RowRaw load_row_raw(const void* w, int wdtype, int d0, bool act, int half, int rot,
+                                               const C* __restrict__ cs, const C* __restrict__ sn, int64_t co_row) {
+  static_assert(sizeof(C) == 2, "vector row parameters need a 16-bit cos/sin type");
+  const bool f32 = wdtype == QH_F32;
+  const char* wb = static_cast<const char*>(w) + (int64_t)(act ? d0 : 0) * (f32 ? 4 : 2);
+  const int64_t co = co_row + (d0 < rot ? (d0 < half ? d0 : d0 - half) : 0);
+  RowRaw r;
+  r.w0 = *reinterpret_cast<const uint4*>(wb);
+  r.w1 = *reinterpret_cast<const uint4*>(wb + (f32 ? 16 : 0));
+  r.c = *reinterpret_cast<const uint4*>(cs + co);
+  r.s = *reinterpret_cast<const uint4*>(sn + co);
+  return r;
+}
+
+template <typename C>
+__device__ __forceinline__ RowParams row_params_from(const RowRaw& r, int wdtype, float wadd, int d0, bool act,
+                                                     int rot) {
+  RowParams rp;
+  if (wdtype == QH_F32) {
+    const float f[8] = {__uint_as_float(r.w0.x), __uint_as_float(r.w0.y), __uint_as_float(r.w0.z),
+                        __uint_as_float(r.w0.w), __uint_as_float(r.w1.x), __uint_as_float(r.w1.y),
+                        __uint_as_float(r.w1.z), __uint_as_float(r.w1.w)};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rp.w[e] = act ? f[e] + wadd : 0.f;
+  } else {
+    Vec16<C> v;
+    v.raw = r.w0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rp.w[e] = act ? to_f32(v.v[e]) + wadd : 0.f;
+  }
+  Vec16<C> c, sv;
+  c.raw = r.c;
+  sv.raw = r.s;
+  const bool in = d0 < rot;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    rp.c[e] = in ? to_f32(c.v[e]) : 0.f;
+    rp.s[e] = in ? to_f32(sv.v[e]) : 0.f;
   }
   return rp;
 }
