@@ -1362,8 +1362,10 @@ struct DecodePrepArgs {
 
 // NTKV: K/V tiles read non-temporally (a large cache streamed once per step past the
 // last-level cache); short caches, read again at the next step, keep the default policy.
-template <typename T, int DP, int G, bool PREP = false, typename C = float, bool NTKV = true>
-__global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
+// NW wavefronts per workgroup (8 for short caches of more than 4 tiles, so that no
+// wave computes two tiles one after the other).
+template <typename T, int DP, int G, bool PREP = false, typename C = float, bool NTKV = true, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void fa_decode_wg_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh,
                                                           kv_ptr<T, PREP> K, int64_t skb, int64_t skh,
                                                           int64_t sks, kv_ptr<T, PREP> V, int64_t svb,
                                                           int64_t svh, int64_t svs, T* __restrict__ O,
@@ -1371,7 +1373,7 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
                                                           int Hkv, int Sk, int D, float scale_log2,
                                                           const DecodePrepArgs<T, C> pa) {
   static_assert(G >= 1 && G <= 8, "query heads per kv-head");
-  constexpr int NW = 4, BN = 32, NS = 2;
+  constexpr int BN = 32, NS = 2;
   constexpr int CPR = DP / 8;    // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;  // rows per 1 KiB load instruction
   constexpr int NI = BN / RPI;   // V load instructions per tile
@@ -1640,7 +1642,7 @@ __global__ __launch_bounds__(256) void fa_decode_wg_kernel(const T* __restrict__
   }
   __syncthreads();
   // combine the four wavefronts in order (fa_decode_combine's arithmetic)
-  for (int idx = threadIdx.x; idx < G * DP; idx += 256) {
+  for (int idx = threadIdx.x; idx < G * DP; idx += 64 * NW) {
     const int g = idx / DP, d = idx % DP;
     float M = -INFINITY;
 #pragma unroll
@@ -2081,6 +2083,10 @@ extern "C" int qh_flash_decode_prepare(const void* q, int64_t sq, const void* k,
                             (int)rot, positions, cap};                                                            \
     if (B * Hkv >= kDecodeWgMinSeqs)                                                                              \
       fa_decode_wg_kernel<T, 128, GV, true, C><<<(unsigned)(B * Hkv), 256, 0, st>>>(                             \
+          (const T*)o, 0, 0, (const T*)k_cache, kcb, kch, kcs, (const T*)v_cache, vcb, vch, vcs, (T*)o, lse,      \
+          seqlens, (int)Hkv, (int)Sk, (int)D, sl2, pa);                                                           \
+    else if (GV <= 4 && Sk > 4 * 32)                                                                               \
+      fa_decode_wg_kernel<T, 128, GV, true, C, false, (GV <= 4 ? 8 : 4)><<<(unsigned)(B * Hkv), 64 * (GV <= 4 ? 8 : 4), 0, st>>>( \
           (const T*)o, 0, 0, (const T*)k_cache, kcb, kch, kcs, (const T*)v_cache, vcb, vch, vcs, (T*)o, lse,      \
           seqlens, (int)Hkv, (int)Sk, (int)D, sl2, pa);                                                           \
     else                                                                                                           \
