@@ -95,14 +95,23 @@ def fill_cache(model, batch, ctx, capacity, seed=0):
 
 
 def decode_step_fn(model, cache, ids, ctx):
-    from qwen_triton.kernels.moe_routing import _native_topk
+    import torch
+    from qwen_triton import _native
+
+    batch, vocab = ids.shape[0], model.config.vocab_size
+    nxt = torch.empty((batch,), dtype=torch.long, device=ids.device)
+    ws = _native.workspace(_native.call("qh_greedy_step_workspace", batch, vocab), ids.device)
 
     def step():
         cache.attention_lengths = [ctx] * len(cache.attention_lengths)
         logits = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1).logits
-        # greedy pick on the library's top-1 kernel (ties to the lowest index, as argmax), the
-        # one greedy_generate's captured step uses
-        return _native_topk(logits[:, -1], 1)[1].squeeze(-1)
+        # greedy pick as greedy_generate's captured step makes it (qh_greedy_step: torch.argmax's
+        # tie and NaN rules, two launches), into a preallocated buffer: the next input ids
+        last = logits[:, -1]
+        _native.call("qh_greedy_step", last.data_ptr(), last.stride(0), batch, vocab, nxt.data_ptr(), None, 0, 0,
+                     None, None, None, ws.data_ptr(), ws.numel(), _native.dtype_code(last.dtype),
+                     _native.stream(last.device))
+        return nxt
 
     return step
 
@@ -115,7 +124,7 @@ def bench_decode(model, steps, warmup, use_graph=True, batch=64, ctx=2048):
     step = decode_step_fn(model, cache, ids, ctx)
     with torch.no_grad():
         for _ in range(max(1, warmup)):
-            eager_tok = step()
+            eager_tok = step().clone()
         sync()
         t0 = time.perf_counter()
         n_eager = max(3, min(steps, 10))
