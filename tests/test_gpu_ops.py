@@ -718,6 +718,7 @@ FA_CASES = [
     (1, 2, 1, 64, 200, 128, True, 136),
     (1, 4, 1, 130, 130, 16, True, 0),
     (2, 8, 2, 1, 513, 128, False, 0),
+    (1, 32, 4, 256, 256, 128, True, 0),  # GQA group 8, as config 4's attention
 ]
 
 
@@ -788,7 +789,7 @@ def test_flash_public_api_matches_reference_fallback_semantics():
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,S,D,causal", [(1, 4, 2, 200, 128, True), (2, 2, 1, 96, 64, False),
-                                                 (1, 2, 2, 130, 32, True)])
+                                                 (1, 2, 2, 130, 32, True), (1, 16, 2, 160, 128, True)])
 def test_flash_backward(B, Hq, Hkv, S, D, causal):
     q = randn(B, Hq, S, D, dtype=torch.bfloat16, seed=110).requires_grad_(True)
     k = randn(B, Hkv, S, D, dtype=torch.bfloat16, seed=111).requires_grad_(True)
