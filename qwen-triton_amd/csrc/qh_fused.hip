@@ -14,7 +14,11 @@ namespace {
 //   v rows:    copied into the value cache at pos[s].
 // The lane layout and the DPP reduction are those of the 16-lane RMSNorm
 // kernel and the RoPE expressions are those of the RoPE kernel.
-template <typename T, typename C>
+// VEC (16-bit cos/sin, 16-byte aligned norm weights and cos/sin rows): every
+// load of a row (the row, its norm weights, cos/sin, the position) is issued
+// before the first use, with no branch in between (load_row_raw), and the row
+// type decides only afterwards what is computed and stored. Same values.
+template <typename T, typename C, bool VEC = false>
 __global__ __launch_bounds__(256) void attn_prepare_kernel(
     const T* __restrict__ q, int64_t sq, const T* __restrict__ k, int64_t sk, const T* __restrict__ v, int64_t sv,
     const void* __restrict__ qw, const void* __restrict__ kw, int wdtype, float eps, float wadd,
@@ -32,6 +36,26 @@ __global__ __launch_bounds__(256) void attn_prepare_kernel(
     const int j = (int)(row - t * HT);
     const int64_t b = t / S;
     const int s = (int)(t - b * S);
+    if constexpr (VEC) {
+      const bool isq = j < Hq, isv = j >= Hq + Hkv;
+      const int h = isq ? j : (isv ? j - Hq - Hkv : j - Hq);
+      const T* src = isq ? q + t * sq : (isv ? v + t * sv : k + t * sk);
+      Vec16<T> xv = ld16(src + h * D + (act ? d0 : 0));
+      const RowRaw rr = load_row_raw<C>(isq ? qw : kw, wdtype, d0, act, half, rot, cs, sn,
+                                        (cos_batch == 1 ? 0 : b) * scb + s * scs);
+      const int64_t p = pos[s];
+      if (!act) xv.raw = make_uint4(0, 0, 0, 0);
+      if (isv) {
+        if (act && p >= 0 && p < cap) st16(vc + b * vcb + h * vch + p * vcs + d0, xv);
+        continue;
+      }
+      const RowParams rp = row_params_from<C>(rr, wdtype, wadd, d0, act, rot);
+      const Vec16<T> o = norm_rope_apply<T>(xv, act, rp, eps, D, d0, hl, half, rot);
+      if (!act) continue;
+      if (isq) st16(q_out + ((b * Hq + h) * (int64_t)S + s) * D + d0, o);
+      else if (p >= 0 && p < cap) st16(kc + b * kcb + h * kch + p * kcs + d0, o);
+      continue;
+    }
     const int64_t p = pos[s];
     Vec16<T> xv;
     xv.raw = make_uint4(0, 0, 0, 0);
@@ -50,6 +74,26 @@ __global__ __launch_bounds__(256) void attn_prepare_kernel(
     if (isq) st16(q_out + ((b * Hq + h) * (int64_t)S + s) * D + d0, o);
     else if (p >= 0 && p < cap) st16(kc + b * kcb + h * kch + p * kcs + d0, o);
   }
+}
+
+// Launch of attn_prepare_kernel, the vector form where it applies (16-bit cos/sin).
+template <typename T, typename C>
+void launch_attn_prepare(bool vec, unsigned grid, hipStream_t st, const T* q, int64_t sq, const T* k, int64_t sk,
+                         const T* v, int64_t sv, const void* qw, const void* kw, int wdtype, float eps, float wadd,
+                         const C* cs, const C* sn, int64_t scb, int64_t scs, int64_t cos_batch, int half, int rot,
+                         T* q_out, T* kc, int64_t kcb, int64_t kch, int64_t kcs, T* vc, int64_t vcb, int64_t vch,
+                         int64_t vcs, const int64_t* pos, int S, int Hq, int Hkv, int D, int64_t cap, int64_t rows) {
+  if constexpr (sizeof(C) == 2) {
+    if (vec) {
+      attn_prepare_kernel<T, C, true><<<grid, 256, 0, st>>>(q, sq, k, sk, v, sv, qw, kw, wdtype, eps, wadd, cs, sn, scb,
+                                                           scs, cos_batch, half, rot, q_out, kc, kcb, kch, kcs, vc,
+                                                           vcb, vch, vcs, pos, S, Hq, Hkv, D, cap, rows);
+      return;
+    }
+  }
+  attn_prepare_kernel<T, C, false><<<grid, 256, 0, st>>>(q, sq, k, sk, v, sv, qw, kw, wdtype, eps, wadd, cs, sn, scb, scs,
+                                                        cos_batch, half, rot, q_out, kc, kcb, kch, kcs, vc, vcb, vch,
+                                                        vcs, pos, S, Hq, Hkv, D, cap, rows);
 }
 
 }  // namespace
@@ -83,15 +127,25 @@ extern "C" int qh_attn_prepare(const void* q, int64_t sq, const void* k, int64_t
   const float wadd = one_plus ? 1.f : 0.f;
   const int64_t nblk = (rows + 15) / 16;
   const unsigned grid = (unsigned)(nblk < 65536 ? nblk : 65536);
+  const bool vec = cdtype != QH_F32 && aligned16(qw) && aligned16(kw) && aligned16(cos) && aligned16(sin) &&
+                   scb % 8 == 0 && scs % 8 == 0;
 #define QH_PREP(T, C)                                                                                            \
-  attn_prepare_kernel<T, C><<<grid, 256, 0, st>>>(                                                              \
-      (const T*)q, sq, (const T*)k, sk, (const T*)v, sv, qw, kw, wdtype, eps, wadd, (const C*)cos, (const C*)sin, \
-      scb, scs, cos_batch, (int)half, (int)rot, (T*)q_out, (T*)k_cache, kcb, kch, kcs, (T*)v_cache, vcb, vch, vcs, \
-      positions, (int)S, (int)Hq, (int)Hkv, (int)D, cap, rows)
+  launch_attn_prepare<T, C>(vec, grid, st, (const T*)q, sq, (const T*)k, sk, (const T*)v, sv, qw, kw, wdtype, eps, \
+                            wadd, (const C*)cos, (const C*)sin, scb, scs, cos_batch, (int)half, (int)rot, (T*)q_out, \
+                            (T*)k_cache, kcb, kch, kcs, (T*)v_cache, vcb, vch, vcs, positions, (int)S, (int)Hq,    \
+                            (int)Hkv, (int)D, cap, rows)
   if (dtype == QH_BF16) {
-    if (cdtype == QH_F32) QH_PREP(bf16_t, float); else QH_PREP(bf16_t, bf16_t);
+    if (cdtype == QH_F32) {
+      QH_PREP(bf16_t, float);
+    } else {
+      QH_PREP(bf16_t, bf16_t);
+    }
   } else {
-    if (cdtype == QH_F32) QH_PREP(f16_t, float); else QH_PREP(f16_t, f16_t);
+    if (cdtype == QH_F32) {
+      QH_PREP(f16_t, float);
+    } else {
+      QH_PREP(f16_t, f16_t);
+    }
   }
 #undef QH_PREP
   QH_CHECK_LAUNCH("qh_attn_prepare");
