@@ -340,7 +340,16 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   static_assert(MT * 16 * RB <= SLOT && CH >= 2, "activation block exceeds the slice's LDS slot");
   static_assert(16 * MT * 16 * 16 * 4 <= kDecodeLds, "K-slice sums exceed the slots");
   __shared__ __align__(16) unsigned char abuf[kDecodeLds];
+  // K-slice partials. MT = 4 (1024 threads for 4 rows per wave per column):
+  // per wave, MT x 64 words of 4 rows (16 i + 4 q .. + 3) of column li, word
+  // i * 64 + q * 16 + li, so a lane writes its 4 rows of a row tile as one
+  // 16-byte word and a summing thread takes 4 outputs. MT < 4: one float per
+  // output, [wave][row][column], and a summing thread takes one output (with 4
+  // outputs per thread too few threads would share the sums).
+  constexpr bool WORDS = MT == 4;
+  f32x4* redw = reinterpret_cast<f32x4*>(abuf);
   float(*red)[MT * 16][16] = reinterpret_cast<float(*)[MT * 16][16]>(abuf);
+  __shared__ float rfac[ROWS && WORDS ? MT * 16 : 1];
   __shared__ float nss[ROWS ? 16 : 1][MT * 16];
   // Workgroup -> (column tile, row group). The ms row groups of a tile get
   // workgroup ids that are equal mod 8, so they run on one XCD and read the
@@ -448,45 +457,98 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   }
   // Sum the K slices in order, one weight matrix at a time through the same
   // LDS buffer. C layout: column li, rows 16 i + 4 q + r.
-  float first[(CG * MT * 256 + 1023) / 1024];
+  if constexpr (WORDS) {
+    constexpr int NW4 = MT * 64;  // words per wave
+    float first[(CG * NW4 + 1023) / 1024][4];
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    __syncthreads();  // every wave's fragments (j = 0) or the previous matrix's sums have been read
+    for (int j = 0; j < NB; ++j) {
+      __syncthreads();  // every wave's fragments (j = 0) or the previous matrix's sums have been read
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+      for (int i = 0; i < MT; ++i) redw[wid * NW4 + i * 64 + q * 16 + li] = acc[j][i];
+      if constexpr (ROWS) {  // each row's RMSNorm factor, once (column group 0's slices, in order)
+        if (j == 0 && threadIdx.x < MT * 16) {
+          float ss = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wid][i * 16 + q * 4 + r][li] = acc[j][i][r];
-    __syncthreads();
-    int slot = 0;
-    for (int idx = threadIdx.x; idx < CG * MT * 256; idx += 1024, ++slot) {
-      const int g = idx / (MT * 256), rem = idx % (MT * 256);
-      const int row = rem / 16, col = rem % 16;
-      float v = 0.f;
-#pragma unroll
-      for (int s2 = 0; s2 < KSP; ++s2) v += red[g * KSP + s2][row][col];
-      const int gn = (tile * CG + g) * 16 + col;
-      const int grow = m0 + row;
-      if (grow >= M || gn >= N) continue;
-      const T* bias = P.bias[pi + j];
-      if constexpr (ROWS) {  // the row's RMSNorm factor (slices summed in order)
-        float ss = 0.f;
-#pragma unroll
-        for (int s2 = 0; s2 < KSP; ++s2) ss += nss[s2][row];  // column group 0's slices
-        v *= rsqrtf(ss / (float)K + nrm.eps);
-      }
-      const float val = v + (bias ? to_f32(bias[gn]) : 0.f);
-      if constexpr (GATED) {
-        if (j == 0) {
-          first[slot] = to_f32(from_f32<OT>(val));
-        } else {
-          const float gt = first[slot], up = to_f32(from_f32<OT>(val));
-          P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
+          for (int s2 = 0; s2 < KSP; ++s2) ss += nss[s2][threadIdx.x];
+          rfac[threadIdx.x] = rsqrtf(ss / (float)K + nrm.eps);
         }
-      } else {
-        OT o = from_f32<OT>(val);
-        const T* res = P.res[pi];
-        if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)grow * P.ldr[pi] + gn]));
-        P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = o;
+      }
+      __syncthreads();
+      int slot = 0;
+      for (int idx = threadIdx.x; idx < CG * NW4; idx += 1024, ++slot) {
+        const int g = idx / NW4, rem = idx % NW4;
+        const int col = rem % 16, row0 = (rem / 64) * 16 + ((rem / 16) % 4) * 4;
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < KSP; ++s2) v += redw[(g * KSP + s2) * NW4 + rem];
+        const int gn = (tile * CG + g) * 16 + col;
+        if (gn >= N) continue;
+        const T* bias = P.bias[pi + j];
+        const float bv = bias ? to_f32(bias[gn]) : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int grow = m0 + row0 + r;
+          if (grow >= M) continue;
+          float val = v[r];
+          if constexpr (ROWS) val *= rfac[row0 + r];
+          val += bv;
+          if constexpr (GATED) {
+            if (j == 0) {
+              first[slot][r] = to_f32(from_f32<OT>(val));
+            } else {
+              const float gt = first[slot][r], up = to_f32(from_f32<OT>(val));
+              P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
+            }
+          } else {
+            OT o = from_f32<OT>(val);
+            const T* res = P.res[pi];
+            if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)grow * P.ldr[pi] + gn]));
+            P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = o;
+          }
+        }
+      }
+    }
+  } else {
+    float first[(CG * MT * 256 + 1023) / 1024];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      __syncthreads();  // every wave's fragments (j = 0) or the previous matrix's sums have been read
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wid][i * 16 + q * 4 + r][li] = acc[j][i][r];
+      __syncthreads();
+      int slot = 0;
+      for (int idx = threadIdx.x; idx < CG * MT * 256; idx += 1024, ++slot) {
+        const int g = idx / (MT * 256), rem = idx % (MT * 256);
+        const int row = rem / 16, col = rem % 16;
+        float v = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < KSP; ++s2) v += red[g * KSP + s2][row][col];
+        const int gn = (tile * CG + g) * 16 + col;
+        const int grow = m0 + row;
+        if (grow >= M || gn >= N) continue;
+        const T* bias = P.bias[pi + j];
+        if constexpr (ROWS) {  // the row's RMSNorm factor (slices summed in order)
+          float ss = 0.f;
+#pragma unroll
+          for (int s2 = 0; s2 < KSP; ++s2) ss += nss[s2][row];  // column group 0's slices
+          v *= rsqrtf(ss / (float)K + nrm.eps);
+        }
+        const float val = v + (bias ? to_f32(bias[gn]) : 0.f);
+        if constexpr (GATED) {
+          if (j == 0) {
+            first[slot] = to_f32(from_f32<OT>(val));
+          } else {
+            const float gt = first[slot], up = to_f32(from_f32<OT>(val));
+            P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
+          }
+        } else {
+          OT o = from_f32<OT>(val);
+          const T* res = P.res[pi];
+          if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)grow * P.ldr[pi] + gn]));
+          P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = o;
+        }
       }
     }
   }
