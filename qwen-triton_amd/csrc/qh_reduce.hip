@@ -947,39 +947,36 @@ __global__ __launch_bounds__(256) void greedy_partial_kernel(const T* __restrict
   }
 }
 
-// Stage 2 (one workgroup): each row's answer from its P partial keys, then the step's
-// bookkeeping: ids[b] = tokens[b, col] = answer, seqlens[b] += 1, col += 1, positions += 1
-// (each pointer optional). One thread reads the counters before writing them.
-__global__ __launch_bounds__(256) void greedy_finish_kernel(const uint64_t* __restrict__ part, int P, int B,
-                                                            int64_t* __restrict__ ids, int64_t* __restrict__ tokens,
-                                                            int64_t ldt, int64_t ncols, int64_t* __restrict__ col,
-                                                            int64_t* __restrict__ positions,
-                                                            int32_t* __restrict__ seqlens) {
-  __shared__ uint64_t sk[4];
-  __shared__ int64_t ans[kGreedyMaxRows];
-  for (int b = 0; b < B; ++b) {
+// Stage 2 (one workgroup, a 16-lane group per row): each row's answer from its P partial
+// keys, then the step's bookkeeping: ids[b] = tokens[b, col] = answer, seqlens[b] += 1 (the
+// row's group), col += 1, positions += 1 (thread 0, after every group has read col). Each
+// pointer is optional.
+__global__ __launch_bounds__(kGreedyMaxRows * 16) void greedy_finish_kernel(
+    const uint64_t* __restrict__ part, int P, int B, int64_t* __restrict__ ids, int64_t* __restrict__ tokens,
+    int64_t ldt, int64_t ncols, int64_t* __restrict__ col, int64_t* __restrict__ positions,
+    int32_t* __restrict__ seqlens) {
+  const int b = threadIdx.x >> 4, l = threadIdx.x & 15;
+  const int64_t c = col ? col[0] : -1;
+  if (b < B) {
     uint64_t best = 0;
-    for (int p = threadIdx.x; p < P; p += 256) {
+    for (int p = l; p < P; p += 16) {
       const uint64_t k = part[(int64_t)b * P + p];
       best = k > best ? k : best;
     }
-    best = wave_max_u64(best);
-    if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = best;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      uint64_t m = sk[0];
-      for (int w = 1; w < 4; ++w) m = sk[w] > m ? sk[w] : m;
-      ans[b] = (int64_t)(uint32_t)~(uint32_t)m;
+    for (int o = 8; o > 0; o >>= 1) {  // within the 16-lane group
+      const uint64_t k2 = ((uint64_t)(uint32_t)__shfl_xor((int)(best >> 32), o) << 32) |
+                          (uint32_t)__shfl_xor((int)(uint32_t)best, o);
+      best = k2 > best ? k2 : best;
     }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    const int64_t c = col ? col[0] : -1;
-    for (int b = 0; b < B; ++b) {
-      if (ids) ids[b] = ans[b];
-      if (tokens && c >= 0 && c < ncols) tokens[(int64_t)b * ldt + c] = ans[b];
+    if (l == 0) {
+      const int64_t ans = (int64_t)(uint32_t)~(uint32_t)best;
+      if (ids) ids[b] = ans;
+      if (tokens && c >= 0 && c < ncols) tokens[(int64_t)b * ldt + c] = ans;
       if (seqlens) seqlens[b] += 1;
     }
+  }
+  __syncthreads();  // every read of col has completed
+  if (threadIdx.x == 0) {
     if (col) col[0] = c + 1;
     if (positions) positions[0] += 1;
   }
@@ -1201,7 +1198,8 @@ extern "C" int qh_greedy_step(const void* logits, int64_t ld, int64_t B, int64_t
   greedy_partial_kernel<TT><<<dim3((unsigned)P, (unsigned)B), 256, 0, st>>>((const TT*)logits, ld, (int)V, part, P)
   if (dtype == QH_BF16) { QH_GREEDY(bf16_t); } else if (dtype == QH_F16) { QH_GREEDY(f16_t); } else { QH_GREEDY(float); }
 #undef QH_GREEDY
-  greedy_finish_kernel<<<1, 256, 0, st>>>(part, P, (int)B, ids, tokens, ldt, ncols, col, positions, seqlens);
+  greedy_finish_kernel<<<1, kGreedyMaxRows * 16, 0, st>>>(part, P, (int)B, ids, tokens, ldt, ncols, col, positions,
+                                                         seqlens);
   QH_CHECK_LAUNCH("qh_greedy_step");
   return QH_OK;
 }

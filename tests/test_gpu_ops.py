@@ -1274,7 +1274,7 @@ def test_gated_delta_rule_matches_oracle(B, S, H, K, V, dtype, init):
 # ---------------------------------------------------------------------------
 # greedy decode step
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("B,V", [(1, 151936), (3, 1000), (64, 4104), (2, 8)])
+@pytest.mark.parametrize("B,V", [(1, 151936), (3, 1000), (64, 4104), (64, 151936), (2, 8)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_greedy_step_is_argmax_and_advances_the_state(B, V, dtype):
     """qh_greedy_step against torch.argmax of the same values (ties to the lowest column, NaN the
