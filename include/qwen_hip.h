@@ -103,12 +103,13 @@ int qh_kv_append(const void* prefix, const void* suffix, void* out, int64_t B, i
  * Replaces qwen_triton/kernels/embedding.py:50-60 (_embedding_kernel), :97-112. */
 int qh_embedding_fwd(const int64_t* ids, const void* w, int64_t stride_w, void* out, int64_t n_tokens,
                      int64_t V, int64_t Hd, int dtype, void* stream);
-/* Workspace bytes of qh_embedding_bwd: id sort space for n_tokens plus two
- * int32 per embedding row (the [first, end) sorted positions of its tokens). */
+/* Workspace bytes of qh_embedding_bwd: id sort space for n_tokens. */
 int64_t qh_embedding_bwd_workspace(int64_t n_tokens, int64_t V);
 /* gw[v,:] = sum_{t: ids[t]==v} gout[t,:] (fp32 sum in token order, stored as
  * wdtype), gw[padding_idx] = 0; rows never referenced are zero. Deterministic
- * (radix sort by id, then each gw row written once: zeros or its ordered sum).
+ * (radix sort by id, then each referenced row written once with its ordered
+ * sum, the others with zeros; a wave walks a range of rows and the sorted ids
+ * together, so no per-row table is built).
  * Replaces qwen_triton/kernels/embedding.py:78-94 (_embedding_backward_kernel), :124-145. */
 int qh_embedding_bwd(const int64_t* ids, const void* gout, void* gw, void* ws, int64_t ws_bytes,
                      int64_t n_tokens, int64_t V, int64_t Hd, int64_t padding_idx, int gdtype,

@@ -123,85 +123,73 @@ __global__ __launch_bounds__(64) void segment_rows_vec(const uint32_t* __restric
   }
 }
 
-__global__ __launch_bounds__(256) void fill_i32(int32_t* __restrict__ p, int64_t n, int32_t v) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = v;
-}
+// Embedding weight gradient, every row written exactly once after the sort, by waves of two
+// roles in one launch (no wave both loads gradient rows and streams stores: stores count in the
+// same vmcnt as loads, so a load wait would also wait for the store stream).
+// - Zero waves (the first zgrid workgroups): a wave owns rpw <= 128 consecutive rows, finds the
+//   first sorted position with a key at or above its first row by a 64-way search (one load per
+//   lane per round, about log64(n) rounds), marks the rows some token hits (64 keys per load),
+//   then writes zeros to the others (the padding row included).
+// - Run waves (the rest, one per sorted position): the first position of each key's run sums
+//   the run's gradient rows in position order (fp32, rounded once) into the row, except for the
+//   padding row and ids outside [0, V).
+constexpr int64_t kEmbRowsPerWave = 128;
 
-// runs[k] = [first, end) sorted positions of key k (keys below n_target only).
-__global__ __launch_bounds__(256) void mark_runs(const uint32_t* __restrict__ keys, int64_t n, uint32_t n_target,
-                                                 int2* __restrict__ runs) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const uint32_t k = keys[i];
-  if (k >= n_target || (i > 0 && keys[i - 1] == k)) return;
-  int64_t e = i + 1;
-  while (e < n && keys[e] == k) ++e;
-  runs[k] = make_int2((int)i, (int)e);
-}
-
-// Embedding weight gradient written row by row, each row exactly once: zeros
-// for rows no token hit (and the padding row), else the ordered fp32 sum of
-// the row's gradient rows, rounded once. A wave takes tiles of 16 consecutive
-// rows (grid-stride, so neighbouring waves write neighbouring tiles). Their
-// run bounds come in through scalar loads, and the rows that need loads are
-// done before the zero rows: stores count in the same vmcnt as loads, so a
-// wait for a load also waits for every store issued before it.
 template <typename S, typename O>
-__global__ __launch_bounds__(256) void embedding_grad_rows(const int2* __restrict__ runs,
-                                                           const uint32_t* __restrict__ vals,
-                                                           const S* __restrict__ src, O* __restrict__ dst, int64_t V,
-                                                           int64_t D, int64_t skip_key) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  for (int64_t v0 = ((int64_t)blockIdx.x * 4 + wave) * 16; v0 < V; v0 += (int64_t)gridDim.x * 64) {
-    const int nr = (int)(V - v0 < 16 ? V - v0 : 16);
-    const int2* wr = runs + v0;
-    uint32_t hits = 0;
-    if (nr == 16) {
+__global__ __launch_bounds__(256) void embedding_rows_roles(const uint32_t* __restrict__ keys,
+                                                            const uint32_t* __restrict__ vals, int n,
+                                                            const S* __restrict__ src, O* __restrict__ dst, int64_t V,
+                                                            int64_t D, int64_t skip_key, int64_t rpw, int zgrid) {
+  __shared__ uint32_t hitw[4][4];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if ((int)blockIdx.x >= zgrid) {  // run waves
+    const int i = (blockIdx.x - zgrid) * 4 + wid;
+    if (i >= n) return;
+    const uint32_t k = keys[i];
+    if ((int64_t)k >= V || (int64_t)k == skip_key || (i > 0 && keys[i - 1] == k)) return;
+    int e = i + 1;
+    while (e < n && keys[e] == k) ++e;
+    O* drow = dst + (int64_t)k * D;
+    for (int64_t c = lane * 8; c < D; c += 64 * 8) {
+      float acc[8];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int2 se = wr[r];
-        if (se.x >= 0 && v0 + r != skip_key) hits |= 1u << r;
-      }
-    } else {
-      for (int r = 0; r < nr; ++r) {
-        const int2 se = wr[r];
-        if (se.x >= 0 && v0 + r != skip_key) hits |= 1u << r;
-      }
+      for (int q = 0; q < 8; ++q) acc[q] = 0.f;
+      run_sum8(vals, i, e, src, D, c, acc);
+      st8f(drow + c, acc);
     }
-    for (int r = 0; r < nr; ++r) {
-      if (!(hits >> r & 1)) continue;
-      const int2 se = wr[r];
-      O* drow = dst + (v0 + r) * D;
-      for (int64_t c = lane * 8; c < D; c += 2 * 64 * 8) {
-        const int64_t c2 = c + 64 * 8;
-        float a[8], b[8];
+    return;
+  }
+  const int64_t wave = (int64_t)blockIdx.x * 4 + wid;
+  const int64_t a = wave * rpw, b = a + rpw < V ? a + rpw : V;
+  if (lane < 4) hitw[wid][lane] = 0u;
+  __syncthreads();  // every wave of a zero-role workgroup reaches both barriers (empty ranges too)
+  // first position p in [0, n) with keys[p] >= a (n if none); wave-uniform throughout
+  int lo = 0, len = a < b ? n : 0;
+  while (len > 0) {
+    const int step = (len + 63) / 64;
+    const int idx = lo + lane * step;
+    const bool less = idx < lo + len && (int64_t)keys[idx] < a;
+    const int c = __popcll(__ballot(less));
+    if (c == 0) break;
+    const int nlo = lo + (c - 1) * step + 1;
+    const int hi = lo + c * step < lo + len ? lo + c * step : lo + len;
+    lo = nlo;
+    len = hi - nlo;
+  }
+  // mark the hit rows of [a, b): 64 sorted keys per round
+  for (int p = lo; a < b && p < n; p += 64) {
+    const int64_t k = p + lane < n ? (int64_t)keys[p + lane] : V;
+    if (k < b && k != skip_key) atomicOr(&hitw[wid][(k - a) >> 5], 1u << ((k - a) & 31));
+    if (__any(k >= b)) break;  // keys are sorted: the range ends in this round
+  }
+  __syncthreads();
+  float z[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) a[q] = 0.f, b[q] = 0.f;
-        for (int j = se.x; j < se.y; ++j) {
-          const S* sr = src + (int64_t)vals[j] * D;
-          float t[8], u[8];
-          ld8f(sr + c, t);
-          if (c2 < D) ld8f(sr + c2, u);
-#pragma unroll
-          for (int q = 0; q < 8; ++q) a[q] += t[q];
-          if (c2 < D)
-#pragma unroll
-            for (int q = 0; q < 8; ++q) b[q] += u[q];
-        }
-        st8f(drow + c, a);
-        if (c2 < D) st8f(drow + c2, b);
-      }
-    }
-    float z[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) z[q] = 0.f;
-    for (int r = 0; r < nr; ++r) {
-      if (hits >> r & 1) continue;
-      O* drow = dst + (v0 + r) * D;
-      for (int64_t c = lane * 8; c < D; c += 64 * 8) st8f(drow + c, z);
-    }
+  for (int q = 0; q < 8; ++q) z[q] = 0.f;
+  for (int64_t r = a; r < b; ++r) {
+    if (hitw[wid][(r - a) >> 5] >> ((r - a) & 31) & 1) continue;
+    O* drow = dst + r * D;
+    for (int64_t c = lane * 8; c < D; c += 64 * 8) st8f(drow + c, z);
   }
 }
 
@@ -268,10 +256,10 @@ static int sort_indices(const int64_t* idx, int64_t n, int64_t n_target, void* w
 
 }  // namespace
 
-// Sort space for the token ids plus a run table of two int32 per embedding row.
+// Sort space for the token ids (V is part of the signature; the rows need no table).
 extern "C" int64_t qh_embedding_bwd_workspace(int64_t n_tokens, int64_t V) {
   if (n_tokens <= 0 || V <= 0) return 0;
-  return scatter_ws_bytes(n_tokens) + align256(V * 8);
+  return scatter_ws_bytes(n_tokens);
 }
 
 extern "C" int64_t qh_index_add_workspace(int64_t n_src) { return scatter_ws_bytes(n_src); }
@@ -290,11 +278,11 @@ extern "C" int qh_embedding_bwd(const int64_t* ids, const void* gout, void* gw, 
     return QH_E_WORKSPACE;
   }
   const int64_t sort_bytes = scatter_ws_bytes(n_tokens);
-  uint32_t *keys = nullptr, *vals = nullptr;
-  int rc = sort_indices(ids, n_tokens, V, ws, sort_bytes, &keys, &vals, st, "qh_embedding_bwd");
-  if (rc) return rc;
   const bool vec = Hd % 8 == 0 && aligned16(gout) && aligned16(gw);
   if (!vec) {
+    uint32_t *keys = nullptr, *vals = nullptr;
+    int rc = sort_indices(ids, n_tokens, V, ws, sort_bytes, &keys, &vals, st, "qh_embedding_bwd");
+    if (rc) return rc;
     rc = qh_zero(gw, V * Hd * wsz, stream);
     if (rc) return rc;
     rc = launch_segments<false>(keys, vals, n_tokens, gout, gdtype, Hd, gw, wdtype, Hd, Hd, (uint32_t)V, padding_idx,
@@ -303,12 +291,19 @@ extern "C" int qh_embedding_bwd(const int64_t* ids, const void* gout, void* gw, 
     QH_CHECK_LAUNCH("qh_embedding_bwd");
     return QH_OK;
   }
-  int2* runs = (int2*)((char*)ws + sort_bytes);
-  fill_i32<<<(int)std::min<int64_t>(ceil_div(2 * V, 256), 2048), 256, 0, st>>>((int32_t*)runs, 2 * V, -1);
-  mark_runs<<<(int)ceil_div(n_tokens, 256), 256, 0, st>>>(keys, n_tokens, (uint32_t)V, runs);
-  const int grid = (int)std::min<int64_t>(ceil_div(V, 64), 2048);
-#define QH_EROWS(S, O) \
-  embedding_grad_rows<S, O><<<grid, 256, 0, st>>>(runs, vals, (const S*)gout, (O*)gw, V, Hd, padding_idx)
+  uint32_t *keys = nullptr, *vals = nullptr;
+  int rc = sort_indices(ids, n_tokens, V, ws, sort_bytes, &keys, &vals, st, "qh_embedding_bwd");
+  if (rc) return rc;
+  // zero waves: about 8 per CU (more for tables above 2048 x 128 rows), each over a contiguous
+  // range of rows; then one run wave per sorted position
+  const int64_t waves = std::max<int64_t>(std::min<int64_t>(ceil_div(V, 16), 2048), ceil_div(V, kEmbRowsPerWave));
+  const int64_t rpw = ceil_div(V, waves);
+  const int64_t zgrid = ceil_div(ceil_div(V, rpw), 4);
+  const int64_t grid = zgrid + ceil_div(n_tokens, 4);
+  QH_CHECK_ARG(grid < (1ll << 31), "qh_embedding_bwd: grid too large");
+#define QH_EROWS(S, O)                                                                                   \
+  embedding_rows_roles<S, O><<<(unsigned)grid, 256, 0, st>>>(keys, vals, (int)n_tokens, (const S*)gout, (O*)gw, V, \
+                                                             Hd, padding_idx, rpw, (int)zgrid)
 #define QH_EROWS_O(S)                                      \
   switch (wdtype) {                                        \
     case QH_F32: QH_EROWS(S, float); break;                \

@@ -213,6 +213,71 @@ def test_embedding_backward_is_token_order_fp32_sum(H):
     assert torch.equal(w.grad.cpu().view(torch.int16), exp.to(torch.bfloat16).view(torch.int16))
 
 
+@pytest.mark.parametrize("n,wdt", [(1, torch.bfloat16), (771, torch.bfloat16), (16384, torch.bfloat16),
+                                   (16385, torch.bfloat16), (4000, torch.float32)])
+def test_embedding_backward_writes_every_row(n, wdt):
+    """qh_embedding_bwd through the C ABI into a gradient buffer full of 7.0: every row is written
+    (exact zeros for unreferenced rows and the padding row) and each hit row is the token-order
+    fp32 sum rounded once (the row walk's search starts and ends its ranges at every run
+    boundary whatever the token count)."""
+    V, H, pad = 5000, 64, 7
+    g = _gen(55)
+    ids = torch.randint(0, 300, (n,), generator=g)
+    ids[1:min(6, n)] = pad
+    ids[-1] = V - 1
+    go = torch.randn(n, H, generator=g).to(torch.bfloat16)
+    gw = torch.full((V, H), 7.0, dtype=wdt, device=DEV)
+    ids_d, go_d = ids.to(DEV), go.to(DEV)
+    ws = _native.workspace(_native.call("qh_embedding_bwd_workspace", n, V), gw.device)
+    c0 = native_calls("qh_embedding_bwd")
+    _native.call("qh_embedding_bwd", ids_d.data_ptr(), go_d.data_ptr(), gw.data_ptr(), ws.data_ptr(), ws.numel(),
+                 n, V, H, pad, _native.dtype_code(torch.bfloat16), _native.dtype_code(wdt), _native.stream(gw.device))
+    assert native_calls("qh_embedding_bwd") == c0 + 1
+    exp = torch.zeros(V, H, dtype=torch.float32)
+    flat_go = go.float()
+    for t, v in enumerate(ids.tolist()):
+        exp[v] += flat_go[t]
+    exp[pad] = 0
+    exp = exp.to(wdt)
+    got = gw.cpu()
+    bits = torch.int16 if wdt == torch.bfloat16 else torch.int32
+    assert torch.equal(got.view(bits), exp.view(bits))
+
+
+def test_embedding_backward_in_a_captured_graph():
+    """qh_embedding_bwd captured in a HIP graph (the device-wide id sort and the row walk):
+    every replay, with eager work between replays, equals the eager result bit for bit."""
+    V, H, n, pad = 3000, 128, 2000, 3
+    g = _gen(56)
+    ids = torch.randint(0, 500, (n,), generator=g).to(DEV)
+    go = torch.randn(n, H, generator=g).to(torch.bfloat16).to(DEV)
+    ws = _native.workspace(_native.call("qh_embedding_bwd_workspace", n, V), go.device)
+    gw = torch.full((V, H), 5.0, dtype=torch.bfloat16, device=DEV)
+
+    def run():
+        _native.call("qh_embedding_bwd", ids.data_ptr(), go.data_ptr(), gw.data_ptr(), ws.data_ptr(), ws.numel(),
+                     n, V, H, pad, _native.dtype_code(torch.bfloat16), _native.dtype_code(torch.bfloat16),
+                     _native.stream(gw.device))
+
+    run()
+    torch.cuda.synchronize()
+    eager = gw.clone()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            run()
+    torch.cuda.current_stream().wait_stream(s)
+    for r in range(3):
+        gw.fill_(float(r + 7))
+        x = torch.randn(256, 256, device=DEV) @ torch.randn(256, 256, device=DEV)  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(x).all()
+        assert torch.equal(gw.view(torch.int16), eager.view(torch.int16)), f"replay {r}"
+
+
 # ---------------------------------------------------------------------------
 # Softmax / cross-entropy
 # ---------------------------------------------------------------------------
