@@ -605,6 +605,24 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
     const int nj = RC > 1 ? min(n + j, P.N[pi] - 1) : n;  // columns past N re-read the last row
     brow[j] = P.B[pi + (RC > 1 ? 0 : j)] + (int64_t)nj * P.ldb[pi + (RC > 1 ? 0 : j)];
   }
+  // Bias and residual of the row this lane writes (lane i writes row i), loaded before the
+  // weight stream so their latency is not added after the reduction. C may be the residual
+  // itself: each element is read and then written by this lane only.
+  float pb[NB], pr[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) pb[j] = 0.f, pr[j] = 0.f;
+  if (lane < MR && lane < M) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const T* bias = P.bias[pi + (RC > 1 ? 0 : j)];
+      if (bias != nullptr) pb[j] = to_f32(bias[RC > 1 ? min(n + j, P.N[pi] - 1) : n]);
+      if constexpr (!GATED) {
+        const T* res = P.res[pi];
+        if (res != nullptr && (RC == 1 || n + j < P.N[pi]))
+          pr[j] = to_f32(res[(int64_t)lane * P.ldr[pi] + n + (RC > 1 ? j : 0)]);
+      }
+    }
+  }
   float acc[NB][MR], ss[MR];
 #pragma unroll
   for (int i = 0; i < MR; ++i) {
@@ -664,16 +682,15 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
     for (int j = 0; j < NB; ++j) {
       v[j] = acc[j][i];
       if constexpr (ROWS) v[j] *= rsqrtf(ss[i] / (float)K + nrm.eps);
-      const T* bias = P.bias[pi + (RC > 1 ? 0 : j)];
-      v[j] += bias ? to_f32(bias[RC > 1 ? min(n + j, P.N[pi] - 1) : n]) : 0.f;
+      v[j] += pb[j];
     }
     if constexpr (RC > 1) {
-      const T* res = P.res[pi];
+      const bool res = P.res[pi] != nullptr;
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
         if (n + j >= P.N[pi]) continue;
         OT o = from_f32<OT>(v[j]);
-        if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)i * P.ldr[pi] + n + j]));
+        if (res) o = from_f32<OT>(to_f32(o) + pr[j]);
         P.C[pi][(int64_t)i * P.ldc[pi] + n + j] = o;
       }
     } else if constexpr (GATED) {
@@ -681,8 +698,7 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
       P.C[pi][(int64_t)i * P.ldc[pi] + n] = from_f32<OT>(gt * sigmoidf_(gt) * up);
     } else {
       OT o = from_f32<OT>(v[0]);
-      const T* res = P.res[pi];
-      if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)i * P.ldr[pi] + n]));
+      if (P.res[pi] != nullptr) o = from_f32<OT>(to_f32(o) + pr[0]);
       P.C[pi][(int64_t)i * P.ldc[pi] + n] = o;
     }
   }
