@@ -239,6 +239,13 @@ struct EpiTile {
   __device__ __forceinline__ Vec16<T> row8(int r, int c8) const { return ld16(base + at(r, 8 * c8)); }
 };
 
+// Problems that define kPersistent = true place their tiles through tile_at()
+// on a logical index (see the schedule in gemm_tile_kernel).
+template <class P, class = void>
+struct TilePersistent : std::false_type {};
+template <class P>
+struct TilePersistent<P, std::void_t<decltype(P::kPersistent)>> : std::integral_constant<bool, P::kPersistent> {};
+
 template <typename T, int BM, int BN, int BK, int NS, bool AT, bool BT, class P>
 __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
   using TA = OpTile<T, BM, BK, AT>;
@@ -251,34 +258,47 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char qh_tile_smem[];
   T* smem = reinterpret_cast<T*>(qh_tile_smem);
 
+  // Tile schedule. Problems with kPersistent take logical tiles by XCD: the
+  // workgroups of XCD x = blockIdx % 8 walk the range [x * per, (x + 1) * per)
+  // of logical tiles (per = the tile count padded to a multiple of 8, over 8)
+  // in steps of gridDim / 8 from blockIdx / 8, so the tiles an XCD runs at once
+  // are consecutive; a grid of the padded tile count gives each workgroup one
+  // tile, a smaller grid (one workgroup per CU) makes the workgroups persistent
+  // (their operand strides must be the same for every tile). The other
+  // problems place one tile per workgroup themselves.
   TileCtx<T> c;
-  if (!p.tile(c)) return;
+  int t_local = 0, t_step = 0, t_end = 0, t_base = 0;
+  constexpr bool kPersist = TilePersistent<P>::value;
+  if constexpr (kPersist) {
+    t_end = (p.tiles_total() + 7) / 8;
+    t_base = (int)(blockIdx.x & 7) * t_end;
+    t_local = (int)(blockIdx.x >> 3);
+    t_step = (int)(gridDim.x >> 3);
+    if (t_local >= t_end || !p.tile_at(t_base + t_local, c)) return;
+  } else {
+    if (!p.tile(c)) return;
+  }
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wid / WGN, wn = wid % WGN;
   const uint32_t lds0 = lds_addr(smem);
-  const uint32_t voa = TA::voff(c.lda, wid);
-  const uint32_t vob = TB::voff(c.ldb, wid);
 
   f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = zero16();
 
   constexpr int NPT = TA::PW + TB::PW;  // DMA instructions per wave and k-tile
   constexpr int ND = TM * (AT ? 2 : 1) + TN * (BT ? 2 : 1);  // LDS reads per k16 step
   constexpr int NM = TM * TN;
-  const int nk = (c.K + BK - 1) / BK;
   auto stage = [&](int kt) { return smem + (kt % NS) * STAGE; };
-  auto issue = [&](int kt) {
+  const uint32_t voa = TA::voff(c.lda, wid), vob = TB::voff(c.ldb, wid);
+  auto issue_for = [&](const TileCtx<T>& cc, int kt, uint32_t va, uint32_t vb) {
     const int k0 = kt * BK;
-    const int vk = c.K - k0;
+    const int vk = cc.K - k0;
     const uint32_t base = lds0 + (uint32_t)((kt % NS) * STAGE * (int)sizeof(T));
-    TA::issue(base, [&](int i, int k) { return p.a_at(c, i, k); }, k0, c.vm, vk, voa, wid);
-    TB::issue(base + (uint32_t)(TA::ELEMS * sizeof(T)), [&](int i, int k) { return p.b_at(c, i, k); }, k0, c.vn, vk,
-              vob, wid);
+    TA::issue(base, [&](int i, int k) { return p.a_at(cc, i, k); }, k0, cc.vm, vk, va, wid);
+    TB::issue(base + (uint32_t)(TA::ELEMS * sizeof(T)), [&](int i, int k) { return p.b_at(cc, i, k); }, k0, cc.vn, vk,
+              vb, wid);
   };
+  auto issue = [&](int kt) { issue_for(c, kt, voa, vob); };
   // Make k-tile kt visible to every wave, with `after` later tiles still in flight.
   auto land = [&](int kt, int after) {
     if (after <= 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -307,34 +327,90 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af[b][i], bf[b][j], acc[i][j]);
   };
-  // Tiles 0 .. NS-1 fill every stage. After the barrier that lands tile kt+1,
-  // every wave has finished reading tile kt (its last fragments were read
-  // before that barrier), so tile kt+NS can go into tile kt's stage.
-  if (nk > 0) {
-    const int pro = nk < NS ? nk : NS;
-    for (int t = 0; t < pro; ++t) issue(t);
-    land(0, pro - 1);
-    read(stage(0), 0, 0);
-  }
-  for (int kt = 0; kt < nk; ++kt) {
-    // steps 0 .. KS-2 of tile kt, each overlapping the next step's reads
+  bool warm = false;  // k-tile 0 of c was issued during the previous tile's epilogue
+  for (;;) {
 #pragma unroll
-    for (int st = 0; st + 1 < KS; ++st) {
-      read(stage(kt), st + 1, (st + 1) & 1);
-      mma(st & 1);
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = zero16();
+    const int nk = (c.K + BK - 1) / BK;
+    // Tiles 0 .. NS-1 fill every stage. After the barrier that lands tile kt+1,
+    // every wave has finished reading tile kt (its last fragments were read
+    // before that barrier), so tile kt+NS can go into tile kt's stage.
+    if (nk > 0) {
+      const int pro = nk < NS ? nk : NS;
+      if (warm) {
+        // k-tile 0 is in flight with the previous tile's epilogue stores (vmcnt
+        // counts both): wait for all of them, then fill the other stages
+        land(0, 0);
+        for (int t = 1; t < pro; ++t) issue(t);
+      } else {
+        for (int t = 0; t < pro; ++t) issue(t);
+        land(0, pro - 1);
+      }
+      read(stage(0), 0, 0);
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+      // steps 0 .. KS-2 of tile kt, each overlapping the next step's reads
+#pragma unroll
+      for (int st = 0; st + 1 < KS; ++st) {
+        read(stage(kt), st + 1, (st + 1) & 1);
+        mma(st & 1);
+        mma_schedule<ND, NM * 3 / 4>(std::make_integer_sequence<int, NM>{});
+      }
+      if (kt + 1 < nk) {
+        // tiles issued so far: 0 .. min(kt + NS - 1, nk - 1)
+        const int issued = kt + NS - 1 < nk - 1 ? kt + NS - 1 : nk - 1;
+        land(kt + 1, issued - (kt + 1));
+        if (kt + NS < nk) issue(kt + NS);  // into the stage tile kt used
+      }
+      // last step of tile kt; the next tile's first fragments are read meanwhile
+      // (after the last tile this reads an unused stage, harmlessly)
+      read(stage(kt + 1), 0, 0);
+      mma((KS - 1) & 1);
       mma_schedule<ND, NM * 3 / 4>(std::make_integer_sequence<int, NM>{});
     }
-    if (kt + 1 < nk) {
-      // tiles issued so far: 0 .. min(kt + NS - 1, nk - 1)
-      const int issued = kt + NS - 1 < nk - 1 ? kt + NS - 1 : nk - 1;
-      land(kt + 1, issued - (kt + 1));
-      if (kt + NS < nk) issue(kt + NS);  // into the stage tile kt used
+    if constexpr (!kPersist) {
+      break;
+    } else {
+      TileCtx<T> cn;
+      t_local += t_step;
+      if (!(t_local < t_end && p.tile_at(t_base + t_local, cn))) break;
+      // Hand-over: the next tile's k-tile 0 goes into stage 0 while this tile's
+      // epilogue stages its rows through stage 1 (two halves of 64 rows per wave)
+      // or stores straight from registers.
+      __syncthreads();  // every wave is done with the operand stages
+      if ((cn.K + BK - 1) / BK > 0) issue_for(cn, 0, voa, vob);  // strides are the same for every tile
+      bool staged = false;
+      if constexpr (P::kVecEpilogue) {
+        if (p.vec_ok()) {
+          static_assert(TM % 2 == 0 && NWAVE * (WTM / 2) * WTN <= STAGE, "half tiles fill one stage");
+          EpiTile<T, WTM / 2, WTN> et{smem + STAGE + wid * ((WTM / 2) * WTN)};
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < TM / 2; ++i)
+#pragma unroll
+              for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                  for (int r = 0; r < 4; ++r)
+                    et.put(32 * i + 4 * (lane >> 5) + 8 * g + r, 32 * j + (lane & 31),
+                           from_f32<T>(acc[h * (TM / 2) + i][j][4 * g + r]));
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            __builtin_amdgcn_wave_barrier();
+            p.template epilogue_vec<WTM / 2>(c, et, wm * WTM + h * (WTM / 2), wn * WTN, lane);
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this half's rows are read before the next is staged
+            __builtin_amdgcn_wave_barrier();
+          }
+          staged = true;
+        }
+      }
+      if (!staged) p.template epilogue<TM, TN>(c, acc, wm * WTM, wn * WTN, lane);
+      c = cn;
+      warm = true;
     }
-    // last step of tile kt; the next tile's first fragments are read meanwhile
-    // (after the last tile this reads an unused stage, harmlessly)
-    read(stage(kt + 1), 0, 0);
-    mma((KS - 1) & 1);
-    mma_schedule<ND, NM * 3 / 4>(std::make_integer_sequence<int, NM>{});
   }
   if constexpr (P::kVecEpilogue) {
     if (p.vec_ok()) {
@@ -375,18 +451,23 @@ struct DenseProblem {
   int M, N, K, tiles_m, tiles_n;
 
   static constexpr bool kVecEpilogue = std::is_same<OT, T>::value && !ACC;
+  static constexpr bool kPersistent = true;
   __device__ __forceinline__ bool vec_ok() const { return bias == nullptr; }
-  template <class ET>
+  // ROWS rows of 64 columns staged in et, written at tile rows wr.., columns wc..
+  template <int ROWS = 128, class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
-    for (int q = lane; q < 128 * 8; q += 64) {
+    for (int q = lane; q < ROWS * 8; q += 64) {
       const int r = q >> 3, c8 = q & 7;
       const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
       if (row < M && col < N) st16(reinterpret_cast<T*>(C) + (int64_t)row * ldc + col, et.row8(r, c8));
     }
   }
-  __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
+  __device__ __forceinline__ int tiles_total() const { return tiles_m * tiles_n; }
+  // Logical tile t (grouped by 8 M-tiles) of the output; false past the last.
+  __device__ __forceinline__ bool tile_at(int t, TileCtx<T>& c) const {
+    if (t >= tiles_m * tiles_n) return false;
     int tm, tn;
-    tile_order(tiles_m, tiles_n, tm, tn);
+    tile_group_order(t, tiles_m, tiles_n, tm, tn);
     c.m0 = tm * BM;
     c.n0 = tn * BN;
     c.K = K;
@@ -450,6 +531,10 @@ template <typename T, int BM, int BN, int BK, int NS, bool AT, bool BT, class P>
 int launch_tile(const P& p, int grid, hipStream_t st, const char* name) {
   constexpr int lds = tile_lds_bytes<BM, BN, BK, NS, T>();
   auto kern = gemm_tile_kernel<T, BM, BN, BK, NS, AT, BT, P>;
+  if (TilePersistent<P>::value && (grid <= 0 || grid % 8 != 0)) {  // the XCD schedule covers every tile only then
+    qh::set_error("%s: grid %d is not a positive multiple of 8", name, grid);
+    return QH_E_ARG;
+  }
   // The dynamic-LDS limit is raised once per instantiation and device.
   static uint64_t attr_set = 0;
   int dev = 0;
@@ -473,6 +558,23 @@ int launch_tile(const P& p, int grid, hipStream_t st, const char* name) {
 constexpr int kDenseBK = 64, kDenseNS = 2;
 constexpr int TBKS = kDenseBK;  // split-K ranges are whole k-tiles
 
+// Workgroups of a dense tile launch: the tile count padded to a multiple of 8
+// (one tile each), or, from two rounds of tiles on, one persistent workgroup
+// per CU (a multiple of 8: each XCD walks its range of tiles), which hands each
+// tile's first k-tile load over to the previous tile's epilogue.
+static int dense_grid(int tiles) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 8;
+    cus[dev] = n / 8 * 8;
+  }
+  const int padded = (tiles + 7) / 8 * 8;
+  return tiles >= 2 * cus[dev] ? cus[dev] : padded;
+}
+
 template <typename T, typename OT, int BM, int BN, bool AT, bool BT>
 int dense_tile(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_t ldc, const T* bias, int M, int N,
                int K, hipStream_t st) {
@@ -489,7 +591,8 @@ int dense_tile(const T* A, int64_t lda, const T* B, int64_t ldb, OT* C, int64_t 
   p.K = K;
   p.tiles_m = (M + BM - 1) / BM;
   p.tiles_n = (N + BN - 1) / BN;
-  return launch_tile<T, BM, BN, kDenseBK, kDenseNS, AT, BT>(p, p.tiles_m * p.tiles_n, st, "qh_gemm_tile");
+  return launch_tile<T, BM, BN, kDenseBK, kDenseNS, AT, BT>(p, dense_grid(p.tiles_m * p.tiles_n), st,
+                                                            "qh_gemm_tile");
 }
 
 template <typename T, typename OT>
@@ -1633,7 +1736,8 @@ extern "C" int qh_gemm_acc(int trans_a, int trans_b, int64_t M, int64_t N, int64
     p.K = (int)K;                                                                                     \
     p.tiles_m = (int)((M + 255) / 256);                                                               \
     p.tiles_n = (int)((N + 255) / 256);                                                               \
-    rc = launch_tile<TT, 256, 256, kDenseBK, kDenseNS, ATV, BTV>(p, p.tiles_m * p.tiles_n, st, "qh_gemm_acc"); \
+    rc = launch_tile<TT, 256, 256, kDenseBK, kDenseNS, ATV, BTV>(p, dense_grid(p.tiles_m * p.tiles_n), st,   \
+                                                                 "qh_gemm_acc");                             \
   }
 #define QH_ACC(TT)                                               \
   if (!trans_a && !trans_b) QH_ACC_L(TT, false, false)           \

@@ -75,12 +75,10 @@ __device__ __forceinline__ void transpose8x8(const uint4 (&in)[8], uint4 (&out)[
 }
 
 // Workgroups are dealt round-robin to the 8 XCDs: renumber so each XCD walks a
-// contiguous range of logical tiles, then order tiles in groups of 8 M-tiles so
-// concurrently running tiles share operand panels in the XCD's L2.
-__device__ __forceinline__ void tile_order(int tiles_m, int tiles_n, int& tm, int& tn) {
-  int pid = blockIdx.x;
-  const int nblk = gridDim.x;
-  if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
+// contiguous range of logical tiles (tile_order), then order tiles in groups of
+// 8 M-tiles (tile_group_order, on a logical tile index) so concurrently running
+// tiles share operand panels in the XCD's L2.
+__device__ __forceinline__ void tile_group_order(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   constexpr int GROUP = 8;
   const int group_size = GROUP * tiles_n;
   const int g = pid / group_size;
@@ -89,4 +87,10 @@ __device__ __forceinline__ void tile_order(int tiles_m, int tiles_n, int& tm, in
   const int in_group = pid - g * group_size;
   tm = first_m + in_group % gm;
   tn = in_group / gm;
+}
+__device__ __forceinline__ void tile_order(int tiles_m, int tiles_n, int& tm, int& tn) {
+  int pid = blockIdx.x;
+  const int nblk = gridDim.x;
+  if ((nblk & 7) == 0) pid = (pid & 7) * (nblk >> 3) + (pid >> 3);
+  tile_group_order(pid, tiles_m, tiles_n, tm, tn);
 }
