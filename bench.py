@@ -39,9 +39,10 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 # HBM bytes per launch of the decode attention as the config-3 step runs it (one
 # fa_decode_wg_kernel<bf16,128,2,PREP> dispatch on the interleaved K/V cache, non-temporal loads),
 # from the two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of `bench.py --workload roofline`,
-# each scaled by the same counter's reading for a 1 GiB copy (fetch x 1048576 / 524310.0, write
-# x 1.000): 263125.5 KiB x 1.99992 + 512 KiB = 539,382,701 bytes.
-DECODE_TRAFFIC_BYTES = 539_382_701
+# each scaled by the same counter's reading for a 1 GiB copy (fetch x 1048576 / 524307.5, write
+# x 1.000): 264342.7 KiB x 1.99993 + 512 KiB = 541,878,003 bytes (1.0069x the algorithmic bytes;
+# the rest is every wave's own copy of the rows' norm weights and cos/sin).
+DECODE_TRAFFIC_BYTES = 541_878_003
 
 QWEN3_06B = dict(model_type="qwen3", vocab_size=151936, hidden_size=1024, intermediate_size=3072,
                  num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8, head_dim=128,
