@@ -220,7 +220,8 @@ int qh_moe_up(const void* X, int64_t ldx, int64_t R, int64_t K, const void* cons
               const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* G, void* U, void* H, int64_t ldo,
               int dtype, void* stream);
 /* C = A Wd_e^T per segment, rounded; with wrow (per-row weights) C =
- * round(round(A Wd_e^T) * wrow[r]). */
+ * round(round(A Wd_e^T) * wrow[r]). C is written as 16-byte rows: N and ldc
+ * multiples of 8, C 16-byte aligned (else QH_E_ARG). */
 int qh_moe_down(const void* A, int64_t lda, int64_t R, int64_t K, const void* const* d_table, int64_t ldw, int64_t N,
                 const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* C, int64_t ldc, const void* wrow,
                 int dtype, void* stream);

@@ -452,7 +452,11 @@ struct DenseProblem {
 
   static constexpr bool kVecEpilogue = std::is_same<OT, T>::value && !ACC;
   static constexpr bool kPersistent = true;
-  __device__ __forceinline__ bool vec_ok() const { return bias == nullptr; }
+  // 16-byte row stores write 8 columns at once: only without bias, with N and ldc multiples of 8
+  // and C 16-byte aligned (else a row's last chunk would run into the next row)
+  __device__ __forceinline__ bool vec_ok() const {
+    return bias == nullptr && (N & 7) == 0 && (ldc & 7) == 0 && ((uintptr_t)C & 15) == 0;
+  }
   // ROWS rows of 64 columns staged in et, written at tile rows wr.., columns wc..
   template <int ROWS = 128, class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
@@ -1459,6 +1463,8 @@ extern "C" int qh_moe_down(const void* A, int64_t lda, int64_t R, int64_t K, con
   QH_CHECK_ARG(R >= 0 && K > 0 && N > 0 && E > 0 && E <= 65536 && K % 8 == 0 && ldc >= N,
                "qh_moe_down: bad shape");
   QH_CHECK_ARG(moe_ok(A, lda) && ldw % 8 == 0, "qh_moe_down: A must be 16-byte aligned with strides multiples of 8");
+  QH_CHECK_ARG(N % 8 == 0 && moe_ok(C, ldc),  // the epilogue stores 16-byte rows of 8 columns
+               "qh_moe_down: C must be 16-byte aligned with N and ldc multiples of 8");
   QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_down: bf16/f16 only");
   if (R == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;

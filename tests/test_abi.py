@@ -54,6 +54,8 @@ def test_argument_errors_are_reported_without_launching():
         _native.call("qh_rope", 0, 1, 1, 1, 1, 0, 0, 1, 1, 1, 1, 0, 1, 1, 1, 4, 3, 0, _native.BF16, _native.BF16, 0)
     with pytest.raises(_native.NativeError, match="k=5 > C=4"):
         _native.call("qh_topk", 0, 0, 0, 1, 4, 5, _native.F32, 0)
+    with pytest.raises(_native.NativeError, match="N and ldc multiples of 8"):  # 16-byte output rows
+        _native.call("qh_moe_down", 0, 8, 1, 8, 0, 8, 100, 0, 0, 1, 0, 100, 0, _native.BF16, 0)
     with pytest.raises(_native.NativeError, match="head dim"):
         _native.call("qh_flash_fwd", 0, 0, 0, 8, 0, 0, 0, 8, 0, 0, 0, 8, 0, 0, 0, 8, 0, 1, 1, 1, 1, 1, 200, 1.0, 1,
                      0, _native.BF16, 0)

@@ -737,6 +737,36 @@ def test_gemm_large_tile_layouts_and_tails(ta, tb, out_dtype):
     assert torch.equal(c, c2)
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 1), (1, 0)])
+@pytest.mark.parametrize("out_dtype,with_bias", [(torch.bfloat16, False), (torch.bfloat16, True),
+                                                 (torch.float32, False)])
+def test_gemm_persistent_tiles_with_tails(ta, tb, out_dtype, with_bias):
+    """Two or more rounds of 256x256 tiles (here 33 x 17 = 561) take persistent workgroups, one per
+    CU, each issuing its next tile's first k-tile load before the epilogue (16-byte rows staged in
+    two halves for bf16 output without bias, register stores otherwise); M, N and K end in partial
+    tiles (8229 = 32*256 + 37, 4196 = 16*256 + 100, 1000 = 15*64 + 40). Two runs are bitwise equal."""
+    M, N, Kd = 8229, 4196, 1000
+    a = randn(M, Kd, dtype=torch.bfloat16, seed=305)
+    b = randn(N, Kd, dtype=torch.bfloat16, seed=306, scale=0.05)
+    bias = randn(N, dtype=torch.bfloat16, seed=307) if with_bias else None
+    a_op = a.t().contiguous() if ta else a
+    b_op = b.t().contiguous() if tb else b
+
+    def run():
+        c = torch.empty(M, N, dtype=out_dtype, device=DEV)
+        _native.call("qh_gemm", ta, tb, M, N, Kd, a_op.data_ptr(), a_op.stride(0), b_op.data_ptr(), b_op.stride(0),
+                     c.data_ptr(), N, bias.data_ptr() if with_bias else 0, _native.BF16, _native.dtype_code(out_dtype),
+                     _native.stream(a.device))
+        return c
+
+    c = run()
+    ref = a.float() @ b.float().t()
+    if with_bias:
+        ref = ref + bias.float()
+    close(c, ref, **(dict(atol=2e-3, rtol=2e-3) if out_dtype == torch.float32 else BF16_TOL))
+    assert torch.equal(c, run())
+
+
 @pytest.mark.parametrize("ta,tb", [(1, 1), (0, 0), (0, 1), (1, 0)])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 def test_gemm_split_k(ta, tb, out_dtype):
