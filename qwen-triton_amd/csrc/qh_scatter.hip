@@ -128,7 +128,7 @@ __global__ __launch_bounds__(64) void segment_rows_vec(const uint32_t* __restric
 // same vmcnt as loads, so a load wait would also wait for the store stream).
 // - Zero waves (the first zgrid workgroups): a wave owns rpw <= 128 consecutive rows, finds the
 //   first sorted position with a key at or above its first row by a 64-way search (one load per
-//   lane per round, about log64(n) rounds), marks the rows some token hits (64 keys per load),
+//   lane per step, about log64(n) steps), marks the rows some token hits (64 keys per load),
 //   then writes zeros to the others (the padding row included).
 // - Run waves (the rest, one per sorted position): the first position of each key's run sums
 //   the run's gradient rows in position order (fp32, rounded once) into the row, except for the
@@ -176,11 +176,11 @@ __global__ __launch_bounds__(256) void embedding_rows_roles(const uint32_t* __re
     lo = nlo;
     len = hi - nlo;
   }
-  // mark the hit rows of [a, b): 64 sorted keys per round
+  // mark the hit rows of [a, b): 64 sorted keys per load
   for (int p = lo; a < b && p < n; p += 64) {
     const int64_t k = p + lane < n ? (int64_t)keys[p + lane] : V;
     if (k < b && k != skip_key) atomicOr(&hitw[wid][(k - a) >> 5], 1u << ((k - a) & 31));
-    if (__any(k >= b)) break;  // keys are sorted: the range ends in this round
+    if (__any(k >= b)) break;  // keys are sorted: the range ends within these 64 keys
   }
   __syncthreads();
   float z[8];
