@@ -767,6 +767,28 @@ def test_gemm_persistent_tiles_with_tails(ta, tb, out_dtype, with_bias):
     assert torch.equal(c, run())
 
 
+@pytest.mark.parametrize("tb", [0, 1])
+def test_gemm_acc_persistent_tiles(tb):
+    """qh_gemm_acc (fp32 C += A B^T, the fused LM head's dX accumulation) at 33 x 17 output tiles,
+    i.e. on persistent workgroups with the register epilogue at every hand-over; M and N end in
+    partial tiles. Two accumulations from the same C are bitwise equal."""
+    M, N, Kd = 8232, 4104, 512
+    a = randn(M, Kd, dtype=torch.bfloat16, seed=320)
+    b = randn(N, Kd, dtype=torch.bfloat16, seed=321, scale=0.05)
+    c0 = randn(M, N, seed=322)
+    b_op = b.t().contiguous() if tb else b
+
+    def run():
+        c = c0.clone()
+        _native.call("qh_gemm_acc", 0, tb, M, N, Kd, a.data_ptr(), a.stride(0), b_op.data_ptr(), b_op.stride(0),
+                     c.data_ptr(), N, _native.BF16, _native.stream(a.device))
+        return c
+
+    c = run()
+    close(c, c0 + a.float() @ b.float().t(), atol=2e-3, rtol=2e-3)
+    assert torch.equal(c, run())
+
+
 @pytest.mark.parametrize("ta,tb", [(1, 1), (0, 0), (0, 1), (1, 0)])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 def test_gemm_split_k(ta, tb, out_dtype):
