@@ -817,8 +817,8 @@ def main() -> None:
     ap.add_argument("--no-other-configs", action="store_true", help="default run: skip the config 1/2/4 keys")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (see DESIGN.md for how it "
-              "would shard); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the kernels run on one "
+              "GPU's share of the work); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     os.environ.setdefault("QWEN_TRITON_STRICT", "1")
     import torch
