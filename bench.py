@@ -404,6 +404,58 @@ def bench_fa(steps, warmup):
             "fa_bwd_frac": round(bwd_flop / bwd_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
+def bench_gdr(steps, warmup):
+    """Qwen3-Next linear attention's gated delta rule over whole sequences (32 value heads, key and
+    value head dims 128, bf16, 4 sequences x 4096 tokens): HIP-event time of one
+    `qh_gated_delta_rule` launch, tokens per second, the time per sequential token step, the
+    algorithmic bytes (q, k, v read, output written once, decay/beta, final state) over the time,
+    and the oracle (fp32 torch on the host cores) on a bounded sample, scaled per (token, head)."""
+    import torch
+    import torch.nn.functional as F
+    from oracle import ops as O
+    from qwen_triton.kernels.linear_attention import gated_delta_rule_sequence
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    B, S, H, Dk, Dv = 4, 4096, 32, 128, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = F.normalize(torch.randn(B, S, H, Dk, device="cuda", generator=g), dim=-1).bfloat16()
+    k = F.normalize(torch.randn(B, S, H, Dk, device="cuda", generator=g), dim=-1).bfloat16()
+    v = torch.randn(B, S, H, Dv, device="cuda", generator=g).bfloat16()
+    decay = -F.softplus(torch.randn(B, S, H, device="cuda", generator=g)) * 0.5
+    beta = torch.sigmoid(torch.randn(B, S, H, device="cuda", generator=g))
+    for _ in range(max(1, warmup)):
+        gated_delta_rule_sequence(q, k, v, decay, beta)
+    sync()
+    evs = []
+    for _ in range(steps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        gated_delta_rule_sequence(q, k, v, decay, beta)
+        b.record()
+        evs.append((a, b))
+    sync()
+    ms = min(x.elapsed_time(y) for x, y in evs)
+    nbytes = 2 * (q.numel() + k.numel() + 2 * v.numel()) + 4 * 2 * decay.numel() + 4 * B * H * Dk * Dv
+    # oracle: 1 sequence x 128 tokens x 4 heads, fp32, median of 3
+    Sc, Hc = 128, 4
+    qc, kc, vc = (t[:1, :Sc, :Hc].float().cpu() for t in (q, k, v))
+    gc, bc = decay[:1, :Sc, :Hc].cpu(), beta[:1, :Sc, :Hc].cpu()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.gated_delta_rule(qc, kc, vc, gc, bc, dtype=torch.float32)
+        ts.append(time.perf_counter() - t0)
+    cpu_s = sorted(ts)[1]
+    cpu_tok_s = Sc * Hc / cpu_s / H  # tokens of all 32 heads per second
+    return {"gdr_ms": round(ms, 3), "tokens": B * S, "heads": H, "gdr_tok_s": round(B * S / ms * 1e3, 1),
+            "us_per_token_step": round(ms * 1e3 / S, 3), "gbs": round(nbytes / ms / 1e6, 1),
+            "hbm_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "cpu_baseline": {"value": round(cpu_tok_s, 1), "unit": "tok/s (all 32 heads)",
+                             "cores": torch.get_num_threads(), "kind": "port",
+                             "sample": f"oracle fp32 gated delta rule, 1 sequence x {Sc} tokens x {Hc} heads "
+                                       f"({cpu_s * 1e3:.1f} ms), scaled per (token, head)"}}
+
+
 def bench_dense(steps, warmup):
     import torch
     from qwen_triton.kernels import cross_entropy as CE
@@ -810,7 +862,7 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "fa", "dense", "gemm", "roofline", "moe", "ops"])
+                    choices=["decode", "fa", "dense", "gemm", "roofline", "moe", "ops", "gdr"])
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--gemm-shape", default=None, help="--workload gemm: time only the shape with this label")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -848,6 +900,11 @@ def main() -> None:
     if args.workload == "moe":
         res = bench_moe(args.steps, args.warmup)
         print(json.dumps({"metric": "Qwen3-MoE layer fwd/bwd (config 4, 30B-A3B shape)", **res}), flush=True)
+        return
+    if args.workload == "gdr":
+        res = bench_gdr(args.steps, args.warmup)
+        print(json.dumps({"metric": "Qwen3-Next gated delta rule (4 x 4096 tokens, 32 heads, 128/128)", **res}),
+              flush=True)
         return
     if args.workload == "dense":
         res = bench_dense(args.steps, args.warmup)

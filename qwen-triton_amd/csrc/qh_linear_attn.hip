@@ -11,14 +11,32 @@
 // workgroup owns one (b, h, 64-column value block) for the whole sequence and keeps its slice of
 // S in registers: wave w takes value columns 16 w .. 16 w + 15, and lane (kg, vi) = (lane / 16,
 // lane % 16) holds rows kg * KPL .. kg * KPL + KPL - 1 of column vi, so the two K reductions of a
-// token are in-lane sums plus an xor tree over the four row groups. The next token's q, k, v, g
-// and beta are loaded while the current token updates the state. The state is read and written
-// once per launch.
+// token are in-lane sums plus an xor tree over the four row groups. The inputs of kGdrChunk
+// tokens at a time (q, k, this block's v columns, g, beta) are loaded by the whole workgroup with
+// coalesced loads into registers while the previous chunk's tokens are processed, then written to
+// the other half of a double-buffered LDS stage (one barrier per chunk): a token's loads are
+// requested a chunk ahead rather than one token ahead, so their latency (far longer than a
+// token's arithmetic) is not waited for per token, and each lane reads its rows from LDS as
+// broadcasts. The state is read and written once per launch.
 #include "qh_common.h"
 
 namespace {
 
-constexpr int kGdrCols = 64;  // value columns per workgroup
+constexpr int kGdrCols = 64;   // value columns per workgroup
+constexpr int kGdrChunk = 32;  // tokens per LDS stage
+constexpr int kGdrKMax = 128;  // key head dim the stage rows hold
+
+// x[l] + x[l ^ 16] and x[l] + x[l ^ 32] in registers (v_permlane16/32_swap with x in both operands
+// hand each lane the pair in a fixed order; the sum is the same on both lanes of a pair), instead of
+// LDS permutes, whose latency sits on every token's dependent chain.
+__device__ __forceinline__ float pair16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 template <typename T, int KPL>
 __global__ __launch_bounds__(256) void gdr_kernel(const T* __restrict__ Q, const T* __restrict__ Kt,
@@ -50,47 +68,95 @@ __global__ __launch_bounds__(256) void gdr_kernel(const T* __restrict__ Q, const
   const float* bb = Beta + (int64_t)b * sgb + (int64_t)h * sgh;
   T* ob = O + (int64_t)b * sob + (int64_t)h * soh;
 
-  float qn[KPL], kn[KPL], vn = 0.f, gn = 0.f, betan = 0.f;
-  auto load = [&](int t) {
+  // Chunk staging: thread tid loads q/k elements tid + 256 j of the chunk's [C, K] rows, v
+  // elements tid + 256 j of its [C, 64] block, and (tid < C) g / (64 <= tid < 64 + C) beta.
+  constexpr int C = kGdrChunk, NQK = C * kGdrKMax / 256, NV = C * kGdrCols / 256;
+  __shared__ T qs[2][C][kGdrKMax], ks[2][C][kGdrKMax], vs[2][C][kGdrCols];
+  __shared__ float gs[2][C], bs[2][C];
+  const int tid = threadIdx.x;
+  T rq[NQK], rk[NQK], rv[NV];
+  float rg = 0.f;
+  auto stage_load = [&](int t0) {
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      const bool ok = k0 + i < K;
-      // q * scale rounded to T, as the reference scales the query tensor before the recurrence
-      qn[i] = ok ? to_f32(from_f32<T>(to_f32(qb[(int64_t)t * sqs + k0 + i]) * scale)) : 0.f;
-      kn[i] = ok ? to_f32(kb[(int64_t)t * sqs + k0 + i]) : 0.f;
+    for (int j = 0; j < NQK; ++j) {
+      const int e = tid + 256 * j, tt = e / K, d = e - tt * K;
+      const bool ok = tt < C && t0 + tt < S;
+      rq[j] = ok ? qb[(int64_t)(t0 + tt) * sqs + d] : (T)0.f;
+      rk[j] = ok ? kb[(int64_t)(t0 + tt) * sqs + d] : (T)0.f;
     }
-    vn = cok ? to_f32(vbp[(int64_t)t * svs + col]) : 0.f;
-    gn = gb[(int64_t)t * sgs];
-    betan = bb[(int64_t)t * sgs];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int e = tid + 256 * j, tt = e / kGdrCols, c = e - tt * kGdrCols, gc = vb * kGdrCols + c;
+      rv[j] = (t0 + tt < S && gc < Vd) ? vbp[(int64_t)(t0 + tt) * svs + gc] : (T)0.f;
+    }
+    if (tid < C) rg = t0 + tid < S ? gb[(int64_t)(t0 + tid) * sgs] : 0.f;
+    else if (tid >= 64 && tid < 64 + C) rg = t0 + tid - 64 < S ? bb[(int64_t)(t0 + tid - 64) * sgs] : 0.f;
   };
-  if (S > 0) load(0);
-  for (int t = 0; t < S; ++t) {
-    float q[KPL], k[KPL];
+  auto stage_store = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      q[i] = qn[i];
-      k[i] = kn[i];
+    for (int j = 0; j < NQK; ++j) {
+      const int e = tid + 256 * j, tt = e / K, d = e - tt * K;
+      if (tt < C) {
+        // q * scale rounded to T, as the reference scales the query tensor before the recurrence
+        qs[buf][tt][d] = from_f32<T>(to_f32(rq[j]) * scale);
+        ks[buf][tt][d] = rk[j];
+      }
     }
-    const float v = vn, decay = __expf(gn), beta = betan;
-    if (t + 1 < S) load(t + 1);
-    float kv = 0.f;
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      st[i] *= decay;
-      kv += st[i] * k[i];
+    for (int j = 0; j < NV; ++j) {
+      const int e = tid + 256 * j, tt = e / kGdrCols, c = e - tt * kGdrCols;
+      vs[buf][tt][c] = rv[j];
     }
-    kv += __shfl_xor(kv, 16);
-    kv += __shfl_xor(kv, 32);
-    const float d = (v - kv) * beta;
-    float o = 0.f;
+    if (tid < C) gs[buf][tid] = rg;
+    else if (tid >= 64 && tid < 64 + C) bs[buf][tid - 64] = rg;
+  };
+  // Stage rows hold kGdrKMax entries; those at or past K are never staged: zero them once, so the
+  // token loop reads every row entry a lane owns (k0 + i < 4 KPL <= kGdrKMax) without a guard (a
+  // zero q/k entry meets a zero state row, as a masked one would).
+  for (int e = tid; e < 2 * C * (kGdrKMax - K); e += 256) {
+    const int bufz = e / (C * (kGdrKMax - K)), r = e % (C * (kGdrKMax - K));
+    const int tt = r / (kGdrKMax - K), d = K + r % (kGdrKMax - K);
+    qs[bufz][tt][d] = (T)0.f;
+    ks[bufz][tt][d] = (T)0.f;
+  }
+  if (S > 0) {
+    stage_load(0);
+    stage_store(0);
+  }
+  __syncthreads();
+  for (int t0 = 0; t0 < S; t0 += C) {
+    const int buf = (t0 / C) & 1;
+    const bool more = t0 + C < S;
+    if (more) stage_load(t0 + C);  // in flight while this chunk's tokens run
+    const int nt = S - t0 < C ? S - t0 : C;
+    for (int tt = 0; tt < nt; ++tt) {
+      float q[KPL], k[KPL];
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      st[i] += k[i] * d;
-      o += st[i] * q[i];
+      for (int i = 0; i < KPL; ++i) {  // unguarded: every entry is staged or zero
+        q[i] = to_f32(qs[buf][tt][k0 + i]);
+        k[i] = to_f32(ks[buf][tt][k0 + i]);
+      }
+      const float v = to_f32(vs[buf][tt][w * 16 + vi]);  // columns past Vd are staged as zero
+      const float decay = __expf(gs[buf][tt]), beta = bs[buf][tt];
+      float kv = 0.f;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) {
+        st[i] *= decay;
+        kv += st[i] * k[i];
+      }
+      kv = pair32_sum(pair16_sum(kv));
+      const float d = (v - kv) * beta;
+      float o = 0.f;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) {
+        st[i] += k[i] * d;
+        o += st[i] * q[i];
+      }
+      o = pair32_sum(pair16_sum(o));
+      if (kg == 0 && cok) ob[(int64_t)(t0 + tt) * sos + col] = from_f32<T>(o);
     }
-    o += __shfl_xor(o, 16);
-    o += __shfl_xor(o, 32);
-    if (kg == 0 && cok) ob[(int64_t)t * sos + col] = from_f32<T>(o);
+    if (more) stage_store(buf ^ 1);  // the other stage held the previous chunk, read by all before the last barrier
+    __syncthreads();
   }
   if (state_out && cok) {
     float* so = state_out + ((int64_t)bh * K) * Vd;
