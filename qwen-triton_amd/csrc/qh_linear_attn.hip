@@ -13,8 +13,8 @@
 // lane % 16) holds rows kg * KPL .. kg * KPL + KPL - 1 of column vi, so the two K reductions of a
 // token are in-lane sums plus an xor tree over the four row groups. The inputs of kGdrChunk
 // tokens at a time (q, k, this block's v columns, g, beta) are loaded by the whole workgroup with
-// coalesced loads into registers while the previous chunk's tokens are processed, then written to
-// the other half of a double-buffered LDS stage (one barrier per chunk): a token's loads are
+// coalesced loads into registers while the previous chunk's tokens are processed, then written
+// (q and k widened to fp32) to the other half of a double-buffered LDS stage (one barrier per chunk): a token's loads are
 // requested a chunk ahead rather than one token ahead, so their latency (far longer than a
 // token's arithmetic) is not waited for per token, and each lane reads its rows from LDS as
 // broadcasts. The state is read and written once per launch.
@@ -71,7 +71,9 @@ __global__ __launch_bounds__(256) void gdr_kernel(const T* __restrict__ Q, const
   // Chunk staging: thread tid loads q/k elements tid + 256 j of the chunk's [C, K] rows, v
   // elements tid + 256 j of its [C, 64] block, and (tid < C) g / (64 <= tid < 64 + C) beta.
   constexpr int C = kGdrChunk, NQK = C * kGdrKMax / 256, NV = C * kGdrCols / 256;
-  __shared__ T qs[2][C][kGdrKMax], ks[2][C][kGdrKMax], vs[2][C][kGdrCols];
+  // q and k staged as fp32 (q already scaled and rounded to T), so a token's rows need no conversion
+  __shared__ float qs[2][C][kGdrKMax], ks[2][C][kGdrKMax];
+  __shared__ T vs[2][C][kGdrCols];
   __shared__ float gs[2][C], bs[2][C];
   const int tid = threadIdx.x;
   T rq[NQK], rk[NQK], rv[NV];
@@ -98,8 +100,8 @@ __global__ __launch_bounds__(256) void gdr_kernel(const T* __restrict__ Q, const
       const int e = tid + 256 * j, tt = e / K, d = e - tt * K;
       if (tt < C) {
         // q * scale rounded to T, as the reference scales the query tensor before the recurrence
-        qs[buf][tt][d] = from_f32<T>(to_f32(rq[j]) * scale);
-        ks[buf][tt][d] = rk[j];
+        qs[buf][tt][d] = to_f32(from_f32<T>(to_f32(rq[j]) * scale));
+        ks[buf][tt][d] = to_f32(rk[j]);
       }
     }
 #pragma unroll
@@ -116,8 +118,8 @@ __global__ __launch_bounds__(256) void gdr_kernel(const T* __restrict__ Q, const
   for (int e = tid; e < 2 * C * (kGdrKMax - K); e += 256) {
     const int bufz = e / (C * (kGdrKMax - K)), r = e % (C * (kGdrKMax - K));
     const int tt = r / (kGdrKMax - K), d = K + r % (kGdrKMax - K);
-    qs[bufz][tt][d] = (T)0.f;
-    ks[bufz][tt][d] = (T)0.f;
+    qs[bufz][tt][d] = 0.f;
+    ks[bufz][tt][d] = 0.f;
   }
   if (S > 0) {
     stage_load(0);
@@ -133,8 +135,8 @@ __global__ __launch_bounds__(256) void gdr_kernel(const T* __restrict__ Q, const
       float q[KPL], k[KPL];
 #pragma unroll
       for (int i = 0; i < KPL; ++i) {  // unguarded: every entry is staged or zero
-        q[i] = to_f32(qs[buf][tt][k0 + i]);
-        k[i] = to_f32(ks[buf][tt][k0 + i]);
+        q[i] = qs[buf][tt][k0 + i];
+        k[i] = ks[buf][tt][k0 + i];
       }
       const float v = to_f32(vs[buf][tt][w * 16 + vi]);  // columns past Vd are staged as zero
       const float decay = __expf(gs[buf][tt]), beta = bs[buf][tt];
