@@ -474,6 +474,8 @@ def bench_dense(steps, warmup):
     from qwen_triton.kernels import fused_linear_cross_entropy
 
     def step(fused=False):
+        for t in (x, wg, wu, wd, wl):  # released as optimizer.zero_grad(set_to_none=True) does each step
+            t.grad = None
         h = MM.triton_matmul(silu_mul(MM.triton_matmul(x, wg), MM.triton_matmul(x, wu)), wd)
         if fused:  # LM head + CE without the [16384, 151936] logits (recomputed per vocabulary chunk)
             loss = fused_linear_cross_entropy(h, wl, labels)
@@ -572,8 +574,10 @@ def bench_moe(steps, warmup, loop_reps=1):
     Times (HIP events, inputs resident): the expert path forward without autograd (routing +
     dispatch + grouped GEMMs + combine), the expert path forward + backward with autograd
     (router logits, input and every expert weight get gradients), and the whole decoder layer
-    (RMSNorm, attention, MoE block) forward + backward. The reference's per-expert loop is timed
-    once beside them."""
+    (RMSNorm, attention, MoE block) forward + backward. Each training step first releases the
+    previous step's gradients (zero_grad(set_to_none=True), as a training loop does), so it writes
+    fresh gradients instead of adding into old ones. The reference's per-expert loop is timed once
+    beside them."""
     import torch
     from qwen_triton import QwenTritonConfig
     from qwen_triton.models.core import QwenDecoderLayer
@@ -620,6 +624,8 @@ def bench_moe(steps, warmup, loop_reps=1):
     lg = logits.clone().requires_grad_(True)
 
     def train():
+        blk.zero_grad(set_to_none=True)  # a training loop's per-step release: no accumulation into old grads
+        xg.grad = lg.grad = None
         w, sel = blk.route(lg, torch.bfloat16)
         out = blk.experts_forward(xg, w, sel)
         torch.autograd.backward(out, go)
@@ -641,6 +647,8 @@ def bench_moe(steps, warmup, loop_reps=1):
     cos, sin = rot(hs, pos)
 
     def layer_step():
+        layer.zero_grad(set_to_none=True)
+        hs.grad = None
         out, _ = layer(hs, (cos, sin))
         torch.autograd.backward(out, gl)
 

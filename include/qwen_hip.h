@@ -215,10 +215,13 @@ int qh_moe_gather(const void* X, int64_t ldx, const int32_t* rows, int64_t R, in
  * qwen_triton/modules/moe.py:45-51 (QwenMLP = modules/mlp.py:19-22 over
  * TritonLinear, kernels/matmul.py:130-155, and silu_mul, kernels/swiglu.py). */
 /* G = Xs Wg_e^T, U = Xs Wu_e^T (each rounded), H = round(silu(G) * U) per
- * expert segment; G and U (both or neither) may be NULL. I % 128 == 0. */
-int qh_moe_up(const void* X, int64_t ldx, int64_t R, int64_t K, const void* const* gu_table, int64_t ldw, int64_t I,
-              const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* G, void* U, void* H, int64_t ldo,
-              int dtype, void* stream);
+ * expert segment; G and U (both or neither) may be NULL. I % 128 == 0.
+ * rows == NULL: X holds the R sorted rows (Xs = X, e.g. from qh_moe_gather).
+ * rows != NULL: X holds the tokens and sorted row r is X[rows[r]] (rows from
+ * qh_moe_dispatch, each a valid row of X), gathered by the product itself. */
+int qh_moe_up(const void* X, int64_t ldx, const int32_t* rows, int64_t R, int64_t K, const void* const* gu_table,
+              int64_t ldw, int64_t I, const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* G, void* U,
+              void* H, int64_t ldo, int dtype, void* stream);
 /* C = A Wd_e^T per segment, rounded; with wrow (per-row weights) C =
  * round(round(A Wd_e^T) * wrow[r]). C is written as 16-byte rows: N and ldc
  * multiples of 8, C 16-byte aligned (else QH_E_ARG). */

@@ -104,6 +104,20 @@ struct NTile {
       }
     }
   }
+  // Row of the tile that this lane loads in DMA instruction i (its row pointer
+  // is fixed for the whole tile when rows are gathered).
+  static __device__ __forceinline__ int lane_row(int wid, int i) {
+    return RPI * (wid + NWAVE * i) + (int)(threadIdx.x & 63) / CPR;
+  }
+  // Rows reached through per-lane row pointers (gathered operands): rowp[i] is
+  // the lane's row lane_row(wid, i), already clamped to a valid row.
+  static __device__ __forceinline__ void issue_rows(uint32_t lds, const T* const (&rowp)[PW], int k0, int vk, int wid) {
+    const int lane = threadIdx.x & 63;
+    int kc = 8 * ((lane % CPR) ^ sw(RPI * wid + lane / CPR));
+    if (kc > vk - 8) kc = vk - 8;  // vk is a positive multiple of 8
+#pragma unroll
+    for (int i = 0; i < PW; ++i) lds_dma16(rowp[i] + k0 + kc, lds + (uint32_t)(wid + NWAVE * i) * 1024u);
+  }
   // Zero the k chunks at or past vk (all rows).
   static __device__ __forceinline__ void zero_k_tail(T* S, int vk) {
     for (int idx = threadIdx.x; idx < ROWS * CPR; idx += NTHR) {
@@ -246,6 +260,13 @@ struct TilePersistent : std::false_type {};
 template <class P>
 struct TilePersistent<P, std::void_t<decltype(P::kPersistent)>> : std::integral_constant<bool, P::kPersistent> {};
 
+// Problems that define kGatherA = true give the A tile's rows through
+// a_row(ctx, i) (a pointer to row i's k = 0), so the rows may lie anywhere.
+template <class P, class = void>
+struct TileGatherA : std::false_type {};
+template <class P>
+struct TileGatherA<P, std::void_t<decltype(P::kGatherA)>> : std::integral_constant<bool, P::kGatherA> {};
+
 template <typename T, int BM, int BN, int BK, int NS, bool AT, bool BT, class P>
 __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
   using TA = OpTile<T, BM, BK, AT>;
@@ -269,6 +290,8 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
   TileCtx<T> c;
   int t_local = 0, t_step = 0, t_end = 0, t_base = 0;
   constexpr bool kPersist = TilePersistent<P>::value;
+  constexpr bool kGather = TileGatherA<P>::value;
+  static_assert(!(kGather && (kPersist || AT)), "gathered A rows: k-contiguous A, one tile per workgroup");
   if constexpr (kPersist) {
     t_end = (p.tiles_total() + 7) / 8;
     t_base = (int)(blockIdx.x & 7) * t_end;
@@ -290,11 +313,22 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
   constexpr int NM = TM * TN;
   auto stage = [&](int kt) { return smem + (kt % NS) * STAGE; };
   const uint32_t voa = TA::voff(c.lda, wid), vob = TB::voff(c.ldb, wid);
+  // Gathered A: the lane's row pointers, taken once for the tile (rows past
+  // the valid ones repeat the last valid row; the epilogue drops them).
+  const T* arow[kGather ? TA::PW : 1];
+  if constexpr (kGather) {
+#pragma unroll
+    for (int i = 0; i < TA::PW; ++i) {
+      const int r = TA::lane_row(wid, i);
+      arow[i] = p.a_row(c, r < c.vm ? r : c.vm - 1);
+    }
+  }
   auto issue_for = [&](const TileCtx<T>& cc, int kt, uint32_t va, uint32_t vb) {
     const int k0 = kt * BK;
     const int vk = cc.K - k0;
     const uint32_t base = lds0 + (uint32_t)((kt % NS) * STAGE * (int)sizeof(T));
-    TA::issue(base, [&](int i, int k) { return p.a_at(cc, i, k); }, k0, cc.vm, vk, va, wid);
+    if constexpr (kGather) TA::issue_rows(base, arow, k0, vk, wid);
+    else TA::issue(base, [&](int i, int k) { return p.a_at(cc, i, k); }, k0, cc.vm, vk, va, wid);
     TB::issue(base + (uint32_t)(TA::ELEMS * sizeof(T)), [&](int i, int k) { return p.b_at(cc, i, k); }, k0, cc.vn, vk,
               vb, wid);
   };
@@ -646,10 +680,14 @@ __device__ __forceinline__ bool seg_tile(const int32_t* seg, const int32_t* toff
 // An N-tile holds 128 features: its 256 B-rows alternate 32-row blocks of
 // gate and up rows, so each wavefront's two 32-column MFMA tiles hold the
 // same features of gate and up and the epilogue forms H directly (G and U are
-// rounded to T first, as the expert MLP's two GEMMs would).
-template <typename T>
+// rounded to T first, as the expert MLP's two GEMMs would). With GA the A rows
+// are gathered: sorted row i is token row rows[i] of X, so no sorted copy of
+// the routed rows is written first.
+template <typename T, bool GA = false>
 struct MoeUpProblem {
+  static constexpr bool kGatherA = GA;
   const T* X;
+  const int32_t* rows;  // GA: token row of each sorted row
   const T* const* Wt;  // 2E pointers: gate_e, up_e
   T *G, *U, *H;        // G and U may be null
   const int32_t *seg, *toff;
@@ -673,6 +711,9 @@ struct MoeUpProblem {
   }
   __device__ __forceinline__ const T* a_at(const TileCtx<T>& c, int i, int k) const {
     return X + (int64_t)(c.m0 + i) * ldx + k;
+  }
+  __device__ __forceinline__ const T* a_row(const TileCtx<T>& c, int i) const {
+    return X + (int64_t)rows[c.m0 + i] * ldx;
   }
   __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
     const int b = i >> 5;
@@ -1392,9 +1433,10 @@ namespace {
 bool moe_ok(const void* p, int64_t ld) { return aligned16(p) && ld % 8 == 0; }
 }  // namespace
 
-extern "C" int qh_moe_up(const void* X, int64_t ldx, int64_t R, int64_t K, const void* const* gu_table, int64_t ldw,
-                         int64_t I, const int32_t* seg_off, const int32_t* tile_off, int64_t E, void* G, void* U,
-                         void* H, int64_t ldo, int dtype, void* stream) {
+extern "C" int qh_moe_up(const void* X, int64_t ldx, const int32_t* rows, int64_t R, int64_t K,
+                         const void* const* gu_table, int64_t ldw, int64_t I, const int32_t* seg_off,
+                         const int32_t* tile_off, int64_t E, void* G, void* U, void* H, int64_t ldo, int dtype,
+                         void* stream) {
   QH_CHECK_ARG(R >= 0 && K > 0 && I > 0 && E > 0 && E <= 65536, "qh_moe_up: bad shape");
   QH_CHECK_ARG(I % 128 == 0 && K % 8 == 0 && ldo >= I, "qh_moe_up: needs I %% 128 == 0, K %% 8 == 0");
   QH_CHECK_ARG(moe_ok(X, ldx) && ldw % 8 == 0 && moe_ok(H, ldo) && (G == nullptr) == (U == nullptr),
@@ -1404,10 +1446,11 @@ extern "C" int qh_moe_up(const void* X, int64_t ldx, int64_t R, int64_t K, const
   hipStream_t st = (hipStream_t)stream;
   const int tn = (int)(I / 128);
   int rc = QH_OK;
-#define QH_UP(T)                                                                                        \
+#define QH_UP(T, GA)                                                                                    \
   {                                                                                                     \
-    MoeUpProblem<T> p;                                                                                  \
+    MoeUpProblem<T, GA> p;                                                                              \
     p.X = (const T*)X;                                                                                  \
+    p.rows = rows;                                                                                      \
     p.Wt = (const T* const*)gu_table;                                                                   \
     p.G = (T*)G;                                                                                        \
     p.U = (T*)U;                                                                                        \
@@ -1423,7 +1466,11 @@ extern "C" int qh_moe_up(const void* X, int64_t ldx, int64_t R, int64_t K, const
     p.tiles_n = tn;                                                                                     \
     rc = launch_moe<T, false, false>(p, moe_row_grid(R, E, tn), st, "qh_moe_up");                       \
   }
-  if (dtype == QH_BF16) QH_UP(bf16_t) else QH_UP(f16_t)
+  if (rows != nullptr) {
+    if (dtype == QH_BF16) QH_UP(bf16_t, true) else QH_UP(f16_t, true)
+  } else {
+    if (dtype == QH_BF16) QH_UP(bf16_t, false) else QH_UP(f16_t, false)
+  }
 #undef QH_UP
   if (rc) return rc;
   QH_CHECK_LAUNCH("qh_moe_up");

@@ -89,9 +89,10 @@ def grouped_training_ok(hidden: int, intermediate: int) -> bool:
 
 def _tile_forward(flat, routing_weights, selected, gu_table, dn_table, n_experts, intermediate, ldw_gu, ldw_dn,
                   keep_gu: bool):
-    """Expert forward on the 256x256 tile kernels: dispatch (256-row tiles), gather of the routed rows,
-    gate/up with SiLU-mul (G and U are written only when the backward needs them), down (unscaled D)
-    and the combine with the routing-weight multiply. Returns out and the tensors the backward uses."""
+    """Expert forward on the 256x256 tile kernels: dispatch (256-row tiles), gate/up with SiLU-mul
+    (for training on a gathered copy of the routed rows, which the weight gradients read, with G and
+    U written; for inference gathering the token rows itself), down (unscaled D) and the combine
+    with the routing-weight multiply. Returns out and the tensors the backward uses."""
     t, hidden = flat.shape
     k = selected.shape[1]
     r = t * k
@@ -110,12 +111,17 @@ def _tile_forward(flat, routing_weights, selected, gu_table, dn_table, n_experts
                  ws.numel(), rows.data_ptr(), wsorted.data_ptr(), inv.data_ptr(), seg.data_ptr(), toff.data_ptr(),
                  code, st)
     x = flat.contiguous()
-    xs = torch.empty((r, hidden), dtype=dt, device=dev)
-    _native.call("qh_moe_gather", x.data_ptr(), hidden, rows.data_ptr(), r, hidden, xs.data_ptr(), hidden, code, st)
+    if keep_gu:  # the backward's weight gradients read the routed rows in sorted order
+        xs = torch.empty((r, hidden), dtype=dt, device=dev)
+        _native.call("qh_moe_gather", x.data_ptr(), hidden, rows.data_ptr(), r, hidden, xs.data_ptr(), hidden, code,
+                     st)
+        a, a_rows = xs, None
+    else:  # inference: gate/up gathers the token rows itself
+        xs, a, a_rows = None, x, rows.data_ptr()
     g = torch.empty((r, intermediate), dtype=dt, device=dev) if keep_gu else None
     u = torch.empty_like(g) if keep_gu else None
     h = torch.empty((r, intermediate), dtype=dt, device=dev)
-    _native.call("qh_moe_up", xs.data_ptr(), hidden, r, hidden, gu_table.data_ptr(), ldw_gu, intermediate,
+    _native.call("qh_moe_up", a.data_ptr(), hidden, a_rows, r, hidden, gu_table.data_ptr(), ldw_gu, intermediate,
                  seg.data_ptr(), toff.data_ptr(), n_experts, None if g is None else g.data_ptr(),
                  None if u is None else u.data_ptr(), h.data_ptr(), intermediate, code, st)
     d = torch.empty((r, hidden), dtype=dt, device=dev)

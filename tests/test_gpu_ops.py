@@ -1117,6 +1117,58 @@ def test_moe_inference_tile_path_matches_training_forward(E, k, T):
     close(inf, _loop_experts(blk, x, w, sel), atol=2e-2, rtol=2e-2)
 
 
+@pytest.mark.parametrize("E,k,T,hidden", [(4, 2, 700, 200), (8, 2, 1100, 256), (16, 4, 1200, 2048)])
+def test_moe_up_gathers_token_rows(E, k, T, hidden):
+    """qh_moe_up reading the token rows through the dispatch's row list (the inference forward)
+    writes G, U and H bit for bit as on a gathered copy of the rows (the training forward): K tails
+    (hidden not a multiple of 64), partial 256-row tiles, an expert without rows, a row stride
+    past the row; H within the bf16 band of fp32 torch per expert."""
+    from qwen_triton.kernels.moe_experts import TRAIN_TILE_M
+
+    blk = _moe_block(E, k, hidden=hidden, seed=E + 300)
+    ld = hidden + 24
+    xfull = randn(T, ld, dtype=torch.bfloat16, seed=290)
+    logits = randn(T, E, seed=291) * 2
+    logits[:, -1] = -30.0  # an expert without rows
+    w, sel = blk.route(logits, torch.bfloat16)
+    sel, w = sel.contiguous(), w.contiguous()
+    r, inter, bf = T * k, 128, torch.bfloat16
+    code, st = _native.dtype_code(bf), _native.stream(xfull.device)
+    ws = _native.workspace(_native.call("qh_moe_dispatch_workspace", T, k, E), xfull.device)
+    rows = torch.empty(r, dtype=torch.int32, device=DEV)
+    wsorted = torch.empty(r, dtype=bf, device=DEV)
+    inv = torch.empty(r, dtype=torch.int32, device=DEV)
+    seg = torch.empty(E + 1, dtype=torch.int32, device=DEV)
+    toff = torch.empty_like(seg)
+    _native.call("qh_moe_dispatch", sel.data_ptr(), w.data_ptr(), T, k, E, TRAIN_TILE_M, ws.data_ptr(), ws.numel(),
+                 rows.data_ptr(), wsorted.data_ptr(), inv.data_ptr(), seg.data_ptr(), toff.data_ptr(), code, st)
+    xs = torch.empty(r, hidden, dtype=bf, device=DEV)
+    _native.call("qh_moe_gather", xfull.data_ptr(), ld, rows.data_ptr(), r, hidden, xs.data_ptr(), hidden, code, st)
+    gu, _ = blk._expert_tables(xfull.device)
+    ldw = blk.experts[0].gate_proj.weight.stride(0)
+
+    def up(a, lda, row_list):
+        g, u, h = (torch.full((r, inter), 7.0, dtype=bf, device=DEV) for _ in range(3))
+        _native.call("qh_moe_up", a.data_ptr(), lda, row_list, r, hidden, gu.data_ptr(), ldw, inter, seg.data_ptr(),
+                     toff.data_ptr(), E, g.data_ptr(), u.data_ptr(), h.data_ptr(), inter, code, st)
+        return g, u, h
+
+    ref = up(xs, hidden, None)
+    got = up(xfull, ld, rows.data_ptr())
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    segs = seg.cpu().tolist()
+    assert segs[E] - segs[E - 1] == 0 and max(b - a for a, b in zip(segs, segs[1:])) > TRAIN_TILE_M
+    xr = xfull[:, :hidden][rows.long()].float()
+    for e in range(E):
+        a, b = segs[e], segs[e + 1]
+        if a == b:
+            continue
+        gref = xr[a:b] @ blk.experts[e].gate_proj.weight.float().t()
+        uref = xr[a:b] @ blk.experts[e].up_proj.weight.float().t()
+        close(got[2][a:b].float(), torch.nn.functional.silu(gref) * uref, atol=2e-2, rtol=2e-2)
+
+
 @pytest.mark.parametrize("E,k,T", [(8, 2, 300), (4, 2, 700), (16, 4, 257)])
 def test_moe_grouped_training_matches_loop_gradients(E, k, T):
     """Autograd through the grouped training kernels vs the per-expert loop: output and the
