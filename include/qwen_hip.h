@@ -437,6 +437,9 @@ int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const voi
                  const void* o, const void* dout, const float* lse, void* dq, void* dk, void* dv, void* ws,
                  int64_t ws_bytes, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
                  float scale, int causal, int64_t causal_offset, int dtype, void* stream);
+/* Bytes of split-KV partials qh_flash_decode needs: 0 where head dim 128 meets
+ * at least 512 (sequence, kv-head) pairs (one workgroup per pair, partials
+ * combined on chip), else B * Hq * splits * (D + 2) * 4. */
 int64_t qh_flash_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk, int64_t D);
 /* Single-query attention (Sq == 1, no mask) over a KV cache: split-KV partials
  * + fixed-order combine. q strides (batch, head); o contiguous [B,Hq,1,D].
@@ -455,8 +458,9 @@ int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const void* k, int6
  * device memory (code under HIP graph capture, serving loops or harnesses that
  * forbid hipMalloc). The split partials live in a static 16 MiB device array
  * per GPU (held from the first call on that GPU until the process ends);
- * shapes whose partials need more (qh_flash_decode_workspace, or 0 where head
- * dim 128 meets at least 512 (sequence, kv-head) pairs) return QH_E_WORKSPACE.
+ * shapes whose partials need more (qh_flash_decode_workspace; 0 where head
+ * dim 128 meets at least 512 (sequence, kv-head) pairs, which then touch no
+ * scratch) return QH_E_WORKSPACE.
  * Results equal qh_flash_decode's bit for bit. Calls that overlap on one GPU
  * share the array and race; serialise them (one stream). */
 int qh_flash_decode_noalloc(const void* q, int64_t sqb, int64_t sqh, const void* k, int64_t skb, int64_t skh,

@@ -1885,9 +1885,14 @@ extern "C" int qh_flash_bwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
   return QH_OK;
 }
 
+// The workgroup kernel (head dim 128, at least kDecodeWgMinSeqs (sequence,
+// kv-head) pairs) combines its partials in LDS and needs no workspace; the
+// split kernel keeps [B*Hq, splits, D+2] fp32 partials.
+static bool decode_on_chip(int64_t B, int64_t Hkv, int dp) { return dp == 128 && B * Hkv >= kDecodeWgMinSeqs; }
+
 extern "C" int64_t qh_flash_decode_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sk, int64_t D) {
   const int dp = pick_dp(D);
-  if (!dp || Hkv <= 0) return 0;
+  if (!dp || Hkv <= 0 || B <= 0 || decode_on_chip(B, Hkv, dp)) return 0;
   const int ns = decode_splits(B, Hkv, Sk);
   return B * Hq * ns * (dp + 2) * 4;
 }
@@ -1918,7 +1923,7 @@ extern "C" int qh_flash_decode(const void* q, int64_t sqb, int64_t sqh, const vo
   }
   hipStream_t st = (hipStream_t)stream;
   const float sl2 = scale * kLog2e;
-  if (dp == 128 && B * Hkv >= kDecodeWgMinSeqs) {
+  if (decode_on_chip(B, Hkv, dp)) {
     // many sequences: one workgroup per (b, kv-head), combined in LDS
 #define QH_WG(T, GV)                                                                                              \
   fa_decode_wg_kernel<T, 128, GV><<<(unsigned)(B * Hkv), 256, 0, st>>>(                                         \
@@ -2012,9 +2017,8 @@ extern "C" int qh_flash_decode_noalloc(const void* q, int64_t sqb, int64_t sqh, 
                                        int64_t Hq, int64_t Hkv, int64_t Sk, int64_t D, float scale, int dtype,
                                        void* stream) {
   QH_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && Sk >= 0, "qh_flash_decode_noalloc: bad shape");
-  // the workgroup kernel (head dim 128, many sequences) keeps its partials on chip
-  const bool on_chip = pick_dp(D) == 128 && B * Hkv >= kDecodeWgMinSeqs;
-  const int64_t need = on_chip ? 0 : qh_flash_decode_workspace(B, Hq, Hkv, Sk, D);
+  // 0 for the workgroup kernel (head dim 128, many sequences), which keeps its partials on chip
+  const int64_t need = qh_flash_decode_workspace(B, Hq, Hkv, Sk, D);
   if (need > kDecodeScratchBytes) {
     qh::set_error("qh_flash_decode_noalloc: this shape needs %lld bytes of split partials, more than the %lld-byte "
                   "static scratch; use qh_flash_decode with a workspace",

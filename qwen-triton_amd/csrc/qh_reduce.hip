@@ -892,11 +892,12 @@ static void launch_topk(const void* x, void* vals, int64_t* idx, int64_t N, int6
 // semantics: NaN counts as the largest value, ties go to the lowest column)
 // and the step's bookkeeping in device memory. An element's key is
 // (order-preserving value bits, NaN above +inf) << 32 | ~column, so the
-// largest key is the answer whatever the reduction order.
+// largest key is the answer whatever the reduction order; -0.0 keys as +0.0
+// (the two compare equal, so the lower column wins between them).
 constexpr int kGreedyMaxRows = 64;  // rows one launch serves
 
 __device__ __forceinline__ uint64_t greedy_key(float v, int c) {
-  uint32_t b = __float_as_uint(v);
+  uint32_t b = v == 0.f ? 0u : __float_as_uint(v);
   b = (v != v) ? 0xFFFFFFFFu : (b ^ ((b >> 31) ? 0xFFFFFFFFu : 0x80000000u));
   return ((uint64_t)b << 32) | (uint32_t)~(uint32_t)c;
 }

@@ -12,6 +12,7 @@ forward ``x W^T`` (NT), input grad ``dy W`` (B transposed view) and weight grad
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
@@ -19,6 +20,14 @@ from .. import _native
 from ._common import OpGuard, needs_grad, Unsupported
 
 _GUARD = OpGuard("Matmul")
+
+# Inference products behind an RMSNorm (q/k/v, gate/up) read a copy of their weights with the norm
+# weight folded in (``_folded_group``): one extra copy of those weights per model, about 0.59 GB at
+# Qwen3-0.6B (28 layers x (8 + 12) MB), kept on the norm weight until ``release_folded_weights``.
+# With the switch off (or QWEN_TRITON_FOLD_NORM=0) no copy is made: the launch scales the weight
+# fragments itself (``qh_gemm_multi_ex``, same bits for more than 4 rows) where its shape fits one
+# load chunk per workgroup, and the layer otherwise runs the separate norm and products.
+FOLD_NORM_WEIGHTS = os.environ.get("QWEN_TRITON_FOLD_NORM", "1") != "0"
 
 
 def _torch_matmul(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
@@ -110,7 +119,36 @@ def linear_group_norm_ok(x: torch.Tensor, weights: list[torch.Tensor], norm_weig
     if not (norm_weight.is_cuda and norm_weight.dim() == 1 and norm_weight.shape[0] == k
             and norm_weight.is_contiguous() and norm_weight.dtype == x.dtype):
         return False
-    return not gated or (len(weights) == 2 and weights[0].shape[0] == weights[1].shape[0])
+    if gated and not (len(weights) == 2 and weights[0].shape[0] == weights[1].shape[0]):
+        return False
+    if FOLD_NORM_WEIGHTS:
+        return True
+    ns = (ctypes.c_int64 * len(weights))(*(w.shape[0] for w in weights))
+    return bool(_native.call("qh_gemm_multi_norm_fits", x.numel() // k, k, int(gated), len(weights),
+                             ctypes.addressof(ns)))
+
+
+def release_folded_weights(module: torch.nn.Module) -> int:
+    """Free the norm-folded weight copies made for ``module``'s inference products (they are made
+    again on the next such call while ``FOLD_NORM_WEIGHTS`` is on). Returns the bytes released.
+    Captured graphs that read the copies keep them alive until the graphs are dropped."""
+    freed = 0
+    for t in list(module.parameters()) + list(module.buffers()):
+        store = t.__dict__.pop("_qh_folded", None)
+        for _, folded, fb in (store or {}).values():
+            freed += sum(w.numel() * w.element_size() for w in folded)
+            freed += sum(b.numel() * b.element_size() for b in (fb or []) if b is not None)
+    return freed
+
+
+def folded_weight_tensors(module: torch.nn.Module) -> list[torch.Tensor]:
+    """The norm-folded weight copies currently kept for ``module`` (see ``_folded_group``)."""
+    out = []
+    for t in list(module.parameters()) + list(module.buffers()):
+        for _, folded, fb in getattr(t, "_qh_folded", {}).values():
+            out.extend(folded)
+            out.extend(b for b in (fb or []) if b is not None)
+    return out
 
 
 def _folded_group(weights: list[torch.Tensor], biases: list[torch.Tensor | None] | None, norm_weight: torch.Tensor,
@@ -214,6 +252,8 @@ def _linear_group_rms(x, x2, weights, biases, gated, norm):
     (``qh_gemm_multi_rms``)."""
     nw, eps, one_plus = norm
     k, m = x2.shape[1], x2.shape[0]
+    if not FOLD_NORM_WEIGHTS:
+        return _linear_group_norm_in_kernel(x, x2, weights, biases, gated, norm)
     concat = not gated and len(weights) > 1
     fw, fb = _folded_group(weights, biases, nw, one_plus, concat)
     n = len(fw)
@@ -236,6 +276,28 @@ def _linear_group_rms(x, x2, weights, biases, gated, norm):
             c0 += w.shape[0]
         return cols
     return [outs[0].view(*lead, outs[0].shape[1])]
+
+
+def _linear_group_norm_in_kernel(x, x2, weights, biases, gated, norm):
+    """``linear_group(..., norm=...)`` without a folded copy: the launch scales the weight
+    fragments by the norm weight itself (``qh_gemm_multi_ex``)."""
+    nw, eps, one_plus = norm
+    k, m = x2.shape[1], x2.shape[0]
+    n = len(weights)
+    bptr, ldb, nn_, bias_addr = _group_plan(weights, biases)[:4]
+    outs = [torch.empty((m, w.shape[0]), dtype=x.dtype, device=x.device) for w in (weights[:1] if gated else weights)]
+    arr_p = ctypes.c_void_p * n
+    arr_l = ctypes.c_int64 * n
+    cptr = arr_p(*([o.data_ptr() for o in outs] + [None] * (n - len(outs))))
+    ldc = arr_l(*([o.stride(0) for o in outs] + [0] * (n - len(outs))))
+    code = _native.dtype_code(x.dtype)
+    _native.call("qh_gemm_multi_ex", m, k, x2.data_ptr(), x2.stride(0), n, ctypes.addressof(bptr),
+                 ctypes.addressof(ldb), ctypes.addressof(nn_), ctypes.addressof(cptr), ctypes.addressof(ldc),
+                 bias_addr, None, None, int(gated), nw.data_ptr(), code, float(eps), int(bool(one_plus)), code,
+                 _native.stream(x.device))
+    lead = x.shape[:-1]
+    outs = [o.view(*lead, o.shape[1]) for o in outs]
+    return outs[0] if gated else outs
 
 
 def _native_matmul_forward(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:

@@ -29,6 +29,7 @@ from transformers.modeling_outputs import CausalLMOutputWithPast
 
 from qwen_triton.configs import QwenTritonConfig
 from qwen_triton.kernels.cross_entropy import triton_cross_entropy
+from qwen_triton.kernels import matmul as _matmul
 from qwen_triton.kernels.matmul import linear_group, linear_group_norm_ok, linear_group_ok
 from qwen_triton.kernels.residual_add import residual_add
 from qwen_triton.kernels.rmsnorm import add_rmsnorm, add_rmsnorm_ok
@@ -142,7 +143,8 @@ class QwenDecoderLayer(nn.Module):
             return False
         # the answer depends on the activation shape and on the weights (a cast or a reassignment
         # of the parameters changes their dtype or storage)
-        key = (hidden_states.shape[0] * hidden_states.shape[1], hidden_states.dtype, hidden_states.device) + tuple(
+        key = (hidden_states.shape[0] * hidden_states.shape[1], hidden_states.dtype, hidden_states.device,
+               _matmul.FOLD_NORM_WEIGHTS) + tuple(
             (w.data_ptr(), w.dtype) for w in (attn.q_proj.weight, attn.o_proj.weight, mlp.gate_proj.weight,
                                               mlp.down_proj.weight, self.input_layernorm.weight,
                                               self.post_attention_layernorm.weight))
@@ -456,13 +458,17 @@ class QwenTritonForCausalLM(nn.Module):
     def greedy_graphs(self, batch: int, prompt: int, max_new_tokens: int):
         """The captured-graph runner (``models.graphs.GreedyGraphs``) for this generation shape,
         created on first use and kept (the four most recent shapes; ``release_graphs`` frees them).
-        Runners are keyed on the parameters' storage too, so replaced parameters get new graphs."""
+        Runners are keyed on the parameters' storage and version counters too, so parameters that
+        are replaced or updated in place (a checkpoint ``copy_``, an optimizer step) get new graphs,
+        captured over freshly derived tensors (norm-folded weights); a runner keeps the derived
+        tensors its graphs read alive itself."""
         from collections import OrderedDict
 
         from qwen_triton.models.graphs import GreedyGraphs
 
         w = self.lm_head.weight
-        key = (batch, prompt, max_new_tokens, w.dtype, w.device, tuple(p.data_ptr() for p in self.parameters()))
+        key = (batch, prompt, max_new_tokens, w.dtype, w.device, _matmul.FOLD_NORM_WEIGHTS,
+               tuple((p.data_ptr(), p._version) for p in self.parameters()))
         runners = self.__dict__.setdefault("_graph_runners", OrderedDict())
         runner = runners.get(key)
         if runner is None:
@@ -475,6 +481,13 @@ class QwenTritonForCausalLM(nn.Module):
     def release_graphs(self) -> None:
         """Drop the captured generation graphs and their caches."""
         self.__dict__.pop("_graph_runners", None)
+
+    def release_folded_weights(self) -> int:
+        """Free the norm-folded copies of the q/k/v and gate/up weights that batched inference
+        keeps (about 0.59 GB at Qwen3-0.6B; ``kernels.matmul.FOLD_NORM_WEIGHTS`` turns them off),
+        and the captured graphs that read them. Returns the bytes released."""
+        self.release_graphs()
+        return _matmul.release_folded_weights(self)
 
     @torch.no_grad()
     def _greedy_generate_graph(self, input_ids: torch.LongTensor, max_new_tokens: int) -> torch.LongTensor:

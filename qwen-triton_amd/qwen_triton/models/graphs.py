@@ -14,9 +14,11 @@ are two library launches (``qh_greedy_step``), or for more than 64 rows a top-1 
 torch ops on the same buffers.
 
 Both are captured on first use. Each replay overwrites the same buffers (cache, tokens), so a
-runner serves one call at a time; the graphs hold the parameters' storage addresses, so a model
-whose parameters are replaced (not updated in place) gets new runners (the owner keys them on
-those addresses).
+runner serves one call at a time. The graphs hold the addresses of the parameters and of tensors
+derived from them (norm-folded weights, rotary tables): the owner keys runners on the parameters'
+storage and version counters, so replaced or in-place-updated parameters get new runners, and a
+runner holds references to the derived tensors its graphs read, so that a rebuilt fold or a
+regrown rotary table never frees memory a graph still reads.
 """
 from __future__ import annotations
 
@@ -56,6 +58,7 @@ class GreedyGraphs:
                                    seqlens=torch.full((batch,), prompt + 1, dtype=torch.int32, device=device))
         self.prefill_graph: torch.cuda.CUDAGraph | None = None
         self.step_graph: torch.cuda.CUDAGraph | None = None
+        self._derived: list[torch.Tensor] = []
         # the pick and the step's bookkeeping in two library launches (qh_greedy_step) when the
         # shape allows; otherwise top-1 and torch ops on the same buffers
         vocab = model.config.vocab_size
@@ -126,6 +129,19 @@ class GreedyGraphs:
         with torch.cuda.graph(step):
             self._step_body()
         self.prefill_graph, self.step_graph = prefill, step
+        self._derived = self._derived_tensors()
+
+    def _derived_tensors(self) -> list[torch.Tensor]:
+        """Tensors the captured graphs read that the model keeps outside its parameters: the
+        norm-folded weights and the rotary tables (held here so they outlive a rebuild)."""
+        from qwen_triton.kernels.matmul import folded_weight_tensors
+        from qwen_triton.modules.rotary import QwenRotaryEmbedding
+
+        held = folded_weight_tensors(self.model)
+        for mod in self.model.modules():
+            if isinstance(mod, QwenRotaryEmbedding):
+                held.extend(mod._tables.values())
+        return held
 
     @torch.no_grad()
     def prefill(self, input_ids: torch.Tensor) -> torch.Tensor:

@@ -46,7 +46,9 @@ def test_workspace_queries_are_host_only():
     # Delta and log2-scale LSE per query, rows padded to a multiple of 64 plus one 64-query tile
     assert _native.call("qh_flash_bwd_workspace", 8, 16, 4096) == 2 * 8 * 16 * (4096 + 64) * 4
     assert _native.call("qh_flash_bwd_workspace", 1, 2, 65) == 2 * 1 * 2 * (128 + 64) * 4
-    assert _native.call("qh_flash_decode_workspace", 64, 16, 8, 2049, 128) > 0
+    # 64 sequences x 8 kv-heads at head dim 128: one workgroup per pair, partials combined on chip
+    assert _native.call("qh_flash_decode_workspace", 64, 16, 8, 2049, 128) == 0
+    assert _native.call("qh_flash_decode_workspace", 8, 32, 8, 2900, 128) > 0
 
 
 def test_argument_errors_are_reported_without_launching():

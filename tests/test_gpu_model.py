@@ -428,6 +428,68 @@ def test_greedy_generate_graph_replay_matches_eager(moe, prompt):
     assert launched == 2 * cfg.num_hidden_layers
 
 
+def test_graph_runner_follows_in_place_weight_updates():
+    """Cached greedy graphs read the parameters and tensors derived from them (norm-folded
+    weights, rotary tables) by address. After an in-place update of the weights (as a checkpoint
+    load's ``copy_`` or an optimizer step does) the next graph generation must equal the eager
+    loop on the new weights, not replay the old folded copies; a regrown rotary table must not
+    free what an older runner reads."""
+    cfg = _cfg(max_position_embeddings=1024)
+    m = _model(cfg, seed=31)
+    ids = torch.randint(0, cfg.vocab_size, (2, 19), generator=torch.Generator().manual_seed(32)).cuda()
+    new = 12
+    with torch.no_grad():
+        g0 = m.greedy_generate(ids, max_new_tokens=new, use_graph=True)
+        assert torch.equal(g0, m.greedy_generate(ids, max_new_tokens=new))
+        donor = _model(cfg, seed=33)
+        for p, q in zip(m.parameters(), donor.parameters()):
+            p.copy_(q)  # in place: same storage, new values
+        eager = m.greedy_generate(ids, max_new_tokens=new)
+        graph = m.greedy_generate(ids, max_new_tokens=new, use_graph=True)
+        assert not torch.equal(eager, g0)
+        assert torch.equal(graph, eager)
+        # a longer generation regrows the rotary tables; the runner of the shorter one still replays
+        m.greedy_generate(ids, max_new_tokens=700, use_graph=False)
+        assert torch.equal(m.greedy_generate(ids, max_new_tokens=new, use_graph=True), eager)
+
+
+def test_fold_switch_off_keeps_no_weight_copies(monkeypatch):
+    """With ``FOLD_NORM_WEIGHTS`` off the norm-fused products scale the weight fragments in the
+    launch (no folded copy is kept) and give the folded path's bits for more than 4 rows;
+    ``release_folded_weights`` frees the copies the folded path made."""
+    from qwen_triton.kernels import matmul
+
+    cfg = _cfg()
+    m = _model(cfg, seed=35)
+    ids = torch.randint(0, cfg.vocab_size, (8, 12), generator=torch.Generator().manual_seed(36)).cuda()
+    outs = {}
+    for fold in (True, False):
+        monkeypatch.setattr(matmul, "FOLD_NORM_WEIGHTS", fold)
+        assert m.release_folded_weights() >= 0
+        c0 = _native.CALLS["qh_gemm_multi_rms"]
+        with torch.no_grad():
+            p = m(input_ids=ids[:, :8], use_cache=True)
+            steps = [p.logits[:, -1]]
+            for t in range(8, 12):
+                steps.append(m(input_ids=ids[:, t:t + 1], past_key_values=p.past_key_values,
+                               use_cache=True).logits[:, -1])
+        outs[fold] = torch.stack(steps, 1)
+        kept = matmul.folded_weight_tensors(m)
+        if fold:
+            assert _native.CALLS["qh_gemm_multi_rms"] > c0 and kept
+            qkv = sum(w.numel() for w in (m.model.layers[0].self_attn.q_proj.weight,
+                                          m.model.layers[0].self_attn.k_proj.weight,
+                                          m.model.layers[0].self_attn.v_proj.weight,
+                                          m.model.layers[0].mlp.gate_proj.weight,
+                                          m.model.layers[0].mlp.up_proj.weight))
+            assert sum(w.numel() for w in kept) == qkv * cfg.num_hidden_layers
+        else:
+            assert _native.CALLS["qh_gemm_multi_rms"] == c0 and not kept
+    assert torch.equal(outs[True], outs[False])
+    monkeypatch.setattr(matmul, "FOLD_NORM_WEIGHTS", True)
+    assert m.release_folded_weights() == 0
+
+
 def test_fused_decode_prepare_in_model_bitwise(monkeypatch):
     # 64 sequences x 8 kv-heads: decode steps take qh_flash_decode_prepare (norm, RoPE and cache
     # writes inside the decode-attention kernel); the separate prepare pass must give identical

@@ -1457,7 +1457,13 @@ def test_greedy_step_is_argmax_and_advances_the_state(B, V, dtype):
     if B >= 3:
         x[2, V - 1] = float("nan")               # NaN is the largest value
         x[2, V - 3] = float("nan")
+    if B >= 2 and V >= 8:
+        x[1] = -x[1].abs() - 1                   # a row whose maximum is zero, -0.0 before +0.0:
+        x[1, 3] = -0.0                           # they compare equal, the earlier column wins
+        x[1, 7] = 0.0
     expect = x.float().cpu().argmax(dim=-1)
+    if B >= 2 and V >= 8:
+        assert int(expect[1]) == 3
     ids = torch.full((B, 1), -5, dtype=torch.long, device=DEV)
     tokens = torch.full((B, 6), -7, dtype=torch.long, device=DEV)
     col = torch.full((1, 1), 2, dtype=torch.long, device=DEV)

@@ -44,10 +44,12 @@ def _decode(name, q, k, v, seqlens, D):
 
 
 def test_flash_decode_noalloc_matches_workspace_entry():
-    # first a larger split-KV call (8 sequences x 8 kv heads, 2900 keys, GQA 4, per-sequence lengths),
-    # then a smaller one (1 sequence, 300 keys, GQA 2, no lengths): the second reuses the array the
-    # first left filled
-    cases = [(8, 32, 8, 3000, 2900, 128, True, 11), (1, 16, 8, 320, 300, 128, False, 12)]
+    # first the config-3 shape (64 sequences x 8 kv heads, 2049 keys, GQA 2, per-sequence lengths:
+    # the workgroup kernel, partials on chip, no scratch), then a larger split-KV call (8 sequences
+    # x 8 kv heads, 2900 keys, GQA 4, per-sequence lengths), then a smaller one (1 sequence, 300
+    # keys, GQA 2, no lengths): the last reuses the array the one before left filled
+    cases = [(64, 16, 8, 2112, 2049, 128, True, 10), (8, 32, 8, 3000, 2900, 128, True, 11),
+             (1, 16, 8, 320, 300, 128, False, 12)]
     for B, Hq, Hkv, cap, Sk, D, use_lens, seed in cases:
         print(f"[no_alloc] B={B} Hq={Hq} Hkv={Hkv} Sk={Sk} D={D} seqlens={use_lens}", flush=True)
         q, kc, vc = _inputs(B, Hq, Hkv, cap, D, seed)
