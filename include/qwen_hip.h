@@ -32,6 +32,11 @@ const char* qh_version(void);
 int qh_zero(void* ptr, int64_t nbytes, void* stream);
 
 /* ---- elementwise -------------------------------------------------------- */
+/* dst[i] = round(src[i] * scale[0]) in dtype (fp32 src 16-byte aligned, scale a
+ * device pointer). No counterpart in the reference: it applies the upstream
+ * gradient of the fused LM head + cross-entropy (known only in the backward)
+ * to the gradients the forward formed unscaled. */
+int qh_scale_cast(const float* src, void* dst, int64_t n, const float* scale, int dtype, void* stream);
 /* out = x + r over n contiguous elements.
  * Replaces qwen_triton/kernels/residual_add.py:50-60 (_residual_add_kernel), :86-101. */
 int qh_add(const void* x, const void* r, void* out, int64_t n, int dtype, void* stream);
@@ -131,7 +136,8 @@ int qh_ce_fwd(const void* logits, int64_t stride, const int64_t* targets, float*
               float* loss_out, float* nvalid_out, int64_t N, int64_t V, int64_t ignore_index, int dtype,
               void* stream);
 /* glogits = (softmax - onehot(t)) * grad_loss[0] / max(1, nvalid[0]); ignored rows 0.
- * grad_loss and nvalid are device pointers (no host sync).
+ * grad_loss and nvalid are device pointers (no host sync). glogits may be logits
+ * itself (in place, gstride == stride).
  * Replaces qwen_triton/kernels/cross_entropy.py:108-139, :180-192. */
 int qh_ce_bwd(const void* logits, int64_t stride, const int64_t* targets, const float* lse,
               const float* grad_loss, const float* nvalid, void* glogits, int64_t gstride, int64_t N,
@@ -372,18 +378,31 @@ int64_t qh_lmce_workspace(int64_t N, int64_t V);
 int qh_lmce_fwd(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets, int64_t N,
                 int64_t V, int64_t H, int64_t ignore_index, float* lse, float* loss_rows, float* loss_out,
                 float* nvalid_out, void* ws, int64_t ws_bytes, int dtype, void* stream);
-/* Logit gradient of the vocabulary columns [v0, v0 + Vc): G[row, j] =
- * (exp(logit[row, v0 + j] - lse[row]) - [v0 + j == target]) * grad_loss[0] /
- * max(1, nvalid[0]) in the activation dtype (ignored rows 0), recomputing the
- * logits of those columns; G [N, Vc] with row stride ldg (Vc % 8 == 0). The
- * caller forms dW[v0:v0+Vc] = G^T X and dX += G W[v0:v0+Vc] (qh_gemm_acc). */
-int qh_lmce_grad(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets, const float* lse,
-                 const float* grad_loss, const float* nvalid, int64_t N, int64_t v0, int64_t Vc, int64_t H,
-                 int64_t ignore_index, void* G, int64_t ldg, int dtype, void* stream);
+/* The fused LM head + cross-entropy with gradients, one block of rows at a
+ * time, with no recomputed logits: Z = X W^T for a block of rows (the only
+ * [rows, V] buffer), the row's logsumexp from per-64-column partials formed in
+ * the same GEMM's epilogue, then the logit gradient formed in Z in place
+ * (qh_ce_bwd) and multiplied into dX (these rows) and dW (accumulated over the
+ * blocks, qh_gemm_acc). No counterpart in the reference; it replaces, fused,
+ * the same calls as qh_lmce_fwd above, with gradients. */
+/* Workspace bytes of qh_lmce_rows_fwd: per-64-column partials and target logits. */
+int64_t qh_lmce_rows_workspace(int64_t N, int64_t V);
+/* Z [N, V] (row stride ldz) = X W^T rounded to the dtype; lse[row] and
+ * loss_rows[row] = lse - logit[target] (0 for ignore_index rows, NaN for
+ * targets outside [0, V)) as qh_lmce_fwd gives them. bf16/f16, V % 8 == 0. */
+int qh_lmce_rows_fwd(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets, int64_t N,
+                     int64_t V, int64_t H, int64_t ignore_index, void* Z, int64_t ldz, float* lse, float* loss_rows,
+                     void* ws, int64_t ws_bytes, int dtype, void* stream);
+/* *nvalid_out = number of targets != ignore_index (fp32, exact below 2^24). */
+int qh_lmce_count(const int64_t* targets, int64_t N, int64_t ignore_index, float* nvalid_out, void* stream);
+/* *loss_out = sum(loss_rows) / max(1, n_valid), *nvalid_out = n_valid (fixed-order
+ * fp32 sums, as qh_ce_fwd's finish). */
+int qh_lmce_finish(const float* loss_rows, const int64_t* targets, int64_t N, int64_t ignore_index,
+                   float* loss_out, float* nvalid_out, void* stream);
 /* C[M,N] += A(M,K) . B(N,K)^T with fp32 C and bf16/f16 operands in the operand
  * views of qh_gemm (256x256 tile kernel). No counterpart in the reference: the
- * fixed-order accumulation of the fused cross-entropy's input gradient over
- * vocabulary chunks. */
+ * fixed-order accumulation of the fused cross-entropy's weight gradient over
+ * row blocks. */
 int qh_gemm_acc(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, const void* B,
                 int64_t ldb, float* C, int64_t ldc, int dtype, void* stream);
 

@@ -6,6 +6,8 @@
 // oversubscribing the dispatcher. fp32 math, one rounding on store.
 #include "qh_common.h"
 
+#include <algorithm>
+
 namespace {
 
 // ---------------------------------------------------------------------------
@@ -319,6 +321,36 @@ __global__ __launch_bounds__(256) void embedding_scalar(const int64_t* __restric
 // ===========================================================================
 // C ABI
 // ===========================================================================
+// dst = round(src * scale[0]) in T (fp32 src, scale read on the device).
+template <typename T>
+__global__ __launch_bounds__(256) void scale_cast_kernel(const float* __restrict__ src, T* __restrict__ dst,
+                                                         int64_t n, const float* __restrict__ scale) {
+  const float s = scale[0];
+  const int64_t n4 = n / 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const float4 v = reinterpret_cast<const float4*>(src)[i];
+    dst[4 * i] = from_f32<T>(v.x * s);
+    dst[4 * i + 1] = from_f32<T>(v.y * s);
+    dst[4 * i + 2] = from_f32<T>(v.z * s);
+    dst[4 * i + 3] = from_f32<T>(v.w * s);
+  }
+  for (int64_t i = 4 * n4 + blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride)
+    dst[i] = from_f32<T>(src[i] * s);
+}
+
+extern "C" int qh_scale_cast(const float* src, void* dst, int64_t n, const float* scale, int dtype, void* stream) {
+  QH_CHECK_ARG(n >= 0 && src != nullptr && dst != nullptr && scale != nullptr, "qh_scale_cast: bad arguments");
+  QH_CHECK_ARG(aligned16(src), "qh_scale_cast: src must be 16-byte aligned");
+  if (n == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t grid = std::min<int64_t>(ceil_div(n / 4 + 1, 256), 4096);
+  QH_DISPATCH_DTYPE(dtype, T, "qh_scale_cast",
+                    scale_cast_kernel<T><<<(unsigned)grid, 256, 0, st>>>(src, (T*)dst, n, scale));
+  QH_CHECK_LAUNCH("qh_scale_cast");
+  return QH_OK;
+}
+
 extern "C" int qh_add(const void* x, const void* r, void* out, int64_t n, int dtype, void* stream) {
   QH_CHECK_ARG(n >= 0, "qh_add: negative n");
   if (n == 0) return QH_OK;

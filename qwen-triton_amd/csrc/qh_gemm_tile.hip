@@ -1284,27 +1284,32 @@ struct LmceFwdProblem {
   __device__ __forceinline__ void epilogue(const TileCtx<T>&, const f32x16 (&)[TM][TN], int, int, int) const {}
 };
 
-// Backward of one vocabulary chunk [v0, v0 + N): recomputes its logits and
-// writes G[row][col] = (exp(s - lse[row]) - [v0 + col == target]) * g / n_valid
-// in T (ignored rows 0), the unfused cross-entropy backward's values for
-// these columns.
+// Logits of a block of rows for the fused LM head + cross-entropy with
+// gradients: Z = X W^T rounded to T and written out (the caller turns Z into
+// the logit gradient in place), and per row the (max, sum of exp) of every
+// 64-column block of the rounded logits plus the target logit, so the row's
+// logsumexp needs no further pass over Z. Persistent like the dense problem;
+// each wavefront reduces its own 64 columns, so no cross-wave step is needed
+// in the epilogue.
 template <typename T>
-struct LmceGradProblem {
+struct LmceLogitsProblem {
   const T* X;
-  const T* W;  // first row = vocabulary entry v0
+  const T* W;
+  T* Z;
   const int64_t* tgt;
-  const float* lse;
-  const float* gloss;
-  const float* nvalid;
-  T* G;
-  int64_t ldx, ldw, ldg, v0, ignore;
-  int M, N, K, tiles_m, tiles_n;
+  float2* part;   // [nblk][M] (max, sum of exp): a wave's rows are consecutive, stores coalesce
+  float* tlogit;  // [M]
+  int64_t ldx, ldw, ldz;
+  int M, N, K, tiles_m, tiles_n, nblk;
 
   static constexpr bool kVecEpilogue = true;
+  static constexpr bool kPersistent = true;
   __device__ __forceinline__ bool vec_ok() const { return true; }
-  __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
+  __device__ __forceinline__ int tiles_total() const { return tiles_m * tiles_n; }
+  __device__ __forceinline__ bool tile_at(int t, TileCtx<T>& c) const {
+    if (t >= tiles_m * tiles_n) return false;
     int tm, tn;
-    tile_order(tiles_m, tiles_n, tm, tn);
+    tile_group_order(t, tiles_m, tiles_n, tm, tn);
     c.m0 = tm * 256;
     c.n0 = tn * 256;
     c.K = K;
@@ -1321,32 +1326,100 @@ struct LmceGradProblem {
   __device__ __forceinline__ const T* b_at(const TileCtx<T>& c, int i, int k) const {
     return W + (int64_t)(c.n0 + i) * ldw + k;
   }
-  template <class ET>
+  template <int ROWS = 128, class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
-    const float scale = gloss[0] / fmaxf(nvalid[0], 1.f);
-    for (int q = lane; q < 128 * 8; q += 64) {
+    for (int q = lane; q < ROWS * 8; q += 64) {  // the rounded logits, 8 lanes per 128-byte row piece
       const int r = q >> 3, c8 = q & 7;
       const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
-      if (row >= M || col >= N) continue;
-      const int64_t t = tgt[row];
-      Vec16<T> o;
-      if (t == ignore) {
-        o.raw = make_uint4(0, 0, 0, 0);
-      } else {
-        const Vec16<T> v = et.row8(r, c8);
-        const float l = lse[row];
+      if (row < M && col < N) st16(Z + (int64_t)row * ldz + col, et.row8(r, c8));
+    }
+    const int ncol = max(0, min(64, c.vn - wc));
+    const int blk = (c.n0 + wc) >> 6;
+    for (int r = lane; r < ROWS; r += 64) {
+      const int row = c.m0 + wr + r;
+      if (row >= M || ncol == 0) continue;
+      float m = -INFINITY, sum = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pr = __expf(to_f32(v.v[e]) - l);
-          o.v[e] = from_f32<T>((pr - (v0 + col + e == t ? 1.f : 0.f)) * scale);
+      for (int c8 = 0; c8 < 8; ++c8) {
+        if (8 * c8 >= ncol) break;
+        const Vec16<T> v = et.row8(r, c8);
+        float lm = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (8 * c8 + e < ncol) lm = fmaxf(lm, to_f32(v.v[e]));
+        if (lm > m) {
+          sum = m == -INFINITY ? 0.f : sum * __expf(m - lm);
+          m = lm;
+        }
+        if (m != -INFINITY) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (8 * c8 + e < ncol) sum += __expf(to_f32(v.v[e]) - m);
         }
       }
-      st16(G + (int64_t)row * ldg + col, o);
+      part[(int64_t)blk * M + row] = make_float2(m, sum);
+      const int64_t tc = tgt[row] - (int64_t)(c.n0 + wc);
+      if (tc >= 0 && tc < ncol) tlogit[row] = to_f32(et.row8(r, (int)(tc >> 3)).v[tc & 7]);
     }
   }
   template <int TM, int TN>
   __device__ __forceinline__ void epilogue(const TileCtx<T>&, const f32x16 (&)[TM][TN], int, int, int) const {}
 };
+
+// lse and loss_rows of the row block from LmceLogitsProblem's [nblk][M]
+// partials: 64 consecutive rows per workgroup; wave w folds the blocks
+// b = w, w + 16, ... of its lane's row in order, eight loads in flight at a time
+// (lanes read consecutive rows: coalesced), then the 16 wave results are folded
+// in wave order.
+constexpr int kCombWaves = 16;
+__global__ __launch_bounds__(64 * kCombWaves) void lmce_combine_cols_kernel(
+    const float2* __restrict__ part, const float* __restrict__ tlogit, const int64_t* __restrict__ tgt, int64_t N,
+    int nblk, int64_t V, int64_t ignore, float* __restrict__ lse, float* __restrict__ loss_rows) {
+  __shared__ float sm[kCombWaves][64], ss[kCombWaves][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 64 + lane;
+  float m = -INFINITY, s = 0.f;
+  if (row < N) {
+    constexpr int U = 8;
+    for (int b0 = w; b0 < nblk; b0 += kCombWaves * U) {
+      float2 p[U];
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        const int b = b0 + kCombWaves * j;
+        p[j] = b < nblk ? part[(int64_t)b * N + row] : make_float2(-INFINITY, 0.f);
+      }
+#pragma unroll
+      for (int j = 0; j < U; ++j) lmce_merge(m, s, p[j].x, p[j].y);
+    }
+  }
+  sm[w][lane] = m;
+  ss[w][lane] = s;
+  __syncthreads();
+  if (w != 0 || row >= N) return;
+  m = sm[0][lane];
+  s = ss[0][lane];
+#pragma unroll
+  for (int i = 1; i < kCombWaves; ++i) lmce_merge(m, s, sm[i][lane], ss[i][lane]);
+  const int64_t t = tgt[row];
+  const float l = m + __logf(s);
+  if (t == ignore) {
+    lse[row] = 0.f;
+    loss_rows[row] = 0.f;
+  } else {
+    lse[row] = l;
+    loss_rows[row] = (t >= 0 && t < V) ? l - tlogit[row] : __int_as_float(0x7fc00000);
+  }
+}
+
+// n_valid = number of targets != ignore (fp32, exact below 2^24 rows).
+__global__ __launch_bounds__(1024) void lmce_count_kernel(const int64_t* __restrict__ tgt, int64_t N, int64_t ignore,
+                                                          float* __restrict__ nvalid_out) {
+  __shared__ float red[16];
+  float n = 0.f;
+  for (int64_t i = threadIdx.x; i < N; i += 1024) n += (tgt[i] != ignore) ? 1.f : 0.f;
+  n = block_sum(n, red);
+  if (threadIdx.x == 0) nvalid_out[0] = n;
+}
 
 // lse[row] from the row's tile partials (tile order), loss_rows[row] =
 // lse - target logit (0 for ignored rows, NaN for targets outside [0, V)).
@@ -1719,45 +1792,74 @@ extern "C" int qh_lmce_fwd(const void* X, int64_t ldx, const void* W, int64_t ld
   return QH_OK;
 }
 
-extern "C" int qh_lmce_grad(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets,
-                            const float* lse, const float* grad_loss, const float* nvalid, int64_t N, int64_t v0,
-                            int64_t Vc, int64_t H, int64_t ignore_index, void* G, int64_t ldg, int dtype,
-                            void* stream) {
-  QH_CHECK_ARG(N >= 0 && Vc > 0 && H > 0 && v0 >= 0 && N < (1ll << 31) && Vc < (1ll << 31) && H < (1ll << 31),
-               "qh_lmce_grad: bad shape");
-  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_lmce_grad: bf16/f16 only");
-  QH_CHECK_ARG(aligned16(X) && aligned16(W) && aligned16(G) && ldx % 8 == 0 && ldw % 8 == 0 && ldg % 8 == 0 &&
-                   H % 8 == 0 && Vc % 8 == 0 && ldx >= H && ldw >= H && ldg >= Vc,
-               "qh_lmce_grad: 16-byte aligned operands with H, Vc, ldx, ldw, ldg multiples of 8 required");
+extern "C" int64_t qh_lmce_rows_workspace(int64_t N, int64_t V) {
+  if (N <= 0 || V <= 0) return 0;
+  return N * ((V + 63) / 64) * 2 * 4 + N * 4;  // 64-column partials, target logits
+}
+
+extern "C" int qh_lmce_rows_fwd(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets,
+                                int64_t N, int64_t V, int64_t H, int64_t ignore_index, void* Z, int64_t ldz, float* lse,
+                                float* loss_rows, void* ws, int64_t ws_bytes, int dtype, void* stream) {
+  QH_CHECK_ARG(N >= 0 && V > 0 && H > 0 && N < (1ll << 31) && V < (1ll << 31) && H < (1ll << 31),
+               "qh_lmce_rows_fwd: bad shape N=%lld V=%lld H=%lld", (long long)N, (long long)V, (long long)H);
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_lmce_rows_fwd: bf16/f16 only");
+  QH_CHECK_ARG(aligned16(X) && aligned16(W) && aligned16(Z) && ldx % 8 == 0 && ldw % 8 == 0 && ldz % 8 == 0 &&
+                   H % 8 == 0 && V % 8 == 0 && ldx >= H && ldw >= H && ldz >= V,
+               "qh_lmce_rows_fwd: 16-byte aligned rows with H, V, ldx, ldw, ldz multiples of 8 required");
+  QH_CHECK_ARG(ws_bytes >= qh_lmce_rows_workspace(N, V), "qh_lmce_rows_fwd: workspace %lld < %lld",
+               (long long)ws_bytes, (long long)qh_lmce_rows_workspace(N, V));
+  QH_CHECK_ARG(lse != nullptr && loss_rows != nullptr, "qh_lmce_rows_fwd: lse and loss_rows are required");
   if (N == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;
+  const int nblk = (int)((V + 63) / 64);
+  float2* part = (float2*)ws;
+  float* tlog = (float*)(part + N * nblk);
   int rc = QH_OK;
-#define QH_LMCEG(TT)                                                                             \
-  {                                                                                              \
-    LmceGradProblem<TT> p;                                                                       \
-    p.X = (const TT*)X;                                                                          \
-    p.W = (const TT*)W + v0 * ldw;                                                               \
-    p.tgt = targets;                                                                             \
-    p.lse = lse;                                                                                 \
-    p.gloss = grad_loss;                                                                         \
-    p.nvalid = nvalid;                                                                           \
-    p.G = (TT*)G;                                                                                \
-    p.ldx = ldx;                                                                                 \
-    p.ldw = ldw;                                                                                 \
-    p.ldg = ldg;                                                                                 \
-    p.v0 = v0;                                                                                   \
-    p.ignore = ignore_index;                                                                     \
-    p.M = (int)N;                                                                                \
-    p.N = (int)Vc;                                                                               \
-    p.K = (int)H;                                                                                \
-    p.tiles_m = (int)((N + 255) / 256);                                                          \
-    p.tiles_n = (int)((Vc + 255) / 256);                                                         \
-    rc = launch_tile<TT, 256, 256, kDenseBK, kDenseNS, false, false>(p, p.tiles_m * p.tiles_n, st, "qh_lmce_grad"); \
+#define QH_LMCER(TT)                                                                               \
+  {                                                                                                \
+    LmceLogitsProblem<TT> p;                                                                       \
+    p.X = (const TT*)X;                                                                            \
+    p.W = (const TT*)W;                                                                            \
+    p.Z = (TT*)Z;                                                                                  \
+    p.tgt = targets;                                                                               \
+    p.part = part;                                                                                 \
+    p.tlogit = tlog;                                                                               \
+    p.ldx = ldx;                                                                                   \
+    p.ldw = ldw;                                                                                   \
+    p.ldz = ldz;                                                                                   \
+    p.M = (int)N;                                                                                  \
+    p.N = (int)V;                                                                                  \
+    p.K = (int)H;                                                                                  \
+    p.tiles_m = (int)((N + 255) / 256);                                                            \
+    p.tiles_n = (int)((V + 255) / 256);                                                            \
+    p.nblk = nblk;                                                                                 \
+    rc = launch_tile<TT, 256, 256, kDenseBK, kDenseNS, false, false>(p, dense_grid(p.tiles_m * p.tiles_n), st, \
+                                                                     "qh_lmce_rows_fwd");          \
   }
-  if (dtype == QH_BF16) QH_LMCEG(bf16_t) else QH_LMCEG(f16_t)
-#undef QH_LMCEG
+  if (dtype == QH_BF16) QH_LMCER(bf16_t) else QH_LMCER(f16_t)
+#undef QH_LMCER
   if (rc) return rc;
-  QH_CHECK_LAUNCH("qh_lmce_grad");
+  lmce_combine_cols_kernel<<<(unsigned)((N + 63) / 64), 64 * kCombWaves, 0, st>>>(part, tlog, targets, N, nblk, V,
+                                                                                   ignore_index, lse, loss_rows);
+  QH_CHECK_LAUNCH("qh_lmce_rows_fwd");
+  return QH_OK;
+}
+
+extern "C" int qh_lmce_count(const int64_t* targets, int64_t N, int64_t ignore_index, float* nvalid_out,
+                             void* stream) {
+  QH_CHECK_ARG(N >= 0 && N < (1ll << 31) && nvalid_out != nullptr, "qh_lmce_count: bad arguments");
+  lmce_count_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(targets, N, ignore_index, nvalid_out);
+  QH_CHECK_LAUNCH("qh_lmce_count");
+  return QH_OK;
+}
+
+extern "C" int qh_lmce_finish(const float* loss_rows, const int64_t* targets, int64_t N, int64_t ignore_index,
+                              float* loss_out, float* nvalid_out, void* stream) {
+  QH_CHECK_ARG(N >= 0 && N < (1ll << 31) && loss_out != nullptr && nvalid_out != nullptr,
+               "qh_lmce_finish: bad arguments");
+  lmce_finalize_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(loss_rows, targets, N, ignore_index, loss_out,
+                                                            nvalid_out);
+  QH_CHECK_LAUNCH("qh_lmce_finish");
   return QH_OK;
 }
 

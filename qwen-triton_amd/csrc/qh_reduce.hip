@@ -522,11 +522,12 @@ __global__ __launch_bounds__(1024) void ce_finalize(const float* __restrict__ lo
   }
 }
 
+// g may be logits itself (same stride): each element is read and then written by one thread.
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void ce_bwd_kernel(const T* __restrict__ logits, int64_t stride,
+__global__ __launch_bounds__(256) void ce_bwd_kernel(const T* logits, int64_t stride,
                                                      const int64_t* __restrict__ tgt, const float* __restrict__ lse,
                                                      const float* __restrict__ gloss, const float* __restrict__ nvalid,
-                                                     T* __restrict__ g, int64_t gstride, int64_t V, int64_t ignore) {
+                                                     T* g, int64_t gstride, int64_t V, int64_t ignore) {
   const int64_t row = blockIdx.x;
   const int64_t t = tgt[row];
   T* gr = g + row * gstride;

@@ -466,8 +466,8 @@ def test_moe_decoder_layer_config4_full_size():
 # ---------------------------------------------------------------------------
 def test_fused_lm_head_cross_entropy_config2_full_size():
     """Loss, dX and dW of fused_linear_cross_entropy at config 2's LM-head shape against fp32 torch
-    (logits in fp32 from the same bf16 inputs) and against the unfused HIP path; each dW row block of a
-    vocabulary chunk is written once, dX accumulates over the 19 chunks in order."""
+    (logits in fp32 from the same bf16 inputs) and against the unfused HIP path; four blocks of 4096
+    rows, each block's logits computed once, dW accumulated over the blocks in order."""
     T, H, V = 16384, 1024, 151936
     x0 = _randn((T, H), 71)
     w0 = _randn((V, H), 72, scale=0.02)
