@@ -20,10 +20,11 @@
 //  * Tile order is XCD-aware: the 8 XCDs each take a contiguous run of tiles
 //    (grouped 8 M-tiles at a time) so operand panels are reused out of the
 //    XCD's own L2.
-//  * M <= 128 (decode, short prefill) uses 1024-thread workgroups of MFMA
-//    16x16x32 whose 16 wavefronts split K, so the weight matrix is requested
-//    in one or two memory round trips; partials are summed through LDS in a
-//    fixed order.
+//  * 4 < M <= 128 (batched decode, short prefill) uses 1024-thread workgroups
+//    of MFMA 16x16x32 over R x 32 or R x 16 tiles whose operands stream
+//    through a ring of LDS stages, 16 wavefronts splitting K into 4 or 16
+//    slices (by K alone) summed through LDS in a fixed order; M <= 4 one
+//    wavefront per output column.
 #include "qh_mfma.h"
 #include "qh_lds.h"
 
@@ -210,49 +211,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const T* __restrict__ A,
 }
 
 // ---------------------------------------------------------------------------
-// Skinny GEMM for M <= 128 (decode), "NN" layout (both operands k-contiguous).
-// MFMA 16x16x32 with operand fragments loaded straight from global memory
-// (the activation rows stay cache-resident; each weight byte is read once).
-// 16x16x32 layout for lane l: A row l%16 / B col l%16 with k = 8*(l/16)+e;
-// C col l%16, rows 4*(l/16)+r.
+// Decode products (M <= 128): the operand set of one launch, the norm fusion
+// parameters, and helpers shared by the batch-1 and the chunked kernels.
 // ---------------------------------------------------------------------------
-// Decode GEMM for M <= 128: one 1024-thread workgroup (16 wavefronts) per
-// 16*CG output columns. The 16 waves form CG column groups x KSP K slices;
-// each wave streams its 16 weight columns over its K slice with every load of
-// a chunk (up to CH 32-wide k-steps) in flight before the first multiply, so
-// a whole layer's weight matrix is requested from memory in one or two round
-// trips. The KSP partial tiles are summed through LDS in slice order
-// (deterministic, no workspace, no cross-workgroup traffic).
-//
-// One launch can serve several products that share the activations A (the
-// q/k/v or gate/up projections of a layer): workgroups are assigned to the
-// products' column tiles in order, each computing exactly what a launch of
-// its own product would. GATED (two products of equal N): every wave
-// multiplies the same A fragments by both weight matrices and the epilogue
-// writes silu(gate) * up, each product rounded to OT first, as separate GEMMs
-// followed by the SiLU-mul kernel would.
-//
-// k mapping per 32-wide step: lane group q = lane / 16 takes k0 + 8 q .. +7,
-// so the four groups of a row read 64 contiguous bytes.
-//
-// NORM: the rows of A are RMSNorm inputs h. The kernel multiplies h by the
-// weight operand round((w + wadd) * B) (the norm weight applied to the weight
-// fragments: 8 NB values per lane and step instead of 8 MT activation values,
-// which every column tile would scale again) and scales each output row by
-// rsqrt(mean_k(h^2) + eps) after the sum over K: RMSNorm followed by the
-// product with the per-row factor moved past the (linear) sum, and one
-// rounding per product term, as the separate norm's normalised operand has.
-// Every workgroup holds all K columns of its rows (its waves' K slices each
-// loaded in one chunk), so the row sums of squares are this lane's pairs
-// (v_dot2), the four lane groups of a row, then the slices in order through
-// LDS in the epilogue; the multiplies never wait for them. NORM modes 2 and 3
-// are the same with the norm weight already folded into B (B = round((w + wadd)
-// * W), made once per weight): the weight fragments are used as loaded and the
-// results equal mode 1's bit for bit. Mode 2 keeps mode 1's one load chunk per K
-// slice (a loop of a run-time chunk count holds more registers and spilled);
-// mode 3 serves the shapes whose slices need several chunks.
-// Residual (per product, optional): C = round(round(product) + R), the
-// residual-add kernel's rounding.
 constexpr int kMaxProducts = 4;
 template <typename T, typename OT>
 struct DecodeProducts {
@@ -272,28 +233,57 @@ struct DecodeNorm {
   int folded;  // 1: the weight is folded into B (row factor only)
 };
 
+// One product's fields as a kernel uses them. Product 0's are read with constant offsets, so
+// the kernel's argument loads are issued together at its start; only a launch of several
+// products looks its product up (a chain of dependent argument loads measured 0.5-0.7 us of a
+// 5-6 us launch). The model's decode launches all have one product (q/k/v concatenated, gate
+// and up as one gated pair).
+template <typename T, typename OT>
+struct ProductView {
+  const T* B;
+  int64_t ldb;
+  int N, first;
+  OT* C;
+  int64_t ldc;
+  const T* bias;
+  const T* res;
+  int64_t ldr;
+};
+template <typename T, typename OT>
+__device__ __forceinline__ ProductView<T, OT> product_view(const DecodeProducts<T, OT>& P, int i) {
+  return ProductView<T, OT>{P.B[i], P.ldb[i], P.N[i], P.tile0[i], P.C[i], P.ldc[i], P.bias[i], P.res[i], P.ldr[i]};
+}
+// Materialises a kernel argument in scalar registers here (the compiler would otherwise sink
+// its load past the first branch that needs it, or merge it into a computed-address load).
+template <typename X>
+__device__ __forceinline__ void sgpr_now(X& x) {
+  asm volatile("" : "+s"(x));
+}
+template <typename T, typename OT>
+__device__ __forceinline__ void sgpr_now(ProductView<T, OT>& v) {
+  sgpr_now(v.B);
+  sgpr_now(v.ldb);
+  sgpr_now(v.N);
+  sgpr_now(v.first);
+  sgpr_now(v.C);
+  sgpr_now(v.ldc);
+  sgpr_now(v.bias);
+  sgpr_now(v.res);
+  sgpr_now(v.ldr);
+}
+// The product of column tile (or column) t: the last i < count with first[i] <= t.
+template <typename T, typename OT>
+__device__ __forceinline__ int product_of(const DecodeProducts<T, OT>& P, int t) {
+  int pi = 0;
+  while (pi + 1 < P.count && t >= P.tile0[pi + 1]) ++pi;
+  return pi;
+}
+
 // NORM template mode: 0 none, 1 weight applied in the kernel, 2 folded into B
 // (3: folded, K slices in several chunks; chosen at launch).
 __host__ __device__ constexpr int decode_norm_mode(const DecodeNorm* n) {
   return n == nullptr ? 0 : (n->folded ? 2 : (n->w != nullptr ? 1 : 0));
 }
-
-// k-steps of 32 whose loads one wave issues together (a NORM launch needs its
-// whole K slice in one chunk). A chunk's activation block (16 MT rows x 32 CH k)
-// is staged in the LDS slot of the wave's K slice: 128 KB / KSP, shared by the
-// slice's 16 / KSP column groups, so MT x CH <= 128 / KSP, with rows of at least
-// 128 bytes (CH >= 2). Weight fragments of a chunk stay in registers (CH x NB).
-constexpr int kDecodeLds = 128 * 1024;
-__host__ __device__ constexpr int decode_chunk(int mt, bool gated, int ksp = 16) {
-  return ksp >= 16 ? (mt == 1 ? (gated ? 4 : 8) : (mt == 2 ? 4 : 2))
-                   : (mt <= 2 ? (gated ? 4 : 8) : (gated ? 4 : (ksp <= 4 ? 8 : 4)));
-}
-// NORM launches: the same chunks.
-__host__ __device__ constexpr int decode_norm_chunk(int mt, bool gated, int ksp = 16) {
-  return decode_chunk(mt, gated, ksp);
-}
-// Longest row a NORM launch normalises.
-constexpr int kDecodeNormMaxK = 8192;
 
 // acc + sum of the squares of 8 packed 16-bit values, two per v_dot2 (fp32 sums).
 template <typename T>
@@ -316,243 +306,6 @@ __device__ __forceinline__ float sumsq8(const typename Mfma<T>::v8& v, float acc
   return acc;
 }
 
-// NTB: weights loaded non-temporally (each weight tile read by one workgroup, ms == 1); with
-// several row groups per column tile the repeat reads should find the tile in the caches.
-template <typename T, typename OT, int MT, int KSP, bool GATED, int NORM, bool NTB = true>
-__global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__ A, int64_t lda,
-                                                           const DecodeProducts<T, OT> P, const DecodeNorm nrm,
-                                                           int M, int K, int kr, int ms, int tiles) {
-  constexpr int CG = 16 / KSP;
-  constexpr bool SCALE = NORM == 1, ROWS = NORM != 0;  // weight scaled here; row factor applied
-  constexpr bool ONE = NORM == 1 || NORM == 2;         // each K slice in one load chunk
-  constexpr int NB = GATED ? 2 : 1;                   // weight matrices per wave
-  constexpr int CH = decode_chunk(MT, GATED, KSP);    // k-steps loaded together
-  typedef typename Mfma<T>::v8 v8;
-  // Activation rows of a chunk: the waves of a K slice DMA its 16 MT x (64 CH
-  // bytes) block into the slice's LDS slot as whole 128-byte lines (a row-per-
-  // lane fragment load would touch 16 half-used lines per instruction, measured
-  // 3-4x slower from L2), 16-byte slots XOR-swizzled per row so the fragment
-  // reads are conflict-free; the slice's CG column groups share the block. The
-  // K-slice sums reuse the slots after a barrier.
-  constexpr int SLOT = kDecodeLds / KSP;  // LDS bytes per K slice
-  constexpr int RB = CH * 64;             // bytes of one activation row in a chunk
-  constexpr int S16 = RB / 16;            // 16-byte slots per row
-  static_assert(MT * 16 * RB <= SLOT && CH >= 2, "activation block exceeds the slice's LDS slot");
-  static_assert(16 * MT * 16 * 16 * 4 <= kDecodeLds, "K-slice sums exceed the slots");
-  __shared__ __align__(16) unsigned char abuf[kDecodeLds];
-  // K-slice partials. MT = 4 (1024 threads for 4 rows per wave per column):
-  // per wave, MT x 64 words of 4 rows (16 i + 4 q .. + 3) of column li, word
-  // i * 64 + q * 16 + li, so a lane writes its 4 rows of a row tile as one
-  // 16-byte word and a summing thread takes 4 outputs. MT < 4: one float per
-  // output, [wave][row][column], and a summing thread takes one output (with 4
-  // outputs per thread too few threads would share the sums).
-  constexpr bool WORDS = MT == 4;
-  f32x4* redw = reinterpret_cast<f32x4*>(abuf);
-  float(*red)[MT * 16][16] = reinterpret_cast<float(*)[MT * 16][16]>(abuf);
-  __shared__ float rfac[ROWS && WORDS ? MT * 16 : 1];
-  __shared__ float nss[ROWS ? 16 : 1][MT * 16];
-  // Workgroup -> (column tile, row group). The ms row groups of a tile get
-  // workgroup ids that are equal mod 8, so they run on one XCD and read the
-  // tile's weights through the same L2.
-  const int bid = (int)blockIdx.x;
-  const int rest = bid >> 3;
-  const int mg = rest % ms;
-  const int gtile = (rest / ms) * 8 + (bid & 7);
-  if (gtile >= tiles) return;
-  const int m0 = mg * MT * 16;
-  int pi = 0;
-  while (pi + 1 < P.count && gtile >= P.tile0[pi + 1]) ++pi;
-  const int tile = gtile - P.tile0[pi];
-  const int N = P.N[pi];
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int cg = wid / KSP, ks = wid % KSP;
-  const int li = lane & 15, q = lane >> 4;
-  const int n = (tile * CG + cg) * 16 + li;
-  const bool nok = n < N;
-  const T* brow[NB];
-#pragma unroll
-  for (int j = 0; j < NB; ++j) brow[j] = P.B[pi + j] + (int64_t)(nok ? n : 0) * P.ldb[pi + j];
-  const int kb = ks * kr, ke = min(K, kb + kr);
-  f32x4 acc[NB][MT];
-#pragma unroll
-  for (int j = 0; j < NB; ++j)
-#pragma unroll
-    for (int i = 0; i < MT; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  v8 zero;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
-  // Every wave runs the same number of chunks (with NORM modes 1 and 2 exactly
-  // one; slices past K load zeros), so all of them reach the barriers.
-  auto swz = [](int r) { return S16 >= 16 ? (r & 15) : ((r >> 1) & 7); };  // slot s of row r: chunk s ^ swz(r)
-  unsigned char* slot = abuf + ks * SLOT;
-  const uint32_t abase = lds_addr(slot);
-  const int nch = ONE ? 1 : (kr + 32 * CH - 1) / (32 * CH);
-  float sq[MT];  // NORM: this lane's row sums of squares (over all its chunks)
-#pragma unroll
-  for (int i = 0; i < MT; ++i) sq[i] = 0.f;
-  for (int ci = 0; ci < nch; ++ci) {
-    const int k0 = kb + ci * 32 * CH;
-    v8 b[CH][NB];
-    v8 wr[SCALE ? CH : 1];  // norm weights (dtype T) of this lane's 8 columns per step
-    if (ci > 0) {  // the previous chunk's fragments have been read from the slot
-      if constexpr (CG > 1) __syncthreads();
-      else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
-#pragma unroll
-    for (int j = cg; j < MT * CH; j += CG) {
-      const int c = j * 64 + lane, r = c / S16;
-      const int m = m0 + r, k = k0 + ((c % S16) ^ swz(r)) * 8;
-      // rows past M and chunks past the slice stage A[0..7] (in bounds; zeroed below)
-      lds_dma16(m < M && k < ke ? A + (int64_t)m * lda + k : A, abase + j * 1024);
-    }
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int k = k0 + u * 32 + q * 8;
-      const bool kok = k < ke;
-      if constexpr (SCALE) wr[u] = kok ? *reinterpret_cast<const v8*>((const T*)nrm.w + k) : zero;
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        // weights read by one workgroup per decode step: non-temporal, so they do not evict cached data
-        if (nok && kok) {
-          if constexpr (NTB) b[u][j] = __builtin_nontemporal_load(reinterpret_cast<const v8*>(brow[j] + k));
-          else b[u][j] = *reinterpret_cast<const v8*>(brow[j] + k);
-        } else {
-          b[u][j] = zero;
-        }
-      }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged rows (untracked DMA) and the weights
-    if constexpr (CG > 1) __syncthreads();             // and the slice's other column groups' rows
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const bool kok = k0 + u * 32 + q * 8 < ke;
-      if constexpr (SCALE) {  // the weight operand round((w + wadd) * B): 8 NB values per lane, not 8 MT
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float wv = to_f32(wr[u][e]) + nrm.wadd;
-#pragma unroll
-          for (int j = 0; j < NB; ++j) b[u][j][e] = from_f32<T>(to_f32(b[u][j][e]) * wv);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const int r = i * 16 + li;
-        v8 a;
-        if (m0 + r < M && kok) a = *reinterpret_cast<const v8*>(slot + r * RB + (((u * 4 + q) ^ swz(r)) << 4));
-        else a = zero;
-        if constexpr (ROWS) sq[i] = sumsq8<T>(a, sq[i]);  // row sums of squares (the epilogue adds the slices)
-#pragma unroll
-        for (int j = 0; j < NB; ++j) acc[j][i] = mma16<T>(a, b[u][j], acc[j][i]);
-      }
-    }
-  }
-  if constexpr (ROWS) {
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      float v = sq[i];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      if (q == 0) nss[wid][i * 16 + li] = v;
-    }
-  }
-  // Sum the K slices in order, one weight matrix at a time through the same
-  // LDS buffer. C layout: column li, rows 16 i + 4 q + r.
-  if constexpr (WORDS) {
-    constexpr int NW4 = MT * 64;  // words per wave
-    float first[(CG * NW4 + 1023) / 1024][4];
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      __syncthreads();  // every wave's fragments (j = 0) or the previous matrix's sums have been read
-#pragma unroll
-      for (int i = 0; i < MT; ++i) redw[wid * NW4 + i * 64 + q * 16 + li] = acc[j][i];
-      if constexpr (ROWS) {  // each row's RMSNorm factor, once (column group 0's slices, in order)
-        if (j == 0 && threadIdx.x < MT * 16) {
-          float ss = 0.f;
-#pragma unroll
-          for (int s2 = 0; s2 < KSP; ++s2) ss += nss[s2][threadIdx.x];
-          rfac[threadIdx.x] = rsqrtf(ss / (float)K + nrm.eps);
-        }
-      }
-      __syncthreads();
-      int slot = 0;
-      for (int idx = threadIdx.x; idx < CG * NW4; idx += 1024, ++slot) {
-        const int g = idx / NW4, rem = idx % NW4;
-        const int col = rem % 16, row0 = (rem / 64) * 16 + ((rem / 16) % 4) * 4;
-        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s2 = 0; s2 < KSP; ++s2) v += redw[(g * KSP + s2) * NW4 + rem];
-        const int gn = (tile * CG + g) * 16 + col;
-        if (gn >= N) continue;
-        const T* bias = P.bias[pi + j];
-        const float bv = bias ? to_f32(bias[gn]) : 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int grow = m0 + row0 + r;
-          if (grow >= M) continue;
-          float val = v[r];
-          if constexpr (ROWS) val *= rfac[row0 + r];
-          val += bv;
-          if constexpr (GATED) {
-            if (j == 0) {
-              first[slot][r] = to_f32(from_f32<OT>(val));
-            } else {
-              const float gt = first[slot][r], up = to_f32(from_f32<OT>(val));
-              P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
-            }
-          } else {
-            OT o = from_f32<OT>(val);
-            const T* res = P.res[pi];
-            if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)grow * P.ldr[pi] + gn]));
-            P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = o;
-          }
-        }
-      }
-    }
-  } else {
-    float first[(CG * MT * 256 + 1023) / 1024];
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      __syncthreads();  // every wave's fragments (j = 0) or the previous matrix's sums have been read
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[wid][i * 16 + q * 4 + r][li] = acc[j][i][r];
-      __syncthreads();
-      int slot = 0;
-      for (int idx = threadIdx.x; idx < CG * MT * 256; idx += 1024, ++slot) {
-        const int g = idx / (MT * 256), rem = idx % (MT * 256);
-        const int row = rem / 16, col = rem % 16;
-        float v = 0.f;
-#pragma unroll
-        for (int s2 = 0; s2 < KSP; ++s2) v += red[g * KSP + s2][row][col];
-        const int gn = (tile * CG + g) * 16 + col;
-        const int grow = m0 + row;
-        if (grow >= M || gn >= N) continue;
-        const T* bias = P.bias[pi + j];
-        if constexpr (ROWS) {  // the row's RMSNorm factor (slices summed in order)
-          float ss = 0.f;
-#pragma unroll
-          for (int s2 = 0; s2 < KSP; ++s2) ss += nss[s2][row];  // column group 0's slices
-          v *= rsqrtf(ss / (float)K + nrm.eps);
-        }
-        const float val = v + (bias ? to_f32(bias[gn]) : 0.f);
-        if constexpr (GATED) {
-          if (j == 0) {
-            first[slot] = to_f32(from_f32<OT>(val));
-          } else {
-            const float gt = first[slot], up = to_f32(from_f32<OT>(val));
-            P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
-          }
-        } else {
-          OT o = from_f32<OT>(val);
-          const T* res = P.res[pi];
-          if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)grow * P.ldr[pi] + gn]));
-          P.C[pi][(int64_t)grow * P.ldc[pi] + gn] = o;
-        }
-      }
-    }
-  }
-}
 
 // Decode products of at most kGemvMaxRows activation rows (batch-1 and small-
 // batch decode): one wavefront per output column of every product, each wave
@@ -594,16 +347,33 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
   constexpr int CH = gemv_chunk(MR, GATED, RC);
   typedef typename Mfma<T>::v8 v8;
   const int lane = threadIdx.x & 63;
+  // P.tile0 holds the first column of each product here; a gated launch has one product
+  ProductView<T, OT> pv = product_view(P, 0);
+  sgpr_now(pv);
+  const T* Bup = P.B[1];  // GATED: the up projection
+  int64_t ldbup = P.ldb[1];
+  const T* biasup = P.bias[1];
+  if constexpr (GATED) {
+    sgpr_now(Bup);
+    sgpr_now(ldbup);
+    sgpr_now(biasup);
+  }
+  int count = P.count;
+  sgpr_now(count);
+  sgpr_now(A);
+  sgpr_now(lda);
   const int col = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * RC;
   if (col >= ncols) return;
-  int pi = 0;  // P.tile0 holds the first column of each product here
-  while (pi + 1 < P.count && col >= P.tile0[pi + 1]) ++pi;
-  const int n = col - P.tile0[pi];
+  if (count > 1) pv = product_view(P, product_of(P, col));
+  const int n = col - pv.first;
+  const int Np = pv.N;
   const T* brow[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
-    const int nj = RC > 1 ? min(n + j, P.N[pi] - 1) : n;  // columns past N re-read the last row
-    brow[j] = P.B[pi + (RC > 1 ? 0 : j)] + (int64_t)nj * P.ldb[pi + (RC > 1 ? 0 : j)];
+    const int nj = RC > 1 ? min(n + j, Np - 1) : n;  // columns past N re-read the last row
+    const T* bj = GATED && j == 1 ? Bup : pv.B;
+    const int64_t lj = GATED && j == 1 ? ldbup : pv.ldb;
+    brow[j] = bj + (int64_t)nj * lj;
   }
   // Bias and residual of the row this lane writes (lane i writes row i), loaded before the
   // weight stream so their latency is not added after the reduction. C may be the residual
@@ -614,12 +384,11 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
   if (lane < MR && lane < M) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const T* bias = P.bias[pi + (RC > 1 ? 0 : j)];
-      if (bias != nullptr) pb[j] = to_f32(bias[RC > 1 ? min(n + j, P.N[pi] - 1) : n]);
+      const T* bias = GATED && j == 1 ? biasup : pv.bias;
+      if (bias != nullptr) pb[j] = to_f32(bias[RC > 1 ? min(n + j, Np - 1) : n]);
       if constexpr (!GATED) {
-        const T* res = P.res[pi];
-        if (res != nullptr && (RC == 1 || n + j < P.N[pi]))
-          pr[j] = to_f32(res[(int64_t)lane * P.ldr[pi] + n + (RC > 1 ? j : 0)]);
+        if (pv.res != nullptr && (RC == 1 || n + j < Np))
+          pr[j] = to_f32(pv.res[(int64_t)lane * pv.ldr + n + (RC > 1 ? j : 0)]);
       }
     }
   }
@@ -684,22 +453,24 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
       if constexpr (ROWS) v[j] *= rsqrtf(ss[i] / (float)K + nrm.eps);
       v[j] += pb[j];
     }
+    OT* const Cp = pv.C;
+    const int64_t ldc = pv.ldc;
     if constexpr (RC > 1) {
-      const bool res = P.res[pi] != nullptr;
+      const bool res = pv.res != nullptr;
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        if (n + j >= P.N[pi]) continue;
+        if (n + j >= Np) continue;
         OT o = from_f32<OT>(v[j]);
         if (res) o = from_f32<OT>(to_f32(o) + pr[j]);
-        P.C[pi][(int64_t)i * P.ldc[pi] + n + j] = o;
+        Cp[(int64_t)i * ldc + n + j] = o;
       }
     } else if constexpr (GATED) {
       const float gt = to_f32(from_f32<OT>(v[0])), up = to_f32(from_f32<OT>(v[1]));
-      P.C[pi][(int64_t)i * P.ldc[pi] + n] = from_f32<OT>(gt * sigmoidf_(gt) * up);
+      Cp[(int64_t)i * ldc + n] = from_f32<OT>(gt * sigmoidf_(gt) * up);
     } else {
       OT o = from_f32<OT>(v[0]);
-      if (P.res[pi] != nullptr) o = from_f32<OT>(to_f32(o) + pr[0]);
-      P.C[pi][(int64_t)i * P.ldc[pi] + n] = o;
+      if (pv.res != nullptr) o = from_f32<OT>(to_f32(o) + pr[0]);
+      Cp[(int64_t)i * ldc + n] = o;
     }
   }
 }
@@ -763,121 +534,354 @@ void launch_gemv_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int
 #undef QH_GV
 }
 
-// Returns QH_E_ARG (nothing launched) when a norm prologue is asked for a
-// shape whose K slices do not fit one load chunk (decode_norm_fits).
-// Launch shape of a decode-kernel launch. K slices per column group (ksp): 4
-// for wide outputs (4 column groups x 4 slices); 8 from 65 rows when 16-column
-// tiles would need more than one workgroup per CU (2 column groups share each
-// slice's activation block: a 128-row q/k/v launch 11.9 us instead of 14.0, gate/
-// up 16.3 instead of 18.0; slower at 1024 columns and at 64 rows); else 16. Row
-// groups per column tile (ms): with few column tiles, up to one workgroup per
-// 16 rows, until about one workgroup per CU.
-struct DecodePlan {
-  int ksp, cols, tiles, kr, ms, mtw;
-  bool norm_fits;
-};
-
-static DecodePlan decode_plan(int M, int K, bool gated, bool norm, int count, const int* N, int ksp_force,
-                              int ms_force) {
-  DecodePlan d{};
-  int maxN = 0;
-  for (int i = 0; i < count; ++i) maxN = N[i] > maxN ? N[i] : maxN;
-  const bool wide = !gated && !norm && maxN > 8192;
-  const int mt = (M + 15) / 16;
-  d.ksp = wide ? 4 : 16;
-  if (!wide && mt > 4) {  // 8 slices when 16-column tiles would need more than one workgroup per CU
-    int t16 = 0;
-    for (int i = 0; i < (gated ? 1 : count); ++i) t16 += (N[i] + 15) / 16;
-    int ms16 = 1;
-    while (ms16 * 4 < mt) ms16 *= 2;
-    if (t16 * ms16 > 256) d.ksp = 8;
+// ---------------------------------------------------------------------------
+// Decode products for 4 < M <= 128 rows (batched decode, short prefill), both
+// operands k-contiguous: one 1024-thread workgroup (16 wavefronts) per tile of
+// R activation rows by C = 32 or 16 weight rows (output columns), all K:
+//  * the tile's operands stream through a ring of NST LDS stages, chunk by
+//    chunk of K: direct-to-LDS loads by the whole workgroup (1 KB per wave and
+//    instruction, whole 128-byte lines), 16-byte slots XOR-swizzled per row so
+//    the fragment reads are conflict-free; NST - 1 chunks are in flight while
+//    one is multiplied, and a chunk's stage is refilled right after the
+//    barrier that follows its last reader;
+//  * per CU this moves R x K activation and C x K weight bytes, with R and C
+//    chosen so that about one workgroup runs per CU (a 64-row q/k/v product:
+//    32 x 32 tiles, 128 KB per CU, where a copy of all 64 rows per 16 weight
+//    columns moved 160 KB);
+//  * the 16 waves are KS K slices x 16 / KS (row group, column block) pairs;
+//    slice s takes the 32-wide MFMA k-steps t = s (mod KS) in increasing order,
+//    then the slices are summed in order through LDS. KS = 4 for K <= 1536,
+//    else 16, so the summation order of every output depends on K alone: the
+//    grouped, gated and single products of one K give equal bits, whatever the
+//    tile shape or the number of columns.
+// Several products sharing A (q/k/v, gate/up) are served by one launch: tiles
+// are dealt to the products' columns in order. GATED (two products of equal N):
+// a tile holds gate and up columns side by side (two column blocks, KS = 4, or
+// the halves of one block, KS = 16) and the epilogue writes silu(gate) * up,
+// each rounded to OT first, as separate products and the SiLU-mul kernel would.
+// NORM: the rows of A are RMSNorm inputs h; the products use the weight
+// operand round((w + wadd) * B) (formed here from the LDS fragments with
+// scale_b, else folded into B beforehand: equal bits) and each output row is
+// scaled by rsqrt(mean_k(h^2) + eps) after the sum over K (the row sums of
+// squares: this lane's pairs by v_dot2, the four lane groups of a row, then
+// the slices in order), then bias. Residual (per product, optional):
+// C = round(round(product) + R), the residual-add kernel's rounding.
+// ---------------------------------------------------------------------------
+template <int N>
+__device__ __forceinline__ void wait_vm_upto(int n) {
+  // wait until at most n vector memory instructions of this wave are in flight (n <= N)
+  if constexpr (N > 0) {
+    if (n >= N) {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(N));
+      return;
+    }
+    wait_vm_upto<N - 1>(n);
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
-  if (!wide && (ksp_force == 8 || ksp_force == 16)) d.ksp = ksp_force;
-  d.cols = 16 * (16 / d.ksp);
-  const int nprod = gated ? 1 : count;  // the gated pair shares its column tiles
-  d.tiles = 0;
-  for (int i = 0; i < nprod; ++i) d.tiles += (N[i] + d.cols - 1) / d.cols;
-  d.kr = ((K + d.ksp - 1) / d.ksp + 31) / 32 * 32;
-  int ms = 1;
-  while (ms * 4 < mt) ms *= 2;  // at most 4 row tiles (64 rows) per workgroup
-  while (ms < mt && d.tiles * ms * 2 <= 256) ms *= 2;
-  if (ms > mt) ms = mt;
-  if (ms_force > 0 && ms_force <= mt) ms = ms_force;
-  d.ms = ms;
-  d.mtw = (mt + ms - 1) / ms;
-  d.norm_fits = K <= kDecodeNormMaxK && d.kr <= 32 * decode_norm_chunk(d.mtw, gated, d.ksp);
-  return d;
 }
 
-// Returns QH_E_ARG (nothing launched) when a norm prologue is asked for a
-// shape whose K slices do not fit one load chunk (decode_norm_fits).
+template <typename T, typename OT, int WR, int KS, int U, int NST, bool GATED, bool NORM>
+__global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__ A, int64_t lda,
+                                                           const DecodeProducts<T, OT> P, const DecodeNorm nrm, int M,
+                                                           int K, int ms, int tiles, int scale_b) {
+  constexpr int NWC = KS == 4 ? 2 : 1;           // 16-column blocks per tile
+  constexpr int NWR = KS == 4 ? 2 : 1;           // row groups of waves
+  constexpr int R = 16 * NWR * WR, C = 16 * NWC;  // tile rows and weight rows
+  constexpr int OC = GATED ? C / 2 : C;           // output columns per tile
+  constexpr int KC = 32 * KS * U;                 // K per chunk
+  constexpr int S16 = KC / 8;                     // 16-byte slots per staged row
+  constexpr int STAGE = (R + C) * KC * 2;
+  constexpr int SLOTS = (R + C) * S16;            // slots per stage
+  constexpr int D = (SLOTS + 1023) / 1024;        // loads per thread and chunk
+  static_assert(S16 >= 16 && SLOTS % 64 == 0, "row swizzle and per-wave loads");
+  static_assert(NST * STAGE <= 144 * 1024, "LDS stages");
+  static_assert(16 * WR * 64 * 16 <= NST * STAGE, "K-slice partials reuse the stages");
+  static_assert(D * (NST - 1) <= 63, "vmcnt");
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ __align__(16) unsigned char smem[NST * STAGE];
+  __shared__ float nss[NORM ? KS : 1][R];  // row sums of squares per K slice
+  // workgroup -> (column tile, row group): the ms row groups of a tile get ids equal mod 8,
+  // so they run on one XCD and read the tile's weights through the same L2
+  ProductView<T, OT> pv = product_view(P, 0);  // a gated launch has one product
+  sgpr_now(pv);
+  const T* Bup = P.B[1];  // GATED: the up projection
+  int64_t ldbup = P.ldb[1];
+  const T* biasup = P.bias[1];
+  int count = P.count;
+  if constexpr (GATED) {
+    sgpr_now(Bup);
+    sgpr_now(ldbup);
+    sgpr_now(biasup);
+  }
+  sgpr_now(count);
+  sgpr_now(A);
+  sgpr_now(lda);
+  const int bid = (int)blockIdx.x;
+  const int rest = bid >> 3;
+  const int mg = rest % ms;
+  const int gtile = (rest / ms) * 8 + (bid & 7);
+  if (gtile >= tiles) return;
+  if (count > 1) pv = product_view(P, product_of(P, gtile));
+  const int tile = gtile - pv.first;
+  const int N = pv.N;
+  const int m0 = mg * R;
+  const int tid = (int)threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int ks = wid % KS, st = wid / KS, rb = st / NWC, cb = st % NWC;
+  const int li = lane & 15, q = lane >> 4;
+  // source row of each of this thread's stage slots (fixed over the chunks): staged rows
+  // 0..R-1 are activation rows (rows past M repeat row M - 1; their outputs are not
+  // stored), R..R+C-1 weight rows (past N: row N - 1)
+  const T* src[D];
+  int soff[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int p = min(d * 1024 + tid, SLOTS - 1);
+    const int r = p / S16;
+    soff[d] = ((p % S16) ^ (r & 15)) * 8;
+    if (r < R) {
+      src[d] = A + (int64_t)min(m0 + r, M - 1) * lda;
+    } else {
+      const int j = r - R;
+      int sel = 0, col;
+      if constexpr (GATED) {
+        sel = j / OC;  // gate rows, then up rows
+        col = tile * OC + j % OC;
+      } else {
+        col = tile * C + j;
+      }
+      const T* bp = GATED && sel ? Bup : pv.B;
+      const int64_t ldbp = GATED && sel ? ldbup : pv.ldb;
+      src[d] = bp + (int64_t)min(col, N - 1) * ldbp;
+    }
+  }
+  const uint32_t sbase = lds_addr(smem);
+  int dw = 0;  // loads this wave issues per chunk (SLOTS is a multiple of 64)
+#pragma unroll
+  for (int d = 0; d < D; ++d) dw += d * 1024 + wid * 64 < SLOTS ? 1 : 0;
+  auto issue = [&](int c) {
+    const int k0 = c * KC;
+    const uint32_t lb = sbase + (uint32_t)((c % NST) * STAGE);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (d * 1024 + wid * 64 < SLOTS) {  // wave-uniform
+        const int k = k0 + soff[d];
+        lds_dma16(src[d] + (k < K ? k : 0), lb + (uint32_t)((d * 1024 + wid * 64) * 16));
+      }
+    }
+  };
+  const int nch = (K + KC - 1) / KC;
+  for (int c = 0; c < min(nch, NST - 1); ++c) issue(c);
+  v8 zero;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) zero[e] = (T)0.f;
+  f32x4 acc[WR];
+  float sq[WR];
+#pragma unroll
+  for (int i = 0; i < WR; ++i) {
+    acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    sq[i] = 0.f;
+  }
+  // NORM with scale_b: the weight row's norm-weight factor per lane (gate and up share it)
+  for (int c = 0; c < nch; ++c) {
+    wait_vm_upto<D * (NST - 2)>(dw * (min(nch, c + NST - 1) - 1 - c));  // chunk c has landed
+    __syncthreads();  // ... for every wave, and chunk c - 1's stage is free
+    if (c + NST - 1 < nch) issue(c + NST - 1);
+    const unsigned char* sp = smem + (c % NST) * STAGE;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int sl = (u * KS + ks) * 4 + q;  // logical slot: k = c KC + 8 sl .. + 7
+      const int k = c * KC + sl * 8;
+      const bool kok = k < K;
+      const int rB = R + cb * 16 + li;
+      v8 b = kok ? *reinterpret_cast<const v8*>(sp + rB * (KC * 2) + ((sl ^ (rB & 15)) << 4)) : zero;
+      if constexpr (NORM) {
+        if (scale_b && kok) {  // round((w + wadd) * B), as the folded weights hold it
+          const v8 w = *reinterpret_cast<const v8*>((const T*)nrm.w + k);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) b[e] = from_f32<T>(to_f32(b[e]) * (to_f32(w[e]) + nrm.wadd));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < WR; ++i) {
+        const int r = (rb * WR + i) * 16 + li;
+        const v8 a = kok ? *reinterpret_cast<const v8*>(sp + r * (KC * 2) + ((sl ^ (r & 15)) << 4)) : zero;
+        if constexpr (NORM) {
+          if (cb == 0) sq[i] = sumsq8<T>(a, sq[i]);
+        }
+        acc[i] = mma16<T>(a, b, acc[i]);
+      }
+    }
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < WR; ++i) {
+      float v = sq[i];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (cb == 0 && q == 0) nss[ks][(rb * WR + i) * 16 + li] = v;
+    }
+  }
+  __syncthreads();  // every wave's fragment reads are done: the partials reuse the stages
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
+#pragma unroll
+  for (int i = 0; i < WR; ++i) red[(wid * WR + i) * 64 + lane] = acc[i];
+  __syncthreads();
+  // element (row group g, column block c, row block i, lane l, row r of the lane's four):
+  // the K slices summed in order
+  auto slice_sum = [&](int g, int c, int i, int l, int r) {
+    float v = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < KS; ++s2) v += red[(((g * NWC + c) * KS + s2) * WR + i) * 64 + l][r];
+    return v;
+  };
+  auto row_factor = [&](int row) {
+    float ss = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < KS; ++s2) ss += nss[s2][row];
+    return rsqrtf(ss / (float)K + nrm.eps);
+  };
+  if constexpr (GATED) {
+    constexpr int E = NWR * WR * (KS == 4 ? 256 : 128);
+    for (int e = tid; e < E; e += 1024) {
+      int g, i, l, lu, cu, oc, r;
+      if constexpr (KS == 4) {  // column block 0 gate, 1 up
+        g = e / (WR * 256);
+        i = (e >> 8) % WR;
+        r = (e >> 6) & 3;
+        l = e & 63;
+        lu = l;
+        cu = 1;
+        oc = l & 15;
+      } else {  // lanes 0-7 of a block gate, 8-15 up
+        g = 0;
+        i = e >> 7;
+        r = (e >> 5) & 3;
+        const int lq = (e >> 3) & 3, lc = e & 7;
+        l = lq * 16 + lc;
+        lu = l + 8;
+        cu = 0;
+        oc = lc;
+      }
+      const int row = (g * WR + i) * 16 + (l >> 4) * 4 + r;
+      const int grow = m0 + row, gn = tile * OC + oc;
+      if (grow >= M || gn >= N) continue;
+      float vg = slice_sum(g, 0, i, l, r), vu = slice_sum(g, cu, i, lu, r);
+      if constexpr (NORM) {
+        const float f = row_factor(row);
+        vg *= f;
+        vu *= f;
+      }
+      const T* bg = pv.bias;
+      const T* bu = biasup;
+      const float gt = to_f32(from_f32<OT>(vg + (bg ? to_f32(bg[gn]) : 0.f)));
+      const float up = to_f32(from_f32<OT>(vu + (bu ? to_f32(bu[gn]) : 0.f)));
+      pv.C[(int64_t)grow * pv.ldc + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
+    }
+  } else {
+    constexpr int E = NWR * NWC * WR * 256;
+    const T* bias = pv.bias;
+    const T* res = pv.res;
+    OT* const Cp = pv.C;
+    const int64_t ldc = pv.ldc, ldr = pv.ldr;
+    for (int e = tid; e < E; e += 1024) {
+      const int g = e / (NWC * WR * 256), c = (e / (WR * 256)) % NWC, i = (e >> 8) % WR;
+      const int r = (e >> 6) & 3, l = e & 63;
+      const int row = (g * WR + i) * 16 + (l >> 4) * 4 + r;
+      const int grow = m0 + row, gn = tile * OC + c * 16 + (l & 15);
+      if (grow >= M || gn >= N) continue;
+      float v = slice_sum(g, c, i, l, r);
+      if constexpr (NORM) v *= row_factor(row);
+      v += bias ? to_f32(bias[gn]) : 0.f;
+      OT o = from_f32<OT>(v);
+      if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)grow * ldr + gn]));
+      Cp[(int64_t)grow * ldc + gn] = o;
+    }
+  }
+}
+
+// Launch shape: K slices (4 or 16, by K alone), rows per tile (R = 16 x NWR x WR), row groups
+// per column tile (ms, until about one workgroup per CU), and the chunk ring (U k-steps per
+// slice and chunk, NST stages of at most 48 KB).
+struct DecodePlan {
+  int ks, wr, ms, oc, tiles;
+};
+
+static DecodePlan decode_plan(int M, int K, bool gated, int count, const int* N) {
+  DecodePlan p{};
+  p.ks = K <= 1536 ? 4 : 16;
+  const int nwr = p.ks == 4 ? 2 : 1, c = p.ks == 4 ? 32 : 16;
+  const int wrmax = p.ks == 4 ? 4 : 2;
+  p.oc = gated ? c / 2 : c;
+  p.tiles = 0;
+  for (int i = 0; i < (gated ? 1 : count); ++i) p.tiles += (N[i] + p.oc - 1) / p.oc;
+  const int mtu = (M + 16 * nwr - 1) / (16 * nwr);
+  int ms = 1;
+  while ((mtu + ms - 1) / ms > wrmax) ms *= 2;
+  while (ms < mtu && p.tiles * ms * 2 <= 256) ms *= 2;
+  const int wr = (mtu + ms - 1) / ms;
+  p.wr = wr <= 1 ? 1 : (wr <= 2 ? 2 : 4);
+  p.ms = ms;
+  return p;
+}
+
 template <typename T, typename OT>
 int launch_decode_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int M, int K, bool gated,
-                           hipStream_t st, int ms_force = 0, const DecodeNorm* nrm = nullptr, int ksp_force = 0) {
+                           hipStream_t st, const DecodeNorm* nrm = nullptr) {
   const int nmode = decode_norm_mode(nrm);
   const bool norm = nmode != 0;
-  if (M <= kGemvMaxRows && ms_force == 0 && ksp_force == 0) {
-    if (norm && !std::is_same<T, OT>::value) return QH_E_ARG;
-    launch_gemv_products<T, OT>(a, lda, P, M, K, gated, norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f, 0}, st);
+  if (norm && !std::is_same<T, OT>::value) return QH_E_ARG;
+  const DecodeNorm nz = norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f, 0};
+  if (M <= kGemvMaxRows) {
+    launch_gemv_products<T, OT>(a, lda, P, M, K, gated, nz, st);
     return QH_OK;
   }
-  // modes 1 and 2 load each K slice in one chunk; folded weights whose slices do not fit
-  // one chunk take the plain plan (mode 3)
-  DecodePlan d = decode_plan(M, K, gated, nmode != 0, P.count, P.N, ksp_force, ms_force);
-  int kmode = nmode;
-  if (nmode == 2 && !d.norm_fits) {
-    d = decode_plan(M, K, gated, false, P.count, P.N, ksp_force, ms_force);
-    kmode = 3;
-  }
+  const DecodePlan d = decode_plan(M, K, gated, P.count, P.N);
   const int nprod = gated ? 1 : P.count;
   P.tile0[0] = 0;
-  for (int i = 0; i < nprod; ++i) P.tile0[i + 1] = P.tile0[i] + (P.N[i] + d.cols - 1) / d.cols;
+  for (int i = 0; i < nprod; ++i) P.tile0[i + 1] = P.tile0[i] + (P.N[i] + d.oc - 1) / d.oc;
   if (gated) P.count = 1;
-  const int tiles = d.tiles, kr = d.kr, ms = d.ms, mtw = d.mtw, ksp = d.ksp;
-  const int grid = (tiles + 7) / 8 * 8 * ms;
-  if (nmode == 1 && !d.norm_fits) return QH_E_ARG;
-  const DecodeNorm nz = norm ? *nrm : DecodeNorm{nullptr, 0.f, 0.f, 0};
-  constexpr bool kNormOk = std::is_same<T, OT>::value;  // the only instantiation a norm launch reaches
-  if (norm && !kNormOk) return QH_E_ARG;
-#define QH_DG(MTV, KSPV, GV, NV)                                                                        \
-  do {                                                                                                 \
-    if (ms == 1) gemm_decode_kernel<T, OT, MTV, KSPV, GV, NV, true><<<grid, 1024, 0, st>>>(a, lda, P, nz, M, K, kr, ms, tiles); \
-    else gemm_decode_kernel<T, OT, MTV, KSPV, GV, NV, false><<<grid, 1024, 0, st>>>(a, lda, P, nz, M, K, kr, ms, tiles); \
-  } while (0)
-#define QH_DG_K(MTV, GV, NV) \
-  if (ksp == 8) QH_DG(MTV, 8, GV, NV); else QH_DG(MTV, 16, GV, NV);
-#define QH_DG_W(MTV)                                           \
-  if constexpr (kNormOk) {                                     \
-    if (nmode == 1) {                                          \
-      if (gated) { QH_DG_K(MTV, true, 1) } else { QH_DG_K(MTV, false, 1) } \
-      return QH_OK;                                            \
-    }                                                          \
-    if (kmode == 2) {                                          \
-      if (gated) { QH_DG_K(MTV, true, 2) } else { QH_DG_K(MTV, false, 2) } \
-      return QH_OK;                                            \
-    }                                                          \
-    if (kmode == 3) {                                          \
-      if (gated) { QH_DG_K(MTV, true, 3) } else { QH_DG_K(MTV, false, 3) } \
-      return QH_OK;                                            \
-    }                                                          \
-  }                                                            \
-  if (gated) { QH_DG_K(MTV, true, 0) }                         \
-  else if (ksp == 4) QH_DG(MTV, 4, false, 0);                  \
-  else { QH_DG_K(MTV, false, 0) }
-  if (mtw == 1) { QH_DG_W(1) } else if (mtw == 2) { QH_DG_W(2) } else if (mtw == 3) { QH_DG_W(3) } else { QH_DG_W(4) }
-#undef QH_DG_W
-#undef QH_DG_K
-#undef QH_DG
+  const int grid = (d.tiles + 7) / 8 * 8 * d.ms;
+  const int scale_b = nmode == 1 ? 1 : 0;
+  // (WR, KS, U, NST): stages of 32 x 32 + 32 rows x 256 k (32 KB), 64 + 32 x 256 (48 KB),
+  // 128 + 32 x 128 (40 KB), 16 + 16 x 512 (32 KB), 32 + 16 x 512 (48 KB)
+#define QH_DK(WRV, KSV, UV, NSTV, GV, NV)                                                     \
+  gemm_decode_kernel<T, OT, WRV, KSV, UV, NSTV, GV, NV><<<grid, 1024, 0, st>>>(a, lda, P, nz, M, K, d.ms, \
+                                                                               d.tiles, scale_b)
+#define QH_DK_S(GV, NV)                                               \
+  if (d.ks == 4) {                                                    \
+    if (d.wr == 1) QH_DK(1, 4, 2, 4, GV, NV);                         \
+    else if (d.wr == 2) QH_DK(2, 4, 2, 3, GV, NV);                    \
+    else QH_DK(4, 4, 1, 3, GV, NV);                                   \
+  } else {                                                            \
+    if (d.wr == 1) QH_DK(1, 16, 1, 4, GV, NV);                        \
+    else QH_DK(2, 16, 1, 3, GV, NV);                                  \
+  }
+  if constexpr (std::is_same<T, OT>::value) {
+    if (gated) {
+      if (norm) { QH_DK_S(true, true) } else { QH_DK_S(true, false) }
+      return QH_OK;
+    }
+    if (norm) {
+      QH_DK_S(false, true)
+      return QH_OK;
+    }
+  }
+  QH_DK_S(false, false)
+#undef QH_DK_S
+#undef QH_DK
   return QH_OK;
 }
 
-// Whether a norm-prologue launch of M rows, K columns fits (all K slices of
-// every workgroup loaded in one chunk); mirrors launch_decode_products.
+// A norm-prologue launch fits every shape qh_gemm_multi takes (M <= 128): the batch-1 kernel
+// and the chunked kernel both sum the squares over any K.
 static bool decode_norm_fits(int M, int K, bool gated, int count, const int64_t* N) {
-  if (M <= kGemvMaxRows) return true;  // the one-wave-per-column kernel normalises any K
-  int n32[kMaxProducts];
-  for (int i = 0; i < count && i < kMaxProducts; ++i) n32[i] = (int)N[i];
-  return decode_plan(M, K, gated, true, count, n32, 0, 0).norm_fits;
+  (void)M;
+  (void)K;
+  (void)gated;
+  (void)count;
+  (void)N;
+  return true;
 }
 
 template <typename T, typename OT>
@@ -1285,7 +1289,7 @@ extern "C" int qh_gemm_multi_ex(int64_t M, int64_t K, const void* A, int64_t lda
       P.N[i] = (int)N[i];                                                                               \
     }                                                                                                   \
     P.count = count;                                                                                    \
-    rc = launch_decode_products<T, T>((const T*)A, lda, P, (int)M, (int)K, gated != 0, st, 0, &nrm);   \
+    rc = launch_decode_products<T, T>((const T*)A, lda, P, (int)M, (int)K, gated != 0, st, &nrm);   \
   }
   if (dtype == QH_BF16) QH_MULTI(bf16_t) else QH_MULTI(f16_t)
 #undef QH_MULTI
@@ -1328,7 +1332,7 @@ extern "C" int qh_gemm_multi_rms(int64_t M, int64_t K, const void* A, int64_t ld
       P.N[i] = (int)N[i];                                                                               \
     }                                                                                                   \
     P.count = count;                                                                                    \
-    rc = launch_decode_products<T, T>((const T*)A, lda, P, (int)M, (int)K, gated != 0, st, 0, &nrm);   \
+    rc = launch_decode_products<T, T>((const T*)A, lda, P, (int)M, (int)K, gated != 0, st, &nrm);   \
   }
   if (dtype == QH_BF16) QH_MULTI(bf16_t) else QH_MULTI(f16_t)
 #undef QH_MULTI
