@@ -340,7 +340,7 @@ constexpr int kGemvTwoColMin = 4096;
 template <typename T, typename OT, int MR, bool GATED, int NORM, int RC = 1>
 __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ A, int64_t lda,
                                                           const DecodeProducts<T, OT> P, const DecodeNorm nrm, int M,
-                                                          int K, int ncols) {
+                                                          int K, int ncols, int count) {
   static_assert(RC == 1 || !GATED, "a wave takes several columns of non-gated products only");
   constexpr bool SCALE = NORM == 1, ROWS = NORM != 0;  // activation scaled here; row factor applied
   constexpr int NB = GATED ? 2 : RC;
@@ -358,7 +358,8 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
     sgpr_now(ldbup);
     sgpr_now(biasup);
   }
-  int count = P.count;
+  // count (= P.count) is a direct argument: the trailing ints then fill the 16-byte argument
+  // load they share, so no other argument is loaded into its padding register (after a wait)
   sgpr_now(count);
   sgpr_now(A);
   sgpr_now(lda);
@@ -497,7 +498,7 @@ void launch_gemv_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int
   }
   if (rc > 1) {
     const unsigned grid = (unsigned)((ncols + 4 * rc - 1) / (4 * rc));
-#define QH_GR(MRV, NV, RCV) gemv_decode_kernel<T, OT, MRV, false, NV, RCV><<<grid, 256, 0, st>>>(a, lda, P, nz, M, K, ncols)
+#define QH_GR(MRV, NV, RCV) gemv_decode_kernel<T, OT, MRV, false, NV, RCV><<<grid, 256, 0, st>>>(a, lda, P, nz, M, K, ncols, P.count)
 #define QH_GW(MRV, NV) \
   if (rc == 2) QH_GR(MRV, NV, 2); else QH_GR(MRV, NV, kGemvWideCols);
     if constexpr (std::is_same<T, OT>::value) {
@@ -516,7 +517,7 @@ void launch_gemv_products(const T* a, int64_t lda, DecodeProducts<T, OT>& P, int
     return;
   }
   const unsigned grid = (unsigned)((ncols + 3) / 4);
-#define QH_GV(MRV, GV, NV) gemv_decode_kernel<T, OT, MRV, GV, NV><<<grid, 256, 0, st>>>(a, lda, P, nz, M, K, ncols)
+#define QH_GV(MRV, GV, NV) gemv_decode_kernel<T, OT, MRV, GV, NV><<<grid, 256, 0, st>>>(a, lda, P, nz, M, K, ncols, P.count)
 #define QH_GV_M(MRV)                                                      \
   if constexpr (std::is_same<T, OT>::value) {                             \
     if (nmode == 1) {                                                     \
