@@ -253,14 +253,8 @@ template <typename T, typename OT>
 __device__ __forceinline__ ProductView<T, OT> product_view(const DecodeProducts<T, OT>& P, int i) {
   return ProductView<T, OT>{P.B[i], P.ldb[i], P.N[i], P.tile0[i], P.C[i], P.ldc[i], P.bias[i], P.res[i], P.ldr[i]};
 }
-// Materialises a kernel argument in scalar registers here (the compiler would otherwise sink
-// its load past the first branch that needs it, or merge it into a computed-address load).
-template <typename X>
-__device__ __forceinline__ void sgpr_now(X& x) {
-  asm volatile("" : "+s"(x));
-}
 template <typename T, typename OT>
-__device__ __forceinline__ void sgpr_now(ProductView<T, OT>& v) {
+__device__ __forceinline__ void view_now(ProductView<T, OT>& v) {
   sgpr_now(v.B);
   sgpr_now(v.ldb);
   sgpr_now(v.N);
@@ -349,7 +343,7 @@ __global__ __launch_bounds__(256) void gemv_decode_kernel(const T* __restrict__ 
   const int lane = threadIdx.x & 63;
   // P.tile0 holds the first column of each product here; a gated launch has one product
   ProductView<T, OT> pv = product_view(P, 0);
-  sgpr_now(pv);
+  view_now(pv);
   const T* Bup = P.B[1];  // GATED: the up projection
   int64_t ldbup = P.ldb[1];
   const T* biasup = P.bias[1];
@@ -605,7 +599,7 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   // workgroup -> (column tile, row group): the ms row groups of a tile get ids equal mod 8,
   // so they run on one XCD and read the tile's weights through the same L2
   ProductView<T, OT> pv = product_view(P, 0);  // a gated launch has one product
-  sgpr_now(pv);
+  view_now(pv);
   const T* Bup = P.B[1];  // GATED: the up projection
   int64_t ldbup = P.ldb[1];
   const T* biasup = P.bias[1];
