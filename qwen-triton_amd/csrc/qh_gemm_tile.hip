@@ -1124,14 +1124,23 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float* __restrict__ P
   }
 }
 
-// Splits for a dense product (1 = no split): few 256x256 tiles and long K.
+// Splits for a dense product (1 = no split): fewer 256x256 tiles than one round of workgroups
+// (256) and long K. Each split's K range is at least 1024; the count is the smallest that fills
+// the rounds it needs within 10% of the best fill up to 16 splits (a 128-tile product with
+// K = 151936, the LM head's input gradient for 8192 rows, ran on half the CUs unsplit: 3.26 ms).
 inline int splitk_count(int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
-  if (M < 256 || N < 256 || tiles >= 128 || K < 2048) return 1;
-  int64_t s = (384 + tiles - 1) / tiles;
-  if (s > K / 1024) s = K / 1024;
-  if (s > 16) s = 16;
-  return s < 2 ? 1 : (int)s;
+  if (M < 256 || N < 256 || tiles >= 256 || K < 2048) return 1;
+  const int64_t smax = K / 1024 < 16 ? K / 1024 : 16;
+  auto fill = [&](int64_t s) {
+    const int64_t w = s * tiles;
+    return (double)w / (double)(((w + 255) / 256) * 256);
+  };
+  double best = 0.0;
+  for (int64_t s = 1; s <= smax; ++s) best = fill(s) > best ? fill(s) : best;
+  for (int64_t s = 1; s <= smax; ++s)
+    if (fill(s) >= 0.9 * best && s * tiles >= 192) return (int)s;
+  return (int)smax;
 }
 
 template <typename T, typename OT, bool AT, bool BT>
