@@ -267,6 +267,15 @@ struct TileGatherA : std::false_type {};
 template <class P>
 struct TileGatherA<P, std::void_t<decltype(P::kGatherA)>> : std::integral_constant<bool, P::kGatherA> {};
 
+// Problems that define kSkipRows = true (grouped products whose segments leave
+// partial M-tiles) skip the fragment reads and MFMAs of a wavefront's 32-row
+// blocks that hold no valid row: a nearly empty tail tile of an expert then
+// costs its loads, not a full tile's products.
+template <class P, class = void>
+struct TileSkipRows : std::false_type {};
+template <class P>
+struct TileSkipRows<P, std::void_t<decltype(P::kSkipRows)>> : std::integral_constant<bool, P::kSkipRows> {};
+
 template <typename T, int BM, int BN, int BK, int NS, bool AT, bool BT, class P>
 __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
   using TA = OpTile<T, BM, BK, AT>;
@@ -349,17 +358,23 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
     }
   };
   V8<T> af[2][TM], bf[2][TN];
-  auto read = [&](const T* S, int kk, int b) {
+  constexpr bool kSkip = TileSkipRows<P>::value;
+  int live = TM;  // kSkip: this wavefront's 32-row blocks with a valid row (set per tile)
+  // sk: std::true_type for the copy of the k-loop that runs partial tiles
+  // (branches on live), std::false_type for the branch-free full-tile copy
+  auto read = [&](auto sk, const T* S, int kk, int b) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) af[b][i] = TA::frag(S, wm * WTM + 32 * i, kk);
+    for (int i = 0; i < TM; ++i)
+      if (!decltype(sk)::value || i < live) af[b][i] = TA::frag(S, wm * WTM + 32 * i, kk);
 #pragma unroll
     for (int j = 0; j < TN; ++j) bf[b][j] = TB::frag(S + TA::ELEMS, wn * WTN + 32 * j, kk);
   };
-  auto mma = [&](int b) {
+  auto mma = [&](auto sk, int b) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
+      if (!decltype(sk)::value || i < live)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af[b][i], bf[b][j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<T>::mma(af[b][i], bf[b][j], acc[i][j]);
   };
   bool warm = false;  // k-tile 0 of c was issued during the previous tile's epilogue
   for (;;) {
@@ -367,6 +382,10 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = zero16();
+    if constexpr (kSkip) {
+      const int lr = c.vm - wm * WTM;  // valid rows from this wavefront's first row
+      live = __builtin_amdgcn_readfirstlane(lr <= 0 ? 0 : (lr >= WTM ? TM : (lr + 31) / 32));
+    }
     const int nk = (c.K + BK - 1) / BK;
     // Tiles 0 .. NS-1 fill every stage. After the barrier that lands tile kt+1,
     // every wave has finished reading tile kt (its last fragments were read
@@ -382,28 +401,32 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
         for (int t = 0; t < pro; ++t) issue(t);
         land(0, pro - 1);
       }
-      read(stage(0), 0, 0);
     }
-    for (int kt = 0; kt < nk; ++kt) {
-      // steps 0 .. KS-2 of tile kt, each overlapping the next step's reads
+    auto kloop = [&](auto sk) {
+      if (nk > 0) read(sk, stage(0), 0, 0);
+      for (int kt = 0; kt < nk; ++kt) {
+        // steps 0 .. KS-2 of tile kt, each overlapping the next step's reads
 #pragma unroll
-      for (int st = 0; st + 1 < KS; ++st) {
-        read(stage(kt), st + 1, (st + 1) & 1);
-        mma(st & 1);
+        for (int st = 0; st + 1 < KS; ++st) {
+          read(sk, stage(kt), st + 1, (st + 1) & 1);
+          mma(sk, st & 1);
+          mma_schedule<ND, NM * 3 / 4>(std::make_integer_sequence<int, NM>{});
+        }
+        if (kt + 1 < nk) {
+          // tiles issued so far: 0 .. min(kt + NS - 1, nk - 1)
+          const int issued = kt + NS - 1 < nk - 1 ? kt + NS - 1 : nk - 1;
+          land(kt + 1, issued - (kt + 1));
+          if (kt + NS < nk) issue(kt + NS);  // into the stage tile kt used
+        }
+        // last step of tile kt; the next tile's first fragments are read meanwhile
+        // (after the last tile this reads an unused stage, harmlessly)
+        read(sk, stage(kt + 1), 0, 0);
+        mma(sk, (KS - 1) & 1);
         mma_schedule<ND, NM * 3 / 4>(std::make_integer_sequence<int, NM>{});
       }
-      if (kt + 1 < nk) {
-        // tiles issued so far: 0 .. min(kt + NS - 1, nk - 1)
-        const int issued = kt + NS - 1 < nk - 1 ? kt + NS - 1 : nk - 1;
-        land(kt + 1, issued - (kt + 1));
-        if (kt + NS < nk) issue(kt + NS);  // into the stage tile kt used
-      }
-      // last step of tile kt; the next tile's first fragments are read meanwhile
-      // (after the last tile this reads an unused stage, harmlessly)
-      read(stage(kt + 1), 0, 0);
-      mma((KS - 1) & 1);
-      mma_schedule<ND, NM * 3 / 4>(std::make_integer_sequence<int, NM>{});
-    }
+    };
+    if (kSkip && live < TM) kloop(std::integral_constant<bool, kSkip>{});
+    else kloop(std::false_type{});
     if constexpr (!kPersist) {
       break;
     } else {
@@ -716,6 +739,7 @@ __device__ __forceinline__ bool seg_tile(const int32_t* seg, const int32_t* toff
 template <typename T, bool GA = false>
 struct MoeUpProblem {
   static constexpr bool kGatherA = GA;
+  static constexpr bool kSkipRows = true;
   const T* X;
   const int32_t* rows;  // GA: token row of each sorted row
   const T* const* Wt;  // 2E pointers: gate_e, up_e
@@ -813,6 +837,7 @@ struct MoeUpProblem {
 //      and s = sigmoid(g): C = go u s (1 + g (1 - s)), C2 = go g s
 template <typename T, bool BT, int EPI>
 struct MoeRowProblem {
+  static constexpr bool kSkipRows = true;
   const T* A;
   const T* const* Wt;  // E pointers
   T* C;
@@ -919,6 +944,7 @@ struct MoeRowProblem {
 // [Wg_e ; Wu_e] (K = 2I; I is a multiple of 64 so no k-tile straddles).
 template <typename T>
 struct MoeDxProblem {
+  static constexpr bool kSkipRows = true;
   const T *dG, *dU;
   const T* const* Wt;  // 2E pointers: gate_e, up_e ([I, H] each)
   T* C;
