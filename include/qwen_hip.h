@@ -111,10 +111,12 @@ int qh_embedding_fwd(const int64_t* ids, const void* w, int64_t stride_w, void* 
 /* Workspace bytes of qh_embedding_bwd: id sort space for n_tokens. */
 int64_t qh_embedding_bwd_workspace(int64_t n_tokens, int64_t V);
 /* gw[v,:] = sum_{t: ids[t]==v} gout[t,:] (fp32 sum in token order, stored as
- * wdtype), gw[padding_idx] = 0; rows never referenced are zero. Deterministic
- * (radix sort by id, then each referenced row written once with its ordered
- * sum, the others with zeros; a wave walks a range of rows and the sorted ids
- * together, so no per-row table is built).
+ * wdtype), gw[padding_idx] = 0; rows never referenced are zero; ids outside
+ * [0, V) contribute nothing. Deterministic: every row is written once. Up to
+ * 32768 tokens (with Hd a multiple of 8 and 16-byte aligned buffers) in one
+ * launch without a sort: workgroup g of G owns the rows v = g mod G and keeps
+ * the position-ordered list of its hits in LDS; above that, a radix sort by id
+ * first. The workspace is the sort's (unused by the single launch).
  * Replaces qwen_triton/kernels/embedding.py:78-94 (_embedding_backward_kernel), :124-145. */
 int qh_embedding_bwd(const int64_t* ids, const void* gout, void* gw, void* ws, int64_t ws_bytes,
                      int64_t n_tokens, int64_t V, int64_t Hd, int64_t padding_idx, int gdtype,

@@ -1,9 +1,12 @@
 // Deterministic scatter-add operators: embedding backward and index_add.
 //
-// Instead of float atomics (whose summation order depends on timing), the
-// (row-index, source-position) pairs are sorted with a stable LSD radix sort
-// (rocPRIM) and each destination row is produced by exactly one workgroup that
-// sums its sources in source order in fp32 and rounds once.
+// Instead of float atomics (whose summation order depends on timing), every
+// destination row is produced by exactly one wave (or, for the slices of a hot
+// embedding row, one wave per column slice) that sums its sources in source order
+// in fp32 and rounds once. The embedding backward of up to 32768 tokens finds each
+// workgroup's sources in LDS without a sort (embedding_bwd_interleaved); larger
+// token counts and index_add sort the (row-index, source-position) pairs with a
+// stable LSD radix sort (rocPRIM) first.
 #include <algorithm>
 #include <cstring>
 #include <rocprim/rocprim.hpp>
@@ -193,6 +196,265 @@ __global__ __launch_bounds__(256) void embedding_rows_roles(const uint32_t* __re
   }
 }
 
+// Row pieces of VN elements for the single-launch embedding backward (16-byte aligned pieces of
+// 8, naturally aligned pieces of 2).
+template <typename T, int VN>
+struct EmbPiece {
+  static constexpr int B = VN * (int)sizeof(T);
+  union {
+    T v[VN];
+    uint32_t w[B >= 4 ? B / 4 : 1];
+  };
+};
+
+template <typename T, int VN>
+__device__ __forceinline__ EmbPiece<T, VN> emb_load(const T* p) {
+  EmbPiece<T, VN> r;
+  constexpr int B = EmbPiece<T, VN>::B;
+  if constexpr (B % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 16; ++i) {
+      const uint4 x = reinterpret_cast<const uint4*>(p)[i];
+      r.w[4 * i] = x.x, r.w[4 * i + 1] = x.y, r.w[4 * i + 2] = x.z, r.w[4 * i + 3] = x.w;
+    }
+  } else if constexpr (B == 8) {
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = x.x, r.w[1] = x.y;
+  } else if constexpr (B == 4) {
+    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else {
+    r.v[0] = *p;
+  }
+  return r;
+}
+
+typedef unsigned int qh_u32x2 __attribute__((ext_vector_type(2)));
+
+template <typename T, int VN>
+__device__ __forceinline__ void emb_store_nt(T* p, const float (&o)[VN]) {
+  EmbPiece<T, VN> u;
+#pragma unroll
+  for (int k = 0; k < VN; ++k) u.v[k] = from_f32<T>(o[k]);
+  constexpr int B = EmbPiece<T, VN>::B;
+  if constexpr (B % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < B / 16; ++i) {
+      const qh_u32x4 x = {u.w[4 * i], u.w[4 * i + 1], u.w[4 * i + 2], u.w[4 * i + 3]};
+      __builtin_nontemporal_store(x, reinterpret_cast<qh_u32x4*>(p) + i);
+    }
+  } else if constexpr (B == 8) {
+    const qh_u32x2 x = {u.w[0], u.w[1]};
+    __builtin_nontemporal_store(x, reinterpret_cast<qh_u32x2*>(p));
+  } else if constexpr (B == 4) {
+    __builtin_nontemporal_store(u.w[0], reinterpret_cast<uint32_t*>(p));
+  } else {
+    uint16_t h;
+    __builtin_memcpy(&h, &u.v[0], 2);
+    __builtin_nontemporal_store(h, reinterpret_cast<uint16_t*>(p));
+  }
+}
+
+// Embedding weight gradient in one launch, without a sort, for up to kEmbLdsTokens tokens.
+// Workgroup g of G (a power of two) owns the rows v with v mod G = g, as local rows v / G. The
+// interleave spreads the low ids, which BPE vocabularies give their most frequent tokens, over
+// all workgroups.
+// 1. Its threads read every token id once (coalesced) and stage, per position, an LDS entry
+//    local_row << 16 | position for the tokens that hit its rows (none for ids outside [0, V)
+//    and for the padding row), and count the hits per row.
+// 2. A stable compaction turns the staged entries into the position-ordered list of hits: each
+//    thread counts the hits of a contiguous block of positions, a block-wide exclusive scan
+//    gives its offset. Wave 0 meanwhile lists the hit rows in two classes by hit count.
+// 3. Every row of the workgroup is written once. The first kEmbZeroWaves waves write zeros to
+//    the rows no token hits (16-byte non-temporal stores). The other waves take work items from
+//    an LDS queue: first the kEmbHotCols-column slices of the rows with at least kEmbHot hits,
+//    then the other hit rows whole. An item walks the list (64 entries per LDS read) and adds
+//    the matching tokens' gradient rows in position order (fp32, rounded once), the loads of up
+//    to U tokens in flight; a hot row's tokens so run as kEmbHotCols-column chains on several
+//    waves at once. The zero waves join the queue when their rows are done.
+// The sums and the rounding are those of the sorted form: the result is the same bit for bit.
+constexpr int kEmbThreads = 1024, kEmbWaves = kEmbThreads / 64, kEmbZeroWaves = 12;
+constexpr int kEmbIdsPerThread = 32;
+constexpr int64_t kEmbLdsTokens = (int64_t)kEmbThreads * kEmbIdsPerThread;  // positions fit 16 bits
+constexpr int kEmbMaxRows = 2048;  // local rows per workgroup
+constexpr int kEmbHot = 32, kEmbHotVN = 2, kEmbHotU = 32;  // hot-row slices: 64 lanes x 2 columns
+constexpr int kEmbHotCols = 64 * kEmbHotVN;
+
+// acc[k][.] += the rows of the list's tokens on local row r, in list order, at the VN columns
+// c + 64 VN k of this lane (columns at or past D are skipped); U tokens per batch of loads.
+template <int VN, int NCH, int U, typename S>
+__device__ __forceinline__ void emb_sum(const uint32_t* list, int L, uint32_t r, const S* __restrict__ src, int D,
+                                        int c, float (&acc)[NCH][VN]) {
+  const int lane = threadIdx.x & 63;
+  for (int p = 0; p < L; p += 64) {
+    const uint32_t e = p + lane < L ? list[p + lane] : 0xffffffffu;
+    uint64_t mk = __ballot(e >> 16 == r);
+    while (mk) {
+      int pos[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        pos[u] = -1;
+        if (mk) {
+          const int j = __builtin_ctzll(mk);
+          mk &= mk - 1;
+          pos[u] = __builtin_amdgcn_readlane((int)e, j) & 0xffff;
+        }
+      }
+      // Every load is issued, unconditionally, before the first add: an empty slot re-reads the
+      // batch's first row and a column at or past D reads column 0 (neither is stored), and an
+      // empty slot adds +0, which leaves an fp32 sum that starts at +0 unchanged bit for bit.
+      EmbPiece<S, VN> t[U][NCH];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+          const int col = c + 64 * VN * k;
+          t[u][k] = emb_load<S, VN>(src + (int64_t)(pos[u] >= 0 ? pos[u] : pos[0]) * D + (col < D ? col : 0));
+        }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < NCH; ++k)
+#pragma unroll
+          for (int q = 0; q < VN; ++q) acc[k][q] += pos[u] >= 0 ? to_f32(t[u][k].v[q]) : 0.f;
+    }
+  }
+}
+
+template <typename S, typename O>
+__global__ __launch_bounds__(kEmbThreads) void embedding_bwd_interleaved(const int64_t* __restrict__ ids, int n,
+                                                                         const S* __restrict__ src,
+                                                                         O* __restrict__ dst, int64_t V, int D,
+                                                                         int64_t pad, int shift, int R) {
+  extern __shared__ uint32_t emb_sm[];
+  uint32_t* list = emb_sm;  // n entries
+  uint32_t* cnt = list + n;  // hits per local row
+  uint32_t* hot = cnt + R;   // local rows with >= kEmbHot hits, ascending
+  uint32_t* cold = hot + R;  // the other hit rows, ascending
+  __shared__ int wsum[kEmbWaves];
+  __shared__ int qnh, qnc, qhead;
+  constexpr uint32_t kNone = 0xffffffffu;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t g = blockIdx.x, G = int64_t(1) << shift;
+  const int rows = g < V ? (int)((V - 1 - g) >> shift) + 1 : 0;
+  for (int i = tid; i < rows; i += kEmbThreads) cnt[i] = 0u;
+  if (tid == 0) qhead = 0;
+  __syncthreads();
+  {
+    int64_t v[kEmbIdsPerThread];
+#pragma unroll
+    for (int j = 0; j < kEmbIdsPerThread; ++j) {
+      const int i = tid + j * kEmbThreads;
+      v[j] = i < n ? ids[i] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kEmbIdsPerThread; ++j) {
+      const int i = tid + j * kEmbThreads;
+      if (i < n) {
+        uint32_t e = kNone;
+        if (v[j] >= 0 && v[j] < V && (v[j] & (G - 1)) == g && v[j] != pad) {
+          const uint32_t r = (uint32_t)(v[j] >> shift);
+          e = r << 16 | (uint32_t)i;
+          atomicAdd(&cnt[r], 1u);
+        }
+        list[i] = e;
+      }
+    }
+  }
+  __syncthreads();
+  // compaction: thread t takes positions [t J, t J + J)
+  const int J = (n + kEmbThreads - 1) / kEmbThreads;
+  uint32_t mine[kEmbIdsPerThread];
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < kEmbIdsPerThread; ++j) {
+    const int p = tid * J + j;
+    mine[j] = j < J && p < n ? list[p] : kNone;
+    c += mine[j] != kNone;
+  }
+  int incl = c;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  if (lane == 63) wsum[wid] = incl;
+  if (wid == 0) {  // hit rows by class, ascending
+    int nh = 0, nc = 0;
+    for (int r0 = 0; r0 < rows; r0 += 64) {
+      const int r = r0 + lane;
+      const uint32_t k = r < rows ? cnt[r] : 0u;
+      const uint64_t hm = __ballot(k >= (uint32_t)kEmbHot), cm = __ballot(k > 0u && k < (uint32_t)kEmbHot);
+      if (k >= (uint32_t)kEmbHot)
+        hot[nh + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(hm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)hm, 0u))] = r;
+      else if (k > 0u)
+        cold[nc + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(cm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)cm, 0u))] = r;
+      nh += __popcll(hm);
+      nc += __popcll(cm);
+    }
+    if (lane == 0) qnh = nh, qnc = nc;
+  }
+  __syncthreads();  // every thread holds its entries; the wave totals and the row classes are in
+  int off = incl - c, L = 0;
+#pragma unroll
+  for (int w = 0; w < kEmbWaves; ++w) {
+    const int s = wsum[w];
+    off += w < wid ? s : 0;
+    L += s;
+  }
+#pragma unroll
+  for (int j = 0; j < kEmbIdsPerThread; ++j)
+    if (mine[j] != kNone) list[off++] = mine[j];
+  __syncthreads();
+
+  const int ns = (D + kEmbHotCols - 1) / kEmbHotCols;  // slices of a hot row
+  const int nhi = qnh * ns, nitems = nhi + qnc;
+  auto next = [&]() {
+    int q = 0;
+    if (lane == 0) q = atomicAdd(&qhead, 1);
+    return __builtin_amdgcn_readfirstlane(q);
+  };
+  int q = next();
+  for (; q < nhi; q = next()) {  // slices of the hot rows first: their chains are the longest
+    const int h = q / ns, s = q - h * ns;
+    const uint32_t r = hot[h];
+    O* drow = dst + ((int64_t)r * G + g) * D;
+    const int cc = s * kEmbHotCols + lane * kEmbHotVN;
+    float acc[1][kEmbHotVN];
+#pragma unroll
+    for (int k = 0; k < kEmbHotVN; ++k) acc[0][k] = 0.f;
+    emb_sum<kEmbHotVN, 1, kEmbHotU>(list, L, r, src, D, cc, acc);
+    if (cc < D) emb_store_nt<O, kEmbHotVN>(drow + cc, acc[0]);
+  }
+  if (wid < kEmbZeroWaves) {  // local rows wid, wid + Z, wid + 2Z, ... that no token hits
+    float z[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) z[k] = 0.f;
+    for (int m0 = 0; wid + kEmbZeroWaves * m0 < rows; m0 += 64) {
+      const int r = wid + kEmbZeroWaves * (m0 + lane);
+      uint64_t mk = __ballot(r < rows && cnt[r] == 0u);
+      while (mk) {
+        const int j = __builtin_ctzll(mk);
+        mk &= mk - 1;
+        O* drow = dst + ((int64_t)(wid + kEmbZeroWaves * (m0 + j)) * G + g) * D;
+        for (int cc = lane * 8; cc < D; cc += 64 * 8) emb_store_nt<O, 8>(drow + cc, z);
+      }
+    }
+  }
+  for (; q < nitems; q = next()) {  // the other hit rows whole, 1024 columns per pass
+    const uint32_t r = cold[q - nhi];
+    O* drow = dst + ((int64_t)r * G + g) * D;
+    for (int c0 = 0; c0 < D; c0 += 2 * 64 * 8) {
+      float acc[2][8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[0][k] = acc[1][k] = 0.f;
+      const int cc = c0 + lane * 8;
+      emb_sum<8, 2, 4>(list, L, r, src, D, cc, acc);
+      if (cc < D) emb_store_nt<O, 8>(drow + cc, acc[0]);
+      if (cc + 512 < D) emb_store_nt<O, 8>(drow + cc + 512, acc[1]);
+    }
+  }
+}
+
 template <bool ACC>
 static int launch_segments(const uint32_t* keys, const uint32_t* vals, int64_t n, const void* src, int sdt,
                            int64_t stride_s, void* dst, int ddt, int64_t stride_d, int64_t D, uint32_t n_target,
@@ -254,6 +516,61 @@ static int sort_indices(const int64_t* idx, int64_t n, int64_t n_target, void* w
   return QH_OK;
 }
 
+template <typename S, typename O>
+static int launch_embedding_interleaved_t(const int64_t* ids, const void* gout, void* gw, int64_t n, int64_t V, int64_t D,
+                                     int64_t pad, hipStream_t st) {
+  // G = 256 workgroups (fewer for a smaller vocabulary, more when a workgroup would own more
+  // than kEmbMaxRows rows), a power of two
+  int shift = 0;
+  while (shift < 8 && (int64_t(1) << shift) < V) ++shift;
+  while (ceil_div(V, int64_t(1) << shift) > kEmbMaxRows) ++shift;
+  const int64_t G = int64_t(1) << shift, R = ceil_div(V, G);
+  QH_CHECK_ARG(G < (1ll << 31) && D < (1ll << 31), "qh_embedding_bwd: grid too large");
+  const int lds = (int)(4 * (n + 3 * R));
+  // the dynamic-LDS limit is raised once per instantiation and device
+  static uint64_t attr_set = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    qh::set_error("qh_embedding_bwd: no current device");
+    return QH_E_HIP;
+  }
+  if (!(attr_set >> dev & 1)) {
+    const hipError_t e = hipFuncSetAttribute((const void*)embedding_bwd_interleaved<S, O>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)(4 * (kEmbLdsTokens + 3 * kEmbMaxRows)));
+    if (e != hipSuccess) {
+      qh::set_error("qh_embedding_bwd: cannot raise the LDS limit: %s", hipGetErrorString(e));
+      return QH_E_HIP;
+    }
+    attr_set |= 1ull << dev;
+  }
+  embedding_bwd_interleaved<S, O><<<(unsigned)G, kEmbThreads, lds, st>>>(ids, (int)n, (const S*)gout, (O*)gw, V,
+                                                                          (int)D, pad, shift, (int)R);
+  return QH_OK;
+}
+
+static int launch_embedding_interleaved(const int64_t* ids, const void* gout, void* gw, int64_t n, int64_t V, int64_t D,
+                                   int64_t pad, int gdtype, int wdtype, hipStream_t st) {
+  int rc = QH_OK;
+#define QH_ER_O(S)                                                                                   \
+  switch (wdtype) {                                                                                  \
+    case QH_F32: rc = launch_embedding_interleaved_t<S, float>(ids, gout, gw, n, V, D, pad, st); break;   \
+    case QH_F16: rc = launch_embedding_interleaved_t<S, f16_t>(ids, gout, gw, n, V, D, pad, st); break;   \
+    case QH_BF16: rc = launch_embedding_interleaved_t<S, bf16_t>(ids, gout, gw, n, V, D, pad, st); break; \
+    default: qh::set_error("qh_embedding_bwd: bad weight dtype"); return QH_E_DTYPE;                 \
+  }
+  switch (gdtype) {
+    case QH_F32: QH_ER_O(float); break;
+    case QH_F16: QH_ER_O(f16_t); break;
+    case QH_BF16: QH_ER_O(bf16_t); break;
+    default: qh::set_error("qh_embedding_bwd: bad grad dtype"); return QH_E_DTYPE;
+  }
+#undef QH_ER_O
+  if (rc) return rc;
+  QH_CHECK_LAUNCH("qh_embedding_bwd");
+  return QH_OK;
+}
+
 }  // namespace
 
 // Sort space for the token ids (V is part of the signature; the rows need no table).
@@ -291,6 +608,8 @@ extern "C" int qh_embedding_bwd(const int64_t* ids, const void* gout, void* gw, 
     QH_CHECK_LAUNCH("qh_embedding_bwd");
     return QH_OK;
   }
+  if (n_tokens <= kEmbLdsTokens) return launch_embedding_interleaved(ids, gout, gw, n_tokens, V, Hd, padding_idx, gdtype,
+                                                                wdtype, st);
   uint32_t *keys = nullptr, *vals = nullptr;
   int rc = sort_indices(ids, n_tokens, V, ws, sort_bytes, &keys, &vals, st, "qh_embedding_bwd");
   if (rc) return rc;

@@ -244,6 +244,68 @@ def test_embedding_backward_writes_every_row(n, wdt):
     assert torch.equal(got.view(bits), exp.view(bits))
 
 
+def _embedding_bwd_abi(ids, go, V, pad, wdt):
+    n, H = go.shape
+    gw = torch.full((V, H), 7.0, dtype=wdt, device=DEV)
+    ids_d, go_d = ids.to(DEV), go.to(DEV)
+    ws = _native.workspace(_native.call("qh_embedding_bwd_workspace", n, V), gw.device)
+    _native.call("qh_embedding_bwd", ids_d.data_ptr(), go_d.data_ptr(), gw.data_ptr(), ws.data_ptr(), ws.numel(),
+                 n, V, H, pad, _native.dtype_code(go.dtype), _native.dtype_code(wdt), _native.stream(gw.device))
+    return gw.cpu()
+
+
+def _embedding_bwd_expected(ids, go, V, pad, wdt):
+    exp = torch.zeros(V, go.shape[1], dtype=torch.float32)
+    flat_go = go.float()
+    for t, v in enumerate(ids.tolist()):
+        if 0 <= v < V:
+            exp[v] += flat_go[t]
+    if 0 <= pad < V:
+        exp[pad] = 0
+    return exp.to(wdt)
+
+
+@pytest.mark.parametrize("case", ["one_id", "one_range", "out_of_range", "tiny_vocab", "wide_rows", "f32_grad",
+                                  "max_tokens", "above_max_tokens"])
+def test_embedding_backward_id_distributions(case):
+    """Every row written once, each hit row the token-order fp32 sum rounded once, for id
+    distributions that load one workgroup's row range heavily (every token on one id; every token
+    within a few hundred rows), ids outside [0, V) (no contribution), a vocabulary smaller than
+    the workgroup count, rows wider than one 1024-column pass with a partial tail, fp32 incoming
+    gradients into fp16 weights, and the token counts either side of the single-launch limit
+    (32768; above it the ids are sorted first)."""
+    g = _gen(57)
+    V, H, n, pad, wdt, gdt = 5000, 64, 3000, 7, torch.bfloat16, torch.bfloat16
+    if case == "one_id":
+        ids = torch.full((n,), 1234, dtype=torch.int64)
+    elif case == "one_range":
+        n = 20000
+        ids = torch.randint(4000, 4400, (n,), generator=g)
+    elif case == "out_of_range":
+        ids = torch.randint(-50, V + 50, (n,), generator=g)
+        ids[:3] = torch.tensor([-(2 ** 40), 2 ** 40, V])
+    elif case == "tiny_vocab":
+        V, pad = 3, 1
+        ids = torch.randint(0, V, (n,), generator=g)
+    elif case == "wide_rows":
+        V, H = 3000, 1032
+        ids = torch.randint(0, 500, (n,), generator=g)
+    elif case == "f32_grad":
+        wdt, gdt = torch.float16, torch.float32
+        ids = torch.randint(0, 300, (n,), generator=g)
+    elif case == "max_tokens":
+        V, H, n = 20000, 16, 32768
+        ids = torch.randint(0, V, (n,), generator=g)
+    else:
+        V, H, n = 20000, 16, 32769
+        ids = torch.randint(0, V, (n,), generator=g)
+    go = torch.randn(n, H, generator=g).to(gdt)
+    got = _embedding_bwd_abi(ids, go, V, pad, wdt)
+    exp = _embedding_bwd_expected(ids, go, V, pad, wdt)
+    bits = torch.int16 if wdt != torch.float32 else torch.int32
+    assert torch.equal(got.view(bits), exp.view(bits))
+
+
 def test_embedding_backward_in_a_captured_graph():
     """qh_embedding_bwd captured in a HIP graph (the device-wide id sort and the row walk):
     every replay, with eager work between replays, equals the eager result bit for bit."""
