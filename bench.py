@@ -839,6 +839,13 @@ def bench_ops(reps=20):
     ms = gpu_ms(lambda: K.triton_index_add(tgt2, src, idx))
     record("a13", "index_add (1024 rows into 16384)", [T, 2048], ms, 3 * 1024 * 2048 * 2, 1024,
            lambda: O.index_add(tgt2[:4096].cpu(), src[:256].cpu(), (idx[:256] % 4096).cpu(), dtype=f32), 256)
+    # floors of the small launches above, timed the same way: an empty kernel back to back, and
+    # torch's device copy of the same bytes as softmax fwd and the S=4096 KV write (8.4 MB each way)
+    ms = gpu_ms(lambda: torch.cuda._sleep(0))
+    record("floor", "empty launch", [], ms, 0, 1)
+    cs, cd = torch.empty(T * E, device="cuda"), torch.empty(T * E, device="cuda")
+    ms = gpu_ms(lambda: cd.copy_(cs))
+    record("floor", "device copy 8.4 MB", [T * E], ms, 2 * T * E * 4, 1)
     return {"cpu_cores": cores, "rows": rows}
 
 

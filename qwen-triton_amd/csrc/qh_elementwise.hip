@@ -236,6 +236,42 @@ __global__ __launch_bounds__(256) void kv_write_vec(T* __restrict__ cache, int64
   }
 }
 
+// The same write for planes of at least kKvPlaneMin 16-byte chunks per (sequence, head):
+// blockIdx.y is the (b, h) pair, so the chunk index needs one 32-bit division (by the
+// chunks per row), and each thread has kKvPlaneU loads in flight before its stores.
+constexpr int kKvPlaneU = 4, kKvPlaneMin = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(256) void kv_write_plane(T* __restrict__ cache, int64_t scb, int64_t sch, int64_t scs,
+                                                      const T* __restrict__ val, int64_t svb, int64_t svh,
+                                                      int64_t svs, const int64_t* __restrict__ pos, int H, int S,
+                                                      int vpr, int64_t cap) {
+  constexpr int VN = Vec16<T>::N;
+  const int b = (int)blockIdx.y / H, h = (int)blockIdx.y - b * H;
+  T* cb = cache + b * scb + h * sch;
+  const T* vb = val + b * svb + h * svh;
+  const int plane = S * vpr;
+  const int base = (int)blockIdx.x * (256 * kKvPlaneU) + (int)threadIdx.x;
+  Vec16<T> t[kKvPlaneU];
+  int64_t dst[kKvPlaneU];
+#pragma unroll
+  for (int u = 0; u < kKvPlaneU; ++u) {
+    const int i = base + u * 256;
+    dst[u] = -1;
+    if (i < plane) {
+      const int s = i / vpr, d = (i - s * vpr) * VN;
+      const int64_t p = pos[s];
+      if (p >= 0 && p < cap) {
+        t[u] = ld16(vb + s * svs + d);
+        dst[u] = p * scs + d;
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kKvPlaneU; ++u)
+    if (dst[u] >= 0) st16(cb + dst[u], t[u]);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void kv_write_scalar(T* __restrict__ cache, int64_t scb, int64_t sch,
                                                        int64_t scs, int64_t scd, const T* __restrict__ val,
@@ -467,7 +503,12 @@ extern "C" int qh_kv_write(void* cache, int64_t scb, int64_t sch, int64_t scs, i
     const bool vec = scd == 1 && svd == 1 && D % VN == 0 && aligned16(cache) && aligned16(values) &&
                      scb % VN == 0 && sch % VN == 0 && scs % VN == 0 && svb % VN == 0 && svh % VN == 0 &&
                      svs % VN == 0;
-    if (vec) {
+    if (vec && S * (D / VN) >= kKvPlaneMin && S * (D / VN) < (1ll << 30) && B * H < 65536) {
+      const int vpr = (int)(D / VN);
+      const dim3 grid((unsigned)ceil_div(S * vpr, 256 * kKvPlaneU), (unsigned)(B * H));
+      kv_write_plane<T><<<grid, 256, 0, st>>>((T*)cache, scb, sch, scs, (const T*)values, svb, svh, svs, positions,
+                                              (int)H, (int)S, vpr, cap);
+    } else if (vec) {
       const int64_t total = B * H * S * (D / VN);
       kv_write_vec<T><<<grid_for(total), 256, 0, st>>>((T*)cache, scb, sch, scs, (const T*)values, svb, svh, svs,
                                                        positions, H, S, D / VN, cap, total);

@@ -168,6 +168,25 @@ def test_write_attention_kv_strided_bf16_and_out_of_range():
     assert torch.count_nonzero(big[:, :, 32:]).item() == 0
 
 
+@pytest.mark.parametrize("S,D", [(700, 128), (64, 128), (2048, 64)])
+def test_write_attention_kv_prefill_planes(S, D):
+    """Prefill-sized writes (at least 1024 16-byte chunks per sequence and head: one kernel block
+    row per (b, h) pair, four chunks per thread) into a strided cache view: the written rows equal
+    the oracle's, positions past the view's capacity are skipped, and nothing else changes
+    (S = 700 leaves a partial last block)."""
+    B, H, cap = 2, 3, 2 * S
+    big = torch.zeros(B, H, cap + 32, D, dtype=torch.bfloat16, device=DEV)
+    cache = big[:, :, :cap]
+    values = randn(B, H, S, D, dtype=torch.bfloat16, seed=44)
+    positions = torch.randperm(cap + 16, generator=_gen(45))[:S]  # some land past the view: skipped
+    K.write_attention_kv(cache, values, positions.to(DEV))
+    keep = positions < cap
+    exp = torch.zeros(B, H, cap, D, dtype=torch.bfloat16)
+    exp[:, :, positions[keep]] = values.cpu()[:, :, keep]
+    assert torch.equal(cache.cpu(), exp)
+    assert torch.count_nonzero(big[:, :, cap:]).item() == 0
+
+
 def test_append_attention_kv():
     a, b = randn(2, 3, 5, 64, dtype=torch.bfloat16, seed=42), randn(2, 3, 2, 64, dtype=torch.bfloat16, seed=43)
     assert torch.equal(K.append_attention_kv(a, b).cpu(), O.kv_append(a, b))
@@ -343,7 +362,7 @@ def test_embedding_backward_in_a_captured_graph():
 # ---------------------------------------------------------------------------
 # Softmax / cross-entropy
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("shape", [(1000, 128), (7, 5000), (3, 64)])
+@pytest.mark.parametrize("shape", [(1000, 128), (1001, 256), (7, 5000), (3, 64)])
 def test_softmax_forward_backward(shape):
     x = randn(*shape, seed=60, scale=3.0).requires_grad_(True)
     y = K.triton_softmax(x)
