@@ -387,7 +387,7 @@ int qh_lmce_fwd(const void* X, int64_t ldx, const void* W, int64_t ldw, const in
  * (qh_ce_bwd) and multiplied into dX (these rows) and dW (accumulated over the
  * blocks, qh_gemm_acc). No counterpart in the reference; it replaces, fused,
  * the same calls as qh_lmce_fwd above, with gradients. */
-/* Workspace bytes of qh_lmce_rows_fwd: per-64-column partials and target logits. */
+/* Workspace bytes of qh_lmce_rows_fwd: per-64-column (max, sum of exp) partials. */
 int64_t qh_lmce_rows_workspace(int64_t N, int64_t V);
 /* Z [N, V] (row stride ldz) = X W^T rounded to the dtype; lse[row] and
  * loss_rows[row] = lse - logit[target] (0 for ignore_index rows, NaN for

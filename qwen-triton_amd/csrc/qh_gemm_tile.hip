@@ -1352,18 +1352,19 @@ struct LmceFwdProblem {
 // Logits of a block of rows for the fused LM head + cross-entropy with
 // gradients: Z = X W^T rounded to T and written out (the caller turns Z into
 // the logit gradient in place), and per row the (max, sum of exp) of every
-// 64-column block of the rounded logits plus the target logit, so the row's
-// logsumexp needs no further pass over Z. Persistent like the dense problem;
-// each wavefront reduces its own 64 columns, so no cross-wave step is needed
-// in the epilogue.
+// 64-column block of the rounded logits, so the row's logsumexp needs no
+// further pass over Z (the combine reads the target logits from Z). The
+// epilogue issues no global load: on gfx9 vmcnt also counts stores, so a load
+// waited for in the epilogue would wait for the tile's Z stores and for the
+// next tile's first operand loads. Persistent like the dense problem; each
+// wavefront reduces its own 64 columns, so no cross-wave step is needed in the
+// epilogue.
 template <typename T>
 struct LmceLogitsProblem {
   const T* X;
   const T* W;
   T* Z;
-  const int64_t* tgt;
   float2* part;   // [nblk][M] (max, sum of exp): a wave's rows are consecutive, stores coalesce
-  float* tlogit;  // [M]
   int64_t ldx, ldw, ldz;
   int M, N, K, tiles_m, tiles_n, nblk;
 
@@ -1423,8 +1424,6 @@ struct LmceLogitsProblem {
         }
       }
       part[(int64_t)blk * M + row] = make_float2(m, sum);
-      const int64_t tc = tgt[row] - (int64_t)(c.n0 + wc);
-      if (tc >= 0 && tc < ncol) tlogit[row] = to_f32(et.row8(r, (int)(tc >> 3)).v[tc & 7]);
     }
   }
   template <int TM, int TN>
@@ -1435,10 +1434,11 @@ struct LmceLogitsProblem {
 // partials: 64 consecutive rows per workgroup; wave w folds the blocks
 // b = w, w + 16, ... of its lane's row in order, eight loads in flight at a time
 // (lanes read consecutive rows: coalesced), then the 16 wave results are folded
-// in wave order.
+// in wave order. The target logit is read from Z (the rounded logits).
 constexpr int kCombWaves = 16;
+template <typename T>
 __global__ __launch_bounds__(64 * kCombWaves) void lmce_combine_cols_kernel(
-    const float2* __restrict__ part, const float* __restrict__ tlogit, const int64_t* __restrict__ tgt, int64_t N,
+    const float2* __restrict__ part, const T* __restrict__ Z, int64_t ldz, const int64_t* __restrict__ tgt, int64_t N,
     int nblk, int64_t V, int64_t ignore, float* __restrict__ lse, float* __restrict__ loss_rows) {
   __shared__ float sm[kCombWaves][64], ss[kCombWaves][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -1472,7 +1472,7 @@ __global__ __launch_bounds__(64 * kCombWaves) void lmce_combine_cols_kernel(
     loss_rows[row] = 0.f;
   } else {
     lse[row] = l;
-    loss_rows[row] = (t >= 0 && t < V) ? l - tlogit[row] : __int_as_float(0x7fc00000);
+    loss_rows[row] = (t >= 0 && t < V) ? l - to_f32(Z[row * ldz + t]) : __int_as_float(0x7fc00000);
   }
 }
 
@@ -1859,7 +1859,7 @@ extern "C" int qh_lmce_fwd(const void* X, int64_t ldx, const void* W, int64_t ld
 
 extern "C" int64_t qh_lmce_rows_workspace(int64_t N, int64_t V) {
   if (N <= 0 || V <= 0) return 0;
-  return N * ((V + 63) / 64) * 2 * 4 + N * 4;  // 64-column partials, target logits
+  return N * ((V + 63) / 64) * 2 * 4;  // 64-column (max, sum of exp) partials
 }
 
 extern "C" int qh_lmce_rows_fwd(const void* X, int64_t ldx, const void* W, int64_t ldw, const int64_t* targets,
@@ -1878,7 +1878,6 @@ extern "C" int qh_lmce_rows_fwd(const void* X, int64_t ldx, const void* W, int64
   hipStream_t st = (hipStream_t)stream;
   const int nblk = (int)((V + 63) / 64);
   float2* part = (float2*)ws;
-  float* tlog = (float*)(part + N * nblk);
   int rc = QH_OK;
 #define QH_LMCER(TT)                                                                               \
   {                                                                                                \
@@ -1886,9 +1885,7 @@ extern "C" int qh_lmce_rows_fwd(const void* X, int64_t ldx, const void* W, int64
     p.X = (const TT*)X;                                                                            \
     p.W = (const TT*)W;                                                                            \
     p.Z = (TT*)Z;                                                                                  \
-    p.tgt = targets;                                                                               \
     p.part = part;                                                                                 \
-    p.tlogit = tlog;                                                                               \
     p.ldx = ldx;                                                                                   \
     p.ldw = ldw;                                                                                   \
     p.ldz = ldz;                                                                                   \
@@ -1900,12 +1897,13 @@ extern "C" int qh_lmce_rows_fwd(const void* X, int64_t ldx, const void* W, int64
     p.nblk = nblk;                                                                                 \
     rc = launch_tile<TT, 256, 256, kDenseBK, kDenseNS, false, false>(p, dense_grid(p.tiles_m * p.tiles_n), st, \
                                                                      "qh_lmce_rows_fwd");          \
+    if (rc == QH_OK)                                                                               \
+      lmce_combine_cols_kernel<TT><<<(unsigned)((N + 63) / 64), 64 * kCombWaves, 0, st>>>(        \
+          part, (const TT*)Z, ldz, targets, N, nblk, V, ignore_index, lse, loss_rows);             \
   }
   if (dtype == QH_BF16) QH_LMCER(bf16_t) else QH_LMCER(f16_t)
 #undef QH_LMCER
   if (rc) return rc;
-  lmce_combine_cols_kernel<<<(unsigned)((N + 63) / 64), 64 * kCombWaves, 0, st>>>(part, tlog, targets, N, nblk, V,
-                                                                                   ignore_index, lse, loss_rows);
   QH_CHECK_LAUNCH("qh_lmce_rows_fwd");
   return QH_OK;
 }
