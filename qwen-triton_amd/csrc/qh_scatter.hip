@@ -86,17 +86,41 @@ __device__ __forceinline__ void st8f(T* p, const float (&o)[8]) {
   }
 }
 
-// Sum of the source rows vals[s..e) (in that order, fp32, starting from
-// `init`) for the 8-column chunk at element offset c.
-template <typename S>
+// U source rows from position j (all loads issued before the first add), added in order;
+// 16-bit rows stay packed until their add, so a batch costs 4 registers per row.
+template <int U, typename S>
+__device__ __forceinline__ void run_batch8(const uint32_t* __restrict__ vals, int64_t j, const S* __restrict__ src,
+                                           int64_t stride_s, int64_t c, float (&acc)[8]) {
+  if constexpr (sizeof(S) == 4) {
+    float t[U][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) ld8f(src + (int64_t)vals[j + u] * stride_s + c, t[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] += t[u][q];
+  } else {
+    Vec16<S> t[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) t[u] = ld16(src + (int64_t)vals[j + u] * stride_s + c);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] += to_f32(t[u].v[q]);
+  }
+}
+
+// Sum of the source rows vals[s..e) (in that order, fp32, onto acc) for the
+// 8-column chunk at element offset c: batches of B rows of loads while B
+// remain (at most 4 for fp32 rows), then single rows (a run of one row costs
+// one load).
+template <int BMAX = 8, typename S>
 __device__ __forceinline__ void run_sum8(const uint32_t* __restrict__ vals, int64_t s, int64_t e,
                                          const S* __restrict__ src, int64_t stride_s, int64_t c, float (&acc)[8]) {
-  for (int64_t j = s; j < e; ++j) {
-    float t[8];
-    ld8f(src + (int64_t)vals[j] * stride_s + c, t);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) acc[q] += t[q];
-  }
+  constexpr int B = sizeof(S) == 4 && BMAX > 4 ? 4 : BMAX;
+  int64_t j = s;
+  for (; j + B <= e; j += B) run_batch8<B>(vals, j, src, stride_s, c, acc);
+  for (; j < e; ++j) run_batch8<1>(vals, j, src, stride_s, c, acc);
 }
 
 // segment_rows with 8-column vector chunks: one wave per sorted position
@@ -157,7 +181,7 @@ __global__ __launch_bounds__(256) void embedding_rows_roles(const uint32_t* __re
       float acc[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc[q] = 0.f;
-      run_sum8(vals, i, e, src, D, c, acc);
+      run_sum8<4>(vals, i, e, src, D, c, acc);
       st8f(drow + c, acc);
     }
     return;

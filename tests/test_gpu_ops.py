@@ -285,14 +285,14 @@ def _embedding_bwd_expected(ids, go, V, pad, wdt):
 
 
 @pytest.mark.parametrize("case", ["one_id", "one_range", "out_of_range", "tiny_vocab", "wide_rows", "f32_grad",
-                                  "max_tokens", "above_max_tokens"])
+                                  "max_tokens", "above_max_tokens", "above_max_tokens_hot_id"])
 def test_embedding_backward_id_distributions(case):
     """Every row written once, each hit row the token-order fp32 sum rounded once, for id
     distributions that load one workgroup's row range heavily (every token on one id; every token
     within a few hundred rows), ids outside [0, V) (no contribution), a vocabulary smaller than
     the workgroup count, rows wider than one 1024-column pass with a partial tail, fp32 incoming
     gradients into fp16 weights, and the token counts either side of the single-launch limit
-    (32768; above it the ids are sorted first)."""
+    (32768; above it the ids are sorted first, also with one id on 30% of the tokens)."""
     g = _gen(57)
     V, H, n, pad, wdt, gdt = 5000, 64, 3000, 7, torch.bfloat16, torch.bfloat16
     if case == "one_id":
@@ -315,6 +315,10 @@ def test_embedding_backward_id_distributions(case):
     elif case == "max_tokens":
         V, H, n = 20000, 16, 32768
         ids = torch.randint(0, V, (n,), generator=g)
+    elif case == "above_max_tokens_hot_id":  # sorted path with one run of ~12000 tokens
+        V, H, n = 20000, 16, 40003
+        ids = torch.randint(0, V, (n,), generator=g)
+        ids[torch.rand(n, generator=g) < 0.3] = 77
     else:
         V, H, n = 20000, 16, 32769
         ids = torch.randint(0, V, (n,), generator=g)
@@ -505,6 +509,30 @@ def test_index_add(dtype):
     close(out, exp, **(F32_TOL if dtype == torch.float32 else dict(atol=5e-2, rtol=2e-2)))
     out2 = K.triton_index_add(tgt.clone(), src, index)
     assert torch.equal(out, out2)
+
+
+def test_index_add_is_source_order_fp32_sum_signed_zeros():
+    """fp32 index_add bit for bit against a sequential loop in source order: runs of 1 to 20 sources
+    per target row (every mix of the summation's batches of four rows and single rows), targets
+    holding -0.0 and +0.0, sources holding +-0.0."""
+    T, D, n = 24, 40, 260
+    g = _gen(90)
+    tgt = torch.randn(T, D, generator=g)
+    tgt[0] = -0.0
+    tgt[1] = 0.0
+    tgt[2, ::2] = -0.0
+    src = torch.randn(n, D, generator=g)
+    src[::7] = -0.0
+    src[3::11] = 0.0
+    counts = [1 + (r * 7) % 20 for r in range(T)]
+    index = torch.cat([torch.full((c,), r) for r, c in enumerate(counts)])[:n]
+    index = index[torch.randperm(index.numel(), generator=g)]
+    src = src[:index.numel()]
+    exp = tgt.clone()
+    for j, r in enumerate(index.tolist()):
+        exp[r] = exp[r] + src[j]
+    out = K.triton_index_add(tgt.to(DEV), src.to(DEV), index.to(DEV))
+    assert torch.equal(out.cpu().view(torch.int32), exp.view(torch.int32))
 
 
 def test_index_add_autograd():
