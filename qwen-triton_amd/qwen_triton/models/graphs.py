@@ -22,6 +22,9 @@ regrown rotary table never frees memory a graph still reads.
 """
 from __future__ import annotations
 
+import gc
+import weakref
+
 import torch
 
 from qwen_triton import _native
@@ -47,7 +50,10 @@ class GreedyGraphs:
     def __init__(self, model, batch: int, prompt: int, max_new: int, dtype: torch.dtype, device) -> None:
         if max_new < 2:
             raise ValueError("graph-captured generation needs at least two new tokens")
-        self.model = model
+        # The owner model keeps its runners; a weak reference back avoids a reference cycle, which
+        # only the cyclic garbage collector would free, at an arbitrary later allocation (possibly
+        # inside another graph's capture, where destroying graphs is not allowed).
+        self._model = weakref.ref(model)
         self.batch, self.prompt, self.max_new = batch, prompt, max_new
         self.cache = model.new_cache(batch, prompt + max_new, dtype, device)
         self.prompt_ids = torch.zeros((batch, prompt), dtype=torch.long, device=device)
@@ -65,6 +71,13 @@ class GreedyGraphs:
         self.greedy_ws = None
         if _greedy_step_ok(batch, vocab, dtype):
             self.greedy_ws = _native.workspace(_native.call("qh_greedy_step_workspace", batch, vocab), device)
+
+    @property
+    def model(self):
+        m = self._model()
+        if m is None:
+            raise RuntimeError("the model of this generation runner no longer exists")
+        return m
 
     def _greedy(self, logits: torch.Tensor) -> None:
         last = logits[:, -1]
@@ -124,10 +137,19 @@ class GreedyGraphs:
             self._step_body()
         torch.cuda.current_stream(dev).wait_stream(side)
         prefill, step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-        with torch.cuda.graph(prefill):
-            self._prefill_body()
-        with torch.cuda.graph(step):
-            self._step_body()
+        # no cyclic garbage collection while capturing: an unreachable object that owns device
+        # resources (another graph, say) must not be destroyed inside a capture
+        gc_was_enabled = gc.isenabled()
+        gc.collect()
+        gc.disable()
+        try:
+            with torch.cuda.graph(prefill):
+                self._prefill_body()
+            with torch.cuda.graph(step):
+                self._step_body()
+        finally:
+            if gc_was_enabled:
+                gc.enable()
         self.prefill_graph, self.step_graph = prefill, step
         self._derived = self._derived_tensors()
 

@@ -197,3 +197,28 @@ def test_golden_qwen3_next_logits_and_cached_decode():
             cache = o.past_key_values
             steps.append(o.logits)
     torch.testing.assert_close(torch.cat(steps, dim=1), logits, atol=2e-4, rtol=2e-4)
+
+
+def test_graph_runner_holds_no_reference_cycle():
+    """A generation runner (``greedy_graphs``) refers back to its model weakly: dropping the model
+    frees it and its runners by reference counting alone, never later in the cyclic garbage
+    collector (which can run inside another graph's capture, where destroying graphs is not
+    allowed). No graph is captured here; the runner is only created."""
+    import gc
+    import weakref
+
+    cfg = QwenTritonConfig.from_hf_config(dict(model_type="qwen3", vocab_size=128, hidden_size=64,
+                                               intermediate_size=128, num_hidden_layers=2, num_attention_heads=4,
+                                               num_key_value_heads=2, head_dim=16, max_position_embeddings=64))
+    model = QwenTritonForCausalLM(cfg)
+    runner = model.greedy_graphs(1, 4, 3)
+    assert runner.model is model
+    gc_was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        ref_model, ref_runner = weakref.ref(model), weakref.ref(runner)
+        del model, runner
+        assert ref_model() is None and ref_runner() is None
+    finally:
+        if gc_was_enabled:
+            gc.enable()
