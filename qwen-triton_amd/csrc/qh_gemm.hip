@@ -622,6 +622,29 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
   const int N = pv.N;
   const int m0 = mg * R;
   const int tid = (int)threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  // Non-gated epilogue: element e of the tile is output (grow, gn); thread tid writes the
+  // elements tid, tid + 1024, ... Their residual is loaded here, before the weight stream,
+  // so that its latency is not added after the reduction (C may be the residual: each
+  // element is read and then written by the same thread).
+  constexpr int EN = NWR * NWC * WR * 256;
+  constexpr int EPT = GATED ? 1 : (EN + 1023) / 1024;
+  auto epi_index = [&](int e, int& grow, int& gn) {
+    const int g = e / (NWC * WR * 256), c = (e / (WR * 256)) % NWC, i = (e >> 8) % WR;
+    const int r = (e >> 6) & 3, l = e & 63;
+    grow = m0 + (g * WR + i) * 16 + (l >> 4) * 4 + r;
+    gn = tile * OC + c * 16 + (l & 15);
+  };
+  float rpre[EPT];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    rpre[k] = 0.f;
+    if constexpr (!GATED) {
+      const int e = tid + k * 1024;
+      int grow, gn;
+      epi_index(e, grow, gn);
+      if (pv.res != nullptr && e < EN && grow < M && gn < N) rpre[k] = to_f32(pv.res[(int64_t)grow * pv.ldr + gn]);
+    }
+  }
   const int ks = wid % KS, st = wid / KS, rb = st / NWC, cb = st % NWC;
   const int li = lane & 15, q = lane >> 4;
   // source row of each of this thread's stage slots (fixed over the chunks): staged rows
@@ -774,22 +797,25 @@ __global__ __launch_bounds__(1024) void gemm_decode_kernel(const T* __restrict__
       pv.C[(int64_t)grow * pv.ldc + gn] = from_f32<OT>(gt * sigmoidf_(gt) * up);
     }
   } else {
-    constexpr int E = NWR * NWC * WR * 256;
     const T* bias = pv.bias;
-    const T* res = pv.res;
+    const bool has_res = pv.res != nullptr;
     OT* const Cp = pv.C;
-    const int64_t ldc = pv.ldc, ldr = pv.ldr;
-    for (int e = tid; e < E; e += 1024) {
+    const int64_t ldc = pv.ldc;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + k * 1024;
+      if (e >= EN) break;
       const int g = e / (NWC * WR * 256), c = (e / (WR * 256)) % NWC, i = (e >> 8) % WR;
       const int r = (e >> 6) & 3, l = e & 63;
       const int row = (g * WR + i) * 16 + (l >> 4) * 4 + r;
-      const int grow = m0 + row, gn = tile * OC + c * 16 + (l & 15);
+      int grow, gn;
+      epi_index(e, grow, gn);
       if (grow >= M || gn >= N) continue;
       float v = slice_sum(g, c, i, l, r);
       if constexpr (NORM) v *= row_factor(row);
       v += bias ? to_f32(bias[gn]) : 0.f;
       OT o = from_f32<OT>(v);
-      if (res != nullptr) o = from_f32<OT>(to_f32(o) + to_f32(res[(int64_t)grow * ldr + gn]));
+      if (has_res) o = from_f32<OT>(to_f32(o) + rpre[k]);
       Cp[(int64_t)grow * ldc + gn] = o;
     }
   }
