@@ -35,9 +35,23 @@ def _rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
     return float((a - e).abs().max()) / max(float(e.abs().max()), 1e-12)
 
 
-def _check(actual, expected, tol, what):
-    err = _rel_err(actual, expected)
+def _rms_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    a, e = actual.detach().double(), expected.detach().double()
+    return float((a - e).norm()) / max(float(e.norm()), 1e-300)
+
+
+_STATS: dict[str, tuple[float, float]] = {}
+
+
+def _check(actual, expected, tol, what, rms_tol=None):
+    """max|diff| / max|ref| <= tol and, when given, the relative RMS error ||diff|| / ||ref|| <= rms_tol
+    (the second bounds the bulk of the elements, small ones included)."""
+    err, rms = _rel_err(actual, expected), _rms_err(actual, expected)
+    _STATS[what] = (err, rms)
+    print(f"[fullsize] {what}: max-rel {err:.3e} rms-rel {rms:.3e}", flush=True)
     assert err <= tol, f"{what}: max|diff| / max|ref| = {err:.3e} > {tol}"
+    if rms_tol is not None:
+        assert rms <= rms_tol, f"{what}: ||diff|| / ||ref|| = {rms:.3e} > {rms_tol}"
 
 
 # ---------------------------------------------------------------------------
@@ -75,17 +89,21 @@ def test_flash_attention_config1_full_size():
             dp = dof @ vf.t().contiguous()
             ds = p * (dp - (dof * o_ref).sum(-1, keepdim=True))
             worst["o"] = max(worst["o"], _rel_err(o[b, h], o_ref))
+            worst["o_rms"] = max(worst.get("o_rms", 0.0), _rms_err(o[b, h], o_ref))
             worst["lse"] = max(worst["lse"], float((lse[b, h] - lse_ref).abs().max()))
-            worst["dq"] = max(worst["dq"], _rel_err(dq[b, h], (ds @ kf) * scale))
+            dq_ref = (ds @ kf) * scale
+            worst["dq"] = max(worst["dq"], _rel_err(dq[b, h], dq_ref))
+            worst["dq_rms"] = max(worst.get("dq_rms", 0.0), _rms_err(dq[b, h], dq_ref))
             dk_ref[b, hk] += (ds.t().contiguous() @ qf) * scale
             dv_ref[b, hk] += p.t().contiguous() @ dof
-    assert worst["o"] <= 2e-2, worst
+    print(f"[fullsize] config1 worst per head: {worst}", flush=True)
+    assert worst["o"] <= 2e-2 and worst["o_rms"] <= 5e-3, worst
     assert worst["lse"] <= 1e-3, worst
-    assert worst["dq"] <= 2e-2, worst
+    assert worst["dq"] <= 2e-2 and worst["dq_rms"] <= 6e-3, worst
     for b in range(B):
         for hk in range(Hkv):
-            _check(dk[b, hk], dk_ref[b, hk], 2e-2, f"dk[{b},{hk}]")
-            _check(dv[b, hk], dv_ref[b, hk], 2e-2, f"dv[{b},{hk}]")
+            _check(dk[b, hk], dk_ref[b, hk], 2e-2, f"dk[{b},{hk}]", rms_tol=6e-3)
+            _check(dv[b, hk], dv_ref[b, hk], 2e-2, f"dv[{b},{hk}]", rms_tol=6e-3)
 
 
 # ---------------------------------------------------------------------------
@@ -107,11 +125,11 @@ def test_decode_attention_config3_full_size():
     kf, vf = kc[:, :, :Sk].float(), vc[:, :, :Sk].float()
     s = (qf @ kf.transpose(-1, -2).contiguous()) * scale  # [B, Hkv, G, Sk]
     ref = (torch.softmax(s, dim=-1) @ vf).view(B, Hq, 1, D)
-    _check(out, ref, 2e-2, "decode")
+    _check(out, ref, 2e-2, "decode", rms_tol=5e-3)
     keep = torch.arange(Sk, device=DEV)[None, :] < lens[:, None].long()  # [B, Sk]
     s_l = s.masked_fill(~keep[:, None, None, :], float("-inf"))
     ref_l = (torch.softmax(s_l, dim=-1) @ vf).view(B, Hq, 1, D)
-    _check(out_l, ref_l, 2e-2, "decode with seqlens")
+    _check(out_l, ref_l, 2e-2, "decode with seqlens", rms_tol=5e-3)
 
 
 # ---------------------------------------------------------------------------
@@ -142,10 +160,10 @@ def test_dense_block_config2_full_size():
     loss_r = torch.nn.functional.cross_entropy(lr, labels)
     loss_r.backward()
     assert abs(float(loss) - float(loss_r)) <= 2e-3 * abs(float(loss_r))
-    _check(y, yr, 2e-2, "down output")
-    _check(logits, lr, 2e-2, "logits")
+    _check(y, yr, 2e-2, "down output", rms_tol=1e-2)
+    _check(logits, lr, 2e-2, "logits", rms_tol=1e-2)
     for name, a, r in (("x", x, xr), ("gate", wg, wgr), ("up", wu, wur), ("down", wd, wdr), ("lm_head", wl, wlr)):
-        _check(a.grad, r.grad, 3e-2, f"d{name}")
+        _check(a.grad, r.grad, 3e-2, f"d{name}", rms_tol=1e-2)
 
 
 # ---------------------------------------------------------------------------
@@ -190,7 +208,7 @@ def test_moe_experts_config4_full_size():
         inf = blk.experts_forward(x0, w, sel)
         ref_inf = loop()
     assert native_calls("qh_moe_up") == c_up + 1
-    _check(inf, ref_inf, 2e-2, "inference forward")
+    _check(inf, ref_inf, 2e-2, "inference forward", rms_tol=2e-3)
 
     def run(grouped):
         nonlocal x
@@ -204,10 +222,37 @@ def test_moe_experts_config4_full_size():
     out, gx, gw = run(True)
     rout, rgx, rgw = run(False)
     assert torch.equal(out, inf)  # the training forward is the inference forward plus saved G, U
-    _check(out, rout, 2e-2, "training forward")
-    _check(gx, rgx, 2e-2, "d input")
+    _check(out, rout, 2e-2, "training forward", rms_tol=2e-3)
+    _check(gx, rgx, 2e-2, "d input", rms_tol=1.5e-2)
     worst = max(_rel_err(a, b) for a, b in zip(gw, rgw))
     assert worst <= 3e-2, f"expert weight gradients: {worst:.3e}"
+
+    # the reference's expert loop (modules/moe.py:32-58: per expert, SwiGLU on its tokens' rows,
+    # times the routing weight, index_add into the output) in fp32 torch, with autograd
+    xr = x0.detach().float().requires_grad_(True)
+    wr = [p.detach().float().requires_grad_(True) for p in weights]
+    acc = torch.zeros((T, H), dtype=torch.float32, device=DEV)
+    wf = w.float()
+    for e in range(len(blk.experts)):
+        tok, slot = (sel == e).nonzero(as_tuple=True)
+        if tok.numel() == 0:
+            continue
+        g_w, u_w, d_w = wr[3 * e], wr[3 * e + 1], wr[3 * e + 2]
+        h = xr[tok]
+        y = (torch.nn.functional.silu(h @ g_w.t()) * (h @ u_w.t())) @ d_w.t()
+        acc = acc.index_add(0, tok, y * wf[tok, slot, None])
+    acc.backward(go.float())
+    _check(out, acc, 2e-2, "training forward vs fp32 loop", rms_tol=1.2e-2)
+    _check(gx, xr.grad, 2e-2, "d input vs fp32 loop", rms_tol=1.2e-2)
+    worst_f32, worst_rms = 0.0, 0.0
+    for a, r in zip(gw, wr):
+        if r.grad is None:  # an expert without tokens: exact zeros
+            assert not bool(a.any()), "expert without tokens has a nonzero weight gradient"
+            continue
+        worst_f32, worst_rms = max(worst_f32, _rel_err(a, r.grad)), max(worst_rms, _rms_err(a, r.grad))
+    print(f"[fullsize] config4 expert weight gradients vs fp32 loop: max-rel {worst_f32:.3e} rms-rel {worst_rms:.3e}",
+          flush=True)
+    assert worst_f32 <= 3e-2 and worst_rms <= 1.2e-2, f"expert weight gradients vs fp32 loop: {worst_f32:.3e}"
 
 
 # ---------------------------------------------------------------------------
@@ -352,15 +397,21 @@ def test_flash_attention_config4_full_size():
                 p = torch.exp(s - lse_ref[:, None])
                 o_ref = p @ vf
                 ds = p * ((dof @ vf.t().contiguous()) - (dof * o_ref).sum(-1, keepdim=True))
+                dq_ref = (ds @ kf) * scale
                 worst["o"] = max(worst["o"], _rel_err(o[b, h], o_ref))
                 worst["lse"] = max(worst["lse"], float((lse[b, h] - lse_ref).abs().max()))
-                worst["dq"] = max(worst["dq"], _rel_err(dq[b, h], (ds @ kf) * scale))
+                worst["dq"] = max(worst["dq"], _rel_err(dq[b, h], dq_ref))
+                for key, a, r in (("o_rms", o[b, h], o_ref), ("dq_rms", dq[b, h], dq_ref)):
+                    worst[key] = max(worst.get(key, 0.0), _rms_err(a, r))
                 dk_ref += (ds.t().contiguous() @ qf) * scale
                 dv_ref += p.t().contiguous() @ dof
             worst["dk"] = max(worst["dk"], _rel_err(dk[b, hk], dk_ref))
             worst["dv"] = max(worst["dv"], _rel_err(dv[b, hk], dv_ref))
-    print("config4 attention:", worst)
+            for key, a, r in (("dk_rms", dk[b, hk], dk_ref), ("dv_rms", dv[b, hk], dv_ref)):
+                worst[key] = max(worst.get(key, 0.0), _rms_err(a, r))
+    print("[fullsize] config4 attention:", worst, flush=True)
     assert worst["o"] <= 2e-2 and worst["dq"] <= 2e-2 and worst["dk"] <= 2e-2 and worst["dv"] <= 2e-2, worst
+    assert max(worst[k] for k in ("o_rms", "dq_rms", "dk_rms", "dv_rms")) <= 6e-3, worst
     assert worst["lse"] <= 1e-3, worst
 
 
@@ -480,8 +531,8 @@ def test_fused_lm_head_cross_entropy_config2_full_size():
     lf = torch.nn.functional.cross_entropy(xf @ wf.t().contiguous(), t)
     lf.backward()
     assert abs(float(loss) - float(lf)) <= 2e-3 * abs(float(lf)), (float(loss), float(lf))
-    _check(x.grad, xf.grad, 3e-2, "dX vs fp32")
-    _check(w.grad, wf.grad, 3e-2, "dW vs fp32")
+    _check(x.grad, xf.grad, 3e-2, "dX vs fp32", rms_tol=5e-3)
+    _check(w.grad, wf.grad, 3e-2, "dW vs fp32", rms_tol=5e-3)
     del xf, wf, lf
     torch.cuda.empty_cache()
     # unfused HIP path (logits materialised)
@@ -489,5 +540,5 @@ def test_fused_lm_head_cross_entropy_config2_full_size():
     lu = K.triton_cross_entropy(K.triton_matmul(xu, wu), t)
     lu.backward()
     assert abs(float(loss) - float(lu)) <= 1e-5 * abs(float(lu))
-    _check(x.grad, xu.grad, 1e-2, "dX vs unfused")
-    _check(w.grad, wu.grad, 1e-2, "dW vs unfused")
+    _check(x.grad, xu.grad, 1e-2, "dX vs unfused", rms_tol=1e-3)
+    _check(w.grad, wu.grad, 1e-2, "dW vs unfused", rms_tol=1e-3)
