@@ -91,7 +91,10 @@ struct NTile {
         lds_dma16_s(vo, at(RPI * n, k0), lds + (uint32_t)n * 1024u);
       }
     } else {
-      const int lane = threadIdx.x & 63;
+      // (the empty asm keeps the lane's clamped addresses inside this rarely taken
+      // branch: hoisted out of the k-loop they stay live in registers through it)
+      int lane = threadIdx.x & 63;
+      asm volatile("" : "+v"(lane));
       const int rin = lane / CPR;
       int kc = 8 * ((lane % CPR) ^ sw(RPI * wid + rin));
       if (kc > vk - 8) kc = vk - 8;  // vk is a positive multiple of 8
@@ -102,6 +105,29 @@ struct NTile {
         if (r > vrows - 1) r = vrows - 1;
         lds_dma16(at(r, k0 + kc), lds + (uint32_t)n * 1024u);
       }
+    }
+  }
+  // Split roles: wave wid also issues the instructions of wave wid + NWAVE/2, whose
+  // rows lie NWAVE/2 RPI rows further on at the same swizzle, so they take the same
+  // scalar row address with the lane offset vo2 = vo + shift(ld) (at() linear in the
+  // row with stride ld).
+  static __device__ __forceinline__ uint32_t shift(int64_t ld) {
+    return (uint32_t)((int64_t)(NWAVE / 2) * RPI * ld * (int64_t)sizeof(T));
+  }
+  template <class AT>
+  static __device__ __forceinline__ void issue2(uint32_t lds, const AT& at, int k0, int vrows, int vk, uint32_t vo,
+                                                uint32_t vo2, int wid) {
+    if (vrows >= ROWS && vk >= BK) {
+#pragma unroll
+      for (int i = 0; i < PW; ++i) {
+        const int n = wid + NWAVE * i;
+        const T* base = at(RPI * n, k0);
+        lds_dma16_s(vo, base, lds + (uint32_t)n * 1024u);
+        lds_dma16_s(vo2, base, lds + (uint32_t)(n + NWAVE / 2) * 1024u);
+      }
+    } else {
+      issue(lds, at, k0, vrows, vk, vo, wid);
+      issue(lds, at, k0, vrows, vk, vo2, wid + NWAVE / 2);
     }
   }
   // Row of the tile that this lane loads in DMA instruction i (its row pointer
@@ -167,7 +193,8 @@ struct TTile {
         lds_dma16_s(vo, at(0, k0 + n * RPI), lds + (uint32_t)n * 1024u);
       }
     } else {
-      const int lane = threadIdx.x & 63;
+      int lane = threadIdx.x & 63;
+      asm volatile("" : "+v"(lane));  // (as in NTile::issue)
       const int kin = lane / CPR, slot = lane % CPR;
 #pragma unroll
       for (int i = 0; i < PW; ++i) {
@@ -178,6 +205,27 @@ struct TTile {
         if (kr > vk - 1) kr = vk - 1;
         lds_dma16(at(col, k0 + kr), lds + (uint32_t)n * 1024u);
       }
+    }
+  }
+  // Split roles (as NTile::issue2): the instructions of wave wid + NWAVE/2 read the
+  // k-rows NWAVE/2 RPI further on at the same swizzle.
+  static __device__ __forceinline__ uint32_t shift(int64_t ld) {
+    return (uint32_t)((int64_t)(NWAVE / 2) * RPI * ld * (int64_t)sizeof(T));
+  }
+  template <class AT>
+  static __device__ __forceinline__ void issue2(uint32_t lds, const AT& at, int k0, int vcols, int vk, uint32_t vo,
+                                                uint32_t vo2, int wid) {
+    if (vcols >= COLS && vk >= BK) {
+#pragma unroll
+      for (int i = 0; i < PW; ++i) {
+        const int n = wid + NWAVE * i;
+        const T* base = at(0, k0 + n * RPI);
+        lds_dma16_s(vo, base, lds + (uint32_t)n * 1024u);
+        lds_dma16_s(vo2, base, lds + (uint32_t)(n + NWAVE / 2) * 1024u);
+      }
+    } else {
+      issue(lds, at, k0, vcols, vk, vo, wid);
+      issue(lds, at, k0, vcols, vk, vo2, wid + NWAVE / 2);
     }
   }
   static __device__ __forceinline__ void zero_k_tail(T* S, int vk) {
@@ -276,6 +324,18 @@ struct TileSkipRows : std::false_type {};
 template <class P>
 struct TileSkipRows<P, std::void_t<decltype(P::kSkipRows)>> : std::integral_constant<bool, P::kSkipRows> {};
 
+// Persistent problems with 16-byte row epilogues that define kSplitStores = true
+// split the wavefronts by role: waves 0 .. NWAVE/2-1 issue every operand load
+// (their own share of each k-tile and that of wave w + NWAVE/2), waves
+// NWAVE/2 .. NWAVE-1 every output store (their own staged rows and those of
+// wave w - NWAVE/2). vmcnt counts both loads and stores, so a wave that waits
+// for a k-tile also waits for its own earlier stores; with the split no wave
+// does both, and a tile's stores drain while the next tile computes.
+template <class P, class = void>
+struct TileSplitStores : std::false_type {};
+template <class P>
+struct TileSplitStores<P, std::void_t<decltype(P::kSplitStores)>> : std::integral_constant<bool, P::kSplitStores> {};
+
 template <typename T, int BM, int BN, int BK, int NS, bool AT, bool BT, class P>
 __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
   using TA = OpTile<T, BM, BK, AT>;
@@ -300,6 +360,8 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
   int t_local = 0, t_step = 0, t_end = 0, t_base = 0;
   constexpr bool kPersist = TilePersistent<P>::value;
   constexpr bool kGather = TileGatherA<P>::value;
+  constexpr bool kSplit = TileSplitStores<P>::value && kPersist && P::kVecEpilogue;
+  static_assert(!(kSplit && kGather), "split roles: k-contiguous row loads");
   static_assert(!(kGather && (kPersist || AT)), "gathered A rows: k-contiguous A, one tile per workgroup");
   if constexpr (kPersist) {
     t_end = (p.tiles_total() + 7) / 8;
@@ -322,6 +384,10 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
   constexpr int NM = TM * TN;
   auto stage = [&](int kt) { return smem + (kt % NS) * STAGE; };
   const uint32_t voa = TA::voff(c.lda, wid), vob = TB::voff(c.ldb, wid);
+  const bool storer = kSplit && wid >= NWAVE / 2;  // wave-uniform
+  // kSplit: lane offsets of the load share of wave wid + NWAVE/2, issued by this (loading) wave
+  const uint32_t voa2 = kSplit ? voa + TA::shift(c.lda) : 0u;
+  const uint32_t vob2 = kSplit ? vob + TB::shift(c.ldb) : 0u;
   // Gathered A: the lane's row pointers, taken once for the tile (rows past
   // the valid ones repeat the last valid row; the epilogue drops them).
   const T* arow[kGather ? TA::PW : 1];
@@ -332,22 +398,43 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
       arow[i] = p.a_row(c, r < c.vm ? r : c.vm - 1);
     }
   }
-  auto issue_for = [&](const TileCtx<T>& cc, int kt, uint32_t va, uint32_t vb) {
+  // the load share of wave w (lane offsets va, vb) of k-tile kt of tile cc
+  auto issue_share = [&](const TileCtx<T>& cc, int kt, uint32_t va, uint32_t vb, int w) {
     const int k0 = kt * BK;
     const int vk = cc.K - k0;
     const uint32_t base = lds0 + (uint32_t)((kt % NS) * STAGE * (int)sizeof(T));
-    if constexpr (kGather) TA::issue_rows(base, arow, k0, vk, wid);
-    else TA::issue(base, [&](int i, int k) { return p.a_at(cc, i, k); }, k0, cc.vm, vk, va, wid);
+    if constexpr (kGather) TA::issue_rows(base, arow, k0, vk, w);
+    else TA::issue(base, [&](int i, int k) { return p.a_at(cc, i, k); }, k0, cc.vm, vk, va, w);
     TB::issue(base + (uint32_t)(TA::ELEMS * sizeof(T)), [&](int i, int k) { return p.b_at(cc, i, k); }, k0, cc.vn, vk,
-              vb, wid);
+              vb, w);
   };
-  auto issue = [&](int kt) { issue_for(c, kt, voa, vob); };
+  auto issue_for = [&](const TileCtx<T>& cc, int kt) {
+    if constexpr (kSplit) {
+      if (!storer) {
+        const int k0 = kt * BK;
+        const int vk = cc.K - k0;
+        const uint32_t base = lds0 + (uint32_t)((kt % NS) * STAGE * (int)sizeof(T));
+        TA::issue2(base, [&](int i, int k) { return p.a_at(cc, i, k); }, k0, cc.vm, vk, voa, voa2, wid);
+        TB::issue2(base + (uint32_t)(TA::ELEMS * sizeof(T)), [&](int i, int k) { return p.b_at(cc, i, k); }, k0,
+                   cc.vn, vk, vob, vob2, wid);
+      }
+    } else {
+      issue_share(cc, kt, voa, vob, wid);
+    }
+  };
+  auto issue = [&](int kt) { issue_for(c, kt); };
   // Make k-tile kt visible to every wave, with `after` later tiles still in flight.
+  // (kSplit: loader waves issue two shares per k-tile; store waves issue no load, so they
+  // do not wait on vmcnt, which counts their stores)
+  constexpr int NPW = kSplit ? 2 * NPT : NPT;
+  static_assert(3 * NPW <= 63, "vmcnt");
   auto land = [&](int kt, int after) {
-    if (after <= 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    else if (after == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(NPT));
-    else if (after == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NPT));
-    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * NPT));
+    if (!storer) {
+      if (after <= 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      else if (after == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(NPW));
+      else if (after == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NPW));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * NPW));
+    }
     __syncthreads();
     const int vk = c.K - kt * BK;
     if (vk < BK) {
@@ -394,7 +481,9 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
       const int pro = nk < NS ? nk : NS;
       if (warm) {
         // k-tile 0 is in flight with the previous tile's epilogue stores (vmcnt
-        // counts both): wait for all of them, then fill the other stages
+        // counts both; with split roles the loading waves store nothing): wait
+        // for all of them, then fill the other stages (stage 1 held the staged
+        // rows until this barrier)
         land(0, 0);
         for (int t = 1; t < pro; ++t) issue(t);
       } else {
@@ -437,9 +526,42 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
       // epilogue stages its rows through stage 1 (two halves of 64 rows per wave)
       // or stores straight from registers.
       __syncthreads();  // every wave is done with the operand stages
-      if ((cn.K + BK - 1) / BK > 0) issue_for(cn, 0, voa, vob);  // strides are the same for every tile
+      if ((cn.K + BK - 1) / BK > 0) issue_for(cn, 0);  // strides are the same for every tile
       bool staged = false;
-      if constexpr (P::kVecEpilogue) {
+      if constexpr (kSplit) {
+        if (p.vec_ok()) {
+          // every wave stages its rows, then the store waves write the rows of two waves each
+          static_assert(TM % 2 == 0 && NWAVE * (WTM / 2) * WTN <= STAGE, "half tiles fill one stage");
+          EpiTile<T, WTM / 2, WTN> et{smem + STAGE + wid * ((WTM / 2) * WTN)};
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < TM / 2; ++i)
+#pragma unroll
+              for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                  for (int r = 0; r < 4; ++r)
+                    et.put(32 * i + 4 * (lane >> 5) + 8 * g + r, 32 * j + (lane & 31),
+                           from_f32<T>(acc[h * (TM / 2) + i][j][4 * g + r]));
+            __syncthreads();  // (waits for this wave's LDS writes) every wave's half is staged
+            if (storer) {
+#pragma unroll
+              for (int o = 0; o < 2; ++o) {
+                const int src = o == 0 ? wid : wid - NWAVE / 2;
+                EpiTile<T, WTM / 2, WTN> es{smem + STAGE + src * ((WTM / 2) * WTN)};
+                p.template epilogue_vec<WTM / 2>(c, es, (src / WGN) * WTM + h * (WTM / 2), (src % WGN) * WTN, lane);
+              }
+              __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the staged rows are read
+            }
+            // the first half is read before the second is staged; the second before the next
+            // tile's k-tile 1 is loaded into this stage (after the barrier of its k-tile 0)
+            if (h == 0) __syncthreads();
+          }
+          staged = true;
+        }
+      } else if constexpr (P::kVecEpilogue) {
         if (p.vec_ok()) {
           static_assert(TM % 2 == 0 && NWAVE * (WTM / 2) * WTN <= STAGE, "half tiles fill one stage");
           EpiTile<T, WTM / 2, WTN> et{smem + STAGE + wid * ((WTM / 2) * WTN)};
@@ -509,6 +631,7 @@ struct DenseProblem {
 
   static constexpr bool kVecEpilogue = std::is_same<OT, T>::value && !ACC;
   static constexpr bool kPersistent = true;
+  static constexpr bool kSplitStores = true;
   // 16-byte row stores write 8 columns at once: only without bias, with N and ldc multiples of 8
   // and C 16-byte aligned (else a row's last chunk would run into the next row)
   __device__ __forceinline__ bool vec_ok() const {
