@@ -638,13 +638,20 @@ struct DenseProblem {
     return bias == nullptr && (N & 7) == 0 && (ldc & 7) == 0 && ((uintptr_t)C & 15) == 0;
   }
   // ROWS rows of 64 columns staged in et, written at tile rows wr.., columns wc..
+  // All of the lane's staged rows are read before its first store: one LDS round trip per call,
+  // not one per 16-byte store.
   template <int ROWS = 128, class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
-    for (int q = lane; q < ROWS * 8; q += 64) {
-      const int r = q >> 3, c8 = q & 7;
-      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
-      if (row < M && col < N) st16(reinterpret_cast<T*>(C) + (int64_t)row * ldc + col, et.row8(r, c8));
-    }
+    constexpr int NQ = ROWS / 8;  // lane rows lane / 8 + 8 u, columns 8 (lane % 8) ..
+    const int r0 = lane >> 3, c8 = lane & 7;
+    const int col = c.n0 + wc + 8 * c8;
+    Vec16<T> v[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) v[u] = et.row8(r0 + 8 * u, c8);
+    T* p0 = reinterpret_cast<T*>(C) + (int64_t)(c.m0 + wr + r0) * ldc + col;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+      if (c.m0 + wr + r0 + 8 * u < M && col < N) st16(p0 + (int64_t)(8 * u) * ldc, v[u]);
   }
   __device__ __forceinline__ int tiles_total() const { return tiles_m * tiles_n; }
   // Logical tile t (grouped by 8 M-tiles) of the output; false past the last.
