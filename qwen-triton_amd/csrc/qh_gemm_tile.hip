@@ -331,10 +331,17 @@ struct TileSkipRows<P, std::void_t<decltype(P::kSkipRows)>> : std::integral_cons
 // wave w - NWAVE/2). vmcnt counts both loads and stores, so a wave that waits
 // for a k-tile also waits for its own earlier stores; with the split no wave
 // does both, and a tile's stores drain while the next tile computes.
+// The store waves call the problem's epilogue_store(); problems that also define
+// kSplitReduce = true give the loading waves epilogue_reduce() on the same two
+// staged half-tiles (row reductions beside the stores).
 template <class P, class = void>
 struct TileSplitStores : std::false_type {};
 template <class P>
 struct TileSplitStores<P, std::void_t<decltype(P::kSplitStores)>> : std::integral_constant<bool, P::kSplitStores> {};
+template <class P, class = void>
+struct TileSplitReduce : std::false_type {};
+template <class P>
+struct TileSplitReduce<P, std::void_t<decltype(P::kSplitReduce)>> : std::integral_constant<bool, P::kSplitReduce> {};
 
 template <typename T, int BM, int BN, int BK, int NS, bool AT, bool BT, class P>
 __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
@@ -531,7 +538,7 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
       if constexpr (kSplit) {
         if (p.vec_ok()) {
           // every wave stages its rows, then the store waves write the rows of two waves each
-          static_assert(TM % 2 == 0 && NWAVE * (WTM / 2) * WTN <= STAGE, "half tiles fill one stage");
+          static_assert(TM % 2 == 0 && NWAVE * (WTM / 2) * WTN <= (NS - 1) * STAGE, "half tiles fit past stage 0");
           EpiTile<T, WTM / 2, WTN> et{smem + STAGE + wid * ((WTM / 2) * WTN)};
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
@@ -551,7 +558,17 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
               for (int o = 0; o < 2; ++o) {
                 const int src = o == 0 ? wid : wid - NWAVE / 2;
                 EpiTile<T, WTM / 2, WTN> es{smem + STAGE + src * ((WTM / 2) * WTN)};
-                p.template epilogue_vec<WTM / 2>(c, es, (src / WGN) * WTM + h * (WTM / 2), (src % WGN) * WTN, lane);
+                p.template epilogue_store<WTM / 2>(c, es, (src / WGN) * WTM + h * (WTM / 2), (src % WGN) * WTN,
+                                                   lane);
+              }
+              __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the staged rows are read
+            } else if constexpr (TileSplitReduce<P>::value) {
+#pragma unroll
+              for (int o = 0; o < 2; ++o) {
+                const int src = o == 0 ? wid : wid + NWAVE / 2;
+                EpiTile<T, WTM / 2, WTN> es{smem + STAGE + src * ((WTM / 2) * WTN)};
+                p.template epilogue_reduce<WTM / 2>(c, es, (src / WGN) * WTM + h * (WTM / 2), (src % WGN) * WTN,
+                                                    lane);
               }
               __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the staged rows are read
             }
@@ -563,7 +580,7 @@ __global__ __launch_bounds__(NTHR) void gemm_tile_kernel(P p) {
         }
       } else if constexpr (P::kVecEpilogue) {
         if (p.vec_ok()) {
-          static_assert(TM % 2 == 0 && NWAVE * (WTM / 2) * WTN <= STAGE, "half tiles fill one stage");
+          static_assert(TM % 2 == 0 && NWAVE * (WTM / 2) * WTN <= (NS - 1) * STAGE, "half tiles fit past stage 0");
           EpiTile<T, WTM / 2, WTN> et{smem + STAGE + wid * ((WTM / 2) * WTN)};
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
@@ -638,6 +655,10 @@ struct DenseProblem {
     return bias == nullptr && (N & 7) == 0 && (ldc & 7) == 0 && ((uintptr_t)C & 15) == 0;
   }
   // ROWS rows of 64 columns staged in et, written at tile rows wr.., columns wc..
+  template <int ROWS, class ET>
+  __device__ __forceinline__ void epilogue_store(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
+    epilogue_vec<ROWS>(c, et, wr, wc, lane);
+  }
   // All of the lane's staged rows are read before its first store: one LDS round trip per call,
   // not one per 16-byte store.
   template <int ROWS = 128, class ET>
@@ -1500,6 +1521,9 @@ struct LmceLogitsProblem {
 
   static constexpr bool kVecEpilogue = true;
   static constexpr bool kPersistent = true;
+  // persistent hand-over: store waves write the logits, loading waves form the row partials
+  static constexpr bool kSplitStores = true;
+  static constexpr bool kSplitReduce = true;
   __device__ __forceinline__ bool vec_ok() const { return true; }
   __device__ __forceinline__ int tiles_total() const { return tiles_m * tiles_n; }
   __device__ __forceinline__ bool tile_at(int t, TileCtx<T>& c) const {
@@ -1524,17 +1548,54 @@ struct LmceLogitsProblem {
   }
   template <int ROWS = 128, class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
-    for (int q = lane; q < ROWS * 8; q += 64) {  // the rounded logits, 8 lanes per 128-byte row piece
-      const int r = q >> 3, c8 = q & 7;
-      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
-      if (row < M && col < N) st16(Z + (int64_t)row * ldz + col, et.row8(r, c8));
+    epilogue_store<ROWS>(c, et, wr, wc, lane);
+    epilogue_reduce<ROWS>(c, et, wr, wc, lane);
+  }
+  template <int ROWS, class ET>
+  __device__ __forceinline__ void epilogue_store(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
+    {
+      // the rounded logits, 8 lanes per 128-byte row piece; all of the lane's staged pieces
+      // are read before its first store (one LDS round trip, not one per store)
+      constexpr int NQ = ROWS / 8;
+      const int r0 = lane >> 3, c8 = lane & 7;
+      const int col = c.n0 + wc + 8 * c8;
+      Vec16<T> v[NQ];
+#pragma unroll
+      for (int u = 0; u < NQ; ++u) v[u] = et.row8(r0 + 8 * u, c8);
+      T* p0 = Z + (int64_t)(c.m0 + wr + r0) * ldz + col;
+#pragma unroll
+      for (int u = 0; u < NQ; ++u)
+        if (c.m0 + wr + r0 + 8 * u < M && col < N) st16(p0 + (int64_t)(8 * u) * ldz, v[u]);
     }
+  }
+  // (max, sum of exp) of each staged row's piece of up to 64 columns, one row per lane
+  template <int ROWS, class ET>
+  __device__ __forceinline__ void epilogue_reduce(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
     const int ncol = max(0, min(64, c.vn - wc));
     const int blk = (c.n0 + wc) >> 6;
     for (int r = lane; r < ROWS; r += 64) {
       const int row = c.m0 + wr + r;
       if (row >= M || ncol == 0) continue;
       float m = -INFINITY, sum = 0.f;
+      if (ncol == 64) {
+        // a whole 64-column piece: the row's 8 pieces read at once, its max first, then one
+        // exp per value
+        Vec16<T> v[8];
+#pragma unroll
+        for (int c8 = 0; c8 < 8; ++c8) v[c8] = et.row8(r, c8);
+#pragma unroll
+        for (int c8 = 0; c8 < 8; ++c8)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) m = fmaxf(m, to_f32(v[c8].v[e]));
+        if (m != -INFINITY) {
+#pragma unroll
+          for (int c8 = 0; c8 < 8; ++c8)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += __expf(to_f32(v[c8].v[e]) - m);
+        }
+        part[(int64_t)blk * M + row] = make_float2(m, sum);
+        continue;
+      }
 #pragma unroll
       for (int c8 = 0; c8 < 8; ++c8) {
         if (8 * c8 >= ncol) break;
