@@ -929,14 +929,22 @@ struct MoeUpProblem {
   __device__ __forceinline__ bool vec_ok() const { return true; }
   // Wavefront tile columns 0..31 hold gate and 32..63 up values of the same 32
   // features.
+  // (all of the lane's staged pieces are read before its first store: one LDS round trip)
   template <class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
     const int row_end = c.m0 + c.vm;
-    for (int q = lane; q < 128 * 4; q += 64) {
-      const int r = q >> 2, c8 = q & 3;
-      const int row = c.m0 + wr + r;
+    const int r0 = lane >> 2, c8 = lane & 3;  // lane rows r0 + 16 u
+    Vec16<T> gvs[8], uvs[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      gvs[u] = et.row8(r0 + 16 * u, c8);
+      uvs[u] = et.row8(r0 + 16 * u, c8 + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int row = c.m0 + wr + r0 + 16 * u;
       if (row >= row_end) continue;
-      const Vec16<T> gv = et.row8(r, c8), uv = et.row8(r, c8 + 4);
+      const Vec16<T> gv = gvs[u], uv = uvs[u];
       Vec16<T> hv;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -1022,36 +1030,68 @@ struct MoeRowProblem {
   }
   static constexpr bool kVecEpilogue = true;
   __device__ __forceinline__ bool vec_ok() const { return true; }
+  // The lane's staged pieces are read 8 at a time, and their rows' routing weights or SiLU
+  // inputs loaded (from clamped rows, unconditionally), before the first of their stores: a
+  // store may alias a later load for the compiler, which would otherwise wait out one round
+  // trip per row.
   template <class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
     const int row_end = c.m0 + c.vm;
-    for (int q = lane; q < 128 * 8; q += 64) {
-      const int r = q >> 3, c8 = q & 7;
-      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
-      if (row >= row_end || col >= N) continue;
-      const Vec16<T> v = et.row8(r, c8);
-      const int64_t o = (int64_t)row * ldc + col;
+    const int r0 = lane >> 3, c8 = lane & 7;  // lane rows r0 + 8 u
+    const int col = c.n0 + wc + 8 * c8;
+    const int colc = col < N ? col : N - 8;  // N is a multiple of 8
+#pragma unroll
+    for (int u0 = 0; u0 < 16; u0 += 8) {
+      Vec16<T> vs[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) vs[u] = et.row8(r0 + 8 * (u0 + u), c8);
       if constexpr (EPI == 0) {
-        st16(C + o, v);
-      } else if constexpr (EPI == 1) {
-        const float w = to_f32(wrow[row]);
-        Vec16<T> out;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) out.v[e] = from_f32<T>(to_f32(v.v[e]) * w);
-        st16(C + o, out);
-      } else {
-        const int64_t og = (int64_t)row * ldg + col;
-        const Vec16<T> gv = ld16(G + og), uv = ld16(U + og);
-        Vec16<T> dg, du;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float go = to_f32(v.v[e]), gf = to_f32(gv.v[e]), uf = to_f32(uv.v[e]);
-          const float sg = sigmoidf_(gf);
-          dg.v[e] = from_f32<T>(go * uf * sg * (1.f + gf * (1.f - sg)));
-          du.v[e] = from_f32<T>(go * gf * sg);
+        for (int u = 0; u < 8; ++u) {
+          const int row = c.m0 + wr + r0 + 8 * (u0 + u);
+          if (row < row_end && col < N) st16(C + (int64_t)row * ldc + col, vs[u]);
         }
-        st16(C + o, dg);
-        st16(C2 + o, du);
+      } else if constexpr (EPI == 1) {
+        float w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int row = c.m0 + wr + r0 + 8 * (u0 + u);
+          w[u] = to_f32(wrow[row < row_end ? row : row_end - 1]);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int row = c.m0 + wr + r0 + 8 * (u0 + u);
+          if (row >= row_end || col >= N) continue;
+          Vec16<T> out;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) out.v[e] = from_f32<T>(to_f32(vs[u].v[e]) * w[u]);
+          st16(C + (int64_t)row * ldc + col, out);
+        }
+      } else {
+        Vec16<T> gv[8], uv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int row = c.m0 + wr + r0 + 8 * (u0 + u);
+          const int64_t og = (int64_t)(row < row_end ? row : row_end - 1) * ldg + colc;
+          gv[u] = ld16(G + og);
+          uv[u] = ld16(U + og);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int row = c.m0 + wr + r0 + 8 * (u0 + u);
+          if (row >= row_end || col >= N) continue;
+          Vec16<T> dg, du;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float go = to_f32(vs[u].v[e]), gf = to_f32(gv[u].v[e]), uf = to_f32(uv[u].v[e]);
+            const float sg = sigmoidf_(gf);
+            dg.v[e] = from_f32<T>(go * uf * sg * (1.f + gf * (1.f - sg)));
+            du.v[e] = from_f32<T>(go * gf * sg);
+          }
+          const int64_t o = (int64_t)row * ldc + col;
+          st16(C + o, dg);
+          st16(C2 + o, du);
+        }
       }
     }
   }
@@ -1126,13 +1166,19 @@ struct MoeDxProblem {
   }
   static constexpr bool kVecEpilogue = true;
   __device__ __forceinline__ bool vec_ok() const { return true; }
+  // (all of the lane's staged pieces are read before its first store: one LDS round trip)
   template <class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
     const int row_end = c.m0 + c.vm;
-    for (int q = lane; q < 128 * 8; q += 64) {
-      const int r = q >> 3, c8 = q & 7;
-      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
-      if (row < row_end && col < N) st16(C + (int64_t)row * ldc + col, et.row8(r, c8));
+    const int r0 = lane >> 3, c8 = lane & 7;  // lane rows r0 + 8 u
+    const int col = c.n0 + wc + 8 * c8;
+    Vec16<T> v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = et.row8(r0 + 8 * u, c8);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int row = c.m0 + wr + r0 + 8 * u;
+      if (row < row_end && col < N) st16(C + (int64_t)row * ldc + col, v[u]);
     }
   }
   template <int TM, int TN>
@@ -1208,10 +1254,16 @@ struct MoeWgradProblem {
   template <class ET>
   __device__ __forceinline__ void epilogue_vec(const TileCtx<T>& c, const ET& et, int wr, int wc, int lane) const {
     T* out = c.out + (int64_t)c.aux * out_stride;
-    for (int q = lane; q < 128 * 8; q += 64) {
-      const int r = q >> 3, c8 = q & 7;
-      const int row = c.m0 + wr + r, col = c.n0 + wc + 8 * c8;
-      if (row < M && col < N) st16(out + (int64_t)row * ldo + col, et.row8(r, c8));
+    // (all of the lane's staged pieces are read before its first store: one LDS round trip)
+    const int r0 = lane >> 3, c8 = lane & 7;  // lane rows r0 + 8 u
+    const int col = c.n0 + wc + 8 * c8;
+    Vec16<T> v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) v[u] = et.row8(r0 + 8 * u, c8);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int row = c.m0 + wr + r0 + 8 * u;
+      if (row < M && col < N) st16(out + (int64_t)row * ldo + col, v[u]);
     }
   }
   template <int TM, int TN>
