@@ -864,6 +864,17 @@ __device__ __forceinline__ int xcd_logical_tile() {
   return (nblk & 7) == 0 ? (pid & 7) * (nblk >> 3) + (pid >> 3) : pid;
 }
 
+// As xcd_logical_tile, over the first `total` logical tiles of a grid sized for
+// an upper bound of the tile count: each XCD takes a run of ceil(total / 8), so
+// the surplus workgroups (which exit, -1) do not all fall on the last XCDs.
+__device__ __forceinline__ int xcd_logical_tile_of(int total) {
+  const int pid = blockIdx.x, nblk = gridDim.x;
+  if ((nblk & 7) != 0) return pid < total ? pid : -1;
+  const int per = (total + 7) >> 3;  // nblk / 8 >= per: the grid covers the bound
+  const int local = pid >> 3, t = (pid & 7) * per + local;
+  return local < per && t < total ? t : -1;
+}
+
 // M-tile tm of the expert-sorted rows: expert e, first row, valid rows.
 __device__ __forceinline__ bool seg_tile(const int32_t* seg, const int32_t* toff, int E, int tm, int& e, int& row0,
                                          int& rows) {
@@ -899,9 +910,9 @@ struct MoeUpProblem {
   int64_t ldx, ldw, ldo;
   int E, I, Kdim, tiles_n;
   __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
-    const int t = xcd_logical_tile();
+    const int t = xcd_logical_tile_of(toff[E] * tiles_n);
     int e, row0, rows;
-    if (!seg_tile(seg, toff, E, t / tiles_n, e, row0, rows)) return false;
+    if (t < 0 || !seg_tile(seg, toff, E, t / tiles_n, e, row0, rows)) return false;
     c.m0 = row0;
     c.n0 = (t % tiles_n) * 128;
     c.K = Kdim;
@@ -1007,9 +1018,9 @@ struct MoeRowProblem {
   int64_t lda, ldw, ldc, ldg;
   int E, N, Kdim, tiles_n;
   __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
-    const int t = xcd_logical_tile();
+    const int t = xcd_logical_tile_of(toff[E] * tiles_n);
     int e, row0, rows;
-    if (!seg_tile(seg, toff, E, t / tiles_n, e, row0, rows)) return false;
+    if (t < 0 || !seg_tile(seg, toff, E, t / tiles_n, e, row0, rows)) return false;
     c.m0 = row0;
     c.n0 = (t % tiles_n) * 256;
     c.K = Kdim;
@@ -1143,9 +1154,9 @@ struct MoeDxProblem {
   int64_t ldg, ldw, ldc;
   int E, I, N, tiles_n;
   __device__ __forceinline__ bool tile(TileCtx<T>& c) const {
-    const int t = xcd_logical_tile();
+    const int t = xcd_logical_tile_of(toff[E] * tiles_n);
     int e, row0, rows;
-    if (!seg_tile(seg, toff, E, t / tiles_n, e, row0, rows)) return false;
+    if (t < 0 || !seg_tile(seg, toff, E, t / tiles_n, e, row0, rows)) return false;
     c.m0 = row0;
     c.n0 = (t % tiles_n) * 256;
     c.K = 2 * I;
