@@ -230,15 +230,18 @@ __global__ __launch_bounds__(256) void kv_write_vec(T* __restrict__ cache, int64
     const int64_t row = i / vpr, d = (i - row * vpr) * VN;
     const int64_t s = row % S, bh = row / S;
     const int64_t h = bh % H, b = bh / H;
+    // the value's address does not depend on its position: both loads are in flight at once
+    const Vec16<T> v = ld16(val + b * svb + h * svh + s * svs + d);
     const int64_t p = pos[s];
     if (p < 0 || p >= cap) continue;
-    st16(cache + b * scb + h * sch + p * scs + d, ld16(val + b * svb + h * svh + s * svs + d));
+    st16(cache + b * scb + h * sch + p * scs + d, v);
   }
 }
 
 // The same write for planes of at least kKvPlaneMin 16-byte chunks per (sequence, head):
 // blockIdx.y is the (b, h) pair, so the chunk index needs one 32-bit division (by the
-// chunks per row), and each thread has kKvPlaneU loads in flight before its stores.
+// chunks per row), and each thread has kKvPlaneU value loads and their position loads in
+// flight at once (chunks past the plane load its last chunk and store nothing).
 constexpr int kKvPlaneU = 4, kKvPlaneMin = 1024;
 
 template <typename T>
@@ -253,23 +256,19 @@ __global__ __launch_bounds__(256) void kv_write_plane(T* __restrict__ cache, int
   const int plane = S * vpr;
   const int base = (int)blockIdx.x * (256 * kKvPlaneU) + (int)threadIdx.x;
   Vec16<T> t[kKvPlaneU];
-  int64_t dst[kKvPlaneU];
+  int64_t p[kKvPlaneU];
+  int d[kKvPlaneU];
 #pragma unroll
   for (int u = 0; u < kKvPlaneU; ++u) {
-    const int i = base + u * 256;
-    dst[u] = -1;
-    if (i < plane) {
-      const int s = i / vpr, d = (i - s * vpr) * VN;
-      const int64_t p = pos[s];
-      if (p >= 0 && p < cap) {
-        t[u] = ld16(vb + s * svs + d);
-        dst[u] = p * scs + d;
-      }
-    }
+    const int i = min(base + u * 256, plane - 1);
+    const int s = i / vpr;
+    d[u] = (i - s * vpr) * VN;
+    t[u] = ld16(vb + s * svs + d[u]);
+    p[u] = pos[s];
   }
 #pragma unroll
   for (int u = 0; u < kKvPlaneU; ++u)
-    if (dst[u] >= 0) st16(cb + dst[u], t[u]);
+    if (base + u * 256 < plane && p[u] >= 0 && p[u] < cap) st16(cb + p[u] * scs + d[u], t[u]);
 }
 
 template <typename T>
