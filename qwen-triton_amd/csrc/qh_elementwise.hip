@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256) void kv_write_vec(T* __restrict__ cache, int64
 // blockIdx.y is the (b, h) pair, so the chunk index needs one 32-bit division (by the
 // chunks per row), and each thread has kKvPlaneU value loads and their position loads in
 // flight at once (chunks past the plane load its last chunk and store nothing).
-constexpr int kKvPlaneU = 4, kKvPlaneMin = 1024;
+constexpr int kKvPlaneU = 2, kKvPlaneMin = 1024;
 
 template <typename T>
 __global__ __launch_bounds__(256) void kv_write_plane(T* __restrict__ cache, int64_t scb, int64_t sch, int64_t scs,
