@@ -947,14 +947,17 @@ def main() -> None:
     torch.cuda.empty_cache()
     others = {}
     if not args.no_other_configs:
-        # the other BASELINE configs' kernels, timed compactly (HIP events / host clock around synchronised steps)
-        others["config1_fa"] = bench_fa(5, 2)
+        # the other BASELINE configs' kernels, timed compactly (HIP events / host clock around synchronised steps).
+        # Each phase starts on a GPU that idled while the host built it: three warm-up steps and ten timed
+        # ones (the first steps after an idle gap run slower; config 4's expert path measured 6.4-6.5 ms
+        # over 3 steps after 1 warm-up against 5.36 over 10 after 3)
+        others["config1_fa"] = bench_fa(10, 3)
         log(f"config 1: {others['config1_fa']}")
         torch.cuda.empty_cache()
-        others["config2_dense"] = bench_dense(3, 1)
+        others["config2_dense"] = bench_dense(10, 3)
         log(f"config 2: {others['config2_dense']}")
         torch.cuda.empty_cache()
-        others["config4_moe"] = bench_moe(3, 1, loop_reps=0)
+        others["config4_moe"] = bench_moe(10, 3, loop_reps=0)
         log(f"config 4: {others['config4_moe']}")
         torch.cuda.empty_cache()
     ms = graph_ms if graph_ms is not None else eager_ms
