@@ -666,6 +666,75 @@ extern "C" int qh_embedding_bwd(const int64_t* ids, const void* gout, void* gw, 
   return QH_OK;
 }
 
+// index_add of at most kIdxScanMax source rows in one launch, without the sort: wave i loads
+// all n indices at once (one round trip) and exits unless position i is the first of its row;
+// else it lists the row's positions in source order (a ballot per 64 positions) and adds those
+// source rows onto the row in that order (fp32, rounded once): the sums of the sorted path.
+// Any one wave scans n indices, so the launch reads n^2 indices from the L2 (32 MB at n = 2048).
+constexpr int kIdxScanMax = 2048;
+
+template <typename T>
+__global__ __launch_bounds__(256) void index_add_scan(T* __restrict__ dst, int64_t stride_d, const T* __restrict__ src,
+                                                      int64_t stride_s, const int64_t* __restrict__ idx, int n,
+                                                      int64_t n_target, int64_t D) {
+  constexpr int NB = kIdxScanMax / 64;
+  __shared__ uint32_t runs[4][kIdxScanMax];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int i = (int)blockIdx.x * 4 + wid;
+  if (i >= n) return;
+  // every index load (clamped positions, unconditional) is issued before the first is used:
+  // the empty asm keeps the compiler from sinking each into the block that tests it
+  int64_t r = idx[i];
+  int64_t v[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) v[b] = idx[min(b * 64 + lane, n - 1)];
+  asm volatile("" : "+v"(r));
+#pragma unroll
+  for (int b = 0; b < NB; ++b) asm volatile("" : "+v"(v[b]));
+  if (r < 0 || r >= n_target) return;
+  uint32_t* run = runs[wid];
+  int cnt = 0;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b * 64 >= n) break;
+    const uint64_t m = __ballot(b * 64 + lane < n && v[b] == r);
+    const int p0 = b * 64;
+    // positions p0 + bit below i that hold the row: i is not its first position
+    const int below = i - p0;  // bits [0, below) lie before i
+    const uint64_t before = below <= 0 ? 0ull : (below >= 64 ? ~0ull : ((1ull << below) - 1));
+    if (m & before) return;
+    const uint64_t after = m & ~before;
+    if ((after >> lane) & 1ull) run[cnt + __popcll(after & ((1ull << lane) - 1))] = (uint32_t)(p0 + lane);
+    cnt += __popcll(after);
+  }
+  __builtin_amdgcn_wave_barrier();  // (LDS runs in order within the wave: the list is written before it is read)
+  // four 8-column chunks per lane at a time (clamped to the row, so every load is issued; only
+  // the stores are guarded): the row's chunks and each source row's chunks load together
+  constexpr int CW = 4;
+  T* drow = dst + r * stride_d;
+  for (int64_t c0 = lane * 8; c0 < D; c0 += 64 * 8 * CW) {
+    int64_t cw[CW];
+#pragma unroll
+    for (int w = 0; w < CW; ++w) cw[w] = min(c0 + (int64_t)w * 512, D - 8);
+    float acc[CW][8];
+#pragma unroll
+    for (int w = 0; w < CW; ++w) ld8f(drow + cw[w], acc[w]);
+    for (int j = 0; j < cnt; ++j) {
+      const T* srow = src + (int64_t)run[j] * stride_s;
+      float t[CW][8];
+#pragma unroll
+      for (int w = 0; w < CW; ++w) ld8f(srow + cw[w], t[w]);
+#pragma unroll
+      for (int w = 0; w < CW; ++w)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[w][q] += t[w][q];
+    }
+#pragma unroll
+    for (int w = 0; w < CW; ++w)
+      if (c0 + w * 512 < D) st8f(drow + c0 + w * 512, acc[w]);
+  }
+}
+
 extern "C" int qh_index_add(void* target, int64_t stride_t, const void* src, int64_t stride_s, const int64_t* index,
                             int64_t n_src, int64_t n_target, int64_t D, void* ws, int64_t ws_bytes, int dtype,
                             void* stream) {
@@ -673,6 +742,27 @@ extern "C" int qh_index_add(void* target, int64_t stride_t, const void* src, int
   QH_CHECK_ARG(n_target < (1ll << 31) - 1 && n_src < (1ll << 31), "qh_index_add: sizes exceed 2^31");
   if (n_src == 0 || D == 0 || n_target == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;
+  const bool vec = D % 8 == 0 && stride_s % 8 == 0 && stride_t % 8 == 0 && aligned16(src) && aligned16(target);
+  if (vec && n_src <= kIdxScanMax) {
+    const unsigned grid = (unsigned)((n_src + 3) / 4);
+    switch (dtype) {
+      case QH_F32:
+        index_add_scan<float><<<grid, 256, 0, st>>>((float*)target, stride_t, (const float*)src, stride_s, index,
+                                                    (int)n_src, n_target, D);
+        break;
+      case QH_F16:
+        index_add_scan<f16_t><<<grid, 256, 0, st>>>((f16_t*)target, stride_t, (const f16_t*)src, stride_s, index,
+                                                    (int)n_src, n_target, D);
+        break;
+      case QH_BF16:
+        index_add_scan<bf16_t><<<grid, 256, 0, st>>>((bf16_t*)target, stride_t, (const bf16_t*)src, stride_s,
+                                                     index, (int)n_src, n_target, D);
+        break;
+      default: qh::set_error("qh_index_add: bad dtype"); return QH_E_DTYPE;
+    }
+    QH_CHECK_LAUNCH("qh_index_add");
+    return QH_OK;
+  }
   uint32_t *keys = nullptr, *vals = nullptr;
   int rc = sort_indices(index, n_src, n_target, ws, ws_bytes, &keys, &vals, st, "qh_index_add");
   if (rc) return rc;

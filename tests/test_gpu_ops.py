@@ -535,6 +535,30 @@ def test_index_add_is_source_order_fp32_sum_signed_zeros():
     assert torch.equal(out.cpu().view(torch.int32), exp.view(torch.int32))
 
 
+@pytest.mark.parametrize("n", [2048, 2049])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_index_add_scan_and_sorted_paths_bit_exact(n, dtype):
+    """Up to 2048 source rows take the one-launch scan (each position checks whether it is the first
+    of its row and adds the row's positions in order), more take the sorted path: both equal a
+    sequential fp32 sum in source order, rounded once, bit for bit; indices outside [0, T) are
+    skipped; one row has a run of 40 sources."""
+    T, D = 300, 64
+    g = _gen(91)
+    tgt = torch.randn(T, D, generator=g).to(dtype)
+    src = torch.randn(n, D, generator=g).to(dtype)
+    index = torch.randint(-20, T + 20, (n,), generator=g)
+    index[:40] = 7
+    index = index[torch.randperm(n, generator=g)]
+    exp = tgt.float().clone()
+    for j, r in enumerate(index.tolist()):
+        if 0 <= r < T:
+            exp[r] = exp[r] + src[j].float()
+    exp = exp.to(dtype)
+    out = K.triton_index_add(tgt.to(DEV), src.to(DEV), index.to(DEV)).cpu()
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(out.view(bits), exp.view(bits))
+
+
 def test_index_add_autograd():
     tgt = randn(20, 32, seed=86).requires_grad_(True)
     src = randn(40, 32, seed=87).requires_grad_(True)
