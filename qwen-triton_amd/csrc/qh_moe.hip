@@ -104,23 +104,33 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const T* __restrict__ 
                                                           const T* __restrict__ w, int k, int64_t E,
                                                           T* __restrict__ out, int64_t H) {
   const int64_t t = blockIdx.x;
-  // The token's k slots are loaded together, then ordered by expert id in
-  // registers (ids of one token are distinct; out-of-range ids sort last and
-  // are dropped).
+  // The token's k slots are loaded together (slots past k repeat slot 0 and are dropped), then
+  // ordered by expert id in registers (ids of one token are distinct; out-of-range ids sort last
+  // and are dropped). The empty asm statements keep every load of a group issued before the
+  // first use: the compiler otherwise sinks each guarded load into the block that tests it and
+  // waits for it there, one round trip per slot.
   int64_t ek[KMAX];
   int32_t pk[KMAX];
   float wk[KMAX];
+  uint32_t wr[KMAX];  // the weights' 16-bit patterns
+  const uint16_t* wb = reinterpret_cast<const uint16_t*>(w);
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) {
-    ek[j] = E;
-    pk[j] = 0;
-    wk[j] = 1.f;
-    if (j < k) {
-      const int64_t e = sel[t * k + j];
-      pk[j] = inv[t * k + j];
-      if (w) wk[j] = to_f32(w[t * k + j]);
-      ek[j] = (e < 0 || e >= E) ? E : e;
-    }
+    const int64_t jj = t * k + (j < k ? j : 0);
+    ek[j] = sel[jj];
+    pk[j] = inv[jj];
+  }
+  if (w) {
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) wr[j] = wb[t * k + (j < k ? j : 0)];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) asm volatile("" : "+v"(wr[j]));
+  }
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    asm volatile("" : "+v"(ek[j]), "+v"(pk[j]));
+    wk[j] = w ? to_f32(__builtin_bit_cast(T, (uint16_t)wr[j])) : 1.f;
+    ek[j] = (j >= k || ek[j] < 0 || ek[j] >= E) ? E : ek[j];
   }
   int nk = 0;
 #pragma unroll
@@ -141,45 +151,64 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const T* __restrict__ 
       wk[q] = sw ? w0 : w1;
     }
   for (int64_t c = threadIdx.x * 8; c < H; c += 256 * 8) {
-    // all rows are requested before the ordered sum consumes them
-    Vec16<T> y[KMAX];
-#pragma unroll
-    for (int j = 0; j < KMAX; ++j)
-      if (j < nk) y[j] = ld16(Y + (int64_t)pk[j] * ldy + c);
     Vec16<T> acc;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc.v[e] = (T)0.f;
+    if (nk > 0) {
+      // every row is requested before the ordered sum consumes them (rows past nk repeat the first)
+      Vec16<T> y[KMAX];
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-      if (j >= nk) break;
+      for (int j = 0; j < KMAX; ++j) y[j] = ld16(Y + (int64_t)pk[j < nk ? j : 0] * ldy + c);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float yv = w ? to_f32(from_f32<T>(to_f32(y[j].v[e]) * wk[j])) : to_f32(y[j].v[e]);
-        acc.v[e] = from_f32<T>(to_f32(acc.v[e]) + yv);
+      for (int j = 0; j < KMAX; ++j) {
+        qh_u32x4 r = __builtin_bit_cast(qh_u32x4, y[j].raw);
+        asm volatile("" : "+v"(r));
+        y[j].raw = __builtin_bit_cast(uint4, r);
+      }
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j) {
+        if (j >= nk) break;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float yv = w ? to_f32(from_f32<T>(to_f32(y[j].v[e]) * wk[j])) : to_f32(y[j].v[e]);
+          acc.v[e] = from_f32<T>(to_f32(acc.v[e]) + yv);
+        }
       }
     }
     st16(out + t * H + c, acc);
   }
 }
 
-// Xs[r] = X[rows[r]] (one workgroup per 4 rows, 16-byte vectors).
+// Xs[r] = X[rows[r]] (one workgroup per 8 rows, two rows per wave, 16-byte vectors): both row
+// indices load together, then up to eight 16-byte loads are in flight before their stores.
 template <typename T>
 __global__ __launch_bounds__(256) void moe_gather_kernel(const T* __restrict__ X, int64_t ldx,
                                                          const int32_t* __restrict__ rows, int64_t R, int64_t H,
                                                          T* __restrict__ Xs, int64_t lds) {
-  const int64_t r = blockIdx.x * 4ll + (threadIdx.x >> 6);
-  if (r >= R) return;
-  const T* src = X + (int64_t)rows[r] * ldx;
-  T* dst = Xs + r * lds;
-  // four 16-byte loads in flight before their stores
+  const int64_t r0 = (blockIdx.x * 4ll + (threadIdx.x >> 6)) * 2;
+  if (r0 >= R) return;
+  const bool two = r0 + 1 < R;
+  const T* src0 = X + (int64_t)rows[r0] * ldx;
+  const T* src1 = X + (int64_t)rows[two ? r0 + 1 : r0] * ldx;
+  T* dst0 = Xs + r0 * lds;
+  T* dst1 = dst0 + lds;
   for (int64_t c0 = (threadIdx.x & 63) * 8; c0 < H; c0 += 4 * 64 * 8) {
-    Vec16<T> v[4];
+    // clamped columns: every load is issued, only the stores are guarded
+    int64_t cc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) cc[u] = min(c0 + (int64_t)u * 512, H - 8);
+    Vec16<T> v0[4], v1[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v0[u] = ld16(src0 + cc[u]);
+      v1[u] = ld16(src1 + cc[u]);
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      if (c0 + u * 512 < H) v[u] = ld16(src + c0 + u * 512);
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (c0 + u * 512 < H) st16(dst + c0 + u * 512, v[u]);
+      if (c0 + u * 512 < H) {
+        st16(dst0 + c0 + u * 512, v0[u]);
+        if (two) st16(dst1 + c0 + u * 512, v1[u]);
+      }
   }
 }
 
@@ -221,6 +250,92 @@ __global__ __launch_bounds__(256) void moe_scale_bwd_kernel(const T* __restrict_
     }
     s = block_sum(s, red);
     if (threadIdx.x == 0) dw[t * k + j] = from_f32<T>(s);
+  }
+}
+
+// The same for top_k <= 8, with every load of a token in flight at once: its slots (expert, row,
+// weight), then its gradient row with every slot's D row, and the k dot products reduced
+// together (one barrier). Per-slot sums and their order are those of moe_scale_bwd_kernel, so
+// the results are equal bit for bit.
+template <typename T>
+__global__ __launch_bounds__(256) void moe_scale_bwd8_kernel(const T* __restrict__ dout, int64_t ldo,
+                                                             const T* __restrict__ D, int64_t ldd,
+                                                             const T* __restrict__ w,
+                                                             const int32_t* __restrict__ inv,
+                                                             const int64_t* __restrict__ sel, int k, int64_t E,
+                                                             int64_t H, T* __restrict__ dD, int64_t ldg,
+                                                             T* __restrict__ dw) {
+  constexpr int KM = 8;
+  __shared__ float red[KM][4];
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const uint16_t* wb = reinterpret_cast<const uint16_t*>(w);
+  int64_t ek[KM];
+  int32_t pk[KM];
+  uint32_t wr[KM];
+#pragma unroll
+  for (int j = 0; j < KM; ++j) {
+    const int64_t jj = t * k + (j < k ? j : 0);
+    ek[j] = sel[jj];
+    pk[j] = inv[jj];
+    wr[j] = wb[jj];
+  }
+  // (empty asm: every slot load is issued before the first is used)
+#pragma unroll
+  for (int j = 0; j < KM; ++j) asm volatile("" : "+v"(ek[j]), "+v"(pk[j]), "+v"(wr[j]));
+  bool ok[KM];
+  int pfirst = -1;
+#pragma unroll
+  for (int j = KM - 1; j >= 0; --j) {
+    ok[j] = j < k && ek[j] >= 0 && ek[j] < E;
+    if (ok[j]) pfirst = pk[j];
+  }
+  float s[KM];
+#pragma unroll
+  for (int j = 0; j < KM; ++j) s[j] = 0.f;
+  if (pfirst >= 0) {  // (token-uniform) some slot has a row; the others read that row and drop it
+    const T* go = dout + t * ldo;
+    for (int64_t c = threadIdx.x * 8; c < H; c += 256 * 8) {
+      const Vec16<T> g = ld16(go + c);
+      Vec16<T> d[KM];
+#pragma unroll
+      for (int j = 0; j < KM; ++j) d[j] = ld16(D + (int64_t)(ok[j] ? pk[j] : pfirst) * ldd + c);
+#pragma unroll
+      for (int j = 0; j < KM; ++j) {
+        qh_u32x4 r = __builtin_bit_cast(qh_u32x4, d[j].raw);
+        asm volatile("" : "+v"(r));
+        d[j].raw = __builtin_bit_cast(uint4, r);
+      }
+#pragma unroll
+      for (int j = 0; j < KM; ++j) {
+        if (!ok[j]) continue;
+        const float wj = to_f32(__builtin_bit_cast(T, (uint16_t)wr[j]));
+        Vec16<T> o;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float gf = to_f32(g.v[q]);
+          o.v[q] = from_f32<T>(gf * wj);
+          s[j] += gf * to_f32(d[j].v[q]);
+        }
+        st16(dD + (int64_t)pk[j] * ldg + c, o);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KM; ++j) s[j] = wave_sum(s[j]);
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < KM; ++j) red[j][wid] = s[j];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+      if (j >= k) break;
+      float tsum = 0.f;
+      for (int i = 0; i < 4; ++i) tsum += red[j][i];  // the wave order of block_sum
+      dw[t * k + j] = ok[j] ? from_f32<T>(tsum) : (T)0.f;
+    }
   }
 }
 
@@ -306,7 +421,7 @@ extern "C" int qh_moe_gather(const void* X, int64_t ldx, const int32_t* rows, in
   QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_moe_gather: bf16/f16 only");
   if (R == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;
-  const unsigned g = (unsigned)((R + 3) / 4);
+  const unsigned g = (unsigned)((R + 7) / 8);
   if (dtype == QH_BF16)
     moe_gather_kernel<bf16_t><<<g, 256, 0, st>>>((const bf16_t*)X, ldx, rows, R, H, (bf16_t*)Xs, lds);
   else
@@ -328,9 +443,14 @@ extern "C" int qh_moe_scale_bwd(const void* dout, int64_t ldo, const void* D, in
   if (n_tokens == 0) return QH_OK;
   hipStream_t st = (hipStream_t)stream;
 #define QH_SB(T)                                                                                              \
-  moe_scale_bwd_kernel<T><<<(unsigned)n_tokens, 256, 0, st>>>((const T*)dout, ldo, (const T*)D, ldd,          \
-                                                              (const T*)weights, inv, selected, (int)top_k,   \
-                                                              n_experts, H, (T*)dD, ldg, (T*)dw)
+  if (top_k <= 8)                                                                                             \
+    moe_scale_bwd8_kernel<T><<<(unsigned)n_tokens, 256, 0, st>>>((const T*)dout, ldo, (const T*)D, ldd,       \
+                                                                 (const T*)weights, inv, selected, (int)top_k, \
+                                                                 n_experts, H, (T*)dD, ldg, (T*)dw);          \
+  else                                                                                                        \
+    moe_scale_bwd_kernel<T><<<(unsigned)n_tokens, 256, 0, st>>>((const T*)dout, ldo, (const T*)D, ldd,        \
+                                                                (const T*)weights, inv, selected, (int)top_k, \
+                                                                n_experts, H, (T*)dD, ldg, (T*)dw)
   if (dtype == QH_BF16) QH_SB(bf16_t); else QH_SB(f16_t);
 #undef QH_SB
   QH_CHECK_LAUNCH("qh_moe_scale_bwd");
