@@ -155,10 +155,11 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const T* __restrict__ 
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc.v[e] = (T)0.f;
     if (nk > 0) {
-      // every row is requested before the ordered sum consumes them (rows past nk repeat the first)
+      // every row is requested before the ordered sum consumes them (rows past nk repeat the first);
+      // non-temporal: the expert rows are read once and exceed the last-level cache
       Vec16<T> y[KMAX];
 #pragma unroll
-      for (int j = 0; j < KMAX; ++j) y[j] = ld16(Y + (int64_t)pk[j < nk ? j : 0] * ldy + c);
+      for (int j = 0; j < KMAX; ++j) y[j] = ld16_nt(Y + (int64_t)pk[j < nk ? j : 0] * ldy + c);
 #pragma unroll
       for (int j = 0; j < KMAX; ++j) {
         qh_u32x4 r = __builtin_bit_cast(qh_u32x4, y[j].raw);
