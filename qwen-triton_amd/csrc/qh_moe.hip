@@ -300,7 +300,8 @@ __global__ __launch_bounds__(256) void moe_scale_bwd8_kernel(const T* __restrict
       const Vec16<T> g = ld16(go + c);
       Vec16<T> d[KM];
 #pragma unroll
-      for (int j = 0; j < KM; ++j) d[j] = ld16(D + (int64_t)(ok[j] ? pk[j] : pfirst) * ldd + c);
+      for (int j = 0; j < KM; ++j)  // (non-temporal: D is read once and exceeds the last-level cache)
+        d[j] = ld16_nt(D + (int64_t)(ok[j] ? pk[j] : pfirst) * ldd + c);
 #pragma unroll
       for (int j = 0; j < KM; ++j) {
         qh_u32x4 r = __builtin_bit_cast(qh_u32x4, d[j].raw);
