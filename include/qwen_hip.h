@@ -444,6 +444,19 @@ int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const voi
                  int64_t sob, int64_t soh, int64_t sos, float* lse, int64_t B, int64_t Hq, int64_t Hkv,
                  int64_t Sq, int64_t Sk, int64_t D, float scale, int causal, int64_t causal_offset, int dtype,
                  void* stream);
+/* qh_flash_fwd (bf16/f16 only) with the model's padding and sliding-window
+ * masks applied in the kernel: key j is also hidden from query i when
+ * window > 0 and j <= i + causal_offset - window, or when key_bits (may be
+ * NULL; 8-byte aligned, bits_stride >= ceil(Sk / 64) words per batch row) has
+ * bit j % 64 of word b * bits_stride + j / 64 clear. A query that sees no key
+ * gets a zero row and LSE = -inf. Tiles with no visible key are skipped.
+ * Replaces the masked fp32 SDPA call of qwen_triton/modules/attention.py:114-119
+ * with the mask of qwen_triton/models/core.py:47-75 (_build_causal_mask). */
+int qh_flash_fwd_masked(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
+                        int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs, void* o,
+                        int64_t sob, int64_t soh, int64_t sos, float* lse, int64_t B, int64_t Hq, int64_t Hkv,
+                        int64_t Sq, int64_t Sk, int64_t D, float scale, int causal, int64_t causal_offset,
+                        const uint64_t* key_bits, int64_t bits_stride, int64_t window, int dtype, void* stream);
 /* Workspace bytes of qh_flash_bwd: Delta = rowsum(O dO) and the LSE in log2 units,
  * per (b, q-head) in rows of Sq rounded up to 64 plus one 64-query tile. */
 int64_t qh_flash_bwd_workspace(int64_t B, int64_t Hq, int64_t Sq);

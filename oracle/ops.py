@@ -83,6 +83,30 @@ def attention(q, k, v, scale, causal=True, groups=1, causal_offset=0, dtype=F64)
     return p @ v, lse
 
 
+def attention_masked(q, k, v, scale, groups=1, causal_offset=0, key_valid=None, window=None, dtype=F64):
+    """Causal attention under the decoder's padding / sliding-window mask, by brute force: key j is
+    visible to query i iff j <= i + causal_offset, j > i + causal_offset - window (window set) and
+    key_valid[b, j] != 0 (qwen_triton/models/core.py:47-75 builds this mask, SDPA applies it at
+    qwen_triton/modules/attention.py:114-119). Hidden keys get -inf, so a query that sees no key
+    has a zero row and LSE -inf (the reference's finite additive mask gives such padding rows,
+    whose outputs are never used, an average instead). Returns (out, lse)."""
+    q, k, v = _d(q, dtype), _expand_kv(_d(k, dtype), groups), _expand_kv(_d(v, dtype), groups)
+    s = (q @ k.transpose(-1, -2)) * scale
+    sq, sk = s.shape[-2], s.shape[-1]
+    pos = torch.arange(sq)[:, None] + causal_offset
+    keys = torch.arange(sk)[None, :]
+    allowed = keys <= pos
+    if window is not None:
+        allowed = allowed & (keys > pos - window)
+    allowed = allowed[None, None].expand(s.shape[0], 1, sq, sk)
+    if key_valid is not None:
+        allowed = allowed & (key_valid.cpu() != 0)[:, None, None, :sk]
+    s = s.masked_fill(~allowed, float("-inf"))
+    lse = torch.logsumexp(s, dim=-1)
+    p = torch.nan_to_num(torch.exp(s - lse[..., None]), nan=0.0)
+    return p @ v, lse
+
+
 def attention_backward(q, k, v, grad_out, scale, causal=True, groups=1, causal_offset=0, dtype=F64):
     """dq, dk, dv from the softmax-attention derivative (dk/dv summed over each GQA group)."""
     qd, kd, vd = _d(q, dtype), _expand_kv(_d(k, dtype), groups), _expand_kv(_d(v, dtype), groups)

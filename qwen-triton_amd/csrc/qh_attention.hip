@@ -246,10 +246,12 @@ struct TileLoader {
   }
 };
 
-template <typename T, int DP>
+// MASKED adds a lower key bound `lo` per query (a sliding window) and a
+// per-key validity word `bits` for the tile (bit j: key kv0 + j may be seen).
+template <typename T, int DP, bool MASKED = false>
 __device__ __forceinline__ void fa_fwd_tile(const T* Kt, const T* Vt, const typename Mfma<T>::v8 (&qf)[DP / 16],
                                             f32x16 (&acc)[DP / 32], float& m, float& l, int kv0, bool need_mask,
-                                            int lim, float scale_log2, int lane) {
+                                            int lim, float scale_log2, int lane, int lo = 0, uint64_t bits = 0) {
   constexpr int CPR = DP / 8, DT = DP / 32, KD = DP / 16;
   typedef typename Mfma<T>::v8 v8;
   const int ql = lane & 31, hf = lane >> 5;
@@ -282,7 +284,9 @@ __device__ __forceinline__ void fa_fwd_tile(const T* Kt, const T* Vt, const type
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = kv0 + kt * 32 + g * 8 + hf * 4 + r;
-          s[kt][g * 4 + r] = key > lim ? -INFINITY : s[kt][g * 4 + r];
+          bool off = key > lim;
+          if constexpr (MASKED) off = off || key < lo || !((bits >> (key - kv0)) & 1);
+          s[kt][g * 4 + r] = off ? -INFINITY : s[kt][g * 4 + r];
         }
   }
   float mx = fmaxf(s[0][0], s[1][0]);
@@ -328,13 +332,18 @@ __device__ __forceinline__ void fa_fwd_tile(const T* Kt, const T* Vt, const type
   }
 }
 
-template <typename T, int DP>
+// MASKED: key j is also hidden from query i when j <= i + coff - window
+// (window > 0) or bit j of the batch row's validity words is clear
+// (kbits non-null; word t covers keys 64t .. 64t + 63).
+template <typename T, int DP, bool MASKED = false>
 __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs,
                                                      const T* __restrict__ K, int64_t skb, int64_t skh, int64_t sks,
                                                      const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs,
                                                      T* __restrict__ O, int64_t sob, int64_t soh, int64_t sos,
                                                      float* __restrict__ LSE, int Hq, int groups, int Sq, int Sk, int D,
-                                                     float scale_log2, int causal, int coff) {
+                                                     float scale_log2, int causal, int coff,
+                                                     const uint64_t* __restrict__ kbits = nullptr, int64_t kbits_b = 0,
+                                                     int window = 0) {
   constexpr int BN = 64, BMQ = 128;
   constexpr int DT = DP / 32, KD = DP / 16;
   typedef typename Mfma<T>::v8 v8;
@@ -375,12 +384,23 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
   // last key visible to this lane's query (causal and/or Sk bound)
   const int lim = causal ? min(Sk - 1, qi + coff) : Sk - 1;
 
-  const TileLoader<T, BN, DP> kload(sks, D), vload(svs, D);
-  if (ntiles > 0) {
-    kload.load(Ks[0], Kb, sks, 0, Sk);
-    vload.load(Vs[0], Vb, svs, 0, Sk);
+  // first tile: with a window, the block's first query sees no key below
+  // qb * BMQ + coff - window + 1
+  int it0 = 0, lo = 0;
+  if constexpr (MASKED) {
+    if (window > 0) {
+      lo = qi + coff - window + 1;
+      const int blo = qb * BMQ + coff - window + 1;
+      it0 = blo > 0 ? blo / BN : 0;
+    }
   }
-  for (int it = 0; it < ntiles; ++it) {
+
+  const TileLoader<T, BN, DP> kload(sks, D), vload(svs, D);
+  if (ntiles > it0) {
+    kload.load(Ks[it0 & 1], Kb, sks, it0 * BN, Sk);
+    vload.load(Vs[it0 & 1], Vb, svs, it0 * BN, Sk);
+  }
+  for (int it = it0; it < ntiles; ++it) {
     const int kv0 = it * BN;
     const int buf = it & 1;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's loads of tile `it` have landed
@@ -393,7 +413,15 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
     // (one code path for both: two inlined copies of the tile would hold the
     // accumulators in different registers on each side)
     const bool need_mask = (kv0 + BN > Sk) || (causal && kv0 + BN - 1 > qw0 + coff);
-    fa_fwd_tile<T, DP>(Ks[buf], Vs[buf], qf, acc, m, l, kv0, need_mask, lim, scale_log2, lane);
+    if constexpr (MASKED) {
+      const uint64_t w = kbits ? kbits[b * kbits_b + it] : ~0ull;  // block-uniform
+      if (w == 0) continue;  // no visible key in the tile (left padding)
+      const bool cut = window > 0 && kv0 < qw0 + 31 + coff - window + 1;
+      fa_fwd_tile<T, DP, true>(Ks[buf], Vs[buf], qf, acc, m, l, kv0, need_mask || cut || w != ~0ull, lim,
+                               scale_log2, lane, lo, w);
+    } else {
+      fa_fwd_tile<T, DP>(Ks[buf], Vs[buf], qf, acc, m, l, kv0, need_mask, lim, scale_log2, lane);
+    }
   }
 
   l = halves_sum(l);
@@ -1750,6 +1778,49 @@ extern "C" int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs
 #undef QH_FWD_D
 #undef QH_FWD
   QH_CHECK_LAUNCH("qh_flash_fwd");
+  return QH_OK;
+}
+
+extern "C" int qh_flash_fwd_masked(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,
+                                   int64_t skh, int64_t sks, const void* v, int64_t svb, int64_t svh, int64_t svs,
+                                   void* o, int64_t sob, int64_t soh, int64_t sos, float* lse, int64_t B, int64_t Hq,
+                                   int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, float scale, int causal,
+                                   int64_t causal_offset, const uint64_t* key_bits, int64_t bits_stride,
+                                   int64_t window, int dtype, void* stream) {
+  QH_CHECK_ARG(B >= 0 && Hq > 0 && Hkv > 0 && Sq >= 0 && Sk >= 0, "qh_flash_fwd_masked: bad shape");
+  QH_CHECK_ARG(Hq % Hkv == 0, "qh_flash_fwd_masked: Hq=%lld not a multiple of Hkv=%lld", (long long)Hq,
+               (long long)Hkv);
+  QH_CHECK_ARG(dtype == QH_BF16 || dtype == QH_F16, "qh_flash_fwd_masked: bf16/f16 only");
+  const int dp = pick_dp(D);
+  QH_CHECK_ARG(dp && D % 8 == 0, "qh_flash_fwd_masked: head dim %lld must be a multiple of 8 and <= 128",
+               (long long)D);
+  QH_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o),
+               "qh_flash_fwd_masked: pointers must be 16-byte aligned");
+  QH_CHECK_ARG(sqs % 8 == 0 && sks % 8 == 0 && svs % 8 == 0 && sqh % 8 == 0 && skh % 8 == 0 && svh % 8 == 0 &&
+                   sqb % 8 == 0 && skb % 8 == 0 && svb % 8 == 0 && sob % 8 == 0 && soh % 8 == 0 && sos % 8 == 0,
+               "qh_flash_fwd_masked: strides must be multiples of 8 elements");
+  QH_CHECK_ARG(B * Hq < 65536 && Sq < (1 << 30) && Sk < (1 << 30), "qh_flash_fwd_masked: too large");
+  QH_CHECK_ARG((Sq + 127) / 128 * B * Hq < (1ll << 31), "qh_flash_fwd_masked: too many query blocks");
+  QH_CHECK_ARG(window >= 0 && window < (1 << 30), "qh_flash_fwd_masked: bad window %lld", (long long)window);
+  QH_CHECK_ARG(causal_offset > -(1ll << 30) && causal_offset < (1ll << 30), "qh_flash_fwd_masked: bad causal offset");
+  QH_CHECK_ARG(key_bits == nullptr || (((uintptr_t)key_bits & 7) == 0 && bits_stride >= (Sk + 63) / 64),
+               "qh_flash_fwd_masked: key_bits must be 8-byte aligned with >= ceil(Sk / 64) words per batch row");
+  if (B * Hq * Sq == 0) return QH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const float sl2 = scale * kLog2e;
+  const int groups = (int)(Hq / Hkv);
+  dim3 grid((unsigned)ceil_div(Sq, 128), (unsigned)(B * Hq));
+#define QH_FWD(T, DPV)                                                                                          \
+  fa_fwd_kernel<T, DPV, true><<<grid, 256, 0, st>>>(                                                          \
+      (const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks, (const T*)v, svb, svh, svs, (T*)o, sob, soh, sos, \
+      lse, (int)Hq, groups, (int)Sq, (int)Sk, (int)D, sl2, causal, (int)causal_offset, key_bits, bits_stride,   \
+      (int)window)
+#define QH_FWD_D(T) \
+  if (dp == 32) QH_FWD(T, 32); else if (dp == 64) QH_FWD(T, 64); else QH_FWD(T, 128);
+  if (dtype == QH_BF16) { QH_FWD_D(bf16_t) } else { QH_FWD_D(f16_t) }
+#undef QH_FWD_D
+#undef QH_FWD
+  QH_CHECK_LAUNCH("qh_flash_fwd_masked");
   return QH_OK;
 }
 

@@ -60,12 +60,30 @@ def _check(q, k, v, num_kv_groups):
         raise Unsupported("flash attention kernels need bf16, fp16 or fp32 q/k/v of one dtype")
 
 
+def pack_key_bits(key_valid: torch.Tensor) -> torch.Tensor:
+    """[B, Sk] 0/1 key validity -> int64 [B, ceil(Sk / 64)] words, bit j % 64 of word j // 64 set
+    when key j may be attended (the layout ``qh_flash_fwd_masked`` reads)."""
+    B, sk = key_valid.shape
+    words = (sk + 63) // 64
+    bits = torch.zeros((B, words * 64), dtype=torch.int64, device=key_valid.device)
+    bits[:, :sk] = (key_valid != 0).to(torch.int64)
+    shifts = torch.arange(64, dtype=torch.int64, device=key_valid.device)
+    # distinct powers of two: the sum is the OR (bit 63 wraps to the sign bit, as intended)
+    return (bits.view(B, words, 64) << shifts).sum(dim=-1)
+
+
 def flash_forward(q, k, v, scale: float, causal: bool, num_kv_groups: int, causal_offset: int = 0,
-                  need_lse: bool = True, seq_major: bool = False):
+                  need_lse: bool = True, seq_major: bool = False, key_bits: torch.Tensor | None = None,
+                  window: int = 0):
     """Launch the forward kernel; returns (out [B,Hq,Sq,D], lse [B,Hq,Sq] fp32 or None). ``out`` is
     contiguous, or with ``seq_major`` the [B,Hq,Sq,D] view of a [B,Sq,Hq,D] buffer (the rows the
-    output projection reads, written in place by the kernel)."""
+    output projection reads, written in place by the kernel). ``key_bits`` (from ``pack_key_bits``)
+    and ``window`` (> 0: key j hidden from query i when j <= i + causal_offset - window) select the
+    masked kernel, bf16/f16 only."""
     _check(q, k, v, num_kv_groups)
+    masked = key_bits is not None or window > 0
+    if masked and q.dtype == torch.float32:
+        raise Unsupported("the masked flash kernel takes bf16/fp16 q/k/v")
     q, k, v = _unit_last(q), _unit_last(k), _unit_last(v)
     B, Hq, Sq, D = q.shape
     Hkv, Sk = k.shape[1], k.shape[2]
@@ -74,26 +92,56 @@ def flash_forward(q, k, v, scale: float, causal: bool, num_kv_groups: int, causa
     else:
         out = torch.empty((B, Hq, Sq, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if need_lse else None
-    _native.call("qh_flash_fwd", q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0),
-                 k.stride(1), k.stride(2), v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), out.data_ptr(),
-                 out.stride(0), out.stride(1), out.stride(2), None if lse is None else lse.data_ptr(), B, Hq, Hkv,
-                 Sq, Sk, D, float(scale), int(bool(causal)), int(causal_offset), _native.dtype_code(q.dtype),
-                 _native.stream(q.device))
+    args = (q.data_ptr(), q.stride(0), q.stride(1), q.stride(2), k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+            v.data_ptr(), v.stride(0), v.stride(1), v.stride(2), out.data_ptr(), out.stride(0), out.stride(1),
+            out.stride(2), None if lse is None else lse.data_ptr(), B, Hq, Hkv, Sq, Sk, D, float(scale),
+            int(bool(causal)), int(causal_offset))
+    if masked:
+        if key_bits is not None:
+            if (key_bits.dtype != torch.int64 or key_bits.dim() != 2 or key_bits.shape[0] != B
+                    or key_bits.shape[1] < (Sk + 63) // 64 or key_bits.stride(1) != 1
+                    or key_bits.device != q.device):
+                raise Unsupported(f"key_bits must be int64 [B, >= ceil(Sk / 64)] on {q.device}")
+        _native.call("qh_flash_fwd_masked", *args, None if key_bits is None else key_bits.data_ptr(),
+                     0 if key_bits is None else key_bits.stride(0), int(window), _native.dtype_code(q.dtype),
+                     _native.stream(q.device))
+    else:
+        _native.call("qh_flash_fwd", *args, _native.dtype_code(q.dtype), _native.stream(q.device))
     return out, lse
 
 
-def attention_rows(q, k, v, scale: float, num_kv_groups: int, causal_offset: int = 0) -> torch.Tensor | None:
+def attention_rows(q, k, v, scale: float, num_kv_groups: int, causal_offset: int = 0,
+                   key_bits: torch.Tensor | None = None, window: int = 0) -> torch.Tensor | None:
     """Causal inference attention (no autograd) returned as the output projection's input rows
     [B, Sq, Hq * D], which the kernel writes in place (no transpose copy); None when the call is not
-    served by the library (the caller then takes its usual path)."""
+    served by the library (the caller then takes its usual path). ``key_bits``/``window`` as in
+    ``flash_forward``."""
     if not _GUARD.use_native(None, q, k, v):
         return None
     try:
-        out = flash_forward(q, k, v, scale, True, num_kv_groups, causal_offset, need_lse=False, seq_major=True)[0]
+        out = flash_forward(q, k, v, scale, True, num_kv_groups, causal_offset, need_lse=False, seq_major=True,
+                            key_bits=key_bits, window=window)[0]
     except Exception as exc:
         _GUARD.failed(exc)
         return None
     return out.transpose(1, 2).reshape(q.shape[0], q.shape[2], -1)
+
+
+def masked_attention(q, k, v, scale: float, num_kv_groups: int, causal_offset: int,
+                     key_bits: torch.Tensor | None, window: int) -> torch.Tensor | None:
+    """Causal inference attention with key padding and/or a sliding window ([B, Hq, Sq, D]); None
+    when the call is not served by the library (autograd, fp32, CPU: the caller then applies the
+    dense mask)."""
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        return None
+    if q.dtype == torch.float32 or not _GUARD.use_native(None, q, k, v):
+        return None
+    try:
+        return flash_forward(q, k, v, scale, True, num_kv_groups, causal_offset, need_lse=False,
+                             key_bits=key_bits, window=window)[0]
+    except Exception as exc:
+        _GUARD.failed(exc)
+        return None
 
 
 def flash_backward(q, k, v, out, grad_out, lse, scale: float, causal: bool, num_kv_groups: int,

@@ -7,7 +7,9 @@ Differences, all in the dispatch rather than the maths:
 
 * without a padding mask the layers get ``attention_mask=None`` and run causal
   flash attention (the reference always built an additive mask, which sent
-  every prefill to fp32 SDPA);
+  every prefill to fp32 SDPA); with one, or with a sliding window, they get a
+  ``CausalPaddingMask``, which inference in bf16/fp16 applies inside the flash
+  kernel and every other call as the reference's additive tensor;
 * the largest cache position is known on the host when ``cache_position`` is
   generated here, so the cache write needs no device-to-host sync;
 * ``greedy_generate`` preallocates the KV cache for the whole generation;
@@ -42,6 +44,7 @@ from qwen_triton.modules import (
     QwenSparseMoeBlock,
     QwenTritonCache,
 )
+from qwen_triton.modules.attention import CausalPaddingMask
 from qwen_triton.modules.cache import StaticDecode
 from qwen_triton.modules.embedding import TritonEmbedding
 from qwen_triton.modules.linear import TritonLinear
@@ -67,10 +70,10 @@ def _parse_dtype(dtype: torch.dtype | str | None) -> torch.dtype | None:
         raise ValueError(f"Unsupported dtype string: {dtype}") from None
 
 
-def _build_causal_mask(attention_mask, batch_size: int, cache_position, device, past_key_values, window_size=None):
-    """Additive fp32 mask [B, 1, q, kv]: causal (optionally windowed) plus key padding."""
+def _build_causal_mask(attention_mask, batch_size: int, cache_position, device, past: int, window_size=None):
+    """Additive fp32 mask [B, 1, q, kv]: causal (optionally windowed) plus key padding; ``past`` is the
+    number of cached keys before this step."""
     q_len = cache_position.shape[0]
-    past = 0 if past_key_values is None else past_key_values.get_seq_length()
     kv_len = past + q_len
     keys = torch.arange(kv_len, device=device)
     allowed = keys[None, :] <= cache_position[:, None]
@@ -85,6 +88,28 @@ def _build_causal_mask(attention_mask, batch_size: int, cache_position, device, 
             am = torch.cat((torch.ones((am.shape[0], kv_len - am.shape[1]), device=device, dtype=am.dtype), am), dim=-1)
         mask = mask + (1.0 - am[:, None, None, :kv_len].to(torch.float32)) * neg
     return mask
+
+
+def _structured_mask(attention_mask, batch_size: int, cache_position, device, past_key_values, window_size,
+                     positions_known: bool) -> CausalPaddingMask:
+    """``_build_causal_mask``'s mask in structured form: the key-validity rows it adds (ones
+    prepended for cached keys the 2-D mask does not cover) and the window; the additive tensor is
+    built only if a layer asks for it, with the cache length read here, before any layer of the
+    step has appended its keys."""
+    q_len = cache_position.shape[0]
+    past = 0 if past_key_values is None else past_key_values.get_seq_length()
+    kv_len = past + q_len
+    key_valid = None
+    if attention_mask is not None:
+        am = attention_mask.to(device)
+        if am.shape[1] < kv_len:
+            am = torch.cat((torch.ones((am.shape[0], kv_len - am.shape[1]), device=device, dtype=am.dtype), am), dim=-1)
+        key_valid = am[:, :kv_len]
+
+    def build():
+        return _build_causal_mask(attention_mask, batch_size, cache_position, device, past, window_size)
+
+    return CausalPaddingMask(build, key_valid, past, q_len, window_size, positions_known)
 
 
 def _layer_uses_moe(config: QwenTritonConfig, layer_idx: int) -> bool:
@@ -253,16 +278,18 @@ class QwenTritonModel(nn.Module):
 
         batch = inputs_embeds.shape[0]
         plain_causal = generated_positions and self._mask_is_trivial(attention_mask)
-        masks: dict[str, torch.Tensor | None] = {}
+        # generated positions are past .. past + seq - 1 (a captured decode step's are not known)
+        positions_known = generated_positions and static is None
+        masks: dict[str, CausalPaddingMask | None] = {}
         if plain_causal:
             masks["full_attention"] = None
         else:
-            masks["full_attention"] = _build_causal_mask(attention_mask, batch, cache_position, inputs_embeds.device,
-                                                         past_key_values)
+            masks["full_attention"] = _structured_mask(attention_mask, batch, cache_position, inputs_embeds.device,
+                                                       past_key_values, None, positions_known)
         if "sliding_attention" in self.config.layer_types and self.config.sliding_window is not None:
-            masks["sliding_attention"] = _build_causal_mask(attention_mask, batch, cache_position,
-                                                            inputs_embeds.device, past_key_values,
-                                                            window_size=self.config.sliding_window)
+            masks["sliding_attention"] = _structured_mask(attention_mask, batch, cache_position,
+                                                          inputs_embeds.device, past_key_values,
+                                                          self.config.sliding_window, positions_known)
 
         hidden = inputs_embeds
         position_embeddings = self.rotary_emb(hidden, position_ids, rope_bound)

@@ -8,8 +8,11 @@ flash kernel):
 * no mask: causal flash attention, aligned bottom-right when queries sit on
   top of cached keys (``causal_offset = kv_len - q_len``); a single query takes
   the split-KV decode kernel;
-* explicit additive mask (padding): fp32 SDPA over repeated KV heads, as the
-  reference does for masked multi-token attention.
+* padding and/or sliding-window mask (``CausalPaddingMask``): the masked flash
+  kernel for inference in bf16/fp16 on the GPU; otherwise (autograd, fp32, CPU)
+  the additive mask with fp32 SDPA over repeated KV heads, as the reference does
+  for masked multi-token attention;
+* explicit additive mask tensor: that fp32 SDPA.
 
 Inference (no autograd, GPU, position-indexed cache): the q/k/v projections
 of up to 128 tokens run as one grouped launch, and q_norm/k_norm, RoPE and the
@@ -48,6 +51,46 @@ def repeat_kv(hidden_states: torch.Tensor, n_rep: int) -> torch.Tensor:
     return hidden_states[:, :, None].expand(b, h, n_rep, s, d).reshape(b, h * n_rep, s, d)
 
 
+class CausalPaddingMask:
+    """The decoder's causal mask (optionally a sliding window) with key padding, kept in the
+    structured form the masked flash kernel applies; the reference builds it as an additive fp32
+    [B, 1, q, kv] tensor (qwen_triton/models/core.py:47-75) that every layer then reads.
+
+    Query i of the step sits at cache position ``past + i`` and sees key j < kv_len iff
+    j <= past + i, j > past + i - window (when a window is set) and ``key_valid[b, j]`` is
+    non-zero. ``dense()`` builds the additive tensor once, for the calls the kernel does not take
+    (autograd, fp32, CPU, caller-given cache positions)."""
+
+    def __init__(self, build_dense, key_valid: torch.Tensor | None, past: int, q_len: int,
+                 window: int | None, positions_known: bool) -> None:
+        self._build_dense = build_dense
+        self._dense: torch.Tensor | None = None
+        self._bits: torch.Tensor | None = None
+        self.key_valid = key_valid  # [B, kv_len] or None
+        self.past, self.q_len, self.kv_len = past, q_len, past + q_len
+        self.window = window
+        self.positions_known = positions_known  # the step's cache positions are past .. past + q_len - 1
+
+    def dense(self) -> torch.Tensor:
+        if self._dense is None:
+            self._dense = self._build_dense()
+        return self._dense
+
+    def kernel_args(self, q: torch.Tensor, k: torch.Tensor):
+        """(key_bits or None, window, causal_offset) for the masked kernel, or None when this call
+        needs the dense mask."""
+        if not self.positions_known or k.shape[2] != self.kv_len or q.shape[2] != self.q_len:
+            return None
+        if self.window is not None and self.window <= 0:
+            return None
+        if self.key_valid is not None:
+            if self.key_valid.shape[0] != q.shape[0]:
+                return None
+            if self._bits is None:
+                self._bits = _fa.pack_key_bits(self.key_valid.to(q.device))
+        return self._bits, self.window or 0, self.past
+
+
 class QwenFullAttention(nn.Module):
     def __init__(self, config: QwenTritonConfig, layer_idx: int) -> None:
         super().__init__()
@@ -69,10 +112,17 @@ class QwenFullAttention(nn.Module):
         self.q_norm = QwenRMSNorm(self.head_dim, eps=config.rms_norm_eps, one_plus_weight=config.norm_one_plus)
         self.k_norm = QwenRMSNorm(self.head_dim, eps=config.rms_norm_eps, one_plus_weight=config.norm_one_plus)
 
-    def _attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor | None,
-                out_dtype: torch.dtype) -> torch.Tensor:
+    def _attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                mask: torch.Tensor | CausalPaddingMask | None, out_dtype: torch.dtype) -> torch.Tensor:
         q_len, kv_len = q.shape[2], k.shape[2]
         groups = self.num_key_value_groups
+        if isinstance(mask, CausalPaddingMask):
+            args = mask.kernel_args(q, k)
+            if args is not None:
+                out = _fa.masked_attention(q, k, v, self.scaling, groups, args[2], args[0], args[1])
+                if out is not None:
+                    return out.to(out_dtype)
+            mask = mask.dense()
         if mask is None:
             on_gpu = q.is_cuda and k.is_cuda
             if on_gpu:
@@ -209,6 +259,13 @@ class QwenFullAttention(nn.Module):
                                           causal_offset=k.shape[2] - q.shape[2])
                 if rows is not None:
                     return rows.view(*input_shape, -1)
+            if isinstance(attention_mask, CausalPaddingMask) and q.shape[2] > 1:
+                args = attention_mask.kernel_args(q, k)
+                if args is not None:
+                    rows = _fa.attention_rows(q, k, v, self.scaling, self.num_key_value_groups,
+                                              causal_offset=args[2], key_bits=args[0], window=args[1])
+                    if rows is not None:
+                        return rows.view(*input_shape, -1)
             out = self._attend(q, k, v, attention_mask, q2.dtype)
         return out.transpose(1, 2).reshape(*input_shape, -1)
 

@@ -54,6 +54,44 @@ def test_prefill_logits_match_oracle():
     _band(out, ref)
 
 
+@pytest.mark.parametrize("window", [None, 40])
+def test_padding_and_window_masks_in_the_flash_kernel(monkeypatch, window):
+    """Left-padded prefill and a cached decode step (and a sliding window on the upper layers) take
+    the masked flash kernel; their logits on the real tokens agree with the same model applying the
+    reference's additive mask through fp32 SDPA."""
+    from qwen_triton.modules.attention import CausalPaddingMask
+
+    kw = dict(use_sliding_window=True, sliding_window=window, max_window_layers=1) if window else {}
+    cfg = _cfg(**kw)
+    m = _model(cfg)
+    gen = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, cfg.vocab_size, (3, 90), generator=gen).cuda()
+    mask = torch.ones_like(ids)
+    mask[1, :70] = 0
+    mask[2, :13] = 0
+    nxt = torch.randint(0, cfg.vocab_size, (3, 1), generator=gen).cuda()
+
+    def run(am):
+        with torch.no_grad():
+            p = m(input_ids=ids, attention_mask=am, use_cache=True)
+            d = m(input_ids=nxt, attention_mask=torch.cat((am, torch.ones_like(nxt)), 1),
+                  past_key_values=p.past_key_values, use_cache=True)
+        return p.logits.float().cpu(), d.logits.float().cpu()
+
+    c0 = _native.CALLS["qh_flash_fwd_masked"]
+    got = run(mask)
+    assert _native.CALLS["qh_flash_fwd_masked"] == c0 + 2 * cfg.num_hidden_layers
+    unpadded = run(torch.ones_like(mask))  # what ignoring the padding would give
+    monkeypatch.setattr(CausalPaddingMask, "kernel_args", lambda self, q, k: None)
+    exp = run(mask)
+    padded = mask.bool().cpu()
+    padded[0] = False  # the real tokens of the padded sequences
+    for g, e, u, rows in zip(got, exp, unpadded, (padded, torch.tensor([[False], [True], [True]]))):
+        _band(g[rows], e[rows])
+        # the padding is live: ignoring it moves these logits far more than the kernel's error
+        assert (g[rows] - e[rows]).abs().max() < 0.2 * (u[rows] - e[rows]).abs().max()
+
+
 def test_cached_decode_matches_full_forward_and_oracle():
     cfg = _cfg()
     m = _model(cfg, seed=1)

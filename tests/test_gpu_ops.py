@@ -1051,6 +1051,60 @@ def test_flash_backward_fp32(B, Hq, Hkv, S, D, causal):
     assert torch.equal(g[0], q.grad) and torch.equal(g[1], k.grad) and torch.equal(g[2], v.grad)
 
 
+def _key_valid(B, Sk, pads, holes, seed):
+    kv = torch.ones(B, Sk, dtype=torch.int64)
+    if pads is not None:
+        for b, n in enumerate(pads):
+            kv[b, :n] = 0  # left padding
+    if holes:
+        gen = torch.Generator().manual_seed(seed)
+        kv &= (torch.rand(B, Sk, generator=gen) < 0.8).to(torch.int64)
+    return kv
+
+
+MASKED_CASES = [  # B, Hq, Hkv, Sq, Sk, D, left pads, random holes, window
+    (3, 8, 2, 200, 200, 128, [0, 70, 150], False, 0),  # whole tiles of padding are skipped
+    (2, 4, 1, 77, 300, 64, None, True, 0),  # prefill on a cache, scattered invalid keys
+    (2, 4, 4, 256, 256, 128, None, False, 100),  # sliding window only
+    (2, 2, 1, 130, 130, 64, [5, 64], False, 37),  # window and padding
+    (4, 8, 2, 1, 333, 128, [0, 1, 100, 300], False, 0),  # padded decode step
+    (1, 2, 2, 300, 300, 32, None, False, 64),  # window of exactly one tile
+    (2, 4, 2, 100, 100, 64, [100, 3], False, 0),  # a sequence of padding only
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Sq,Sk,D,pads,holes,window", MASKED_CASES)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_flash_forward_masked(B, Hq, Hkv, Sq, Sk, D, pads, holes, window, dtype):
+    """Padding / sliding-window masks applied in the flash kernel, against the oracle's brute force
+    over the same mask (query i at cache position i + Sk - Sq); queries that see no key are zero rows
+    with LSE -inf in both."""
+    q = randn(B, Hq, Sq, D, dtype=dtype, seed=150)
+    k = randn(B, Hkv, Sk, D, dtype=dtype, seed=151)
+    v = randn(B, Hkv, Sk, D, dtype=dtype, seed=152)
+    kv = _key_valid(B, Sk, pads, holes, seed=153)
+    use_bits = pads is not None or holes
+    bits = FA.pack_key_bits(kv.cuda()) if use_bits else None
+    scale, off = D ** -0.5, Sk - Sq
+    c0 = native_calls("qh_flash_fwd_masked")
+    out, lse = FA.flash_forward(q, k, v, scale, True, Hq // Hkv, off, key_bits=bits, window=window)
+    assert native_calls("qh_flash_fwd_masked") == c0 + 1
+    eo, el = O.attention_masked(q, k, v, scale, Hq // Hkv, off, kv if use_bits else None, window or None)
+    close(out, eo, **BF16_TOL)
+    close(lse, el, atol=2e-2, rtol=1e-3)
+
+
+def test_pack_key_bits_layout():
+    """Bit j % 64 of word j // 64 is key j (bit 63 lands in the sign bit); keys past Sk are clear."""
+    kv = torch.zeros(2, 130, dtype=torch.int64)
+    kv[0, [0, 63, 64, 129]] = 1
+    kv[1] = 1
+    bits = FA.pack_key_bits(kv.cuda()).cpu()
+    assert bits.shape == (2, 3)
+    assert bits[0].tolist() == [1 - (1 << 63), 1, 2]
+    assert bits[1].tolist() == [-1, -1, 3]
+
+
 def test_flash_public_api_matches_reference_fallback_semantics():
     q = randn(1, 4, 96, 64, dtype=torch.bfloat16, seed=103)
     k = randn(1, 2, 96, 64, dtype=torch.bfloat16, seed=104)

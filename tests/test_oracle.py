@@ -53,6 +53,34 @@ def test_attention_bottom_right_offset_equals_explicit_mask():
     torch.testing.assert_close(out, ref)
 
 
+def test_masked_attention_reduces_to_causal_without_padding_or_window():
+    q, k, v = rn(2, 4, 5, 8, seed=7), rn(2, 2, 9, 8, seed=8), rn(2, 2, 9, 8, seed=9)
+    exp = O.attention(q, k, v, 0.4, True, 2, causal_offset=4)
+    for kv, win in ((None, None), (torch.ones(2, 9), None), (None, 14)):  # a window of 14 covers every key
+        got = O.attention_masked(q, k, v, 0.4, 2, 4, kv, win)
+        assert torch.equal(got[0], exp[0]) and torch.equal(got[1], exp[1])
+
+
+def test_masked_attention_equals_attention_over_the_visible_keys_only():
+    """Each query's row equals plain (unmasked) attention over just the keys it may see, gathered by
+    hand from the padding row and the window; a query that sees none gets a zero row, LSE -inf."""
+    q, k, v = rn(2, 2, 6, 8, seed=10), rn(2, 1, 10, 8, seed=11), rn(2, 1, 10, 8, seed=12)
+    key_valid = torch.tensor([[0, 0, 0, 0, 0, 0, 1, 1, 1, 1], [1, 0, 1, 1, 0, 1, 1, 1, 0, 1]])
+    off, win = 4, 3
+    out, lse = O.attention_masked(q, k, v, 0.5, 2, off, key_valid, win)
+    for b in range(2):
+        for h in range(2):
+            for i in range(6):
+                vis = [j for j in range(10) if i + off - win < j <= i + off and key_valid[b, j]]
+                if not vis:
+                    assert torch.all(out[b, h, i] == 0) and lse[b, h, i] == float("-inf")
+                    continue
+                s = (q[b, h, i].double() @ k[b, 0, vis].double().T) * 0.5
+                torch.testing.assert_close(out[b, h, i], torch.softmax(s, 0) @ v[b, 0, vis].double())
+                torch.testing.assert_close(lse[b, h, i], torch.logsumexp(s, 0))
+    assert (lse == float("-inf")).any()  # batch row 0, queries 0 and 1 see only padding
+
+
 @pytest.mark.parametrize("causal,groups,off", [(True, 2, 0), (False, 1, 0), (True, 1, 3)])
 def test_attention_backward_matches_autograd(causal, groups, off):
     q = rn(1, 4, 6, 8, seed=7).requires_grad_(True)
