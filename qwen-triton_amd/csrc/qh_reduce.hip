@@ -286,6 +286,21 @@ __global__ __launch_bounds__(1024) void colsum_partials(const float* __restrict_
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
   if (c < cols) {
     int64_t r = wv;
+    // four 64-row steps' loads issued together (same order of additions as the loop below)
+    for (; r + 48 + 192 < nrows; r += 256) {
+      float v[4][4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[u][q] = ws[(r + 64 * u + 16 * q) * cols + c];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a0 += v[u][0];
+        a1 += v[u][1];
+        a2 += v[u][2];
+        a3 += v[u][3];
+      }
+    }
     for (; r + 48 < nrows; r += 64) {
       a0 += ws[r * cols + c];
       a1 += ws[(r + 16) * cols + c];
