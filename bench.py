@@ -398,10 +398,40 @@ def bench_fa(steps, warmup):
     bwd_ms = sum(x.elapsed_time(y) for x, y in eb) / steps
     fwd_flop = 2 * B * Hq * D * S * (S + 1)
     bwd_flop = 2.5 * fwd_flop
+
+    # Inference forward with the model's masks (qh_flash_fwd_masked): left padding of
+    # 0, 1/8, ..., 7/8 of the sequence, and a sliding window of 1024 keys. Flops count the visible
+    # (query, key) pairs only: (S - p)(S - p + 1) / 2 per sequence with p padding tokens, and
+    # W (W + 1) / 2 + (S - W) W under a window of W.
+    pads = [S * i // 8 for i in range(B)]
+    valid = torch.ones(B, S, dtype=torch.int64, device="cuda")
+    for b, p in enumerate(pads):
+        valid[b, :p] = 0
+    bits = FA.pack_key_bits(valid)
+    W = 1024
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        sync()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        sync()
+        return a.elapsed_time(b) / steps
+
+    pad_ms = timed(lambda: FA.flash_forward(q, k, v, scale, True, 2, need_lse=False, key_bits=bits))
+    win_ms = timed(lambda: FA.flash_forward(q, k, v, scale, True, 2, need_lse=False, window=W))
+    pad_flop = 4 * Hq * D * sum((S - p) * (S - p + 1) // 2 for p in pads)
+    win_flop = 4 * B * Hq * D * (W * (W + 1) // 2 + (S - W) * W)
     return {"fa_fwd_ms": round(fwd_ms, 3), "fa_bwd_ms": round(bwd_ms, 3),
             "fa_fwd_tflops": round(fwd_flop / fwd_ms / 1e9, 1), "fa_bwd_tflops": round(bwd_flop / bwd_ms / 1e9, 1),
             "fa_fwd_frac": round(fwd_flop / fwd_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
-            "fa_bwd_frac": round(bwd_flop / bwd_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)}
+            "fa_bwd_frac": round(bwd_flop / bwd_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "fa_fwd_left_padded_ms": round(pad_ms, 3), "fa_fwd_left_padded_tflops": round(pad_flop / pad_ms / 1e9, 1),
+            "fa_fwd_window1024_ms": round(win_ms, 3), "fa_fwd_window1024_tflops": round(win_flop / win_ms / 1e9, 1)}
 
 
 def bench_gdr(steps, warmup):

@@ -393,6 +393,9 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
       const int blo = qb * BMQ + coff - window + 1;
       it0 = blo > 0 ? blo / BN : 0;
     }
+    // leading tiles with no visible key (left padding) are not even loaded
+    if (kbits)
+      while (it0 < ntiles && kbits[b * kbits_b + it0] == 0) ++it0;
   }
 
   const TileLoader<T, BN, DP> kload(sks, D), vload(svs, D);
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
     const bool need_mask = (kv0 + BN > Sk) || (causal && kv0 + BN - 1 > qw0 + coff);
     if constexpr (MASKED) {
       const uint64_t w = kbits ? kbits[b * kbits_b + it] : ~0ull;  // block-uniform
-      if (w == 0) continue;  // no visible key in the tile (left padding)
+      if (w == 0) continue;  // no visible key in the tile
       const bool cut = window > 0 && kv0 < qw0 + 31 + coff - window + 1;
       fa_fwd_tile<T, DP, true>(Ks[buf], Vs[buf], qf, acc, m, l, kv0, need_mask || cut || w != ~0ull, lim,
                                scale_log2, lane, lo, w);
