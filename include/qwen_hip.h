@@ -449,7 +449,8 @@ int qh_flash_fwd(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const voi
  * window > 0 and j <= i + causal_offset - window, or when key_bits (may be
  * NULL; 8-byte aligned, bits_stride >= ceil(Sk / 64) words per batch row) has
  * bit j % 64 of word b * bits_stride + j / 64 clear. A query that sees no key
- * gets a zero row and LSE = -inf. Tiles with no visible key are skipped.
+ * gets a zero row and LSE = -inf. Tiles with no visible key are skipped; with
+ * Sq == 1 the q-heads of a kv-head share one workgroup (its keys read once).
  * Replaces the masked fp32 SDPA call of qwen_triton/modules/attention.py:114-119
  * with the mask of qwen_triton/models/core.py:47-75 (_build_causal_mask). */
 int qh_flash_fwd_masked(const void* q, int64_t sqb, int64_t sqh, int64_t sqs, const void* k, int64_t skb,

@@ -335,7 +335,10 @@ __device__ __forceinline__ void fa_fwd_tile(const T* Kt, const T* Vt, const type
 // MASKED: key j is also hidden from query i when j <= i + coff - window
 // (window > 0) or bit j of the batch row's validity words is clear
 // (kbits non-null; word t covers keys 64t .. 64t + 63).
-template <typename T, int DP, bool MASKED = false>
+// PACK (Sq == 1, grid (1, B * Hkv)): the block's rows are the `groups` q-heads
+// of one kv-head, all at query position 0, so the kv-head's keys are read once
+// for all of them.
+template <typename T, int DP, bool MASKED = false, bool PACK = false>
 __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqs,
                                                      const T* __restrict__ K, int64_t skb, int64_t skh, int64_t sks,
                                                      const T* __restrict__ V, int64_t svb, int64_t svh, int64_t svs,
@@ -354,21 +357,27 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
   int rank, bh;
   block_rank_row(rank, bh);
   const int qb = nqb - 1 - rank;  // last query blocks see the most keys
-  const int b = bh / Hq, hq = bh % Hq, hk = hq / groups;
+  const int hkv = Hq / groups;
+  const int b = PACK ? bh / hkv : bh / Hq;
+  const int hk = PACK ? bh % hkv : (bh % Hq) / groups;
+  const int hq = PACK ? hk * groups : bh % Hq;  // PACK: the group's first q-head
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: keeps tile branches scalar
   const int ql = lane & 31, hf = lane >> 5;
   const T* Qb = Q + b * sqb + hq * sqh;
   const T* Kb = uniform_ptr(K + b * skb + hk * skh);
   const T* Vb = uniform_ptr(V + b * svb + hk * svh);
-  const int qw0 = qb * BMQ + wid * 32;
-  const int qi = qw0 + ql;
+  const int qw0 = PACK ? 0 : qb * BMQ + wid * 32;  // query position of the wave's first row
+  const int qi = PACK ? 0 : qw0 + ql;              // this lane's query position
+  const int prow = wid * 32 + ql;                   // PACK: this lane's q-head within the group
+  const bool qvalid = PACK ? prow < groups : qi < Sq;
+  const int64_t qoff = PACK ? (int64_t)prow * sqh : (int64_t)qi * sqs;
 
   v8 qf[KD];
 #pragma unroll
   for (int kd = 0; kd < KD; ++kd) {
     const int d0 = kd * 16 + hf * 8;
-    if (qi < Sq && d0 < D) qf[kd] = load_frag16<T>(Qb + (int64_t)qi * sqs + d0);
+    if (qvalid && d0 < D) qf[kd] = load_frag16<T>(Qb + qoff + d0);
     else
 #pragma unroll
       for (int e = 0; e < 8; ++e) qf[kd][e] = (T)0.f;
@@ -428,8 +437,8 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
   }
 
   l = halves_sum(l);
-  if (qi < Sq) {
-    T* Ob = O + b * sob + hq * soh + (int64_t)qi * sos;
+  if (qvalid) {
+    T* Ob = O + b * sob + hq * soh + (PACK ? (int64_t)prow * soh : (int64_t)qi * sos);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -443,7 +452,10 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const T* __restrict__ Q, in
           *reinterpret_cast<typename Mfma<T>::v4*>(Ob + d) = o4;
         }
       }
-    if (hf == 0 && LSE) LSE[(int64_t)bh * Sq + qi] = l > 0.f ? (m * scale_log2 + __log2f(l)) * kLn2 : -INFINITY;
+    if (hf == 0 && LSE) {
+      const int64_t li = PACK ? (int64_t)b * Hq + hq + prow : (int64_t)bh * Sq + qi;
+      LSE[li] = l > 0.f ? (m * scale_log2 + __log2f(l)) * kLn2 : -INFINITY;
+    }
   }
 }
 
@@ -1812,12 +1824,22 @@ extern "C" int qh_flash_fwd_masked(const void* q, int64_t sqb, int64_t sqh, int6
   hipStream_t st = (hipStream_t)stream;
   const float sl2 = scale * kLog2e;
   const int groups = (int)(Hq / Hkv);
-  dim3 grid((unsigned)ceil_div(Sq, 128), (unsigned)(B * Hq));
-#define QH_FWD(T, DPV)                                                                                          \
-  fa_fwd_kernel<T, DPV, true><<<grid, 256, 0, st>>>(                                                          \
-      (const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks, (const T*)v, svb, svh, svs, (T*)o, sob, soh, sos, \
-      lse, (int)Hq, groups, (int)Sq, (int)Sk, (int)D, sl2, causal, (int)causal_offset, key_bits, bits_stride,   \
-      (int)window)
+  // one query per sequence: the q-heads of a kv-head share a block (its keys are read once)
+  const bool pack = Sq == 1 && groups > 1 && groups <= 128;
+  dim3 grid((unsigned)ceil_div(Sq, 128), (unsigned)(pack ? B * Hkv : B * Hq));
+#define QH_FWD(T, DPV)                                                                                            \
+  do {                                                                                                            \
+    if (pack)                                                                                                     \
+      fa_fwd_kernel<T, DPV, true, true><<<grid, 256, 0, st>>>(                                                    \
+          (const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks, (const T*)v, svb, svh, svs, (T*)o, sob, soh,    \
+          sos, lse, (int)Hq, groups, (int)Sq, (int)Sk, (int)D, sl2, causal, (int)causal_offset, key_bits,         \
+          bits_stride, (int)window);                                                                              \
+    else                                                                                                          \
+      fa_fwd_kernel<T, DPV, true><<<grid, 256, 0, st>>>(                                                          \
+          (const T*)q, sqb, sqh, sqs, (const T*)k, skb, skh, sks, (const T*)v, svb, svh, svs, (T*)o, sob, soh,    \
+          sos, lse, (int)Hq, groups, (int)Sq, (int)Sk, (int)D, sl2, causal, (int)causal_offset, key_bits,         \
+          bits_stride, (int)window);                                                                              \
+  } while (0)
 #define QH_FWD_D(T) \
   if (dp == 32) QH_FWD(T, 32); else if (dp == 64) QH_FWD(T, 64); else QH_FWD(T, 128);
   if (dtype == QH_BF16) { QH_FWD_D(bf16_t) } else { QH_FWD_D(f16_t) }

@@ -1070,6 +1070,9 @@ MASKED_CASES = [  # B, Hq, Hkv, Sq, Sk, D, left pads, random holes, window
     (4, 8, 2, 1, 333, 128, [0, 1, 100, 300], False, 0),  # padded decode step
     (1, 2, 2, 300, 300, 32, None, False, 64),  # window of exactly one tile
     (2, 4, 2, 100, 100, 64, [100, 3], False, 0),  # a sequence of padding only
+    (3, 16, 2, 1, 517, 64, [0, 200, 516], True, 0),  # decode, 8 q-heads per kv-head in one block
+    (2, 6, 2, 1, 90, 32, [10, 0], False, 30),  # decode, 3 q-heads per kv-head, window and padding
+    (2, 4, 4, 1, 200, 128, None, False, 50),  # decode without GQA (one q-head per block)
 ]
 
 
