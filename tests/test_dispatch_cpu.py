@@ -296,3 +296,41 @@ def test_flash_backward_fallback_keeps_the_bottom_right_mask():
     out = _torch_attention_offset(q, k, v, 0.3, True, 2, 4)
     ref = O.attention(q, k, v, 0.3, True, 2, causal_offset=4)[0]
     torch.testing.assert_close(out, ref.to(out.dtype))
+
+
+def test_pack_key_bits_layout_cpu():
+    """Bit j % 64 of word j // 64 is key j (bit 63 is the sign bit); keys past Sk are clear."""
+    from qwen_triton.kernels.flash_attention import pack_key_bits
+
+    kv = torch.zeros(2, 130, dtype=torch.int64)
+    kv[0, [0, 63, 64, 129]] = 1
+    kv[1] = 1
+    assert pack_key_bits(kv).tolist() == [[1 - (1 << 63), 1, 2], [-1, -1, 3]]
+
+
+def test_structured_mask_matches_the_additive_mask_and_keeps_the_step_start():
+    """The structured mask's dense form is the additive mask for the step's first cache length, even
+    when a layer has appended its keys before asking for it; its key rows prepend ones for cached
+    keys the 2-D mask does not cover; the kernel arguments are refused for other shapes."""
+    from types import SimpleNamespace
+
+    from qwen_triton.models.core import _build_causal_mask, _structured_mask
+
+    cache = SimpleNamespace(n=5)
+    cache.get_seq_length = lambda: cache.n
+    am = torch.tensor([[0, 0, 1, 1, 1], [1, 1, 1, 1, 1]])  # covers 5 of the 8 keys (3 cached)
+    pos = torch.arange(5, 8)
+    mask = _structured_mask(am, 2, pos, torch.device("cpu"), cache, 4, True)
+    expect = _build_causal_mask(am, 2, pos, torch.device("cpu"), 5, 4)
+    cache.n = 8  # the first layer wrote the step's keys
+    assert torch.equal(mask.dense(), expect)
+    assert mask.key_valid.tolist() == [[1, 1, 1, 0, 0, 1, 1, 1], [1] * 8]
+    q, k = torch.zeros(2, 4, 3, 8), torch.zeros(2, 2, 8, 8)
+    bits, window, offset = mask.kernel_args(q, k)
+    assert bits.tolist() == [[0b11100111], [0b11111111]] and window == 4 and offset == 5
+    assert mask.kernel_args(q, torch.zeros(2, 2, 9, 8)) is None  # keys beyond the step's length
+    blocked = _structured_mask(am, 2, pos, torch.device("cpu"), cache, None, False)
+    assert blocked.kernel_args(q, torch.zeros(2, 2, 11, 8)) is None  # caller-given positions
+    # the dense form: query 0 (position 5) sees keys 2..5 by the window, minus the padding of row 0
+    visible = expect[0, 0, 0] == 0
+    assert visible.tolist() == [False, False, True, False, False, True, False, False]
