@@ -424,6 +424,19 @@ def bench_fa(steps, warmup):
 
     pad_ms = timed(lambda: FA.flash_forward(q, k, v, scale, True, 2, need_lse=False, key_bits=bits))
     win_ms = timed(lambda: FA.flash_forward(q, k, v, scale, True, 2, need_lse=False, window=W))
+    # A padded decode step at config 3's attention shape (64 sequences, 16 q-heads on 8 kv-heads,
+    # 2049 keys, left padding of (13 b) mod 300 tokens) against the unmasked split-KV decode kernel.
+    Bd, Hqd, Hkd, Skd = 64, 16, 8, 2049
+    qd = torch.randn(Bd, Hqd, 1, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    kd = torch.randn(Bd, Hkd, Skd, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    vd = torch.randn(Bd, Hkd, Skd, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    vdec = torch.ones(Bd, Skd, dtype=torch.int64, device="cuda")
+    for b_ in range(Bd):
+        vdec[b_, :(13 * b_) % 300] = 0
+    bits_d = FA.pack_key_bits(vdec)
+    dec_ms = timed(lambda: FA.flash_decode(qd, kd, vd, scale, Hqd // Hkd))
+    dec_pad_ms = timed(lambda: FA.flash_forward(qd, kd, vd, scale, True, Hqd // Hkd, Skd - 1, need_lse=False,
+                                                key_bits=bits_d))
     pad_flop = 4 * Hq * D * sum((S - p) * (S - p + 1) // 2 for p in pads)
     win_flop = 4 * B * Hq * D * (W * (W + 1) // 2 + (S - W) * W)
     return {"fa_fwd_ms": round(fwd_ms, 3), "fa_bwd_ms": round(bwd_ms, 3),
@@ -431,7 +444,8 @@ def bench_fa(steps, warmup):
             "fa_fwd_frac": round(fwd_flop / fwd_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
             "fa_bwd_frac": round(bwd_flop / bwd_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
             "fa_fwd_left_padded_ms": round(pad_ms, 3), "fa_fwd_left_padded_tflops": round(pad_flop / pad_ms / 1e9, 1),
-            "fa_fwd_window1024_ms": round(win_ms, 3), "fa_fwd_window1024_tflops": round(win_flop / win_ms / 1e9, 1)}
+            "fa_fwd_window1024_ms": round(win_ms, 3), "fa_fwd_window1024_tflops": round(win_flop / win_ms / 1e9, 1),
+            "decode_attention_us": round(dec_ms * 1e3, 1), "decode_attention_padded_us": round(dec_pad_ms * 1e3, 1)}
 
 
 def bench_gdr(steps, warmup):
