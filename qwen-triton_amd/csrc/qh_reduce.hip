@@ -183,17 +183,46 @@ __global__ __launch_bounds__(BT) void rmsnorm_bwd_fast(const T* __restrict__ x, 
 #pragma unroll
     for (int j = 0; j < VN; ++j) pw[i][j] = 0.f;
   const float inv_cols = 1.0f / (float)cols;
-  for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += (int64_t)gridDim.x * RPB) {
+  const int64_t step = (int64_t)gridDim.x * RPB;
+  // With at most two vectors per lane the next row's x and dy are loaded before this row's sums
+  // (clamped to the last row: every load stays in bounds, a group's surplus last loads go unused),
+  // so a group waits for memory once rather than once per row. With more, the extra registers
+  // cost more than the overlap gains.
+  constexpr bool kAhead = NV <= 2;
+  Vec16<T> xn[NV], gn[NV];
+  if constexpr (kAhead) {
+    const int64_t r0 = min((int64_t)blockIdx.x * RPB + grp, rows - 1);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = min((i * G + g) * VN, cols - VN);
+      xn[i] = ld16(x + r0 * cols + c);
+      gn[i] = ld16(gy + r0 * cols + c);
+    }
+  }
+  for (int64_t row = blockIdx.x * (int64_t)RPB + grp; row < rows; row += step) {
     const T* xr = x + row * cols;
     const T* gr = gy + row * cols;
     Vec16<T> xv[NV], gv[NV];
+    if constexpr (kAhead) {
+      const int64_t rn = min(row + step, rows - 1);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        xv[i] = xn[i];
+        gv[i] = gn[i];
+        const int c = min((i * G + g) * VN, cols - VN);
+        xn[i] = ld16(x + rn * cols + c);
+        gn[i] = ld16(gy + rn * cols + c);
+      }
+    }
     float ss = 0.f, dot = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = (i * G + g) * VN;
       if (c < cols) {
-        xv[i] = ld16(xr + c);
-        gv[i] = ld16(gr + c);
+        if constexpr (!kAhead) {
+          xv[i] = ld16(xr + c);
+          gv[i] = ld16(gr + c);
+        }
 #pragma unroll
         for (int j = 0; j < VN; ++j) {
           const float xf = to_f32(xv[i].v[j]), gf = to_f32(gv[i].v[j]);
